@@ -1,0 +1,383 @@
+#!/usr/bin/env python3
+"""Benchmark of the TBE hot path on one MI355X.
+
+Default workload (config 2): TBE fp32 forward, SUM pooling, T=8 tables of
+E=1,000,000 x D=128, B=4096 bags per table, pooling factor U{1..40}, int64
+indices Zipf(1.05) with a per-table permutation (seeded synthetic data; the
+weights are generated on the device).  One step = one
+torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda call over
+the batch, inputs resident in HBM.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config {2,3,4,5}]
+
+Prints one JSON line: lookups/s (whole job), the roofline of the dominant
+kernel (algorithmic bytes per launch / HIP-event-timed launch duration vs
+8 TB/s) and the CPU baseline (FBGEMM's CPU kernel on this host's cores).
+--config 3/4/5 print the same line for the backward, the nbit lookup and the
+mixed nbit workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "torchlib-xpu_amd"))
+
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="bound on the CPU baseline's timed work")
+    return ap.parse_args()
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch recorded by the rocprofv3 PMC summary, if present."""
+    p = REPO / "profiles" / f"{name}.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def time_launches(fn, steps: int, warmup: int):
+    """Returns (wall seconds for `steps` calls, mean per-launch ms from events)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall, statistics.mean(per), statistics.median(per)
+
+
+def cpu_time(fn, budget_s: float, min_runs: int = 3, warm: int = 1):
+    for _ in range(warm):
+        fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < 10):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s and len(times) >= 1:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------
+
+
+def bench_tbe_forward(args, dev):
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 2 indices")
+    inp = bench_inputs.config2()
+    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda
+
+    def step():
+        return op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, idx, off, 0, e32, empty, 0,
+                  False)
+
+    log(f"timing N={inp.N} lookups, {args.steps} steps")
+    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    N = inp.N
+    alg_bytes = N * (D * 4 + 8) + T * B * (8 + D * 4)
+
+    # Cold cache: overwrite a 1 GiB buffer before each timed launch.
+    flush = torch.empty(1 << 28, device=dev, dtype=torch.float32)
+    cold = []
+    for _ in range(5):
+        flush.fill_(1.0)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        step()
+        e.record()
+        torch.cuda.synchronize()
+        cold.append(s.elapsed_time(e))
+    del flush
+
+    res = dict(
+        metric="TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
+        value=N * args.steps / wall,
+        unit="lookups/s",
+        ms_per_step=wall / args.steps * 1e3,
+        dtype="fp32",
+        config={"workload": "config2: TBE fp32 forward SUM, T=8 E=1e6 D=128 B=4096 "
+                            "L~U{1..40} Zipf(1.05) int64 indices",
+                "T": T, "E": E, "D": D, "B": B, "N": N, "indices": "int64"},
+        kernel="tbe_fwd_kernel",
+        alg_bytes=alg_bytes,
+        kernel_ms_mean=mean_ms,
+        kernel_ms_median=med_ms,
+        cold_kernel_ms_median=statistics.median(cold),
+    )
+    traffic = traffic_from_profile("tbe_fwd_config2")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_tbe(args, inp, W)
+    return res, traffic, cpu
+
+
+def cpu_baseline_tbe(args, inp, W):
+    import numpy as np
+
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as orc
+
+    log("CPU baseline: copying weights to host")
+    Wh = W.cpu().numpy()
+    w_off = (np.arange(inp.T) * inp.E[0] * inp.D[0]).astype(np.int64)
+    nthreads = orc.host_threads()
+    fn = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off, inp.D_offsets, inp.E, inp.B, inp.indices,  # noqa: E731
+                                            inp.offsets, 0, nthreads=nthreads)
+    log(f"CPU baseline: FBGEMM SpMDM on {nthreads} threads")
+    med, runs = cpu_time(fn, args.cpu_seconds)
+    fn1 = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off, inp.D_offsets, inp.E, inp.B, inp.indices,  # noqa: E731
+                                             inp.offsets, 0, nthreads=1)
+    med1, runs1 = cpu_time(fn1, args.cpu_seconds / 3, min_runs=1, warm=0)
+    return dict(
+        value=inp.N / med, unit="lookups/s", cores=nthreads, kind="reference",
+        sample=(f"full config-2 batch (N={inp.N} lookups), median of {runs} runs; FBGEMM "
+                f"GenerateEmbeddingSpMDMWithStrides<float,int64,int64,float> from the installed "
+                f"torch (the CPU kernel fbgemm_gpu's CPU TBE forward wraps), {nthreads} threads "
+                f"over (table, 256-bag chunks); 1 thread: {inp.N / med1:.4g} lookups/s "
+                f"({runs1} runs); host CPU: {cpu_model()}"),
+    )
+
+
+def bench_nbit(args, dev, config: int):
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+    from mx_fbgemm.sparse_types import SparseType, padded_row_size_in_bytes
+
+    log(f"generating config {config} indices")
+    inp = bench_inputs.config4() if config == 4 else bench_inputs.config5()
+    tys = [SparseType.from_int(t) for t in inp.tys]
+    strides = [padded_row_size_in_bytes(D, ty, 16) for D, ty in zip(inp.D, tys)]
+    sizes = [E * s for E, s in zip(inp.E, strides)]
+    w_off_np = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.randint(0, 256, (int(sum(sizes)),), generator=g, device=dev, dtype=torch.uint8)
+    for t, ty in enumerate(tys):
+        tab = W[w_off_np[t]: w_off_np[t] + sizes[t]].view(inp.E[t], strides[t])
+        if ty.is_rowwise_quantized():
+            sc = (torch.rand(inp.E[t], generator=g, device=dev) * 9e-3 + 1e-3).half()
+            bi = (torch.rand(inp.E[t], generator=g, device=dev) * 0.2 - 0.1).half()
+            tab[:, 0:2] = sc.view(torch.uint8).view(-1, 2)
+            tab[:, 2:4] = bi.view(torch.uint8).view(-1, 2)
+        else:
+            v = (torch.rand((inp.E[t], inp.D[t]), generator=g, device=dev) * 0.02 - 0.01).half()
+            tab[:, : 2 * inp.D[t]] = v.view(torch.uint8).view(inp.E[t], -1)
+    idx = torch.from_numpy(inp.indices).to(dev, torch.int32)
+    off = torch.from_numpy(inp.offsets).to(dev, torch.int32)
+
+    def mx(kind):
+        return max([D for D, ty in zip(inp.D, tys) if ty == kind], default=0)
+
+    args_ = (W, torch.zeros(0, dtype=torch.uint8, device=dev),
+             torch.zeros(inp.T, dtype=torch.int32, device=dev),
+             torch.from_numpy(w_off_np).to(dev),
+             torch.tensor(inp.tys, dtype=torch.uint8, device=dev),
+             torch.from_numpy(inp.D_offsets).to(dev), inp.total_D, mx(SparseType.INT2),
+             mx(SparseType.INT4), mx(SparseType.INT8), mx(SparseType.FP16), mx(SparseType.FP32),
+             idx, off, 1 if config == 4 else 0, None, 1, None, None, 16)
+    op = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function
+
+    def step():
+        return op(*args_)
+
+    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    N = inp.N
+    unpadded = [strides_u for strides_u in
+                [(D + 4) if ty == SparseType.INT8 else (D // 2 + 4) if ty == SparseType.INT4
+                 else 2 * D for D, ty in zip(inp.D, tys)]]
+    lens = np.diff(inp.offsets).reshape(inp.T, inp.B).sum(1)
+    alg_bytes = int(sum(int(lens[t]) * (unpadded[t] + 4) for t in range(inp.T))
+                    + inp.B * sum(4 + 2 * D for D in inp.D))
+    res = dict(
+        metric="nbit TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
+        value=N * args.steps / wall, unit="lookups/s", ms_per_step=wall / args.steps * 1e3,
+        dtype="int8/int4 codes, fp32 accumulate, fp16 out" if config == 4 else
+        "fp16/int4 codes, fp32 accumulate, fp16 out",
+        config={"workload": (f"config{config}: " + (
+            "nbit MEAN fp16 out, 16 INT8 + 16 INT4 tables E=1e6 D=128 B=16384 L=20"
+            if config == 4 else "mixed nbit SUM fp16 out, 64 tables FP16/INT4 D 32..256 "
+            "B=65536 L~Poisson(15) 10% empty Zipf(1.1)")), "T": inp.T, "B": inp.B, "N": N},
+        kernel="nbit_fwd_kernel", alg_bytes=alg_bytes, kernel_ms_mean=mean_ms,
+        kernel_ms_median=med_ms,
+    )
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        # Bounded sample: the first B_s bags of every table.
+        Bs = min(inp.B, 2048)
+        sel_off = np.concatenate([inp.offsets[t * inp.B: t * inp.B + Bs] for t in range(inp.T)]
+                                 + [[0]])
+        idx_parts = [inp.indices[inp.offsets[t * inp.B]: inp.offsets[t * inp.B + Bs]]
+                     for t in range(inp.T)]
+        sidx = np.concatenate(idx_parts).astype(np.int64)
+        lens_s = np.concatenate([np.diff(inp.offsets[t * inp.B: t * inp.B + Bs + 1])
+                                 for t in range(inp.T)])
+        soff = bench_inputs.offsets_from_lengths(lens_s)
+        del sel_off
+        log("CPU baseline: copying nbit weights to host")
+        Wh = W.cpu().numpy()
+        nthreads = orc.host_threads()
+        fn = lambda: orc.fbgemm_nbit_forward(Wh, w_off_np, inp.tys, inp.D_offsets, inp.E, Bs,  # noqa: E731
+                                             sidx, soff, 1 if config == 4 else 0,
+                                             nthreads=nthreads)
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        cpu = dict(value=sidx.size / med, unit="lookups/s", cores=nthreads, kind="reference",
+                   sample=(f"first {Bs} bags of every table ({sidx.size} lookups), median of "
+                           f"{runs} runs; FBGEMM 8-bit/N-bit/fp16 SpMDM CPU kernels "
+                           f"(scale_bias_last=false) from the installed torch, {nthreads} "
+                           f"threads; host CPU: {cpu_model()}"))
+    return res, traffic_from_profile(f"nbit_fwd_config{config}"), cpu
+
+
+def bench_backward(args, dev):
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 3 (config-2 indices)")
+    inp = bench_inputs.config2()
+    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    m1 = torch.zeros(T * E, device=dev)
+    grad = torch.randn((B, inp.total_D), generator=g, device=dev) * 1e-2
+    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
+    m_off = torch.arange(T, device=dev, dtype=torch.int64) * E
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
+
+    def step():
+        op(grad, W, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits, idx, off, 0,
+           e32, 0, 0, False, m1, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
+
+    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
+                      + inp.indices).size)
+    alg = inp.N * 8 + (T * B + 1) * 8 + B * inp.total_D * 4 + U * (2 * D * 4 + 2 * 4)
+    res = dict(
+        metric="TBE backward + exact rowwise Adagrad lookups/sec, 1 MI355X",
+        value=inp.N * args.steps / wall, unit="lookups/s", ms_per_step=wall / args.steps * 1e3,
+        dtype="fp32",
+        config={"workload": "config3: TBE backward + exact rowwise Adagrad on config-2 shapes",
+                "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
+        kernel="whole backward (transpose + segment reduce + update)", alg_bytes=alg,
+        kernel_ms_mean=mean_ms, kernel_ms_median=med_ms,
+    )
+    return res, None, None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (the TBE would "
+              "shard table-wise over RCCL all-to-all; see the design notes). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import mx_fbgemm  # noqa: F401
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    if args.config == 2:
+        res, traffic, cpu = bench_tbe_forward(args, dev)
+    elif args.config == 3:
+        res, traffic, cpu = bench_backward(args, dev)
+    else:
+        res, traffic, cpu = bench_nbit(args, dev, args.config)
+    achieved = res["alg_bytes"] / (res["kernel_ms_mean"] * 1e-3) / 1e9
+    line = dict(
+        metric=res["metric"], value=res["value"], unit=res["unit"], n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=res["ms_per_step"], higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype=res["dtype"], data="synthetic",
+        config=res["config"],
+        roofline=dict(bound="hbm", achieved=achieved, peak=PEAK_HBM_GBS, unit="GB/s",
+                      frac=achieved / PEAK_HBM_GBS, traffic=traffic,
+                      kernel=res["kernel"], alg_bytes_per_launch=res["alg_bytes"],
+                      launch_ms_mean=res["kernel_ms_mean"],
+                      launch_ms_median=res["kernel_ms_median"]),
+        cpu_baseline=cpu,
+    )
+    if "cold_kernel_ms_median" in res:
+        line["roofline"]["cold_launch_ms_median"] = res["cold_kernel_ms_median"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,208 @@
+/*
+ * mx_fbgemm.h -- C-ABI of the MI355X (gfx950) kernels behind the
+ * torch.ops.fbgemm.* drop-in operators.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * passed as `void*`.  Nothing here allocates: scratch memory is sized by a
+ * *_workspace_bytes() query and handed in by the caller.  All calls are
+ * asynchronous on `stream` and never synchronise the host.  They return
+ * MX_OK (0) or a negative status; mx_last_error() then holds a
+ * thread-local message.
+ *
+ * Which interface each function replaces.  The reference snapshot
+ * (/root/reference) ships no FBGEMM code; its plugin boundary is a
+ * torch.ops.load_library()'d .so whose static initializer registers the
+ * device implementation under the upstream project's own interface
+ * (reference: packages/torchcodec-xpu/src/torchcodec_xpu/__init__.py:25-56,
+ * XpuDeviceInterface.cpp:33-35).  For this path the upstream interface is
+ * the `fbgemm` dispatcher namespace of fbgemm_gpu; the op each function
+ * serves is named in its comment (upstream fbgemm_gpu, recalled names, no
+ * line numbers available offline).
+ */
+#ifndef MX_FBGEMM_H
+#define MX_FBGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+#define MX_OK 0
+#define MX_EINVAL (-1)       /* bad argument (shape, size, enum)             */
+#define MX_EHIP (-2)         /* a HIP runtime call failed                    */
+#define MX_EUNSUPPORTED (-3) /* valid request this build does not implement  */
+#define MX_EWORKSPACE (-4)   /* workspace missing or smaller than required   */
+
+/* ---- enums shared with the host layer ----------------------------------
+ * Element types of dense/jagged tensors (own numbering). */
+#define MX_DTYPE_F32 0
+#define MX_DTYPE_F16 1
+#define MX_DTYPE_BF16 2
+#define MX_DTYPE_F64 3
+
+/* fbgemm_gpu SparseType values (weights_tys / output_dtype). */
+#define MX_SPARSE_FP32 0
+#define MX_SPARSE_FP16 1
+#define MX_SPARSE_INT8 2
+#define MX_SPARSE_INT4 3
+#define MX_SPARSE_INT2 4
+#define MX_SPARSE_BF16 5
+
+/* fbgemm_gpu PoolingMode values. */
+#define MX_POOL_SUM 0
+#define MX_POOL_MEAN 1
+#define MX_POOL_NONE 2
+
+/* Maximum number of jagged dimensions the jagged kernels accept. */
+#define MX_MAX_JAGGED_DIM 4
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mx_version(void);
+
+/* Thread-local text of the last failing call on this thread ("" if none). */
+const char* mx_last_error(void);
+
+/* ---- jagged tensor ops ------------------------------------------------- */
+
+/* Serves fbgemm::jagged_to_padded_dense_forward (and the forward of
+ * fbgemm::jagged_to_padded_dense).
+ *   values   [total_L, inner] elements of `elem_bytes` bytes each
+ *   offsets  num_jagged_dim device arrays (host array of device pointers),
+ *            int32 (offset_bytes 4) or int64 (offset_bytes 8); level 0
+ *            bounds the B = offsets_numel[0]-1 outer rows, level k bounds
+ *            the rows of level k-1
+ *   offsets_numel  host array: entries in each offsets array
+ *   max_lengths    host array: padded length of each jagged dimension
+ *   out      [B, max_lengths[0], ..., max_lengths[k-1], inner]
+ *   pad_bits the padding value's bit pattern in the element type
+ * Positions past a row's length get the padding value; rows longer than
+ * max_length are truncated.  Pure data movement: bit-exact. */
+int mx_jagged_to_padded_dense(const void* values, int64_t elem_bytes, int64_t inner,
+                              int32_t num_jagged_dim, const void* const* offsets,
+                              int32_t offset_bytes, const int64_t* offsets_numel,
+                              const int64_t* max_lengths, uint64_t pad_bits, void* out,
+                              void* stream);
+
+/* Serves fbgemm::dense_to_jagged_forward (and fbgemm::dense_to_jagged).
+ *   dense    [B, max_lengths..., inner]
+ *   out      [total_L, inner]: row i takes dense at its jagged coordinate;
+ *            rows whose coordinate falls outside max_lengths, or past the
+ *            last offset, are written as zero bits. */
+int mx_dense_to_jagged(const void* dense, int64_t elem_bytes, int64_t inner,
+                       int32_t num_jagged_dim, const void* const* offsets, int32_t offset_bytes,
+                       const int64_t* offsets_numel, const int64_t* max_lengths, int64_t total_L,
+                       void* out, void* stream);
+
+/* Serves fbgemm::jagged_dense_elementwise_add_jagged_output.
+ *   out[i] = x[i] + y[coordinate(i)] in the element type's arithmetic
+ *   (f16/bf16 computed in fp32 and rounded to nearest even); where the
+ *   coordinate lies outside y, out[i] = x[i] + 0. */
+int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense, int32_t dtype,
+                                    int64_t inner, int32_t num_jagged_dim,
+                                    const void* const* offsets, int32_t offset_bytes,
+                                    const int64_t* offsets_numel, const int64_t* max_lengths,
+                                    int64_t total_L, void* out, void* stream);
+
+/* ---- TBE training forward ---------------------------------------------- */
+
+/* Serves fbgemm::split_embedding_codegen_forward_unweighted_cuda /
+ * _weighted_cuda (the forward of the split_embedding_codegen_lookup_*
+ * autograd functions), DEVICE placement, fp32 weights.
+ *   weights         fp32, all tables back to back
+ *   weights_offsets int64 [T] element offset of each table
+ *   D_offsets       int32 [T+1]; every D_t a multiple of 4, max_D <= 1024
+ *   indices         [N] int32 (index_bytes 4) or int64 (8)
+ *   offsets         [T*B+1], same integer type as indices, t-major bags
+ *   indice_weights  fp32 [N] or NULL
+ *   out             [B, total_D] fp32 (out_dtype MX_SPARSE_FP32) or fp16
+ * SUM: per column, rows are added in index order starting from +0.0.
+ * MEAN: the sum times (1.0f / L); empty bags give 0. */
+int mx_tbe_forward(const float* weights, const int64_t* weights_offsets,
+                   const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
+                   const void* indices, const void* offsets, int32_t index_bytes,
+                   int32_t pooling_mode, const float* indice_weights, void* out,
+                   int32_t out_dtype, int64_t total_D, void* stream);
+
+/* ---- TBE backward: transpose (sort) and fused exact rowwise Adagrad ----- */
+
+/* Number of info bits used for the bag index b in an info word
+ * ((t << info_B_num_bits) | b); returns -1 if T and B do not fit 32 bits. */
+int32_t mx_tbe_info_B_num_bits(int32_t T, int64_t B);
+
+/* Workspace needed by mx_tbe_transpose_embedding_input (N lookups). */
+size_t mx_tbe_transpose_workspace_bytes(int64_t N, int32_t total_hash_size_bits);
+
+/* Serves fbgemm::transpose_embedding_input (linearize_index + stable radix
+ * sort of pairs + run-length encode + complete cumsum).
+ *   linear_indices[l]      = hash_size_cumsum[t] + indices[l]
+ *   infos (sorted)         = (t << info_B_num_bits) | b
+ *   sorted_linear_indices  keys stably sorted on their low
+ *                          total_hash_size_bits bits
+ *   run / run_lengths      unique keys and their counts, num_runs of them
+ *   cumulative_run_lengths [num_runs+1] exclusive cumsum of run_lengths
+ * Run arrays are sized N; entries past num_runs are left as they were
+ * (num_runs stays on the device).  Integer work: bit-exact. */
+int mx_tbe_transpose_embedding_input(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
+    int32_t info_B_num_bits, const void* indices, const void* offsets, int32_t index_bytes,
+    int64_t N, int64_t* linear_indices, int64_t* sorted_linear_indices, int32_t* infos_sorted,
+    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mx_tbe_backward_rowwise_adagrad. */
+size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, int32_t max_D);
+
+/* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
+ * (the backward of split_embedding_codegen_lookup_rowwise_adagrad_function).
+ * For each distinct (t, i) touched by the batch:
+ *   g      = sum over its occurrences (sorted order) of grad_output[b, D_t slice]
+ *            (MEAN: each occurrence scaled by 1.0f/L of its bag)
+ *   mode 1 (L2):        g += weight_decay * w
+ *   h     += (sum_d g_d^2) / D_t
+ *   m      = learning_rate / (sqrtf(h) + eps)
+ *   c      = 1 (mode 0, 1) or 1 - learning_rate*weight_decay (mode 2)
+ *   w      = fmaf(-m, g, c * w)
+ * weights and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are
+ * updated in place; no atomics, deterministic. */
+int mx_tbe_backward_rowwise_adagrad(
+    float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
+    int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    int32_t pooling_mode, const float* grad_output, int64_t total_D, float* momentum1,
+    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
+    int32_t weight_decay_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- TBE nbit inference forward ---------------------------------------- */
+
+/* Padded size in bytes of one row of a table of type `ty` and dim D:
+ * round_up(unpadded, row_alignment) with unpadded FP32 4D, FP16 2D,
+ * INT8 D+4, INT4 D/2+4, INT2 D/4+4; -1 for an unknown type. */
+int64_t mx_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_alignment);
+
+/* Serves fbgemm::int_nbit_split_embedding_codegen_lookup_function, DEVICE
+ * placement.
+ *   dev_weights     uint8, row (t, i) at weights_offsets[t] + i*row_bytes(t)
+ *   weights_tys     uint8 [T] SparseType per table
+ *   D_offsets       int32 [T+1]
+ *   max_*_D         the host-side maxima the upstream op receives; a type
+ *                   whose max is 0 is not launched
+ *   INT8/INT4/INT2 rows begin with fp16 scale then fp16 bias; INT4 holds
+ *   the even element in the low nibble.  value = scale*q + bias (fp32).
+ *   output_dtype    MX_SPARSE_FP32 or MX_SPARSE_FP16 (round to nearest even)
+ *   out             [B, total_D] */
+int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
+                    const uint8_t* weights_tys, const int32_t* D_offsets, int32_t T, int64_t B,
+                    int32_t max_int2_D, int32_t max_int4_D, int32_t max_int8_D,
+                    int32_t max_float16_D, int32_t max_float32_D, const void* indices,
+                    const void* offsets, int32_t index_bytes, int32_t pooling_mode,
+                    const float* indice_weights, int32_t output_dtype, int32_t row_alignment,
+                    void* out, int64_t total_D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MX_FBGEMM_H */

@@ -1,0 +1,363 @@
+/*
+ * mx_oracle.c -- TEST INFRASTRUCTURE ONLY.  A plain, single-threaded C
+ * restatement of the operators the HIP kernels implement, used by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker.
+ * Nothing in the product links, loads or calls this file.
+ *
+ * The reference snapshot (/root/reference) contains no FBGEMM code; each
+ * function follows the in-container statement of the algorithm it cites:
+ *   torch/include/fbgemm/FbgemmEmbedding.h (FBGEMM's CPU embedding kernels,
+ *   the CPU path fbgemm_gpu's TBE ops wrap), and the recalled fbgemm_gpu
+ *   semantics of transpose_embedding_input and rowwise Adagrad.
+ * Floating point is compiled with -ffp-contract=off: every fmaf() below is
+ * deliberate, every other product is rounded on its own.
+ *
+ * Pins (tests/test_oracle_*.py): FBGEMM's exported CPU kernels called through
+ * oracle/fbgemm_cpu.cpp, torch.nn.functional.embedding_bag, torch autograd,
+ * numpy brute force, and closed forms.
+ */
+#include "mx_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- fp16 helpers (IEEE binary16, round to nearest even) ----------------- */
+
+float orc_half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t man = h & 0x3ffu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else { /* subnormal: normalise */
+      int e = -1;
+      uint32_t m = man;
+      do {
+        ++e;
+        m <<= 1;
+      } while ((m & 0x400u) == 0);
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((m & 0x3ffu) << 13);
+    }
+  } else if (exp == 0x1f) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t orc_float_to_half(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u); /* NaN */
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+  if (ax < 0x38800000u) { /* result is subnormal or zero */
+    if (ax < 0x33000000u) return sign; /* below half the smallest subnormal */
+    const uint32_t e = ax >> 23;
+    const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    /* value = m * 2^(e-150); in units of 2^-24 that is m >> (126 - e) */
+    const int shift = 126 - (int)e; /* 14..24 */
+    const uint32_t rem = m & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    uint32_t r = m >> shift;
+    if (rem > half || (rem == half && (r & 1u))) ++r;
+    return (uint16_t)(sign | r);
+  }
+  /* normal */
+  uint32_t r = ((ax >> 13) - ((127 - 15) << 10));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r;
+  return (uint16_t)(sign | r);
+}
+
+/* ---- TBE forward ------------------------------------------------------------
+ * FbgemmEmbedding.h:26-39: out[i] = sum_j in[indices[j]] (times weights[j]);
+ * if normalize_by_lengths and len > 0: out /= len.  Applied per table with
+ * the TBE layout: bag (t, b) is offsets[t*B+b] .. offsets[t*B+b+1], the
+ * result lands in out[b, D_off[t] : D_off[t+1]].  Weighted rows accumulate
+ * with one fma each (what FBGEMM's vfmadd does); MEAN multiplies by the
+ * float reciprocal of L. */
+void orc_tbe_forward_f32(const float* W, const int64_t* w_off, const int32_t* D_off, int32_t T,
+                         int64_t B, const int64_t* indices, const int64_t* offsets,
+                         int32_t pooling, const float* iw, float* out, int64_t total_D) {
+  for (int32_t t = 0; t < T; ++t) {
+    const int32_t D0 = D_off[t], D = D_off[t + 1] - D_off[t];
+    const float* Wt = W + w_off[t];
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t s = offsets[t * B + b], e = offsets[t * B + b + 1];
+      float* o = out + b * total_D + D0;
+      for (int32_t d = 0; d < D; ++d) o[d] = 0.0f;
+      for (int64_t l = s; l < e; ++l) {
+        const float* row = Wt + indices[l] * D;
+        if (iw) {
+          for (int32_t d = 0; d < D; ++d) o[d] = fmaf(iw[l], row[d], o[d]);
+        } else {
+          for (int32_t d = 0; d < D; ++d) o[d] = o[d] + row[d];
+        }
+      }
+      if (pooling == ORC_POOL_MEAN && e > s) {
+        const float inv = 1.0f / (float)(e - s);
+        for (int32_t d = 0; d < D; ++d) o[d] = o[d] * inv;
+      }
+    }
+  }
+}
+
+/* ---- nbit forward -------------------------------------------------------------
+ * Row (t, i) starts at byte w_off[t] + i * stride_t, stride_t =
+ * round_up(unpadded, row_align).  Quantized rows carry an fp16 scale and
+ * fp16 bias first (scale_bias_last = false, FbgemmEmbedding.h:88-92,
+ * 144-149); INT4/INT2 pack element 0 in the lowest bits.  Per element the
+ * accumulator takes bias then scale*q in one fma, the order of FBGEMM's
+ * rowwise kernels: acc = fma(scale, q, acc + bias). */
+int64_t orc_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_align) {
+  int64_t u;
+  switch (ty) {
+    case ORC_FP32: u = 4ll * D; break;
+    case ORC_FP16: u = 2ll * D; break;
+    case ORC_INT8: u = D + 4ll; break;
+    case ORC_INT4: u = D / 2 + 4ll; break;
+    case ORC_INT2: u = D / 4 + 4ll; break;
+    default: return -1;
+  }
+  if (row_align > 1) u = (u + row_align - 1) / row_align * row_align;
+  return u;
+}
+
+static float nbit_code(const uint8_t* codes, int32_t ty, int32_t d) {
+  switch (ty) {
+    case ORC_FP32: {
+      float f;
+      memcpy(&f, codes + 4 * d, 4);
+      return f;
+    }
+    case ORC_FP16: {
+      uint16_t h;
+      memcpy(&h, codes + 2 * d, 2);
+      return orc_half_to_float(h);
+    }
+    case ORC_INT8: return (float)codes[d];
+    case ORC_INT4: return (float)((codes[d >> 1] >> ((d & 1) * 4)) & 0xf);
+    default: return (float)((codes[d >> 2] >> ((d & 3) * 2)) & 0x3);
+  }
+}
+
+int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
+                     const int32_t* D_off, int32_t T, int64_t B, const int64_t* indices,
+                     const int64_t* offsets, int32_t pooling, const float* iw, int32_t row_align,
+                     int32_t out_f16, void* out, int64_t total_D) {
+  float* acc = NULL;
+  for (int32_t t = 0; t < T; ++t) {
+    const int32_t ty = tys[t];
+    const int32_t D0 = D_off[t], D = D_off[t + 1] - D_off[t];
+    const int64_t stride = orc_nbit_row_bytes(ty, D, row_align);
+    if (stride < 0) {
+      free(acc);
+      return -1;
+    }
+    const int quant = ty == ORC_INT8 || ty == ORC_INT4 || ty == ORC_INT2;
+    float* tmp = (float*)realloc(acc, sizeof(float) * (D > 0 ? D : 1));
+    if (!tmp) {
+      free(acc);
+      return -2;
+    }
+    acc = tmp;
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t s = offsets[t * B + b], e = offsets[t * B + b + 1];
+      for (int32_t d = 0; d < D; ++d) acc[d] = 0.0f;
+      for (int64_t l = s; l < e; ++l) {
+        const uint8_t* row = W + w_off[t] + indices[l] * stride;
+        const float wgt = iw ? iw[l] : 1.0f;
+        if (quant) {
+          uint16_t hs, hb;
+          memcpy(&hs, row, 2);
+          memcpy(&hb, row + 2, 2);
+          float scale = orc_half_to_float(hs), bias = orc_half_to_float(hb);
+          if (iw) {
+            scale = scale * wgt;
+            bias = bias * wgt;
+          }
+          for (int32_t d = 0; d < D; ++d) acc[d] = fmaf(scale, nbit_code(row + 4, ty, d), acc[d] + bias);
+        } else {
+          for (int32_t d = 0; d < D; ++d) {
+            const float v = nbit_code(row, ty, d);
+            acc[d] = iw ? fmaf(wgt, v, acc[d]) : acc[d] + v;
+          }
+        }
+      }
+      if (pooling == ORC_POOL_MEAN && e > s) {
+        const float inv = 1.0f / (float)(e - s);
+        for (int32_t d = 0; d < D; ++d) acc[d] = acc[d] * inv;
+      }
+      if (out_f16) {
+        uint16_t* o = (uint16_t*)out + b * total_D + D0;
+        for (int32_t d = 0; d < D; ++d) o[d] = orc_float_to_half(acc[d]);
+      } else {
+        float* o = (float*)out + b * total_D + D0;
+        for (int32_t d = 0; d < D; ++d) o[d] = acc[d];
+      }
+    }
+  }
+  free(acc);
+  return 0;
+}
+
+/* ---- transpose_embedding_input -----------------------------------------------
+ * linear[l] = hash_size_cumsum[t] + indices[l]; info[l] = (t << nb) | b;
+ * (linear, info) pairs sorted stably on the low `bits` bits of linear;
+ * runs = maximal blocks of equal keys, with their lengths and the exclusive
+ * cumsum of the lengths (recalled fbgemm_gpu transpose_embedding_input:
+ * linearize_index_kernel, radix_sort_pairs, RunLengthEncode,
+ * asynchronous_complete_cumsum).  Stable merge sort on (masked key, position). */
+static const int64_t* g_sort_keys;
+static uint64_t g_sort_mask;
+
+static void merge_sort(int64_t* a, int64_t* tmp, int64_t n) {
+  if (n < 2) return;
+  const int64_t h = n / 2;
+  merge_sort(a, tmp, h);
+  merge_sort(a + h, tmp, n - h);
+  int64_t i = 0, j = h, k = 0;
+  while (i < h && j < n) {
+    const uint64_t ki = (uint64_t)g_sort_keys[a[i]] & g_sort_mask;
+    const uint64_t kj = (uint64_t)g_sort_keys[a[j]] & g_sort_mask;
+    if (kj < ki)
+      tmp[k++] = a[j++];
+    else
+      tmp[k++] = a[i++]; /* ties keep the earlier position: stable */
+  }
+  while (i < h) tmp[k++] = a[i++];
+  while (j < n) tmp[k++] = a[j++];
+  memcpy(a, tmp, sizeof(int64_t) * n);
+}
+
+int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t bits,
+                  const int64_t* indices, const int64_t* offsets, int64_t N, int64_t* linear,
+                  int64_t* sorted, int32_t* infos, int64_t* run, int32_t* run_lengths,
+                  int64_t* num_runs, int32_t* cum) {
+  uint32_t* info_raw = (uint32_t*)malloc(sizeof(uint32_t) * (N > 0 ? N : 1));
+  int64_t* perm = (int64_t*)malloc(sizeof(int64_t) * (N > 0 ? N : 1));
+  int64_t* tmp = (int64_t*)malloc(sizeof(int64_t) * (N > 0 ? N : 1));
+  if (!info_raw || !perm || !tmp) {
+    free(info_raw);
+    free(perm);
+    free(tmp);
+    return -2;
+  }
+  for (int32_t t = 0; t < T; ++t)
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t l = offsets[t * B + b]; l < offsets[t * B + b + 1]; ++l) {
+        linear[l] = hsc[t] + indices[l];
+        info_raw[l] = (nb >= 32 ? 0u : ((uint32_t)t << nb)) | (uint32_t)b;
+      }
+  for (int64_t l = 0; l < N; ++l) perm[l] = l;
+  g_sort_keys = linear;
+  g_sort_mask = bits >= 64 ? ~0ull : ((1ull << bits) - 1ull);
+  merge_sort(perm, tmp, N);
+  int64_t r = -1;
+  for (int64_t i = 0; i < N; ++i) {
+    sorted[i] = linear[perm[i]];
+    infos[i] = (int32_t)info_raw[perm[i]];
+    if (i == 0 || sorted[i] != sorted[i - 1]) {
+      ++r;
+      run[r] = sorted[i];
+      cum[r] = (int32_t)i;
+    }
+  }
+  *num_runs = r + 1;
+  cum[r + 1] = (int32_t)N;
+  for (int64_t k = 0; k <= r; ++k) run_lengths[k] = cum[k + 1] - cum[k];
+  free(info_raw);
+  free(perm);
+  free(tmp);
+  return 0;
+}
+
+/* ---- backward + exact rowwise Adagrad --------------------------------------
+ * For each run (distinct (t, i)), in sorted order of its occurrences:
+ *   g_d  = sum grad_output[b, D_off[t] + d]      (MEAN: each term * (1/L))
+ *   L2 (mode 1):   s_d = g_d + wd * w_d,  else s_d = g_d
+ *   h   += (sum_d s_d^2) / D
+ *   m    = lr / (sqrtf(h) + eps)
+ *   c    = 1 (mode 0), 1 - m*wd (mode 1), 1 - lr*wd (mode 2)
+ *   w_d  = fmaf(-m, g_d, c * w_d)
+ * (recalled rowwise_adagrad rule of fbgemm_gpu's optimizer templates). */
+int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* D_off,
+                                 int32_t T, int64_t B, const int64_t* hsc, int32_t bits,
+                                 const int64_t* indices, const int64_t* offsets, int64_t N,
+                                 int32_t pooling, const float* grad, int64_t total_D, float* m1,
+                                 const int64_t* m1_off, float lr, float eps, float wd,
+                                 int32_t wd_mode, int32_t nb) {
+  const int64_t n = N > 0 ? N : 1;
+  int64_t* linear = (int64_t*)malloc(sizeof(int64_t) * n);
+  int64_t* sorted = (int64_t*)malloc(sizeof(int64_t) * n);
+  int32_t* infos = (int32_t*)malloc(sizeof(int32_t) * n);
+  int64_t* run = (int64_t*)malloc(sizeof(int64_t) * n);
+  int32_t* lens = (int32_t*)malloc(sizeof(int32_t) * n);
+  int32_t* cum = (int32_t*)malloc(sizeof(int32_t) * (n + 1));
+  float* g = (float*)malloc(sizeof(float) * 1024);
+  int rc = 0;
+  if (!linear || !sorted || !infos || !run || !lens || !cum || !g) {
+    rc = -2;
+    goto done;
+  }
+  int64_t nruns = 0;
+  if (N > 0) {
+    rc = orc_transpose(hsc, T, B, nb, bits, indices, offsets, N, linear, sorted, infos, run,
+                       lens, &nruns, cum);
+    if (rc) goto done;
+  }
+  const uint32_t bmask = nb >= 32 ? 0xffffffffu : ((1u << nb) - 1u);
+  for (int64_t r = 0; r < nruns; ++r) {
+    const uint32_t info0 = (uint32_t)infos[cum[r]];
+    const int64_t t = nb >= 32 ? 0 : (int64_t)(info0 >> nb);
+    const int32_t D0 = D_off[t], D = D_off[t + 1] - D_off[t];
+    if (D > 1024) {
+      rc = -1;
+      goto done;
+    }
+    const int64_t idx = run[r] - hsc[t];
+    for (int32_t d = 0; d < D; ++d) g[d] = 0.0f;
+    for (int32_t j = cum[r]; j < cum[r + 1]; ++j) {
+      const int64_t b = (int64_t)((uint32_t)infos[j] & bmask);
+      const float* gr = grad + b * total_D + D0;
+      if (pooling == ORC_POOL_MEAN) {
+        const int64_t L = offsets[t * B + b + 1] - offsets[t * B + b];
+        const float sc = L > 0 ? 1.0f / (float)L : 0.0f;
+        for (int32_t d = 0; d < D; ++d) g[d] = g[d] + gr[d] * sc;
+      } else {
+        for (int32_t d = 0; d < D; ++d) g[d] = g[d] + gr[d];
+      }
+    }
+    float* w = W + w_off[t] + idx * D;
+    float ss = 0.0f;
+    for (int32_t d = 0; d < D; ++d) {
+      const float s = wd_mode == 1 ? fmaf(wd, w[d], g[d]) : g[d];
+      ss = ss + s * s;
+    }
+    float* h = m1 + m1_off[t] + idx;
+    const float hn = *h + ss / (float)D;
+    const float m = lr / (sqrtf(hn) + eps);
+    float c = 1.0f;
+    if (wd_mode == 1) c = 1.0f - m * wd;
+    if (wd_mode == 2) c = 1.0f - lr * wd;
+    for (int32_t d = 0; d < D; ++d) w[d] = fmaf(-m, g[d], c * w[d]);
+    *h = hn;
+  }
+done:
+  free(linear);
+  free(sorted);
+  free(infos);
+  free(run);
+  free(lens);
+  free(cum);
+  free(g);
+  return rc;
+}

@@ -1,0 +1,314 @@
+"""TEST INFRASTRUCTURE ONLY -- the CPU oracle of the mx_fbgemm operators.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg import this module, and only as the checker; the product never does.
+
+* Jagged ops: numpy restatement of the semantics torch's own port of the
+  fbgemm jagged ops states (torch/_inductor/jagged_lowerings.py:161-177:
+  masked load, else padding; :231-249: jagged rows past the max length
+  become 0) -- pinned against aten._jagged_to_padded_dense_forward /
+  _padded_dense_to_jagged_forward on the CPU.
+* TBE forward, nbit forward, transpose_embedding_input and the rowwise
+  Adagrad backward: the C restatement in mx_oracle.c (ctypes), pinned
+  against FBGEMM's CPU kernels (fbgemm_cpu.cpp), F.embedding_bag, torch
+  autograd and brute force.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+BUILD_DIR = ORACLE_DIR / "_build"
+ORACLE_LIB = BUILD_DIR / "libmx_oracle.so"
+FBGEMM_LIB = BUILD_DIR / "libfbgemm_cpu.so"
+
+POOL_SUM, POOL_MEAN = 0, 1
+FP32, FP16, INT8, INT4, INT2 = 0, 1, 2, 3, 4
+
+
+def build(quiet: bool = True) -> None:
+    """Compile the C checkers (make -C oracle)."""
+    import sys
+
+    subprocess.run(["make", "-C", str(ORACLE_DIR), f"PYTHON={sys.executable}"], check=True,
+                   capture_output=quiet)
+
+
+_lib = None
+_fb = None
+
+
+def _load(path: Path):
+    if not path.exists():
+        build()
+    return ctypes.CDLL(str(path))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load(ORACLE_LIB)
+        P = ctypes.c_void_p
+        i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+        _lib.orc_tbe_forward_f32.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64]
+        _lib.orc_tbe_forward_f32.restype = None
+        _lib.orc_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64]
+        _lib.orc_nbit_forward.restype = ctypes.c_int
+        _lib.orc_nbit_row_bytes.argtypes = [i32, i32, i32]
+        _lib.orc_nbit_row_bytes.restype = i64
+        _lib.orc_transpose.argtypes = [P, i32, i64, i32, i32, P, P, i64, P, P, P, P, P, P, P]
+        _lib.orc_transpose.restype = ctypes.c_int
+        _lib.orc_backward_rowwise_adagrad.argtypes = [
+            P, P, P, i32, i64, P, i32, P, P, i64, i32, P, i64, P, P, f32, f32, f32, i32, i32]
+        _lib.orc_backward_rowwise_adagrad.restype = ctypes.c_int
+        _lib.orc_half_to_float.argtypes = [ctypes.c_uint16]
+        _lib.orc_half_to_float.restype = f32
+        _lib.orc_float_to_half.argtypes = [f32]
+        _lib.orc_float_to_half.restype = ctypes.c_uint16
+    return _lib
+
+
+def fbgemm():
+    global _fb
+    if _fb is None:
+        import torch  # noqa: F401  (loads libtorch_cpu, which exports the kernels)
+
+        _fb = _load(FBGEMM_LIB)
+        P = ctypes.c_void_p
+        i32, i64 = ctypes.c_int32, ctypes.c_int64
+        _fb.fb_tbe_forward_f32.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64, P, i32]
+        _fb.fb_tbe_forward_f32.restype = ctypes.c_int
+        _fb.fb_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64, P,
+                                        i32]
+        _fb.fb_nbit_forward.restype = ctypes.c_int
+    return _fb
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# Jagged ops (numpy)
+# ---------------------------------------------------------------------------
+
+
+def dense_index_map(offsets: list[np.ndarray], max_lengths: list[int]) -> np.ndarray:
+    """int64 array [B, *max_lengths]: the values row at each dense position, or -1."""
+    offs = [np.asarray(o, dtype=np.int64) for o in offsets]
+    B = offs[0].shape[0] - 1
+    cur = np.arange(B, dtype=np.int64)
+    valid = np.ones(B, dtype=bool)
+    for k, o in enumerate(offs):
+        safe = np.where(valid, cur, 0)
+        begin = o[safe]
+        length = o[safe + 1] - begin
+        j = np.arange(max_lengths[k], dtype=np.int64)
+        nvalid = valid[..., None] & (j < length[..., None])
+        cur = np.where(nvalid, begin[..., None] + j, 0)
+        valid = nvalid
+    return np.where(valid, cur, -1)
+
+
+def jagged_to_padded_dense(values: np.ndarray, offsets, max_lengths, padding_value=0.0):
+    values = np.asarray(values)
+    m = dense_index_map(offsets, list(max_lengths))
+    inner = values.shape[1:]
+    out = np.empty(m.shape + inner, dtype=values.dtype)
+    out[...] = np.asarray(padding_value).astype(values.dtype)
+    sel = m >= 0
+    out[sel] = values[m[sel]]
+    return out
+
+
+def dense_to_jagged(dense: np.ndarray, offsets, total_L=None):
+    dense = np.asarray(dense)
+    nd = len(offsets)
+    max_lengths = list(dense.shape[1:1 + nd])
+    if total_L is None:
+        total_L = int(np.asarray(offsets[-1])[-1])
+    m = dense_index_map(offsets, max_lengths)
+    inner = dense.shape[1 + nd:]
+    out = np.zeros((total_L,) + inner, dtype=dense.dtype)
+    sel = (m >= 0) & (m < total_L)
+    out[m[sel]] = dense[sel]
+    return out
+
+
+def _bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+def _f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    u = f.astype(np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def jagged_dense_elementwise_add(x: np.ndarray, offsets, y: np.ndarray, dtype: str):
+    """out[i] = x[i] + y[coord(i)] (x[i] + 0 outside y); f16/bf16 in fp32, RNE.
+
+    ``dtype`` is one of "f32", "f64", "f16", "bf16"; bf16 arrays are passed
+    as their uint16 bit patterns."""
+    nd = len(offsets)
+    yz = dense_to_jagged(y, offsets, total_L=x.shape[0])  # y at each jagged row, 0 elsewhere
+    if dtype == "f32":
+        return (x.astype(np.float32) + yz.astype(np.float32)).astype(np.float32)
+    if dtype == "f64":
+        return x.astype(np.float64) + yz.astype(np.float64)
+    if dtype == "f16":
+        return (x.astype(np.float32) + yz.astype(np.float32)).astype(np.float16)
+    if dtype == "bf16":
+        return _f32_to_bf16(_bf16_to_f32(x) + _bf16_to_f32(yz))
+    raise ValueError(dtype)
+    del nd
+
+
+# ---------------------------------------------------------------------------
+# TBE (C restatement)
+# ---------------------------------------------------------------------------
+
+
+def tbe_forward_f32(W, w_off, D_off, B, indices, offsets, pooling=POOL_SUM, indice_weights=None):
+    W = _c(W, np.float32)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    iw = _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    total_D = int(D_off[-1])
+    out = np.zeros((B, total_D), dtype=np.float32)
+    lib().orc_tbe_forward_f32(_p(W), _p(w_off), _p(D_off), T, B, _p(indices), _p(offsets),
+                              pooling, _p(iw), _p(out), total_D)
+    return out
+
+
+def nbit_row_bytes(ty: int, D: int, row_align: int) -> int:
+    return int(lib().orc_nbit_row_bytes(ty, D, row_align))
+
+
+def nbit_forward(W, w_off, tys, D_off, B, indices, offsets, pooling=POOL_SUM,
+                 indice_weights=None, row_align=16, out_f16=True):
+    W = _c(W, np.uint8)
+    w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    iw = _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    total_D = int(D_off[-1])
+    out = np.zeros((B, total_D), dtype=np.float16 if out_f16 else np.float32)
+    rc = lib().orc_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
+                                _p(offsets), pooling, _p(iw), row_align, int(out_f16), _p(out),
+                                total_D)
+    assert rc == 0, f"orc_nbit_forward failed ({rc})"
+    return out
+
+
+def transpose_embedding_input(hsc, B, info_B_num_bits, bits, indices, offsets):
+    hsc = _c(hsc, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    T = hsc.shape[0] - 1
+    N = indices.shape[0]
+    n = max(N, 1)
+    linear = np.zeros(n, np.int64)
+    srt = np.zeros(n, np.int64)
+    infos = np.zeros(n, np.int32)
+    run = np.zeros(n, np.int64)
+    lengths = np.zeros(n, np.int32)
+    cum = np.zeros(n + 1, np.int32)
+    num_runs = np.zeros(1, np.int64)
+    if N:
+        rc = lib().orc_transpose(_p(hsc), T, B, info_B_num_bits, bits, _p(indices), _p(offsets),
+                                 N, _p(linear), _p(srt), _p(infos), _p(run), _p(lengths),
+                                 _p(num_runs), _p(cum))
+        assert rc == 0
+    r = int(num_runs[0])
+    return dict(linear_indices=linear[:N], sorted_linear_indices=srt[:N], infos_sorted=infos[:N],
+                run=run[:r], run_lengths=lengths[:r], num_runs=r, cumulative_run_lengths=cum[:r + 1])
+
+
+def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,
+                             momentum1, m1_off, lr, eps, weight_decay=0.0, weight_decay_mode=0,
+                             info_B_num_bits=26):
+    """Updates copies of W and momentum1; returns (W_new, momentum1_new)."""
+    W = np.array(W, dtype=np.float32, copy=True)
+    m1 = np.array(momentum1, dtype=np.float32, copy=True)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    hsc, m1_off = _c(hsc, np.int64), _c(m1_off, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    grad = _c(grad, np.float32)
+    T = D_off.shape[0] - 1
+    rc = lib().orc_backward_rowwise_adagrad(
+        _p(W), _p(w_off), _p(D_off), T, B, _p(hsc), bits, _p(indices), _p(offsets),
+        indices.shape[0], pooling, _p(grad), grad.shape[1], _p(m1), _p(m1_off), lr, eps,
+        weight_decay, weight_decay_mode, info_B_num_bits)
+    assert rc == 0, f"orc_backward_rowwise_adagrad failed ({rc})"
+    return W, m1
+
+
+def info_B_num_bits(T: int, B: int) -> int:
+    """Bits of b in an info word: 26 unless T or B need another split."""
+    tb = max(0, int(T - 1).bit_length())
+    bb = max(1, int(B - 1).bit_length())
+    if tb + bb > 32:
+        raise ValueError("T, B do not fit 32 bits")
+    if bb <= 26 and tb <= 6:
+        return 26
+    return 32 - tb
+
+
+# ---------------------------------------------------------------------------
+# FBGEMM CPU kernels (pins and CPU baseline)
+# ---------------------------------------------------------------------------
+
+
+def fbgemm_tbe_forward_f32(W, w_off, D_off, rows_per_table, B, indices, offsets, pooling=POOL_SUM,
+                           indice_weights=None, nthreads=1):
+    W = _c(W, np.float32)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    rows = _c(rows_per_table, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    iw = _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    total_D = int(D_off[-1])
+    out = np.zeros((B, total_D), dtype=np.float32)
+    rc = fbgemm().fb_tbe_forward_f32(_p(W), _p(w_off), _p(D_off), T, B, _p(indices), _p(offsets),
+                                     pooling, _p(iw), _p(out), total_D, _p(rows), nthreads)
+    assert rc == 0, f"FBGEMM SpMDM kernel reported failure ({rc})"
+    return out
+
+
+def fbgemm_nbit_forward(W, w_off, tys, D_off, rows_per_table, B, indices, offsets,
+                        pooling=POOL_SUM, indice_weights=None, row_align=16, nthreads=1):
+    W = _c(W, np.uint8)
+    w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
+    rows = _c(rows_per_table, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    iw = _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    total_D = int(D_off[-1])
+    out = np.zeros((B, total_D), dtype=np.float16)
+    rc = fbgemm().fb_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
+                                  _p(offsets), pooling, _p(iw), row_align, 1, _p(out), total_D,
+                                  _p(rows), nthreads)
+    assert rc == 0, f"FBGEMM nbit kernel reported failure ({rc})"
+    return out
+
+
+def host_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1

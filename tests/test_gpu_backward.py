@@ -1,0 +1,176 @@
+"""GPU parity of the TBE backward: transpose_embedding_input (sorted keys,
+infos and run layout: bit-exact) and the fused exact rowwise-Adagrad update
+(weights and momentum within rtol 1e-5 of the oracle; rows the batch does
+not touch bit-identical)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from mx_fbgemm import bench_inputs
+from tbe_helpers import random_tbe, weight_offsets
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-7
+
+
+def _transpose_gpu(dev, inp, info_bits, index_dtype=torch.int64):
+    return torch.ops.fbgemm.transpose_embedding_input(
+        torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+        torch.from_numpy(inp.indices).to(dev, index_dtype),
+        torch.from_numpy(inp.offsets).to(dev, index_dtype), False, None, info_bits)
+
+
+def _check_transpose(dev, inp, index_dtype=torch.int64):
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    exp = orc.transpose_embedding_input(inp.hash_size_cumsum, inp.B, nb, inp.total_hash_size_bits,
+                                        inp.indices, inp.offsets)
+    lin, srt, infos, run, lengths, num_runs, cum = _transpose_gpu(dev, inp, nb, index_dtype)
+    r = int(num_runs.item())
+    assert r == exp["num_runs"]
+    np.testing.assert_array_equal(lin.cpu().numpy(), exp["linear_indices"])
+    np.testing.assert_array_equal(srt.cpu().numpy(), exp["sorted_linear_indices"])
+    np.testing.assert_array_equal(infos.cpu().numpy(), exp["infos_sorted"])
+    np.testing.assert_array_equal(run.cpu().numpy()[:r], exp["run"])
+    np.testing.assert_array_equal(lengths.cpu().numpy()[:r], exp["run_lengths"])
+    np.testing.assert_array_equal(cum.cpu().numpy()[: r + 1], exp["cumulative_run_lengths"])
+
+
+@pytest.mark.parametrize("T,B,rows,max_L,dup", [
+    (1, 1, [1], 1, False),
+    (3, 50, [10, 1000, 70000], 20, False),
+    (2, 300, [5000, 5000], 40, True),      # runs far longer than 64 occurrences
+    (5, 700, [2 ** 20, 3, 100, 9, 2 ** 21], 10, False),  # 22+ key bits: 3 radix passes
+])
+def test_transpose_bit_exact(dev, T, B, rows, max_L, dup):
+    print(f"[case] transpose T={T} B={B} rows={rows}", flush=True)
+    rng = np.random.default_rng(T * 7 + B)
+    inp = random_tbe(rng, T, B, [4] * T, rows, max_L, dup_heavy=dup)
+    _check_transpose(dev, inp)
+    _check_transpose(dev, inp, torch.int32)
+
+
+def _backward_case(dev, inp, pooling, wd=0.0, wd_mode=0, lr=0.01, eps=1e-8, seed=0):
+    rng = np.random.default_rng(seed)
+    W = rng.uniform(-0.01, 0.01, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
+    m1 = rng.uniform(0, 1e-4, size=sum(inp.E)).astype(np.float32)
+    m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
+    grad = rng.normal(0, 1e-2, size=(inp.B, inp.total_D)).astype(np.float32)
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    W_exp, m1_exp = orc.backward_rowwise_adagrad(
+        W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
+        wd, wd_mode, nb)
+    Wd = torch.from_numpy(W).to(dev)
+    m1d = torch.from_numpy(m1).to(dev)
+    empty = torch.zeros(0, device=dev)
+    torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+        torch.from_numpy(grad).to(dev), Wd, empty, empty,
+        torch.zeros(inp.T, dtype=torch.int32, device=dev),
+        torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
+        max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
+        torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty,
+        torch.zeros(inp.T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
+        eps, lr, wd, wd_mode, 0.0)
+    Wg, mg = Wd.cpu().numpy(), m1d.cpu().numpy()
+    np.testing.assert_allclose(mg, m1_exp, rtol=RTOL, atol=0)
+    np.testing.assert_allclose(Wg, W_exp, rtol=RTOL, atol=ATOL)
+    untouched = W_exp == W  # rows the batch never touched must stay bit-identical
+    assert np.array_equal(Wg[untouched], W[untouched])
+    return Wg, W_exp
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("T,B,dims,rows,max_L,dup", [
+    (2, 40, [128, 128], [300, 300], 20, False),
+    (3, 64, [4, 64, 256], [50, 2000, 40], 30, False),
+    (2, 200, [128, 1024], [4, 4], 40, True),       # long runs -> chunked path
+    (1, 3, [128], [1], 2, False),                  # single row, single table
+])
+def test_backward_rowwise_adagrad(dev, pooling, T, B, dims, rows, max_L, dup):
+    print(f"[case] backward T={T} B={B} dims={dims} pool={pooling} dup={dup}", flush=True)
+    rng = np.random.default_rng(B + T)
+    inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
+    _backward_case(dev, inp, pooling, seed=B)
+
+
+@pytest.mark.parametrize("wd_mode,wd", [(1, 0.1), (2, 0.05)])
+def test_backward_weight_decay(dev, wd_mode, wd):
+    print(f"[case] backward weight decay mode {wd_mode}", flush=True)
+    rng = np.random.default_rng(3)
+    inp = random_tbe(rng, 2, 50, [64, 128], [100, 100], 15)
+    _backward_case(dev, inp, 0, wd=wd, wd_mode=wd_mode)
+
+
+def test_config3_full(dev):
+    """Config 3: config-2 indices (Zipf 1.05, up to ~8k duplicates of one row),
+    8 x 1M x 128 fp32 tables, grad N(0, 1e-2), lr 0.01, eps 1e-8, zero momentum.
+    Transpose bit-exact; updated weights/momentum vs oracle at rtol 1e-5."""
+    print("[case] config3 full size", flush=True)
+    inp = bench_inputs.config2()
+    _check_transpose(dev, inp)
+    rng = np.random.default_rng(33)
+    E, D, T = 1_000_000, 128, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    Wd = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    W = Wd.cpu().numpy()
+    m1 = np.zeros(T * E, np.float32)
+    m1d = torch.zeros(T * E, device=dev)
+    grad = rng.normal(0, 1e-2, size=(inp.B, inp.total_D)).astype(np.float32)
+    m1_off = (np.arange(T) * E).astype(np.int64)
+    W_exp, m1_exp = orc.backward_rowwise_adagrad(
+        W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, 0, grad, m1, m1_off, 0.01, 1e-8,
+        0.0, 0, orc.info_B_num_bits(T, inp.B))
+    empty = torch.zeros(0, device=dev)
+    torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+        torch.from_numpy(grad).to(dev), Wd, empty, empty, torch.zeros(T, dtype=torch.int32, device=dev),
+        torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev), D,
+        torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), 0,
+        torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty,
+        torch.zeros(T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
+        1e-8, 0.01, 0.0, 0, 0.0)
+    mg = m1d.cpu().numpy()
+    np.testing.assert_allclose(mg, m1_exp, rtol=RTOL, atol=0)
+    touched = np.flatnonzero(m1_exp)
+    Wg = Wd.cpu().numpy().reshape(T * E, D)
+    np.testing.assert_allclose(Wg[touched], W_exp.reshape(T * E, D)[touched], rtol=RTOL, atol=ATOL)
+    untouched = np.ones(T * E, bool)
+    untouched[touched] = False
+    assert np.array_equal(Wg[untouched], W.reshape(T * E, D)[untouched])
+
+
+def test_module_training_step(dev):
+    """SplitTableBatchedEmbeddingBagsCodegen: forward, loss.backward() applies
+    the fused update; equals forward + oracle update."""
+    print("[case] module training step", flush=True)
+    from mx_fbgemm import ComputeDevice, EmbeddingLocation, PoolingMode
+    from mx_fbgemm.split_table_batched_embeddings_ops_training import (
+        SplitTableBatchedEmbeddingBagsCodegen,
+    )
+
+    specs = [(500, 64, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (300, 128, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)]
+    tbe = SplitTableBatchedEmbeddingBagsCodegen(specs, pooling_mode=PoolingMode.MEAN,
+                                                learning_rate=0.05, eps=1e-6, device=dev)
+    rng = np.random.default_rng(9)
+    inp = random_tbe(rng, 2, 32, [64, 128], [500, 300], 10)
+    W0 = tbe.weights_dev.detach().cpu().numpy().copy()
+    out = tbe(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev))
+    exp = orc.tbe_forward_f32(W0, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, 1)
+    assert np.array_equal(out.detach().cpu().numpy(), exp)
+    gout = torch.from_numpy(rng.normal(0, 1, size=out.shape).astype(np.float32)).to(dev)
+    out.backward(gout)
+    W_exp, m_exp = orc.backward_rowwise_adagrad(
+        W0, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, 1, gout.cpu().numpy(),
+        np.zeros(800, np.float32), np.array([0, 500], np.int64), 0.05, 1e-6, 0.0, 0,
+        orc.info_B_num_bits(2, 32))
+    np.testing.assert_allclose(tbe.weights_dev.detach().cpu().numpy(), W_exp, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)

@@ -1,0 +1,133 @@
+"""GPU parity of the jagged ops against the oracle: bit-exact (pure data
+movement, and one correctly rounded add per element)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from mx_fbgemm import bench_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _offsets(lengths):
+    return bench_inputs.offsets_from_lengths(np.asarray(lengths, dtype=np.int64))
+
+
+def _bits_equal(a: torch.Tensor, b: np.ndarray):
+    a = a.detach().cpu().contiguous()
+    if a.dtype == torch.bfloat16:
+        a = a.view(torch.int16)
+        b = np.asarray(b).view(np.int16)
+    an = a.numpy()
+    assert an.shape == b.shape, (an.shape, b.shape)
+    assert an.tobytes() == np.ascontiguousarray(b).astype(an.dtype).tobytes()
+
+
+CASES = [
+    # (lengths, max_L, D)
+    ([3, 0, 5, 1], 4, 8),          # truncation (len 5 > max_L 4) and an empty row
+    ([0, 0, 0], 3, 16),            # all empty
+    ([7], 7, 3),                   # odd inner size -> 4-byte path
+    ([1, 2, 3, 4, 5, 6], 6, 128),  # 16-byte path
+    ([2, 9, 0, 4], 3, 1),          # inner 1
+]
+
+
+@pytest.mark.parametrize("lengths,max_L,D", CASES)
+@pytest.mark.parametrize("offset_dtype", [torch.int64, torch.int32])
+def test_jagged_to_padded_dense(dev, lengths, max_L, D, offset_dtype):
+    print(f"[case] j2pd lengths={lengths} max_L={max_L} D={D} {offset_dtype}", flush=True)
+    rng = np.random.default_rng(1)
+    off = _offsets(lengths)
+    vals = rng.standard_normal((int(off[-1]), D)).astype(np.float32)
+    exp = orc.jagged_to_padded_dense(vals, [off], [max_L], padding_value=-7.5)
+    got = torch.ops.fbgemm.jagged_to_padded_dense(
+        torch.from_numpy(vals).to(dev), [torch.from_numpy(off).to(dev, offset_dtype)], [max_L],
+        -7.5)
+    _bits_equal(got, exp)
+
+
+@pytest.mark.parametrize("lengths,max_L,D", CASES)
+def test_dense_to_jagged(dev, lengths, max_L, D):
+    print(f"[case] d2j lengths={lengths} max_L={max_L} D={D}", flush=True)
+    rng = np.random.default_rng(2)
+    off = _offsets(lengths)
+    dense = rng.standard_normal((len(lengths), max_L, D)).astype(np.float32)
+    exp = orc.dense_to_jagged(dense, [off])
+    got, got_off = torch.ops.fbgemm.dense_to_jagged(torch.from_numpy(dense).to(dev),
+                                                     [torch.from_numpy(off).to(dev)])
+    _bits_equal(got, exp)
+    assert torch.equal(got_off[0].cpu(), torch.from_numpy(off))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64", "f16", "bf16"])
+@pytest.mark.parametrize("lengths,max_L,D", CASES[:4])
+def test_jagged_dense_add(dev, dtype, lengths, max_L, D):
+    print(f"[case] add {dtype} lengths={lengths} max_L={max_L} D={D}", flush=True)
+    rng = np.random.default_rng(3)
+    off = _offsets(lengths)
+    x = rng.standard_normal((int(off[-1]), D)).astype(np.float32)
+    y = rng.standard_normal((len(lengths), max_L, D)).astype(np.float32)
+    tdt = {"f32": torch.float32, "f64": torch.float64, "f16": torch.float16,
+           "bf16": torch.bfloat16}[dtype]
+    xt = torch.from_numpy(x).to(tdt)
+    yt = torch.from_numpy(y).to(tdt)
+    if dtype == "bf16":
+        xn, yn = xt.view(torch.int16).numpy().view(np.uint16), yt.view(torch.int16).numpy().view(np.uint16)
+    else:
+        xn, yn = xt.numpy(), yt.numpy()
+    exp = orc.jagged_dense_elementwise_add(xn, [off], yn, dtype)
+    got, _ = torch.ops.fbgemm.jagged_dense_elementwise_add_jagged_output(
+        xt.to(dev), [torch.from_numpy(off).to(dev)], yt.to(dev))
+    _bits_equal(got, exp)
+
+
+def test_two_jagged_dims(dev):
+    print("[case] j2pd/d2j two jagged dims", flush=True)
+    rng = np.random.default_rng(4)
+    off0 = _offsets([2, 0, 3])          # 5 level-1 rows
+    off1 = _offsets([1, 4, 0, 2, 3])    # 10 values rows
+    vals = rng.standard_normal((10, 6)).astype(np.float32)
+    exp = orc.jagged_to_padded_dense(vals, [off0, off1], [2, 3], 0.0)
+    offs = [torch.from_numpy(off0).to(dev), torch.from_numpy(off1).to(dev)]
+    got = torch.ops.fbgemm.jagged_to_padded_dense(torch.from_numpy(vals).to(dev), offs, [2, 3])
+    _bits_equal(got, exp)
+    back = torch.ops.fbgemm.dense_to_jagged_forward(got, offs)
+    _bits_equal(back, orc.dense_to_jagged(exp, [off0, off1]))
+
+
+def test_config1_round_trip(dev):
+    """Config 1: j2pd then d2j returns the values bit for bit (all len <= max_L)."""
+    print("[case] config1 round trip B=512 D=128 max_L=64", flush=True)
+    cfg = bench_inputs.config1()
+    v = torch.from_numpy(cfg.values).to(dev)
+    off = torch.from_numpy(cfg.offsets).to(dev)
+    dense = torch.ops.fbgemm.jagged_to_padded_dense(v, [off], [cfg.max_L], 0.0)
+    _bits_equal(dense, orc.jagged_to_padded_dense(cfg.values, [cfg.offsets], [cfg.max_L], 0.0))
+    back, _ = torch.ops.fbgemm.dense_to_jagged(dense, [off])
+    assert torch.equal(back, v)
+
+
+def test_autograd(dev):
+    print("[case] jagged autograd", flush=True)
+    rng = np.random.default_rng(5)
+    off = _offsets([2, 5, 0, 3])
+    vals = torch.from_numpy(rng.standard_normal((10, 4)).astype(np.float32)).to(dev)
+    vals.requires_grad_(True)
+    offt = torch.from_numpy(off).to(dev)
+    dense = torch.ops.fbgemm.jagged_to_padded_dense(vals, [offt], [4], 0.0)
+    g = torch.from_numpy(rng.standard_normal((4, 4, 4)).astype(np.float32)).to(dev)
+    (dense * g).sum().backward()
+    exp = orc.dense_to_jagged(g.cpu().numpy(), [off], total_L=10)  # truncated rows get 0
+    _bits_equal(vals.grad, exp)
+
+    y = torch.from_numpy(rng.standard_normal((4, 4, 4)).astype(np.float32)).to(dev)
+    y.requires_grad_(True)
+    x = vals.detach().clone().requires_grad_(True)
+    out, _ = torch.ops.fbgemm.jagged_dense_elementwise_add_jagged_output(x, [offt], y)
+    gout = torch.from_numpy(rng.standard_normal((10, 4)).astype(np.float32)).to(dev)
+    (out * gout).sum().backward()
+    _bits_equal(x.grad, gout.cpu().numpy())
+    _bits_equal(y.grad, orc.jagged_to_padded_dense(gout.cpu().numpy(), [off], [4], 0.0))

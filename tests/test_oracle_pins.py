@@ -1,0 +1,286 @@
+"""CPU pins of the oracle (no GPU): every oracle function is checked against
+an independent in-container implementation, brute force or a closed form,
+chosen so that a dropped term, a wrong index or a transposed operand fails.
+
+* jagged: aten._jagged_to_padded_dense_forward / _padded_dense_to_jagged_forward
+  (torch's port of the fbgemm jagged ops), bit-exact;
+* TBE forward: FBGEMM's exported CPU SpMDM kernel (the CPU kernel fbgemm_gpu's
+  CPU TBE op wraps), bit-exact; F.embedding_bag within fp32 rounding;
+* nbit: FBGEMM's exported 8-bit / N-bit / fp16 CPU kernels with the TBE row
+  layout (scale_bias_last=false), fp16 output;
+* transpose: numpy stable argsort + unique (brute force), bit-exact;
+* rowwise Adagrad: torch autograd of embedding_bag for the row gradient and
+  the update rule evaluated with torch fp32 ops.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from mx_fbgemm import bench_inputs
+from nbit_helpers import build_weights
+from tbe_helpers import random_tbe, weight_offsets
+
+
+# ---- jagged -----------------------------------------------------------------
+
+@pytest.mark.parametrize("lengths,max_L", [([3, 0, 5, 1], 4), ([0], 2), ([2, 2], 2),
+                                           ([9, 1, 0, 4, 7], 6)])
+def test_jagged_to_padded_dense_vs_aten(lengths, max_L):
+    rng = np.random.default_rng(0)
+    off = bench_inputs.offsets_from_lengths(np.array(lengths))
+    vals = rng.standard_normal((int(off[-1]), 5)).astype(np.float32)
+    exp = torch.ops.aten._jagged_to_padded_dense_forward(
+        torch.from_numpy(vals), [torch.from_numpy(off)], [max_L], 1.25).numpy()
+    got = orc.jagged_to_padded_dense(vals, [off], [max_L], 1.25)
+    assert got.tobytes() == exp.tobytes()
+
+
+@pytest.mark.parametrize("lengths,max_L", [([3, 0, 4, 1], 4), ([2, 2], 2), ([0, 0], 3)])
+def test_dense_to_jagged_vs_aten(lengths, max_L):
+    rng = np.random.default_rng(1)
+    off = bench_inputs.offsets_from_lengths(np.array(lengths))
+    dense = rng.standard_normal((len(lengths), max_L, 3)).astype(np.float32)
+    exp = torch.ops.aten._padded_dense_to_jagged_forward(
+        torch.from_numpy(dense), [torch.from_numpy(off)], int(off[-1])).numpy()
+    got = orc.dense_to_jagged(dense, [off])
+    assert got.tobytes() == exp.tobytes()
+
+
+def test_dense_to_jagged_truncated_rows_are_zero():
+    # A row longer than max_L: positions past max_L have no dense source -> 0
+    # (torch/_inductor/jagged_lowerings.py:248).  aten raises here, so the pin
+    # is the closed form.
+    off = np.array([0, 5], np.int64)
+    dense = np.arange(1 * 3 * 2, dtype=np.float32).reshape(1, 3, 2) + 1
+    got = orc.dense_to_jagged(dense, [off])
+    np.testing.assert_array_equal(got[:3], dense[0])
+    np.testing.assert_array_equal(got[3:], 0)
+
+
+def test_jagged_add_closed_form_and_rounding():
+    off = np.array([0, 2, 5], np.int64)
+    x = np.arange(10, dtype=np.float32).reshape(5, 2)
+    y = np.full((2, 2, 2), 0.5, np.float32)
+    got = orc.jagged_dense_elementwise_add(x, [off], y, "f32")
+    exp = x.copy()
+    exp[[0, 1, 2, 3]] += 0.5  # row 4 (j=2 of bag 1) lies past max_L=2 -> x + 0
+    np.testing.assert_array_equal(got, exp)
+    # f16: computed in fp32 then rounded once (2049 + 1 = 2050 exactly; 2048+1 ties to even)
+    xh = np.array([[2048.0]], np.float16)
+    yh = np.array([[[1.0]]], np.float16)
+    r = orc.jagged_dense_elementwise_add(xh, [np.array([0, 1])], yh, "f16")
+    assert r[0, 0] == np.float16(2048.0)
+    # bf16 round-to-nearest-even of 1 + 2^-8 (a tie) stays 1.0
+    xb = np.array([[0x3F80]], np.uint16)
+    yb = np.array([[[0x3B80]]], np.uint16)  # 2^-8
+    rb = orc.jagged_dense_elementwise_add(xb, [np.array([0, 1])], yb, "bf16")
+    assert rb[0, 0] == 0x3F80
+
+
+def test_two_level_index_map_brute_force():
+    off0 = np.array([0, 2, 2, 5])
+    off1 = np.array([0, 1, 5, 5, 7, 10])
+    m = orc.dense_index_map([off0, off1], [2, 3])
+    for b in range(3):
+        for j0 in range(2):
+            for j1 in range(3):
+                exp = -1
+                if j0 < off0[b + 1] - off0[b]:
+                    r = off0[b] + j0
+                    if j1 < off1[r + 1] - off1[r]:
+                        exp = off1[r] + j1
+                assert m[b, j0, j1] == exp
+
+
+# ---- TBE forward ------------------------------------------------------------
+
+def _tbe_case(seed, T=3, B=20, dims=(8, 128, 36), rows=(50, 70, 9), max_L=12):
+    rng = np.random.default_rng(seed)
+    inp = random_tbe(rng, T, B, list(dims), list(rows), max_L)
+    W = rng.uniform(-1, 1, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    return inp, W
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_tbe_forward_vs_fbgemm_cpu(pooling, weighted):
+    inp, W = _tbe_case(3)
+    iw = np.random.default_rng(4).uniform(0, 2, inp.N).astype(np.float32) if weighted else None
+    got = orc.tbe_forward_f32(W, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, pooling, iw)
+    exp = orc.fbgemm_tbe_forward_f32(W, weight_offsets(inp), inp.D_offsets, inp.E, inp.B,
+                                     inp.indices, inp.offsets, pooling, iw, nthreads=2)
+    np.testing.assert_array_equal(got, exp)  # bit-exact
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_tbe_forward_vs_embedding_bag(pooling):
+    inp, W = _tbe_case(5)
+    got = orc.tbe_forward_f32(W, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, pooling)
+    w_off = weight_offsets(inp)
+    for t in range(inp.T):
+        Wt = torch.from_numpy(W[w_off[t]: w_off[t] + inp.E[t] * inp.D[t]].reshape(inp.E[t], -1))
+        o = inp.offsets[t * inp.B:(t + 1) * inp.B + 1]
+        ref = torch.nn.functional.embedding_bag(
+            torch.from_numpy(inp.indices[o[0]:o[-1]]), Wt, torch.from_numpy(o[:-1] - o[0]),
+            mode="sum" if pooling == 0 else "mean")
+        d0, d1 = inp.D_offsets[t], inp.D_offsets[t + 1]
+        np.testing.assert_allclose(got[:, d0:d1], ref.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_tbe_forward_closed_form():
+    # Two tables, bag sums written by hand.
+    W = np.arange(2 * 4 + 3 * 4, dtype=np.float32)
+    w_off = np.array([0, 8], np.int64)
+    D_off = np.array([0, 4, 8], np.int32)
+    idx = np.array([1, 1, 0, 2, 0], np.int64)
+    off = np.array([0, 2, 3, 5], np.int64)  # T=2? -> 3 bags: needs T*B+1; use B=1? see below
+    # T=2, B=1 would need 3 offsets; use bags (t0,b0)=[1,1], (t1,b0)=[0]  and check
+    off = np.array([0, 2, 3], np.int64)
+    out = orc.tbe_forward_f32(W, w_off, D_off, 1, idx[:3], off, 0)
+    np.testing.assert_array_equal(out[0, :4], 2 * W[4:8])
+    np.testing.assert_array_equal(out[0, 4:], W[8:12])
+    out = orc.tbe_forward_f32(W, w_off, D_off, 1, idx[:3], off, 1)
+    np.testing.assert_array_equal(out[0, :4], W[4:8])  # mean of a repeated row
+
+
+# ---- nbit -------------------------------------------------------------------
+
+@pytest.mark.parametrize("ty", [orc.INT8, orc.INT4, orc.INT2, orc.FP16, orc.FP32])
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_nbit_vs_fbgemm_cpu(ty, pooling):
+    rng = np.random.default_rng(ty * 10 + pooling)
+    dims = [32, 64]
+    rows = [40, 70]
+    inp = random_tbe(rng, 2, 15, dims, rows, 20)
+    buf, w_off = build_weights(rng, [ty, ty], dims, rows)
+    got = orc.nbit_forward(buf, w_off, [ty, ty], inp.D_offsets, inp.B, inp.indices, inp.offsets,
+                           pooling)
+    exp = orc.fbgemm_nbit_forward(buf, w_off, [ty, ty], inp.D_offsets, rows, inp.B, inp.indices,
+                                  inp.offsets, pooling, nthreads=2)
+    # Same terms, same order, same fp32 fma steps: bit-exact fp16 output.
+    np.testing.assert_array_equal(got.view(np.uint16), exp.view(np.uint16))
+
+
+def test_nbit_int8_vs_quantized_embedding_bag_byte():
+    # torch's byte rowwise op keeps fp32 scale/bias at the row end; move ours there.
+    rng = np.random.default_rng(12)
+    E, D, B = 60, 16, 9
+    inp = random_tbe(rng, 1, B, [D], [E], 7)
+    buf, w_off = build_weights(rng, [orc.INT8], [D], [E])
+    stride = orc.nbit_row_bytes(orc.INT8, D, 16)
+    tab = buf.reshape(E, stride)
+    sc = tab[:, 0:2].copy().view(np.float16).astype(np.float32)
+    bi = tab[:, 2:4].copy().view(np.float16).astype(np.float32)
+    packed = np.concatenate([tab[:, 4:4 + D], sc.view(np.uint8).reshape(E, 4),
+                             bi.view(np.uint8).reshape(E, 4)], axis=1)
+    ref = torch.ops.quantized.embedding_bag_byte_rowwise_offsets(
+        torch.from_numpy(packed), torch.from_numpy(inp.indices), torch.from_numpy(inp.offsets),
+        False, 0, False, None, None, True).numpy()
+    got = orc.nbit_forward(buf, w_off, [orc.INT8], inp.D_offsets, B, inp.indices, inp.offsets, 0,
+                           out_f16=False)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_fp16_conversion_matches_numpy():
+    lib = orc.lib()
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000),
+                         np.array([65504, 65519.99, 65520, 6e-8, 3e-8, 2.98e-8, -0.0, np.inf,
+                                   -np.inf, 5.96e-8], np.float32)]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = xs.astype(np.float16).view(np.uint16)
+    got = np.array([lib.orc_float_to_half(float(x)) for x in xs], np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    h = np.arange(0, 65536, dtype=np.uint32).astype(np.uint16)
+    back = np.array([lib.orc_half_to_float(int(v)) for v in h[::7]], np.float32)
+    hv = h[::7].view(np.float16).astype(np.float32)
+    finite = np.isfinite(hv)
+    np.testing.assert_array_equal(back[finite], hv[finite])
+
+
+# ---- transpose + backward ---------------------------------------------------
+
+@pytest.mark.parametrize("seed,T,B,rows,dup", [(0, 3, 40, [10, 1000, 7], False),
+                                                (1, 2, 100, [4, 4], True),
+                                                (2, 1, 1, [1], False)])
+def test_transpose_vs_numpy(seed, T, B, rows, dup):
+    rng = np.random.default_rng(seed)
+    inp = random_tbe(rng, T, B, [4] * T, rows, 15, dup_heavy=dup)
+    nb = orc.info_B_num_bits(T, B)
+    got = orc.transpose_embedding_input(inp.hash_size_cumsum, B, nb, inp.total_hash_size_bits,
+                                        inp.indices, inp.offsets)
+    bag = np.repeat(np.arange(T * B), np.diff(inp.offsets))
+    t, b = bag // B, bag % B
+    lin = inp.hash_size_cumsum[t] + inp.indices
+    info = (t.astype(np.int64) << nb) | b
+    order = np.argsort(lin, kind="stable")
+    np.testing.assert_array_equal(got["linear_indices"], lin)
+    np.testing.assert_array_equal(got["sorted_linear_indices"], lin[order])
+    np.testing.assert_array_equal(got["infos_sorted"].astype(np.int64) & 0xFFFFFFFF, info[order])
+    u, first, counts = np.unique(lin[order], return_index=True, return_counts=True)
+    np.testing.assert_array_equal(got["run"], u)
+    np.testing.assert_array_equal(got["run_lengths"], counts)
+    np.testing.assert_array_equal(got["cumulative_run_lengths"], np.append(first, lin.size))
+    assert got["run_lengths"].sum() == inp.N
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("wd_mode,wd", [(0, 0.0), (1, 0.1), (2, 0.05)])
+def test_adagrad_vs_torch_autograd(pooling, wd_mode, wd):
+    rng = np.random.default_rng(21)
+    dims, rows = [8, 16], [30, 20]
+    inp = random_tbe(rng, 2, 12, dims, rows, 9, empty_frac=0.1)
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
+    m1_off = np.array([0, rows[0]], np.int64)
+    grad = rng.normal(0, 1, size=(inp.B, inp.total_D)).astype(np.float32)
+    lr, eps = 0.1, 1e-6
+    W_new, m_new = orc.backward_rowwise_adagrad(
+        W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
+        wd, wd_mode, orc.info_B_num_bits(2, inp.B))
+    w_off = weight_offsets(inp)
+    for t in range(2):
+        E, D = rows[t], dims[t]
+        Wt = torch.tensor(W[w_off[t]: w_off[t] + E * D].reshape(E, D), requires_grad=True)
+        o = inp.offsets[t * inp.B:(t + 1) * inp.B + 1]
+        out = torch.nn.functional.embedding_bag(
+            torch.from_numpy(inp.indices[o[0]:o[-1]]), Wt, torch.from_numpy(o[:-1] - o[0]),
+            mode="sum" if pooling == 0 else "mean")
+        d0, d1 = inp.D_offsets[t], inp.D_offsets[t + 1]
+        (out * torch.from_numpy(grad[:, d0:d1])).sum().backward()
+        g = Wt.grad.detach()
+        w = Wt.detach()
+        touched = torch.from_numpy(np.isin(np.arange(E), inp.indices[o[0]:o[-1]]))
+        s = g + wd * w if wd_mode == 1 else g
+        h = torch.from_numpy(m1[m1_off[t]: m1_off[t] + E]) + (s * s).sum(1) / D
+        m = lr / (h.sqrt() + eps)
+        c = torch.ones_like(m)
+        if wd_mode == 1:
+            c = 1 - m * wd
+        elif wd_mode == 2:
+            c = torch.full_like(m, 1 - lr * wd)
+        w_ref = torch.where(touched[:, None], c[:, None] * w - m[:, None] * g, w)
+        h_ref = torch.where(touched, h, torch.from_numpy(m1[m1_off[t]: m1_off[t] + E]))
+        np.testing.assert_allclose(W_new[w_off[t]: w_off[t] + E * D].reshape(E, D), w_ref.numpy(),
+                                   rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(m_new[m1_off[t]: m1_off[t] + E], h_ref.numpy(), rtol=1e-5,
+                                   atol=1e-7)
+
+
+def test_adagrad_zero_grad_changes_nothing():
+    rng = np.random.default_rng(2)
+    inp = random_tbe(rng, 1, 10, [8], [20], 5)
+    W = rng.uniform(-1, 1, 160).astype(np.float32)
+    m1 = rng.uniform(0.1, 1, 20).astype(np.float32)
+    W2, m2 = orc.backward_rowwise_adagrad(W, np.array([0]), inp.D_offsets, 10,
+                                          inp.hash_size_cumsum, inp.total_hash_size_bits,
+                                          inp.indices, inp.offsets, 0,
+                                          np.zeros((10, 8), np.float32), m1, np.array([0]), 0.1,
+                                          1e-8)
+    np.testing.assert_array_equal(W2, W)
+    np.testing.assert_array_equal(m2, m1)

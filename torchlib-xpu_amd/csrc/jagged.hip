@@ -1,0 +1,394 @@
+// Jagged <-> padded-dense kernels for gfx950.
+//
+// Semantics follow fbgemm_gpu's jagged_to_padded_dense_forward,
+// dense_to_jagged_forward and jagged_dense_elementwise_add_jagged_output
+// (upstream src/jagged_tensor_ops/, recalled), restated from torch's own
+// port of the same ops: torch/_inductor/jagged_lowerings.py:161-177 (masked
+// load, else padding value) and :231-249 (jagged rows past max length become
+// 0).
+//
+// Design: the ops are pure HBM streams.  One work item moves VEC bytes
+// (16 when the row size and pointers allow it), consecutive work items walk
+// a row, so every wave issues fully coalesced 1 KiB transactions.  The
+// jagged coordinate of a dense row is found by walking the offsets levels
+// (dense -> jagged) or by a binary search per level (jagged -> dense); the
+// offsets are a few KB and stay in L2.
+#include "mx_common.h"
+
+namespace mx {
+namespace {
+
+struct JaggedMeta {
+  const void* off[MX_MAX_JAGGED_DIM];
+  int64_t off_len[MX_MAX_JAGGED_DIM];  // entries in each offsets array
+  int64_t max_len[MX_MAX_JAGGED_DIM];
+  int32_t ndim;
+};
+
+template <int VEC>
+struct alignas(VEC) Chunk {
+  uint8_t b[VEC];
+};
+
+template <typename I>
+__device__ __forceinline__ int64_t off_at(const JaggedMeta& m, int k, int64_t i) {
+  return static_cast<int64_t>(reinterpret_cast<const I*>(m.off[k])[i]);
+}
+
+// Dense row r (over B * prod(max_len)) -> jagged values row, or -1 for padding.
+template <typename I>
+__device__ int64_t dense_to_values_row(int64_t r, const JaggedMeta& m) {
+  int64_t coord[MX_MAX_JAGGED_DIM];
+  for (int k = m.ndim - 1; k >= 0; --k) {
+    coord[k] = r % m.max_len[k];
+    r /= m.max_len[k];
+  }
+  int64_t idx = r;  // b
+  for (int k = 0; k < m.ndim; ++k) {
+    const int64_t begin = off_at<I>(m, k, idx);
+    const int64_t end = off_at<I>(m, k, idx + 1);
+    if (coord[k] >= end - begin) return -1;
+    idx = begin + coord[k];
+  }
+  return idx;
+}
+
+// Last p in [0, n-1) with off[p] <= x, or -1 when x is past the last offset.
+template <typename I>
+__device__ int64_t owner_of(const JaggedMeta& m, int k, int64_t x) {
+  const int64_t n = m.off_len[k];
+  if (n < 2 || x < off_at<I>(m, k, 0) || x >= off_at<I>(m, k, n - 1)) return -1;
+  int64_t lo = 0, hi = n - 1;  // off[lo] <= x < off[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = lo + ((hi - lo) >> 1);
+    if (off_at<I>(m, k, mid) <= x)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// Jagged values row i -> dense row, or -1 if it has no dense position.
+template <typename I>
+__device__ int64_t values_to_dense_row(int64_t i, const JaggedMeta& m) {
+  int64_t coord[MX_MAX_JAGGED_DIM];
+  int64_t idx = i;
+  bool inside = true;
+  for (int k = m.ndim - 1; k >= 0; --k) {
+    const int64_t p = owner_of<I>(m, k, idx);
+    if (p < 0) return -1;
+    coord[k] = idx - off_at<I>(m, k, p);
+    if (coord[k] >= m.max_len[k]) inside = false;
+    idx = p;
+  }
+  if (!inside) return -1;
+  int64_t r = idx;
+  for (int k = 0; k < m.ndim; ++k) r = r * m.max_len[k] + coord[k];
+  return r;
+}
+
+template <int VEC, typename I>
+__global__ void __launch_bounds__(256) j2pd_kernel(const uint8_t* __restrict__ values,
+                                                   uint8_t* __restrict__ out, JaggedMeta m,
+                                                   int64_t rows, int64_t vpr, Chunk<VEC> pad) {
+  const int64_t total = rows * vpr;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
+       w += stride) {
+    const int64_t r = w / vpr;
+    const int64_t v = w - r * vpr;
+    const int64_t src = dense_to_values_row<I>(r, m);
+    Chunk<VEC> c = pad;
+    if (src >= 0) c = reinterpret_cast<const Chunk<VEC>*>(values)[src * vpr + v];
+    reinterpret_cast<Chunk<VEC>*>(out)[w] = c;
+  }
+}
+
+template <int VEC, typename I>
+__global__ void __launch_bounds__(256) d2j_kernel(const uint8_t* __restrict__ dense,
+                                                  uint8_t* __restrict__ out, JaggedMeta m,
+                                                  int64_t total_L, int64_t vpr) {
+  const int64_t total = total_L * vpr;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
+       w += stride) {
+    const int64_t i = w / vpr;
+    const int64_t v = w - i * vpr;
+    const int64_t dr = values_to_dense_row<I>(i, m);
+    Chunk<VEC> c;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) c.b[e] = 0;
+    if (dr >= 0) c = reinterpret_cast<const Chunk<VEC>*>(dense)[dr * vpr + v];
+    reinterpret_cast<Chunk<VEC>*>(out)[w] = c;
+  }
+}
+
+// ---- element arithmetic for the jagged + dense add ------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+// Round to nearest even, NaN kept quiet (same rule as c10::BFloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <int DT>
+struct AddOp;
+
+template <>
+struct AddOp<MX_DTYPE_F32> {
+  static constexpr int kBytes = 4;
+  __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
+    const float r = *reinterpret_cast<const float*>(x) + *reinterpret_cast<const float*>(y);
+    *reinterpret_cast<float*>(o) = r;
+  }
+};
+template <>
+struct AddOp<MX_DTYPE_F64> {
+  static constexpr int kBytes = 8;
+  __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
+    const double r = *reinterpret_cast<const double*>(x) + *reinterpret_cast<const double*>(y);
+    *reinterpret_cast<double*>(o) = r;
+  }
+};
+template <>
+struct AddOp<MX_DTYPE_F16> {
+  static constexpr int kBytes = 2;
+  __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
+    const float r = __half2float(*reinterpret_cast<const __half*>(x)) +
+                    __half2float(*reinterpret_cast<const __half*>(y));
+    *reinterpret_cast<__half*>(o) = __float2half_rn(r);
+  }
+};
+template <>
+struct AddOp<MX_DTYPE_BF16> {
+  static constexpr int kBytes = 2;
+  __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
+    const float r = bf16_to_f32(*reinterpret_cast<const uint16_t*>(x)) +
+                    bf16_to_f32(*reinterpret_cast<const uint16_t*>(y));
+    *reinterpret_cast<uint16_t*>(o) = f32_to_bf16(r);
+  }
+};
+
+template <int VEC, typename I, int DT>
+__global__ void __launch_bounds__(256) jagged_add_kernel(const uint8_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ y,
+                                                         uint8_t* __restrict__ out, JaggedMeta m,
+                                                         int64_t total_L, int64_t vpr) {
+  using Op = AddOp<DT>;
+  const int64_t total = total_L * vpr;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
+       w += stride) {
+    const int64_t i = w / vpr;
+    const int64_t v = w - i * vpr;
+    const int64_t dr = values_to_dense_row<I>(i, m);
+    const Chunk<VEC> cx = reinterpret_cast<const Chunk<VEC>*>(x)[w];
+    Chunk<VEC> cy;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) cy.b[e] = 0;  // +0 in every element type
+    if (dr >= 0) cy = reinterpret_cast<const Chunk<VEC>*>(y)[dr * vpr + v];
+    Chunk<VEC> co;
+#pragma unroll
+    for (int e = 0; e < VEC; e += Op::kBytes) Op::apply(cx.b + e, cy.b + e, co.b + e);
+    reinterpret_cast<Chunk<VEC>*>(out)[w] = co;
+  }
+}
+
+// ---- host side ------------------------------------------------------------
+
+int pick_vec(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
+  for (int vec : {16, 8, 4, 2, 1}) {
+    if (row_bytes % vec) continue;
+    bool ok = true;
+    for (const void* p : ptrs)
+      if (reinterpret_cast<uintptr_t>(p) % vec) ok = false;
+    if (ok) return vec;
+  }
+  return 1;
+}
+
+int grid_for(int64_t items) {
+  const int64_t blocks = ceil_div(items, 256);
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 32;
+  return static_cast<int>(blocks < 1 ? 1 : (blocks > cap ? cap : blocks));
+}
+
+int build_meta(JaggedMeta& m, int32_t ndim, const void* const* offsets, int32_t offset_bytes,
+               const int64_t* offsets_numel, const int64_t* max_lengths) {
+  MX_REQUIRE(ndim >= 1 && ndim <= MX_MAX_JAGGED_DIM, "num_jagged_dim %d not in [1, %d]", ndim,
+             MX_MAX_JAGGED_DIM);
+  MX_REQUIRE(offset_bytes == 4 || offset_bytes == 8, "offsets must be int32 or int64");
+  MX_REQUIRE(offsets != nullptr && offsets_numel != nullptr && max_lengths != nullptr,
+             "null offsets/offsets_numel/max_lengths");
+  m.ndim = ndim;
+  for (int k = 0; k < ndim; ++k) {
+    MX_REQUIRE(offsets_numel[k] >= 1, "offsets[%d] must have at least one entry", k);
+    MX_REQUIRE(offsets[k] != nullptr, "null offsets[%d]", k);
+    MX_REQUIRE(max_lengths[k] >= 0, "negative max_length[%d]", k);
+    m.off[k] = offsets[k];
+    m.off_len[k] = offsets_numel[k];
+    m.max_len[k] = max_lengths[k];
+  }
+  for (int k = ndim; k < MX_MAX_JAGGED_DIM; ++k) {
+    m.off[k] = nullptr;
+    m.off_len[k] = 0;
+    m.max_len[k] = 1;
+  }
+  return MX_OK;
+}
+
+bool valid_elem(int64_t eb) { return eb == 1 || eb == 2 || eb == 4 || eb == 8; }
+
+int64_t dtype_bytes(int32_t dt) {
+  switch (dt) {
+    case MX_DTYPE_F32: return 4;
+    case MX_DTYPE_F64: return 8;
+    case MX_DTYPE_F16:
+    case MX_DTYPE_BF16: return 2;
+    default: return -1;
+  }
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+#define MX_VEC_SWITCH(vec, ...)                             \
+  switch (vec) {                                            \
+    case 16: { constexpr int V = 16; __VA_ARGS__; break; } \
+    case 8: { constexpr int V = 8; __VA_ARGS__; break; }   \
+    case 4: { constexpr int V = 4; __VA_ARGS__; break; }   \
+    case 2: { constexpr int V = 2; __VA_ARGS__; break; }   \
+    default: { constexpr int V = 1; __VA_ARGS__; break; }  \
+  }
+
+extern "C" int mx_jagged_to_padded_dense(const void* values, int64_t elem_bytes, int64_t inner,
+                                         int32_t num_jagged_dim, const void* const* offsets,
+                                         int32_t offset_bytes, const int64_t* offsets_numel,
+                                         const int64_t* max_lengths, uint64_t pad_bits,
+                                         void* out, void* stream) {
+  clear_error();
+  JaggedMeta m;
+  if (int rc = build_meta(m, num_jagged_dim, offsets, offset_bytes, offsets_numel, max_lengths))
+    return rc;
+  MX_REQUIRE(valid_elem(elem_bytes), "element size %lld not supported", (long long)elem_bytes);
+  MX_REQUIRE(inner >= 0, "negative inner size");
+  int64_t rows = offsets_numel[0] - 1;
+  for (int k = 0; k < num_jagged_dim; ++k) rows *= max_lengths[k];
+  const int64_t row_bytes = inner * elem_bytes;
+  if (rows == 0 || row_bytes == 0) return MX_OK;
+  MX_REQUIRE(values != nullptr && out != nullptr, "null values/out");
+  int vec = pick_vec(row_bytes, {values, out});
+  if (vec < elem_bytes) vec = static_cast<int>(elem_bytes);  // keep elements whole
+  MX_REQUIRE(row_bytes % vec == 0, "misaligned tensors");
+  uint8_t pat[16];  // padding pattern replicated over a 16-byte chunk
+  for (int i = 0; i < 16; ++i) pat[i] = static_cast<uint8_t>(pad_bits >> (8 * (i % elem_bytes)));
+  const int64_t vpr = row_bytes / vec;
+  const int grid = grid_for(rows * vpr);
+  auto* s = as_stream(stream);
+  const auto* v = static_cast<const uint8_t*>(values);
+  auto* o = static_cast<uint8_t*>(out);
+  MX_VEC_SWITCH(vec, {
+    Chunk<V> pad;
+    for (int i = 0; i < V; ++i) pad.b[i] = pat[i];
+    if (offset_bytes == 8)
+      j2pd_kernel<V, int64_t><<<grid, 256, 0, s>>>(v, o, m, rows, vpr, pad);
+    else
+      j2pd_kernel<V, int32_t><<<grid, 256, 0, s>>>(v, o, m, rows, vpr, pad);
+  });
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+// Shared host path of dense_to_jagged (x_values == NULL) and of the
+// jagged + dense add (x_values != NULL).
+static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner,
+                            int32_t num_jagged_dim, const void* const* offsets,
+                            int32_t offset_bytes, const int64_t* offsets_numel,
+                            const int64_t* max_lengths, int64_t total_L, const void* x_values,
+                            int32_t add_dtype, void* out, void* stream) {
+  JaggedMeta m;
+  if (int rc = build_meta(m, num_jagged_dim, offsets, offset_bytes, offsets_numel, max_lengths))
+    return rc;
+  MX_REQUIRE(valid_elem(elem_bytes), "element size %lld not supported", (long long)elem_bytes);
+  MX_REQUIRE(inner >= 0 && total_L >= 0, "negative size");
+  const int64_t row_bytes = inner * elem_bytes;
+  if (total_L == 0 || row_bytes == 0) return MX_OK;
+  MX_REQUIRE(out != nullptr, "null out");
+  int64_t dense_rows = offsets_numel[0] - 1;
+  for (int k = 0; k < num_jagged_dim; ++k) dense_rows *= max_lengths[k];
+  MX_REQUIRE(dense != nullptr || dense_rows == 0, "null dense");
+  const int vec0 = x_values ? pick_vec(row_bytes, {dense, out, x_values})
+                            : pick_vec(row_bytes, {dense, out});
+  const int vec = vec0 < elem_bytes ? static_cast<int>(elem_bytes) : vec0;
+  MX_REQUIRE(row_bytes % vec == 0, "misaligned tensors");
+  const int64_t vpr = row_bytes / vec;
+  const int grid = grid_for(total_L * vpr);
+  auto* s = as_stream(stream);
+  const auto* d = static_cast<const uint8_t*>(dense);
+  auto* o = static_cast<uint8_t*>(out);
+  if (x_values == nullptr) {
+    MX_VEC_SWITCH(vec, {
+      if (offset_bytes == 8)
+        d2j_kernel<V, int64_t><<<grid, 256, 0, s>>>(d, o, m, total_L, vpr);
+      else
+        d2j_kernel<V, int32_t><<<grid, 256, 0, s>>>(d, o, m, total_L, vpr);
+    });
+    MX_LAUNCH_CHECK();
+    return MX_OK;
+  }
+  MX_REQUIRE(dtype_bytes(add_dtype) == elem_bytes, "dtype %d does not match element size %lld",
+             add_dtype, (long long)elem_bytes);
+  const auto* x = static_cast<const uint8_t*>(x_values);
+#define MX_ADD_LAUNCH(DTC)                                                                 \
+  MX_VEC_SWITCH(vec, {                                                                     \
+    if constexpr (V >= AddOp<DTC>::kBytes) {                                               \
+      if (offset_bytes == 8)                                                               \
+        jagged_add_kernel<V, int64_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
+      else                                                                                 \
+        jagged_add_kernel<V, int32_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
+    }                                                                                      \
+  })
+  switch (add_dtype) {
+    case MX_DTYPE_F32: MX_ADD_LAUNCH(MX_DTYPE_F32); break;
+    case MX_DTYPE_F64: MX_ADD_LAUNCH(MX_DTYPE_F64); break;
+    case MX_DTYPE_F16: MX_ADD_LAUNCH(MX_DTYPE_F16); break;
+    case MX_DTYPE_BF16: MX_ADD_LAUNCH(MX_DTYPE_BF16); break;
+    default: return set_error(MX_EUNSUPPORTED, "dtype %d not supported", add_dtype);
+  }
+#undef MX_ADD_LAUNCH
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+extern "C" int mx_dense_to_jagged(const void* dense, int64_t elem_bytes, int64_t inner,
+                                  int32_t num_jagged_dim, const void* const* offsets,
+                                  int32_t offset_bytes, const int64_t* offsets_numel,
+                                  const int64_t* max_lengths, int64_t total_L, void* out,
+                                  void* stream) {
+  clear_error();
+  return jagged_output_op(dense, elem_bytes, inner, num_jagged_dim, offsets, offset_bytes,
+                          offsets_numel, max_lengths, total_L, nullptr, 0, out, stream);
+}
+
+extern "C" int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense,
+                                               int32_t dtype, int64_t inner,
+                                               int32_t num_jagged_dim, const void* const* offsets,
+                                               int32_t offset_bytes, const int64_t* offsets_numel,
+                                               const int64_t* max_lengths, int64_t total_L,
+                                               void* out, void* stream) {
+  clear_error();
+  const int64_t eb = dtype_bytes(dtype);
+  if (eb < 0) return set_error(MX_EUNSUPPORTED, "dtype %d not supported", dtype);
+  MX_REQUIRE(x_values != nullptr || total_L == 0, "null x_values");
+  if (total_L == 0 || inner == 0) return MX_OK;
+  return jagged_output_op(y_dense, eb, inner, num_jagged_dim, offsets, offset_bytes,
+                          offsets_numel, max_lengths, total_L, x_values, dtype, out, stream);
+}

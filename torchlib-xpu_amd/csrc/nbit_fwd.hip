@@ -1,0 +1,428 @@
+// Quantized ("nbit") TBE inference forward for gfx950: FP32, FP16, INT8,
+// INT4 and INT2 tables in one launch.
+//
+// Semantics: fbgemm_gpu int_nbit_split_embedding_codegen_lookup_function
+// (upstream codegen/inference/, recalled).  Row layout is the TBE layout of
+// torch/include/fbgemm/FbgemmEmbedding.h:88-92,144-149 (scale_bias_last =
+// false): an fp16 scale and an fp16 bias at the front of each INT8/INT4/INT2
+// row, then the codes, the even element of each INT4 byte in the low
+// nibble; value = scale * q + bias in fp32.  Rows are padded to
+// row_alignment bytes.
+//
+// Design: a wave serves P = 64/G bags of one table at once; each group of G
+// lanes walks its own bag's rows in index order, lane k owning columns
+// [k*CPL, (k+1)*CPL) with CPL = D/G.  A lane reads its CPL codes with one
+// wide load (INT8 D=128: 16 B), the row's qparams with one dword load, and
+// dequantizes in registers as acc += scale*q, keeping sum(bias) apart, so
+// each code costs one convert and one FMA and no cross-lane reduction is
+// needed.  The G indices of a batch are fetched with one coalesced load by
+// the group and handed out with ds_bpermute.  Tables of every type share the
+// launch; the type/width switch is wave-uniform.
+#include "mx_common.h"
+
+namespace mx {
+namespace {
+
+struct NbitArgs {
+  const uint8_t* W;
+  const int64_t* w_off;
+  const uint8_t* tys;
+  const int32_t* D_off;
+  const void* idx;
+  const void* off;
+  const float* iw;
+  void* out;
+  int64_t B;
+  int64_t Bp;  // B rounded up to bags-per-wave
+  int64_t total_D;
+  int64_t nwaves;
+  int32_t T;
+  int32_t pooling;
+  int32_t row_align;
+  int32_t out_f16;
+};
+
+__device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, int32_t align) {
+  int64_t u;
+  switch (ty) {
+    case MX_SPARSE_FP32: u = 4ll * D; break;
+    case MX_SPARSE_FP16: u = 2ll * D; break;
+    case MX_SPARSE_INT8: u = D + 4ll; break;
+    case MX_SPARSE_INT4: u = D / 2 + 4ll; break;
+    case MX_SPARSE_INT2: u = D / 4 + 4ll; break;
+    default: return -1;
+  }
+  if (align > 1) u = (u + align - 1) / align * align;
+  return u;
+}
+
+template <int TY>
+struct TyInfo;
+template <>
+struct TyInfo<MX_SPARSE_FP32> {
+  static constexpr int kBits = 32;
+  static constexpr bool kQ = false;
+};
+template <>
+struct TyInfo<MX_SPARSE_FP16> {
+  static constexpr int kBits = 16;
+  static constexpr bool kQ = false;
+};
+template <>
+struct TyInfo<MX_SPARSE_INT8> {
+  static constexpr int kBits = 8;
+  static constexpr bool kQ = true;
+};
+template <>
+struct TyInfo<MX_SPARSE_INT4> {
+  static constexpr int kBits = 4;
+  static constexpr bool kQ = true;
+};
+template <>
+struct TyInfo<MX_SPARSE_INT2> {
+  static constexpr int kBits = 2;
+  static constexpr bool kQ = true;
+};
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+// Loads BPL bytes (a power of two) starting at p into 32-bit words.
+template <int BPL>
+__device__ __forceinline__ void load_codes(const uint8_t* p, uint32_t (&w)[BPL >= 4 ? BPL / 4 : 1]) {
+  if constexpr (BPL == 1) {
+    w[0] = *p;
+  } else if constexpr (BPL == 2) {
+    w[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else if constexpr (BPL == 4) {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (BPL == 8) {
+    const u32x2a4 v = *reinterpret_cast<const u32x2a4*>(p);
+    w[0] = v.x;
+    w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int q = 0; q < BPL / 16; ++q) {
+      const u32x4a4 v = *reinterpret_cast<const u32x4a4*>(p + 16 * q);
+      w[4 * q + 0] = v.x;
+      w[4 * q + 1] = v.y;
+      w[4 * q + 2] = v.z;
+      w[4 * q + 3] = v.w;
+    }
+  }
+}
+
+// Element e of the lane's chunk as fp32 (the raw code for integer types).
+template <int TY, int BPL>
+__device__ __forceinline__ float elem(const uint32_t (&w)[BPL >= 4 ? BPL / 4 : 1], int e) {
+  constexpr int bits = TyInfo<TY>::kBits;
+  const int bit = e * bits;
+  const uint32_t word = w[bit >> 5];
+  const int sh = bit & 31;
+  if constexpr (TY == MX_SPARSE_FP32) {
+    return __uint_as_float(word);
+  } else if constexpr (TY == MX_SPARSE_FP16) {
+    const uint16_t h = static_cast<uint16_t>(word >> sh);
+    return __half2float(__ushort_as_half(h));
+  } else {
+    return static_cast<float>((word >> sh) & ((1u << bits) - 1u));
+  }
+}
+
+template <typename I>
+__device__ __forceinline__ int64_t idx_at(const void* p, int64_t i) {
+  return static_cast<int64_t>(reinterpret_cast<const I*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_out(const NbitArgs& a, int64_t col_base, int ncols,
+                                          const float* v) {
+  if (a.out_f16) {
+    __half* o = reinterpret_cast<__half*>(a.out) + col_base;
+    for (int e = 0; e < ncols; ++e) o[e] = __float2half_rn(v[e]);
+  } else {
+    float* o = reinterpret_cast<float*>(a.out) + col_base;
+    for (int e = 0; e < ncols; ++e) o[e] = v[e];
+  }
+}
+
+// Fast path: CPL columns per lane, CPL*bits a multiple of 8.
+template <typename I, int G, int TY, int CPL>
+__device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int64_t stride,
+                         int64_t start, int64_t end, int64_t out_col, int g, int k) {
+  constexpr int BITS = TyInfo<TY>::kBits;
+  constexpr bool Q = TyInfo<TY>::kQ;
+  constexpr int BPL = CPL * BITS / 8;
+  constexpr int NW = BPL >= 4 ? BPL / 4 : 1;
+  constexpr int U0 = 96 / (BPL + (Q ? 4 : 0));
+  constexpr int U = U0 < 1 ? 1 : (U0 > 8 ? 8 : U0);
+  const int64_t lane_off = (Q ? 4 : 0) + static_cast<int64_t>(k) * BPL;
+
+  float acc[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) acc[e] = 0.0f;
+  float bsum = 0.0f;
+  const bool weighted = a.iw != nullptr;
+
+  for (int64_t base = start; base < end; base += G) {
+    const int n = static_cast<int>(end - base < G ? end - base : G);
+    const int64_t my_idx = k < n ? idx_at<I>(a.idx, base + k) : 0;
+    const float my_w = (weighted && k < n) ? a.iw[base + k] : 1.0f;
+    for (int j = 0; j < n; j += U) {
+      uint32_t codes[U][NW];
+      uint32_t qp[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t r = __shfl(my_idx, g * G + ((j + u) < n ? (j + u) : 0), 64);
+        if (j + u < n) {
+          const uint8_t* row = Wt + r * stride;
+          load_codes<BPL>(row + lane_off, codes[u]);
+          if constexpr (Q) qp[u] = *reinterpret_cast<const uint32_t*>(row);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float wgt = __shfl(my_w, g * G + ((j + u) < n ? (j + u) : 0), 64);
+        if (j + u < n) {
+          if constexpr (Q) {
+            float scale = __half2float(__ushort_as_half(static_cast<uint16_t>(qp[u] & 0xffffu)));
+            float bias = __half2float(__ushort_as_half(static_cast<uint16_t>(qp[u] >> 16)));
+            if (weighted) {
+              scale *= wgt;
+              bias *= wgt;
+            }
+            bsum += bias;
+#pragma unroll
+            for (int e = 0; e < CPL; ++e)
+              acc[e] = __builtin_fmaf(scale, elem<TY, BPL>(codes[u], e), acc[e]);
+          } else {
+            if (weighted) {
+#pragma unroll
+              for (int e = 0; e < CPL; ++e)
+                acc[e] = __builtin_fmaf(wgt, elem<TY, BPL>(codes[u], e), acc[e]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < CPL; ++e) acc[e] += elem<TY, BPL>(codes[u], e);
+            }
+          }
+        }
+      }
+    }
+  }
+  const int64_t L = end - start;
+  const float inv = (a.pooling == MX_POOL_MEAN && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;
+  float res[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) res[e] = (acc[e] + bsum) * inv;
+  if (L == 0) {
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) res[e] = 0.0f;
+  }
+  const int64_t col = out_col + static_cast<int64_t>(k) * CPL;
+  if (a.out_f16) {
+    __half h[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) h[e] = __float2half_rn(res[e]);
+    __half* o = reinterpret_cast<__half*>(a.out) + col;
+    if constexpr (CPL % 8 == 0) {
+#pragma unroll
+      for (int q = 0; q < CPL / 8; ++q)
+        *reinterpret_cast<uint4*>(o + 8 * q) = *reinterpret_cast<const uint4*>(h + 8 * q);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) o[e] = h[e];
+    }
+  } else {
+    float* o = reinterpret_cast<float*>(a.out) + col;
+    if constexpr (CPL % 4 == 0) {
+#pragma unroll
+      for (int q = 0; q < CPL / 4; ++q)
+        *reinterpret_cast<float4*>(o + 4 * q) =
+            make_float4(res[4 * q], res[4 * q + 1], res[4 * q + 2], res[4 * q + 3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) o[e] = res[e];
+    }
+  }
+}
+
+// Any D: lanes own 8-column blocks, one block sweep per pass over the bag.
+template <typename I, int G>
+__device__ void bag_generic(const NbitArgs& a, int32_t ty, int32_t D,
+                            const uint8_t* __restrict__ Wt, int64_t stride, int64_t start,
+                            int64_t end, int64_t out_col, int k) {
+  const int bits = ty == MX_SPARSE_FP32 ? 32 : ty == MX_SPARSE_FP16 ? 16 : ty == MX_SPARSE_INT8 ? 8
+                 : ty == MX_SPARSE_INT4 ? 4 : 2;
+  const bool q = bits <= 8;
+  const int64_t L = end - start;
+  const float inv = (a.pooling == MX_POOL_MEAN && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;
+  for (int cb = k * 8; cb < D; cb += G * 8) {
+    const int nc = D - cb < 8 ? D - cb : 8;
+    float acc[8];
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    float bsum = 0.0f;
+    for (int64_t l = start; l < end; ++l) {
+      const int64_t r = idx_at<I>(a.idx, l);
+      const float wgt = a.iw ? a.iw[l] : 1.0f;
+      const uint8_t* row = Wt + r * stride;
+      float scale = 1.0f;
+      if (q) {
+        const uint32_t qp = *reinterpret_cast<const uint32_t*>(row);
+        scale = __half2float(__ushort_as_half(static_cast<uint16_t>(qp & 0xffffu))) * wgt;
+        bsum += __half2float(__ushort_as_half(static_cast<uint16_t>(qp >> 16))) * wgt;
+        row += 4;
+      }
+      for (int e = 0; e < nc; ++e) {
+        const int c = cb + e;
+        float v;
+        if (bits == 32) {
+          v = reinterpret_cast<const float*>(row)[c];
+        } else if (bits == 16) {
+          v = __half2float(__ushort_as_half(reinterpret_cast<const uint16_t*>(row)[c]));
+        } else {
+          const int bit = c * bits;
+          v = static_cast<float>((row[bit >> 3] >> (bit & 7)) & ((1 << bits) - 1));
+        }
+        acc[e] = q ? __builtin_fmaf(scale, v, acc[e]) : __builtin_fmaf(wgt, v, acc[e]);
+      }
+    }
+    float res[8];
+    for (int e = 0; e < 8; ++e) res[e] = L > 0 ? (acc[e] + bsum) * inv : 0.0f;
+    store_out(a, out_col + cb, nc, res);
+  }
+}
+
+template <typename I, int G, int TY>
+__device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
+                                             const uint8_t* __restrict__ Wt, int64_t stride,
+                                             int64_t start, int64_t end, int64_t out_col, int g,
+                                             int k) {
+  constexpr int BITS = TyInfo<TY>::kBits;
+  const int cpl = D / G;
+  if (cpl * G == D) {
+    switch (cpl) {
+#define MX_CPL(C)                                                                  \
+  case C:                                                                          \
+    if constexpr ((C * BITS) % 8 == 0 && C * BITS <= 512) {                        \
+      bag_fast<I, G, TY, C>(a, Wt, stride, start, end, out_col, g, k);             \
+      return;                                                                      \
+    }                                                                              \
+    break;
+      MX_CPL(2)
+      MX_CPL(4)
+      MX_CPL(8)
+      MX_CPL(16)
+      MX_CPL(32)
+#undef MX_CPL
+      default: break;
+    }
+  }
+  bag_generic<I, G>(a, TY, D, Wt, stride, start, end, out_col, k);
+}
+
+template <typename I, int G>
+__global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
+  constexpr int P = 64 / G;  // bags per wave
+  const int64_t wave = xcd_remap(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);
+  if (wave >= a.nwaves) return;
+  const int lane = threadIdx.x & 63;
+  const int g = lane / G;
+  const int k = lane % G;
+  const int64_t slot0 = wave * P;
+  const int64_t t = slot0 / a.Bp;
+  if (t >= a.T) return;
+  const int64_t b = slot0 - t * a.Bp + g;
+  const int32_t ty = a.tys[t];
+  const int32_t D0 = a.D_off[t];
+  const int32_t D = a.D_off[t + 1] - D0;
+  const int64_t stride = row_bytes_of(ty, D, a.row_align);
+  const uint8_t* __restrict__ Wt = a.W + a.w_off[t];
+  int64_t start = 0, end = 0;
+  if (b < a.B) {
+    const int64_t bag = t * a.B + b;
+    start = idx_at<I>(a.off, bag);
+    end = idx_at<I>(a.off, bag + 1);
+  }
+  const int64_t out_col = (b < a.B ? b : 0) * a.total_D + D0;
+  if (b >= a.B) return;  // whole group idle; group lanes stay converged
+  switch (ty) {
+    case MX_SPARSE_FP32: dispatch_cpl<I, G, MX_SPARSE_FP32>(a, D, Wt, stride, start, end, out_col, g, k); break;
+    case MX_SPARSE_FP16: dispatch_cpl<I, G, MX_SPARSE_FP16>(a, D, Wt, stride, start, end, out_col, g, k); break;
+    case MX_SPARSE_INT8: dispatch_cpl<I, G, MX_SPARSE_INT8>(a, D, Wt, stride, start, end, out_col, g, k); break;
+    case MX_SPARSE_INT4: dispatch_cpl<I, G, MX_SPARSE_INT4>(a, D, Wt, stride, start, end, out_col, g, k); break;
+    case MX_SPARSE_INT2: dispatch_cpl<I, G, MX_SPARSE_INT2>(a, D, Wt, stride, start, end, out_col, g, k); break;
+    default: break;  // unknown types are rejected on the host
+  }
+}
+
+template <int G>
+int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
+  constexpr int P = 64 / G;
+  a.Bp = ceil_div(a.B, P) * P;
+  a.nwaves = static_cast<int64_t>(a.T) * (a.Bp / P);
+  const int64_t grid = ceil_div(a.nwaves, 4);
+  MX_REQUIRE(grid <= 0x7fffffffll, "too many bags");
+  if (index_bytes == 8)
+    nbit_fwd_kernel<int64_t, G><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
+  else
+    nbit_fwd_kernel<int32_t, G><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int64_t mx_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_alignment) {
+  if (D < 0) return -1;
+  return row_bytes_of(ty, D, row_alignment);
+}
+
+extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
+                               const uint8_t* weights_tys, const int32_t* D_offsets, int32_t T,
+                               int64_t B, int32_t max_int2_D, int32_t max_int4_D,
+                               int32_t max_int8_D, int32_t max_float16_D, int32_t max_float32_D,
+                               const void* indices, const void* offsets, int32_t index_bytes,
+                               int32_t pooling_mode, const float* indice_weights,
+                               int32_t output_dtype, int32_t row_alignment, void* out,
+                               int64_t total_D, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
+             "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
+  MX_REQUIRE(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
+             "output_dtype %d not supported (FP32=0, FP16=1)", output_dtype);
+  MX_REQUIRE(row_alignment >= 1, "row_alignment must be positive");
+  int32_t max_D = 0;
+  for (int32_t d : {max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D}) {
+    MX_REQUIRE(d >= 0, "negative max_D");
+    if (d > max_D) max_D = d;
+  }
+  MX_REQUIRE(max_D <= 1024, "max D %d above 1024", max_D);
+  if (static_cast<int64_t>(T) * B == 0 || total_D == 0) return MX_OK;
+  MX_REQUIRE(dev_weights && weights_offsets && weights_tys && D_offsets && offsets && out,
+             "null pointer argument");
+  NbitArgs a;
+  a.W = dev_weights;
+  a.w_off = weights_offsets;
+  a.tys = weights_tys;
+  a.D_off = D_offsets;
+  a.idx = indices;
+  a.off = offsets;
+  a.iw = indice_weights;
+  a.out = out;
+  a.B = B;
+  a.Bp = 0;
+  a.total_D = total_D;
+  a.nwaves = 0;
+  a.T = T;
+  a.pooling = pooling_mode;
+  a.row_align = row_alignment;
+  a.out_f16 = output_dtype == MX_SPARSE_FP16;
+  auto* s = as_stream(stream);
+  if (max_D <= 256) return launch_nbit<8>(a, index_bytes, s);
+  if (max_D <= 512) return launch_nbit<16>(a, index_bytes, s);
+  return launch_nbit<32>(a, index_bytes, s);
+}

@@ -1,0 +1,724 @@
+// torch.ops.fbgemm.* drop-in registrations for the MI355X kernels.
+//
+// Boundary: the reference plugs a device implementation into its upstream
+// project's own interface from a static initializer of a
+// torch.ops.load_library()'d module (reference:
+// packages/torchcodec-xpu/src/torchcodec_xpu/XpuDeviceInterface.cpp:33-35,
+// __init__.py:25-56).  Here the upstream interface is fbgemm_gpu's `fbgemm`
+// dispatcher namespace: schemas are defined with TORCH_LIBRARY_FRAGMENT and
+// the implementations registered for the CUDA dispatch key, which is the key
+// HIP tensors carry on PyTorch-ROCm, plus Autograd wrappers.  Each op
+// validates its arguments (TORCH_CHECK -> RuntimeError), takes the current
+// HIP stream and calls the C-ABI in libmx_fbgemm_kernels.so; a non-zero
+// status becomes a RuntimeError carrying mx_last_error().  No CPU kernels
+// are registered: CPU tensors raise the dispatcher's NotImplementedError.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/csrc/autograd/custom_function.h>
+#include <torch/library.h>
+
+#include <cstring>
+#include <vector>
+
+#include "mx_fbgemm.h"
+
+using at::Tensor;
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+namespace mx_ops {
+
+#define MX_CALL(expr)                                                                  \
+  do {                                                                                 \
+    const int mx_rc_ = (expr);                                                         \
+    TORCH_CHECK(mx_rc_ == MX_OK, #expr " failed (", mx_rc_, "): ", mx_last_error()); \
+  } while (0)
+
+void* stream_of(const Tensor& t) {
+  return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_gpu(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.defined(), name, " must be defined");
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU (HIP) tensor, got ", t.device());
+}
+
+void check_same_device(const Tensor& a, const Tensor& b, const char* name) {
+  TORCH_CHECK(a.device() == b.device(), name, " is on ", b.device(), " but expected ", a.device());
+}
+
+int32_t index_bytes_of(const Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kLong || t.scalar_type() == at::kInt, name,
+              " must be int32 or int64, got ", t.scalar_type());
+  return t.scalar_type() == at::kLong ? 8 : 4;
+}
+
+// ---------------------------------------------------------------------------
+// Jagged ops
+// ---------------------------------------------------------------------------
+
+int32_t mx_dtype_of(at::ScalarType st) {
+  switch (st) {
+    case at::kFloat: return MX_DTYPE_F32;
+    case at::kHalf: return MX_DTYPE_F16;
+    case at::kBFloat16: return MX_DTYPE_BF16;
+    case at::kDouble: return MX_DTYPE_F64;
+    default: return -1;
+  }
+}
+
+uint64_t pad_bits_of(double pad, at::ScalarType st) {
+  // Convert on the host with torch's own casting rules, then take the bits.
+  Tensor p = at::scalar_tensor(pad, at::TensorOptions().dtype(st));
+  uint64_t bits = 0;
+  std::memcpy(&bits, p.data_ptr(), p.element_size());
+  return bits;
+}
+
+struct OffsetsPack {
+  std::vector<Tensor> keep;
+  std::vector<const void*> ptrs;
+  std::vector<int64_t> numel;
+  int32_t bytes = 8;
+};
+
+OffsetsPack pack_offsets(const std::vector<Tensor>& offsets, const Tensor& like) {
+  TORCH_CHECK(!offsets.empty(), "offsets must hold at least one tensor");
+  TORCH_CHECK(offsets.size() <= MX_MAX_JAGGED_DIM, "at most ", MX_MAX_JAGGED_DIM,
+              " jagged dimensions are supported, got ", offsets.size());
+  OffsetsPack p;
+  p.bytes = index_bytes_of(offsets[0], "offsets");
+  for (const auto& o : offsets) {
+    check_gpu(o, "offsets");
+    check_same_device(like, o, "offsets");
+    TORCH_CHECK(o.dim() == 1, "offsets must be 1-D");
+    TORCH_CHECK(index_bytes_of(o, "offsets") == p.bytes, "all offsets must share one dtype");
+    TORCH_CHECK(o.numel() >= 1, "offsets must not be empty");
+    p.keep.push_back(o.contiguous());
+    p.ptrs.push_back(p.keep.back().data_ptr());
+    p.numel.push_back(o.numel());
+  }
+  return p;
+}
+
+Tensor jagged_to_padded_dense_forward(const Tensor& values, const std::vector<Tensor>& offsets,
+                                      c10::SymIntArrayRef max_lengths_sym, double padding_value) {
+  check_gpu(values, "values");
+  c10::OptionalDeviceGuard guard(values.device());
+  const auto max_lengths = C10_AS_INTARRAYREF_SLOW(max_lengths_sym);
+  TORCH_CHECK(max_lengths.size() == offsets.size(), "max_lengths has ", max_lengths.size(),
+              " entries but there are ", offsets.size(), " offsets");
+  TORCH_CHECK(values.dim() >= 1, "values must have at least one dimension");
+  OffsetsPack p = pack_offsets(offsets, values);
+  const Tensor v = values.contiguous();
+  const int64_t inner_elems = v.dim() == 1 ? 1 : c10::multiply_integers(v.sizes().slice(1));
+  std::vector<int64_t> shape{p.numel[0] - 1};
+  for (auto m : max_lengths) shape.push_back(m);
+  for (int64_t d = 1; d < v.dim(); ++d) shape.push_back(v.size(d));
+  Tensor out = at::empty(shape, v.options());
+  MX_CALL(mx_jagged_to_padded_dense(v.data_ptr(), v.element_size(), inner_elems,
+                                    static_cast<int32_t>(offsets.size()), p.ptrs.data(), p.bytes,
+                                    p.numel.data(), max_lengths.data(),
+                                    pad_bits_of(padding_value, v.scalar_type()), out.data_ptr(),
+                                    stream_of(v)));
+  return out;
+}
+
+int64_t last_offset(const Tensor& o) { return o.numel() == 0 ? 0 : o[-1].item<int64_t>(); }
+
+Tensor dense_to_jagged_forward(const Tensor& dense, const std::vector<Tensor>& offsets,
+                               std::optional<c10::SymInt> total_L_sym) {
+  check_gpu(dense, "dense");
+  c10::OptionalDeviceGuard guard(dense.device());
+  const int64_t nd = static_cast<int64_t>(offsets.size());
+  TORCH_CHECK(dense.dim() >= 1 + nd, "dense must have at least ", 1 + nd, " dimensions");
+  OffsetsPack p = pack_offsets(offsets, dense);
+  TORCH_CHECK(dense.size(0) == p.numel[0] - 1, "dense has ", dense.size(0),
+              " rows but offsets describe ", p.numel[0] - 1);
+  const Tensor d = dense.contiguous();
+  std::vector<int64_t> max_lengths;
+  for (int64_t k = 0; k < nd; ++k) max_lengths.push_back(d.size(1 + k));
+  const int64_t total_L =
+      total_L_sym.has_value() ? total_L_sym->expect_int() : last_offset(p.keep.back());
+  TORCH_CHECK(total_L >= 0, "total_L must be non-negative");
+  std::vector<int64_t> shape{total_L};
+  int64_t inner = 1;
+  for (int64_t k = 1 + nd; k < d.dim(); ++k) {
+    shape.push_back(d.size(k));
+    inner *= d.size(k);
+  }
+  Tensor out = at::empty(shape, d.options());
+  MX_CALL(mx_dense_to_jagged(d.data_ptr(), d.element_size(), inner, static_cast<int32_t>(nd),
+                             p.ptrs.data(), p.bytes, p.numel.data(), max_lengths.data(), total_L,
+                             out.data_ptr(), stream_of(d)));
+  return out;
+}
+
+Tensor jagged_dense_add_forward(const Tensor& x_values, const std::vector<Tensor>& offsets,
+                                const Tensor& y) {
+  check_gpu(x_values, "x_values");
+  check_gpu(y, "y");
+  check_same_device(x_values, y, "y");
+  c10::OptionalDeviceGuard guard(x_values.device());
+  TORCH_CHECK(x_values.scalar_type() == y.scalar_type(), "x_values and y must share a dtype");
+  const int32_t dt = mx_dtype_of(x_values.scalar_type());
+  TORCH_CHECK(dt >= 0, "dtype ", x_values.scalar_type(), " is not supported");
+  const int64_t nd = static_cast<int64_t>(offsets.size());
+  TORCH_CHECK(y.dim() >= 1 + nd, "y must have at least ", 1 + nd, " dimensions");
+  OffsetsPack p = pack_offsets(offsets, x_values);
+  TORCH_CHECK(y.size(0) == p.numel[0] - 1, "y has ", y.size(0), " rows but offsets describe ",
+              p.numel[0] - 1);
+  const Tensor x = x_values.contiguous();
+  const Tensor yc = y.contiguous();
+  std::vector<int64_t> max_lengths;
+  for (int64_t k = 0; k < nd; ++k) max_lengths.push_back(yc.size(1 + k));
+  int64_t inner = 1;
+  for (int64_t k = 1 + nd; k < yc.dim(); ++k) inner *= yc.size(k);
+  const int64_t x_inner = x.dim() == 1 ? 1 : c10::multiply_integers(x.sizes().slice(1));
+  TORCH_CHECK(x_inner == inner, "x_values inner size ", x_inner, " != y inner size ", inner);
+  Tensor out = at::empty_like(x);
+  MX_CALL(mx_jagged_dense_elementwise_add(x.data_ptr(), yc.data_ptr(), dt, inner,
+                                          static_cast<int32_t>(nd), p.ptrs.data(), p.bytes,
+                                          p.numel.data(), max_lengths.data(), x.size(0),
+                                          out.data_ptr(), stream_of(x)));
+  return out;
+}
+
+Tensor jagged_to_padded_dense_backward(const Tensor& grad_output,
+                                       const std::vector<Tensor>& offsets,
+                                       c10::SymInt total_L) {
+  return dense_to_jagged_forward(grad_output, offsets, total_L);
+}
+
+std::vector<c10::SymInt> sym_lengths(const Tensor& dense, int64_t nd) {
+  std::vector<c10::SymInt> v;
+  for (int64_t k = 0; k < nd; ++k) v.emplace_back(dense.size(1 + k));
+  return v;
+}
+
+class JaggedToPaddedDense : public torch::autograd::Function<JaggedToPaddedDense> {
+ public:
+  static Tensor forward(AutogradContext* ctx, const Tensor& values,
+                        const std::vector<Tensor>& offsets, c10::SymIntArrayRef max_lengths,
+                        double padding_value) {
+    ctx->save_for_backward(offsets);
+    ctx->saved_data["total_L"] = values.size(0);
+    at::AutoDispatchBelowADInplaceOrView g;
+    return jagged_to_padded_dense_forward(values, offsets, max_lengths, padding_value);
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const auto offsets = ctx->get_saved_variables();
+    const int64_t total_L = ctx->saved_data["total_L"].toInt();
+    variable_list out(1 + offsets.size() + 2);  // values, offsets..., max_lengths, padding
+    out[0] = dense_to_jagged_forward(grads[0], offsets, c10::SymInt(total_L));
+    return out;
+  }
+};
+
+class DenseToJagged : public torch::autograd::Function<DenseToJagged> {
+ public:
+  static Tensor forward(AutogradContext* ctx, const Tensor& dense,
+                        const std::vector<Tensor>& offsets, std::optional<c10::SymInt> total_L) {
+    ctx->save_for_backward(offsets);
+    std::vector<int64_t> ml;
+    for (size_t k = 0; k < offsets.size(); ++k) ml.push_back(dense.size(1 + k));
+    ctx->saved_data["max_lengths"] = ml;
+    at::AutoDispatchBelowADInplaceOrView g;
+    return dense_to_jagged_forward(dense, offsets, total_L);
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const auto offsets = ctx->get_saved_variables();
+    const auto ml = ctx->saved_data["max_lengths"].toIntVector();
+    std::vector<c10::SymInt> sml(ml.begin(), ml.end());
+    variable_list out(1 + offsets.size() + 1);  // dense, offsets..., total_L
+    out[0] = jagged_to_padded_dense_forward(grads[0], offsets, sml, 0.0);
+    return out;
+  }
+};
+
+class JaggedDenseAdd : public torch::autograd::Function<JaggedDenseAdd> {
+ public:
+  static Tensor forward(AutogradContext* ctx, const Tensor& x, const std::vector<Tensor>& offsets,
+                        const Tensor& y) {
+    ctx->save_for_backward(offsets);
+    std::vector<int64_t> ml;
+    for (size_t k = 0; k < offsets.size(); ++k) ml.push_back(y.size(1 + k));
+    ctx->saved_data["max_lengths"] = ml;
+    at::AutoDispatchBelowADInplaceOrView g;
+    return jagged_dense_add_forward(x, offsets, y);
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const auto offsets = ctx->get_saved_variables();
+    const auto ml = ctx->saved_data["max_lengths"].toIntVector();
+    std::vector<c10::SymInt> sml(ml.begin(), ml.end());
+    variable_list out(1 + offsets.size() + 1);  // x, offsets..., y
+    out[0] = grads[0];
+    out.back() = jagged_to_padded_dense_forward(grads[0], offsets, sml, 0.0);
+    return out;
+  }
+};
+
+Tensor jagged_to_padded_dense_autograd(const Tensor& values, const std::vector<Tensor>& offsets,
+                                       c10::SymIntArrayRef max_lengths, double padding_value) {
+  return JaggedToPaddedDense::apply(values, offsets, max_lengths, padding_value);
+}
+
+std::tuple<Tensor, std::vector<Tensor>> dense_to_jagged_autograd(
+    const Tensor& dense, const std::vector<Tensor>& offsets, std::optional<c10::SymInt> total_L) {
+  return {DenseToJagged::apply(dense, offsets, total_L), offsets};
+}
+
+std::tuple<Tensor, std::vector<Tensor>> jagged_dense_add_autograd(
+    const Tensor& x, const std::vector<Tensor>& offsets, const Tensor& y) {
+  return {JaggedDenseAdd::apply(x, offsets, y), offsets};
+}
+
+Tensor jagged_to_padded_dense_plain(const Tensor& values, const std::vector<Tensor>& offsets,
+                                    c10::SymIntArrayRef max_lengths, double padding_value) {
+  return jagged_to_padded_dense_forward(values, offsets, max_lengths, padding_value);
+}
+
+std::tuple<Tensor, std::vector<Tensor>> dense_to_jagged_plain(
+    const Tensor& dense, const std::vector<Tensor>& offsets, std::optional<c10::SymInt> total_L) {
+  return {dense_to_jagged_forward(dense, offsets, total_L), offsets};
+}
+
+std::tuple<Tensor, std::vector<Tensor>> jagged_dense_add_plain(
+    const Tensor& x, const std::vector<Tensor>& offsets, const Tensor& y) {
+  return {jagged_dense_add_forward(x, offsets, y), offsets};
+}
+
+// ---------------------------------------------------------------------------
+// TBE training
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kPlacementDevice = 0;
+
+void check_device_placement(const Tensor& placements, const Tensor& uvm, const char* what) {
+  // DEVICE-only build: UVM / managed caching placements are not served.
+  TORCH_CHECK(uvm.numel() == 0, what, ": UVM storage is not supported (DEVICE placement only)");
+  if (placements.defined() && placements.numel() > 0) {
+    const Tensor pc = placements.to(at::kCPU, /*non_blocking=*/false);
+    TORCH_CHECK((pc == kPlacementDevice).all().item<bool>(), what,
+                ": every table must use EmbeddingLocation.DEVICE");
+  }
+}
+
+Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
+                   const Tensor& weights_placements, const Tensor& weights_offsets,
+                   const Tensor& D_offsets, int64_t total_D, int64_t max_D, const Tensor& indices,
+                   const Tensor& offsets, int64_t pooling_mode,
+                   const std::optional<Tensor>& indice_weights, int64_t output_dtype) {
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  for (auto* t : {&weights_offsets, &D_offsets, &indices, &offsets}) check_gpu(*t, "TBE argument");
+  TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
+  (void)weights_placements;  // validated once by the module; avoided here (host sync)
+  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat, "dev_weights must be fp32");
+  TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
+  TORCH_CHECK(D_offsets.scalar_type() == at::kInt, "D_offsets must be int32");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = D_offsets.numel() - 1;
+  TORCH_CHECK(T >= 1, "D_offsets must have T+1 >= 2 entries");
+  TORCH_CHECK(weights_offsets.numel() == T, "weights_offsets must have T entries");
+  TORCH_CHECK((offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
+              "output_dtype must be FP32 (0) or FP16 (1)");
+  const float* iw = nullptr;
+  Tensor iwc;
+  if (indice_weights.has_value() && indice_weights->defined()) {
+    check_gpu(*indice_weights, "indice_weights");
+    TORCH_CHECK(indice_weights->scalar_type() == at::kFloat, "indice_weights must be fp32");
+    TORCH_CHECK(indice_weights->numel() == indices.numel(), "indice_weights must match indices");
+    iwc = indice_weights->contiguous();
+    iw = iwc.data_ptr<float>();
+  }
+  auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
+  Tensor out = at::empty({B, total_D}, opts);
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  MX_CALL(mx_tbe_forward(dev_weights.data_ptr<float>(), weights_offsets.data_ptr<int64_t>(),
+                         D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B,
+                         static_cast<int32_t>(max_D), idx.data_ptr(), off.data_ptr(), ib,
+                         static_cast<int32_t>(pooling_mode), iw, out.data_ptr(),
+                         static_cast<int32_t>(output_dtype), total_D, stream_of(dev_weights)));
+  return out;
+}
+
+Tensor forward_unweighted(const Tensor& dev_weights, const Tensor& uvm_weights,
+                          const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+                          const Tensor& weights_offsets, const Tensor& D_offsets,
+                          c10::SymInt total_D, c10::SymInt max_D, const Tensor& indices,
+                          const Tensor& offsets, int64_t pooling_mode,
+                          const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
+                          int64_t output_dtype, bool is_experimental) {
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  (void)uvm_cache_stats;
+  (void)is_experimental;
+  return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
+                     total_D.expect_int(), max_D.expect_int(), indices, offsets, pooling_mode,
+                     std::nullopt, output_dtype);
+}
+
+Tensor forward_weighted(const Tensor& dev_weights, const Tensor& uvm_weights,
+                        const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+                        const Tensor& weights_offsets, const Tensor& D_offsets,
+                        c10::SymInt total_D, c10::SymInt max_D, const Tensor& indices,
+                        const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
+                        const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
+                        int64_t output_dtype, bool is_experimental) {
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  (void)uvm_cache_stats;
+  (void)is_experimental;
+  return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
+                     total_D.expect_int(), max_D.expect_int(), indices, offsets, pooling_mode,
+                     indice_weights, output_dtype);
+}
+
+std::tuple<int64_t, int64_t> get_infos_metadata(const Tensor& unused, int64_t B, int64_t T) {
+  (void)unused;
+  const int32_t nb = mx_tbe_info_B_num_bits(static_cast<int32_t>(T), B);
+  TORCH_CHECK(nb > 0, "T=", T, " and B=", B, " do not fit a 32-bit info word");
+  const int64_t mask = nb >= 32 ? 0xffffffffll : ((int64_t(1) << nb) - 1);
+  return {nb, mask};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_embedding_input(
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, bool nobag, const std::optional<Tensor>& vbe_b_t_map,
+    int64_t info_B_num_bits, int64_t info_B_mask, int64_t total_unique_indices) {
+  (void)info_B_mask;
+  (void)total_unique_indices;
+  TORCH_CHECK(!nobag, "nobag transpose is not supported");
+  TORCH_CHECK(!(vbe_b_t_map.has_value() && vbe_b_t_map->defined()),
+              "variable batch size (VBE) is not supported");
+  check_gpu(indices, "indices");
+  c10::OptionalDeviceGuard guard(indices.device());
+  check_gpu(hash_size_cumsum, "hash_size_cumsum");
+  check_gpu(offsets, "offsets");
+  TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = hash_size_cumsum.numel() - 1;
+  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  const int64_t N = indices.numel();
+  auto o64 = indices.options().dtype(at::kLong);
+  auto o32 = indices.options().dtype(at::kInt);
+  Tensor linear = at::empty({N}, o64), sorted = at::empty({N}, o64);
+  Tensor infos = at::empty({N}, o32), run = at::empty({N}, o64);
+  Tensor lengths = at::zeros({N}, o32), num_runs = at::zeros({1}, o32);
+  Tensor cum = at::zeros({N + 1}, o32);
+  const size_t ws_bytes = mx_tbe_transpose_workspace_bytes(N, total_hash_size_bits);
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  MX_CALL(mx_tbe_transpose_embedding_input(
+      hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
+      static_cast<int32_t>(total_hash_size_bits), static_cast<int32_t>(info_B_num_bits),
+      idx.data_ptr(), off.data_ptr(), ib, N, linear.data_ptr<int64_t>(),
+      sorted.data_ptr<int64_t>(), infos.data_ptr<int32_t>(), run.data_ptr<int64_t>(),
+      lengths.data_ptr<int32_t>(), num_runs.data_ptr<int32_t>(), cum.data_ptr<int32_t>(),
+      ws.data_ptr(), ws_bytes, stream_of(indices)));
+  return {linear, sorted, infos, run, lengths, num_runs, cum};
+}
+
+Tensor backward_rowwise_adagrad_exact(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D_sym,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& lxu_cache_locations,
+    int64_t BT_block_size, int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  (void)lxu_cache_weights;
+  (void)weights_placements;
+  (void)lxu_cache_locations;
+  (void)BT_block_size;
+  (void)max_segment_length_per_warp;
+  (void)stochastic_rounding;  // fp32 weights: no rounding step
+  (void)momentum1_placements;
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  for (auto* t : {&grad_output, &weights_offsets, &D_offsets, &hash_size_cumsum, &indices,
+                  &offsets, &momentum1_dev, &momentum1_offsets})
+    check_gpu(*t, "TBE backward argument");
+  TORCH_CHECK(uvm_weights.numel() == 0 && momentum1_uvm.numel() == 0,
+              "UVM storage is not supported (DEVICE placement only)");
+  TORCH_CHECK(max_norm == 0.0, "max_norm is not supported");
+  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat && dev_weights.is_contiguous(),
+              "dev_weights must be contiguous fp32");
+  TORCH_CHECK(momentum1_dev.scalar_type() == at::kFloat && momentum1_dev.is_contiguous(),
+              "momentum1_dev must be contiguous fp32");
+  TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
+  TORCH_CHECK(momentum1_offsets.scalar_type() == at::kLong, "momentum1_offsets must be int64");
+  TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = D_offsets.numel() - 1;
+  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  const Tensor g = grad_output.contiguous();
+  TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  const int64_t max_D = max_D_sym.expect_int();
+  const int64_t N = indices.numel();
+  const size_t ws_bytes =
+      mx_tbe_backward_workspace_bytes(N, static_cast<int32_t>(total_hash_size_bits),
+                                      static_cast<int32_t>(max_D));
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, dev_weights.options().dtype(at::kByte));
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  MX_CALL(mx_tbe_backward_rowwise_adagrad(
+      dev_weights.data_ptr<float>(), weights_offsets.data_ptr<int64_t>(),
+      D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B, static_cast<int32_t>(max_D),
+      hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(total_hash_size_bits),
+      idx.data_ptr(), off.data_ptr(), ib, N, static_cast<int32_t>(pooling_mode),
+      g.data_ptr<float>(), g.size(1), momentum1_dev.data_ptr<float>(),
+      momentum1_offsets.data_ptr<int64_t>(), static_cast<float>(learning_rate),
+      static_cast<float>(eps), static_cast<float>(weight_decay),
+      static_cast<int32_t>(weight_decay_mode), ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
+  return at::empty({0}, dev_weights.options());
+}
+
+class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagrad> {
+ public:
+  static Tensor forward(AutogradContext* ctx, const Tensor& placeholder,
+                        const Tensor& dev_weights, const Tensor& uvm_weights,
+                        const Tensor& weights_placements, const Tensor& weights_offsets,
+                        const Tensor& D_offsets, int64_t total_D, int64_t max_D,
+                        const Tensor& hash_size_cumsum, int64_t total_hash_size_bits,
+                        const Tensor& indices, const Tensor& offsets, int64_t pooling_mode,
+                        const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
+                        const Tensor& momentum1_placements, const Tensor& momentum1_offsets,
+                        double eps, double learning_rate, double weight_decay,
+                        int64_t weight_decay_mode, double max_norm, int64_t output_dtype) {
+    (void)placeholder;
+    // Stored as IValues: the backward updates dev_weights/momentum1 in place.
+    auto& s = ctx->saved_data;
+    s["dev_weights"] = dev_weights;
+    s["uvm_weights"] = uvm_weights;
+    s["weights_placements"] = weights_placements;
+    s["weights_offsets"] = weights_offsets;
+    s["D_offsets"] = D_offsets;
+    s["hash_size_cumsum"] = hash_size_cumsum;
+    s["indices"] = indices;
+    s["offsets"] = offsets;
+    s["momentum1_dev"] = momentum1_dev;
+    s["momentum1_uvm"] = momentum1_uvm;
+    s["momentum1_placements"] = momentum1_placements;
+    s["momentum1_offsets"] = momentum1_offsets;
+    s["max_D"] = max_D;
+    s["total_hash_size_bits"] = total_hash_size_bits;
+    s["pooling_mode"] = pooling_mode;
+    s["eps"] = eps;
+    s["learning_rate"] = learning_rate;
+    s["weight_decay"] = weight_decay;
+    s["weight_decay_mode"] = weight_decay_mode;
+    s["max_norm"] = max_norm;
+    at::AutoDispatchBelowADInplaceOrView g;
+    return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
+                       total_D, max_D, indices, offsets, pooling_mode, std::nullopt,
+                       output_dtype);
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    auto& s = ctx->saved_data;
+    Tensor grad = grads[0];
+    TORCH_CHECK(grad.scalar_type() == at::kFloat,
+                "the rowwise-Adagrad backward needs an fp32 gradient (output_dtype FP32)");
+    const Tensor empty;
+    backward_rowwise_adagrad_exact(
+        grad.contiguous(), s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
+        s["weights_placements"].toTensor(), s["weights_offsets"].toTensor(),
+        s["D_offsets"].toTensor(), c10::SymInt(s["max_D"].toInt()),
+        s["hash_size_cumsum"].toTensor(), s["total_hash_size_bits"].toInt(),
+        s["indices"].toTensor(), s["offsets"].toTensor(), s["pooling_mode"].toInt(), empty, 0, 0,
+        false, s["momentum1_dev"].toTensor(), s["momentum1_uvm"].toTensor(),
+        s["momentum1_placements"].toTensor(), s["momentum1_offsets"].toTensor(),
+        s["eps"].toDouble(), s["learning_rate"].toDouble(), s["weight_decay"].toDouble(),
+        s["weight_decay_mode"].toInt(), s["max_norm"].toDouble());
+    return variable_list(23);
+  }
+};
+
+Tensor lookup_rowwise_adagrad(
+    const Tensor& placeholder_autograd_tensor, const Tensor& dev_weights,
+    const Tensor& uvm_weights, const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt total_D,
+    c10::SymInt max_D, const Tensor& hash_size_cumsum, int64_t total_hash_size_bits,
+    const Tensor& indices, const Tensor& offsets, int64_t pooling_mode,
+    const std::optional<Tensor>& indice_weights, const std::optional<Tensor>& feature_requires_grad,
+    const Tensor& lxu_cache_locations, bool gradient_clipping, double max_gradient,
+    bool stochastic_rounding, const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
+    const Tensor& momentum1_placements, const Tensor& momentum1_offsets, double eps,
+    double learning_rate, double weight_decay, int64_t weight_decay_mode, double max_norm,
+    int64_t output_dtype) {
+  (void)lxu_cache_weights;
+  (void)feature_requires_grad;
+  (void)lxu_cache_locations;
+  (void)stochastic_rounding;
+  TORCH_CHECK(!(indice_weights.has_value() && indice_weights->defined()),
+              "weighted training lookup is not supported; use the weighted forward op");
+  TORCH_CHECK(!gradient_clipping || max_gradient <= 0.0, "gradient clipping is not supported");
+  return LookupRowwiseAdagrad::apply(
+      placeholder_autograd_tensor, dev_weights, uvm_weights, weights_placements, weights_offsets,
+      D_offsets, total_D.expect_int(), max_D.expect_int(), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, momentum1_dev, momentum1_uvm, momentum1_placements,
+      momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm,
+      output_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// nbit inference
+// ---------------------------------------------------------------------------
+
+Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
+                       const Tensor& weights_placements, const Tensor& weights_offsets,
+                       const Tensor& weights_tys, const Tensor& D_offsets, c10::SymInt total_D_sym,
+                       int64_t max_int2_D, int64_t max_int4_D, int64_t max_int8_D,
+                       int64_t max_float16_D, int64_t max_float32_D, const Tensor& indices,
+                       const Tensor& offsets, int64_t pooling_mode,
+                       const std::optional<Tensor>& indice_weights, int64_t output_dtype,
+                       const std::optional<Tensor>& lxu_cache_weights,
+                       const std::optional<Tensor>& lxu_cache_locations,
+                       std::optional<int64_t> row_alignment, std::optional<int64_t> max_float8_D,
+                       std::optional<int64_t> fp8_exponent_bits,
+                       std::optional<int64_t> fp8_exponent_bias) {
+  (void)weights_placements;
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  (void)fp8_exponent_bits;
+  (void)fp8_exponent_bias;
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  for (auto* t : {&weights_offsets, &weights_tys, &D_offsets, &indices, &offsets})
+    check_gpu(*t, "nbit argument");
+  TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
+  TORCH_CHECK(max_float8_D.value_or(0) == 0, "FP8 tables are not supported");
+  TORCH_CHECK(dev_weights.scalar_type() == at::kByte && dev_weights.is_contiguous(),
+              "dev_weights must be contiguous uint8");
+  TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
+  TORCH_CHECK(weights_tys.scalar_type() == at::kByte, "weights_tys must be uint8");
+  TORCH_CHECK(D_offsets.scalar_type() == at::kInt, "D_offsets must be int32");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = D_offsets.numel() - 1;
+  TORCH_CHECK(T >= 1 && weights_tys.numel() == T && weights_offsets.numel() == T,
+              "weights_tys/weights_offsets must have T entries");
+  TORCH_CHECK((offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  const int64_t total_D = total_D_sym.expect_int();
+  TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
+              "output_dtype must be FP32 (0) or FP16 (1)");
+  const float* iw = nullptr;
+  Tensor iwc;
+  if (indice_weights.has_value() && indice_weights->defined()) {
+    check_gpu(*indice_weights, "indice_weights");
+    TORCH_CHECK(indice_weights->scalar_type() == at::kFloat, "indice_weights must be fp32");
+    iwc = indice_weights->contiguous();
+    iw = iwc.data_ptr<float>();
+  }
+  auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
+  Tensor out = at::empty({B, total_D}, opts);
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  MX_CALL(mx_nbit_forward(
+      dev_weights.data_ptr<uint8_t>(), weights_offsets.data_ptr<int64_t>(),
+      weights_tys.data_ptr<uint8_t>(), D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B,
+      static_cast<int32_t>(max_int2_D), static_cast<int32_t>(max_int4_D),
+      static_cast<int32_t>(max_int8_D), static_cast<int32_t>(max_float16_D),
+      static_cast<int32_t>(max_float32_D), idx.data_ptr(), off.data_ptr(), ib,
+      static_cast<int32_t>(pooling_mode), iw, static_cast<int32_t>(output_dtype),
+      static_cast<int32_t>(row_alignment.value_or(16)), out.data_ptr(), total_D,
+      stream_of(dev_weights)));
+  return out;
+}
+
+}  // namespace mx_ops
+
+TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
+  m.def("jagged_to_padded_dense_forward(Tensor values, Tensor[] offsets, SymInt[] max_lengths, "
+        "float padding_value=0) -> Tensor");
+  m.def("jagged_to_padded_dense(Tensor values, Tensor[] offsets, SymInt[] max_lengths, "
+        "float padding_value=0) -> Tensor");
+  m.def("jagged_to_padded_dense_backward(Tensor grad_output, Tensor[] offsets, SymInt total_L) "
+        "-> Tensor");
+  m.def("dense_to_jagged_forward(Tensor dense, Tensor[] offsets, SymInt? total_L=None) -> Tensor");
+  m.def("dense_to_jagged(Tensor dense, Tensor[] x_offsets, SymInt? total_L=None) "
+        "-> (Tensor, Tensor[])");
+  m.def("jagged_dense_elementwise_add_jagged_output(Tensor x_values, Tensor[] x_offsets, "
+        "Tensor y) -> (Tensor, Tensor[])");
+  m.def("split_embedding_codegen_forward_unweighted_cuda(Tensor dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, Tensor offsets, "
+        "int pooling_mode, Tensor lxu_cache_locations, Tensor uvm_cache_stats, "
+        "int output_dtype, bool is_experimental) -> Tensor");
+  m.def("split_embedding_codegen_forward_weighted_cuda(Tensor dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, Tensor offsets, "
+        "int pooling_mode, Tensor indice_weights, Tensor lxu_cache_locations, "
+        "Tensor uvm_cache_stats, int output_dtype, bool is_experimental) -> Tensor");
+  m.def("get_infos_metadata(Tensor unused, int B, int T) -> (int, int)");
+  m.def("transpose_embedding_input(Tensor hash_size_cumsum, int total_hash_size_bits, "
+        "Tensor indices, Tensor offsets, bool nobag=False, Tensor? vbe_b_t_map=None, "
+        "int info_B_num_bits=26, int info_B_mask=67108863, int total_unique_indices=-1) "
+        "-> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)");
+  m.def("split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda("
+        "Tensor grad_output, Tensor(a!) dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt max_D, Tensor hash_size_cumsum, int total_hash_size_bits, "
+        "Tensor indices, Tensor offsets, int pooling_mode, Tensor lxu_cache_locations, "
+        "int BT_block_size, int max_segment_length_per_warp, bool stochastic_rounding, "
+        "Tensor(b!) momentum1_dev, Tensor momentum1_uvm, Tensor momentum1_placements, "
+        "Tensor momentum1_offsets, float eps=0, float learning_rate=0, float weight_decay=0.0, "
+        "int weight_decay_mode=0, float max_norm=0.0) -> Tensor");
+  m.def("split_embedding_codegen_lookup_rowwise_adagrad_function(Tensor placeholder_autograd_tensor, "
+        "Tensor dev_weights, Tensor uvm_weights, Tensor lxu_cache_weights, "
+        "Tensor weights_placements, Tensor weights_offsets, Tensor D_offsets, SymInt total_D, "
+        "SymInt max_D, Tensor hash_size_cumsum, int total_hash_size_bits, Tensor indices, "
+        "Tensor offsets, int pooling_mode, Tensor? indice_weights, Tensor? feature_requires_grad, "
+        "Tensor lxu_cache_locations, bool gradient_clipping, float max_gradient, "
+        "bool stochastic_rounding, Tensor momentum1_dev, Tensor momentum1_uvm, "
+        "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
+        "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
+        "float max_norm=0.0, int output_dtype=0) -> Tensor");
+  m.def("int_nbit_split_embedding_codegen_lookup_function(Tensor dev_weights, "
+        "Tensor uvm_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor weights_tys, Tensor D_offsets, SymInt total_D, int max_int2_D, int max_int4_D, "
+        "int max_int8_D, int max_float16_D, int max_float32_D, Tensor indices, Tensor offsets, "
+        "int pooling_mode, Tensor? indice_weights, int output_dtype, "
+        "Tensor? lxu_cache_weights, Tensor? lxu_cache_locations, int? row_alignment=None, "
+        "int? max_float8_D=0, int? fp8_exponent_bits=-1, int? fp8_exponent_bias=-1) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
+  m.impl("jagged_to_padded_dense_forward", TORCH_FN(mx_ops::jagged_to_padded_dense_forward));
+  m.impl("jagged_to_padded_dense", TORCH_FN(mx_ops::jagged_to_padded_dense_plain));
+  m.impl("jagged_to_padded_dense_backward", TORCH_FN(mx_ops::jagged_to_padded_dense_backward));
+  m.impl("dense_to_jagged_forward", TORCH_FN(mx_ops::dense_to_jagged_forward));
+  m.impl("dense_to_jagged", TORCH_FN(mx_ops::dense_to_jagged_plain));
+  m.impl("jagged_dense_elementwise_add_jagged_output", TORCH_FN(mx_ops::jagged_dense_add_plain));
+  m.impl("split_embedding_codegen_forward_unweighted_cuda", TORCH_FN(mx_ops::forward_unweighted));
+  m.impl("split_embedding_codegen_forward_weighted_cuda", TORCH_FN(mx_ops::forward_weighted));
+  m.impl("transpose_embedding_input", TORCH_FN(mx_ops::transpose_embedding_input));
+  m.impl("split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
+         TORCH_FN(mx_ops::backward_rowwise_adagrad_exact));
+  m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",
+         TORCH_FN(mx_ops::lookup_rowwise_adagrad));
+  m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
+}
+
+TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {
+  m.impl("jagged_to_padded_dense", TORCH_FN(mx_ops::jagged_to_padded_dense_autograd));
+  m.impl("dense_to_jagged", TORCH_FN(mx_ops::dense_to_jagged_autograd));
+  m.impl("jagged_dense_elementwise_add_jagged_output", TORCH_FN(mx_ops::jagged_dense_add_autograd));
+  m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",
+         TORCH_FN(mx_ops::lookup_rowwise_adagrad));
+}
+
+TORCH_LIBRARY_IMPL(fbgemm, CompositeExplicitAutograd, m) {
+  m.impl("get_infos_metadata", TORCH_FN(mx_ops::get_infos_metadata));
+}

@@ -1,0 +1,726 @@
+// TBE backward for gfx950: transpose_embedding_input (linearize, stable LSD
+// radix sort of (key, info) pairs, run-length encoding) and the fused
+// segment-reduce + exact rowwise-Adagrad update.
+//
+// Semantics: fbgemm_gpu transpose_embedding_input (upstream
+// src/split_embeddings_utils/, recalled) and
+// split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda with
+// the rowwise_adagrad update rule of upstream codegen/genscript/optimizers.py
+// (recalled; textbook rowwise Adagrad):
+//   h += mean_d(g_d^2);  m = lr / (sqrt(h) + eps);  w = c*w - m*g.
+//
+// Design:
+//  * Keys fit 32 bits whenever total_hash_size_bits <= 32, so the sort moves
+//    (u32 key, u32 info) pairs: ceil(bits/8) passes of 8-bit digits.  A pass
+//    is histogram -> one device-wide exclusive scan (digit-major) ->
+//    scatter.  The unit of work is one wave and a 1024-key tile; inside a
+//    tile keys are ranked 64 at a time with 8 ballots (peer mask of equal
+//    digits), so the scatter is stable without block barriers.
+//  * Run-length encoding is a head-flag scan.
+//  * Each run (one distinct (t, i)) is reduced by one wave, lanes owning
+//    columns, occurrences added in sorted order.  Runs longer than kLong are
+//    cut into kChunk-occurrence chunks reduced in parallel into a workspace,
+//    then summed in chunk order by the run's wave.  No atomics: results are
+//    deterministic.
+#include "mx_common.h"
+#include "scan.h"
+
+namespace mx {
+
+__global__ void __launch_bounds__(1024)
+    scan_tiles_kernel(uint32_t* tile_sums, int64_t ntiles, uint32_t* total_out) {
+  __shared__ uint32_t wsum[16];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t per = ceil_div(ntiles, 1024);
+  const int64_t b0 = threadIdx.x * per;
+  uint32_t s = 0;
+  for (int64_t i = b0; i < b0 + per && i < ntiles; ++i) s += tile_sums[i];
+  const uint32_t incl = wave_incl_scan(s);
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+  for (int i = 0; i < 16; ++i) {
+    if (i < w) before += wsum[i];
+    all += wsum[i];
+  }
+  uint32_t run = before + incl - s;
+  for (int64_t i = b0; i < b0 + per && i < ntiles; ++i) {
+    const uint32_t v = tile_sums[i];
+    tile_sums[i] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0 && total_out) *total_out = all;
+}
+
+namespace {
+
+constexpr int kRadixBits = 8;
+constexpr int kRadix = 1 << kRadixBits;
+constexpr int kSortItems = 16;
+constexpr int64_t kSortTile = 64 * kSortItems;  // keys per wave-tile
+constexpr int kLong = 64;                       // runs longer than this are chunked
+constexpr int kChunk = 64;                      // occurrences per chunk
+
+// ---- linearize ------------------------------------------------------------
+
+template <typename I>
+__global__ void __launch_bounds__(256)
+    linearize_kernel(const int64_t* __restrict__ hsc, const I* __restrict__ indices,
+                     const I* __restrict__ offsets, int64_t nbags, int64_t B, int32_t nb,
+                     int64_t N, int64_t* __restrict__ linear_out, uint32_t* __restrict__ keys,
+                     uint32_t* __restrict__ vals) {
+  const int64_t l = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (l >= N) return;
+  // Bag owning position l: last bag with offsets[bag] <= l.
+  int64_t lo = 0, hi = nbags;  // offsets[lo] <= l < offsets[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = lo + ((hi - lo) >> 1);
+    if (static_cast<int64_t>(offsets[mid]) <= l)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  const int64_t t = lo / B;
+  const int64_t b = lo - t * B;
+  const int64_t key = hsc[t] + static_cast<int64_t>(indices[l]);
+  if (linear_out) linear_out[l] = key;
+  keys[l] = static_cast<uint32_t>(key);
+  vals[l] = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+}
+
+// ---- radix sort -----------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+    radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift, int nbits,
+                      uint32_t* __restrict__ hist, int64_t ntiles) {
+  __shared__ uint32_t cnt[4][kRadix];
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  for (int d = lane; d < kRadix; d += 64) cnt[w][d] = 0;
+  __syncthreads();
+  const uint32_t mask = (1u << nbits) - 1u;
+  if (tile < ntiles) {
+#pragma unroll 4
+    for (int it = 0; it < kSortItems; ++it) {
+      const int64_t i = tile * kSortTile + it * 64 + lane;
+      if (i < n) atomicAdd(&cnt[w][(keys[i] >> shift) & mask], 1u);
+    }
+  }
+  __syncthreads();
+  if (tile < ntiles)
+    for (int d = lane; d < kRadix; d += 64) hist[d * ntiles + tile] = cnt[w][d];
+}
+
+struct LoadU32 {
+  const uint32_t* p;
+  __device__ uint32_t operator()(int64_t i) const { return p[i]; }
+};
+
+template <bool LAST>
+__global__ void __launch_bounds__(256)
+    radix_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+                         int64_t n, int shift, int nbits, const uint32_t* __restrict__ hist_scan,
+                         int64_t ntiles, uint32_t* __restrict__ keys_out,
+                         int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out) {
+  __shared__ uint32_t base[4][kRadix];
+  const int w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  if (tile < ntiles)
+    for (int d = lane; d < kRadix; d += 64) base[w][d] = hist_scan[d * ntiles + tile];
+  __syncthreads();
+  if (tile >= ntiles) return;
+  const uint32_t mask = (1u << nbits) - 1u;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int it = 0; it < kSortItems; ++it) {
+    const int64_t i = tile * kSortTile + it * 64 + lane;
+    const bool valid = i < n;
+    const uint32_t k = valid ? keys[i] : 0u;
+    const uint32_t v = valid ? vals[i] : 0u;
+    const uint32_t d = (k >> shift) & mask;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool set = (d >> bit) & 1u;
+      const uint64_t bb = __ballot(set);
+      peers &= set ? bb : ~bb;
+    }
+    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt));
+    const uint32_t pos = base[w][d] + rank;
+    if (valid) {
+      if constexpr (LAST)
+        keys_out64[pos] = static_cast<int64_t>(k);
+      else
+        keys_out[pos] = k;
+      vals_out[pos] = v;
+    }
+    // The lowest lane of each digit group advances that digit's cursor after
+    // every lane of the wave has read it above (LDS ops of a wave are ordered).
+    if (valid && rank == 0) base[w][d] = pos + static_cast<uint32_t>(__popcll(peers));
+  }
+}
+
+__global__ void copy_keys_kernel(const uint32_t* __restrict__ keys,
+                                 const uint32_t* __restrict__ vals, int64_t n,
+                                 int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  keys_out64[i] = keys[i];
+  vals_out[i] = vals[i];
+}
+
+// ---- run-length encoding --------------------------------------------------
+
+struct HeadFlag {
+  const int64_t* keys;
+  __device__ uint32_t operator()(int64_t i) const {
+    return (i == 0 || keys[i] != keys[i - 1]) ? 1u : 0u;
+  }
+};
+
+__global__ void __launch_bounds__(256)
+    rle_write_kernel(const int64_t* __restrict__ keys, int64_t n,
+                     const uint32_t* __restrict__ run_id, const uint32_t* __restrict__ num_runs,
+                     int64_t* __restrict__ run_keys, int32_t* __restrict__ cum) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i == 0) cum[*num_runs] = static_cast<int32_t>(n);
+  if (i >= n) return;
+  if (i == 0 || keys[i] != keys[i - 1]) {
+    const uint32_t r = run_id[i];
+    run_keys[r] = keys[i];
+    cum[r] = static_cast<int32_t>(i);
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    run_lengths_kernel(const int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
+                       int64_t n, int32_t* __restrict__ lengths, int32_t* __restrict__ num_runs_out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t m = *num_runs;
+  if (r == 0 && num_runs_out) *num_runs_out = static_cast<int32_t>(m);
+  if (r >= m || r >= n) return;
+  lengths[r] = cum[r + 1] - cum[r];
+}
+
+struct ChunkCount {
+  const int32_t* cum;
+  __device__ uint32_t operator()(int64_t r) const {
+    const int32_t len = cum[r + 1] - cum[r];
+    return len > kLong ? static_cast<uint32_t>((len + kChunk - 1) / kChunk) : 0u;
+  }
+};
+
+// ---- workspace layout -----------------------------------------------------
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct SortWs {
+  uint32_t* keys[2];
+  uint32_t* vals[2];
+  uint32_t* hist;
+  uint32_t* tiles;
+  uint32_t* run_id;
+  uint32_t* counters;  // [0] num_runs, [1] total chunks
+  size_t bytes;
+};
+
+SortWs carve_sort(uint8_t* base, int64_t N) {
+  SortWs w{};
+  const int64_t n = N > 0 ? N : 1;
+  const int64_t ntiles = ceil_div(n, kSortTile);
+  const int64_t hist_n = kRadix * ntiles;
+  const int64_t scan_buf = scan_tiles(hist_n > n + 1 ? hist_n : n + 1);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  for (int i = 0; i < 2; ++i) {
+    w.keys[i] = reinterpret_cast<uint32_t*>(take(n * 4));
+    w.vals[i] = reinterpret_cast<uint32_t*>(take(n * 4));
+  }
+  w.hist = reinterpret_cast<uint32_t*>(take(hist_n * 4));
+  w.tiles = reinterpret_cast<uint32_t*>(take(scan_buf * 4));
+  w.run_id = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
+  w.counters = reinterpret_cast<uint32_t*>(take(64));
+  w.bytes = off;
+  return w;
+}
+
+struct TransposeOut {
+  int64_t* linear;      // may be null
+  int64_t* sorted;      // [N]
+  int32_t* infos;       // [N]
+  int64_t* run;         // [N]
+  int32_t* run_lengths; // [N]
+  int32_t* num_runs;    // [1]
+  int32_t* cum;         // [N+1]
+};
+
+int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_t nb,
+                  const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+                  const TransposeOut& o, SortWs& w, hipStream_t s) {
+  const int64_t nbags = static_cast<int64_t>(T) * B;
+  const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
+  if (index_bytes == 8)
+    linearize_kernel<int64_t><<<g256, 256, 0, s>>>(
+        hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
+        nb, N, o.linear, w.keys[0], w.vals[0]);
+  else
+    linearize_kernel<int32_t><<<g256, 256, 0, s>>>(
+        hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
+        nb, N, o.linear, w.keys[0], w.vals[0]);
+  MX_LAUNCH_CHECK();
+
+  const int64_t ntiles = ceil_div(N, kSortTile);
+  const dim3 gsort(static_cast<uint32_t>(ceil_div(ntiles, 4)));
+  const int passes = (bits + kRadixBits - 1) / kRadixBits;
+  int cur = 0;
+  if (passes == 0) {
+    copy_keys_kernel<<<g256, 256, 0, s>>>(w.keys[0], w.vals[0], N, o.sorted,
+                                          reinterpret_cast<uint32_t*>(o.infos));
+    MX_LAUNCH_CHECK();
+  }
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * kRadixBits;
+    const int nbits = bits - shift < kRadixBits ? bits - shift : kRadixBits;
+    radix_hist_kernel<<<gsort, 256, 0, s>>>(w.keys[cur], N, shift, nbits, w.hist, ntiles);
+    MX_LAUNCH_CHECK();
+    if (int rc = exclusive_scan(LoadU32{w.hist}, kRadix * ntiles, nullptr, w.hist, nullptr,
+                                w.tiles, s))
+      return rc;
+    const bool last = p == passes - 1;
+    if (last) {
+      radix_scatter_kernel<true><<<gsort, 256, 0, s>>>(
+          w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, nullptr, o.sorted,
+          reinterpret_cast<uint32_t*>(o.infos));
+    } else {
+      radix_scatter_kernel<false><<<gsort, 256, 0, s>>>(
+          w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, w.keys[cur ^ 1], nullptr,
+          w.vals[cur ^ 1]);
+    }
+    MX_LAUNCH_CHECK();
+    cur ^= 1;
+  }
+
+  // Run-length encode the sorted keys.
+  if (int rc = exclusive_scan(HeadFlag{o.sorted}, N, nullptr, w.run_id, &w.counters[0], w.tiles, s))
+    return rc;
+  rle_write_kernel<<<g256, 256, 0, s>>>(o.sorted, N, w.run_id, &w.counters[0], o.run, o.cum);
+  MX_LAUNCH_CHECK();
+  run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths, o.num_runs);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+// ---- segment reduce + rowwise Adagrad -------------------------------------
+
+struct BwdArgs {
+  float* W;
+  const int64_t* w_off;
+  const int32_t* D_off;
+  const int64_t* hsc;
+  const void* offsets;
+  const float* grad;
+  float* m1;
+  const int64_t* m1_off;
+  const int64_t* run;
+  const int32_t* cum;
+  const int32_t* infos;
+  const uint32_t* num_runs;
+  const uint32_t* chunk_start;
+  const uint32_t* total_chunks;
+  float* partial;
+  int64_t B;
+  int64_t total_D;
+  int32_t max_D;
+  int32_t nb;
+  int32_t pooling;
+  int32_t wd_mode;
+  float lr;
+  float eps;
+  float wd;
+};
+
+template <int VEC>
+__device__ __forceinline__ void ldv(const float* p, float (&v)[VEC]) {
+  if constexpr (VEC == 4) {
+    const float4 x = *reinterpret_cast<const float4*>(p);
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+  } else if constexpr (VEC == 2) {
+    const float2 x = *reinterpret_cast<const float2*>(p);
+    v[0] = x.x; v[1] = x.y;
+  } else {
+    v[0] = *p;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void stv(float* p, const float (&v)[VEC]) {
+  if constexpr (VEC == 4)
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else if constexpr (VEC == 2)
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  else
+    *p = v[0];
+}
+
+// Sum of the (MEAN-scaled) gradient rows of occurrences [s0, s1) into g, in
+// order.  All occurrences belong to table t.
+template <typename I, int VEC, int NCH, int U>
+__device__ void sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int64_t s0, int64_t s1,
+                                const bool (&active)[NCH], int lane, float (&g)[NCH][VEC]) {
+  const uint32_t bmask = (a.nb >= 32) ? 0xffffffffu : ((1u << a.nb) - 1u);
+  for (int64_t base = s0; base < s1; base += 64) {
+    const int n = static_cast<int>(s1 - base < 64 ? s1 - base : 64);
+    int32_t my_b = 0;
+    float my_s = 1.0f;
+    if (lane < n) {
+      my_b = static_cast<int32_t>(static_cast<uint32_t>(a.infos[base + lane]) & bmask);
+      if (a.pooling == MX_POOL_MEAN) {
+        const I* off = static_cast<const I*>(a.offsets);
+        const int64_t bag = t * a.B + my_b;
+        const int64_t L = static_cast<int64_t>(off[bag + 1]) - static_cast<int64_t>(off[bag]);
+        my_s = L > 0 ? 1.0f / static_cast<float>(L) : 0.0f;
+      }
+    }
+    for (int j = 0; j < n; j += U) {
+      float v[U][NCH][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          const int64_t b = readlane_i32(my_b, j + u);
+          const float* row = a.grad + b * a.total_D + D0;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if (active[c]) ldv<VEC>(row + (c * 64 + lane) * VEC, v[u][c]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          const float sc = __shfl(my_s, j + u, 64);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if (active[c]) {
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                if (a.pooling == MX_POOL_MEAN)
+                  g[c][e] += __fmul_rn(v[u][c][e], sc);
+                else
+                  g[c][e] += v[u][c][e];
+              }
+            }
+        }
+      }
+    }
+  }
+}
+
+// Pass A: partial sums of the chunks of long runs.
+template <typename I, int VEC, int NCH, int U>
+__global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t total = *a.total_chunks;
+  const int64_t nruns = *a.num_runs;
+  for (int64_t q = wave; q < total; q += nwaves) {
+    // Run r with chunk_start[r] <= q < chunk_start[r+1].
+    int64_t lo = 0, hi = nruns;
+    while (hi - lo > 1) {
+      const int64_t mid = lo + ((hi - lo) >> 1);
+      if (static_cast<int64_t>(a.chunk_start[mid]) <= q)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const int64_t r = lo;
+    const int64_t k = q - a.chunk_start[r];
+    const int64_t s0 = a.cum[r] + k * kChunk;
+    const int64_t s1e = s0 + kChunk;
+    const int64_t s1 = s1e < a.cum[r + 1] ? s1e : a.cum[r + 1];
+    const int64_t t = a.nb >= 32 ? 0 : (static_cast<uint32_t>(a.infos[s0]) >> a.nb);
+    const int32_t D0 = a.D_off[t];
+    const int32_t D = a.D_off[t + 1] - D0;
+    bool active[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
+    float g[NCH][VEC];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) g[c][e] = 0.0f;
+    sum_occurrences<I, VEC, NCH, U>(a, t, D0, s0, s1, active, lane, g);
+    float* dst = a.partial + q * a.max_D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (active[c]) stv<VEC>(dst + (c * 64 + lane) * VEC, g[c]);
+  }
+}
+
+// Pass B: one wave per run -- gradient sum, rowwise Adagrad, in-place update.
+template <typename I, int VEC, int NCH, int U>
+__global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t nruns = *a.num_runs;
+  for (int64_t r = wave; r < nruns; r += nwaves) {
+    const int64_t s0 = a.cum[r];
+    const int64_t s1 = a.cum[r + 1];
+    const int64_t t = a.nb >= 32 ? 0 : (static_cast<uint32_t>(a.infos[s0]) >> a.nb);
+    const int32_t D0 = a.D_off[t];
+    const int32_t D = a.D_off[t + 1] - D0;
+    const int64_t idx = a.run[r] - a.hsc[t];
+    bool active[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
+    float g[NCH][VEC];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) g[c][e] = 0.0f;
+    if (s1 - s0 <= kLong) {
+      sum_occurrences<I, VEC, NCH, U>(a, t, D0, s0, s1, active, lane, g);
+    } else {
+      const int64_t q0 = a.chunk_start[r];
+      const int64_t q1 = q0 + (s1 - s0 + kChunk - 1) / kChunk;
+      for (int64_t q = q0; q < q1; q += U) {
+        float v[U][NCH][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (q + u < q1)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+              if (active[c]) ldv<VEC>(a.partial + (q + u) * a.max_D + (c * 64 + lane) * VEC, v[u][c]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (q + u < q1)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+              if (active[c])
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) g[c][e] += v[u][c][e];
+      }
+    }
+    float* wrow = a.W + a.w_off[t] + idx * D;
+    float w[NCH][VEC];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (!active[c]) continue;
+      ldv<VEC>(wrow + (c * 64 + lane) * VEC, w[c]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float ge = g[c][e];
+        if (a.wd_mode == 1) ge = __builtin_fmaf(a.wd, w[c][e], ge);
+        ss = __builtin_fmaf(ge, ge, ss);
+      }
+    }
+    ss = wave_sum(ss);
+    float* hp = a.m1 + a.m1_off[t] + idx;
+    const float h = *hp + ss / static_cast<float>(D);
+    const float mult = a.lr / (sqrtf(h) + a.eps);
+    float corr = 1.0f;
+    if (a.wd_mode == 1) corr = 1.0f - mult * a.wd;
+    else if (a.wd_mode == 2) corr = 1.0f - a.lr * a.wd;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (!active[c]) continue;
+      float nw[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) nw[e] = __builtin_fmaf(-mult, g[c][e], __fmul_rn(corr, w[c][e]));
+      stv<VEC>(wrow + (c * 64 + lane) * VEC, nw);
+    }
+    if (lane == 0) *hp = h;
+  }
+}
+
+template <typename I, int VEC, int NCH>
+int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
+  constexpr int U = VEC * NCH <= 2 ? 8 : (VEC * NCH <= 4 ? 4 : 2);
+  const int64_t want = ceil_div(N, 4);
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
+  const dim3 grid(static_cast<uint32_t>(want < 1 ? 1 : (want > cap ? cap : want)));
+  bwd_chunk_kernel<I, VEC, NCH, U><<<grid, 256, 0, s>>>(a);
+  MX_LAUNCH_CHECK();
+  bwd_update_kernel<I, VEC, NCH, U><<<grid, 256, 0, s>>>(a);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+template <typename I>
+int dispatch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
+  if (a.max_D <= 64) return launch_bwd<I, 1, 1>(a, N, s);
+  if (a.max_D <= 128) return launch_bwd<I, 2, 1>(a, N, s);
+  if (a.max_D <= 256) return launch_bwd<I, 4, 1>(a, N, s);
+  if (a.max_D <= 512) return launch_bwd<I, 4, 2>(a, N, s);
+  return launch_bwd<I, 4, 4>(a, N, s);
+}
+
+struct BwdWs {
+  SortWs sort;
+  int64_t* sorted;
+  int32_t* infos;
+  int64_t* run;
+  int32_t* run_lengths;
+  int32_t* num_runs;
+  int32_t* cum;
+  uint32_t* chunk_start;
+  float* partial;
+  size_t bytes;
+};
+
+int64_t max_chunks(int64_t N) { return N / kChunk + N / (kLong + 1) + 2; }
+
+BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
+  BwdWs w{};
+  w.sort = carve_sort(base, N);
+  size_t off = w.sort.bytes;
+  const int64_t n = N > 0 ? N : 1;
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  w.sorted = reinterpret_cast<int64_t*>(take(n * 8));
+  w.infos = reinterpret_cast<int32_t*>(take(n * 4));
+  w.run = reinterpret_cast<int64_t*>(take(n * 8));
+  w.run_lengths = reinterpret_cast<int32_t*>(take(n * 4));
+  w.num_runs = reinterpret_cast<int32_t*>(take(4));
+  w.cum = reinterpret_cast<int32_t*>(take((n + 1) * 4));
+  w.chunk_start = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
+  w.partial = reinterpret_cast<float*>(take(static_cast<size_t>(max_chunks(n)) * max_D * 4));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int32_t mx_tbe_info_B_num_bits(int32_t T, int64_t B) {
+  if (T < 0 || B < 0) return -1;
+  int tb = 0;
+  while ((int64_t(1) << tb) < T) ++tb;  // bits for t in [0, T)
+  int bb = 1;
+  while ((int64_t(1) << bb) < B) ++bb;  // bits for b in [0, B)
+  if (tb + bb > 32) return -1;
+  // 26 bits for b (room for 64 tables) unless T or B need a different split.
+  if (bb <= 26 && tb <= 6) return 26;
+  return 32 - tb;
+}
+
+extern "C" size_t mx_tbe_transpose_workspace_bytes(int64_t N, int32_t total_hash_size_bits) {
+  (void)total_hash_size_bits;
+  return carve_sort(nullptr, N).bytes;
+}
+
+static int check_common(int32_t T, int64_t B, int32_t bits, int32_t nb, int32_t index_bytes,
+                        int64_t N) {
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative size");
+  MX_REQUIRE(bits >= 0 && bits <= 32, "total_hash_size_bits %d not in [0, 32]", bits);
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(N < 0x7fffffffll, "N %lld too large for int32 run offsets", (long long)N);
+  MX_REQUIRE(nb >= 1 && nb <= 32, "info_B_num_bits %d invalid", nb);
+  MX_REQUIRE(B <= (int64_t(1) << nb), "B does not fit info_B_num_bits");
+  return MX_OK;
+}
+
+extern "C" int mx_tbe_transpose_embedding_input(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
+    int32_t info_B_num_bits, const void* indices, const void* offsets, int32_t index_bytes,
+    int64_t N, int64_t* linear_indices, int64_t* sorted_linear_indices, int32_t* infos_sorted,
+    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_common(T, B, total_hash_size_bits, info_B_num_bits, index_bytes, N)) return rc;
+  auto* s = as_stream(stream);
+  if (N == 0) {
+    if (num_runs) MX_HIP_CHECK(hipMemsetAsync(num_runs, 0, sizeof(int32_t), s));
+    if (cumulative_run_lengths)
+      MX_HIP_CHECK(hipMemsetAsync(cumulative_run_lengths, 0, sizeof(int32_t), s));
+    return MX_OK;
+  }
+  MX_REQUIRE(hash_size_cumsum && indices && offsets && sorted_linear_indices && infos_sorted &&
+                 sorted_linear_indices_run && run_lengths && num_runs && cumulative_run_lengths,
+             "null pointer argument");
+  SortWs w = carve_sort(static_cast<uint8_t*>(workspace), N);
+  if (workspace == nullptr || workspace_bytes < w.bytes)
+    return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
+  TransposeOut o{linear_indices, sorted_linear_indices, infos_sorted, sorted_linear_indices_run,
+                 run_lengths, num_runs, cumulative_run_lengths};
+  return run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, info_B_num_bits, indices,
+                       offsets, index_bytes, N, o, w, s);
+}
+
+extern "C" size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits,
+                                                  int32_t max_D) {
+  (void)total_hash_size_bits;
+  return carve_bwd(nullptr, N, max_D > 0 ? max_D : 1).bytes;
+}
+
+extern "C" int mx_tbe_backward_rowwise_adagrad(
+    float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
+    int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    int32_t pooling_mode, const float* grad_output, int64_t total_D, float* momentum1,
+    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
+    int32_t weight_decay_mode, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const int32_t nb = mx_tbe_info_B_num_bits(T, B);
+  MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
+  if (int rc = check_common(T, B, total_hash_size_bits, nb, index_bytes, N)) return rc;
+  MX_REQUIRE(max_D > 0 && max_D <= 1024 && max_D % 4 == 0,
+             "max_D %d must be a multiple of 4 in [4, 1024]", max_D);
+  MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
+             "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
+  MX_REQUIRE(weight_decay_mode >= 0 && weight_decay_mode <= 2,
+             "weight_decay_mode %d not supported (0 none, 1 L2, 2 decoupled)", weight_decay_mode);
+  if (N == 0) return MX_OK;
+  MX_REQUIRE(weights && weights_offsets && D_offsets && hash_size_cumsum && indices && offsets &&
+                 grad_output && momentum1 && momentum1_offsets,
+             "null pointer argument");
+  BwdWs w = carve_bwd(static_cast<uint8_t*>(workspace), N, max_D);
+  if (workspace == nullptr || workspace_bytes < w.bytes)
+    return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
+  auto* s = as_stream(stream);
+  TransposeOut o{nullptr, w.sorted, w.infos, w.run, w.run_lengths, w.num_runs, w.cum};
+  if (int rc = run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, nb, indices, offsets,
+                             index_bytes, N, o, w.sort, s))
+    return rc;
+  // Chunk layout of long runs.
+  if (int rc = exclusive_scan(ChunkCount{w.cum}, N, w.num_runs, w.chunk_start,
+                              &w.sort.counters[1], w.sort.tiles, s))
+    return rc;
+  BwdArgs a;
+  a.W = weights;
+  a.w_off = weights_offsets;
+  a.D_off = D_offsets;
+  a.hsc = hash_size_cumsum;
+  a.offsets = offsets;
+  a.grad = grad_output;
+  a.m1 = momentum1;
+  a.m1_off = momentum1_offsets;
+  a.run = w.run;
+  a.cum = w.cum;
+  a.infos = w.infos;
+  a.num_runs = &w.sort.counters[0];
+  a.chunk_start = w.chunk_start;
+  a.total_chunks = &w.sort.counters[1];
+  a.partial = w.partial;
+  a.B = B;
+  a.total_D = total_D;
+  a.max_D = max_D;
+  a.nb = nb;
+  a.pooling = pooling_mode;
+  a.wd_mode = weight_decay_mode;
+  a.lr = learning_rate;
+  a.eps = eps;
+  a.wd = weight_decay;
+  return index_bytes == 8 ? dispatch_bwd<int64_t>(a, N, s) : dispatch_bwd<int32_t>(a, N, s);
+}

@@ -1,0 +1,225 @@
+// Table-batched embedding (TBE) training forward, fp32 weights, gfx950.
+//
+// Semantics: fbgemm_gpu split_embedding_codegen_forward_{unweighted,weighted}
+// (upstream codegen/training/forward/, recalled), i.e. the pooled SpMDM of
+// torch/include/fbgemm/FbgemmEmbedding.h:26-39 applied per table:
+//   out[b, D_off[t] + d] = sum_{l in bag(t,b)} W_t[idx[l], d]   (SUM)
+//   MEAN multiplies the sum by 1/L for L > 0; an empty bag gives 0.
+//
+// Design: one wave64 per bag.  Lane k owns columns [k*VEC, k*VEC+VEC) of
+// each 64*VEC-column chunk, so a wave reads a whole row with one coalesced
+// load (D=128: 64 lanes x 8 B = 512 B) and every column is accumulated in
+// index order -- the sum is bit-identical to a sequential CPU loop.  The
+// bag's indices are fetched 64 at a time with one coalesced load and moved
+// to scalar registers with v_readlane, so row addresses are computed on the
+// scalar unit; U rows are loaded before any is accumulated to keep
+// U * 512 B in flight per wave.  Blocks are remapped so that each XCD works
+// on a contiguous range of bags (t-major), keeping one table's hot rows in
+// one XCD's L2.
+#include "mx_common.h"
+
+namespace mx {
+namespace {
+
+template <int VEC>
+struct VecF;
+template <>
+struct VecF<1> {
+  using T = float;
+};
+template <>
+struct VecF<2> {
+  using T = float2;
+};
+template <>
+struct VecF<4> {
+  using T = float4;
+};
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float* p, float (&v)[VEC]) {
+  using T = typename VecF<VEC>::T;
+  const T x = *reinterpret_cast<const T*>(p);
+  if constexpr (VEC == 1) {
+    v[0] = x;
+  } else if constexpr (VEC == 2) {
+    v[0] = x.x;
+    v[1] = x.y;
+  } else {
+    v[0] = x.x;
+    v[1] = x.y;
+    v[2] = x.z;
+    v[3] = x.w;
+  }
+}
+
+constexpr int kWavesPerBlock = 4;
+
+template <typename I, int VEC, int NCH, int U, bool WEIGHTED, bool OUT_F16>
+__global__ void __launch_bounds__(256)
+    tbe_fwd_kernel(const float* __restrict__ W, const int64_t* __restrict__ w_off,
+                   const int32_t* __restrict__ D_off, int64_t B, const I* __restrict__ indices,
+                   const I* __restrict__ offsets, int32_t pooling, const float* __restrict__ iw,
+                   void* __restrict__ out, int64_t total_D, int64_t nbags) {
+  const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bag = lb * kWavesPerBlock + (threadIdx.x >> 6);
+  if (bag >= nbags) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = bag / B;
+  const int64_t b = bag - t * B;
+  const int32_t D0 = D_off[t];
+  const int32_t D = D_off[t + 1] - D0;
+  const float* __restrict__ Wt = W + w_off[t];
+  const int64_t start = static_cast<int64_t>(offsets[bag]);
+  const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
+
+  float acc[NCH][VEC];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[c][e] = 0.0f;
+
+  bool active[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
+
+  for (int64_t base = start; base < end; base += 64) {
+    const int n = static_cast<int>(end - base < 64 ? end - base : 64);
+    const int64_t my_idx = lane < n ? static_cast<int64_t>(indices[base + lane]) : 0;
+    float my_w = 0.0f;
+    if constexpr (WEIGHTED) my_w = lane < n ? iw[base + lane] : 0.0f;
+    for (int j = 0; j < n; j += U) {
+      float v[U][NCH][VEC];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          const int64_t r = readlane_i64(my_idx, j + u);
+          const float* row = Wt + r * D;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            if (active[c]) load_vec<VEC>(row + (c * 64 + lane) * VEC, v[u][c]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          float wgt = 1.0f;
+          if constexpr (WEIGHTED) wgt = __shfl(my_w, j + u, 64);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            if (active[c]) {
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                if constexpr (WEIGHTED)
+                  acc[c][e] = __builtin_fmaf(wgt, v[u][c][e], acc[c][e]);
+                else
+                  acc[c][e] += v[u][c][e];
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+
+  const int64_t L = end - start;
+  if (pooling == MX_POOL_MEAN && L > 0) {
+    const float inv = 1.0f / static_cast<float>(L);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[c][e] *= inv;
+  }
+
+  const int64_t obase = b * total_D + D0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (!active[c]) continue;
+    const int64_t col = obase + (c * 64 + lane) * VEC;
+    if constexpr (OUT_F16) {
+      __half* o = reinterpret_cast<__half*>(out) + col;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[e] = __float2half_rn(acc[c][e]);
+    } else {
+      float* o = reinterpret_cast<float*>(out) + col;
+      if constexpr (VEC == 4)
+        *reinterpret_cast<float4*>(o) = make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
+      else if constexpr (VEC == 2)
+        *reinterpret_cast<float2*>(o) = make_float2(acc[c][0], acc[c][1]);
+      else
+        o[0] = acc[c][0];
+    }
+  }
+}
+
+template <typename I, int VEC, int NCH, bool WEIGHTED, bool OUT_F16>
+void launch_fwd(hipStream_t s, const float* W, const int64_t* w_off, const int32_t* D_off,
+                int64_t B, const void* idx, const void* off, int32_t pooling, const float* iw,
+                void* out, int64_t total_D, int64_t nbags) {
+  constexpr int U = VEC * NCH <= 2 ? 8 : (VEC * NCH <= 4 ? 4 : 2);
+  const int64_t grid = ceil_div(nbags, kWavesPerBlock);
+  tbe_fwd_kernel<I, VEC, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
+      W, w_off, D_off, B, static_cast<const I*>(idx), static_cast<const I*>(off), pooling, iw, out,
+      total_D, nbags);
+}
+
+template <typename I, bool WEIGHTED, bool OUT_F16>
+int dispatch_fwd(hipStream_t s, int32_t max_D, const float* W, const int64_t* w_off,
+                 const int32_t* D_off, int64_t B, const void* idx, const void* off,
+                 int32_t pooling, const float* iw, void* out, int64_t total_D, int64_t nbags) {
+#define MX_FWD(VEC, NCH) \
+  launch_fwd<I, VEC, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
+  if (max_D <= 64)
+    MX_FWD(1, 1);
+  else if (max_D <= 128)
+    MX_FWD(2, 1);
+  else if (max_D <= 256)
+    MX_FWD(4, 1);
+  else if (max_D <= 512)
+    MX_FWD(4, 2);
+  else
+    MX_FWD(4, 4);
+#undef MX_FWD
+  return MX_OK;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_tbe_forward(const float* weights, const int64_t* weights_offsets,
+                              const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
+                              const void* indices, const void* offsets, int32_t index_bytes,
+                              int32_t pooling_mode, const float* indice_weights, void* out,
+                              int32_t out_dtype, int64_t total_D, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+  MX_REQUIRE(max_D >= 0 && max_D <= 1024 && max_D % 4 == 0,
+             "max_D %d must be a multiple of 4 in [0, 1024]", max_D);
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
+             "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
+  MX_REQUIRE(out_dtype == MX_SPARSE_FP32 || out_dtype == MX_SPARSE_FP16,
+             "output_dtype %d not supported (FP32=0, FP16=1)", out_dtype);
+  const int64_t nbags = static_cast<int64_t>(T) * B;
+  if (nbags == 0 || total_D == 0) return MX_OK;
+  MX_REQUIRE(weights && weights_offsets && D_offsets && offsets && out, "null pointer argument");
+  MX_REQUIRE(ceil_div(nbags, kWavesPerBlock) <= 0x7fffffffll, "too many bags");
+  auto* s = as_stream(stream);
+  const bool w = indice_weights != nullptr;
+  const bool h = out_dtype == MX_SPARSE_FP16;
+#define MX_ARGS s, max_D, weights, weights_offsets, D_offsets, B, indices, offsets, pooling_mode, \
+                indice_weights, out, total_D, nbags
+  if (index_bytes == 8) {
+    if (w) h ? dispatch_fwd<int64_t, true, true>(MX_ARGS) : dispatch_fwd<int64_t, true, false>(MX_ARGS);
+    else h ? dispatch_fwd<int64_t, false, true>(MX_ARGS) : dispatch_fwd<int64_t, false, false>(MX_ARGS);
+  } else {
+    if (w) h ? dispatch_fwd<int32_t, true, true>(MX_ARGS) : dispatch_fwd<int32_t, true, false>(MX_ARGS);
+    else h ? dispatch_fwd<int32_t, false, true>(MX_ARGS) : dispatch_fwd<int32_t, false, false>(MX_ARGS);
+  }
+#undef MX_ARGS
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}

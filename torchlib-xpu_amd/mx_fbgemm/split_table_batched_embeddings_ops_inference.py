@@ -1,0 +1,192 @@
+"""Inference TBE module: the caller that builds the arguments of
+``torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function``.
+
+Mirrors fbgemm_gpu's IntNBitTableBatchedEmbeddingBagsCodegen (upstream
+fbgemm_gpu/split_table_batched_embeddings_ops_inference.py, recalled) for
+DEVICE placement: all tables live in one uint8 HBM buffer, each row padded
+to ``row_alignment`` bytes; INT8/INT4/INT2 rows start with an fp16 scale and
+an fp16 bias.  Also carries the rowwise quantizer that produces that layout
+from fp32 rows.
+"""
+
+from __future__ import annotations
+
+import itertools
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import load_mx_fbgemm_library
+from .sparse_types import (
+    EmbeddingLocation,
+    PoolingMode,
+    SparseType,
+    padded_row_size_in_bytes,
+    unpadded_row_size_in_bytes,
+)
+
+load_mx_fbgemm_library()
+
+
+def quantize_rows(weights: torch.Tensor, weight_ty: SparseType,
+                  row_alignment: int = 16) -> torch.Tensor:
+    """fp32 ``[E, D]`` -> uint8 ``[E, padded_row_bytes]`` in the TBE row layout.
+
+    INT8/INT4/INT2: per row, bias = min, scale = (max - min) / (2^bits - 1),
+    both rounded to fp16; code = round((w - bias) / scale) clamped to the
+    code range (the rowwise min/max scheme of FBGEMM's
+    FloatToFusedNBitRowwiseQuantizedSBHalf, recalled).  FP16/FP32 rows are
+    stored as-is.  Padding bytes are zero."""
+    E, D = weights.shape
+    stride = padded_row_size_in_bytes(D, weight_ty, row_alignment)
+    out = torch.zeros((E, stride), dtype=torch.uint8, device=weights.device)
+    w = weights.float()
+    if weight_ty == SparseType.FP32:
+        out[:, : 4 * D] = w.contiguous().view(torch.uint8).view(E, 4 * D)
+        return out
+    if weight_ty == SparseType.FP16:
+        out[:, : 2 * D] = w.half().contiguous().view(torch.uint8).view(E, 2 * D)
+        return out
+    bits = weight_ty.bit_rate()
+    qmax = (1 << bits) - 1
+    lo = w.min(dim=1).values
+    hi = w.max(dim=1).values
+    scale = ((hi - lo) / qmax).half()
+    bias = lo.half()
+    s32 = scale.float()
+    s32 = torch.where(s32 == 0, torch.ones_like(s32), s32)
+    q = torch.clamp(torch.round((w - bias.float()[:, None]) / s32[:, None]), 0, qmax).to(torch.int32)
+    per_byte = 8 // bits
+    q = q.view(E, D // per_byte, per_byte)
+    packed = torch.zeros((E, D // per_byte), dtype=torch.int32, device=w.device)
+    for k in range(per_byte):
+        packed |= q[:, :, k] << (k * bits)
+    out[:, 0:2] = scale.view(torch.uint8).view(E, 2)
+    out[:, 2:4] = bias.view(torch.uint8).view(E, 2)
+    out[:, 4:4 + D // per_byte] = packed.to(torch.uint8)
+    return out
+
+
+class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
+    """Quantized TBE for inference.
+
+    ``embedding_specs`` holds ``(name, num_embeddings, embedding_dim,
+    weight_ty, location)`` per table; only EmbeddingLocation.DEVICE is
+    supported."""
+
+    def __init__(
+        self,
+        embedding_specs: list[tuple[str, int, int, SparseType, EmbeddingLocation]],
+        pooling_mode: PoolingMode = PoolingMode.SUM,
+        output_dtype: SparseType = SparseType.FP16,
+        row_alignment: int = 16,
+        device: Optional[torch.device] = None,
+    ) -> None:
+        super().__init__()
+        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
+            raise ValueError(f"pooling_mode {pooling_mode} is not supported")
+        if output_dtype not in (SparseType.FP16, SparseType.FP32):
+            raise ValueError("output_dtype must be FP16 or FP32")
+        for _, E, D, ty, loc in embedding_specs:
+            if loc != EmbeddingLocation.DEVICE:
+                raise ValueError("only EmbeddingLocation.DEVICE is supported")
+            if ty not in (SparseType.FP32, SparseType.FP16, SparseType.INT8, SparseType.INT4,
+                          SparseType.INT2):
+                raise ValueError(f"weight type {ty} is not supported")
+            if D <= 0 or D > 1024 or D % 8:
+                raise ValueError(f"embedding_dim {D} must be a positive multiple of 8, <= 1024")
+        device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        self.embedding_specs = embedding_specs
+        self.pooling_mode = pooling_mode
+        self.output_dtype = output_dtype
+        self.row_alignment = row_alignment
+        self.T = len(embedding_specs)
+        dims = [D for _, _, D, _, _ in embedding_specs]
+        rows = [E for _, E, _, _, _ in embedding_specs]
+        tys = [ty for _, _, _, ty, _ in embedding_specs]
+        self.total_D = sum(dims)
+        self.row_bytes = [padded_row_size_in_bytes(D, ty, row_alignment)
+                          for D, ty in zip(dims, tys)]
+        sizes = [E * rb for E, rb in zip(rows, self.row_bytes)]
+        offs = [0] + list(itertools.accumulate(sizes))
+        self.register_buffer("weights_offsets", torch.tensor(offs[:-1], device=device,
+                                                             dtype=torch.int64))
+        self.register_buffer("weights_tys", torch.tensor([t.as_int() for t in tys],
+                                                         device=device, dtype=torch.uint8))
+        self.register_buffer("D_offsets", torch.tensor([0] + list(itertools.accumulate(dims)),
+                                                       device=device, dtype=torch.int32))
+        self.register_buffer("weights_placements",
+                             torch.full((self.T,), int(EmbeddingLocation.DEVICE), device=device,
+                                        dtype=torch.int32))
+        self.register_buffer("weights_dev", torch.zeros(offs[-1], device=device,
+                                                        dtype=torch.uint8))
+        self.register_buffer("weights_uvm", torch.zeros(0, device=device, dtype=torch.uint8),
+                             persistent=False)
+
+        def max_d(*kinds):
+            return max([D for D, ty in zip(dims, tys) if ty in kinds], default=0)
+
+        self.max_int2_D = max_d(SparseType.INT2)
+        self.max_int4_D = max_d(SparseType.INT4)
+        self.max_int8_D = max_d(SparseType.INT8)
+        self.max_float16_D = max_d(SparseType.FP16)
+        self.max_float32_D = max_d(SparseType.FP32)
+        self._rows, self._dims, self._tys = rows, dims, tys
+        for D, ty in zip(dims, tys):
+            unpadded_row_size_in_bytes(D, ty)  # validates the type
+
+    def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
+                per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if (offsets.numel() - 1) % self.T:
+            raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
+        if indices.dtype != offsets.dtype:
+            offsets = offsets.to(indices.dtype)
+        return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
+            self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
+            self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
+            self.max_int8_D, self.max_float16_D, self.max_float32_D, indices, offsets,
+            int(self.pooling_mode), per_sample_weights, self.output_dtype.as_int(), None, None,
+            self.row_alignment)
+
+    @torch.no_grad()
+    def split_embedding_weights(self) -> list[torch.Tensor]:
+        """Per-table uint8 ``[E_t, row_bytes_t]`` views (qparams included)."""
+        out = []
+        for t, (E, rb) in enumerate(zip(self._rows, self.row_bytes)):
+            o = int(self.weights_offsets[t])
+            out.append(self.weights_dev[o:o + E * rb].view(E, rb))
+        return out
+
+    @torch.no_grad()
+    def assign_embedding_weights(self, weights: list[torch.Tensor]) -> None:
+        """Quantize fp32 ``[E_t, D_t]`` tables into the device buffer."""
+        for t, (w, dst) in enumerate(zip(weights, self.split_embedding_weights())):
+            dst.copy_(quantize_rows(w.to(dst.device), self._tys[t], self.row_alignment))
+
+    @torch.no_grad()
+    def fill_random_weights(self, seed: int = 0) -> None:
+        """Random codes, fp16 scale in [1e-3, 1e-2), bias in [-0.1, 0.1)."""
+        g = torch.Generator(device=self.weights_dev.device)
+        g.manual_seed(seed)
+        for t, dst in enumerate(self.split_embedding_weights()):
+            dst.copy_(torch.randint(0, 256, dst.shape, generator=g, device=dst.device,
+                                    dtype=torch.int32).to(torch.uint8))
+            ty = self._tys[t]
+            if ty.is_rowwise_quantized():
+                E = dst.shape[0]
+                sc = (torch.rand(E, generator=g, device=dst.device) * 9e-3 + 1e-3).half()
+                bi = (torch.rand(E, generator=g, device=dst.device) * 0.2 - 0.1).half()
+                dst[:, 0:2] = sc.view(torch.uint8).view(E, 2)
+                dst[:, 2:4] = bi.view(torch.uint8).view(E, 2)
+            elif ty == SparseType.FP16:
+                E, rb = dst.shape
+                D = self._dims[t]
+                v = (torch.rand((E, D), generator=g, device=dst.device) * 0.02 - 0.01).half()
+                dst[:, : 2 * D] = v.view(torch.uint8).view(E, 2 * D)
+            elif ty == SparseType.FP32:
+                E, rb = dst.shape
+                D = self._dims[t]
+                v = torch.rand((E, D), generator=g, device=dst.device) * 0.02 - 0.01
+                dst[:, : 4 * D] = v.view(torch.uint8).view(E, 4 * D)

@@ -1,0 +1,148 @@
+"""Training TBE module: the caller that builds the arguments of
+``torch.ops.fbgemm.split_embedding_codegen_lookup_rowwise_adagrad_function``.
+
+Mirrors fbgemm_gpu's SplitTableBatchedEmbeddingBagsCodegen (upstream
+fbgemm_gpu/split_table_batched_embeddings_ops_training.py, recalled) for the
+path this build serves: DEVICE placement, fp32 weights, SUM/MEAN pooling and
+the EXACT_ROWWISE_ADAGRAD optimizer fused into the backward.  Weights and the
+per-row momentum live in one flat HBM buffer each; tables are laid out back
+to back (weights_offsets, momentum1_offsets in elements).
+"""
+
+from __future__ import annotations
+
+import itertools
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import load_mx_fbgemm_library
+from .sparse_types import ComputeDevice, EmbeddingLocation, EmbOptimType, PoolingMode, SparseType
+
+load_mx_fbgemm_library()
+
+
+def _cumsum(xs: list[int]) -> list[int]:
+    return [0] + list(itertools.accumulate(xs))
+
+
+class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
+    """T embedding tables looked up and pooled in one launch.
+
+    ``embedding_specs`` holds ``(num_embeddings, embedding_dim, location,
+    compute_device)`` per table; only EmbeddingLocation.DEVICE on a GPU is
+    supported.  ``forward(indices, offsets)`` takes t-major offsets of T*B+1
+    entries and returns ``[B, sum(D)]``; ``loss.backward()`` updates the
+    weights and momentum in place (the gradient itself is never materialised).
+    """
+
+    def __init__(
+        self,
+        embedding_specs: list[tuple[int, int, EmbeddingLocation, ComputeDevice]],
+        optimizer: EmbOptimType = EmbOptimType.EXACT_ROWWISE_ADAGRAD,
+        pooling_mode: PoolingMode = PoolingMode.SUM,
+        learning_rate: float = 0.01,
+        eps: float = 1.0e-8,
+        weight_decay: float = 0.0,
+        weight_decay_mode: int = 0,
+        output_dtype: SparseType = SparseType.FP32,
+        device: Optional[torch.device] = None,
+        weights_init: Optional[tuple[float, float]] = None,
+    ) -> None:
+        super().__init__()
+        if optimizer != EmbOptimType.EXACT_ROWWISE_ADAGRAD:
+            raise ValueError(f"optimizer {optimizer} is not supported")
+        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
+            raise ValueError(f"pooling_mode {pooling_mode} is not supported")
+        if output_dtype != SparseType.FP32:
+            raise ValueError("the training lookup produces fp32 output")
+        if not embedding_specs:
+            raise ValueError("at least one table is required")
+        for E, D, loc, cd in embedding_specs:
+            if loc != EmbeddingLocation.DEVICE or cd != ComputeDevice.CUDA:
+                raise ValueError("only EmbeddingLocation.DEVICE on the GPU is supported")
+            if D <= 0 or D % 4 != 0 or D > 1024:
+                raise ValueError(f"embedding_dim {D} must be a positive multiple of 4, <= 1024")
+            if E <= 0:
+                raise ValueError("num_embeddings must be positive")
+        device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        self.embedding_specs = embedding_specs
+        self.pooling_mode = pooling_mode
+        self.learning_rate = float(learning_rate)
+        self.eps = float(eps)
+        self.weight_decay = float(weight_decay)
+        self.weight_decay_mode = int(weight_decay_mode)
+        rows = [E for E, _, _, _ in embedding_specs]
+        dims = [D for _, D, _, _ in embedding_specs]
+        self.T = len(embedding_specs)
+        self.total_D = sum(dims)
+        self.max_D = max(dims)
+        hash_size_cumsum = _cumsum(rows)
+        self.total_hash_size_bits = max(1, int(hash_size_cumsum[-1] - 1).bit_length())
+        if self.total_hash_size_bits > 32:
+            raise ValueError("total hash size above 2^32 rows is not supported")
+        w_elems = [E * D for E, D in zip(rows, dims)]
+        i64 = dict(device=device, dtype=torch.int64)
+        self.register_buffer("weights_offsets", torch.tensor(_cumsum(w_elems)[:-1], **i64))
+        self.register_buffer("D_offsets", torch.tensor(_cumsum(dims), device=device,
+                                                       dtype=torch.int32))
+        self.register_buffer("hash_size_cumsum", torch.tensor(hash_size_cumsum, **i64))
+        self.register_buffer("weights_placements",
+                             torch.full((self.T,), int(EmbeddingLocation.DEVICE), device=device,
+                                        dtype=torch.int32))
+        self.register_buffer("momentum1_offsets", torch.tensor(_cumsum(rows)[:-1], **i64))
+        lo, hi = weights_init if weights_init is not None else (-0.01, 0.01)
+        self.weights_dev = nn.Parameter(
+            torch.empty(sum(w_elems), device=device, dtype=torch.float32).uniform_(lo, hi),
+            requires_grad=False)
+        self.register_buffer("momentum1_dev",
+                             torch.zeros(sum(rows), device=device, dtype=torch.float32))
+        empty_f = torch.zeros(0, device=device, dtype=torch.float32)
+        self.register_buffer("weights_uvm", empty_f.clone(), persistent=False)
+        self.register_buffer("lxu_cache_weights", empty_f.clone(), persistent=False)
+        self.register_buffer("momentum1_uvm", empty_f.clone(), persistent=False)
+        self.register_buffer("lxu_cache_locations",
+                             torch.zeros(0, device=device, dtype=torch.int32), persistent=False)
+        # A zero-element leaf that makes autograd record the lookup even
+        # though the weights are updated by the fused backward, not by autograd.
+        self.placeholder_autograd_tensor = nn.Parameter(
+            torch.zeros(0, device=device, dtype=torch.float32))
+        self._rows = rows
+        self._dims = dims
+
+    def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
+                per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if per_sample_weights is not None:
+            raise ValueError("per_sample_weights are not supported by the training lookup")
+        if offsets.numel() % 1 or (offsets.numel() - 1) % self.T:
+            raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
+        if indices.dtype != offsets.dtype:
+            offsets = offsets.to(indices.dtype)
+        return torch.ops.fbgemm.split_embedding_codegen_lookup_rowwise_adagrad_function(
+            self.placeholder_autograd_tensor, self.weights_dev, self.weights_uvm,
+            self.lxu_cache_weights, self.weights_placements, self.weights_offsets,
+            self.D_offsets, self.total_D, self.max_D, self.hash_size_cumsum,
+            self.total_hash_size_bits, indices, offsets, int(self.pooling_mode), None, None,
+            self.lxu_cache_locations, False, 0.0, False, self.momentum1_dev, self.momentum1_uvm,
+            self.weights_placements, self.momentum1_offsets, self.eps, self.learning_rate,
+            self.weight_decay, self.weight_decay_mode, 0.0, int(SparseType.FP32.as_int()))
+
+    @torch.no_grad()
+    def split_embedding_weights(self) -> list[torch.Tensor]:
+        """Per-table ``[E_t, D_t]`` views of the flat weight buffer."""
+        out = []
+        for t, (E, D) in enumerate(zip(self._rows, self._dims)):
+            o = int(self.weights_offsets[t])
+            out.append(self.weights_dev.detach()[o:o + E * D].view(E, D))
+        return out
+
+    @torch.no_grad()
+    def split_optimizer_states(self) -> list[list[torch.Tensor]]:
+        """Per-table ``[[momentum1 (E_t,)]]`` views."""
+        out = []
+        for t, E in enumerate(self._rows):
+            o = int(self.momentum1_offsets[t])
+            out.append([self.momentum1_dev[o:o + E]])
+        return out
