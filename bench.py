@@ -43,7 +43,10 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
+                    help="workload; 2 (default) is the headline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU baseline's timed work")
@@ -355,6 +358,15 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4,
+                          "launches": args.steps}))
+        return
     if args.config == 2:
         res, traffic, cpu = bench_tbe_forward(args, dev)
     elif args.config == 3:
