@@ -1,0 +1,109 @@
+"""The C-ABI library loads without a GPU, exports every function
+include/mx_fbgemm.h declares, and its host-side argument checks and size
+queries behave -- no compute call is made here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (binds the HIP runtime torch ships before the library loads)
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "mx_fbgemm.h"
+LIB = REPO / "torchlib-xpu_amd" / "mx_fbgemm" / "lib" / "libmx_fbgemm_kernels.so"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(mx_[a-z_0-9]+)\s*\(",
+                                 text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} not built (run __graft_entry__.build())")
+    return ctypes.CDLL(str(LIB))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for must in ("mx_jagged_to_padded_dense", "mx_dense_to_jagged", "mx_jagged_dense_elementwise_add",
+                 "mx_tbe_forward", "mx_tbe_transpose_embedding_input",
+                 "mx_tbe_backward_rowwise_adagrad", "mx_nbit_forward", "mx_last_error"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_last_error(lib):
+    assert lib.mx_version() >= 100
+    lib.mx_last_error.restype = ctypes.c_char_p
+    assert isinstance(lib.mx_last_error(), bytes)
+
+
+def test_row_bytes(lib):
+    f = lib.mx_nbit_row_bytes
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    assert f(2, 128, 16) == 144   # INT8: 128 + 4 -> 144
+    assert f(3, 128, 16) == 80    # INT4: 64 + 4 -> 80
+    assert f(4, 128, 16) == 48    # INT2: 32 + 4 -> 48
+    assert f(1, 128, 16) == 256   # FP16
+    assert f(0, 100, 16) == 400   # FP32
+    assert f(2, 128, 1) == 132
+    assert f(9, 128, 16) == -1
+
+
+def test_info_bits(lib):
+    f = lib.mx_tbe_info_B_num_bits
+    f.restype = ctypes.c_int32
+    f.argtypes = [ctypes.c_int32, ctypes.c_int64]
+    assert f(8, 4096) == 26
+    assert f(64, 1 << 26) == 26
+    assert f(128, 1000) == 25      # 7 bits for t leave 25 for b
+    assert f(1 << 20, 1 << 20) == -1
+
+
+def test_workspace_sizes_grow(lib):
+    f = lib.mx_tbe_backward_workspace_bytes
+    f.restype = ctypes.c_size_t
+    f.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32]
+    a, b = f(1000, 23, 128), f(100000, 23, 128)
+    assert 0 < a < b
+    g = lib.mx_tbe_transpose_workspace_bytes
+    g.restype = ctypes.c_size_t
+    g.argtypes = [ctypes.c_int64, ctypes.c_int32]
+    assert 0 < g(1000, 23) < a
+
+
+def test_bad_arguments_rejected_before_any_launch(lib):
+    lib.mx_last_error.restype = ctypes.c_char_p
+    P = ctypes.c_void_p
+    f = lib.mx_tbe_forward
+    f.argtypes = [P, P, P, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, P, P, ctypes.c_int32,
+                  ctypes.c_int32, P, P, ctypes.c_int32, ctypes.c_int64, P]
+    # index_bytes 3 is invalid
+    assert f(None, None, None, 1, 1, 128, None, None, 3, 0, None, None, 0, 128, None) == -1
+    assert b"int32 or int64" in lib.mx_last_error()
+    # max_D not a multiple of 4
+    assert f(None, None, None, 1, 1, 130, None, None, 8, 0, None, None, 0, 130, None) == -1
+    # pooling NONE is not served
+    assert f(None, None, None, 1, 1, 128, None, None, 8, 2, None, None, 0, 128, None) == -1
+    # empty problem: success without touching the device
+    assert f(None, None, None, 0, 0, 128, None, None, 8, 0, None, None, 0, 128, None) == 0
+    g = lib.mx_nbit_forward
+    g.argtypes = [P, P, P, P, ctypes.c_int32, ctypes.c_int64] + [ctypes.c_int32] * 5 + \
+        [P, P, ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int64, P]
+    assert g(None, None, None, None, 1, 1, 0, 0, 2048, 0, 0, None, None, 4, 0, None, 1, 16, None,
+             2048, None) == -1  # max D above 1024
+    assert b"1024" in lib.mx_last_error()
+    h = lib.mx_tbe_backward_rowwise_adagrad
+    h.restype = ctypes.c_int
+    assert h(None, None, None, 1, 4, 128, None, 23, None, None, 8, ctypes.c_int64(10), 0, None,
+             ctypes.c_int64(128), None, None, ctypes.c_float(0.1), ctypes.c_float(1e-8),
+             ctypes.c_float(0.0), 7, None, ctypes.c_size_t(0), None) == -1  # weight_decay_mode 7

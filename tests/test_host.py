@@ -1,0 +1,107 @@
+"""Host-side logic without a GPU: enums, row sizes, the TBE modules' argument
+builders (constructed on the CPU device; no op is called) and the rowwise
+quantizer's TBE row layout (checked by decoding it with the oracle)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from mx_fbgemm import ComputeDevice, EmbeddingLocation, PoolingMode, SparseType, bench_inputs
+from mx_fbgemm.sparse_types import padded_row_size_in_bytes, unpadded_row_size_in_bytes
+from mx_fbgemm.split_table_batched_embeddings_ops_inference import (
+    IntNBitTableBatchedEmbeddingBagsCodegen,
+    quantize_rows,
+)
+from mx_fbgemm.split_table_batched_embeddings_ops_training import (
+    SplitTableBatchedEmbeddingBagsCodegen,
+)
+
+
+def test_enums_match_fbgemm_values():
+    assert [s.as_int() for s in (SparseType.FP32, SparseType.FP16, SparseType.INT8, SparseType.INT4,
+                                 SparseType.INT2, SparseType.BF16)] == [0, 1, 2, 3, 4, 5]
+    assert (PoolingMode.SUM, PoolingMode.MEAN, PoolingMode.NONE) == (0, 1, 2)
+    assert EmbeddingLocation.DEVICE == 0 and EmbeddingLocation.HOST == 3
+    assert SparseType.from_int(3) == SparseType.INT4
+
+
+@pytest.mark.parametrize("ty,D,unpadded,padded", [(SparseType.INT8, 128, 132, 144),
+                                                  (SparseType.INT4, 128, 68, 80),
+                                                  (SparseType.INT2, 64, 20, 32),
+                                                  (SparseType.FP16, 36, 72, 80),
+                                                  (SparseType.FP32, 8, 32, 32)])
+def test_row_sizes(ty, D, unpadded, padded):
+    assert unpadded_row_size_in_bytes(D, ty) == unpadded
+    assert padded_row_size_in_bytes(D, ty, 16) == padded
+    assert orc.nbit_row_bytes(ty.as_int(), D, 16) == padded
+
+
+def test_training_module_arguments():
+    specs = [(100, 64, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (7, 128, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (2 ** 20, 4, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)]
+    m = SplitTableBatchedEmbeddingBagsCodegen(specs, device="cpu")
+    assert m.weights_offsets.tolist() == [0, 6400, 6400 + 896]
+    assert m.D_offsets.tolist() == [0, 64, 192, 196]
+    assert m.hash_size_cumsum.tolist() == [0, 100, 107, 107 + 2 ** 20]
+    assert m.total_hash_size_bits == 21
+    assert m.momentum1_offsets.tolist() == [0, 100, 107]
+    assert m.weights_dev.numel() == 6400 + 896 + 4 * 2 ** 20
+    assert m.total_D == 196 and m.max_D == 128
+    w = m.split_embedding_weights()
+    assert [tuple(x.shape) for x in w] == [(100, 64), (7, 128), (2 ** 20, 4)]
+    assert float(m.weights_dev.abs().max()) <= 0.01
+
+
+def test_training_module_rejects_unsupported():
+    with pytest.raises(ValueError):
+        SplitTableBatchedEmbeddingBagsCodegen(
+            [(10, 6, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)], device="cpu")  # D % 4
+    with pytest.raises(ValueError):
+        SplitTableBatchedEmbeddingBagsCodegen(
+            [(10, 8, EmbeddingLocation.MANAGED, ComputeDevice.CUDA)], device="cpu")
+    with pytest.raises(ValueError):
+        SplitTableBatchedEmbeddingBagsCodegen(
+            [(10, 8, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)], pooling_mode=PoolingMode.NONE,
+            device="cpu")
+
+
+def test_inference_module_arguments():
+    specs = [("a", 10, 128, SparseType.INT8, EmbeddingLocation.DEVICE),
+             ("b", 20, 64, SparseType.INT4, EmbeddingLocation.DEVICE),
+             ("c", 5, 32, SparseType.FP16, EmbeddingLocation.DEVICE)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, device="cpu")
+    assert m.row_bytes == [144, 48, 64]
+    assert m.weights_offsets.tolist() == [0, 1440, 1440 + 960]
+    assert m.weights_tys.tolist() == [2, 3, 1]
+    assert (m.max_int8_D, m.max_int4_D, m.max_float16_D, m.max_int2_D, m.max_float32_D) == \
+        (128, 64, 32, 0, 0)
+    assert m.weights_dev.numel() == 1440 + 960 + 320
+
+
+@pytest.mark.parametrize("ty", [SparseType.INT8, SparseType.INT4, SparseType.INT2, SparseType.FP16])
+def test_quantize_rows_layout_decodes(ty):
+    torch.manual_seed(0)
+    E, D = 50, 32
+    w = torch.rand(E, D) * 2 - 1
+    q = quantize_rows(w, ty).numpy()
+    # Decode each row alone through the oracle (a bag per row, SUM) and compare.
+    idx = np.arange(E, dtype=np.int64)
+    off = np.arange(E + 1, dtype=np.int64)
+    dec = orc.nbit_forward(q.reshape(-1), np.array([0]), [ty.as_int()], np.array([0, D], np.int32), E,
+                           idx, off, 0, out_f16=False)
+    step = {SparseType.INT8: 2 / 255, SparseType.INT4: 2 / 15, SparseType.INT2: 2 / 3,
+            SparseType.FP16: 1e-3}[ty]
+    assert np.max(np.abs(dec - w.numpy())) <= step * 0.51 + 2e-3
+
+
+def test_bench_inputs_shapes():
+    c2 = bench_inputs.config2(E=1000, B=64)
+    assert c2.offsets.size == 8 * 64 + 1 and c2.indices.min() >= 0 and c2.indices.max() < 1000
+    lengths = np.diff(c2.offsets)
+    assert lengths.min() >= 1 and lengths.max() <= 40
+    c4 = bench_inputs.config4(E=100, B=16)
+    assert c4.tys == [2] * 16 + [3] * 16 and np.all(np.diff(c4.offsets) == 20)
+    c5 = bench_inputs.config5(T=8, B=200, e_hi=1e5)
+    assert c5.D == [32, 64, 128, 256] * 2 and (np.diff(c5.offsets) == 0).mean() > 0.05

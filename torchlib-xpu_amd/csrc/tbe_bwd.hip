@@ -170,6 +170,15 @@ __global__ void copy_keys_kernel(const uint32_t* __restrict__ keys,
   vals_out[i] = vals[i];
 }
 
+// Clears up to two int32 scalars (a kernel, not a memset, so the call can be
+// captured in a graph).
+__global__ void zero_two_kernel(int32_t* a, int32_t* b) {
+  if (threadIdx.x == 0) {
+    if (a) *a = 0;
+    if (b) *b = 0;
+  }
+}
+
 // ---- run-length encoding --------------------------------------------------
 
 struct HeadFlag {
@@ -640,10 +649,11 @@ extern "C" int mx_tbe_transpose_embedding_input(
   clear_error();
   if (int rc = check_common(T, B, total_hash_size_bits, info_B_num_bits, index_bytes, N)) return rc;
   auto* s = as_stream(stream);
-  if (N == 0) {
-    if (num_runs) MX_HIP_CHECK(hipMemsetAsync(num_runs, 0, sizeof(int32_t), s));
-    if (cumulative_run_lengths)
-      MX_HIP_CHECK(hipMemsetAsync(cumulative_run_lengths, 0, sizeof(int32_t), s));
+  if (N == 0) {  // no runs: num_runs = 0, cumulative_run_lengths = {0}
+    if (num_runs || cumulative_run_lengths) {
+      zero_two_kernel<<<1, 64, 0, s>>>(num_runs, cumulative_run_lengths);
+      MX_LAUNCH_CHECK();
+    }
     return MX_OK;
   }
   MX_REQUIRE(hash_size_cumsum && indices && offsets && sorted_linear_indices && infos_sorted &&

@@ -15,7 +15,6 @@ import fails loudly when the native libraries are missing.
 from __future__ import annotations
 
 import ctypes
-import os
 import traceback
 from pathlib import Path
 
@@ -73,8 +72,6 @@ def load_mx_fbgemm_library() -> None:
         )
     exceptions = []
     try:
-        if os.environ.get("MX_FBGEMM_FORCE_LOAD_FAILURE"):
-            raise OSError("load failure forced by MX_FBGEMM_FORCE_LOAD_FAILURE")
         # Kernel library first (global so the extension's DT_NEEDED resolves to
         # this exact file), then the extension that registers the ops.
         ctypes.CDLL(str(KERNEL_LIBRARY), mode=ctypes.RTLD_GLOBAL)
