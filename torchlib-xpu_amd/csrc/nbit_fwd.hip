@@ -20,6 +20,12 @@
 // launch; the type/width switch is wave-uniform.
 #include "mx_common.h"
 
+// Bytes of row data each lane keeps in flight (sets the rows loaded before
+// any is accumulated).
+#ifndef MX_NBIT_INFLIGHT_BYTES
+#define MX_NBIT_INFLIGHT_BYTES 96
+#endif
+
 namespace mx {
 namespace {
 
@@ -153,7 +159,7 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   constexpr bool Q = TyInfo<TY>::kQ;
   constexpr int BPL = CPL * BITS / 8;
   constexpr int NW = BPL >= 4 ? BPL / 4 : 1;
-  constexpr int U0 = 96 / (BPL + (Q ? 4 : 0));
+  constexpr int U0 = MX_NBIT_INFLIGHT_BYTES / (BPL + (Q ? 4 : 0));
   constexpr int U = U0 < 1 ? 1 : (U0 > 8 ? 8 : U0);
   const int64_t lane_off = (Q ? 4 : 0) + static_cast<int64_t>(k) * BPL;
 
@@ -291,7 +297,7 @@ __device__ void bag_generic(const NbitArgs& a, int32_t ty, int32_t D,
   }
 }
 
-template <typename I, int G, int TY>
+template <typename I, int G, int MAXCPL, int TY>
 __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
                                              const uint8_t* __restrict__ Wt, int64_t stride,
                                              int64_t start, int64_t end, int64_t out_col, int g,
@@ -302,7 +308,7 @@ __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
     switch (cpl) {
 #define MX_CPL(C)                                                                  \
   case C:                                                                          \
-    if constexpr ((C * BITS) % 8 == 0 && C * BITS <= 512) {                        \
+    if constexpr ((C * BITS) % 8 == 0 && C * BITS <= 512 && C <= MAXCPL) {         \
       bag_fast<I, G, TY, C>(a, Wt, stride, start, end, out_col, g, k);             \
       return;                                                                      \
     }                                                                              \
@@ -319,10 +325,18 @@ __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
   bag_generic<I, G>(a, TY, D, Wt, stride, start, end, out_col, k);
 }
 
-template <typename I, int G>
+// MAXCPL bounds the columns per lane compiled into this instance: the kernel's
+// register budget is set by its widest path, so a launch whose tables are all
+// narrow (max D <= 16*G) runs an instance without the 32-column paths.
+// One launch per table type present: the instance holds only that type's
+// paths (fewer registers, higher occupancy); waves whose table has another
+// type return at once.
+template <typename I, int G, int MAXCPL, int TY>
 __global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
   constexpr int P = 64 / G;  // bags per wave
-  const int64_t wave = xcd_remap(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);
+  // Hardware block order (round-robin over the XCDs): tables of different
+  // types interleave on every XCD, so no XCD is left with only the slow ones.
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (wave >= a.nwaves) return;
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
@@ -332,6 +346,7 @@ __global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
   if (t >= a.T) return;
   const int64_t b = slot0 - t * a.Bp + g;
   const int32_t ty = a.tys[t];
+  if (ty != TY) return;
   const int32_t D0 = a.D_off[t];
   const int32_t D = a.D_off[t + 1] - D0;
   const int64_t stride = row_bytes_of(ty, D, a.row_align);
@@ -344,17 +359,10 @@ __global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
   }
   const int64_t out_col = (b < a.B ? b : 0) * a.total_D + D0;
   if (b >= a.B) return;  // whole group idle; group lanes stay converged
-  switch (ty) {
-    case MX_SPARSE_FP32: dispatch_cpl<I, G, MX_SPARSE_FP32>(a, D, Wt, stride, start, end, out_col, g, k); break;
-    case MX_SPARSE_FP16: dispatch_cpl<I, G, MX_SPARSE_FP16>(a, D, Wt, stride, start, end, out_col, g, k); break;
-    case MX_SPARSE_INT8: dispatch_cpl<I, G, MX_SPARSE_INT8>(a, D, Wt, stride, start, end, out_col, g, k); break;
-    case MX_SPARSE_INT4: dispatch_cpl<I, G, MX_SPARSE_INT4>(a, D, Wt, stride, start, end, out_col, g, k); break;
-    case MX_SPARSE_INT2: dispatch_cpl<I, G, MX_SPARSE_INT2>(a, D, Wt, stride, start, end, out_col, g, k); break;
-    default: break;  // unknown types are rejected on the host
-  }
+  dispatch_cpl<I, G, MAXCPL, TY>(a, D, Wt, stride, start, end, out_col, g, k);
 }
 
-template <int G>
+template <int G, int MAXCPL, int TY>
 int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
   constexpr int P = 64 / G;
   a.Bp = ceil_div(a.B, P) * P;
@@ -362,11 +370,21 @@ int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
   const int64_t grid = ceil_div(a.nwaves, 4);
   MX_REQUIRE(grid <= 0x7fffffffll, "too many bags");
   if (index_bytes == 8)
-    nbit_fwd_kernel<int64_t, G><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
+    nbit_fwd_kernel<int64_t, G, MAXCPL, TY><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
   else
-    nbit_fwd_kernel<int32_t, G><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
+    nbit_fwd_kernel<int32_t, G, MAXCPL, TY><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   return MX_OK;
+}
+
+// Lanes per bag and widest compiled path from the type's largest D.
+template <int TY>
+int launch_type(const NbitArgs& a, int32_t max_D, int32_t index_bytes, hipStream_t s) {
+  if (max_D <= 0) return MX_OK;
+  if (max_D <= 128) return launch_nbit<8, 16, TY>(a, index_bytes, s);
+  if (max_D <= 256) return launch_nbit<8, 32, TY>(a, index_bytes, s);
+  if (max_D <= 512) return launch_nbit<16, 32, TY>(a, index_bytes, s);
+  return launch_nbit<32, 32, TY>(a, index_bytes, s);
 }
 
 }  // namespace
@@ -422,7 +440,11 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   a.row_align = row_alignment;
   a.out_f16 = output_dtype == MX_SPARSE_FP16;
   auto* s = as_stream(stream);
-  if (max_D <= 256) return launch_nbit<8>(a, index_bytes, s);
-  if (max_D <= 512) return launch_nbit<16>(a, index_bytes, s);
-  return launch_nbit<32>(a, index_bytes, s);
+  // Tables of a type whose max_*_D is 0 are not served (the upstream contract:
+  // the maxima describe the tables).
+  if (int rc = launch_type<MX_SPARSE_INT8>(a, max_int8_D, index_bytes, s)) return rc;
+  if (int rc = launch_type<MX_SPARSE_INT4>(a, max_int4_D, index_bytes, s)) return rc;
+  if (int rc = launch_type<MX_SPARSE_INT2>(a, max_int2_D, index_bytes, s)) return rc;
+  if (int rc = launch_type<MX_SPARSE_FP16>(a, max_float16_D, index_bytes, s)) return rc;
+  return launch_type<MX_SPARSE_FP32>(a, max_float32_D, index_bytes, s);
 }
