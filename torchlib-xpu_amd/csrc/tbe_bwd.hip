@@ -59,8 +59,8 @@ constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kSortItems = 16;
 constexpr int64_t kSortTile = 64 * kSortItems;  // keys per wave-tile
-constexpr int kLong = 64;                       // runs longer than this are chunked
-constexpr int kChunk = 64;                      // occurrences per chunk
+constexpr int kLong = 32;                       // runs longer than this are chunked
+constexpr int kChunk = 32;                      // occurrences per chunk
 
 // ---- linearize ------------------------------------------------------------
 
@@ -212,6 +212,20 @@ __global__ void __launch_bounds__(256)
   lengths[r] = cum[r + 1] - cum[r];
 }
 
+// chunk_run[q] = the run that owns chunk q (runs longer than kLong only).
+__global__ void __launch_bounds__(256)
+    chunk_map_kernel(const int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
+                     const uint32_t* __restrict__ chunk_start, uint32_t* __restrict__ chunk_run,
+                     int64_t n) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n || r >= static_cast<int64_t>(*num_runs)) return;
+  const int32_t len = cum[r + 1] - cum[r];
+  if (len <= kLong) return;
+  const uint32_t q0 = chunk_start[r];
+  const int32_t nq = (len + kChunk - 1) / kChunk;
+  for (int32_t i = 0; i < nq; ++i) chunk_run[q0 + i] = static_cast<uint32_t>(r);
+}
+
 struct ChunkCount {
   const int32_t* cum;
   __device__ uint32_t operator()(int64_t r) const {
@@ -326,6 +340,8 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
 
 // ---- segment reduce + rowwise Adagrad -------------------------------------
 
+constexpr int kMaxCachedTables = 512;  // table metadata kept in LDS up to this T
+
 struct BwdArgs {
   float* W;
   const int64_t* w_off;
@@ -340,10 +356,12 @@ struct BwdArgs {
   const int32_t* infos;
   const uint32_t* num_runs;
   const uint32_t* chunk_start;
+  const uint32_t* chunk_run;
   const uint32_t* total_chunks;
   float* partial;
   int64_t B;
   int64_t total_D;
+  int32_t T;
   int32_t max_D;
   int32_t nb;
   int32_t pooling;
@@ -353,41 +371,71 @@ struct BwdArgs {
   float wd;
 };
 
-template <int VEC>
-__device__ __forceinline__ void ldv(const float* p, float (&v)[VEC]) {
-  if constexpr (VEC == 4) {
-    const float4 x = *reinterpret_cast<const float4*>(p);
-    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-  } else if constexpr (VEC == 2) {
-    const float2 x = *reinterpret_cast<const float2*>(p);
-    v[0] = x.x; v[1] = x.y;
-  } else {
-    v[0] = *p;
+// Per-table metadata, staged in LDS when T is small enough.
+struct TableMeta {
+  int64_t hsc[kMaxCachedTables];
+  int64_t w_off[kMaxCachedTables];
+  int64_t m1_off[kMaxCachedTables];
+  int32_t D_off[kMaxCachedTables + 1];
+};
+
+__device__ __forceinline__ void stage_meta(const BwdArgs& a, TableMeta& m) {
+  if (a.T <= kMaxCachedTables) {
+    for (int i = threadIdx.x; i <= a.T; i += blockDim.x) {
+      m.D_off[i] = a.D_off[i];
+      if (i < a.T) {
+        m.hsc[i] = a.hsc[i];
+        m.w_off[i] = a.w_off[i];
+        m.m1_off[i] = a.m1_off[i];
+      }
+    }
   }
+  __syncthreads();
 }
 
-template <int VEC>
-__device__ __forceinline__ void stv(float* p, const float (&v)[VEC]) {
-  if constexpr (VEC == 4)
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-  else if constexpr (VEC == 2)
-    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
-  else
-    *p = v[0];
+struct MetaView {
+  const BwdArgs& a;
+  const TableMeta& m;
+  bool cached;
+  __device__ int64_t hsc(int64_t t) const { return cached ? m.hsc[t] : a.hsc[t]; }
+  __device__ int64_t w_off(int64_t t) const { return cached ? m.w_off[t] : a.w_off[t]; }
+  __device__ int64_t m1_off(int64_t t) const { return cached ? m.m1_off[t] : a.m1_off[t]; }
+  __device__ int32_t D_off(int64_t t) const { return cached ? m.D_off[t] : a.D_off[t]; }
+};
+
+__device__ __forceinline__ void ld4(const float* p, float (&v)[4]) {
+  const float4 x = *reinterpret_cast<const float4*>(p);
+  v[0] = x.x;
+  v[1] = x.y;
+  v[2] = x.z;
+  v[3] = x.w;
 }
 
-// Sum of the (MEAN-scaled) gradient rows of occurrences [s0, s1) into g, in
-// order.  All occurrences belong to table t.
-template <typename I, int VEC, int NCH, int U>
-__device__ void sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int64_t s0, int64_t s1,
-                                const bool (&active)[NCH], int lane, float (&g)[NCH][VEC]) {
-  const uint32_t bmask = (a.nb >= 32) ? 0xffffffffu : ((1u << a.nb) - 1u);
-  for (int64_t base = s0; base < s1; base += 64) {
-    const int n = static_cast<int>(s1 - base < 64 ? s1 - base : 64);
+__device__ __forceinline__ void st4(float* p, const float (&v)[4]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ int64_t table_of(const BwdArgs& a, int32_t info) {
+  return a.nb >= 32 ? 0 : static_cast<int64_t>(static_cast<uint32_t>(info) >> a.nb);
+}
+
+// Group-level (G lanes, lane k) sum of the (MEAN-scaled) gradient rows of
+// occurrences [s0, s1) of table t, in order.  Lane k owns columns
+// (c*G + k)*4 .. +4 for c < NCH.  Called with the whole group converged.
+// `info0` is lane k's infos[s0 + k] (valid for k < s1 - s0), already loaded
+// by the caller to find the table.
+template <typename I, int G, int NCH, int U>
+__device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int32_t D,
+                                      int64_t s0, int64_t s1, int g, int k, int32_t info0,
+                                      float (&acc)[NCH][4]) {
+  const uint32_t bmask = a.nb >= 32 ? 0xffffffffu : ((1u << a.nb) - 1u);
+  for (int64_t base = s0; base < s1; base += G) {
+    const int n = static_cast<int>(s1 - base < G ? s1 - base : G);
     int32_t my_b = 0;
     float my_s = 1.0f;
-    if (lane < n) {
-      my_b = static_cast<int32_t>(static_cast<uint32_t>(a.infos[base + lane]) & bmask);
+    if (k < n) {
+      const int32_t info = base == s0 ? info0 : a.infos[base + k];
+      my_b = static_cast<int32_t>(static_cast<uint32_t>(info) & bmask);
       if (a.pooling == MX_POOL_MEAN) {
         const I* off = static_cast<const I*>(a.offsets);
         const int64_t bag = t * a.B + my_b;
@@ -396,31 +444,27 @@ __device__ void sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int64_t
       }
     }
     for (int j = 0; j < n; j += U) {
-      float v[U][NCH][VEC];
+      float v[U][NCH][4];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
-          const int64_t b = readlane_i32(my_b, j + u);
+          const int64_t b = __shfl(my_b, g * G + j + u, 64);
           const float* row = a.grad + b * a.total_D + D0;
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            if (active[c]) ldv<VEC>(row + (c * 64 + lane) * VEC, v[u][c]);
+            if ((c * G + k) * 4 < D) ld4(row + (c * G + k) * 4, v[u][c]);
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
-          const float sc = __shfl(my_s, j + u, 64);
+          const float sc = __shfl(my_s, g * G + j + u, 64);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            if (active[c]) {
+            if ((c * G + k) * 4 < D) {
 #pragma unroll
-              for (int e = 0; e < VEC; ++e) {
-                if (a.pooling == MX_POOL_MEAN)
-                  g[c][e] += __fmul_rn(v[u][c][e], sc);
-                else
-                  g[c][e] += v[u][c][e];
-              }
+              for (int e = 0; e < 4; ++e)
+                acc[c][e] += a.pooling == MX_POOL_MEAN ? __fmul_rn(v[u][c][e], sc) : v[u][c][e];
             }
         }
       }
@@ -428,146 +472,220 @@ __device__ void sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int64_t
   }
 }
 
-// Pass A: partial sums of the chunks of long runs.
-template <typename I, int VEC, int NCH, int U>
+// Rowwise Adagrad on one row held by a G-lane group (lane k owns columns
+// (c*G + k)*4 .. +4): h += mean(g^2), m = lr / (sqrt(h) + eps),
+// w = fma(-m, g, c*w); lane 0 of the group writes h.
+template <int G, int NCH>
+__device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int k,
+                                               const float (&gs)[NCH][4], const float (&w)[NCH][4],
+                                               float* wrow, float* hp, float h0) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if ((c * G + k) * 4 >= D) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ge = a.wd_mode == 1 ? __builtin_fmaf(a.wd, w[c][e], gs[c][e]) : gs[c][e];
+      ss = __builtin_fmaf(ge, ge, ss);
+    }
+  }
+#pragma unroll
+  for (int m = G / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);  // group tree, fixed order
+  const float h = h0 + ss / static_cast<float>(D);
+  const float mult = a.lr / (sqrtf(h) + a.eps);
+  float corr = 1.0f;
+  if (a.wd_mode == 1)
+    corr = 1.0f - mult * a.wd;
+  else if (a.wd_mode == 2)
+    corr = 1.0f - a.lr * a.wd;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if ((c * G + k) * 4 >= D) continue;
+    float nw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) nw[e] = __builtin_fmaf(-mult, gs[c][e], __fmul_rn(corr, w[c][e]));
+    st4(wrow + (c * G + k) * 4, nw);
+  }
+  if (k == 0) *hp = h;
+}
+
+// Pass B (long runs): one 256-thread block per run longer than kLong.  The
+// 256/G groups sum the run's chunk partials round-robin (group j takes
+// chunks j, j + 256/G, ...), the group vectors are combined in group order
+// through LDS, and group 0 applies the update.
+template <int G, int NCH, int U>
+__global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
+  __shared__ TableMeta meta;
+  constexpr int NG = 256 / G;
+  __shared__ float part[NG][G * NCH * 4];
+  stage_meta(a, meta);
+  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
+  const int grp = threadIdx.x / G, k = threadIdx.x % G;
+  const int64_t total = *a.total_chunks;
+  for (int64_t q = blockIdx.x; q < total; q += gridDim.x) {
+    const uint32_t r = a.chunk_run[q];
+    if (q > 0 && a.chunk_run[q - 1] == r) continue;  // not the run's first chunk (block-uniform)
+    const int64_t s0 = a.cum[r];
+    const int64_t s1 = a.cum[r + 1];
+    const int64_t t = table_of(a, a.infos[s0]);
+    const int32_t D0 = mv.D_off(t);
+    const int32_t D = mv.D_off(t + 1) - D0;
+    (void)D0;
+    const int64_t q1 = q + (s1 - s0 + kChunk - 1) / kChunk;
+    float gs[NCH][4];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
+    for (int64_t qq = q + grp; qq < q1; qq += NG * U) {
+      float v[U][NCH][4];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (qq + u * NG < q1)
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if ((c * G + k) * 4 < D) ld4(a.partial + (qq + u * NG) * a.max_D + (c * G + k) * 4, v[u][c]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (qq + u * NG < q1)
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if ((c * G + k) * 4 < D)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) gs[c][e] += v[u][c][e];
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part[grp][(c * G + k) * 4 + e] = gs[c][e];
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = part[0][(c * G + k) * 4 + e];
+          for (int j = 1; j < NG; ++j) x += part[j][(c * G + k) * 4 + e];
+          gs[c][e] = x;
+        }
+      const int64_t idx = a.run[r] - mv.hsc(t);
+      float* wrow = a.W + mv.w_off(t) + idx * D;
+      float* hp = a.m1 + mv.m1_off(t) + idx;
+      float w[NCH][4];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
+      adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, *hp);
+    }
+    __syncthreads();
+  }
+}
+
+// Pass A: one group per chunk of a long run -> partial sum in the workspace.
+template <typename I, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
+  __shared__ TableMeta meta;
+  stage_meta(a, meta);
+  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
+  constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
   const int64_t total = *a.total_chunks;
-  const int64_t nruns = *a.num_runs;
-  for (int64_t q = wave; q < total; q += nwaves) {
-    // Run r with chunk_start[r] <= q < chunk_start[r+1].
-    int64_t lo = 0, hi = nruns;
-    while (hi - lo > 1) {
-      const int64_t mid = lo + ((hi - lo) >> 1);
-      if (static_cast<int64_t>(a.chunk_start[mid]) <= q)
-        lo = mid;
-      else
-        hi = mid;
-    }
-    const int64_t r = lo;
-    const int64_t k = q - a.chunk_start[r];
-    const int64_t s0 = a.cum[r] + k * kChunk;
-    const int64_t s1e = s0 + kChunk;
-    const int64_t s1 = s1e < a.cum[r + 1] ? s1e : a.cum[r + 1];
-    const int64_t t = a.nb >= 32 ? 0 : (static_cast<uint32_t>(a.infos[s0]) >> a.nb);
-    const int32_t D0 = a.D_off[t];
-    const int32_t D = a.D_off[t + 1] - D0;
-    bool active[NCH];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
-    float g[NCH][VEC];
+  for (int64_t qb = wave * P; qb < total; qb += nwaves * P) {
+    const int64_t q = qb + g;
+    if (q >= total) continue;
+    const int64_t r = a.chunk_run[q];
+    const int64_t s0 = a.cum[r] + (q - a.chunk_start[r]) * kChunk;
+    const int64_t e0 = a.cum[r + 1];
+    const int64_t s1 = s0 + kChunk < e0 ? s0 + kChunk : e0;
+    const int32_t info0 = k < s1 - s0 ? a.infos[s0 + k] : 0;
+    const int64_t t = table_of(a, __shfl(info0, g * G, 64));
+    const int32_t D0 = mv.D_off(t);
+    const int32_t D = mv.D_off(t + 1) - D0;
+    float acc[NCH][4];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) g[c][e] = 0.0f;
-    sum_occurrences<I, VEC, NCH, U>(a, t, D0, s0, s1, active, lane, g);
+      for (int e = 0; e < 4; ++e) acc[c][e] = 0.0f;
+    group_sum_occurrences<I, G, NCH, U>(a, t, D0, D, s0, s1, g, k, info0, acc);
     float* dst = a.partial + q * a.max_D;
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
-      if (active[c]) stv<VEC>(dst + (c * 64 + lane) * VEC, g[c]);
+      if ((c * G + k) * 4 < D) st4(dst + (c * G + k) * 4, acc[c]);
   }
 }
 
-// Pass B: one wave per run -- gradient sum, rowwise Adagrad, in-place update.
-template <typename I, int VEC, int NCH, int U>
+// Pass B (runs of at most kLong occurrences): one G-lane group per run --
+// gradient sum in sorted order, rowwise Adagrad, in-place update.  The
+// table of a run comes from the first batch of infos, which is kept for the
+// gradient sum.
+template <typename I, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
+  __shared__ TableMeta meta;
+  stage_meta(a, meta);
+  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
+  constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * P;
   const int64_t nruns = *a.num_runs;
-  for (int64_t r = wave; r < nruns; r += nwaves) {
-    const int64_t s0 = a.cum[r];
-    const int64_t s1 = a.cum[r + 1];
-    const int64_t t = a.nb >= 32 ? 0 : (static_cast<uint32_t>(a.infos[s0]) >> a.nb);
-    const int32_t D0 = a.D_off[t];
-    const int32_t D = a.D_off[t + 1] - D0;
-    const int64_t idx = a.run[r] - a.hsc[t];
-    bool active[NCH];
+  for (int64_t r = wave * P + g; r < nruns; r += stride) {
+    const int64_t cs0 = a.cum[r];
+    const int64_t cs1 = a.cum[r + 1];
+    const int64_t ckey = a.run[r];
+    if (cs1 - cs0 > kLong) continue;  // long runs: bwd_long_run_kernel
+    const int32_t info0 = k < cs1 - cs0 ? a.infos[cs0 + k] : 0;
+    const int64_t t = table_of(a, __shfl(info0, g * G, 64));
+    const int32_t D0 = mv.D_off(t);
+    const int32_t D = mv.D_off(t + 1) - D0;
+    const int64_t idx = ckey - mv.hsc(t);
+    float* wrow = a.W + mv.w_off(t) + idx * D;
+    float* hp = a.m1 + mv.m1_off(t) + idx;
+    float w[NCH][4];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
-    float g[NCH][VEC];
+    for (int c = 0; c < NCH; ++c)
+      if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
+    const float h0 = *hp;
+    float gs[NCH][4];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) g[c][e] = 0.0f;
-    if (s1 - s0 <= kLong) {
-      sum_occurrences<I, VEC, NCH, U>(a, t, D0, s0, s1, active, lane, g);
-    } else {
-      const int64_t q0 = a.chunk_start[r];
-      const int64_t q1 = q0 + (s1 - s0 + kChunk - 1) / kChunk;
-      for (int64_t q = q0; q < q1; q += U) {
-        float v[U][NCH][VEC];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (q + u < q1)
-#pragma unroll
-            for (int c = 0; c < NCH; ++c)
-              if (active[c]) ldv<VEC>(a.partial + (q + u) * a.max_D + (c * 64 + lane) * VEC, v[u][c]);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (q + u < q1)
-#pragma unroll
-            for (int c = 0; c < NCH; ++c)
-              if (active[c])
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) g[c][e] += v[u][c][e];
-      }
-    }
-    float* wrow = a.W + a.w_off[t] + idx * D;
-    float w[NCH][VEC];
-    float ss = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (!active[c]) continue;
-      ldv<VEC>(wrow + (c * 64 + lane) * VEC, w[c]);
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        float ge = g[c][e];
-        if (a.wd_mode == 1) ge = __builtin_fmaf(a.wd, w[c][e], ge);
-        ss = __builtin_fmaf(ge, ge, ss);
-      }
-    }
-    ss = wave_sum(ss);
-    float* hp = a.m1 + a.m1_off[t] + idx;
-    const float h = *hp + ss / static_cast<float>(D);
-    const float mult = a.lr / (sqrtf(h) + a.eps);
-    float corr = 1.0f;
-    if (a.wd_mode == 1) corr = 1.0f - mult * a.wd;
-    else if (a.wd_mode == 2) corr = 1.0f - a.lr * a.wd;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      if (!active[c]) continue;
-      float nw[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) nw[e] = __builtin_fmaf(-mult, g[c][e], __fmul_rn(corr, w[c][e]));
-      stv<VEC>(wrow + (c * 64 + lane) * VEC, nw);
-    }
-    if (lane == 0) *hp = h;
+      for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
+    group_sum_occurrences<I, G, NCH, U>(a, t, D0, D, cs0, cs1, g, k, info0, gs);
+    adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, h0);
   }
 }
 
-template <typename I, int VEC, int NCH>
+template <typename I, int G, int NCH>
 int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
-  constexpr int U = VEC * NCH <= 2 ? 8 : (VEC * NCH <= 4 ? 4 : 2);
-  const int64_t want = ceil_div(N, 4);
+  constexpr int U = NCH <= 1 ? 4 : 2;   // runs are short: keep registers low
+  constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
+  constexpr int P = 64 / G;
+  const int64_t want = ceil_div(N, 4 * P);
   const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
   const dim3 grid(static_cast<uint32_t>(want < 1 ? 1 : (want > cap ? cap : want)));
-  bwd_chunk_kernel<I, VEC, NCH, U><<<grid, 256, 0, s>>>(a);
+  bwd_chunk_kernel<I, G, NCH, UC><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
-  bwd_update_kernel<I, VEC, NCH, U><<<grid, 256, 0, s>>>(a);
+  const int64_t long_cap = static_cast<int64_t>(num_cus()) * 4;
+  const int64_t long_want = ceil_div(N, kChunk);
+  bwd_long_run_kernel<G, NCH, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
+  MX_LAUNCH_CHECK();
+  bwd_update_kernel<I, G, NCH, U><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
 
+// Lanes per run (G) and float4 chunks per lane (NCH) from the widest table.
 template <typename I>
 int dispatch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
-  if (a.max_D <= 64) return launch_bwd<I, 1, 1>(a, N, s);
-  if (a.max_D <= 128) return launch_bwd<I, 2, 1>(a, N, s);
-  if (a.max_D <= 256) return launch_bwd<I, 4, 1>(a, N, s);
-  if (a.max_D <= 512) return launch_bwd<I, 4, 2>(a, N, s);
-  return launch_bwd<I, 4, 4>(a, N, s);
+  if (a.max_D <= 64) return launch_bwd<I, 16, 1>(a, N, s);
+  if (a.max_D <= 128) return launch_bwd<I, 16, 2>(a, N, s);
+  if (a.max_D <= 256) return launch_bwd<I, 32, 2>(a, N, s);
+  if (a.max_D <= 512) return launch_bwd<I, 64, 2>(a, N, s);
+  return launch_bwd<I, 64, 4>(a, N, s);
 }
 
 struct BwdWs {
@@ -579,11 +697,12 @@ struct BwdWs {
   int32_t* num_runs;
   int32_t* cum;
   uint32_t* chunk_start;
+  uint32_t* chunk_run;
   float* partial;
   size_t bytes;
 };
 
-int64_t max_chunks(int64_t N) { return N / kChunk + N / (kLong + 1) + 2; }
+int64_t max_chunks(int64_t N) { return N / kChunk + N / (kLong + 1) + 2; }  // >= sum of ceil(len/kChunk)
 
 BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   BwdWs w{};
@@ -602,6 +721,7 @@ BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   w.num_runs = reinterpret_cast<int32_t*>(take(4));
   w.cum = reinterpret_cast<int32_t*>(take((n + 1) * 4));
   w.chunk_start = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
+  w.chunk_run = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(max_chunks(n)) * 4));
   w.partial = reinterpret_cast<float*>(take(static_cast<size_t>(max_chunks(n)) * max_D * 4));
   w.bytes = off;
   return w;
@@ -707,6 +827,9 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   if (int rc = exclusive_scan(ChunkCount{w.cum}, N, w.num_runs, w.chunk_start,
                               &w.sort.counters[1], w.sort.tiles, s))
     return rc;
+  chunk_map_kernel<<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), 256, 0, s>>>(
+      w.cum, &w.sort.counters[0], w.chunk_start, w.chunk_run, N);
+  MX_LAUNCH_CHECK();
   BwdArgs a;
   a.W = weights;
   a.w_off = weights_offsets;
@@ -721,6 +844,8 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   a.infos = w.infos;
   a.num_runs = &w.sort.counters[0];
   a.chunk_start = w.chunk_start;
+  a.chunk_run = w.chunk_run;
+  a.T = T;
   a.total_chunks = &w.sort.counters[1];
   a.partial = w.partial;
   a.B = B;
