@@ -1,8 +1,7 @@
-// Device-wide exclusive prefix sum of 32-bit counts produced by a functor,
-// in three launches: per-tile reduce, one-block scan of the tile sums, and
-// per-tile scan + write.  The effective length may live on the device
-// (`n_dev`, e.g. a run count), so no host synchronisation is needed; `n` is
-// the host-side upper bound that sizes the grid.
+// Device-wide exclusive prefix sum of 32-bit counts produced by a functor, in
+// one launch (decoupled look-back).  The effective length may live on the
+// device (`n_dev`, e.g. a run count), so no host synchronisation is needed;
+// `n` is the host-side upper bound that sizes the grid.
 #pragma once
 
 #include "mx_common.h"
@@ -51,42 +50,90 @@ __device__ __forceinline__ int64_t eff_len(int64_t n, const int32_t* n_dev) {
   return m < n ? m : n;
 }
 
-template <class F>
-__global__ void __launch_bounds__(kScanThreads)
-    scan_reduce_kernel(F f, int64_t n, const int32_t* n_dev, uint32_t* tile_sums) {
-  const int64_t m = eff_len(n, n_dev);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
-  uint32_t s = 0;
-#pragma unroll
-  for (int it = 0; it < kScanItems; ++it) {
-    const int64_t i = base + it * kScanThreads + threadIdx.x;
-    if (i < m) s += f(i);
-  }
-  uint32_t total;
-  block_excl_scan(s, &total);
-  if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
-}
+// Single-pass scan with decoupled look-back.  Tiles take a ticket in launch
+// order, publish their aggregate, then walk back over predecessors' status
+// words (aggregate or inclusive prefix, packed with the value in one 64-bit
+// word) until an inclusive prefix is found.  A tile only waits on tiles that
+// took earlier tickets, which are already running and publish their
+// aggregate before they wait themselves, so every wait ends.  The status
+// words and the ticket must be zero before the launch.
+struct ScanState {
+  unsigned long long* status;  // one word per tile
+  unsigned int* ticket;        // [0] next tile, [1] set if a look-back gave up
+};
 
-// One block: exclusive scan of tile_sums[0..ntiles) in place; *total_out = sum.
-__global__ void __launch_bounds__(1024)
-    scan_tiles_kernel(uint32_t* tile_sums, int64_t ntiles, uint32_t* total_out);
+constexpr unsigned long long kScanFlagAgg = 1ull << 62;
+constexpr unsigned long long kScanFlagIncl = 2ull << 62;
+constexpr int kScanSpinLimit = 1 << 22;
 
 template <class F>
 __global__ void __launch_bounds__(kScanThreads)
-    scan_write_kernel(F f, int64_t n, const int32_t* n_dev, const uint32_t* tile_prefix,
-                      uint32_t* out) {
+    scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total_out,
+                        ScanState st, int64_t ntiles) {
+  __shared__ uint32_t s_tile, s_prefix;
+  if (threadIdx.x == 0) s_tile = atomicAdd(st.ticket, 1u);
+  __syncthreads();
+  const int64_t tile = s_tile;
   const int64_t m = eff_len(n, n_dev);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + threadIdx.x * kScanItems;
+  const int64_t base = tile * kScanTile + threadIdx.x * kScanItems;
   uint32_t v[kScanItems];
-  uint32_t s = 0;
+  uint32_t sum = 0;
 #pragma unroll
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
     v[it] = i < m ? f(i) : 0u;
-    s += v[it];
+    sum += v[it];
   }
-  uint32_t total;
-  uint32_t run = block_excl_scan(s, &total) + tile_prefix[blockIdx.x];
+  uint32_t tile_total;
+  const uint32_t excl = block_excl_scan(sum, &tile_total);
+  if (threadIdx.x < 64) {  // wave 0 looks back 64 predecessors at a time
+    const int lane = threadIdx.x;
+    uint32_t prefix = 0;
+    if (tile == 0) {
+      if (lane == 0)
+        __hip_atomic_store(&st.status[0], kScanFlagIncl | tile_total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      if (lane == 0)
+        __hip_atomic_store(&st.status[tile], kScanFlagAgg | tile_total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      int64_t j = tile - 1;  // nearest predecessor not yet folded in
+      int spins = 0;
+      while (true) {
+        const int64_t idx = j - lane;
+        const unsigned long long w =
+            idx >= 0 ? __hip_atomic_load(&st.status[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : kScanFlagIncl;  // before tile 0: an inclusive prefix of 0
+        const unsigned long long flag = w >> 62;
+        if (__ballot(flag == 0) != 0ull) {  // some predecessor has not published yet
+          if (++spins > kScanSpinLimit) {   // never expected; keeps the wait bounded
+            if (lane == 0) st.ticket[1] = 1u;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        const unsigned long long incl = __ballot(flag == 2);
+        // Fold lanes up to (and including) the nearest inclusive prefix.
+        const int stop = incl ? __builtin_ctzll(incl) : 63;
+        uint32_t v = lane <= stop ? static_cast<uint32_t>(w) : 0u;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+        prefix += v;
+        if (incl) break;
+        j -= 64;
+      }
+      if (lane == 0)
+        __hip_atomic_store(&st.status[tile], kScanFlagIncl | (prefix + tile_total),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0) {
+      s_prefix = prefix;
+      if (tile == ntiles - 1 && total_out) *total_out = prefix + tile_total;
+    }
+  }
+  __syncthreads();
+  uint32_t run = s_prefix + excl;
 #pragma unroll
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
@@ -96,16 +143,14 @@ __global__ void __launch_bounds__(kScanThreads)
 }
 
 // out[i] = sum_{j<i} f(j) for i < effective length; *total = sum of all.
-// `tile_buf` needs scan_tiles(n) entries.
+// `st` must have scan_tiles(n) zeroed status words and a zeroed ticket.
 template <class F>
 int exclusive_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
-                   uint32_t* tile_buf, hipStream_t s) {
+                   ScanState st, hipStream_t s) {
   const int64_t nt = scan_tiles(n);
   if (nt > 0x7fffffffll) return set_error(MX_EINVAL, "scan too long");
-  const dim3 grid(static_cast<uint32_t>(nt));
-  scan_reduce_kernel<F><<<grid, kScanThreads, 0, s>>>(f, n, n_dev, tile_buf);
-  scan_tiles_kernel<<<1, 1024, 0, s>>>(tile_buf, nt, total);
-  scan_write_kernel<F><<<grid, kScanThreads, 0, s>>>(f, n, n_dev, tile_buf, out);
+  scan_onepass_kernel<F><<<dim3(static_cast<uint32_t>(nt)), kScanThreads, 0, s>>>(
+      f, n, n_dev, out, total, st, nt);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }

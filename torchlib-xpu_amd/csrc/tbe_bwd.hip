@@ -27,32 +27,6 @@
 
 namespace mx {
 
-__global__ void __launch_bounds__(1024)
-    scan_tiles_kernel(uint32_t* tile_sums, int64_t ntiles, uint32_t* total_out) {
-  __shared__ uint32_t wsum[16];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t per = ceil_div(ntiles, 1024);
-  const int64_t b0 = threadIdx.x * per;
-  uint32_t s = 0;
-  for (int64_t i = b0; i < b0 + per && i < ntiles; ++i) s += tile_sums[i];
-  const uint32_t incl = wave_incl_scan(s);
-  if (lane == 63) wsum[w] = incl;
-  __syncthreads();
-  uint32_t before = 0, all = 0;
-  for (int i = 0; i < 16; ++i) {
-    if (i < w) before += wsum[i];
-    all += wsum[i];
-  }
-  uint32_t run = before + incl - s;
-  for (int64_t i = b0; i < b0 + per && i < ntiles; ++i) {
-    const uint32_t v = tile_sums[i];
-    tile_sums[i] = run;
-    run += v;
-  }
-  if (threadIdx.x == 0 && total_out) *total_out = all;
-}
-
 namespace {
 
 constexpr int kRadixBits = 8;
@@ -61,6 +35,8 @@ constexpr int kSortItems = 16;
 constexpr int64_t kSortTile = 64 * kSortItems;  // keys per wave-tile
 constexpr int kLong = 32;                       // runs longer than this are chunked
 constexpr int kChunk = 32;                      // occurrences per chunk
+// Scans per backward: one per radix pass (at most 4), run heads, chunk layout.
+constexpr int kScanSlots = 6;
 
 // ---- linearize ------------------------------------------------------------
 
@@ -242,7 +218,8 @@ struct SortWs {
   uint32_t* keys[2];
   uint32_t* vals[2];
   uint32_t* hist;
-  uint32_t* tiles;
+  unsigned long long* scan_state;  // kScanSlots slots of (tiles + 1) zeroed words
+  int64_t scan_slot_words;
   uint32_t* run_id;
   uint32_t* counters;  // [0] num_runs, [1] total chunks
   size_t bytes;
@@ -253,7 +230,7 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   const int64_t n = N > 0 ? N : 1;
   const int64_t ntiles = ceil_div(n, kSortTile);
   const int64_t hist_n = kRadix * ntiles;
-  const int64_t scan_buf = scan_tiles(hist_n > n + 1 ? hist_n : n + 1);
+  const int64_t slot_words = scan_tiles(hist_n > n + 1 ? hist_n : n + 1) + 2;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     uint8_t* p = base ? base + off : nullptr;
@@ -265,11 +242,24 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
     w.vals[i] = reinterpret_cast<uint32_t*>(take(n * 4));
   }
   w.hist = reinterpret_cast<uint32_t*>(take(hist_n * 4));
-  w.tiles = reinterpret_cast<uint32_t*>(take(scan_buf * 4));
+  w.scan_state = reinterpret_cast<unsigned long long*>(take(kScanSlots * slot_words * 8));
+  w.scan_slot_words = slot_words;
   w.run_id = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
   w.counters = reinterpret_cast<uint32_t*>(take(64));
   w.bytes = off;
   return w;
+}
+
+// Scan-state slot i: status words, then the ticket pair in the last word.
+ScanState scan_slot(const SortWs& w, int i) {
+  unsigned long long* base = w.scan_state + i * w.scan_slot_words;
+  return ScanState{base, reinterpret_cast<unsigned int*>(base + w.scan_slot_words - 1)};
+}
+
+__global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0ull;
 }
 
 struct TransposeOut {
@@ -287,6 +277,13 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
                   const TransposeOut& o, SortWs& w, hipStream_t s) {
   const int64_t nbags = static_cast<int64_t>(T) * B;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
+  {  // every scan's look-back state starts at zero (a kernel, not a memset)
+    const int64_t words = kScanSlots * w.scan_slot_words;
+    const int64_t blocks = ceil_div(words, 256);
+    zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 1024 ? blocks : 1024)), 256, 0, s>>>(
+        w.scan_state, words);
+    MX_LAUNCH_CHECK();
+  }
   if (index_bytes == 8)
     linearize_kernel<int64_t><<<g256, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
@@ -312,7 +309,7 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
     radix_hist_kernel<<<gsort, 256, 0, s>>>(w.keys[cur], N, shift, nbits, w.hist, ntiles);
     MX_LAUNCH_CHECK();
     if (int rc = exclusive_scan(LoadU32{w.hist}, kRadix * ntiles, nullptr, w.hist, nullptr,
-                                w.tiles, s))
+                                scan_slot(w, p), s))
       return rc;
     const bool last = p == passes - 1;
     if (last) {
@@ -329,7 +326,8 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   }
 
   // Run-length encode the sorted keys.
-  if (int rc = exclusive_scan(HeadFlag{o.sorted}, N, nullptr, w.run_id, &w.counters[0], w.tiles, s))
+  if (int rc = exclusive_scan(HeadFlag{o.sorted}, N, nullptr, w.run_id, &w.counters[0],
+                              scan_slot(w, 4), s))
     return rc;
   rle_write_kernel<<<g256, 256, 0, s>>>(o.sorted, N, w.run_id, &w.counters[0], o.run, o.cum);
   MX_LAUNCH_CHECK();
@@ -825,7 +823,7 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
     return rc;
   // Chunk layout of long runs.
   if (int rc = exclusive_scan(ChunkCount{w.cum}, N, w.num_runs, w.chunk_start,
-                              &w.sort.counters[1], w.sort.tiles, s))
+                              &w.sort.counters[1], scan_slot(w.sort, 5), s))
     return rc;
   chunk_map_kernel<<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), 256, 0, s>>>(
       w.cum, &w.sort.counters[0], w.chunk_start, w.chunk_run, N);
