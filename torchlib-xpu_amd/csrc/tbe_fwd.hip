@@ -6,16 +6,15 @@
 //   out[b, D_off[t] + d] = sum_{l in bag(t,b)} W_t[idx[l], d]   (SUM)
 //   MEAN multiplies the sum by 1/L for L > 0; an empty bag gives 0.
 //
-// Design: one wave64 per bag.  Lane k owns columns [k*VEC, k*VEC+VEC) of
-// each 64*VEC-column chunk, so a wave reads a whole row with one coalesced
-// load (D=128: 64 lanes x 8 B = 512 B) and every column is accumulated in
-// index order -- the sum is bit-identical to a sequential CPU loop.  The
-// bag's indices are fetched 64 at a time with one coalesced load and moved
-// to scalar registers with v_readlane, so row addresses are computed on the
-// scalar unit; U rows are loaded before any is accumulated to keep
-// U * 512 B in flight per wave.  Blocks are remapped so that each XCD works
-// on a contiguous range of bags (t-major), keeping one table's hot rows in
-// one XCD's L2.
+// Design: G lanes per bag (G = 32 for D <= 128: two bags per wave64).  Lane
+// k owns 4*NCH columns, so a group reads a whole row with one coalesced
+// float4 load per lane and every column is accumulated in index order -- the
+// sum is bit-identical to a sequential CPU loop.  A bag's indices are fetched
+// G at a time with one coalesced load and handed out with ds_bpermute; U rows
+// are loaded before any is accumulated (D=128: 8 x 512 B in flight per bag).
+// Blocks are remapped so that each XCD works on a contiguous range of bags
+// (t-major), keeping one table's hot rows in one XCD's L2 (measured: 27.8 us
+// vs 31.0 us without the remap on config 2).
 #include "mx_common.h"
 
 namespace mx {
@@ -55,16 +54,23 @@ __device__ __forceinline__ void load_vec(const float* p, float (&v)[VEC]) {
 
 constexpr int kWavesPerBlock = 4;
 
-template <typename I, int VEC, int NCH, int U, bool WEIGHTED, bool OUT_F16>
+// A wave serves 64/G bags at once, G lanes per bag, lane k owning columns
+// (c*G + k)*4 .. +4 (float4 loads: a D=128 row is one 512 B access of 32
+// lanes).  Several bags per wave keep several independent offsets -> indices
+// -> rows chains in flight; each column is still summed in index order.
+template <typename I, int G, int NCH, int U, bool WEIGHTED, bool OUT_F16>
 __global__ void __launch_bounds__(256)
-    tbe_fwd_kernel(const float* __restrict__ W, const int64_t* __restrict__ w_off,
-                   const int32_t* __restrict__ D_off, int64_t B, const I* __restrict__ indices,
-                   const I* __restrict__ offsets, int32_t pooling, const float* __restrict__ iw,
-                   void* __restrict__ out, int64_t total_D, int64_t nbags) {
+    tbe_fwd_group_kernel(const float* __restrict__ W, const int64_t* __restrict__ w_off,
+                         const int32_t* __restrict__ D_off, int64_t B,
+                         const I* __restrict__ indices, const I* __restrict__ offsets,
+                         int32_t pooling, const float* __restrict__ iw, void* __restrict__ out,
+                         int64_t total_D, int64_t nbags) {
+  constexpr int P = 64 / G;
   const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t bag = lb * kWavesPerBlock + (threadIdx.x >> 6);
-  if (bag >= nbags) return;
   const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
+  const int64_t bag = (lb * kWavesPerBlock + (threadIdx.x >> 6)) * P + g;
+  if (bag >= nbags) return;  // whole group
   const int64_t t = bag / B;
   const int64_t b = bag - t * B;
   const int32_t D0 = D_off[t];
@@ -73,93 +79,84 @@ __global__ void __launch_bounds__(256)
   const int64_t start = static_cast<int64_t>(offsets[bag]);
   const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
 
-  float acc[NCH][VEC];
+  float acc[NCH][4];
 #pragma unroll
   for (int c = 0; c < NCH; ++c)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[c][e] = 0.0f;
-
+    for (int e = 0; e < 4; ++e) acc[c][e] = 0.0f;
   bool active[NCH];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) active[c] = (c * 64 + lane) * VEC < D;
+  for (int c = 0; c < NCH; ++c) active[c] = (c * G + k) * 4 < D;
 
-  for (int64_t base = start; base < end; base += 64) {
-    const int n = static_cast<int>(end - base < 64 ? end - base : 64);
-    const int64_t my_idx = lane < n ? static_cast<int64_t>(indices[base + lane]) : 0;
+  for (int64_t base = start; base < end; base += G) {
+    const int n = static_cast<int>(end - base < G ? end - base : G);
+    const int64_t my_idx = k < n ? static_cast<int64_t>(indices[base + k]) : 0;
     float my_w = 0.0f;
-    if constexpr (WEIGHTED) my_w = lane < n ? iw[base + lane] : 0.0f;
+    if constexpr (WEIGHTED) my_w = k < n ? iw[base + k] : 0.0f;
     for (int j = 0; j < n; j += U) {
-      float v[U][NCH][VEC];
+      float v[U][NCH][4];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
-          const int64_t r = readlane_i64(my_idx, j + u);
+          const int64_t r = __shfl(my_idx, g * G + j + u, 64);
           const float* row = Wt + r * D;
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) {
-            if (active[c]) load_vec<VEC>(row + (c * 64 + lane) * VEC, v[u][c]);
-          }
+          for (int c = 0; c < NCH; ++c)
+            if (active[c]) load_vec<4>(row + (c * G + k) * 4, v[u][c]);
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
           float wgt = 1.0f;
-          if constexpr (WEIGHTED) wgt = __shfl(my_w, j + u, 64);
+          if constexpr (WEIGHTED) wgt = __shfl(my_w, g * G + j + u, 64);
 #pragma unroll
-          for (int c = 0; c < NCH; ++c) {
+          for (int c = 0; c < NCH; ++c)
             if (active[c]) {
 #pragma unroll
-              for (int e = 0; e < VEC; ++e) {
+              for (int e = 0; e < 4; ++e) {
                 if constexpr (WEIGHTED)
                   acc[c][e] = __builtin_fmaf(wgt, v[u][c][e], acc[c][e]);
                 else
                   acc[c][e] += v[u][c][e];
               }
             }
-          }
         }
       }
     }
   }
-
   const int64_t L = end - start;
   if (pooling == MX_POOL_MEAN && L > 0) {
     const float inv = 1.0f / static_cast<float>(L);
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[c][e] *= inv;
+      for (int e = 0; e < 4; ++e) acc[c][e] *= inv;
   }
-
   const int64_t obase = b * total_D + D0;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (!active[c]) continue;
-    const int64_t col = obase + (c * 64 + lane) * VEC;
+    const int64_t col = obase + (c * G + k) * 4;
     if constexpr (OUT_F16) {
       __half* o = reinterpret_cast<__half*>(out) + col;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[e] = __float2half_rn(acc[c][e]);
+      for (int e = 0; e < 4; ++e) o[e] = __float2half_rn(acc[c][e]);
     } else {
-      float* o = reinterpret_cast<float*>(out) + col;
-      if constexpr (VEC == 4)
-        *reinterpret_cast<float4*>(o) = make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
-      else if constexpr (VEC == 2)
-        *reinterpret_cast<float2*>(o) = make_float2(acc[c][0], acc[c][1]);
-      else
-        o[0] = acc[c][0];
+      *reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + col) =
+          make_float4(acc[c][0], acc[c][1], acc[c][2], acc[c][3]);
     }
   }
 }
 
-template <typename I, int VEC, int NCH, bool WEIGHTED, bool OUT_F16>
-void launch_fwd(hipStream_t s, const float* W, const int64_t* w_off, const int32_t* D_off,
-                int64_t B, const void* idx, const void* off, int32_t pooling, const float* iw,
-                void* out, int64_t total_D, int64_t nbags) {
-  constexpr int U = VEC * NCH <= 2 ? 8 : (VEC * NCH <= 4 ? 4 : 2);
-  const int64_t grid = ceil_div(nbags, kWavesPerBlock);
-  tbe_fwd_kernel<I, VEC, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
+template <typename I, int G, int NCH, bool WEIGHTED, bool OUT_F16>
+void launch_fwd_group(hipStream_t s, const float* W, const int64_t* w_off, const int32_t* D_off,
+                      int64_t B, const void* idx, const void* off, int32_t pooling,
+                      const float* iw, void* out, int64_t total_D, int64_t nbags) {
+  constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
+  constexpr int P = 64 / G;
+  const int64_t grid = ceil_div(nbags, kWavesPerBlock * P);
+  tbe_fwd_group_kernel<I, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
       W, w_off, D_off, B, static_cast<const I*>(idx), static_cast<const I*>(off), pooling, iw, out,
       total_D, nbags);
 }
@@ -168,19 +165,19 @@ template <typename I, bool WEIGHTED, bool OUT_F16>
 int dispatch_fwd(hipStream_t s, int32_t max_D, const float* W, const int64_t* w_off,
                  const int32_t* D_off, int64_t B, const void* idx, const void* off,
                  int32_t pooling, const float* iw, void* out, int64_t total_D, int64_t nbags) {
-#define MX_FWD(VEC, NCH) \
-  launch_fwd<I, VEC, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
+#define MX_FWD_G(G, NCH) \
+  launch_fwd_group<I, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
   if (max_D <= 64)
-    MX_FWD(1, 1);
+    MX_FWD_G(16, 1);  // 4 bags per wave
   else if (max_D <= 128)
-    MX_FWD(2, 1);
+    MX_FWD_G(32, 1);  // 2 bags per wave, one D=128 row per 32 lanes x 16 B
   else if (max_D <= 256)
-    MX_FWD(4, 1);
+    MX_FWD_G(64, 1);
   else if (max_D <= 512)
-    MX_FWD(4, 2);
+    MX_FWD_G(64, 2);
   else
-    MX_FWD(4, 4);
-#undef MX_FWD
+    MX_FWD_G(64, 4);
+#undef MX_FWD_G
   return MX_OK;
 }
 
