@@ -56,6 +56,12 @@ extern "C" {
 #define MX_POOL_MEAN 1
 #define MX_POOL_NONE 2
 
+/* fbgemm_gpu BoundsCheckMode values. */
+#define MX_BOUNDS_FATAL 0
+#define MX_BOUNDS_WARNING 1
+#define MX_BOUNDS_IGNORE 2
+#define MX_BOUNDS_NONE 3
+
 /* Maximum number of jagged dimensions the jagged kernels accept. */
 #define MX_MAX_JAGGED_DIM 4
 
@@ -174,6 +180,25 @@ int mx_tbe_backward_rowwise_adagrad(
     int32_t pooling_mode, const float* grad_output, int64_t total_D, float* momentum1,
     const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
     int32_t weight_decay_mode, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- index validation ---------------------------------------------------- */
+
+/* Serves fbgemm::bounds_check_indices (the check callers run before a TBE
+ * lookup).  indices [N] and offsets [T*B+1] share one integer type and are
+ * repaired in place:
+ *   - offsets become o'[i] = max_{j<=i} clamp(o[j], 0, N) (in range and
+ *     non-decreasing, so bags never overlap);
+ *   - every index of bag (t, b), positions [o'[t*B+b], o'[t*B+b+1]),
+ *     outside [0, rows_per_table[t]) becomes 0;
+ *   - each repaired entry adds one to *warning (device int64).
+ * mode FATAL only counts (nothing is repaired; the caller raises on a
+ * non-zero count), WARNING and IGNORE repair and count, NONE does nothing.
+ * Workspace: mx_bounds_check_workspace_bytes(T, B). */
+size_t mx_bounds_check_workspace_bytes(int32_t T, int64_t B);
+int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B, void* indices,
+                            void* offsets, int32_t index_bytes, int64_t N, int32_t mode,
+                            int64_t* warning, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* ---- TBE nbit inference forward ---------------------------------------- */
 

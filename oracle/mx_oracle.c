@@ -361,3 +361,41 @@ done:
   free(g);
   return rc;
 }
+
+/* ---- bounds_check_indices -------------------------------------------------
+ * fbgemm_gpu bounds_check_indices (recalled), modes FATAL 0 / WARNING 1 /
+ * IGNORE 2 / NONE 3, with this build's stated repair contract: offsets
+ * o'[i] = max_{j<=i} clamp(o[j], 0, N); indices of bag (t, b) -- positions
+ * [o'[t*B+b], o'[t*B+b+1]) -- outside [0, rows[t]) set to 0; each repaired
+ * entry counts one; FATAL counts without repairing. */
+int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* indices,
+                         int64_t* offsets, int64_t N, int32_t mode) {
+  if (mode == 3) return 0;
+  int64_t bad = 0;
+  const int64_t nb = (int64_t)T * B;
+  int64_t* rep = (int64_t*)malloc(sizeof(int64_t) * (nb + 1));
+  if (!rep) return -1;
+  int64_t run = 0;
+  for (int64_t i = 0; i <= nb; ++i) {
+    const int64_t c = offsets[i] < 0 ? 0 : (offsets[i] > N ? N : offsets[i]);
+    run = c > run ? c : run;
+    rep[i] = run;
+  }
+  for (int64_t bag = 0; bag < nb; ++bag) {
+    const int64_t t = bag / B;
+    for (int64_t l = rep[bag]; l < rep[bag + 1]; ++l) {
+      if (indices[l] < 0 || indices[l] >= rows[t]) {
+        ++bad;
+        if (mode != 0) indices[l] = 0;
+      }
+    }
+  }
+  for (int64_t i = 0; i <= nb; ++i) {
+    if (rep[i] != offsets[i]) {
+      ++bad;
+      if (mode != 0) offsets[i] = rep[i];
+    }
+  }
+  free(rep);
+  return bad;
+}

@@ -38,4 +38,6 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
                                  int32_t pooling, const float* grad, int64_t total_D, float* m1,
                                  const int64_t* m1_off, float lr, float eps, float wd,
                                  int32_t wd_mode, int32_t nb);
+int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* indices,
+                         int64_t* offsets, int64_t N, int32_t mode);
 #endif

@@ -67,6 +67,8 @@ def lib():
         _lib.orc_backward_rowwise_adagrad.argtypes = [
             P, P, P, i32, i64, P, i32, P, P, i64, i32, P, i64, P, P, f32, f32, f32, i32, i32]
         _lib.orc_backward_rowwise_adagrad.restype = ctypes.c_int
+        _lib.orc_bounds_check.argtypes = [P, i32, i64, P, P, i64, i32]
+        _lib.orc_bounds_check.restype = i64
         _lib.orc_half_to_float.argtypes = [ctypes.c_uint16]
         _lib.orc_half_to_float.restype = f32
         _lib.orc_float_to_half.argtypes = [f32]
@@ -256,6 +258,18 @@ def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, po
         weight_decay, weight_decay_mode, info_B_num_bits)
     assert rc == 0, f"orc_backward_rowwise_adagrad failed ({rc})"
     return W, m1
+
+
+def bounds_check_indices(rows_per_table, indices, offsets, mode):
+    """Returns (indices', offsets', count) -- repaired copies and the number of
+    out-of-range entries."""
+    rows = _c(rows_per_table, np.int64)
+    idx = np.array(indices, dtype=np.int64, copy=True)
+    off = np.array(offsets, dtype=np.int64, copy=True)
+    T = rows.shape[0]
+    B = (off.shape[0] - 1) // T
+    n = lib().orc_bounds_check(_p(rows), T, B, _p(idx), _p(off), idx.shape[0], mode)
+    return idx, off, int(n)
 
 
 def info_B_num_bits(T: int, B: int) -> int:

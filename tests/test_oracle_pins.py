@@ -284,3 +284,59 @@ def test_adagrad_zero_grad_changes_nothing():
                                           1e-8)
     np.testing.assert_array_equal(W2, W)
     np.testing.assert_array_equal(m2, m1)
+
+
+# ---- bounds_check_indices ---------------------------------------------------
+
+def _bounds_brute(rows, idx, off, mode):
+    """Straight restatement with Python ints (independent of the C loops)."""
+    idx, off = [int(x) for x in idx], [int(x) for x in off]
+    T = len(rows)
+    B = (len(off) - 1) // T
+    N = len(idx)
+    if mode == 3:
+        return idx, off, 0
+    rep, run = [], 0
+    for o in off:
+        run = max(run, min(max(o, 0), N))
+        rep.append(run)
+    bad = 0
+    out_idx = list(idx)
+    for bag in range(T * B):
+        for l in range(rep[bag], rep[bag + 1]):
+            if not (0 <= idx[l] < rows[bag // B]):
+                bad += 1
+                if mode != 0:
+                    out_idx[l] = 0
+    bad += sum(1 for a, b in zip(rep, off) if a != b)
+    return (out_idx if mode != 0 else idx), (rep if mode != 0 else off), bad
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+@pytest.mark.parametrize("case", ["clean", "bad_indices", "bad_offsets"])
+def test_bounds_check_vs_python(mode, case):
+    rng = np.random.default_rng(5)
+    T, B = 3, 7
+    rows = np.array([10, 3, 50])
+    lengths = rng.integers(0, 6, T * B)
+    off = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    N = int(off[-1])
+    idx = np.concatenate([rng.integers(0, rows[t], int(off[(t + 1) * B] - off[t * B]))
+                          for t in range(T)]).astype(np.int64)
+    if case == "bad_indices":
+        idx[::5] = rng.integers(-3, 60, idx[::5].size)
+    if case == "bad_offsets":
+        off[4] = -2
+        off[9] = N + 5  # also makes offsets non-monotone
+    got_idx, got_off, n = orc.bounds_check_indices(rows, idx, off, mode)
+    exp_idx, exp_off, bad = _bounds_brute(rows, idx, off, mode)
+    assert n == bad
+    np.testing.assert_array_equal(got_idx, exp_idx)
+    np.testing.assert_array_equal(got_off, exp_off)
+    if case == "clean":
+        assert n == 0
+    if mode in (1, 2):  # repaired arrays are safe to look up
+        assert np.all(np.diff(got_off) >= 0) and got_off[0] >= 0 and got_off[-1] <= N
+        for bag in range(T * B):
+            seg = got_idx[got_off[bag]:got_off[bag + 1]]
+            assert np.all((seg >= 0) & (seg < rows[bag // B]))

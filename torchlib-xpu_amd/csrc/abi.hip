@@ -3,6 +3,7 @@
 #include <string>
 
 #include "mx_common.h"
+#include "scan.h"
 
 namespace mx {
 
@@ -35,6 +36,12 @@ int num_cus() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+__global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0ull;
 }
 
 }  // namespace mx

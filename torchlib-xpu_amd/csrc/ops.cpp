@@ -573,6 +573,66 @@ Tensor lookup_rowwise_adagrad(
 }
 
 // ---------------------------------------------------------------------------
+// bounds_check_indices
+// ---------------------------------------------------------------------------
+
+void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
+                          const Tensor& offsets, int64_t bounds_check_mode, const Tensor& warning,
+                          const std::optional<Tensor>& weights,
+                          const std::optional<Tensor>& B_offsets, c10::SymInt max_B,
+                          const std::optional<Tensor>& b_t_map, int64_t info_B_num_bits,
+                          int64_t info_B_mask, int64_t bounds_check_version) {
+  (void)max_B;
+  (void)info_B_num_bits;
+  (void)info_B_mask;
+  (void)bounds_check_version;
+  check_gpu(indices, "indices");
+  c10::OptionalDeviceGuard guard(indices.device());
+  check_gpu(offsets, "offsets");
+  check_gpu(rows_per_table, "rows_per_table");
+  check_gpu(warning, "warning");
+  TORCH_CHECK(!(B_offsets.has_value() && B_offsets->defined()) &&
+                  !(b_t_map.has_value() && b_t_map->defined()),
+              "variable batch size (VBE) is not supported");
+  TORCH_CHECK(bounds_check_mode >= MX_BOUNDS_FATAL && bounds_check_mode <= MX_BOUNDS_NONE,
+              "bounds_check_mode must be FATAL(0), WARNING(1), IGNORE(2) or NONE(3)");
+  TORCH_CHECK(rows_per_table.scalar_type() == at::kLong, "rows_per_table must be int64");
+  TORCH_CHECK(warning.scalar_type() == at::kLong && warning.numel() >= 1 &&
+                  warning.is_contiguous(),
+              "warning must be a contiguous int64 tensor");
+  TORCH_CHECK(indices.is_contiguous() && offsets.is_contiguous(),
+              "indices and offsets are repaired in place and must be contiguous");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = rows_per_table.numel();
+  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  if (weights.has_value() && weights->defined())
+    TORCH_CHECK(weights->numel() == indices.numel(), "per-sample weights have ",
+                weights->numel(), " entries but there are ", indices.numel(), " indices");
+  if (bounds_check_mode == MX_BOUNDS_NONE) return;
+  const Tensor rows = rows_per_table.contiguous();
+  const size_t ws_bytes = mx_bounds_check_workspace_bytes(static_cast<int32_t>(T), B);
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
+  if (bounds_check_mode == MX_BOUNDS_FATAL) {
+    Tensor count = at::zeros({1}, warning.options());
+    MX_CALL(mx_bounds_check_indices(rows.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
+                                    indices.data_ptr(), offsets.data_ptr(), ib, indices.numel(),
+                                    MX_BOUNDS_FATAL, count.data_ptr<int64_t>(), ws.data_ptr(),
+                                    ws_bytes, stream_of(indices)));
+    const int64_t n = count.item<int64_t>();  // FATAL synchronises to report
+    TORCH_CHECK(n == 0, "bounds_check_indices: ", n,
+                " out-of-range indices/offsets (BoundsCheckMode.FATAL)");
+    return;
+  }
+  MX_CALL(mx_bounds_check_indices(rows.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
+                                  indices.data_ptr(), offsets.data_ptr(), ib, indices.numel(),
+                                  static_cast<int32_t>(bounds_check_mode),
+                                  warning.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
+                                  stream_of(indices)));
+}
+
+// ---------------------------------------------------------------------------
 // nbit inference
 // ---------------------------------------------------------------------------
 
@@ -685,6 +745,10 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
         "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
         "float max_norm=0.0, int output_dtype=0) -> Tensor");
+  m.def("bounds_check_indices(Tensor rows_per_table, Tensor(a!) indices, Tensor(b!) offsets, "
+        "int bounds_check_mode, Tensor(c!) warning, Tensor? weights=None, "
+        "Tensor? B_offsets=None, SymInt max_B=-1, Tensor? b_t_map=None, int info_B_num_bits=-1, "
+        "int info_B_mask=-1, int bounds_check_version=1) -> ()");
   m.def("int_nbit_split_embedding_codegen_lookup_function(Tensor dev_weights, "
         "Tensor uvm_weights, Tensor weights_placements, Tensor weights_offsets, "
         "Tensor weights_tys, Tensor D_offsets, SymInt total_D, int max_int2_D, int max_int4_D, "
@@ -709,6 +773,7 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",
          TORCH_FN(mx_ops::lookup_rowwise_adagrad));
   m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
+  m.impl("bounds_check_indices", TORCH_FN(mx_ops::bounds_check_indices));
 }
 
 TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {

@@ -1,7 +1,8 @@
-// Device-wide exclusive prefix sum of 32-bit counts produced by a functor, in
-// one launch (decoupled look-back).  The effective length may live on the
-// device (`n_dev`, e.g. a run count), so no host synchronisation is needed;
-// `n` is the host-side upper bound that sizes the grid.
+// Device-wide prefix scan of 32-bit values produced by a functor, in one
+// launch (decoupled look-back), for an associative operator (sum or max).
+// The effective length may live on the device (`n_dev`, e.g. a run count),
+// so no host synchronisation is needed; `n` is the host-side upper bound that
+// sizes the grid.
 #pragma once
 
 #include "mx_common.h"
@@ -14,34 +15,48 @@ constexpr int64_t kScanTile = kScanThreads * kScanItems;
 
 inline int64_t scan_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
 
+struct SumOp {
+  static __device__ __forceinline__ uint32_t identity() { return 0u; }
+  static __device__ __forceinline__ uint32_t apply(uint32_t a, uint32_t b) { return a + b; }
+};
+
+struct MaxOp {
+  static __device__ __forceinline__ uint32_t identity() { return 0u; }
+  static __device__ __forceinline__ uint32_t apply(uint32_t a, uint32_t b) { return a > b ? a : b; }
+};
+
 // Inclusive scan over the 64 lanes of a wave.
+template <class Op = SumOp>
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const uint32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
+    if (lane >= d) v = Op::apply(o, v);
   }
   return v;
 }
 
-// Exclusive scan across a 256-thread block; returns the block total in *total.
+// Exclusive scan across a 256-thread block; returns the block aggregate in *total.
+template <class Op = SumOp>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   __shared__ uint32_t wsum[kScanThreads / 64];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  const uint32_t incl = wave_incl_scan(v);
+  const uint32_t incl = wave_incl_scan<Op>(v);
   if (lane == 63) wsum[w] = incl;
   __syncthreads();
-  uint32_t before = 0, all = 0;
+  uint32_t before = Op::identity(), all = Op::identity();
 #pragma unroll
   for (int i = 0; i < kScanThreads / 64; ++i) {
-    if (i < w) before += wsum[i];
-    all += wsum[i];
+    if (i < w) before = Op::apply(before, wsum[i]);
+    all = Op::apply(all, wsum[i]);
   }
   __syncthreads();
   *total = all;
-  return before + incl - v;
+  // Exclusive value of this lane: the inclusive scan of the previous lane.
+  const uint32_t prev = __shfl_up(incl, 1, 64);
+  return lane == 0 ? before : Op::apply(before, prev);
 }
 
 __device__ __forceinline__ int64_t eff_len(int64_t n, const int32_t* n_dev) {
@@ -66,7 +81,8 @@ constexpr unsigned long long kScanFlagAgg = 1ull << 62;
 constexpr unsigned long long kScanFlagIncl = 2ull << 62;
 constexpr int kScanSpinLimit = 1 << 22;
 
-template <class F>
+// INCL = false: out[i] = op(f(0..i-1)) (identity at 0); true: op(f(0..i)).
+template <class F, class Op, bool INCL>
 __global__ void __launch_bounds__(kScanThreads)
     scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total_out,
                         ScanState st, int64_t ntiles) {
@@ -77,18 +93,18 @@ __global__ void __launch_bounds__(kScanThreads)
   const int64_t m = eff_len(n, n_dev);
   const int64_t base = tile * kScanTile + threadIdx.x * kScanItems;
   uint32_t v[kScanItems];
-  uint32_t sum = 0;
+  uint32_t agg = Op::identity();
 #pragma unroll
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
-    v[it] = i < m ? f(i) : 0u;
-    sum += v[it];
+    v[it] = i < m ? f(i) : Op::identity();
+    agg = Op::apply(agg, v[it]);
   }
   uint32_t tile_total;
-  const uint32_t excl = block_excl_scan(sum, &tile_total);
+  const uint32_t excl = block_excl_scan<Op>(agg, &tile_total);
   if (threadIdx.x < 64) {  // wave 0 looks back 64 predecessors at a time
     const int lane = threadIdx.x;
-    uint32_t prefix = 0;
+    uint32_t prefix = Op::identity();
     if (tile == 0) {
       if (lane == 0)
         __hip_atomic_store(&st.status[0], kScanFlagIncl | tile_total, __ATOMIC_RELAXED,
@@ -103,7 +119,7 @@ __global__ void __launch_bounds__(kScanThreads)
         const int64_t idx = j - lane;
         const unsigned long long w =
             idx >= 0 ? __hip_atomic_load(&st.status[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                     : kScanFlagIncl;  // before tile 0: an inclusive prefix of 0
+                     : (kScanFlagIncl | Op::identity());  // before tile 0
         const unsigned long long flag = w >> 62;
         if (__ballot(flag == 0) != 0ull) {  // some predecessor has not published yet
           if (++spins > kScanSpinLimit) {   // never expected; keeps the wait bounded
@@ -116,43 +132,54 @@ __global__ void __launch_bounds__(kScanThreads)
         const unsigned long long incl = __ballot(flag == 2);
         // Fold lanes up to (and including) the nearest inclusive prefix.
         const int stop = incl ? __builtin_ctzll(incl) : 63;
-        uint32_t v = lane <= stop ? static_cast<uint32_t>(w) : 0u;
+        uint32_t x = lane <= stop ? static_cast<uint32_t>(w) : Op::identity();
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-        prefix += v;
+        for (int mm = 32; mm >= 1; mm >>= 1) x = Op::apply(x, __shfl_xor(x, mm, 64));
+        prefix = Op::apply(x, prefix);
         if (incl) break;
         j -= 64;
       }
       if (lane == 0)
-        __hip_atomic_store(&st.status[tile], kScanFlagIncl | (prefix + tile_total),
+        __hip_atomic_store(&st.status[tile], kScanFlagIncl | Op::apply(prefix, tile_total),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (lane == 0) {
       s_prefix = prefix;
-      if (tile == ntiles - 1 && total_out) *total_out = prefix + tile_total;
+      if (tile == ntiles - 1 && total_out) *total_out = Op::apply(prefix, tile_total);
     }
   }
   __syncthreads();
-  uint32_t run = s_prefix + excl;
+  uint32_t run = Op::apply(s_prefix, excl);
 #pragma unroll
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
+    if constexpr (INCL) run = Op::apply(run, v[it]);
     if (i < m) out[i] = run;
-    run += v[it];
+    if constexpr (!INCL) run = Op::apply(run, v[it]);
   }
 }
 
-// out[i] = sum_{j<i} f(j) for i < effective length; *total = sum of all.
+// Prefix scan of f over [0, effective length); *total = the whole aggregate.
 // `st` must have scan_tiles(n) zeroed status words and a zeroed ticket.
-template <class F>
-int exclusive_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
-                   ScanState st, hipStream_t s) {
+template <class F, class Op = SumOp, bool INCL = false>
+int prefix_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
+                ScanState st, hipStream_t s) {
   const int64_t nt = scan_tiles(n);
   if (nt > 0x7fffffffll) return set_error(MX_EINVAL, "scan too long");
-  scan_onepass_kernel<F><<<dim3(static_cast<uint32_t>(nt)), kScanThreads, 0, s>>>(
+  scan_onepass_kernel<F, Op, INCL><<<dim3(static_cast<uint32_t>(nt)), kScanThreads, 0, s>>>(
       f, n, n_dev, out, total, st, nt);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
+
+// out[i] = sum_{j<i} f(j); *total = sum of all.
+template <class F>
+int exclusive_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
+                   ScanState st, hipStream_t s) {
+  return prefix_scan<F, SumOp, false>(f, n, n_dev, out, total, st, s);
+}
+
+// Fills p[0..n) with zeros (a kernel, not a memset, so callers can capture it).
+__global__ void zero_u64_kernel(unsigned long long* p, int64_t n);
 
 }  // namespace mx

@@ -256,12 +256,6 @@ ScanState scan_slot(const SortWs& w, int i) {
   return ScanState{base, reinterpret_cast<unsigned int*>(base + w.scan_slot_words - 1)};
 }
 
-__global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    p[i] = 0ull;
-}
-
 struct TransposeOut {
   int64_t* linear;      // may be null
   int64_t* sorted;      // [N]

@@ -41,6 +41,7 @@ OPS = (
     "split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
     "split_embedding_codegen_lookup_rowwise_adagrad_function",
     "int_nbit_split_embedding_codegen_lookup_function",
+    "bounds_check_indices",
 )
 
 _loaded = False
@@ -103,6 +104,7 @@ def load_mx_fbgemm_library() -> None:
 load_mx_fbgemm_library()
 
 from .sparse_types import (  # noqa: E402
+    BoundsCheckMode,
     ComputeDevice,
     EmbeddingLocation,
     EmbOptimType,
@@ -111,6 +113,7 @@ from .sparse_types import (  # noqa: E402
 )
 
 __all__ = [
+    "BoundsCheckMode",
     "ComputeDevice",
     "EmbeddingLocation",
     "EmbOptimType",

@@ -62,6 +62,13 @@ class EmbeddingLocation(enum.IntEnum):
     HOST = 3
 
 
+class BoundsCheckMode(enum.IntEnum):
+    FATAL = 0
+    WARNING = 1
+    IGNORE = 2
+    NONE = 3
+
+
 class ComputeDevice(enum.IntEnum):
     CPU = 0
     CUDA = 1

@@ -19,6 +19,7 @@ from torch import nn
 
 from . import load_mx_fbgemm_library
 from .sparse_types import (
+    BoundsCheckMode,
     EmbeddingLocation,
     PoolingMode,
     SparseType,
@@ -82,6 +83,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         output_dtype: SparseType = SparseType.FP16,
         row_alignment: int = 16,
         device: Optional[torch.device] = None,
+        bounds_check_mode: BoundsCheckMode = BoundsCheckMode.WARNING,
     ) -> None:
         super().__init__()
         if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
@@ -102,6 +104,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.pooling_mode = pooling_mode
         self.output_dtype = output_dtype
         self.row_alignment = row_alignment
+        self.bounds_check_mode = BoundsCheckMode(bounds_check_mode)
         self.T = len(embedding_specs)
         dims = [D for _, _, D, _, _ in embedding_specs]
         rows = [E for _, E, _, _, _ in embedding_specs]
@@ -133,6 +136,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.max_int8_D = max_d(SparseType.INT8)
         self.max_float16_D = max_d(SparseType.FP16)
         self.max_float32_D = max_d(SparseType.FP32)
+        self.register_buffer("rows_per_table", torch.tensor(rows, device=device,
+                                                            dtype=torch.int64))
+        self.register_buffer("bounds_check_warning", torch.zeros(1, device=device,
+                                                                 dtype=torch.int64))
         self._rows, self._dims, self._tys = rows, dims, tys
         for D, ty in zip(dims, tys):
             unpadded_row_size_in_bytes(D, ty)  # validates the type
@@ -143,6 +150,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
             raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
         if indices.dtype != offsets.dtype:
             offsets = offsets.to(indices.dtype)
+        if self.bounds_check_mode != BoundsCheckMode.NONE:
+            torch.ops.fbgemm.bounds_check_indices(self.rows_per_table, indices, offsets,
+                                                  int(self.bounds_check_mode),
+                                                  self.bounds_check_warning, per_sample_weights)
         return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
             self.weights_dev, self.weights_uvm, self.weights_placements, self.weights_offsets,
             self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,

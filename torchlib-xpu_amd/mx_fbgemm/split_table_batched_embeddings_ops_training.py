@@ -18,7 +18,14 @@ import torch
 from torch import nn
 
 from . import load_mx_fbgemm_library
-from .sparse_types import ComputeDevice, EmbeddingLocation, EmbOptimType, PoolingMode, SparseType
+from .sparse_types import (
+    BoundsCheckMode,
+    ComputeDevice,
+    EmbeddingLocation,
+    EmbOptimType,
+    PoolingMode,
+    SparseType,
+)
 
 load_mx_fbgemm_library()
 
@@ -35,6 +42,9 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     supported.  ``forward(indices, offsets)`` takes t-major offsets of T*B+1
     entries and returns ``[B, sum(D)]``; ``loss.backward()`` updates the
     weights and momentum in place (the gradient itself is never materialised).
+    Indices and offsets are first validated, and repaired in place, by
+    ``torch.ops.fbgemm.bounds_check_indices`` (BoundsCheckMode.WARNING by
+    default, as upstream); the count accumulates in ``bounds_check_warning``.
     """
 
     def __init__(
@@ -49,6 +59,7 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         output_dtype: SparseType = SparseType.FP32,
         device: Optional[torch.device] = None,
         weights_init: Optional[tuple[float, float]] = None,
+        bounds_check_mode: BoundsCheckMode = BoundsCheckMode.WARNING,
     ) -> None:
         super().__init__()
         if optimizer != EmbOptimType.EXACT_ROWWISE_ADAGRAD:
@@ -74,6 +85,7 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.eps = float(eps)
         self.weight_decay = float(weight_decay)
         self.weight_decay_mode = int(weight_decay_mode)
+        self.bounds_check_mode = BoundsCheckMode(bounds_check_mode)
         rows = [E for E, _, _, _ in embedding_specs]
         dims = [D for _, D, _, _ in embedding_specs]
         self.T = len(embedding_specs)
@@ -109,6 +121,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         # though the weights are updated by the fused backward, not by autograd.
         self.placeholder_autograd_tensor = nn.Parameter(
             torch.zeros(0, device=device, dtype=torch.float32))
+        self.register_buffer("rows_per_table", torch.tensor(rows, **i64))
+        self.register_buffer("bounds_check_warning", torch.zeros(1, **i64))
         self._rows = rows
         self._dims = dims
 
@@ -116,10 +130,14 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
                 per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
         if per_sample_weights is not None:
             raise ValueError("per_sample_weights are not supported by the training lookup")
-        if offsets.numel() % 1 or (offsets.numel() - 1) % self.T:
+        if (offsets.numel() - 1) % self.T:
             raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
         if indices.dtype != offsets.dtype:
             offsets = offsets.to(indices.dtype)
+        if self.bounds_check_mode != BoundsCheckMode.NONE:
+            torch.ops.fbgemm.bounds_check_indices(self.rows_per_table, indices, offsets,
+                                                  int(self.bounds_check_mode),
+                                                  self.bounds_check_warning)
         return torch.ops.fbgemm.split_embedding_codegen_lookup_rowwise_adagrad_function(
             self.placeholder_autograd_tensor, self.weights_dev, self.weights_uvm,
             self.lxu_cache_weights, self.weights_placements, self.weights_offsets,
