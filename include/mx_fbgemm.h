@@ -200,6 +200,30 @@ int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B,
                             int64_t* warning, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* ---- rowwise quantization codecs ---------------------------------------- */
+
+/* Serve fbgemm::FloatToFused8BitRowwiseQuantized / HalfToFused8BitRowwiseQuantized
+ * and fbgemm::Fused8BitRowwiseQuantizedToFloat / ...ToHalf.
+ * Fused 8-bit row: D codes, fp32 scale, fp32 bias (D + 8 bytes);
+ * scale = (max - min) / 255, bias = min, q = rint((x - min) * 255 / (max - min + 1e-8));
+ * dequantized value = fma(q, scale, bias).  in/out dtype: MX_DTYPE_F32 or F16. */
+int mx_quantize_fused8bit_rowwise(const void* in, int32_t in_dtype, int64_t rows, int64_t D,
+                                  uint8_t* out, void* stream);
+int mx_dequantize_fused8bit_rowwise(const uint8_t* in, int64_t rows, int64_t D, void* out,
+                                    int32_t out_dtype, void* stream);
+
+/* Serve fbgemm::FloatToFusedNBitRowwiseQuantizedSBHalf / HalfTo... and
+ * fbgemm::FusedNBitRowwiseQuantizedSBHalfToFloat / ...ToHalf (bit_rate 2, 4, 8).
+ * Row: ceil(D*bit_rate/8) code bytes (element 0 in the lowest bits), fp16
+ * scale, fp16 bias; bias = half(min), scale = half((max - bias) / (2^b - 1))
+ * (1 for a zero range or an underflowing scale), q = clamp(rint((x - bias) *
+ * (1/scale)), 0, 2^b - 1); dequantized value = fma(q, scale, bias). */
+int mx_quantize_fused_nbit_rowwise(const void* in, int32_t in_dtype, int64_t rows, int64_t D,
+                                   int32_t bit_rate, uint8_t* out, void* stream);
+int mx_dequantize_fused_nbit_rowwise(const uint8_t* in, int64_t rows, int64_t D,
+                                     int32_t bit_rate, void* out, int32_t out_dtype,
+                                     void* stream);
+
 /* ---- TBE nbit inference forward ---------------------------------------- */
 
 /* Padded size in bytes of one row of a table of type `ty` and dim D:

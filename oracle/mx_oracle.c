@@ -399,3 +399,94 @@ int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* ind
   free(rep);
   return bad;
 }
+
+/* ---- rowwise quantization codecs -------------------------------------------
+ * FBGEMM's FloatOrHalfToFused8BitRowwiseQuantizedSBFloat and
+ * FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf (declared in
+ * torch/include/fbgemm/QuantUtils.h), as fbgemm_gpu's
+ * FloatToFused8BitRowwiseQuantized / FloatToFusedNBitRowwiseQuantizedSBHalf
+ * use them:
+ *   8-bit: scale = (max - min) / 255, q = rint((x - min) * (255 / (range +
+ *          1e-8))), row = D codes + fp32 scale + fp32 bias(=min);
+ *   N-bit: bias = half(min), scale = half((max - bias) / (2^b - 1)) (1 when
+ *          the range is 0, or when the scale underflows / its inverse
+ *          overflows), q = clamp(rint((x - bias) / scale'), 0, 2^b - 1) with
+ *          scale' = 1/scale computed once, packed low bits first, row =
+ *          ceil(D*b/8) bytes + fp16 scale + fp16 bias. */
+void orc_quantize_8bit(const float* x, int64_t rows, int64_t D, uint8_t* out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* v = x + r * D;
+    uint8_t* o = out + r * (D + 8);
+    float mn = INFINITY, mx = -INFINITY;
+    for (int64_t j = 0; j < D; ++j) {
+      mn = v[j] < mn ? v[j] : mn;
+      mx = v[j] > mx ? v[j] : mx;
+    }
+    const float range = mx - mn;
+    const float scale = range / 255.0f;
+    const float inv = 255.0f / (range + 1e-8f);
+    for (int64_t j = 0; j < D; ++j) o[j] = (uint8_t)rintf((v[j] - mn) * inv);
+    memcpy(o + D, &scale, 4);
+    memcpy(o + D + 4, &mn, 4);
+  }
+}
+
+void orc_dequantize_8bit(const uint8_t* in, int64_t rows, int64_t D, float* out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint8_t* q = in + r * (D + 8);
+    float scale, bias;
+    memcpy(&scale, q + D, 4);
+    memcpy(&bias, q + D + 4, 4);
+    for (int64_t j = 0; j < D; ++j) out[r * D + j] = fmaf((float)q[j], scale, bias);
+  }
+}
+
+void orc_quantize_nbit(const float* x, int64_t rows, int64_t D, int32_t bits, uint8_t* out) {
+  const int per = 8 / bits;
+  const int64_t nbytes = (D + per - 1) / per;
+  const int qmax = (1 << bits) - 1;
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* v = x + r * D;
+    uint8_t* o = out + r * (nbytes + 4);
+    float mn = INFINITY, mx = -INFINITY;
+    for (int64_t j = 0; j < D; ++j) {
+      mn = v[j] < mn ? v[j] : mn;
+      mx = v[j] > mx ? v[j] : mx;
+    }
+    const float bias = orc_half_to_float(orc_float_to_half(mn));
+    const float range = mx - bias;
+    float scale = range == 0.0f ? 1.0f : range / (float)qmax;
+    scale = orc_half_to_float(orc_float_to_half(scale));
+    if (scale == 0.0f) scale = 1.0f;
+    float inv = 1.0f / scale;
+    if (isinf(inv)) {
+      scale = 1.0f;
+      inv = 1.0f;
+    }
+    memset(o, 0, nbytes);
+    for (int64_t j = 0; j < D; ++j) {
+      float q = rintf((v[j] - bias) * inv);
+      q = q < 0.0f ? 0.0f : (q > (float)qmax ? (float)qmax : q);
+      o[j / per] |= (uint8_t)((uint32_t)q << ((j % per) * bits));
+    }
+    const uint16_t hs = orc_float_to_half(scale), hb = orc_float_to_half(bias);
+    memcpy(o + nbytes, &hs, 2);
+    memcpy(o + nbytes + 2, &hb, 2);
+  }
+}
+
+void orc_dequantize_nbit(const uint8_t* in, int64_t rows, int64_t D, int32_t bits, float* out) {
+  const int per = 8 / bits;
+  const int64_t nbytes = (D + per - 1) / per;
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint8_t* q = in + r * (nbytes + 4);
+    uint16_t hs, hb;
+    memcpy(&hs, q + nbytes, 2);
+    memcpy(&hb, q + nbytes + 2, 2);
+    const float scale = orc_half_to_float(hs), bias = orc_half_to_float(hb);
+    for (int64_t j = 0; j < D; ++j) {
+      const uint32_t c = (q[j / per] >> ((j % per) * bits)) & ((1u << bits) - 1u);
+      out[r * D + j] = fmaf((float)c, scale, bias);
+    }
+  }
+}

@@ -40,4 +40,8 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
                                  int32_t wd_mode, int32_t nb);
 int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* indices,
                          int64_t* offsets, int64_t N, int32_t mode);
+void orc_quantize_8bit(const float* x, int64_t rows, int64_t D, uint8_t* out);
+void orc_dequantize_8bit(const uint8_t* in, int64_t rows, int64_t D, float* out);
+void orc_quantize_nbit(const float* x, int64_t rows, int64_t D, int32_t bits, uint8_t* out);
+void orc_dequantize_nbit(const uint8_t* in, int64_t rows, int64_t D, int32_t bits, float* out);
 #endif

@@ -69,6 +69,12 @@ def lib():
         _lib.orc_backward_rowwise_adagrad.restype = ctypes.c_int
         _lib.orc_bounds_check.argtypes = [P, i32, i64, P, P, i64, i32]
         _lib.orc_bounds_check.restype = i64
+        for name in ("orc_quantize_8bit", "orc_dequantize_8bit"):
+            getattr(_lib, name).argtypes = [P, i64, i64, P]
+            getattr(_lib, name).restype = None
+        for name in ("orc_quantize_nbit", "orc_dequantize_nbit"):
+            getattr(_lib, name).argtypes = [P, i64, i64, i32, P]
+            getattr(_lib, name).restype = None
         _lib.orc_half_to_float.argtypes = [ctypes.c_uint16]
         _lib.orc_half_to_float.restype = f32
         _lib.orc_float_to_half.argtypes = [f32]
@@ -270,6 +276,39 @@ def bounds_check_indices(rows_per_table, indices, offsets, mode):
     B = (off.shape[0] - 1) // T
     n = lib().orc_bounds_check(_p(rows), T, B, _p(idx), _p(off), idx.shape[0], mode)
     return idx, off, int(n)
+
+
+def quantize_fused8bit(x):
+    x = _c(x, np.float32)
+    rows, D = x.shape
+    out = np.zeros((rows, D + 8), np.uint8)
+    lib().orc_quantize_8bit(_p(x), rows, D, _p(out))
+    return out
+
+
+def dequantize_fused8bit(q):
+    q = _c(q, np.uint8)
+    rows, D = q.shape[0], q.shape[1] - 8
+    out = np.zeros((rows, D), np.float32)
+    lib().orc_dequantize_8bit(_p(q), rows, D, _p(out))
+    return out
+
+
+def quantize_fused_nbit(x, bits):
+    x = _c(x, np.float32)
+    rows, D = x.shape
+    per = 8 // bits
+    out = np.zeros((rows, (D + per - 1) // per + 4), np.uint8)
+    lib().orc_quantize_nbit(_p(x), rows, D, bits, _p(out))
+    return out
+
+
+def dequantize_fused_nbit(q, bits, D):
+    q = _c(q, np.uint8)
+    rows = q.shape[0]
+    out = np.zeros((rows, D), np.float32)
+    lib().orc_dequantize_nbit(_p(q), rows, D, bits, _p(out))
+    return out
 
 
 def info_B_num_bits(T: int, B: int) -> int:

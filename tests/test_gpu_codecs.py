@@ -1,0 +1,89 @@
+"""GPU parity of the rowwise quantization codecs: bit-exact against the C
+oracle, which is itself pinned bit-exactly to torch's
+quantized::embedding_bag_{byte,4bit,2bit}_prepack/unpack (FBGEMM's CPU codecs)
+in test_oracle_pins.py; plus the TBE-layout packer feeding the nbit lookup."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows(rng, n, D):
+    x = (rng.standard_normal((n, D)) * rng.uniform(1e-3, 10, (n, 1))).astype(np.float32)
+    x[0] = 0.25            # constant row
+    x[1, :] = np.linspace(-1, 1, D)
+    return x
+
+
+@pytest.mark.parametrize("D", [1, 7, 16, 64, 128, 200])
+def test_fused8bit_round_trip_bits(dev, D):
+    print(f"[case] fused8bit D={D}", flush=True)
+    x = _rows(np.random.default_rng(D), 300, D)
+    q = torch.ops.fbgemm.FloatToFused8BitRowwiseQuantized(torch.from_numpy(x).to(dev))
+    np.testing.assert_array_equal(q.cpu().numpy(), orc.quantize_fused8bit(x))
+    d = torch.ops.fbgemm.Fused8BitRowwiseQuantizedToFloat(q)
+    np.testing.assert_array_equal(d.cpu().numpy(), orc.dequantize_fused8bit(q.cpu().numpy()))
+    h = torch.ops.fbgemm.Fused8BitRowwiseQuantizedToHalf(q)
+    np.testing.assert_array_equal(h.cpu().numpy(), d.cpu().numpy().astype(np.float16))
+    xh = torch.from_numpy(x).half()
+    qh = torch.ops.fbgemm.HalfToFused8BitRowwiseQuantized(xh.to(dev))
+    np.testing.assert_array_equal(qh.cpu().numpy(), orc.quantize_fused8bit(xh.float().numpy()))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("D", [8, 16, 36, 128, 256])
+def test_fused_nbit_round_trip_bits(dev, bits, D):
+    print(f"[case] fused nbit bits={bits} D={D}", flush=True)
+    x = _rows(np.random.default_rng(D * bits), 300, D)
+    q = torch.ops.fbgemm.FloatToFusedNBitRowwiseQuantizedSBHalf(torch.from_numpy(x).to(dev), bits)
+    np.testing.assert_array_equal(q.cpu().numpy(), orc.quantize_fused_nbit(x, bits))
+    d = torch.ops.fbgemm.FusedNBitRowwiseQuantizedSBHalfToFloat(q, bits)
+    np.testing.assert_array_equal(d.cpu().numpy(), orc.dequantize_fused_nbit(q.cpu().numpy(), bits, D))
+    xh = torch.from_numpy(x).half()
+    qh = torch.ops.fbgemm.HalfToFusedNBitRowwiseQuantizedSBHalf(xh.to(dev), bits)
+    np.testing.assert_array_equal(qh.cpu().numpy(), orc.quantize_fused_nbit(xh.float().numpy(), bits))
+
+
+@pytest.mark.parametrize("ty", ["INT8", "INT4", "INT2", "FP16"])
+def test_inference_module_assign_and_lookup(dev, ty):
+    """quantize_rows' TBE layout decodes (through the nbit lookup) to the
+    codec's own dequantization, and the module matches the oracle."""
+    print(f"[case] inference module {ty}", flush=True)
+    from mx_fbgemm import EmbeddingLocation, PoolingMode, SparseType
+    from mx_fbgemm.split_table_batched_embeddings_ops_inference import (
+        IntNBitTableBatchedEmbeddingBagsCodegen,
+    )
+    from tbe_helpers import random_tbe
+
+    sty = SparseType[ty]
+    E, D, B = 60, 32, 12
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(
+        [("a", E, D, sty, EmbeddingLocation.DEVICE), ("b", E, 2 * D, sty, EmbeddingLocation.DEVICE)],
+        pooling_mode=PoolingMode.SUM, output_dtype=SparseType.FP32, device=dev)
+    rng = np.random.default_rng(7)
+    ws = [torch.from_numpy(rng.uniform(-1, 1, (E, d)).astype(np.float32)) for d in (D, 2 * D)]
+    m.assign_embedding_weights([w.to(dev) for w in ws])
+    # one-row bags decode each row exactly once
+    idx = np.tile(np.arange(E), 2).astype(np.int64)
+    off = np.arange(2 * E + 1, dtype=np.int64)
+    got = m(torch.from_numpy(idx).to(dev), torch.from_numpy(off).to(dev)).cpu().numpy()
+    for t, w in enumerate(ws):
+        d = w.shape[1]
+        if sty == SparseType.FP16:
+            exp = w.half().float().numpy()
+        else:
+            q = orc.quantize_fused_nbit(w.numpy(), sty.bit_rate())
+            exp = orc.dequantize_fused_nbit(q, sty.bit_rate(), d)
+        cols = slice(0, D) if t == 0 else slice(D, 3 * D)
+        np.testing.assert_allclose(got[:, cols], exp, rtol=1e-6, atol=1e-6)
+    # pooled lookup vs the oracle on the packed buffer
+    inp = random_tbe(rng, 2, B, [D, 2 * D], [E, E], 9)
+    res = m(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev))
+    buf = m.weights_dev.cpu().numpy()
+    exp = orc.nbit_forward(buf, m.weights_offsets.cpu().numpy(), [sty.as_int()] * 2,
+                           inp.D_offsets, B, inp.indices, inp.offsets, 0, out_f16=False)
+    np.testing.assert_allclose(res.cpu().numpy(), exp, rtol=1e-5, atol=1e-5)

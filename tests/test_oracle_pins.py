@@ -340,3 +340,28 @@ def test_bounds_check_vs_python(mode, case):
         for bag in range(T * B):
             seg = got_idx[got_off[bag]:got_off[bag + 1]]
             assert np.all((seg >= 0) & (seg < rows[bag // B]))
+
+
+# ---- rowwise quantization codecs -------------------------------------------
+
+@pytest.mark.parametrize("D", [1, 7, 16, 36, 128])
+def test_codecs_vs_torch_quantized_prepack(D):
+    rng = np.random.default_rng(D)
+    x = (rng.standard_normal((100, D)) * rng.uniform(1e-3, 10, (100, 1))).astype(np.float32)
+    x[0] = 0.5
+    xt = torch.from_numpy(x)
+    q8 = orc.quantize_fused8bit(x)
+    np.testing.assert_array_equal(q8, torch.ops.quantized.embedding_bag_byte_prepack(xt).numpy())
+    np.testing.assert_array_equal(
+        orc.dequantize_fused8bit(q8),
+        torch.ops.quantized.embedding_bag_byte_unpack(torch.from_numpy(q8)).numpy())
+    for bits, pack, unpack in ((4, torch.ops.quantized.embedding_bag_4bit_prepack,
+                                torch.ops.quantized.embedding_bag_4bit_unpack),
+                               (2, torch.ops.quantized.embedding_bag_2bit_prepack,
+                                torch.ops.quantized.embedding_bag_2bit_unpack)):
+        if D % (8 // bits):
+            continue
+        q = orc.quantize_fused_nbit(x, bits)
+        np.testing.assert_array_equal(q, pack(xt).numpy())
+        np.testing.assert_array_equal(orc.dequantize_fused_nbit(q, bits, D),
+                                      unpack(torch.from_numpy(q)).numpy())

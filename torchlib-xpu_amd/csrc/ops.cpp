@@ -633,6 +633,103 @@ void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
 }
 
 // ---------------------------------------------------------------------------
+// Rowwise quantization codecs
+// ---------------------------------------------------------------------------
+
+Tensor rows_2d(const Tensor& t, const char* name) {
+  check_gpu(t, name);
+  TORCH_CHECK(t.dim() >= 1, name, " must have at least one dimension");
+  return t.contiguous().view({-1, t.size(-1)});
+}
+
+std::vector<int64_t> with_last(const Tensor& t, int64_t last) {
+  std::vector<int64_t> shape(t.sizes().begin(), t.sizes().end());
+  shape.back() = last;
+  return shape;
+}
+
+Tensor quantize_8bit(const Tensor& input) {
+  const Tensor x = rows_2d(input, "input");
+  c10::OptionalDeviceGuard guard(x.device());
+  const int32_t dt = mx_dtype_of(x.scalar_type());
+  TORCH_CHECK(dt == MX_DTYPE_F32 || dt == MX_DTYPE_F16, "input must be float32 or float16");
+  const int64_t D = x.size(1);
+  Tensor out = at::empty(with_last(input, D + 8), x.options().dtype(at::kByte));
+  MX_CALL(mx_quantize_fused8bit_rowwise(x.data_ptr(), dt, x.size(0), D, out.data_ptr<uint8_t>(),
+                                        stream_of(x)));
+  return out;
+}
+
+Tensor dequantize_8bit(const Tensor& input, at::ScalarType st) {
+  const Tensor q = rows_2d(input, "input");
+  c10::OptionalDeviceGuard guard(q.device());
+  TORCH_CHECK(q.scalar_type() == at::kByte, "input must be uint8");
+  const int64_t D = q.size(1) - 8;
+  TORCH_CHECK(D >= 0, "rows must hold at least the 8 bytes of scale and bias");
+  Tensor out = at::empty(with_last(input, D), q.options().dtype(st));
+  MX_CALL(mx_dequantize_fused8bit_rowwise(q.data_ptr<uint8_t>(), q.size(0), D, out.data_ptr(),
+                                          mx_dtype_of(st), stream_of(q)));
+  return out;
+}
+
+Tensor quantize_nbit(const Tensor& input, int64_t bit_rate) {
+  const Tensor x = rows_2d(input, "input");
+  c10::OptionalDeviceGuard guard(x.device());
+  const int32_t dt = mx_dtype_of(x.scalar_type());
+  TORCH_CHECK(dt == MX_DTYPE_F32 || dt == MX_DTYPE_F16, "input must be float32 or float16");
+  TORCH_CHECK(bit_rate == 2 || bit_rate == 4 || bit_rate == 8, "bit_rate must be 2, 4 or 8");
+  const int64_t D = x.size(1);
+  const int64_t per = 8 / bit_rate;
+  const int64_t nbytes = (D + per - 1) / per;
+  Tensor out = at::empty(with_last(input, nbytes + 4), x.options().dtype(at::kByte));
+  MX_CALL(mx_quantize_fused_nbit_rowwise(x.data_ptr(), dt, x.size(0), D,
+                                         static_cast<int32_t>(bit_rate), out.data_ptr<uint8_t>(),
+                                         stream_of(x)));
+  return out;
+}
+
+Tensor dequantize_nbit(const Tensor& input, int64_t bit_rate, at::ScalarType st) {
+  const Tensor q = rows_2d(input, "input");
+  c10::OptionalDeviceGuard guard(q.device());
+  TORCH_CHECK(q.scalar_type() == at::kByte, "input must be uint8");
+  TORCH_CHECK(bit_rate == 2 || bit_rate == 4 || bit_rate == 8, "bit_rate must be 2, 4 or 8");
+  const int64_t D = (q.size(1) - 4) * (8 / bit_rate);
+  TORCH_CHECK(D >= 0, "rows must hold at least the 4 bytes of scale and bias");
+  Tensor out = at::empty(with_last(input, D), q.options().dtype(st));
+  MX_CALL(mx_dequantize_fused_nbit_rowwise(q.data_ptr<uint8_t>(), q.size(0), D,
+                                           static_cast<int32_t>(bit_rate), out.data_ptr(),
+                                           mx_dtype_of(st), stream_of(q)));
+  return out;
+}
+
+Tensor float_to_8bit(const Tensor& t) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat, "input must be float32");
+  return quantize_8bit(t);
+}
+Tensor half_to_8bit(const Tensor& t) {
+  TORCH_CHECK(t.scalar_type() == at::kHalf, "input must be float16");
+  return quantize_8bit(t);
+}
+Tensor float_or_half_to_8bit(const Tensor& t) { return quantize_8bit(t); }
+Tensor fused8bit_to_float(const Tensor& t) { return dequantize_8bit(t, at::kFloat); }
+Tensor fused8bit_to_half(const Tensor& t) { return dequantize_8bit(t, at::kHalf); }
+Tensor float_to_nbit(const Tensor& t, int64_t bit_rate) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat, "input must be float32");
+  return quantize_nbit(t, bit_rate);
+}
+Tensor half_to_nbit(const Tensor& t, int64_t bit_rate) {
+  TORCH_CHECK(t.scalar_type() == at::kHalf, "input must be float16");
+  return quantize_nbit(t, bit_rate);
+}
+Tensor float_or_half_to_nbit(const Tensor& t, int64_t bit_rate) { return quantize_nbit(t, bit_rate); }
+Tensor nbit_to_float(const Tensor& t, int64_t bit_rate) {
+  return dequantize_nbit(t, bit_rate, at::kFloat);
+}
+Tensor nbit_to_half(const Tensor& t, int64_t bit_rate) {
+  return dequantize_nbit(t, bit_rate, at::kHalf);
+}
+
+// ---------------------------------------------------------------------------
 // nbit inference
 // ---------------------------------------------------------------------------
 
@@ -745,6 +842,16 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
         "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
         "float max_norm=0.0, int output_dtype=0) -> Tensor");
+  m.def("FloatToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
+  m.def("HalfToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
+  m.def("FloatOrHalfToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
+  m.def("Fused8BitRowwiseQuantizedToFloat(Tensor input) -> Tensor");
+  m.def("Fused8BitRowwiseQuantizedToHalf(Tensor input) -> Tensor");
+  m.def("FloatToFusedNBitRowwiseQuantizedSBHalf(Tensor input, int bit_rate) -> Tensor");
+  m.def("HalfToFusedNBitRowwiseQuantizedSBHalf(Tensor input, int bit_rate) -> Tensor");
+  m.def("FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf(Tensor input, int bit_rate) -> Tensor");
+  m.def("FusedNBitRowwiseQuantizedSBHalfToFloat(Tensor input, int bit_rate) -> Tensor");
+  m.def("FusedNBitRowwiseQuantizedSBHalfToHalf(Tensor input, int bit_rate) -> Tensor");
   m.def("bounds_check_indices(Tensor rows_per_table, Tensor(a!) indices, Tensor(b!) offsets, "
         "int bounds_check_mode, Tensor(c!) warning, Tensor? weights=None, "
         "Tensor? B_offsets=None, SymInt max_B=-1, Tensor? b_t_map=None, int info_B_num_bits=-1, "
@@ -774,6 +881,16 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
          TORCH_FN(mx_ops::lookup_rowwise_adagrad));
   m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
   m.impl("bounds_check_indices", TORCH_FN(mx_ops::bounds_check_indices));
+  m.impl("FloatToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_to_8bit));
+  m.impl("HalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::half_to_8bit));
+  m.impl("FloatOrHalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_or_half_to_8bit));
+  m.impl("Fused8BitRowwiseQuantizedToFloat", TORCH_FN(mx_ops::fused8bit_to_float));
+  m.impl("Fused8BitRowwiseQuantizedToHalf", TORCH_FN(mx_ops::fused8bit_to_half));
+  m.impl("FloatToFusedNBitRowwiseQuantizedSBHalf", TORCH_FN(mx_ops::float_to_nbit));
+  m.impl("HalfToFusedNBitRowwiseQuantizedSBHalf", TORCH_FN(mx_ops::half_to_nbit));
+  m.impl("FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf", TORCH_FN(mx_ops::float_or_half_to_nbit));
+  m.impl("FusedNBitRowwiseQuantizedSBHalfToFloat", TORCH_FN(mx_ops::nbit_to_float));
+  m.impl("FusedNBitRowwiseQuantizedSBHalfToHalf", TORCH_FN(mx_ops::nbit_to_half));
 }
 
 TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {

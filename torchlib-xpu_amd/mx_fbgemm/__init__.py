@@ -42,6 +42,16 @@ OPS = (
     "split_embedding_codegen_lookup_rowwise_adagrad_function",
     "int_nbit_split_embedding_codegen_lookup_function",
     "bounds_check_indices",
+    "FloatToFused8BitRowwiseQuantized",
+    "HalfToFused8BitRowwiseQuantized",
+    "FloatOrHalfToFused8BitRowwiseQuantized",
+    "Fused8BitRowwiseQuantizedToFloat",
+    "Fused8BitRowwiseQuantizedToHalf",
+    "FloatToFusedNBitRowwiseQuantizedSBHalf",
+    "HalfToFusedNBitRowwiseQuantizedSBHalf",
+    "FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf",
+    "FusedNBitRowwiseQuantizedSBHalfToFloat",
+    "FusedNBitRowwiseQuantizedSBHalfToHalf",
 )
 
 _loaded = False

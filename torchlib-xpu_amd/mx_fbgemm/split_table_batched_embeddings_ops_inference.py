@@ -32,40 +32,30 @@ load_mx_fbgemm_library()
 
 def quantize_rows(weights: torch.Tensor, weight_ty: SparseType,
                   row_alignment: int = 16) -> torch.Tensor:
-    """fp32 ``[E, D]`` -> uint8 ``[E, padded_row_bytes]`` in the TBE row layout.
+    """fp32/fp16 ``[E, D]`` (on the GPU) -> uint8 ``[E, padded_row_bytes]`` in
+    the TBE row layout.
 
-    INT8/INT4/INT2: per row, bias = min, scale = (max - min) / (2^bits - 1),
-    both rounded to fp16; code = round((w - bias) / scale) clamped to the
-    code range (the rowwise min/max scheme of FBGEMM's
-    FloatToFusedNBitRowwiseQuantizedSBHalf, recalled).  FP16/FP32 rows are
+    INT8/INT4/INT2 rows are quantized by
+    ``torch.ops.fbgemm.FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf`` (bit rate
+    8/4/2: fp16 scale and bias) and the two fp16 qparams are moved from the
+    row end to the row front, as the TBE layout wants; FP16/FP32 rows are
     stored as-is.  Padding bytes are zero."""
+    if not weights.is_cuda:
+        raise ValueError("quantize_rows runs on the GPU; move the weights to the device first")
     E, D = weights.shape
     stride = padded_row_size_in_bytes(D, weight_ty, row_alignment)
     out = torch.zeros((E, stride), dtype=torch.uint8, device=weights.device)
-    w = weights.float()
     if weight_ty == SparseType.FP32:
-        out[:, : 4 * D] = w.contiguous().view(torch.uint8).view(E, 4 * D)
+        out[:, : 4 * D] = weights.float().contiguous().view(torch.uint8).view(E, 4 * D)
         return out
     if weight_ty == SparseType.FP16:
-        out[:, : 2 * D] = w.half().contiguous().view(torch.uint8).view(E, 2 * D)
+        out[:, : 2 * D] = weights.half().contiguous().view(torch.uint8).view(E, 2 * D)
         return out
-    bits = weight_ty.bit_rate()
-    qmax = (1 << bits) - 1
-    lo = w.min(dim=1).values
-    hi = w.max(dim=1).values
-    scale = ((hi - lo) / qmax).half()
-    bias = lo.half()
-    s32 = scale.float()
-    s32 = torch.where(s32 == 0, torch.ones_like(s32), s32)
-    q = torch.clamp(torch.round((w - bias.float()[:, None]) / s32[:, None]), 0, qmax).to(torch.int32)
-    per_byte = 8 // bits
-    q = q.view(E, D // per_byte, per_byte)
-    packed = torch.zeros((E, D // per_byte), dtype=torch.int32, device=w.device)
-    for k in range(per_byte):
-        packed |= q[:, :, k] << (k * bits)
-    out[:, 0:2] = scale.view(torch.uint8).view(E, 2)
-    out[:, 2:4] = bias.view(torch.uint8).view(E, 2)
-    out[:, 4:4 + D // per_byte] = packed.to(torch.uint8)
+    q = torch.ops.fbgemm.FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf(
+        weights.contiguous(), weight_ty.bit_rate())
+    nbytes = q.shape[1] - 4
+    out[:, 0:4] = q[:, nbytes:]
+    out[:, 4:4 + nbytes] = q[:, :nbytes]
     return out
 
 
