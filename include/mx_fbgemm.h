@@ -161,15 +161,17 @@ int mx_tbe_transpose_embedding_input(
 /* Workspace needed by mx_tbe_backward_rowwise_adagrad. */
 size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, int32_t max_D);
 
-/* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
- * (the backward of split_embedding_codegen_lookup_rowwise_adagrad_function).
+/* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_{unweighted,
+ * weighted}_exact_cuda (the backward of
+ * split_embedding_codegen_lookup_rowwise_adagrad_function).
  * For each distinct (t, i) touched by the batch:
- *   g      = sum over its occurrences (sorted order) of grad_output[b, D_t slice]
- *            (MEAN: each occurrence scaled by 1.0f/L of its bag)
- *   mode 1 (L2):        g += weight_decay * w
- *   h     += (sum_d g_d^2) / D_t
+ *   g      = sum over its occurrences (sorted order) of grad_output[b, D_t slice],
+ *            each term scaled by 1.0f/L of its bag (MEAN) and then by its
+ *            per-sample weight (indice_weights [N], weighted lookups; NULL otherwise)
+ *   s      = g + weight_decay * w (mode 1, L2) or g
+ *   h     += (sum_d s_d^2) / D_t
  *   m      = learning_rate / (sqrtf(h) + eps)
- *   c      = 1 (mode 0, 1) or 1 - learning_rate*weight_decay (mode 2)
+ *   c      = 1 (mode 0), 1 - m*weight_decay (mode 1), 1 - learning_rate*weight_decay (mode 2)
  *   w      = fmaf(-m, g, c * w)
  * weights and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are
  * updated in place; no atomics, deterministic. */
@@ -177,9 +179,22 @@ int mx_tbe_backward_rowwise_adagrad(
     float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
     int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
-    int32_t pooling_mode, const float* grad_output, int64_t total_D, float* momentum1,
-    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
-    int32_t weight_decay_mode, void* workspace, size_t workspace_bytes, void* stream);
+    int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
+    float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
+    float weight_decay, int32_t weight_decay_mode, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* Serves fbgemm::split_embedding_codegen_grad_indice_weights_cuda: the gradient
+ * of a weighted lookup's per-sample weights,
+ *   grad_indice_weights[l] = sum_d grad_output[b, D_off[t] + d] * W_t[indices[l], d]
+ * (MEAN: times 1.0f/L), 0 for tables with feature_requires_grad[t] == 0
+ * (feature_requires_grad may be NULL: every table). */
+int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D, const float* weights,
+                               const int64_t* weights_offsets, const int32_t* D_offsets,
+                               int32_t T, int64_t B, int32_t max_D, const void* indices,
+                               const void* offsets, int32_t index_bytes, int32_t pooling_mode,
+                               const int32_t* feature_requires_grad, float* grad_indice_weights,
+                               void* stream);
 
 /* ---- index validation ---------------------------------------------------- */
 

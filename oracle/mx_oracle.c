@@ -238,10 +238,11 @@ static void merge_sort(int64_t* a, int64_t* tmp, int64_t n) {
   memcpy(a, tmp, sizeof(int64_t) * n);
 }
 
-int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t bits,
-                  const int64_t* indices, const int64_t* offsets, int64_t N, int64_t* linear,
-                  int64_t* sorted, int32_t* infos, int64_t* run, int32_t* run_lengths,
-                  int64_t* num_runs, int32_t* cum) {
+/* pos (optional): pos[i] = position in `indices` of the i-th sorted entry. */
+static int transpose_impl(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t bits,
+                          const int64_t* indices, const int64_t* offsets, int64_t N,
+                          int64_t* linear, int64_t* sorted, int32_t* infos, int64_t* run,
+                          int32_t* run_lengths, int64_t* num_runs, int32_t* cum, int64_t* pos) {
   uint32_t* info_raw = (uint32_t*)malloc(sizeof(uint32_t) * (N > 0 ? N : 1));
   int64_t* perm = (int64_t*)malloc(sizeof(int64_t) * (N > 0 ? N : 1));
   int64_t* tmp = (int64_t*)malloc(sizeof(int64_t) * (N > 0 ? N : 1));
@@ -265,6 +266,7 @@ int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t 
   for (int64_t i = 0; i < N; ++i) {
     sorted[i] = linear[perm[i]];
     infos[i] = (int32_t)info_raw[perm[i]];
+    if (pos) pos[i] = perm[i];
     if (i == 0 || sorted[i] != sorted[i - 1]) {
       ++r;
       run[r] = sorted[i];
@@ -280,9 +282,18 @@ int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t 
   return 0;
 }
 
+int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t bits,
+                  const int64_t* indices, const int64_t* offsets, int64_t N, int64_t* linear,
+                  int64_t* sorted, int32_t* infos, int64_t* run, int32_t* run_lengths,
+                  int64_t* num_runs, int32_t* cum) {
+  return transpose_impl(hsc, T, B, nb, bits, indices, offsets, N, linear, sorted, infos, run,
+                        run_lengths, num_runs, cum, NULL);
+}
+
 /* ---- backward + exact rowwise Adagrad --------------------------------------
  * For each run (distinct (t, i)), in sorted order of its occurrences:
- *   g_d  = sum grad_output[b, D_off[t] + d]      (MEAN: each term * (1/L))
+ *   g_d  = sum grad_output[b, D_off[t] + d]      (MEAN: each term * (1/L),
+ *                                                 weighted: then * iw[l])
  *   L2 (mode 1):   s_d = g_d + wd * w_d,  else s_d = g_d
  *   h   += (sum_d s_d^2) / D
  *   m    = lr / (sqrtf(h) + eps)
@@ -292,7 +303,8 @@ int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t 
 int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* D_off,
                                  int32_t T, int64_t B, const int64_t* hsc, int32_t bits,
                                  const int64_t* indices, const int64_t* offsets, int64_t N,
-                                 int32_t pooling, const float* grad, int64_t total_D, float* m1,
+                                 int32_t pooling, const float* iw, const float* grad,
+                                 int64_t total_D, float* m1,
                                  const int64_t* m1_off, float lr, float eps, float wd,
                                  int32_t wd_mode, int32_t nb) {
   const int64_t n = N > 0 ? N : 1;
@@ -302,16 +314,17 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
   int64_t* run = (int64_t*)malloc(sizeof(int64_t) * n);
   int32_t* lens = (int32_t*)malloc(sizeof(int32_t) * n);
   int32_t* cum = (int32_t*)malloc(sizeof(int32_t) * (n + 1));
+  int64_t* pos = (int64_t*)malloc(sizeof(int64_t) * n);
   float* g = (float*)malloc(sizeof(float) * 1024);
   int rc = 0;
-  if (!linear || !sorted || !infos || !run || !lens || !cum || !g) {
+  if (!linear || !sorted || !infos || !run || !lens || !cum || !pos || !g) {
     rc = -2;
     goto done;
   }
   int64_t nruns = 0;
   if (N > 0) {
-    rc = orc_transpose(hsc, T, B, nb, bits, indices, offsets, N, linear, sorted, infos, run,
-                       lens, &nruns, cum);
+    rc = transpose_impl(hsc, T, B, nb, bits, indices, offsets, N, linear, sorted, infos, run,
+                        lens, &nruns, cum, pos);
     if (rc) goto done;
   }
   const uint32_t bmask = nb >= 32 ? 0xffffffffu : ((1u << nb) - 1u);
@@ -328,13 +341,10 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
     for (int32_t j = cum[r]; j < cum[r + 1]; ++j) {
       const int64_t b = (int64_t)((uint32_t)infos[j] & bmask);
       const float* gr = grad + b * total_D + D0;
-      if (pooling == ORC_POOL_MEAN) {
-        const int64_t L = offsets[t * B + b + 1] - offsets[t * B + b];
-        const float sc = L > 0 ? 1.0f / (float)L : 0.0f;
-        for (int32_t d = 0; d < D; ++d) g[d] = g[d] + gr[d] * sc;
-      } else {
-        for (int32_t d = 0; d < D; ++d) g[d] = g[d] + gr[d];
-      }
+      const int64_t L = offsets[t * B + b + 1] - offsets[t * B + b];
+      const float sc = pooling == ORC_POOL_MEAN ? 1.0f / (float)L : 1.0f; /* L >= 1 here */
+      const float wl = iw ? iw[pos[j]] : 1.0f;
+      for (int32_t d = 0; d < D; ++d) g[d] = g[d] + (gr[d] * sc) * wl;
     }
     float* w = W + w_off[t] + idx * D;
     float ss = 0.0f;
@@ -358,8 +368,37 @@ done:
   free(run);
   free(lens);
   free(cum);
+  free(pos);
   free(g);
   return rc;
+}
+
+/* ---- gradient of the per-sample weights ------------------------------------
+ * giw[l] = sum_d grad_output[b, D_off[t] + d] * W_t[indices[l], d], d ascending,
+ * times 1/L under MEAN; 0 for tables with frg[t] == 0 (frg may be NULL).
+ * Summation order differs from the GPU's (tree over lanes): compare at rtol. */
+void orc_grad_indice_weights(const float* grad, int64_t total_D, const float* W,
+                             const int64_t* w_off, const int32_t* D_off, int32_t T, int64_t B,
+                             const int64_t* indices, const int64_t* offsets, int32_t pooling,
+                             const int32_t* frg, float* giw) {
+  for (int32_t t = 0; t < T; ++t) {
+    const int32_t D0 = D_off[t], D = D_off[t + 1] - D_off[t];
+    for (int64_t b = 0; b < B; ++b) {
+      const int64_t s = offsets[t * B + b], e = offsets[t * B + b + 1];
+      const float sc = pooling == ORC_POOL_MEAN && e > s ? 1.0f / (float)(e - s) : 1.0f;
+      for (int64_t l = s; l < e; ++l) {
+        if (frg && frg[t] == 0) {
+          giw[l] = 0.0f;
+          continue;
+        }
+        const float* row = W + w_off[t] + indices[l] * D;
+        const float* gr = grad + b * total_D + D0;
+        double acc = 0.0;
+        for (int32_t d = 0; d < D; ++d) acc += (double)gr[d] * (double)row[d];
+        giw[l] = pooling == ORC_POOL_MEAN ? (float)acc * sc : (float)acc;
+      }
+    }
+  }
 }
 
 /* ---- bounds_check_indices -------------------------------------------------

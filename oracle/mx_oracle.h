@@ -35,9 +35,13 @@ int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t 
 int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* D_off,
                                  int32_t T, int64_t B, const int64_t* hsc, int32_t bits,
                                  const int64_t* indices, const int64_t* offsets, int64_t N,
-                                 int32_t pooling, const float* grad, int64_t total_D, float* m1,
-                                 const int64_t* m1_off, float lr, float eps, float wd,
-                                 int32_t wd_mode, int32_t nb);
+                                 int32_t pooling, const float* iw, const float* grad,
+                                 int64_t total_D, float* m1, const int64_t* m1_off, float lr,
+                                 float eps, float wd, int32_t wd_mode, int32_t nb);
+void orc_grad_indice_weights(const float* grad, int64_t total_D, const float* W,
+                             const int64_t* w_off, const int32_t* D_off, int32_t T, int64_t B,
+                             const int64_t* indices, const int64_t* offsets, int32_t pooling,
+                             const int32_t* frg, float* giw);
 int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* indices,
                          int64_t* offsets, int64_t N, int32_t mode);
 void orc_quantize_8bit(const float* x, int64_t rows, int64_t D, uint8_t* out);

@@ -65,8 +65,10 @@ def lib():
         _lib.orc_transpose.argtypes = [P, i32, i64, i32, i32, P, P, i64, P, P, P, P, P, P, P]
         _lib.orc_transpose.restype = ctypes.c_int
         _lib.orc_backward_rowwise_adagrad.argtypes = [
-            P, P, P, i32, i64, P, i32, P, P, i64, i32, P, i64, P, P, f32, f32, f32, i32, i32]
+            P, P, P, i32, i64, P, i32, P, P, i64, i32, P, P, i64, P, P, f32, f32, f32, i32, i32]
         _lib.orc_backward_rowwise_adagrad.restype = ctypes.c_int
+        _lib.orc_grad_indice_weights.argtypes = [P, i64, P, P, P, i32, i64, P, P, i32, P, P]
+        _lib.orc_grad_indice_weights.restype = None
         _lib.orc_bounds_check.argtypes = [P, i32, i64, P, P, i64, i32]
         _lib.orc_bounds_check.restype = i64
         for name in ("orc_quantize_8bit", "orc_dequantize_8bit"):
@@ -249,21 +251,39 @@ def transpose_embedding_input(hsc, B, info_B_num_bits, bits, indices, offsets):
 
 def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,
                              momentum1, m1_off, lr, eps, weight_decay=0.0, weight_decay_mode=0,
-                             info_B_num_bits=26):
-    """Updates copies of W and momentum1; returns (W_new, momentum1_new)."""
+                             info_B_num_bits=26, indice_weights=None):
+    """Updates copies of W and momentum1; returns (W_new, momentum1_new).
+    ``indice_weights`` (fp32 [N]) makes it the weighted backward."""
     W = np.array(W, dtype=np.float32, copy=True)
     m1 = np.array(momentum1, dtype=np.float32, copy=True)
     w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
     hsc, m1_off = _c(hsc, np.int64), _c(m1_off, np.int64)
     indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
     grad = _c(grad, np.float32)
+    iw = None if indice_weights is None else _c(indice_weights, np.float32)
+    assert iw is None or iw.shape[0] == indices.shape[0]
     T = D_off.shape[0] - 1
     rc = lib().orc_backward_rowwise_adagrad(
         _p(W), _p(w_off), _p(D_off), T, B, _p(hsc), bits, _p(indices), _p(offsets),
-        indices.shape[0], pooling, _p(grad), grad.shape[1], _p(m1), _p(m1_off), lr, eps,
-        weight_decay, weight_decay_mode, info_B_num_bits)
+        indices.shape[0], pooling, None if iw is None else _p(iw), _p(grad), grad.shape[1],
+        _p(m1), _p(m1_off), lr, eps, weight_decay, weight_decay_mode, info_B_num_bits)
     assert rc == 0, f"orc_backward_rowwise_adagrad failed ({rc})"
     return W, m1
+
+
+def grad_indice_weights(grad, W, w_off, D_off, B, indices, offsets, pooling=POOL_SUM,
+                        feature_requires_grad=None):
+    """fp32 [N]: d(out)/d(indice_weights[l]) contracted with grad_output."""
+    grad, W = _c(grad, np.float32), _c(W, np.float32)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    frg = None if feature_requires_grad is None else _c(feature_requires_grad, np.int32)
+    T = D_off.shape[0] - 1
+    out = np.zeros(indices.shape[0], dtype=np.float32)
+    lib().orc_grad_indice_weights(_p(grad), grad.shape[1], _p(W), _p(w_off), _p(D_off), T, B,
+                                  _p(indices), _p(offsets), pooling,
+                                  None if frg is None else _p(frg), _p(out))
+    return out
 
 
 def bounds_check_indices(rows_per_table, indices, offsets, mode):

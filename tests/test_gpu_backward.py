@@ -52,29 +52,37 @@ def test_transpose_bit_exact(dev, T, B, rows, max_L, dup):
     _check_transpose(dev, inp, torch.int32)
 
 
-def _backward_case(dev, inp, pooling, wd=0.0, wd_mode=0, lr=0.01, eps=1e-8, seed=0):
+def _backward_case(dev, inp, pooling, wd=0.0, wd_mode=0, lr=0.01, eps=1e-8, seed=0,
+                   weighted=False, index_dtype=torch.int64):
     rng = np.random.default_rng(seed)
     W = rng.uniform(-0.01, 0.01, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
     m1 = rng.uniform(0, 1e-4, size=sum(inp.E)).astype(np.float32)
     m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
     grad = rng.normal(0, 1e-2, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(-2.0, 2.0, inp.N).astype(np.float32) if weighted else None
     nb = orc.info_B_num_bits(inp.T, inp.B)
     W_exp, m1_exp = orc.backward_rowwise_adagrad(
         W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
         inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
-        wd, wd_mode, nb)
+        wd, wd_mode, nb, indice_weights=iw)
     Wd = torch.from_numpy(W).to(dev)
     m1d = torch.from_numpy(m1).to(dev)
     empty = torch.zeros(0, device=dev)
-    torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
-        torch.from_numpy(grad).to(dev), Wd, empty, empty,
-        torch.zeros(inp.T, dtype=torch.int32, device=dev),
-        torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
-        max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
-        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
-        torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty,
-        torch.zeros(inp.T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
-        eps, lr, wd, wd_mode, 0.0)
+    head = (torch.from_numpy(grad).to(dev), Wd, empty, empty,
+            torch.zeros(inp.T, dtype=torch.int32, device=dev),
+            torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
+            max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+            torch.from_numpy(inp.indices).to(dev, index_dtype),
+            torch.from_numpy(inp.offsets).to(dev, index_dtype), pooling)
+    tail = (torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty,
+            torch.zeros(inp.T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
+            eps, lr, wd, wd_mode, 0.0)
+    if weighted:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda(
+            *head, torch.from_numpy(iw).to(dev), *tail)
+    else:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+            *head, *tail)
     Wg, mg = Wd.cpu().numpy(), m1d.cpu().numpy()
     np.testing.assert_allclose(mg, m1_exp, rtol=RTOL, atol=0)
     np.testing.assert_allclose(Wg, W_exp, rtol=RTOL, atol=ATOL)
@@ -95,6 +103,57 @@ def test_backward_rowwise_adagrad(dev, pooling, T, B, dims, rows, max_L, dup):
     rng = np.random.default_rng(B + T)
     inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
     _backward_case(dev, inp, pooling, seed=B)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("T,B,dims,rows,max_L,dup", [
+    (3, 64, [4, 64, 256], [50, 2000, 40], 30, False),
+    (2, 200, [128, 1024], [4, 4], 40, True),       # long runs -> chunked path
+    (2, 500, [128, 32], [3, 20000], 25, True),     # one row per >1000 occurrences
+])
+def test_backward_weighted(dev, pooling, T, B, dims, rows, max_L, dup):
+    """Weighted backward: every occurrence's gradient slice is scaled by its
+    per-sample weight (after the MEAN 1/L); weights of both signs."""
+    print(f"[case] weighted backward T={T} B={B} dims={dims} pool={pooling}", flush=True)
+    rng = np.random.default_rng(B * 3 + T)
+    inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
+    _backward_case(dev, inp, pooling, seed=B + 1, weighted=True)
+    _backward_case(dev, inp, pooling, seed=B + 2, weighted=True, index_dtype=torch.int32)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("dims", [[8, 36, 64], [128, 4], [256, 512, 1024]])
+def test_grad_indice_weights(dev, pooling, dims):
+    """split_embedding_codegen_grad_indice_weights_cuda vs the oracle (fp64
+    dot product): rtol 1e-5 of sum_d |g_d * w_d|; masked tables exactly 0."""
+    print(f"[case] grad_indice_weights dims={dims} pool={pooling}", flush=True)
+    T = len(dims)
+    rng = np.random.default_rng(sum(dims) + pooling)
+    inp = random_tbe(rng, T, 70, dims, [300] * T, 25, empty_frac=0.1)
+    W = rng.uniform(-1, 1, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
+    grad = rng.normal(0, 1, size=(inp.B, inp.total_D)).astype(np.float32)
+    frg = (np.arange(T) % 2 == 0).astype(np.int32)
+    w_off = weight_offsets(inp)
+    exp = orc.grad_indice_weights(grad, W, w_off, inp.D_offsets, inp.B, inp.indices, inp.offsets,
+                                  pooling, frg)
+    mag = orc.grad_indice_weights(np.abs(grad), np.abs(W), w_off, inp.D_offsets, inp.B,
+                                  inp.indices, inp.offsets, pooling)
+    empty = torch.zeros(0, device=dev)
+    for idt, f in ((torch.int64, frg), (torch.int32, frg), (torch.int64, None)):
+        got = torch.ops.fbgemm.split_embedding_codegen_grad_indice_weights_cuda(
+            torch.from_numpy(grad).to(dev), torch.from_numpy(W).to(dev), empty, empty,
+            torch.zeros(T, dtype=torch.int32, device=dev), torch.from_numpy(w_off).to(dev),
+            torch.from_numpy(inp.D_offsets).to(dev), max(dims),
+            torch.from_numpy(inp.indices).to(dev, idt), torch.from_numpy(inp.offsets).to(dev, idt),
+            torch.zeros(0, dtype=torch.int32, device=dev),
+            None if f is None else torch.from_numpy(f).to(dev), pooling).cpu().numpy()
+        ref = exp if f is not None else orc.grad_indice_weights(
+            grad, W, w_off, inp.D_offsets, inp.B, inp.indices, inp.offsets, pooling)
+        assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-30), np.max(np.abs(got - ref) / mag)
+        if f is not None:
+            for t in np.flatnonzero(f == 0):
+                o = inp.offsets[t * inp.B], inp.offsets[(t + 1) * inp.B]
+                assert not got[o[0]:o[1]].any()
 
 
 @pytest.mark.parametrize("wd_mode,wd", [(1, 0.1), (2, 0.05)])
@@ -172,5 +231,49 @@ def test_module_training_step(dev):
         inp.total_hash_size_bits, inp.indices, inp.offsets, 1, gout.cpu().numpy(),
         np.zeros(800, np.float32), np.array([0, 500], np.int64), 0.05, 1e-6, 0.0, 0,
         orc.info_B_num_bits(2, 32))
+    np.testing.assert_allclose(tbe.weights_dev.detach().cpu().numpy(), W_exp, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_module_training_step_weighted(dev, pooling):
+    """Weighted training lookup through the module: forward bit-exact vs the
+    oracle, per-sample weight gradient (table 1 masked by
+    feature_requires_grad) and the fused weighted update vs the oracle."""
+    print(f"[case] module weighted training step pool={pooling}", flush=True)
+    from mx_fbgemm import ComputeDevice, EmbeddingLocation, PoolingMode
+    from mx_fbgemm.split_table_batched_embeddings_ops_training import (
+        SplitTableBatchedEmbeddingBagsCodegen,
+    )
+
+    specs = [(400, 32, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (200, 128, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (90, 256, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)]
+    tbe = SplitTableBatchedEmbeddingBagsCodegen(specs, pooling_mode=PoolingMode(pooling),
+                                                learning_rate=0.05, eps=1e-6, device=dev)
+    rng = np.random.default_rng(19)
+    inp = random_tbe(rng, 3, 24, [32, 128, 256], [400, 200, 90], 12, empty_frac=0.1)
+    iw = rng.uniform(0.1, 2.0, inp.N).astype(np.float32)
+    psw = torch.from_numpy(iw).to(dev).requires_grad_()
+    frg = torch.tensor([1, 0, 1], dtype=torch.int32, device=dev)
+    W0 = tbe.weights_dev.detach().cpu().numpy().copy()
+    out = tbe(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), psw,
+              frg)
+    exp = orc.tbe_forward_f32(W0, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, pooling, iw)
+    assert np.array_equal(out.detach().cpu().numpy(), exp)
+    gout_np = rng.normal(0, 1, size=out.shape).astype(np.float32)
+    out.backward(torch.from_numpy(gout_np).to(dev))
+    giw = orc.grad_indice_weights(gout_np, W0, weight_offsets(inp), inp.D_offsets, inp.B,
+                                  inp.indices, inp.offsets, pooling, frg.cpu().numpy())
+    mag = orc.grad_indice_weights(np.abs(gout_np), np.abs(W0), weight_offsets(inp),
+                                  inp.D_offsets, inp.B, inp.indices, inp.offsets, pooling)
+    got = psw.grad.cpu().numpy()
+    assert np.all(np.abs(got - giw) <= 1e-5 * mag + 1e-30)
+    W_exp, m_exp = orc.backward_rowwise_adagrad(
+        W0, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, gout_np,
+        np.zeros(690, np.float32), np.array([0, 400, 600], np.int64), 0.05, 1e-6, 0.0, 0,
+        orc.info_B_num_bits(3, 24), indice_weights=iw)
     np.testing.assert_allclose(tbe.weights_dev.detach().cpu().numpy(), W_exp, rtol=RTOL, atol=ATOL)
     np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)

@@ -131,3 +131,33 @@ def test_autograd(dev):
     (out * gout).sum().backward()
     _bits_equal(x.grad, gout.cpu().numpy())
     _bits_equal(y.grad, orc.jagged_to_padded_dense(gout.cpu().numpy(), [off], [4], 0.0))
+
+
+def test_autograd_two_jagged_dims(dev):
+    """Backward of the 2-level jagged ops: d(j2pd) = d2j of the upstream
+    gradient (truncated/padded positions get 0), d(d2j) = j2pd with pad 0."""
+    print("[case] jagged autograd, two jagged dims", flush=True)
+    rng = np.random.default_rng(6)
+    off0 = _offsets([2, 0, 3])
+    off1 = _offsets([1, 4, 0, 2, 3])
+    offs = [torch.from_numpy(off0).to(dev), torch.from_numpy(off1).to(dev)]
+    vals = torch.from_numpy(rng.standard_normal((10, 3)).astype(np.float32)).to(dev).requires_grad_()
+    dense = torch.ops.fbgemm.jagged_to_padded_dense(vals, offs, [2, 3], 0.0)
+    g = rng.standard_normal(tuple(dense.shape)).astype(np.float32)
+    (dense * torch.from_numpy(g).to(dev)).sum().backward()
+    _bits_equal(vals.grad, orc.dense_to_jagged(g, [off0, off1], total_L=10))
+    d = torch.from_numpy(rng.standard_normal((3, 2, 3, 3)).astype(np.float32)).to(dev).requires_grad_()
+    jv, _ = torch.ops.fbgemm.dense_to_jagged(d, offs)
+    gj = rng.standard_normal(tuple(jv.shape)).astype(np.float32)
+    (jv * torch.from_numpy(gj).to(dev)).sum().backward()
+    _bits_equal(d.grad, orc.jagged_to_padded_dense(gj, [off0, off1], [2, 3], 0.0))
+
+
+def test_jagged_to_padded_dense_backward_op(dev):
+    print("[case] jagged_to_padded_dense_backward op", flush=True)
+    rng = np.random.default_rng(8)
+    off = _offsets([3, 0, 6, 2])
+    g = rng.standard_normal((4, 4, 5)).astype(np.float32)
+    got = torch.ops.fbgemm.jagged_to_padded_dense_backward(
+        torch.from_numpy(g).to(dev), [torch.from_numpy(off).to(dev)], 11)
+    _bits_equal(got, orc.dense_to_jagged(g, [off], total_L=11))

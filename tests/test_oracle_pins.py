@@ -228,9 +228,24 @@ def test_transpose_vs_numpy(seed, T, B, rows, dup):
     assert got["run_lengths"].sum() == inp.N
 
 
+def _torch_bag(Wt, idx, starts, pooling, psw):
+    """torch autograd graph of one table's pooled lookup.  Weighted MEAN is
+    written as SUM with per-sample weights psw / L (torch's embedding_bag takes
+    per-sample weights under mode='sum' only), which has the same value and
+    derivatives as (sum_l psw_l W[i_l]) / L."""
+    if psw is None:
+        return torch.nn.functional.embedding_bag(idx, Wt, starts,
+                                                 mode="sum" if pooling == 0 else "mean")
+    if pooling == 1:
+        lens = torch.diff(torch.cat([starts, torch.tensor([idx.numel()])]))
+        psw = psw / torch.repeat_interleave(lens.to(psw.dtype), lens)
+    return torch.nn.functional.embedding_bag(idx, Wt, starts, mode="sum", per_sample_weights=psw)
+
+
 @pytest.mark.parametrize("pooling", [0, 1])
 @pytest.mark.parametrize("wd_mode,wd", [(0, 0.0), (1, 0.1), (2, 0.05)])
-def test_adagrad_vs_torch_autograd(pooling, wd_mode, wd):
+@pytest.mark.parametrize("weighted", [False, True])
+def test_adagrad_vs_torch_autograd(pooling, wd_mode, wd, weighted):
     rng = np.random.default_rng(21)
     dims, rows = [8, 16], [30, 20]
     inp = random_tbe(rng, 2, 12, dims, rows, 9, empty_frac=0.1)
@@ -238,19 +253,20 @@ def test_adagrad_vs_torch_autograd(pooling, wd_mode, wd):
     m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
     m1_off = np.array([0, rows[0]], np.int64)
     grad = rng.normal(0, 1, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(-1.5, 1.5, inp.N).astype(np.float32) if weighted else None
     lr, eps = 0.1, 1e-6
     W_new, m_new = orc.backward_rowwise_adagrad(
         W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
         inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
-        wd, wd_mode, orc.info_B_num_bits(2, inp.B))
+        wd, wd_mode, orc.info_B_num_bits(2, inp.B), indice_weights=iw)
     w_off = weight_offsets(inp)
     for t in range(2):
         E, D = rows[t], dims[t]
         Wt = torch.tensor(W[w_off[t]: w_off[t] + E * D].reshape(E, D), requires_grad=True)
         o = inp.offsets[t * inp.B:(t + 1) * inp.B + 1]
-        out = torch.nn.functional.embedding_bag(
-            torch.from_numpy(inp.indices[o[0]:o[-1]]), Wt, torch.from_numpy(o[:-1] - o[0]),
-            mode="sum" if pooling == 0 else "mean")
+        psw = None if iw is None else torch.from_numpy(iw[o[0]:o[-1]])
+        out = _torch_bag(Wt, torch.from_numpy(inp.indices[o[0]:o[-1]]),
+                         torch.from_numpy(o[:-1] - o[0]), pooling, psw)
         d0, d1 = inp.D_offsets[t], inp.D_offsets[t + 1]
         (out * torch.from_numpy(grad[:, d0:d1])).sum().backward()
         g = Wt.grad.detach()
@@ -284,6 +300,36 @@ def test_adagrad_zero_grad_changes_nothing():
                                           1e-8)
     np.testing.assert_array_equal(W2, W)
     np.testing.assert_array_equal(m2, m1)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_grad_indice_weights_vs_torch_autograd(pooling):
+    rng = np.random.default_rng(23)
+    dims, rows = [8, 36, 128], [40, 25, 30]
+    inp = random_tbe(rng, 3, 10, dims, rows, 11, empty_frac=0.1)
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    grad = rng.normal(0, 1, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(0.2, 2.0, inp.N).astype(np.float32)
+    w_off = weight_offsets(inp)
+    frg = np.array([1, 0, 1], np.int32)
+    got = orc.grad_indice_weights(grad, W, w_off, inp.D_offsets, inp.B, inp.indices,
+                                  inp.offsets, pooling, frg)
+    all_on = orc.grad_indice_weights(grad, W, w_off, inp.D_offsets, inp.B, inp.indices,
+                                     inp.offsets, pooling)
+    for t in range(3):
+        E, D = rows[t], dims[t]
+        Wt = torch.tensor(W[w_off[t]: w_off[t] + E * D].reshape(E, D))
+        o = inp.offsets[t * inp.B:(t + 1) * inp.B + 1]
+        psw = torch.tensor(iw[o[0]:o[-1]], requires_grad=True)
+        out = _torch_bag(Wt, torch.from_numpy(inp.indices[o[0]:o[-1]]),
+                         torch.from_numpy(o[:-1] - o[0]), pooling, psw)
+        d0, d1 = inp.D_offsets[t], inp.D_offsets[t + 1]
+        (out * torch.from_numpy(grad[:, d0:d1])).sum().backward()
+        np.testing.assert_allclose(all_on[o[0]:o[-1]], psw.grad.numpy(), rtol=1e-5, atol=1e-5)
+        if frg[t]:
+            np.testing.assert_array_equal(got[o[0]:o[-1]], all_on[o[0]:o[-1]])
+        else:
+            assert not got[o[0]:o[-1]].any()
 
 
 # ---- bounds_check_indices ---------------------------------------------------

@@ -426,13 +426,16 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   return {linear, sorted, infos, run, lengths, num_runs, cum};
 }
 
-Tensor backward_rowwise_adagrad_exact(
+// Shared body of the unweighted and weighted backward ops; `indice_weights`
+// undefined = unweighted.
+Tensor backward_rowwise_adagrad_impl(
     const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
     const Tensor& lxu_cache_weights, const Tensor& weights_placements,
     const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D_sym,
     const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
-    const Tensor& offsets, int64_t pooling_mode, const Tensor& lxu_cache_locations,
-    int64_t BT_block_size, int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
+    const Tensor& lxu_cache_locations, int64_t BT_block_size,
+    int64_t max_segment_length_per_warp, bool stochastic_rounding,
     const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
     const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
     int64_t weight_decay_mode, double max_norm) {
@@ -472,16 +475,114 @@ Tensor backward_rowwise_adagrad_exact(
                                       static_cast<int32_t>(max_D));
   Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, dev_weights.options().dtype(at::kByte));
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  Tensor iwc;
+  if (indice_weights.defined()) {
+    check_gpu(indice_weights, "indice_weights");
+    TORCH_CHECK(indice_weights.scalar_type() == at::kFloat, "indice_weights must be fp32");
+    TORCH_CHECK(indice_weights.numel() == N, "indice_weights has ", indice_weights.numel(),
+                " entries but there are ", N, " indices");
+    iwc = indice_weights.contiguous();
+  }
   MX_CALL(mx_tbe_backward_rowwise_adagrad(
       dev_weights.data_ptr<float>(), weights_offsets.data_ptr<int64_t>(),
       D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B, static_cast<int32_t>(max_D),
       hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(total_hash_size_bits),
       idx.data_ptr(), off.data_ptr(), ib, N, static_cast<int32_t>(pooling_mode),
-      g.data_ptr<float>(), g.size(1), momentum1_dev.data_ptr<float>(),
+      iwc.defined() ? iwc.data_ptr<float>() : nullptr, g.data_ptr<float>(), g.size(1),
+      momentum1_dev.data_ptr<float>(),
       momentum1_offsets.data_ptr<int64_t>(), static_cast<float>(learning_rate),
       static_cast<float>(eps), static_cast<float>(weight_decay),
       static_cast<int32_t>(weight_decay_mode), ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
   return at::empty({0}, dev_weights.options());
+}
+
+Tensor backward_rowwise_adagrad_exact(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& lxu_cache_locations,
+    int64_t BT_block_size, int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  return backward_rowwise_adagrad_impl(
+      grad_output, dev_weights, uvm_weights, lxu_cache_weights, weights_placements,
+      weights_offsets, D_offsets, std::move(max_D), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, Tensor(), lxu_cache_locations, BT_block_size,
+      max_segment_length_per_warp, stochastic_rounding, momentum1_dev, momentum1_uvm,
+      momentum1_placements, momentum1_offsets, eps, learning_rate, weight_decay,
+      weight_decay_mode, max_norm);
+}
+
+Tensor backward_rowwise_adagrad_weighted_exact(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
+    const Tensor& lxu_cache_locations, int64_t BT_block_size,
+    int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  TORCH_CHECK(indice_weights.defined(), "the weighted backward needs indice_weights");
+  return backward_rowwise_adagrad_impl(
+      grad_output, dev_weights, uvm_weights, lxu_cache_weights, weights_placements,
+      weights_offsets, D_offsets, std::move(max_D), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, indice_weights, lxu_cache_locations, BT_block_size,
+      max_segment_length_per_warp, stochastic_rounding, momentum1_dev, momentum1_uvm,
+      momentum1_placements, momentum1_offsets, eps, learning_rate, weight_decay,
+      weight_decay_mode, max_norm);
+}
+
+// Gradient of the per-sample weights of a weighted SUM/MEAN lookup (fp32 [N]):
+// grad_indice_weights[l] = <grad_output[b, D_t slice], W_t[indices[l]]>, times
+// 1/L under MEAN; 0 for tables whose feature_requires_grad entry is 0.
+Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
+                           const Tensor& uvm_weights, const Tensor& lxu_cache_weights,
+                           const Tensor& weights_placements, const Tensor& weights_offsets,
+                           const Tensor& D_offsets, c10::SymInt max_D_sym, const Tensor& indices,
+                           const Tensor& offsets, const Tensor& lxu_cache_locations,
+                           const std::optional<Tensor>& feature_requires_grad,
+                           int64_t pooling_mode) {
+  (void)lxu_cache_weights;
+  (void)weights_placements;
+  (void)lxu_cache_locations;
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  for (auto* t : {&grad_output, &weights_offsets, &D_offsets, &indices, &offsets})
+    check_gpu(*t, "grad_indice_weights argument");
+  TORCH_CHECK(uvm_weights.numel() == 0, "UVM storage is not supported (DEVICE placement only)");
+  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat && dev_weights.is_contiguous(),
+              "dev_weights must be contiguous fp32");
+  TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
+  TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
+  TORCH_CHECK(D_offsets.scalar_type() == at::kInt, "D_offsets must be int32");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = D_offsets.numel() - 1;
+  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  const Tensor g = grad_output.contiguous();
+  TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  Tensor frg;
+  if (feature_requires_grad.has_value() && feature_requires_grad->defined() &&
+      feature_requires_grad->numel() > 0) {
+    check_gpu(*feature_requires_grad, "feature_requires_grad");
+    TORCH_CHECK(feature_requires_grad->numel() == T, "feature_requires_grad must have T entries");
+    frg = feature_requires_grad->to(at::kInt).contiguous();
+  }
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  Tensor out = at::empty({indices.numel()}, dev_weights.options());
+  MX_CALL(mx_tbe_grad_indice_weights(
+      g.data_ptr<float>(), g.size(1), dev_weights.data_ptr<float>(),
+      weights_offsets.data_ptr<int64_t>(), D_offsets.data_ptr<int32_t>(),
+      static_cast<int32_t>(T), B, static_cast<int32_t>(max_D_sym.expect_int()), idx.data_ptr(),
+      off.data_ptr(), ib, static_cast<int32_t>(pooling_mode),
+      frg.defined() ? frg.data_ptr<int32_t>() : nullptr, out.data_ptr<float>(),
+      stream_of(dev_weights)));
+  return out;
 }
 
 class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagrad> {
@@ -492,6 +593,8 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
                         const Tensor& D_offsets, int64_t total_D, int64_t max_D,
                         const Tensor& hash_size_cumsum, int64_t total_hash_size_bits,
                         const Tensor& indices, const Tensor& offsets, int64_t pooling_mode,
+                        const std::optional<Tensor>& indice_weights,
+                        const std::optional<Tensor>& feature_requires_grad,
                         const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
                         const Tensor& momentum1_placements, const Tensor& momentum1_offsets,
                         double eps, double learning_rate, double weight_decay,
@@ -507,6 +610,10 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     s["hash_size_cumsum"] = hash_size_cumsum;
     s["indices"] = indices;
     s["offsets"] = offsets;
+    // Optional (not plain Tensor) arguments: an absent one is no autograd input.
+    s["indice_weights"] = indice_weights.has_value() ? *indice_weights : Tensor();
+    s["feature_requires_grad"] =
+        feature_requires_grad.has_value() ? *feature_requires_grad : Tensor();
     s["momentum1_dev"] = momentum1_dev;
     s["momentum1_uvm"] = momentum1_uvm;
     s["momentum1_placements"] = momentum1_placements;
@@ -521,9 +628,16 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     s["max_norm"] = max_norm;
     at::AutoDispatchBelowADInplaceOrView g;
     return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
-                       total_D, max_D, indices, offsets, pooling_mode, std::nullopt,
+                       total_D, max_D, indices, offsets, pooling_mode, indice_weights,
                        output_dtype);
   }
+
+  // indice_weights is argument 13 of forward() (after ctx) and, when present,
+  // the 10th Tensor argument, i.e. autograd edge 9; backward returns one slot
+  // per argument.
+  static constexpr size_t kIndiceWeightsArg = 13;
+  static constexpr size_t kIndiceWeightsEdge = 9;
+  static constexpr size_t kNumInputs = 25;
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     auto& s = ctx->saved_data;
@@ -531,17 +645,31 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     TORCH_CHECK(grad.scalar_type() == at::kFloat,
                 "the rowwise-Adagrad backward needs an fp32 gradient (output_dtype FP32)");
     const Tensor empty;
-    backward_rowwise_adagrad_exact(
-        grad.contiguous(), s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
+    const Tensor g = grad.contiguous();
+    const Tensor iw = s["indice_weights"].toTensor();
+    variable_list out(kNumInputs);
+    // The weight gradient reads the rows before the fused update below
+    // overwrites them (same stream, so ordered).
+    if (iw.defined() && ctx->needs_input_grad(kIndiceWeightsEdge)) {
+      const Tensor frg = s["feature_requires_grad"].toTensor();
+      out[kIndiceWeightsArg] = grad_indice_weights(
+          g, s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
+          s["weights_placements"].toTensor(), s["weights_offsets"].toTensor(),
+          s["D_offsets"].toTensor(), c10::SymInt(s["max_D"].toInt()), s["indices"].toTensor(),
+          s["offsets"].toTensor(), empty,
+          frg.defined() ? std::optional<Tensor>(frg) : std::nullopt, s["pooling_mode"].toInt());
+    }
+    backward_rowwise_adagrad_impl(
+        g, s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
         s["weights_placements"].toTensor(), s["weights_offsets"].toTensor(),
         s["D_offsets"].toTensor(), c10::SymInt(s["max_D"].toInt()),
         s["hash_size_cumsum"].toTensor(), s["total_hash_size_bits"].toInt(),
-        s["indices"].toTensor(), s["offsets"].toTensor(), s["pooling_mode"].toInt(), empty, 0, 0,
-        false, s["momentum1_dev"].toTensor(), s["momentum1_uvm"].toTensor(),
+        s["indices"].toTensor(), s["offsets"].toTensor(), s["pooling_mode"].toInt(), iw, empty,
+        0, 0, false, s["momentum1_dev"].toTensor(), s["momentum1_uvm"].toTensor(),
         s["momentum1_placements"].toTensor(), s["momentum1_offsets"].toTensor(),
         s["eps"].toDouble(), s["learning_rate"].toDouble(), s["weight_decay"].toDouble(),
         s["weight_decay_mode"].toInt(), s["max_norm"].toDouble());
-    return variable_list(23);
+    return out;
   }
 };
 
@@ -558,16 +686,14 @@ Tensor lookup_rowwise_adagrad(
     double learning_rate, double weight_decay, int64_t weight_decay_mode, double max_norm,
     int64_t output_dtype) {
   (void)lxu_cache_weights;
-  (void)feature_requires_grad;
   (void)lxu_cache_locations;
   (void)stochastic_rounding;
-  TORCH_CHECK(!(indice_weights.has_value() && indice_weights->defined()),
-              "weighted training lookup is not supported; use the weighted forward op");
   TORCH_CHECK(!gradient_clipping || max_gradient <= 0.0, "gradient clipping is not supported");
   return LookupRowwiseAdagrad::apply(
       placeholder_autograd_tensor, dev_weights, uvm_weights, weights_placements, weights_offsets,
       D_offsets, total_D.expect_int(), max_D.expect_int(), hash_size_cumsum, total_hash_size_bits,
-      indices, offsets, pooling_mode, momentum1_dev, momentum1_uvm, momentum1_placements,
+      indices, offsets, pooling_mode, indice_weights, feature_requires_grad, momentum1_dev,
+      momentum1_uvm, momentum1_placements,
       momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm,
       output_dtype);
 }
@@ -832,6 +958,21 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "Tensor(b!) momentum1_dev, Tensor momentum1_uvm, Tensor momentum1_placements, "
         "Tensor momentum1_offsets, float eps=0, float learning_rate=0, float weight_decay=0.0, "
         "int weight_decay_mode=0, float max_norm=0.0) -> Tensor");
+  m.def("split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda("
+        "Tensor grad_output, Tensor(a!) dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt max_D, Tensor hash_size_cumsum, int total_hash_size_bits, "
+        "Tensor indices, Tensor offsets, int pooling_mode, Tensor indice_weights, "
+        "Tensor lxu_cache_locations, int BT_block_size, int max_segment_length_per_warp, "
+        "bool stochastic_rounding, Tensor(b!) momentum1_dev, Tensor momentum1_uvm, "
+        "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
+        "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
+        "float max_norm=0.0) -> Tensor");
+  m.def("split_embedding_codegen_grad_indice_weights_cuda(Tensor grad_output, "
+        "Tensor dev_weights, Tensor uvm_weights, Tensor lxu_cache_weights, "
+        "Tensor weights_placements, Tensor weights_offsets, Tensor D_offsets, SymInt max_D, "
+        "Tensor indices, Tensor offsets, Tensor lxu_cache_locations, "
+        "Tensor? feature_requires_grad, int pooling_mode=0) -> Tensor");
   m.def("split_embedding_codegen_lookup_rowwise_adagrad_function(Tensor placeholder_autograd_tensor, "
         "Tensor dev_weights, Tensor uvm_weights, Tensor lxu_cache_weights, "
         "Tensor weights_placements, Tensor weights_offsets, Tensor D_offsets, SymInt total_D, "
@@ -879,6 +1020,10 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
          TORCH_FN(mx_ops::backward_rowwise_adagrad_exact));
   m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",
          TORCH_FN(mx_ops::lookup_rowwise_adagrad));
+  m.impl("split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda",
+         TORCH_FN(mx_ops::backward_rowwise_adagrad_weighted_exact));
+  m.impl("split_embedding_codegen_grad_indice_weights_cuda",
+         TORCH_FN(mx_ops::grad_indice_weights));
   m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
   m.impl("bounds_check_indices", TORCH_FN(mx_ops::bounds_check_indices));
   m.impl("FloatToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_to_8bit));

@@ -45,7 +45,8 @@ __global__ void __launch_bounds__(256)
     linearize_kernel(const int64_t* __restrict__ hsc, const I* __restrict__ indices,
                      const I* __restrict__ offsets, int64_t nbags, int64_t B, int32_t nb,
                      int64_t N, int64_t* __restrict__ linear_out, uint32_t* __restrict__ keys,
-                     uint32_t* __restrict__ vals) {
+                     uint32_t* __restrict__ vals, const float* __restrict__ iw,
+                     uint32_t* __restrict__ vals2) {
   const int64_t l = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (l >= N) return;
   // Bag owning position l: last bag with offsets[bag] <= l.
@@ -63,6 +64,7 @@ __global__ void __launch_bounds__(256)
   if (linear_out) linear_out[l] = key;
   keys[l] = static_cast<uint32_t>(key);
   vals[l] = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+  if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
 }
 
 // ---- radix sort -----------------------------------------------------------
@@ -99,7 +101,8 @@ __global__ void __launch_bounds__(256)
     radix_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
                          int64_t n, int shift, int nbits, const uint32_t* __restrict__ hist_scan,
                          int64_t ntiles, uint32_t* __restrict__ keys_out,
-                         int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out) {
+                         int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
+                         const uint32_t* __restrict__ vals2, uint32_t* __restrict__ vals2_out) {
   __shared__ uint32_t base[4][kRadix];
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -115,6 +118,7 @@ __global__ void __launch_bounds__(256)
     const bool valid = i < n;
     const uint32_t k = valid ? keys[i] : 0u;
     const uint32_t v = valid ? vals[i] : 0u;
+    const uint32_t v2 = (valid && vals2) ? vals2[i] : 0u;
     const uint32_t d = (k >> shift) & mask;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < nbits; ++bit) {
@@ -130,6 +134,7 @@ __global__ void __launch_bounds__(256)
       else
         keys_out[pos] = k;
       vals_out[pos] = v;
+      if (vals2) vals2_out[pos] = v2;
     }
     // The lowest lane of each digit group advances that digit's cursor after
     // every lane of the wave has read it above (LDS ops of a wave are ordered).
@@ -139,11 +144,14 @@ __global__ void __launch_bounds__(256)
 
 __global__ void copy_keys_kernel(const uint32_t* __restrict__ keys,
                                  const uint32_t* __restrict__ vals, int64_t n,
-                                 int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out) {
+                                 int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
+                                 const uint32_t* __restrict__ vals2,
+                                 uint32_t* __restrict__ vals2_out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   keys_out64[i] = keys[i];
   vals_out[i] = vals[i];
+  if (vals2) vals2_out[i] = vals2[i];
 }
 
 // Clears up to two int32 scalars (a kernel, not a memset, so the call can be
@@ -217,6 +225,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 struct SortWs {
   uint32_t* keys[2];
   uint32_t* vals[2];
+  uint32_t* vals2[2];  // per-sample weights (weighted backward only)
   uint32_t* hist;
   unsigned long long* scan_state;  // kScanSlots slots of (tiles + 1) zeroed words
   int64_t scan_slot_words;
@@ -240,6 +249,7 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   for (int i = 0; i < 2; ++i) {
     w.keys[i] = reinterpret_cast<uint32_t*>(take(n * 4));
     w.vals[i] = reinterpret_cast<uint32_t*>(take(n * 4));
+    w.vals2[i] = reinterpret_cast<uint32_t*>(take(n * 4));
   }
   w.hist = reinterpret_cast<uint32_t*>(take(hist_n * 4));
   w.scan_state = reinterpret_cast<unsigned long long*>(take(kScanSlots * slot_words * 8));
@@ -264,11 +274,15 @@ struct TransposeOut {
   int32_t* run_lengths; // [N]
   int32_t* num_runs;    // [1]
   int32_t* cum;         // [N+1]
+  float* weights_sorted;  // [N] per-sample weights in sorted order, or null
 };
 
 int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_t nb,
                   const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
-                  const TransposeOut& o, SortWs& w, hipStream_t s) {
+                  const float* iw, const TransposeOut& o, SortWs& w, hipStream_t s) {
+  // With per-sample weights the weights travel with the keys as a second payload.
+  uint32_t* const v2[2] = {iw ? w.vals2[0] : nullptr, iw ? w.vals2[1] : nullptr};
+  uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
   const int64_t nbags = static_cast<int64_t>(T) * B;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
   {  // every scan's look-back state starts at zero (a kernel, not a memset)
@@ -281,11 +295,11 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   if (index_bytes == 8)
     linearize_kernel<int64_t><<<g256, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
-        nb, N, o.linear, w.keys[0], w.vals[0]);
+        nb, N, o.linear, w.keys[0], w.vals[0], iw, v2[0]);
   else
     linearize_kernel<int32_t><<<g256, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
-        nb, N, o.linear, w.keys[0], w.vals[0]);
+        nb, N, o.linear, w.keys[0], w.vals[0], iw, v2[0]);
   MX_LAUNCH_CHECK();
 
   const int64_t ntiles = ceil_div(N, kSortTile);
@@ -294,7 +308,7 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   int cur = 0;
   if (passes == 0) {
     copy_keys_kernel<<<g256, 256, 0, s>>>(w.keys[0], w.vals[0], N, o.sorted,
-                                          reinterpret_cast<uint32_t*>(o.infos));
+                                          reinterpret_cast<uint32_t*>(o.infos), v2[0], v2_final);
     MX_LAUNCH_CHECK();
   }
   for (int p = 0; p < passes; ++p) {
@@ -309,11 +323,11 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
     if (last) {
       radix_scatter_kernel<true><<<gsort, 256, 0, s>>>(
           w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, nullptr, o.sorted,
-          reinterpret_cast<uint32_t*>(o.infos));
+          reinterpret_cast<uint32_t*>(o.infos), v2[cur], v2_final);
     } else {
       radix_scatter_kernel<false><<<gsort, 256, 0, s>>>(
           w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, w.keys[cur ^ 1], nullptr,
-          w.vals[cur ^ 1]);
+          w.vals[cur ^ 1], v2[cur], v2[cur ^ 1]);
     }
     MX_LAUNCH_CHECK();
     cur ^= 1;
@@ -346,6 +360,7 @@ struct BwdArgs {
   const int64_t* run;
   const int32_t* cum;
   const int32_t* infos;
+  const float* iw_sorted;  // per-sample weights in sorted order, or null
   const uint32_t* num_runs;
   const uint32_t* chunk_start;
   const uint32_t* chunk_run;
@@ -424,7 +439,8 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
   for (int64_t base = s0; base < s1; base += G) {
     const int n = static_cast<int>(s1 - base < G ? s1 - base : G);
     int32_t my_b = 0;
-    float my_s = 1.0f;
+    float my_s = 1.0f;  // MEAN: 1/L of the occurrence's bag
+    float my_w = 1.0f;  // weighted: the occurrence's per-sample weight
     if (k < n) {
       const int32_t info = base == s0 ? info0 : a.infos[base + k];
       my_b = static_cast<int32_t>(static_cast<uint32_t>(info) & bmask);
@@ -434,7 +450,9 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
         const int64_t L = static_cast<int64_t>(off[bag + 1]) - static_cast<int64_t>(off[bag]);
         my_s = L > 0 ? 1.0f / static_cast<float>(L) : 0.0f;
       }
+      if (a.iw_sorted) my_w = a.iw_sorted[base + k];
     }
+    const bool mean = a.pooling == MX_POOL_MEAN, weighted = a.iw_sorted != nullptr;
     for (int j = 0; j < n; j += U) {
       float v[U][NCH][4];
 #pragma unroll
@@ -451,12 +469,17 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
           const float sc = __shfl(my_s, g * G + j + u, 64);
+          const float wt = __shfl(my_w, g * G + j + u, 64);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
             if ((c * G + k) * 4 < D) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e)
-                acc[c][e] += a.pooling == MX_POOL_MEAN ? __fmul_rn(v[u][c][e], sc) : v[u][c][e];
+              for (int e = 0; e < 4; ++e) {
+                float x = v[u][c][e];
+                if (mean) x = __fmul_rn(x, sc);
+                if (weighted) x = __fmul_rn(x, wt);
+                acc[c][e] += x;
+              }
             }
         }
       }
@@ -690,6 +713,7 @@ struct BwdWs {
   int32_t* cum;
   uint32_t* chunk_start;
   uint32_t* chunk_run;
+  float* weights_sorted;
   float* partial;
   size_t bytes;
 };
@@ -714,6 +738,7 @@ BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   w.cum = reinterpret_cast<int32_t*>(take((n + 1) * 4));
   w.chunk_start = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
   w.chunk_run = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(max_chunks(n)) * 4));
+  w.weights_sorted = reinterpret_cast<float*>(take(n * 4));
   w.partial = reinterpret_cast<float*>(take(static_cast<size_t>(max_chunks(n)) * max_D * 4));
   w.bytes = off;
   return w;
@@ -775,9 +800,9 @@ extern "C" int mx_tbe_transpose_embedding_input(
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   TransposeOut o{linear_indices, sorted_linear_indices, infos_sorted, sorted_linear_indices_run,
-                 run_lengths, num_runs, cumulative_run_lengths};
+                 run_lengths, num_runs, cumulative_run_lengths, nullptr};
   return run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, info_B_num_bits, indices,
-                       offsets, index_bytes, N, o, w, s);
+                       offsets, index_bytes, N, nullptr, o, w, s);
 }
 
 extern "C" size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits,
@@ -790,9 +815,10 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
     float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
     int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
-    int32_t pooling_mode, const float* grad_output, int64_t total_D, float* momentum1,
-    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
-    int32_t weight_decay_mode, void* workspace, size_t workspace_bytes, void* stream) {
+    int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
+    float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
+    float weight_decay, int32_t weight_decay_mode, void* workspace, size_t workspace_bytes,
+    void* stream) {
   clear_error();
   const int32_t nb = mx_tbe_info_B_num_bits(T, B);
   MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
@@ -811,9 +837,10 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   auto* s = as_stream(stream);
-  TransposeOut o{nullptr, w.sorted, w.infos, w.run, w.run_lengths, w.num_runs, w.cum};
+  TransposeOut o{nullptr, w.sorted, w.infos, w.run, w.run_lengths, w.num_runs, w.cum,
+                 indice_weights ? w.weights_sorted : nullptr};
   if (int rc = run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, nb, indices, offsets,
-                             index_bytes, N, o, w.sort, s))
+                             index_bytes, N, indice_weights, o, w.sort, s))
     return rc;
   // Chunk layout of long runs.
   if (int rc = exclusive_scan(ChunkCount{w.cum}, N, w.num_runs, w.chunk_start,
@@ -834,6 +861,7 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   a.run = w.run;
   a.cum = w.cum;
   a.infos = w.infos;
+  a.iw_sorted = indice_weights ? w.weights_sorted : nullptr;
   a.num_runs = &w.sort.counters[0];
   a.chunk_start = w.chunk_start;
   a.chunk_run = w.chunk_run;

@@ -149,6 +149,81 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Gradient of the per-sample weights of a weighted lookup:
+//   grad_iw[l] = sum_d grad_output[b, D_off[t] + d] * W_t[idx[l], d]
+// (MEAN: times 1/L), 0 for tables whose feature_requires_grad entry is 0.
+// Same G-lane-per-bag mapping as the forward; the bag's gradient slice stays
+// in registers, each row's dot product is reduced over the group in a fixed
+// xor-tree order.
+template <typename I, int G, int NCH, int U>
+__global__ void __launch_bounds__(256)
+    grad_indice_weights_kernel(const float* __restrict__ grad, int64_t total_D,
+                               const float* __restrict__ W, const int64_t* __restrict__ w_off,
+                               const int32_t* __restrict__ D_off, int64_t B,
+                               const I* __restrict__ indices, const I* __restrict__ offsets,
+                               int32_t pooling, const int32_t* __restrict__ frg,
+                               float* __restrict__ out, int64_t nbags) {
+  constexpr int P = 64 / G;
+  const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
+  const int64_t bag = (lb * kWavesPerBlock + (threadIdx.x >> 6)) * P + g;
+  if (bag >= nbags) return;  // whole group
+  const int64_t t = bag / B;
+  const int64_t b = bag - t * B;
+  const int64_t start = static_cast<int64_t>(offsets[bag]);
+  const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
+  if (frg != nullptr && frg[t] == 0) {
+    for (int64_t l = start + k; l < end; l += G) out[l] = 0.0f;
+    return;
+  }
+  const int32_t D0 = D_off[t];
+  const int32_t D = D_off[t + 1] - D0;
+  const float* __restrict__ Wt = W + w_off[t];
+  bool active[NCH];
+  float gv[NCH][4];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    active[c] = (c * G + k) * 4 < D;
+    if (active[c])
+      load_vec<4>(grad + b * total_D + D0 + (c * G + k) * 4, gv[c]);
+    else
+      gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 0.0f;
+  }
+  const int64_t L = end - start;
+  const float inv = (pooling == MX_POOL_MEAN && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;
+  for (int64_t base = start; base < end; base += G) {
+    const int n = static_cast<int>(end - base < G ? end - base : G);
+    const int64_t my_idx = k < n ? static_cast<int64_t>(indices[base + k]) : 0;
+    for (int j = 0; j < n; j += U) {
+      float v[U][NCH][4];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          const int64_t r = __shfl(my_idx, g * G + j + u, 64);
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if (active[c]) load_vec<4>(Wt + r * D + (c * G + k) * 4, v[u][c]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u < n) {
+          float dot = 0.0f;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+            if (active[c])
+#pragma unroll
+              for (int e = 0; e < 4; ++e) dot = __builtin_fmaf(gv[c][e], v[u][c][e], dot);
+#pragma unroll
+          for (int m = G / 2; m >= 1; m >>= 1) dot += __shfl_xor(dot, m, 64);
+          if (k == 0) out[base + j + u] = pooling == MX_POOL_MEAN ? __fmul_rn(dot, inv) : dot;
+        }
+      }
+    }
+  }
+}
+
 template <typename I, int G, int NCH, bool WEIGHTED, bool OUT_F16>
 void launch_fwd_group(hipStream_t s, const float* W, const int64_t* w_off, const int32_t* D_off,
                       int64_t B, const void* idx, const void* off, int32_t pooling,
@@ -217,6 +292,55 @@ extern "C" int mx_tbe_forward(const float* weights, const int64_t* weights_offse
     else h ? dispatch_fwd<int32_t, false, true>(MX_ARGS) : dispatch_fwd<int32_t, false, false>(MX_ARGS);
   }
 #undef MX_ARGS
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D,
+                                          const float* weights, const int64_t* weights_offsets,
+                                          const int32_t* D_offsets, int32_t T, int64_t B,
+                                          int32_t max_D, const void* indices, const void* offsets,
+                                          int32_t index_bytes, int32_t pooling_mode,
+                                          const int32_t* feature_requires_grad,
+                                          float* grad_indice_weights, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+  MX_REQUIRE(max_D >= 0 && max_D <= 1024 && max_D % 4 == 0,
+             "max_D %d must be a multiple of 4 in [0, 1024]", max_D);
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
+             "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
+  const int64_t nbags = static_cast<int64_t>(T) * B;
+  if (nbags == 0) return MX_OK;
+  MX_REQUIRE(grad_output && weights && weights_offsets && D_offsets && offsets &&
+                 grad_indice_weights,
+             "null pointer argument");
+  auto* s = as_stream(stream);
+#define MX_GIW(I, G, NCH, U)                                                                   \
+  grad_indice_weights_kernel<I, G, NCH, U><<<dim3(static_cast<uint32_t>(                      \
+                                               ceil_div(nbags, kWavesPerBlock * (64 / G)))),   \
+                                           256, 0, s>>>(                                      \
+      grad_output, total_D, weights, weights_offsets, D_offsets, B,                            \
+      static_cast<const I*>(indices), static_cast<const I*>(offsets), pooling_mode,            \
+      feature_requires_grad, grad_indice_weights, nbags)
+#define MX_GIW_D(I)                 \
+  if (max_D <= 64)                  \
+    MX_GIW(I, 16, 1, 8);            \
+  else if (max_D <= 128)            \
+    MX_GIW(I, 32, 1, 8);            \
+  else if (max_D <= 256)            \
+    MX_GIW(I, 64, 1, 8);            \
+  else if (max_D <= 512)            \
+    MX_GIW(I, 64, 2, 4);            \
+  else                              \
+    MX_GIW(I, 64, 4, 2);
+  if (index_bytes == 8) {
+    MX_GIW_D(int64_t)
+  } else {
+    MX_GIW_D(int32_t)
+  }
+#undef MX_GIW_D
+#undef MX_GIW
   MX_LAUNCH_CHECK();
   return MX_OK;
 }

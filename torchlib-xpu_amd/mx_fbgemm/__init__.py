@@ -39,6 +39,8 @@ OPS = (
     "get_infos_metadata",
     "transpose_embedding_input",
     "split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
+    "split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda",
+    "split_embedding_codegen_grad_indice_weights_cuda",
     "split_embedding_codegen_lookup_rowwise_adagrad_function",
     "int_nbit_split_embedding_codegen_lookup_function",
     "bounds_check_indices",

@@ -45,6 +45,10 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     Indices and offsets are first validated, and repaired in place, by
     ``torch.ops.fbgemm.bounds_check_indices`` (BoundsCheckMode.WARNING by
     default, as upstream); the count accumulates in ``bounds_check_warning``.
+    ``per_sample_weights`` (fp32, one per index) make it a weighted lookup:
+    each row is scaled by its weight before pooling, the fused update uses the
+    weighted row gradient, and the weights themselves receive a gradient when
+    they require one (``feature_requires_grad`` [T] masks tables out).
     """
 
     def __init__(
@@ -127,9 +131,13 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self._dims = dims
 
     def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
-                per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
+                per_sample_weights: Optional[torch.Tensor] = None,
+                feature_requires_grad: Optional[torch.Tensor] = None) -> torch.Tensor:
         if per_sample_weights is not None:
-            raise ValueError("per_sample_weights are not supported by the training lookup")
+            if per_sample_weights.dtype != torch.float32:
+                raise ValueError("per_sample_weights must be fp32")
+            if per_sample_weights.numel() != indices.numel():
+                raise ValueError("per_sample_weights must have one entry per index")
         if (offsets.numel() - 1) % self.T:
             raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
         if indices.dtype != offsets.dtype:
@@ -137,12 +145,13 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         if self.bounds_check_mode != BoundsCheckMode.NONE:
             torch.ops.fbgemm.bounds_check_indices(self.rows_per_table, indices, offsets,
                                                   int(self.bounds_check_mode),
-                                                  self.bounds_check_warning)
+                                                  self.bounds_check_warning, per_sample_weights)
         return torch.ops.fbgemm.split_embedding_codegen_lookup_rowwise_adagrad_function(
             self.placeholder_autograd_tensor, self.weights_dev, self.weights_uvm,
             self.lxu_cache_weights, self.weights_placements, self.weights_offsets,
             self.D_offsets, self.total_D, self.max_D, self.hash_size_cumsum,
-            self.total_hash_size_bits, indices, offsets, int(self.pooling_mode), None, None,
+            self.total_hash_size_bits, indices, offsets, int(self.pooling_mode),
+            per_sample_weights, feature_requires_grad,
             self.lxu_cache_locations, False, 0.0, False, self.momentum1_dev, self.momentum1_uvm,
             self.weights_placements, self.momentum1_offsets, self.eps, self.learning_rate,
             self.weight_decay, self.weight_decay_mode, 0.0, int(SparseType.FP32.as_int()))
