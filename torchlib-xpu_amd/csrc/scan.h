@@ -81,16 +81,33 @@ constexpr unsigned long long kScanFlagAgg = 1ull << 62;
 constexpr unsigned long long kScanFlagIncl = 2ull << 62;
 constexpr int kScanSpinLimit = 1 << 22;
 
-// INCL = false: out[i] = op(f(0..i-1)) (identity at 0); true: op(f(0..i)).
-template <class F, class Op, bool INCL>
+// Default epilogue: out[i] = scanned value; *total_out = whole aggregate.
+struct StoreOut {
+  uint32_t* out;
+  uint32_t* total_out;
+  __device__ void operator()(int64_t i, uint32_t v) const { out[i] = v; }
+  __device__ void total(uint32_t t) const {
+    if (total_out) *total_out = t;
+  }
+};
+
+// INCL = false: epi(i, op(f(0..i-1))) (identity at 0); true: epi(i, op(f(0..i))).
+// epi.total(aggregate) runs once, in the last tile.
+template <class F, class Op, bool INCL, class Epi>
 __global__ void __launch_bounds__(kScanThreads)
-    scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total_out,
-                        ScanState st, int64_t ntiles) {
+    scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
+                        int64_t ntiles) {
+  (void)ntiles;
   __shared__ uint32_t s_tile, s_prefix;
   if (threadIdx.x == 0) s_tile = atomicAdd(st.ticket, 1u);
   __syncthreads();
   const int64_t tile = s_tile;
   const int64_t m = eff_len(n, n_dev);
+  // Tiles past the effective length hold only identities: they return at once
+  // (later tiles are past it too, so nobody looks back at them) and the tile
+  // holding element m-1 (tile 0 when m == 0) reports the total.
+  const int64_t last = m > 0 ? (m - 1) / kScanTile : 0;
+  if (tile > last) return;  // block-uniform
   const int64_t base = tile * kScanTile + threadIdx.x * kScanItems;
   uint32_t v[kScanItems];
   uint32_t agg = Op::identity();
@@ -145,7 +162,7 @@ __global__ void __launch_bounds__(kScanThreads)
     }
     if (lane == 0) {
       s_prefix = prefix;
-      if (tile == ntiles - 1 && total_out) *total_out = Op::apply(prefix, tile_total);
+      if (tile == last) epi.total(Op::apply(prefix, tile_total));
     }
   }
   __syncthreads();
@@ -154,22 +171,28 @@ __global__ void __launch_bounds__(kScanThreads)
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
     if constexpr (INCL) run = Op::apply(run, v[it]);
-    if (i < m) out[i] = run;
+    if (i < m) epi(i, run);
     if constexpr (!INCL) run = Op::apply(run, v[it]);
   }
 }
 
 // Prefix scan of f over [0, effective length); *total = the whole aggregate.
 // `st` must have scan_tiles(n) zeroed status words and a zeroed ticket.
+template <class F, class Op = SumOp, bool INCL = false, class Epi = StoreOut>
+int prefix_scan_epi(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
+                    hipStream_t s) {
+  const int64_t nt = scan_tiles(n);
+  if (nt > 0x7fffffffll) return set_error(MX_EINVAL, "scan too long");
+  scan_onepass_kernel<F, Op, INCL, Epi><<<dim3(static_cast<uint32_t>(nt)), kScanThreads, 0, s>>>(
+      f, n, n_dev, epi, st, nt);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
 template <class F, class Op = SumOp, bool INCL = false>
 int prefix_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
                 ScanState st, hipStream_t s) {
-  const int64_t nt = scan_tiles(n);
-  if (nt > 0x7fffffffll) return set_error(MX_EINVAL, "scan too long");
-  scan_onepass_kernel<F, Op, INCL><<<dim3(static_cast<uint32_t>(nt)), kScanThreads, 0, s>>>(
-      f, n, n_dev, out, total, st, nt);
-  MX_LAUNCH_CHECK();
-  return MX_OK;
+  return prefix_scan_epi<F, Op, INCL, StoreOut>(f, n, n_dev, StoreOut{out, total}, st, s);
 }
 
 // out[i] = sum_{j<i} f(j); *total = sum of all.

@@ -11,16 +11,24 @@
 //
 // Design:
 //  * Keys fit 32 bits whenever total_hash_size_bits <= 32, so the sort moves
-//    (u32 key, u32 info) pairs: ceil(bits/8) passes of 8-bit digits.  A pass
-//    is histogram -> one device-wide exclusive scan (digit-major) ->
-//    scatter.  The unit of work is one wave and a 1024-key tile; inside a
-//    tile keys are ranked 64 at a time with 8 ballots (peer mask of equal
-//    digits), so the scatter is stable without block barriers.
-//  * Run-length encoding is a head-flag scan.
-//  * Each run (one distinct (t, i)) is reduced by one wave, lanes owning
-//    columns, occurrences added in sorted order.  Runs longer than kLong are
-//    cut into kChunk-occurrence chunks reduced in parallel into a workspace,
-//    then summed in chunk order by the run's wave.  No atomics: results are
+//    (u32 key, u32 info) pairs: ceil(bits/8) LSD passes of 8-bit digits.
+//  * linearize: a block takes 4096 consecutive positions, finds the bag range
+//    they span with two cooperative 128-ary searches, lets every non-empty
+//    bag mark its first position in LDS and gives each position the latest
+//    mark (a max-scan), so no per-position search.  The same kernel
+//    accumulates the global digit histograms of every pass (LDS, then one
+//    atomic per bin and block).
+//  * One launch per pass ("onesweep"): a block ranks a 2048-key tile (each
+//    wave 512 keys, 64 at a time, stable ranks from 8 ballots), then thread d
+//    finds how many keys of digit d earlier tiles hold through a decoupled
+//    look-back over per-(tile, digit) status words, and the tile scatters.
+//    Tiles take tickets in launch order, so every wait ends.
+//  * Run-length encoding is a head-flag scan whose epilogue writes the run
+//    keys and offsets.
+//  * Each run (one distinct (t, i)) is reduced by one G-lane group, lanes
+//    owning columns, occurrences added in sorted order.  Runs longer than
+//    kLong are cut into kChunk-occurrence chunks reduced in parallel into a
+//    workspace, then summed in chunk order.  No atomics on data: results are
 //    deterministic.
 #include "mx_common.h"
 #include "scan.h"
@@ -31,114 +39,290 @@ namespace {
 
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
-constexpr int kSortItems = 16;
-constexpr int64_t kSortTile = 64 * kSortItems;  // keys per wave-tile
-constexpr int kLong = 32;                       // runs longer than this are chunked
-constexpr int kChunk = 32;                      // occurrences per chunk
-// Scans per backward: one per radix pass (at most 4), run heads, chunk layout.
-constexpr int kScanSlots = 6;
+constexpr int kMaxPasses = 4;
+constexpr int kSweepItems = 8;                        // keys per lane per pass
+constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;  // 512 keys per wave
+constexpr int64_t kSweepTile = 4 * kSweepWaveKeys;    // 2048 keys per block
+constexpr int kLinItems = 16;
+constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
+constexpr int kLong = 32;                             // runs longer than this are chunked
+constexpr int kChunk = 32;                            // occurrences per chunk
+// One-pass scans per backward: run heads, chunk layout.
+constexpr int kScanSlots = 2;
+// Upper bound of the chunk count: sum over runs longer than kLong of
+// ceil(len / kChunk) <= N / kChunk + (number of such runs).
+int64_t max_chunks(int64_t N) { return N / kChunk + N / (kLong + 1) + 2; }
+
+__device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
+  const int nb = bits - p * kRadixBits;
+  return nb >= kRadixBits ? (kRadix - 1u) : ((1u << nb) - 1u);
+}
 
 // ---- linearize ------------------------------------------------------------
+
+// A block takes kLinTile consecutive positions; wave w owns positions
+// [w * kLinTile / 4, (w + 1) * kLinTile / 4), 64 consecutive ones per item.
+constexpr int kLinWavePos = kLinTile / 4;
 
 template <typename I>
 __global__ void __launch_bounds__(256)
     linearize_kernel(const int64_t* __restrict__ hsc, const I* __restrict__ indices,
                      const I* __restrict__ offsets, int64_t nbags, int64_t B, int32_t nb,
-                     int64_t N, int64_t* __restrict__ linear_out, uint32_t* __restrict__ keys,
-                     uint32_t* __restrict__ vals, const float* __restrict__ iw,
-                     uint32_t* __restrict__ vals2) {
-  const int64_t l = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (l >= N) return;
-  // Bag owning position l: last bag with offsets[bag] <= l.
-  int64_t lo = 0, hi = nbags;  // offsets[lo] <= l < offsets[hi]
-  while (hi - lo > 1) {
-    const int64_t mid = lo + ((hi - lo) >> 1);
-    if (static_cast<int64_t>(offsets[mid]) <= l)
-      lo = mid;
-    else
-      hi = mid;
+                     int64_t N, int32_t bits, int32_t passes, int64_t* __restrict__ linear_out,
+                     uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
+                     const float* __restrict__ iw, uint32_t* __restrict__ vals2,
+                     uint32_t* __restrict__ ghist) {
+  __shared__ uint32_t s_mark[kLinTile];  // bag (relative to blo) starting at each position
+  __shared__ int64_t s_range[2][2];      // [half][lo, hi] of the cooperative searches
+  __shared__ uint32_t s_cnt[2][2];       // [half][wave of the half]
+  __shared__ uint32_t s_wmax[4];
+  __shared__ uint32_t h[kMaxPasses][kRadix];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t l0 = static_cast<int64_t>(blockIdx.x) * kLinTile;
+  const int64_t lend = l0 + kLinTile < N ? l0 + kLinTile : N;
+  const int64_t pbase = l0 + w * kLinWavePos + lane;  // item it: pbase + it * 64
+  I idx[kLinItems];
+#pragma unroll
+  for (int it = 0; it < kLinItems; ++it) {  // in flight during the searches below
+    const int64_t l = pbase + it * 64;
+    idx[it] = l < lend ? indices[l] : I(0);
   }
-  const int64_t t = lo / B;
-  const int64_t b = lo - t * B;
-  const int64_t key = hsc[t] + static_cast<int64_t>(indices[l]);
-  if (linear_out) linear_out[l] = key;
-  keys[l] = static_cast<uint32_t>(key);
-  vals[l] = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
-  if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
-}
-
-// ---- radix sort -----------------------------------------------------------
-
-__global__ void __launch_bounds__(256)
-    radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift, int nbits,
-                      uint32_t* __restrict__ hist, int64_t ntiles) {
-  __shared__ uint32_t cnt[4][kRadix];
-  const int w = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + w;
-  for (int d = lane; d < kRadix; d += 64) cnt[w][d] = 0;
-  __syncthreads();
-  const uint32_t mask = (1u << nbits) - 1u;
-  if (tile < ntiles) {
-#pragma unroll 4
-    for (int it = 0; it < kSortItems; ++it) {
-      const int64_t i = tile * kSortTile + it * 64 + lane;
-      if (i < n) atomicAdd(&cnt[w][(keys[i] >> shift) & mask], 1u);
+  // Last bag with offsets[bag] <= target (0 when none), for the block's first
+  // (half 0) and last (half 1) position: 128-ary searches, one probe per
+  // thread and round, so ceil(log128(nbags)) dependent loads instead of
+  // log2(nbags).  Invariant: offsets[lo] <= target < offsets[hi] (hi = nbags:
+  // past the end).
+  {
+    const int half = threadIdx.x >> 7, q = threadIdx.x & 127;
+    const int64_t target = half == 0 ? l0 : lend - 1;
+    if (q == 0) {
+      s_range[half][0] = 0;
+      s_range[half][1] = nbags;
+    }
+    __syncthreads();
+    while (true) {
+      const int64_t lo = s_range[0][0], hi = s_range[0][1];
+      const int64_t lo1 = s_range[1][0], hi1 = s_range[1][1];
+      if (hi - lo <= 1 && hi1 - lo1 <= 1) break;  // block-uniform
+      const int64_t mylo = half == 0 ? lo : lo1, myhi = half == 0 ? hi : hi1;
+      const int64_t stride = (myhi - mylo + 127) / 128;
+      const int64_t pos = mylo + q * stride;
+      // Probe q = 0 is lo itself (true by the invariant); probes past hi are false.
+      const bool le = myhi - mylo > 1 && pos < myhi &&
+                      (q == 0 || static_cast<int64_t>(offsets[pos]) <= target);
+      const uint64_t bal = __ballot(le);
+      if (lane == 0) s_cnt[half][w & 1] = __popcll(bal);
+      __syncthreads();
+      if (q == 0 && myhi - mylo > 1) {
+        const int64_t c = s_cnt[half][0] + s_cnt[half][1];  // probes 0..c-1 are <= target
+        const int64_t nlo = mylo + (c - 1) * stride;
+        const int64_t nhi = mylo + c * stride;
+        s_range[half][0] = nlo;
+        s_range[half][1] = nhi < myhi ? nhi : myhi;
+      }
+      __syncthreads();
     }
   }
+  const int64_t blo = s_range[0][0], bhi = s_range[1][0];
+  for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
+  // Bag of every position without a search when the block spans few bags:
+  // each non-empty bag marks its first position, and position l's bag is the
+  // largest mark at or before l (an inclusive max-scan; bag ids grow with
+  // position, and position l0 belongs to bag blo, mark 0).
+  const bool marked = bhi - blo < 4 * kLinTile;  // block-uniform
+  uint32_t rel[kLinItems];
+  if (marked) {
+    for (int i = threadIdx.x; i < kLinTile; i += 256) s_mark[i] = 0u;
+    __syncthreads();
+    for (int64_t b = blo + threadIdx.x; b <= bhi; b += 256) {
+      const int64_t o0 = static_cast<int64_t>(offsets[b]);
+      const int64_t o1 = static_cast<int64_t>(offsets[b + 1]);
+      if (o1 > o0 && o0 >= l0 && o0 < lend) s_mark[o0 - l0] = static_cast<uint32_t>(b - blo);
+    }
+    __syncthreads();
+    uint32_t wmax = 0u;
+#pragma unroll
+    for (int it = 0; it < kLinItems; ++it) {
+      const uint32_t m = s_mark[w * kLinWavePos + it * 64 + lane];
+      wmax = m > wmax ? m : wmax;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const uint32_t o = __shfl_xor(wmax, d, 64);
+      wmax = o > wmax ? o : wmax;
+    }
+    if (lane == 0) s_wmax[w] = wmax;
+    __syncthreads();
+    uint32_t carry = 0u;  // largest mark before this wave's positions
+    for (int i = 0; i < w; ++i) carry = s_wmax[i] > carry ? s_wmax[i] : carry;
+#pragma unroll
+    for (int it = 0; it < kLinItems; ++it) {
+      uint32_t v = wave_incl_scan<MaxOp>(s_mark[w * kLinWavePos + it * 64 + lane]);
+      v = v > carry ? v : carry;
+      rel[it] = v;
+      carry = __shfl(v, 63, 64);
+    }
+  } else {
+    // Many empty bags inside the block: per-position binary search.
+#pragma unroll
+    for (int it = 0; it < kLinItems; ++it) {
+      const int64_t l = pbase + it * 64;
+      int64_t lo = blo, hi = bhi + 1;  // offsets[hi] > l for every l of the block
+      while (l < lend && hi - lo > 1) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if (static_cast<int64_t>(offsets[mid]) <= l)
+          lo = mid;
+        else
+          hi = mid;
+      }
+      rel[it] = static_cast<uint32_t>(lo - blo);
+    }
+    __syncthreads();  // h cleared
+  }
+#pragma unroll
+  for (int it = 0; it < kLinItems; ++it) {
+    const int64_t l = pbase + it * 64;
+    if (l >= lend) continue;
+    const int64_t bag = blo + rel[it];
+    const int64_t t = bag / B;
+    const int64_t b = bag - t * B;
+    const int64_t key = hsc[t] + static_cast<int64_t>(idx[it]);
+    if (linear_out) linear_out[l] = key;
+    const uint32_t k32 = static_cast<uint32_t>(key);
+    keys[l] = k32;
+    vals[l] = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+    if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
+    for (int p = 0; p < passes; ++p)
+      atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
+  }
   __syncthreads();
-  if (tile < ntiles)
-    for (int d = lane; d < kRadix; d += 64) hist[d * ntiles + tile] = cnt[w][d];
+  for (int i = threadIdx.x; i < passes * kRadix; i += 256) {
+    const uint32_t c = (&h[0][0])[i];
+    if (c) atomicAdd(&ghist[i], c);
+  }
 }
 
-struct LoadU32 {
-  const uint32_t* p;
-  __device__ uint32_t operator()(int64_t i) const { return p[i]; }
-};
+// ---- radix sort: one launch per pass --------------------------------------
 
+constexpr unsigned long long kSweepAgg = 1ull << 62;
+constexpr unsigned long long kSweepIncl = 2ull << 62;
+
+// status: [tiles][kRadix] zeroed words; ticket: zeroed [2] (next tile, give-up
+// flag).  ghist: this pass's global digit counts.
 template <bool LAST>
 __global__ void __launch_bounds__(256)
-    radix_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-                         int64_t n, int shift, int nbits, const uint32_t* __restrict__ hist_scan,
-                         int64_t ntiles, uint32_t* __restrict__ keys_out,
-                         int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
-                         const uint32_t* __restrict__ vals2, uint32_t* __restrict__ vals2_out) {
-  __shared__ uint32_t base[4][kRadix];
+    onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+                    const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
+                    const uint32_t* __restrict__ ghist, unsigned long long* status,
+                    unsigned int* ticket, uint32_t* __restrict__ keys_out,
+                    int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
+                    uint32_t* __restrict__ vals2_out) {
+  __shared__ unsigned int s_tile;
+  __shared__ uint32_t cnt[4][kRadix];  // per-wave digit counts, then per-wave prefixes
+  __shared__ uint32_t s_base[kRadix];
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t tile = static_cast<int64_t>(blockIdx.x) * 4 + w;
-  if (tile < ntiles)
-    for (int d = lane; d < kRadix; d += 64) base[w][d] = hist_scan[d * ntiles + tile];
+  if (threadIdx.x == 0) s_tile = atomicAdd(ticket, 1u);
+  for (int i = threadIdx.x; i < 4 * kRadix; i += 256) (&cnt[0][0])[i] = 0u;
   __syncthreads();
-  if (tile >= ntiles) return;
+  const int64_t tile = s_tile;
+  const int64_t i0 = tile * kSweepTile + w * kSweepWaveKeys + lane;
+  uint32_t k[kSweepItems], v[kSweepItems], v2[kSweepItems], rank[kSweepItems];
+#pragma unroll
+  for (int it = 0; it < kSweepItems; ++it) {
+    const int64_t i = i0 + it * 64;
+    const bool valid = i < n;
+    k[it] = valid ? keys[i] : 0u;
+    v[it] = valid ? vals[i] : 0u;
+    v2[it] = (valid && vals2) ? vals2[i] : 0u;
+  }
   const uint32_t mask = (1u << nbits) - 1u;
   const uint64_t lt = (1ull << lane) - 1ull;
-  for (int it = 0; it < kSortItems; ++it) {
-    const int64_t i = tile * kSortTile + it * 64 + lane;
-    const bool valid = i < n;
-    const uint32_t k = valid ? keys[i] : 0u;
-    const uint32_t v = valid ? vals[i] : 0u;
-    const uint32_t v2 = (valid && vals2) ? vals2[i] : 0u;
-    const uint32_t d = (k >> shift) & mask;
+#pragma unroll
+  for (int it = 0; it < kSweepItems; ++it) {
+    const bool valid = i0 + it * 64 < n;
+    const uint32_t d = (k[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < nbits; ++bit) {
       const bool set = (d >> bit) & 1u;
       const uint64_t bb = __ballot(set);
       peers &= set ? bb : ~bb;
     }
-    const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lt));
-    const uint32_t pos = base[w][d] + rank;
-    if (valid) {
-      if constexpr (LAST)
-        keys_out64[pos] = static_cast<int64_t>(k);
-      else
-        keys_out[pos] = k;
-      vals_out[pos] = v;
-      if (vals2) vals2_out[pos] = v2;
+    const uint32_t before = cnt[w][d];
+    rank[it] = before + static_cast<uint32_t>(__popcll(peers & lt));
+    // The lowest lane of each digit group advances the wave's count after
+    // every lane has read it (LDS operations of a wave are ordered).
+    if (valid && (peers & lt) == 0ull) cnt[w][d] = before + static_cast<uint32_t>(__popcll(peers));
+  }
+  __syncthreads();
+  const int d = threadIdx.x;  // one digit per thread from here on
+  const uint32_t c0 = cnt[0][d], c1 = cnt[1][d], c2 = cnt[2][d], c3 = cnt[3][d];
+  const uint32_t total = c0 + c1 + c2 + c3;
+  cnt[0][d] = 0u;
+  cnt[1][d] = c0;
+  cnt[2][d] = c0 + c1;
+  cnt[3][d] = c0 + c1 + c2;
+  const bool used = d <= static_cast<int>(mask);  // same for every tile of the pass
+  uint32_t gall;
+  const uint32_t goff = block_excl_scan<SumOp>(used ? ghist[d] : 0u, &gall);
+  uint32_t prefix = 0u;
+  if (used) {
+    unsigned long long* mine = status + tile * kRadix + d;
+    if (tile == 0) {
+      __hip_atomic_store(mine, kSweepIncl | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      __hip_atomic_store(mine, kSweepAgg | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Look back kLookBack predecessors per round (independent loads), folding
+      // them nearest first until an inclusive word; an unpublished word
+      // (flag 0) ends the round and the next round resumes there.
+      constexpr int kLookBack = 8;
+      int64_t j = tile - 1;  // nearest predecessor not yet folded in
+      int spins = 0;
+      bool done = false;
+      while (!done) {
+        unsigned long long x[kLookBack];
+#pragma unroll
+        for (int q = 0; q < kLookBack; ++q)
+          x[q] = j - q >= 0 ? __hip_atomic_load(status + (j - q) * kRadix + d, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : kSweepIncl;  // before tile 0 (never reached: tile 0 is inclusive)
+        int folded = 0;
+#pragma unroll
+        for (int q = 0; q < kLookBack; ++q) {
+          if (done || folded < q) continue;  // stopped earlier in this round
+          const unsigned long long flag = x[q] >> 62;
+          if (flag == 0ull) continue;
+          prefix += static_cast<uint32_t>(x[q]);
+          folded = q + 1;
+          if (flag == 2ull) done = true;
+        }
+        j -= folded;
+        if (!done && folded < kLookBack) {  // waiting on an unpublished predecessor
+          if (++spins > kScanSpinLimit) {   // never expected; keeps the wait bounded
+            ticket[1] = 1u;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      __hip_atomic_store(mine, kSweepIncl | (prefix + total), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
-    // The lowest lane of each digit group advances that digit's cursor after
-    // every lane of the wave has read it above (LDS ops of a wave are ordered).
-    if (valid && rank == 0) base[w][d] = pos + static_cast<uint32_t>(__popcll(peers));
+  }
+  s_base[d] = goff + prefix;
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kSweepItems; ++it) {
+    if (i0 + it * 64 >= n) continue;
+    const uint32_t dd = (k[it] >> shift) & mask;
+    const uint32_t pos = s_base[dd] + cnt[w][dd] + rank[it];
+    if (pos >= n) continue;  // only after a look-back gave up; keeps stores in bounds
+    if constexpr (LAST)
+      keys_out64[pos] = static_cast<int64_t>(k[it]);
+    else
+      keys_out[pos] = k[it];
+    vals_out[pos] = v[it];
+    if (vals2) vals2_out[pos] = v2[it];
   }
 }
 
@@ -172,42 +356,35 @@ struct HeadFlag {
   }
 };
 
-__global__ void __launch_bounds__(256)
-    rle_write_kernel(const int64_t* __restrict__ keys, int64_t n,
-                     const uint32_t* __restrict__ run_id, const uint32_t* __restrict__ num_runs,
-                     int64_t* __restrict__ run_keys, int32_t* __restrict__ cum) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i == 0) cum[*num_runs] = static_cast<int32_t>(n);
-  if (i >= n) return;
-  if (i == 0 || keys[i] != keys[i - 1]) {
-    const uint32_t r = run_id[i];
-    run_keys[r] = keys[i];
-    cum[r] = static_cast<int32_t>(i);
+// Epilogue of the head-flag scan: element i with exclusive head count r
+// starts run r when it is a head.
+struct RleEpi {
+  const int64_t* keys;
+  int64_t n;
+  int64_t* run_keys;
+  int32_t* cum;
+  uint32_t* num_runs;        // device count used by later kernels
+  int32_t* num_runs_out;     // the op's int32 output, may be null
+  __device__ void operator()(int64_t i, uint32_t r) const {
+    if (i == 0 || keys[i] != keys[i - 1]) {
+      run_keys[r] = keys[i];
+      cum[r] = static_cast<int32_t>(i);
+    }
   }
-}
+  __device__ void total(uint32_t t) const {
+    *num_runs = t;
+    if (num_runs_out) *num_runs_out = static_cast<int32_t>(t);
+    cum[t] = static_cast<int32_t>(n);
+  }
+};
 
 __global__ void __launch_bounds__(256)
     run_lengths_kernel(const int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
-                       int64_t n, int32_t* __restrict__ lengths, int32_t* __restrict__ num_runs_out) {
+                       int64_t n, int32_t* __restrict__ lengths) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t m = *num_runs;
-  if (r == 0 && num_runs_out) *num_runs_out = static_cast<int32_t>(m);
   if (r >= m || r >= n) return;
   lengths[r] = cum[r + 1] - cum[r];
-}
-
-// chunk_run[q] = the run that owns chunk q (runs longer than kLong only).
-__global__ void __launch_bounds__(256)
-    chunk_map_kernel(const int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
-                     const uint32_t* __restrict__ chunk_start, uint32_t* __restrict__ chunk_run,
-                     int64_t n) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n || r >= static_cast<int64_t>(*num_runs)) return;
-  const int32_t len = cum[r + 1] - cum[r];
-  if (len <= kLong) return;
-  const uint32_t q0 = chunk_start[r];
-  const int32_t nq = (len + kChunk - 1) / kChunk;
-  for (int32_t i = 0; i < nq; ++i) chunk_run[q0 + i] = static_cast<uint32_t>(r);
 }
 
 struct ChunkCount {
@@ -218,18 +395,34 @@ struct ChunkCount {
   }
 };
 
+// Epilogue of the chunk-count scan: chunk_start[r] = first chunk of run r
+// (runs of at most kLong occurrences own no chunk).
+struct ChunkEpi {
+  uint32_t* chunk_start;
+  uint32_t* total_chunks;
+  __device__ void operator()(int64_t r, uint32_t q0) const { chunk_start[r] = q0; }
+  __device__ void total(uint32_t t) const { *total_chunks = t; }
+};
+
 // ---- workspace layout -----------------------------------------------------
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int64_t sweep_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kSweepTile); }
+// Per pass: [tiles][kRadix] status words, then one word holding the ticket pair.
+int64_t sweep_pass_words(int64_t n) { return sweep_tiles(n) * kRadix + 32; }
 
 struct SortWs {
   uint32_t* keys[2];
   uint32_t* vals[2];
   uint32_t* vals2[2];  // per-sample weights (weighted backward only)
-  uint32_t* hist;
-  unsigned long long* scan_state;  // kScanSlots slots of (tiles + 1) zeroed words
+  // Zeroed before every call, contiguous: scan slots, digit histograms, sweep state.
+  unsigned long long* zeroed;
+  unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
-  uint32_t* run_id;
+  uint32_t* ghist;                 // [kMaxPasses][kRadix]
+  unsigned long long* sweep;       // kMaxPasses x sweep_pass_words
+  int64_t sweep_words;
   uint32_t* counters;  // [0] num_runs, [1] total chunks
   size_t bytes;
 };
@@ -237,9 +430,7 @@ struct SortWs {
 SortWs carve_sort(uint8_t* base, int64_t N) {
   SortWs w{};
   const int64_t n = N > 0 ? N : 1;
-  const int64_t ntiles = ceil_div(n, kSortTile);
-  const int64_t hist_n = kRadix * ntiles;
-  const int64_t slot_words = scan_tiles(hist_n > n + 1 ? hist_n : n + 1) + 2;
+  const int64_t slot_words = scan_tiles(n + 1) + 2;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     uint8_t* p = base ? base + off : nullptr;
@@ -251,13 +442,25 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
     w.vals[i] = reinterpret_cast<uint32_t*>(take(n * 4));
     w.vals2[i] = reinterpret_cast<uint32_t*>(take(n * 4));
   }
-  w.hist = reinterpret_cast<uint32_t*>(take(hist_n * 4));
-  w.scan_state = reinterpret_cast<unsigned long long*>(take(kScanSlots * slot_words * 8));
-  w.scan_slot_words = slot_words;
-  w.run_id = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
+  w.scan_slot_words = align256(slot_words * 8) / 8;
+  w.sweep_words = sweep_pass_words(n);
+  const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
+  const size_t hist_bytes = align256(kMaxPasses * kRadix * 4);
+  uint8_t* z = take(scan_bytes + hist_bytes + kMaxPasses * w.sweep_words * 8);
+  w.zeroed = reinterpret_cast<unsigned long long*>(z);
+  w.scan_state = w.zeroed;
+  w.ghist = z ? reinterpret_cast<uint32_t*>(z + scan_bytes) : nullptr;
+  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + scan_bytes + hist_bytes) : nullptr;
   w.counters = reinterpret_cast<uint32_t*>(take(64));
   w.bytes = off;
   return w;
+}
+
+// Words to clear for a sort of `passes` passes (the sweep state of unused
+// passes is left alone).
+int64_t zeroed_words(const SortWs& w, int passes) {
+  return kScanSlots * w.scan_slot_words + align256(kMaxPasses * kRadix * 4) / 8 +
+         passes * w.sweep_words;
 }
 
 // Scan-state slot i: status words, then the ticket pair in the last word.
@@ -271,8 +474,8 @@ struct TransposeOut {
   int64_t* sorted;      // [N]
   int32_t* infos;       // [N]
   int64_t* run;         // [N]
-  int32_t* run_lengths; // [N]
-  int32_t* num_runs;    // [1]
+  int32_t* run_lengths; // [N], may be null
+  int32_t* num_runs;    // [1], may be null
   int32_t* cum;         // [N+1]
   float* weights_sorted;  // [N] per-sample weights in sorted order, or null
 };
@@ -285,26 +488,28 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
   const int64_t nbags = static_cast<int64_t>(T) * B;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
-  {  // every scan's look-back state starts at zero (a kernel, not a memset)
-    const int64_t words = kScanSlots * w.scan_slot_words;
+  const int passes = (bits + kRadixBits - 1) / kRadixBits;
+  {  // look-back state of every scan and pass, and the histograms, start at zero
+    const int64_t words = zeroed_words(w, passes);
     const int64_t blocks = ceil_div(words, 256);
-    zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 1024 ? blocks : 1024)), 256, 0, s>>>(
-        w.scan_state, words);
+    zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 2048 ? blocks : 2048)), 256, 0, s>>>(
+        w.zeroed, words);
     MX_LAUNCH_CHECK();
   }
+  const dim3 glin(static_cast<uint32_t>(ceil_div(N, kLinTile)));
   if (index_bytes == 8)
-    linearize_kernel<int64_t><<<g256, 256, 0, s>>>(
+    linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
-        nb, N, o.linear, w.keys[0], w.vals[0], iw, v2[0]);
+        nb, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
   else
-    linearize_kernel<int32_t><<<g256, 256, 0, s>>>(
+    linearize_kernel<int32_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
-        nb, N, o.linear, w.keys[0], w.vals[0], iw, v2[0]);
+        nb, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
   MX_LAUNCH_CHECK();
 
-  const int64_t ntiles = ceil_div(N, kSortTile);
-  const dim3 gsort(static_cast<uint32_t>(ceil_div(ntiles, 4)));
-  const int passes = (bits + kRadixBits - 1) / kRadixBits;
+  const int64_t ntiles = sweep_tiles(N);
+  if (ntiles > 0xffffffffll) return set_error(MX_EINVAL, "too many sort tiles");
+  const dim3 gsweep(static_cast<uint32_t>(ntiles));
   int cur = 0;
   if (passes == 0) {
     copy_keys_kernel<<<g256, 256, 0, s>>>(w.keys[0], w.vals[0], N, o.sorted,
@@ -314,33 +519,31 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
     const int nbits = bits - shift < kRadixBits ? bits - shift : kRadixBits;
-    radix_hist_kernel<<<gsort, 256, 0, s>>>(w.keys[cur], N, shift, nbits, w.hist, ntiles);
-    MX_LAUNCH_CHECK();
-    if (int rc = exclusive_scan(LoadU32{w.hist}, kRadix * ntiles, nullptr, w.hist, nullptr,
-                                scan_slot(w, p), s))
-      return rc;
-    const bool last = p == passes - 1;
-    if (last) {
-      radix_scatter_kernel<true><<<gsort, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, nullptr, o.sorted,
-          reinterpret_cast<uint32_t*>(o.infos), v2[cur], v2_final);
+    unsigned long long* st = w.sweep + p * w.sweep_words;
+    unsigned int* ticket = reinterpret_cast<unsigned int*>(st + ntiles * kRadix);
+    const uint32_t* gh = w.ghist + p * kRadix;
+    if (p == passes - 1) {
+      onesweep_kernel<true><<<gsweep, 256, 0, s>>>(
+          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, nullptr, o.sorted,
+          reinterpret_cast<uint32_t*>(o.infos), v2_final);
     } else {
-      radix_scatter_kernel<false><<<gsort, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], N, shift, nbits, w.hist, ntiles, w.keys[cur ^ 1], nullptr,
-          w.vals[cur ^ 1], v2[cur], v2[cur ^ 1]);
+      onesweep_kernel<false><<<gsweep, 256, 0, s>>>(
+          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, w.keys[cur ^ 1],
+          nullptr, w.vals[cur ^ 1], v2[cur ^ 1]);
     }
     MX_LAUNCH_CHECK();
     cur ^= 1;
   }
 
   // Run-length encode the sorted keys.
-  if (int rc = exclusive_scan(HeadFlag{o.sorted}, N, nullptr, w.run_id, &w.counters[0],
-                              scan_slot(w, 4), s))
+  if (int rc = prefix_scan_epi(HeadFlag{o.sorted}, N, nullptr,
+                               RleEpi{o.sorted, N, o.run, o.cum, &w.counters[0], o.num_runs},
+                               scan_slot(w, 0), s))
     return rc;
-  rle_write_kernel<<<g256, 256, 0, s>>>(o.sorted, N, w.run_id, &w.counters[0], o.run, o.cum);
-  MX_LAUNCH_CHECK();
-  run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths, o.num_runs);
-  MX_LAUNCH_CHECK();
+  if (o.run_lengths) {
+    run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths);
+    MX_LAUNCH_CHECK();
+  }
   return MX_OK;
 }
 
@@ -363,7 +566,7 @@ struct BwdArgs {
   const float* iw_sorted;  // per-sample weights in sorted order, or null
   const uint32_t* num_runs;
   const uint32_t* chunk_start;
-  const uint32_t* chunk_run;
+  uint32_t* chunk_run;  // written by bwd_chunk_kernel, read by bwd_long_run_kernel
   const uint32_t* total_chunks;
   float* partial;
   int64_t B;
@@ -524,75 +727,97 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
   if (k == 0) *hp = h;
 }
 
-// Pass B (long runs): one 256-thread block per run longer than kLong.  The
-// 256/G groups sum the run's chunk partials round-robin (group j takes
-// chunks j, j + 256/G, ...), the group vectors are combined in group order
-// through LDS, and group 0 applies the update.
+// Pass B (long runs): a block owns the long runs whose first chunk lies in
+// its kLongRange-chunk range (found by one parallel read of chunk_run; a long
+// run has at least two chunks, so at most two start in a range) and handles
+// them one after another.  Per run, the 256/G groups sum the run's chunk
+// partials round-robin (group j takes chunks j, j + 256/G, ...), the group
+// vectors are combined in group order through LDS, and group 0 applies the
+// update.
+constexpr int kLongRange = 4;  // chunks per block range
+
 template <int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
   __shared__ TableMeta meta;
   constexpr int NG = 256 / G;
   __shared__ float part[NG][G * NCH * 4];
+  __shared__ uint32_t s_runs[kLongRange];
+  __shared__ int s_nruns;
   stage_meta(a, meta);
   const MetaView mv{a, meta, a.T <= kMaxCachedTables};
   const int grp = threadIdx.x / G, k = threadIdx.x % G;
   const int64_t total = *a.total_chunks;
-  for (int64_t q = blockIdx.x; q < total; q += gridDim.x) {
-    const uint32_t r = a.chunk_run[q];
-    if (q > 0 && a.chunk_run[q - 1] == r) continue;  // not the run's first chunk (block-uniform)
-    const int64_t s0 = a.cum[r];
-    const int64_t s1 = a.cum[r + 1];
-    const int64_t t = table_of(a, a.infos[s0]);
-    const int32_t D0 = mv.D_off(t);
-    const int32_t D = mv.D_off(t + 1) - D0;
-    (void)D0;
-    const int64_t q1 = q + (s1 - s0 + kChunk - 1) / kChunk;
-    float gs[NCH][4];
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
-    for (int64_t qq = q + grp; qq < q1; qq += NG * U) {
-      float v[U][NCH][4];
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (qq + u * NG < q1)
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-            if ((c * G + k) * 4 < D) ld4(a.partial + (qq + u * NG) * a.max_D + (c * G + k) * 4, v[u][c]);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (qq + u * NG < q1)
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-            if ((c * G + k) * 4 < D)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) gs[c][e] += v[u][c][e];
+  for (int64_t q0 = static_cast<int64_t>(blockIdx.x) * kLongRange; q0 < total;
+       q0 += static_cast<int64_t>(gridDim.x) * kLongRange) {
+    if (threadIdx.x < 64) {  // wave 0 lists the runs starting in the range, in order
+      const int64_t q = q0 + threadIdx.x;
+      const bool in = threadIdx.x < kLongRange && q < total;
+      const uint32_t r = in ? a.chunk_run[q] : 0u;
+      const bool start = in && (q == 0 || a.chunk_run[q - 1] != r);
+      const uint64_t bal = __ballot(start);
+      if (start) s_runs[__popcll(bal & ((1ull << threadIdx.x) - 1ull))] = r;
+      if (threadIdx.x == 0) s_nruns = __popcll(bal);
     }
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) part[grp][(c * G + k) * 4 + e] = gs[c][e];
     __syncthreads();
-    if (grp == 0) {
+    const int nr = s_nruns;
+    for (int ri = 0; ri < nr; ++ri) {
+      const uint32_t r = s_runs[ri];
+      const int64_t s0 = a.cum[r];
+      const int64_t s1 = a.cum[r + 1];
+      const int64_t t = table_of(a, a.infos[s0]);
+      const int32_t D0 = mv.D_off(t);
+      const int32_t D = mv.D_off(t + 1) - D0;
+      (void)D0;
+      const int64_t qf = a.chunk_start[r];  // the run's first chunk
+      const int64_t q1 = qf + (s1 - s0 + kChunk - 1) / kChunk;
+      float gs[NCH][4];
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = part[0][(c * G + k) * 4 + e];
-          for (int j = 1; j < NG; ++j) x += part[j][(c * G + k) * 4 + e];
-          gs[c][e] = x;
-        }
-      const int64_t idx = a.run[r] - mv.hsc(t);
-      float* wrow = a.W + mv.w_off(t) + idx * D;
-      float* hp = a.m1 + mv.m1_off(t) + idx;
-      float w[NCH][4];
+        for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
+      for (int64_t qq = qf + grp; qq < q1; qq += NG * U) {
+        float v[U][NCH][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (qq + u * NG < q1)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+              if ((c * G + k) * 4 < D) ld4(a.partial + (qq + u * NG) * a.max_D + (c * G + k) * 4, v[u][c]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (qq + u * NG < q1)
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+              if ((c * G + k) * 4 < D)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gs[c][e] += v[u][c][e];
+      }
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
-      adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, *hp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[grp][(c * G + k) * 4 + e] = gs[c][e];
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = part[0][(c * G + k) * 4 + e];
+            for (int j = 1; j < NG; ++j) x += part[j][(c * G + k) * 4 + e];
+            gs[c][e] = x;
+          }
+        const int64_t idx = a.run[r] - mv.hsc(t);
+        float* wrow = a.W + mv.w_off(t) + idx * D;
+        float* hp = a.m1 + mv.m1_off(t) + idx;
+        float w[NCH][4];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
+        adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, *hp);
+      }
+      __syncthreads();
     }
-    __syncthreads();
+    __syncthreads();  // s_runs / s_nruns are rewritten for the next range
   }
 }
 
@@ -608,10 +833,29 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
   const int64_t total = *a.total_chunks;
+  const int64_t nruns = *a.num_runs;
   for (int64_t qb = wave * P; qb < total; qb += nwaves * P) {
     const int64_t q = qb + g;
     if (q >= total) continue;
-    const int64_t r = a.chunk_run[q];
+    // Owner of chunk q: the last run whose first chunk is <= q (runs without
+    // chunks share the next long run's start, which is larger).  G-ary
+    // search, one probe per lane and round; invariant
+    // chunk_start[lo] <= q < chunk_start[hi] (hi = nruns: past the end).
+    int64_t lo = 0, hi = nruns;
+    while (hi - lo > 1) {
+      const int64_t stride = (hi - lo + G - 1) / G;
+      const int64_t pos = lo + k * stride;
+      const bool le = pos < hi && (k == 0 || static_cast<int64_t>(a.chunk_start[pos]) <= q);
+      const uint64_t bal = __ballot(le);
+      uint64_t mine = bal;
+      if constexpr (G < 64) mine = (bal >> (g * G)) & ((1ull << G) - 1ull);
+      const int c = __popcll(mine);
+      const int64_t nhi = lo + c * stride;
+      lo += (c - 1) * stride;
+      hi = nhi < hi ? nhi : hi;
+    }
+    const int64_t r = lo;
+    if (k == 0) a.chunk_run[q] = static_cast<uint32_t>(r);  // for bwd_long_run_kernel
     const int64_t s0 = a.cum[r] + (q - a.chunk_start[r]) * kChunk;
     const int64_t e0 = a.cum[r + 1];
     const int64_t s1 = s0 + kChunk < e0 ? s0 + kChunk : e0;
@@ -684,8 +928,8 @@ int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   const dim3 grid(static_cast<uint32_t>(want < 1 ? 1 : (want > cap ? cap : want)));
   bwd_chunk_kernel<I, G, NCH, UC><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
-  const int64_t long_cap = static_cast<int64_t>(num_cus()) * 4;
-  const int64_t long_want = ceil_div(N, kChunk);
+  const int64_t long_cap = static_cast<int64_t>(num_cus()) * 16;
+  const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
   bwd_long_run_kernel<G, NCH, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   bwd_update_kernel<I, G, NCH, U><<<grid, 256, 0, s>>>(a);
@@ -708,8 +952,6 @@ struct BwdWs {
   int64_t* sorted;
   int32_t* infos;
   int64_t* run;
-  int32_t* run_lengths;
-  int32_t* num_runs;
   int32_t* cum;
   uint32_t* chunk_start;
   uint32_t* chunk_run;
@@ -718,7 +960,6 @@ struct BwdWs {
   size_t bytes;
 };
 
-int64_t max_chunks(int64_t N) { return N / kChunk + N / (kLong + 1) + 2; }  // >= sum of ceil(len/kChunk)
 
 BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   BwdWs w{};
@@ -733,8 +974,6 @@ BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   w.sorted = reinterpret_cast<int64_t*>(take(n * 8));
   w.infos = reinterpret_cast<int32_t*>(take(n * 4));
   w.run = reinterpret_cast<int64_t*>(take(n * 8));
-  w.run_lengths = reinterpret_cast<int32_t*>(take(n * 4));
-  w.num_runs = reinterpret_cast<int32_t*>(take(4));
   w.cum = reinterpret_cast<int32_t*>(take((n + 1) * 4));
   w.chunk_start = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
   w.chunk_run = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(max_chunks(n)) * 4));
@@ -774,6 +1013,8 @@ static int check_common(int32_t T, int64_t B, int32_t bits, int32_t nb, int32_t 
   MX_REQUIRE(N < 0x7fffffffll, "N %lld too large for int32 run offsets", (long long)N);
   MX_REQUIRE(nb >= 1 && nb <= 32, "info_B_num_bits %d invalid", nb);
   MX_REQUIRE(B <= (int64_t(1) << nb), "B does not fit info_B_num_bits");
+  MX_REQUIRE(N == 0 || (T > 0 && B > 0), "%lld indices but no bags (T=%d, B=%lld)",
+             (long long)N, T, (long long)B);
   return MX_OK;
 }
 
@@ -837,18 +1078,17 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   if (workspace == nullptr || workspace_bytes < w.bytes)
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   auto* s = as_stream(stream);
-  TransposeOut o{nullptr, w.sorted, w.infos, w.run, w.run_lengths, w.num_runs, w.cum,
+  TransposeOut o{nullptr, w.sorted, w.infos, w.run, nullptr, nullptr, w.cum,
                  indice_weights ? w.weights_sorted : nullptr};
   if (int rc = run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, nb, indices, offsets,
                              index_bytes, N, indice_weights, o, w.sort, s))
     return rc;
   // Chunk layout of long runs.
-  if (int rc = exclusive_scan(ChunkCount{w.cum}, N, w.num_runs, w.chunk_start,
-                              &w.sort.counters[1], scan_slot(w.sort, 5), s))
+  if (int rc = prefix_scan_epi(
+          ChunkCount{w.cum}, N, reinterpret_cast<const int32_t*>(&w.sort.counters[0]),
+          ChunkEpi{w.chunk_start, &w.sort.counters[1]}, scan_slot(w.sort, 1),
+          s))
     return rc;
-  chunk_map_kernel<<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), 256, 0, s>>>(
-      w.cum, &w.sort.counters[0], w.chunk_start, w.chunk_run, N);
-  MX_LAUNCH_CHECK();
   BwdArgs a;
   a.W = weights;
   a.w_off = weights_offsets;
