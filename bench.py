@@ -340,7 +340,7 @@ def bench_backward(args, dev):
         kernel="whole backward (transpose + segment reduce + update)", alg_bytes=alg,
         kernel_ms_mean=mean_ms, kernel_ms_median=med_ms,
     )
-    return res, None, None
+    return res, traffic_from_profile("tbe_bwd_config3"), None
 
 
 def main():
