@@ -116,8 +116,9 @@ int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense, i
 
 /* Serves fbgemm::split_embedding_codegen_forward_unweighted_cuda /
  * _weighted_cuda (the forward of the split_embedding_codegen_lookup_*
- * autograd functions), DEVICE placement, fp32 weights.
- *   weights         fp32, all tables back to back
+ * autograd functions), DEVICE placement, fp32 or fp16 weights.
+ *   weights         all tables back to back, fp32 (weights_ty MX_SPARSE_FP32)
+ *                   or fp16 (MX_SPARSE_FP16; widened to fp32 per element)
  *   weights_offsets int64 [T] element offset of each table
  *   D_offsets       int32 [T+1]; every D_t a multiple of 4, max_D <= 1024
  *   indices         [N] int32 (index_bytes 4) or int64 (8)
@@ -126,7 +127,7 @@ int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense, i
  *   out             [B, total_D] fp32 (out_dtype MX_SPARSE_FP32) or fp16
  * SUM: per column, rows are added in index order starting from +0.0.
  * MEAN: the sum times (1.0f / L); empty bags give 0. */
-int mx_tbe_forward(const float* weights, const int64_t* weights_offsets,
+int mx_tbe_forward(const void* weights, int32_t weights_ty, const int64_t* weights_offsets,
                    const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
                    const void* indices, const void* offsets, int32_t index_bytes,
                    int32_t pooling_mode, const float* indice_weights, void* out,
@@ -173,25 +174,31 @@ size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, 
  *   m      = learning_rate / (sqrtf(h) + eps)
  *   c      = 1 (mode 0), 1 - m*weight_decay (mode 1), 1 - learning_rate*weight_decay (mode 2)
  *   w      = fmaf(-m, g, c * w)
- * weights and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are
- * updated in place; no atomics, deterministic. */
+ * weights (fp32, or fp16 with weights_ty MX_SPARSE_FP16: w read as fp32, the
+ * new value rounded to fp16 -- to nearest even, or stochastically when
+ * stochastic_rounding != 0: |w| plus a uniform random amount below fp16's
+ * last place, then truncated, the random bits a hash of (seed, element))
+ * and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are updated
+ * in place; no atomics, deterministic for a given seed. */
 int mx_tbe_backward_rowwise_adagrad(
-    float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
-    int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
+    int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
     int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
     float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
-    float weight_decay, int32_t weight_decay_mode, void* workspace, size_t workspace_bytes,
-    void* stream);
+    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Serves fbgemm::split_embedding_codegen_grad_indice_weights_cuda: the gradient
  * of a weighted lookup's per-sample weights,
  *   grad_indice_weights[l] = sum_d grad_output[b, D_off[t] + d] * W_t[indices[l], d]
  * (MEAN: times 1.0f/L), 0 for tables with feature_requires_grad[t] == 0
- * (feature_requires_grad may be NULL: every table). */
-int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D, const float* weights,
-                               const int64_t* weights_offsets, const int32_t* D_offsets,
-                               int32_t T, int64_t B, int32_t max_D, const void* indices,
+ * (feature_requires_grad may be NULL: every table); weights fp32 or fp16
+ * (weights_ty) as in mx_tbe_forward. */
+int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D, const void* weights,
+                               int32_t weights_ty, const int64_t* weights_offsets,
+                               const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
+                               const void* indices,
                                const void* offsets, int32_t index_bytes, int32_t pooling_mode,
                                const int32_t* feature_requires_grad, float* grad_indice_weights,
                                void* stream);

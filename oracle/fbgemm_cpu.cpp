@@ -92,6 +92,29 @@ extern "C" int fb_tbe_forward_f32(const float* W, const int64_t* w_off, const in
   });
 }
 
+// fp16 weight rows (raw binary16 bits), fp32 output: the kernel fbgemm_gpu's
+// CPU TBE forward uses for fp16 weights.
+extern "C" int fb_tbe_forward_f16w(const uint16_t* W, const int64_t* w_off, const int32_t* D_off,
+                                   int T, int64_t B, const int64_t* indices,
+                                   const int64_t* offsets, int pooling, const float* iw,
+                                   float* out, int64_t total_D, const int64_t* rows_per_table,
+                                   int nthreads) {
+  using K = fbgemm::EmbeddingSpMDMKernelSignature<uint16_t, int64_t, int64_t, float>::Type;
+  std::vector<K> kern(T);
+  for (int t = 0; t < T; ++t) {
+    const int D = D_off[t + 1] - D_off[t];
+    kern[t] = fbgemm::GenerateEmbeddingSpMDMWithStrides<uint16_t, int64_t, int64_t, float>(
+        D, iw != nullptr, pooling == 1, 16, false, true, total_D, D);
+  }
+  return parallel_bags(T, B, nthreads, [&](int t, int64_t b0, int64_t b1) {
+    std::vector<int64_t> off;
+    rebase(offsets, t * B + b0, b1 - b0, off);
+    const int64_t s = offsets[t * B + b0];
+    return kern[t](b1 - b0, off.back(), rows_per_table[t], W + w_off[t], indices + s, off.data(),
+                   iw ? iw + s : nullptr, out + b0 * total_D + D_off[t]);
+  });
+}
+
 extern "C" int fb_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                                const int32_t* D_off, int T, int64_t B, const int64_t* indices,
                                const int64_t* offsets, int pooling, const float* iw,

@@ -94,6 +94,8 @@ def fbgemm():
         i32, i64 = ctypes.c_int32, ctypes.c_int64
         _fb.fb_tbe_forward_f32.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64, P, i32]
         _fb.fb_tbe_forward_f32.restype = ctypes.c_int
+        _fb.fb_tbe_forward_f16w.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64, P, i32]
+        _fb.fb_tbe_forward_f16w.restype = ctypes.c_int
         _fb.fb_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64, P,
                                         i32]
         _fb.fb_nbit_forward.restype = ctypes.c_int
@@ -349,6 +351,10 @@ def info_B_num_bits(T: int, B: int) -> int:
 
 def fbgemm_tbe_forward_f32(W, w_off, D_off, rows_per_table, B, indices, offsets, pooling=POOL_SUM,
                            indice_weights=None, nthreads=1):
+    """FBGEMM's CPU SpMDM, fp32 output; fp16 ``W`` uses the fp16-input kernel."""
+    if np.asarray(W).dtype == np.float16:
+        return _fbgemm_tbe_forward_f16w(W, w_off, D_off, rows_per_table, B, indices, offsets,
+                                        pooling, indice_weights, nthreads)
     W = _c(W, np.float32)
     w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
     rows = _c(rows_per_table, np.int64)
@@ -359,6 +365,22 @@ def fbgemm_tbe_forward_f32(W, w_off, D_off, rows_per_table, B, indices, offsets,
     out = np.zeros((B, total_D), dtype=np.float32)
     rc = fbgemm().fb_tbe_forward_f32(_p(W), _p(w_off), _p(D_off), T, B, _p(indices), _p(offsets),
                                      pooling, _p(iw), _p(out), total_D, _p(rows), nthreads)
+    assert rc == 0, f"FBGEMM SpMDM kernel reported failure ({rc})"
+    return out
+
+
+def _fbgemm_tbe_forward_f16w(W, w_off, D_off, rows_per_table, B, indices, offsets, pooling,
+                             indice_weights, nthreads):
+    W = _c(W, np.float16)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    rows = _c(rows_per_table, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    iw = _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    total_D = int(D_off[-1])
+    out = np.zeros((B, total_D), dtype=np.float32)
+    rc = fbgemm().fb_tbe_forward_f16w(_p(W), _p(w_off), _p(D_off), T, B, _p(indices), _p(offsets),
+                                      pooling, _p(iw), _p(out), total_D, _p(rows), nthreads)
     assert rc == 0, f"FBGEMM SpMDM kernel reported failure ({rc})"
     return out
 

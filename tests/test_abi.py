@@ -84,26 +84,44 @@ def test_workspace_sizes_grow(lib):
 def test_bad_arguments_rejected_before_any_launch(lib):
     lib.mx_last_error.restype = ctypes.c_char_p
     P = ctypes.c_void_p
+    i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
     f = lib.mx_tbe_forward
-    f.argtypes = [P, P, P, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, P, P, ctypes.c_int32,
-                  ctypes.c_int32, P, P, ctypes.c_int32, ctypes.c_int64, P]
+    f.argtypes = [P, i32, P, P, i32, i64, i32, P, P, i32, i32, P, P, i32, i64, P]
     # index_bytes 3 is invalid
-    assert f(None, None, None, 1, 1, 128, None, None, 3, 0, None, None, 0, 128, None) == -1
+    assert f(None, 0, None, None, 1, 1, 128, None, None, 3, 0, None, None, 0, 128, None) == -1
     assert b"int32 or int64" in lib.mx_last_error()
     # max_D not a multiple of 4
-    assert f(None, None, None, 1, 1, 130, None, None, 8, 0, None, None, 0, 130, None) == -1
+    assert f(None, 0, None, None, 1, 1, 130, None, None, 8, 0, None, None, 0, 130, None) == -1
+    assert b"multiple of 4" in lib.mx_last_error()
     # pooling NONE is not served
-    assert f(None, None, None, 1, 1, 128, None, None, 8, 2, None, None, 0, 128, None) == -1
-    # empty problem: success without touching the device
-    assert f(None, None, None, 0, 0, 128, None, None, 8, 0, None, None, 0, 128, None) == 0
+    assert f(None, 0, None, None, 1, 1, 128, None, None, 8, 2, None, None, 0, 128, None) == -1
+    assert b"pooling_mode" in lib.mx_last_error()
+    # bf16 weights are not served
+    assert f(None, 5, None, None, 1, 1, 128, None, None, 8, 0, None, None, 0, 128, None) == -1
+    assert b"weights type" in lib.mx_last_error()
+    # empty problem: success without touching the device (fp32 and fp16 weights)
+    assert f(None, 0, None, None, 0, 0, 128, None, None, 8, 0, None, None, 0, 128, None) == 0
+    assert f(None, 1, None, None, 0, 0, 128, None, None, 8, 0, None, None, 0, 128, None) == 0
     g = lib.mx_nbit_forward
-    g.argtypes = [P, P, P, P, ctypes.c_int32, ctypes.c_int64] + [ctypes.c_int32] * 5 + \
-        [P, P, ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int64, P]
+    g.argtypes = [P, P, P, P, i32, i64] + [i32] * 5 + \
+        [P, P, i32, i32, P, i32, i32, P, i64, P]
     assert g(None, None, None, None, 1, 1, 0, 0, 2048, 0, 0, None, None, 4, 0, None, 1, 16, None,
              2048, None) == -1  # max D above 1024
     assert b"1024" in lib.mx_last_error()
     h = lib.mx_tbe_backward_rowwise_adagrad
     h.restype = ctypes.c_int
-    assert h(None, None, None, 1, 4, 128, None, 23, None, None, 8, ctypes.c_int64(10), 0, None,
-             ctypes.c_int64(128), None, None, ctypes.c_float(0.1), ctypes.c_float(1e-8),
-             ctypes.c_float(0.0), 7, None, ctypes.c_size_t(0), None) == -1  # weight_decay_mode 7
+    h.argtypes = [P, i32, P, P, i32, i64, i32, P, i32, P, P, i32, i64, i32, P, P, i64, P, P,
+                  f32, f32, f32, i32, i32, ctypes.c_uint64, P, ctypes.c_size_t, P]
+    args = [None, 0, None, None, 1, 4, 128, None, 23, None, None, 8, 10, 0, None, None, 128,
+            None, None, 0.1, 1e-8, 0.0, 0, 0, 0, None, 0, None]
+    bad_mode = list(args)
+    bad_mode[22] = 7  # weight_decay_mode
+    assert h(*bad_mode) == -1
+    assert b"weight_decay_mode" in lib.mx_last_error()
+    bad_ty = list(args)
+    bad_ty[1] = 2  # INT8 training weights
+    assert h(*bad_ty) == -1
+    assert b"weights type" in lib.mx_last_error()
+    empty = list(args)
+    empty[12] = 0  # N = 0: nothing to do
+    assert h(*empty) == 0

@@ -277,3 +277,157 @@ def test_module_training_step_weighted(dev, pooling):
         orc.info_B_num_bits(3, 24), indice_weights=iw)
     np.testing.assert_allclose(tbe.weights_dev.detach().cpu().numpy(), W_exp, rtol=RTOL, atol=ATOL)
     np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)
+
+
+# ---- fp16 weights: round-to-nearest-even or stochastic rounding -------------
+
+def _f16_bracket(u: np.ndarray, rel: float = 2e-6):
+    """fp16 values bracketing fp32 ``u`` widened by ``rel`` (the GPU's fp32
+    update may differ from the oracle's in its last bits): (lower, upper)."""
+    a = u - np.abs(u) * rel
+    b = u + np.abs(u) * rel
+    la = a.astype(np.float16)
+    la = np.where(la.astype(np.float32) > a, np.nextafter(la, np.float16(-np.inf)), la)
+    hb = b.astype(np.float16)
+    hb = np.where(hb.astype(np.float32) < b, np.nextafter(hb, np.float16(np.inf)), hb)
+    return la, hb
+
+
+def _fp16_update(dev, inp, sr, seed=0, lr=0.05, eps=1e-6, pooling=0, weighted=False):
+    rng = np.random.default_rng(seed)
+    W16 = rng.uniform(-1, 1, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float16)
+    m1 = rng.uniform(0, 1e-3, size=sum(inp.E)).astype(np.float32)
+    m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
+    grad = rng.normal(0, 1e-1, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(0.5, 1.5, inp.N).astype(np.float32) if weighted else None
+    u, m1_exp = orc.backward_rowwise_adagrad(
+        W16.astype(np.float32), weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
+        0.0, 0, orc.info_B_num_bits(inp.T, inp.B), indice_weights=iw)
+    Wd = torch.from_numpy(W16).to(dev)
+    m1d = torch.from_numpy(m1).to(dev)
+    empty = torch.zeros(0, device=dev)
+    head = (torch.from_numpy(grad).to(dev), Wd, empty, empty,
+            torch.zeros(inp.T, dtype=torch.int32, device=dev),
+            torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
+            max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+            torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling)
+    tail = (torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, sr, m1d, empty,
+            torch.zeros(inp.T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
+            eps, lr, 0.0, 0, 0.0)
+    if weighted:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda(
+            *head, torch.from_numpy(iw).to(dev), *tail)
+    else:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+            *head, *tail)
+    np.testing.assert_allclose(m1d.cpu().numpy(), m1_exp, rtol=RTOL, atol=0)
+    got = Wd.cpu().numpy()
+    untouched = u == W16.astype(np.float32)
+    assert np.array_equal(got[untouched].view(np.uint16), W16[untouched].view(np.uint16))
+    lo, hi = _f16_bracket(u)
+    gf = got.astype(np.float32)
+    out = (gf < lo.astype(np.float32)) | (gf > hi.astype(np.float32))
+    assert not out.any(), f"{out.sum()} fp16 results outside the bracket of the fp32 update"
+    return got, u, ~untouched
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_fp16_weights_round_to_nearest(dev, pooling, weighted):
+    """stochastic_rounding=False: the fp16 result is the fp32 update rounded
+    to nearest even (equal to numpy's rounding of the oracle's fp32 update
+    except within a few fp32 ulps of a tie)."""
+    print(f"[case] fp16 weights RNE pool={pooling} weighted={weighted}", flush=True)
+    rng = np.random.default_rng(41)
+    inp = random_tbe(rng, 2, 300, [128, 64], [2000, 500], 20)
+    got, u, touched = _fp16_update(dev, inp, False, seed=3, pooling=pooling, weighted=weighted)
+    rn = u.astype(np.float16)
+    same = got[touched].view(np.uint16) == rn[touched].view(np.uint16)
+    assert same.mean() > 0.995, same.mean()
+
+
+def _sr_statistics(got, u, touched):
+    """Fraction of elements rounded away from zero, per decile of their
+    distance from the toward-zero neighbour (in fp16 places)."""
+    uz = u[touched]
+    g = got[touched].astype(np.float32)
+    rz = uz.astype(np.float16)  # RNE first, then step toward zero where it overshot
+    rz = np.where(np.abs(rz.astype(np.float32)) > np.abs(uz),
+                  np.nextafter(rz, np.float16(0)), rz)
+    ulp = np.abs(np.nextafter(rz, np.sign(uz).astype(np.float16) * np.float16(np.inf))
+                 .astype(np.float32) - rz.astype(np.float32))
+    f = (np.abs(uz) - np.abs(rz.astype(np.float32))) / ulp
+    away = g != rz.astype(np.float32)
+    keep = (f > 1e-3) & (f < 1 - 1e-3) & np.isfinite(f)  # skip (near-)representable values
+    return f[keep], away[keep]
+
+
+def test_fp16_weights_stochastic_rounding(dev):
+    """stochastic_rounding=True: every result is one of the two fp16
+    neighbours of the fp32 update, rounded away from zero with probability
+    equal to its distance from the toward-zero neighbour (checked per decile
+    over ~200k elements), and the same torch seed gives the same result."""
+    print("[case] fp16 weights stochastic rounding", flush=True)
+    rng = np.random.default_rng(43)
+    inp = random_tbe(rng, 2, 1024, [128, 128], [1500, 1500], 30, empty_frac=0.0)
+    torch.manual_seed(123)
+    got, u, touched = _fp16_update(dev, inp, True, seed=5)
+    f, away = _sr_statistics(got, u, touched)
+    assert f.size > 100_000, f.size
+    for lo_ in np.arange(0, 1, 0.1):
+        sel = (f >= lo_) & (f < lo_ + 0.1)
+        assert sel.sum() > 2000
+        p = away[sel].mean()
+        assert abs(p - f[sel].mean()) < 0.03, (lo_, p, f[sel].mean())
+    torch.manual_seed(123)
+    again, _, _ = _fp16_update(dev, inp, True, seed=5)
+    assert np.array_equal(again.view(np.uint16), got.view(np.uint16))
+    torch.manual_seed(124)
+    other, _, _ = _fp16_update(dev, inp, True, seed=5)
+    assert not np.array_equal(other.view(np.uint16), got.view(np.uint16))
+
+
+@pytest.mark.parametrize("sr", [False, True])
+def test_module_training_step_fp16(dev, sr):
+    """fp16 weights through the module (weighted, per-sample-weight gradient):
+    forward bit-exact vs the oracle on the widened weights; the update within
+    the fp16 bracket of the oracle's fp32 update."""
+    print(f"[case] module fp16 training step sr={sr}", flush=True)
+    from mx_fbgemm import ComputeDevice, EmbeddingLocation, PoolingMode, SparseType
+    from mx_fbgemm.split_table_batched_embeddings_ops_training import (
+        SplitTableBatchedEmbeddingBagsCodegen,
+    )
+
+    specs = [(300, 64, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (200, 128, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)]
+    tbe = SplitTableBatchedEmbeddingBagsCodegen(
+        specs, pooling_mode=PoolingMode.SUM, learning_rate=0.05, eps=1e-6, device=dev,
+        weights_init=(-1.0, 1.0), weights_precision=SparseType.FP16, stochastic_rounding=sr)
+    assert tbe.weights_dev.dtype == torch.float16
+    rng = np.random.default_rng(17)
+    inp = random_tbe(rng, 2, 40, [64, 128], [300, 200], 10)
+    iw = rng.uniform(0.5, 1.5, inp.N).astype(np.float32)
+    psw = torch.from_numpy(iw).to(dev).requires_grad_()
+    W0 = tbe.weights_dev.detach().cpu().numpy().copy()
+    out = tbe(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), psw)
+    exp = orc.tbe_forward_f32(W0, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, 0, iw)
+    assert out.dtype == torch.float32 and np.array_equal(out.detach().cpu().numpy(), exp)
+    gout = rng.normal(0, 1, size=out.shape).astype(np.float32)
+    out.backward(torch.from_numpy(gout).to(dev))
+    giw = orc.grad_indice_weights(gout, W0, weight_offsets(inp), inp.D_offsets, inp.B,
+                                  inp.indices, inp.offsets, 0)
+    mag = orc.grad_indice_weights(np.abs(gout), np.abs(W0).astype(np.float32),
+                                  weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                                  inp.offsets, 0)
+    assert np.all(np.abs(psw.grad.cpu().numpy() - giw) <= 1e-5 * mag + 1e-30)
+    u, m_exp = orc.backward_rowwise_adagrad(
+        W0.astype(np.float32), weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, 0, gout, np.zeros(500, np.float32),
+        np.array([0, 300], np.int64), 0.05, 1e-6, 0.0, 0, orc.info_B_num_bits(2, 40),
+        indice_weights=iw)
+    np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)
+    got = tbe.weights_dev.detach().cpu().numpy().astype(np.float32)
+    lo, hi = _f16_bracket(u)
+    assert np.all((got >= lo.astype(np.float32)) & (got <= hi.astype(np.float32)))

@@ -50,6 +50,26 @@ def test_forward_matches_oracle(dev, T, B, dims, rows, max_L, pooling, index_dty
     _exact(got, exp)
 
 
+@pytest.mark.parametrize("T,B,dims,rows,max_L", SHAPES[1:4])
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_fp16_weights_match_oracle(dev, T, B, dims, rows, max_L, pooling, weighted):
+    """fp16 weight rows, fp32 output: each weight widened to fp32, summed in
+    index order -- bit-exact to the oracle (itself bit-exact to FBGEMM's
+    fp16-input CPU kernel)."""
+    print(f"[case] tbe fwd fp16 weights T={T} B={B} dims={dims} pool={pooling} w={weighted}",
+          flush=True)
+    rng = np.random.default_rng(20 + T * B)
+    inp = random_tbe(rng, T, B, dims, rows, max_L)
+    W16 = rng.uniform(-1, 1, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float16)
+    iw = rng.uniform(0, 2, size=inp.N).astype(np.float32) if weighted else None
+    exp = orc.tbe_forward_f32(W16, weight_offsets(inp), inp.D_offsets, B, inp.indices,
+                              inp.offsets, pooling, iw)
+    got = tbe_forward_gpu(dev, torch.from_numpy(W16).to(dev), inp, pooling,
+                          indice_weights=None if iw is None else torch.from_numpy(iw))
+    _exact(got, exp)
+
+
 @pytest.mark.parametrize("pooling", [0, 1])
 def test_weighted_and_fp16_out(dev, pooling):
     print(f"[case] tbe fwd weighted + fp16 out pool={pooling}", flush=True)

@@ -116,6 +116,22 @@ def test_tbe_forward_vs_fbgemm_cpu(pooling, weighted):
 
 
 @pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_tbe_forward_fp16_weights_vs_fbgemm_cpu(pooling, weighted):
+    """fp16 weight rows: the oracle widens each weight to fp32 and sums in
+    index order; FBGEMM's fp16-input SpMDM kernel (fp32 output) must agree
+    bit for bit."""
+    inp, W = _tbe_case(7)
+    W16 = W.astype(np.float16)
+    iw = np.random.default_rng(8).uniform(0, 2, inp.N).astype(np.float32) if weighted else None
+    got = orc.tbe_forward_f32(W16, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,
+                              inp.offsets, pooling, iw)
+    exp = orc.fbgemm_tbe_forward_f32(W16, weight_offsets(inp), inp.D_offsets, inp.E, inp.B,
+                                     inp.indices, inp.offsets, pooling, iw, nthreads=2)
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
 def test_tbe_forward_vs_embedding_bag(pooling):
     inp, W = _tbe_case(5)
     got = orc.tbe_forward_f32(W, weight_offsets(inp), inp.D_offsets, inp.B, inp.indices,

@@ -13,6 +13,7 @@
 // status becomes a RuntimeError carrying mx_last_error().  No CPU kernels
 // are registered: CPU tensors raise the dispatcher's NotImplementedError.
 #include <ATen/ATen.h>
+#include <ATen/hip/HIPGeneratorImpl.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/custom_function.h>
@@ -305,6 +306,24 @@ void check_device_placement(const Tensor& placements, const Tensor& uvm, const c
   }
 }
 
+// Element type of TBE training weights: fp32 or fp16 rows.
+int32_t weights_ty_of(const Tensor& w) {
+  TORCH_CHECK(w.is_contiguous(), "dev_weights must be contiguous");
+  if (w.scalar_type() == at::kFloat) return MX_SPARSE_FP32;
+  if (w.scalar_type() == at::kHalf) return MX_SPARSE_FP16;
+  TORCH_CHECK(false, "dev_weights must be fp32 or fp16, got ", w.scalar_type());
+  return -1;
+}
+
+// Seed of one stochastic-rounding update: drawn from the device's default
+// generator (so torch.manual_seed makes it reproducible) and advanced per call.
+uint64_t next_rounding_seed(const Tensor& on) {
+  auto gen = at::cuda::detail::getDefaultCUDAGenerator(on.device().index());
+  std::lock_guard<std::mutex> lock(gen.mutex());
+  const auto inputs = at::check_generator<at::CUDAGeneratorImpl>(gen)->philox_engine_inputs(4);
+  return inputs.first ^ (inputs.second * 0xD1B54A32D192ED03ull);
+}
+
 Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
                    const Tensor& weights_placements, const Tensor& weights_offsets,
                    const Tensor& D_offsets, int64_t total_D, int64_t max_D, const Tensor& indices,
@@ -315,7 +334,7 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
   for (auto* t : {&weights_offsets, &D_offsets, &indices, &offsets}) check_gpu(*t, "TBE argument");
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
   (void)weights_placements;  // validated once by the module; avoided here (host sync)
-  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat, "dev_weights must be fp32");
+  const int32_t wty = weights_ty_of(dev_weights);
   TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
   TORCH_CHECK(D_offsets.scalar_type() == at::kInt, "D_offsets must be int32");
   const int32_t ib = index_bytes_of(indices, "indices");
@@ -339,7 +358,7 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
   auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
   Tensor out = at::empty({B, total_D}, opts);
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
-  MX_CALL(mx_tbe_forward(dev_weights.data_ptr<float>(), weights_offsets.data_ptr<int64_t>(),
+  MX_CALL(mx_tbe_forward(dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
                          D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B,
                          static_cast<int32_t>(max_D), idx.data_ptr(), off.data_ptr(), ib,
                          static_cast<int32_t>(pooling_mode), iw, out.data_ptr(),
@@ -444,7 +463,6 @@ Tensor backward_rowwise_adagrad_impl(
   (void)lxu_cache_locations;
   (void)BT_block_size;
   (void)max_segment_length_per_warp;
-  (void)stochastic_rounding;  // fp32 weights: no rounding step
   (void)momentum1_placements;
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
@@ -454,8 +472,7 @@ Tensor backward_rowwise_adagrad_impl(
   TORCH_CHECK(uvm_weights.numel() == 0 && momentum1_uvm.numel() == 0,
               "UVM storage is not supported (DEVICE placement only)");
   TORCH_CHECK(max_norm == 0.0, "max_norm is not supported");
-  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat && dev_weights.is_contiguous(),
-              "dev_weights must be contiguous fp32");
+  const int32_t wty = weights_ty_of(dev_weights);
   TORCH_CHECK(momentum1_dev.scalar_type() == at::kFloat && momentum1_dev.is_contiguous(),
               "momentum1_dev must be contiguous fp32");
   TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
@@ -483,8 +500,11 @@ Tensor backward_rowwise_adagrad_impl(
                 " entries but there are ", N, " indices");
     iwc = indice_weights.contiguous();
   }
+  // fp16 weights: the update rounds stochastically when asked (fp32: no rounding step).
+  const bool sr = wty == MX_SPARSE_FP16 && stochastic_rounding;
+  const uint64_t seed = sr ? next_rounding_seed(dev_weights) : 0;
   MX_CALL(mx_tbe_backward_rowwise_adagrad(
-      dev_weights.data_ptr<float>(), weights_offsets.data_ptr<int64_t>(),
+      dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
       D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B, static_cast<int32_t>(max_D),
       hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(total_hash_size_bits),
       idx.data_ptr(), off.data_ptr(), ib, N, static_cast<int32_t>(pooling_mode),
@@ -492,7 +512,8 @@ Tensor backward_rowwise_adagrad_impl(
       momentum1_dev.data_ptr<float>(),
       momentum1_offsets.data_ptr<int64_t>(), static_cast<float>(learning_rate),
       static_cast<float>(eps), static_cast<float>(weight_decay),
-      static_cast<int32_t>(weight_decay_mode), ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
+      static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0, seed, ws.data_ptr(), ws_bytes,
+      stream_of(dev_weights)));
   return at::empty({0}, dev_weights.options());
 }
 
@@ -554,8 +575,7 @@ Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
   for (auto* t : {&grad_output, &weights_offsets, &D_offsets, &indices, &offsets})
     check_gpu(*t, "grad_indice_weights argument");
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM storage is not supported (DEVICE placement only)");
-  TORCH_CHECK(dev_weights.scalar_type() == at::kFloat && dev_weights.is_contiguous(),
-              "dev_weights must be contiguous fp32");
+  const int32_t wty = weights_ty_of(dev_weights);
   TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
   TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
   TORCH_CHECK(D_offsets.scalar_type() == at::kInt, "D_offsets must be int32");
@@ -574,9 +594,9 @@ Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
     frg = feature_requires_grad->to(at::kInt).contiguous();
   }
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
-  Tensor out = at::empty({indices.numel()}, dev_weights.options());
+  Tensor out = at::empty({indices.numel()}, dev_weights.options().dtype(at::kFloat));
   MX_CALL(mx_tbe_grad_indice_weights(
-      g.data_ptr<float>(), g.size(1), dev_weights.data_ptr<float>(),
+      g.data_ptr<float>(), g.size(1), dev_weights.data_ptr(), wty,
       weights_offsets.data_ptr<int64_t>(), D_offsets.data_ptr<int32_t>(),
       static_cast<int32_t>(T), B, static_cast<int32_t>(max_D_sym.expect_int()), idx.data_ptr(),
       off.data_ptr(), ib, static_cast<int32_t>(pooling_mode),
@@ -598,7 +618,8 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
                         const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
                         const Tensor& momentum1_placements, const Tensor& momentum1_offsets,
                         double eps, double learning_rate, double weight_decay,
-                        int64_t weight_decay_mode, double max_norm, int64_t output_dtype) {
+                        int64_t weight_decay_mode, double max_norm, int64_t output_dtype,
+                        bool stochastic_rounding) {
     (void)placeholder;
     // Stored as IValues: the backward updates dev_weights/momentum1 in place.
     auto& s = ctx->saved_data;
@@ -626,6 +647,7 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     s["weight_decay"] = weight_decay;
     s["weight_decay_mode"] = weight_decay_mode;
     s["max_norm"] = max_norm;
+    s["stochastic_rounding"] = stochastic_rounding;
     at::AutoDispatchBelowADInplaceOrView g;
     return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
                        total_D, max_D, indices, offsets, pooling_mode, indice_weights,
@@ -637,7 +659,7 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
   // per argument.
   static constexpr size_t kIndiceWeightsArg = 13;
   static constexpr size_t kIndiceWeightsEdge = 9;
-  static constexpr size_t kNumInputs = 25;
+  static constexpr size_t kNumInputs = 26;
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     auto& s = ctx->saved_data;
@@ -665,7 +687,8 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
         s["D_offsets"].toTensor(), c10::SymInt(s["max_D"].toInt()),
         s["hash_size_cumsum"].toTensor(), s["total_hash_size_bits"].toInt(),
         s["indices"].toTensor(), s["offsets"].toTensor(), s["pooling_mode"].toInt(), iw, empty,
-        0, 0, false, s["momentum1_dev"].toTensor(), s["momentum1_uvm"].toTensor(),
+        0, 0, s["stochastic_rounding"].toBool(), s["momentum1_dev"].toTensor(),
+        s["momentum1_uvm"].toTensor(),
         s["momentum1_placements"].toTensor(), s["momentum1_offsets"].toTensor(),
         s["eps"].toDouble(), s["learning_rate"].toDouble(), s["weight_decay"].toDouble(),
         s["weight_decay_mode"].toInt(), s["max_norm"].toDouble());
@@ -687,7 +710,6 @@ Tensor lookup_rowwise_adagrad(
     int64_t output_dtype) {
   (void)lxu_cache_weights;
   (void)lxu_cache_locations;
-  (void)stochastic_rounding;
   TORCH_CHECK(!gradient_clipping || max_gradient <= 0.0, "gradient clipping is not supported");
   return LookupRowwiseAdagrad::apply(
       placeholder_autograd_tensor, dev_weights, uvm_weights, weights_placements, weights_offsets,
@@ -695,7 +717,7 @@ Tensor lookup_rowwise_adagrad(
       indices, offsets, pooling_mode, indice_weights, feature_requires_grad, momentum1_dev,
       momentum1_uvm, momentum1_placements,
       momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm,
-      output_dtype);
+      output_dtype, stochastic_rounding);
 }
 
 // ---------------------------------------------------------------------------

@@ -552,7 +552,7 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
 constexpr int kMaxCachedTables = 512;  // table metadata kept in LDS up to this T
 
 struct BwdArgs {
-  float* W;
+  void* W;  // fp32 or fp16 rows (the kernels' WT)
   const int64_t* w_off;
   const int32_t* D_off;
   const int64_t* hsc;
@@ -579,6 +579,8 @@ struct BwdArgs {
   float lr;
   float eps;
   float wd;
+  int32_t sr;     // fp16 weights: stochastic rounding instead of round-to-nearest-even
+  uint64_t seed;  // random bits of the stochastic rounding: hash(seed, element)
 };
 
 // Per-table metadata, staged in LDS when T is small enough.
@@ -690,13 +692,68 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
   }
 }
 
+// ---- weight rows: fp32, or fp16 with round-to-nearest-even / stochastic
+// rounding of the updated value ---------------------------------------------
+
+__device__ __forceinline__ void ld_row4(const float* p, float (&v)[4]) { ld4(p, v); }
+
+__device__ __forceinline__ void ld_row4(const __half* p, float (&v)[4]) {
+  const uint2 x = *reinterpret_cast<const uint2*>(p);
+  v[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.x & 0xffffu)));
+  v[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.x >> 16)));
+  v[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.y & 0xffffu)));
+  v[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.y >> 16)));
+}
+
+// 32 random bits for element `elem` of a call seeded with `seed`: the
+// splitmix64 output function (Steele, Lea, Flood 2014) of seed + elem * golden.
+__device__ __forceinline__ uint32_t sr_bits(uint64_t seed, uint64_t elem) {
+  uint64_t z = seed + elem * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return static_cast<uint32_t>(z >> 32);
+}
+
+// Stochastic rounding to fp16: add to |x| a uniform amount below fp16's last
+// place at x's binade (13 random bits in the fp32 mantissa positions fp16
+// drops), then round toward zero, so x rounds up with probability equal to
+// its distance from the lower neighbour.  The noise is the exact difference
+// of two fp32 values of x's sign and exponent.
+__device__ __forceinline__ __half round_half_sr(float x, uint32_t rnd) {
+  const uint32_t signexp = __float_as_uint(x) & 0xff800000u;
+  const float noise = __uint_as_float(signexp | (rnd >> 19)) - __uint_as_float(signexp);
+  return __float2half_rz(x + noise);
+}
+
+__device__ __forceinline__ void st_row4(const BwdArgs&, float* p, int64_t, const float (&v)[4]) {
+  st4(p, v);
+}
+
+// elem: index of p[0] in the weights buffer (keys the random bits).
+__device__ __forceinline__ void st_row4(const BwdArgs& a, __half* p, int64_t elem,
+                                        const float (&v)[4]) {
+  __half h[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    h[e] = a.sr ? round_half_sr(v[e], sr_bits(a.seed, static_cast<uint64_t>(elem + e)))
+                : __float2half_rn(v[e]);
+  uint2 x;
+  x.x = static_cast<uint32_t>(__half_as_ushort(h[0])) |
+        (static_cast<uint32_t>(__half_as_ushort(h[1])) << 16);
+  x.y = static_cast<uint32_t>(__half_as_ushort(h[2])) |
+        (static_cast<uint32_t>(__half_as_ushort(h[3])) << 16);
+  *reinterpret_cast<uint2*>(p) = x;
+}
+
 // Rowwise Adagrad on one row held by a G-lane group (lane k owns columns
 // (c*G + k)*4 .. +4): h += mean(g^2), m = lr / (sqrt(h) + eps),
-// w = fma(-m, g, c*w); lane 0 of the group writes h.
-template <int G, int NCH>
+// w = fma(-m, g, c*w); lane 0 of the group writes h.  `row0` is the
+// weights-buffer index of the row's first element.
+template <int G, int NCH, typename WT>
 __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int k,
                                                const float (&gs)[NCH][4], const float (&w)[NCH][4],
-                                               float* wrow, float* hp, float h0) {
+                                               WT* wrow, int64_t row0, float* hp, float h0) {
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -722,7 +779,7 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
     float nw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) nw[e] = __builtin_fmaf(-mult, gs[c][e], __fmul_rn(corr, w[c][e]));
-    st4(wrow + (c * G + k) * 4, nw);
+    st_row4(a, wrow + (c * G + k) * 4, row0 + (c * G + k) * 4, nw);
   }
   if (k == 0) *hp = h;
 }
@@ -736,7 +793,7 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
 // update.
 constexpr int kLongRange = 4;  // chunks per block range
 
-template <int G, int NCH, int U>
+template <typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
   __shared__ TableMeta meta;
   constexpr int NG = 256 / G;
@@ -807,13 +864,14 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
             gs[c][e] = x;
           }
         const int64_t idx = a.run[r] - mv.hsc(t);
-        float* wrow = a.W + mv.w_off(t) + idx * D;
+        const int64_t row0 = mv.w_off(t) + idx * D;
+        WT* wrow = static_cast<WT*>(a.W) + row0;
         float* hp = a.m1 + mv.m1_off(t) + idx;
         float w[NCH][4];
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
-          if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
-        adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, *hp);
+          if ((c * G + k) * 4 < D) ld_row4(wrow + (c * G + k) * 4, w[c]);
+        adagrad_update<G, NCH>(a, D, k, gs, w, wrow, row0, hp, *hp);
       }
       __syncthreads();
     }
@@ -880,7 +938,7 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
 // gradient sum in sorted order, rowwise Adagrad, in-place update.  The
 // table of a run comes from the first batch of infos, which is kept for the
 // gradient sum.
-template <typename I, int G, int NCH, int U>
+template <typename I, typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
   __shared__ TableMeta meta;
   stage_meta(a, meta);
@@ -901,12 +959,13 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
     const int32_t D0 = mv.D_off(t);
     const int32_t D = mv.D_off(t + 1) - D0;
     const int64_t idx = ckey - mv.hsc(t);
-    float* wrow = a.W + mv.w_off(t) + idx * D;
+    const int64_t row0 = mv.w_off(t) + idx * D;
+    WT* wrow = static_cast<WT*>(a.W) + row0;
     float* hp = a.m1 + mv.m1_off(t) + idx;
     float w[NCH][4];
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
-      if ((c * G + k) * 4 < D) ld4(wrow + (c * G + k) * 4, w[c]);
+      if ((c * G + k) * 4 < D) ld_row4(wrow + (c * G + k) * 4, w[c]);
     const float h0 = *hp;
     float gs[NCH][4];
 #pragma unroll
@@ -914,11 +973,11 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
     group_sum_occurrences<I, G, NCH, U>(a, t, D0, D, cs0, cs1, g, k, info0, gs);
-    adagrad_update<G, NCH>(a, D, k, gs, w, wrow, hp, h0);
+    adagrad_update<G, NCH>(a, D, k, gs, w, wrow, row0, hp, h0);
   }
 }
 
-template <typename I, int G, int NCH>
+template <typename I, typename WT, int G, int NCH>
 int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   constexpr int U = NCH <= 1 ? 4 : 2;   // runs are short: keep registers low
   constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
@@ -930,21 +989,21 @@ int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   MX_LAUNCH_CHECK();
   const int64_t long_cap = static_cast<int64_t>(num_cus()) * 16;
   const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
-  bwd_long_run_kernel<G, NCH, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
+  bwd_long_run_kernel<WT, G, NCH, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
-  bwd_update_kernel<I, G, NCH, U><<<grid, 256, 0, s>>>(a);
+  bwd_update_kernel<I, WT, G, NCH, U><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
 
 // Lanes per run (G) and float4 chunks per lane (NCH) from the widest table.
-template <typename I>
+template <typename I, typename WT>
 int dispatch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
-  if (a.max_D <= 64) return launch_bwd<I, 16, 1>(a, N, s);
-  if (a.max_D <= 128) return launch_bwd<I, 16, 2>(a, N, s);
-  if (a.max_D <= 256) return launch_bwd<I, 32, 2>(a, N, s);
-  if (a.max_D <= 512) return launch_bwd<I, 64, 2>(a, N, s);
-  return launch_bwd<I, 64, 4>(a, N, s);
+  if (a.max_D <= 64) return launch_bwd<I, WT, 16, 1>(a, N, s);
+  if (a.max_D <= 128) return launch_bwd<I, WT, 16, 2>(a, N, s);
+  if (a.max_D <= 256) return launch_bwd<I, WT, 32, 2>(a, N, s);
+  if (a.max_D <= 512) return launch_bwd<I, WT, 64, 2>(a, N, s);
+  return launch_bwd<I, WT, 64, 4>(a, N, s);
 }
 
 struct BwdWs {
@@ -1053,13 +1112,13 @@ extern "C" size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_
 }
 
 extern "C" int mx_tbe_backward_rowwise_adagrad(
-    float* weights, const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
-    int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
+    int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
     int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
     float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
-    float weight_decay, int32_t weight_decay_mode, void* workspace, size_t workspace_bytes,
-    void* stream) {
+    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
+    void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   const int32_t nb = mx_tbe_info_B_num_bits(T, B);
   MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
@@ -1070,6 +1129,8 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
              "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
   MX_REQUIRE(weight_decay_mode >= 0 && weight_decay_mode <= 2,
              "weight_decay_mode %d not supported (0 none, 1 L2, 2 decoupled)", weight_decay_mode);
+  MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
+             "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
   if (N == 0) return MX_OK;
   MX_REQUIRE(weights && weights_offsets && D_offsets && hash_size_cumsum && indices && offsets &&
                  grad_output && momentum1 && momentum1_offsets,
@@ -1117,5 +1178,11 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   a.lr = learning_rate;
   a.eps = eps;
   a.wd = weight_decay;
-  return index_bytes == 8 ? dispatch_bwd<int64_t>(a, N, s) : dispatch_bwd<int32_t>(a, N, s);
+  a.sr = stochastic_rounding != 0 ? 1 : 0;
+  a.seed = seed;
+  if (weights_ty == MX_SPARSE_FP16)
+    return index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, N, s)
+                            : dispatch_bwd<int32_t, __half>(a, N, s);
+  return index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, N, s)
+                          : dispatch_bwd<int32_t, float>(a, N, s);
 }

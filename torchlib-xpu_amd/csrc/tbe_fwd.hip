@@ -1,10 +1,11 @@
-// Table-batched embedding (TBE) training forward, fp32 weights, gfx950.
+// Table-batched embedding (TBE) training forward, fp32 or fp16 weights, gfx950.
 //
 // Semantics: fbgemm_gpu split_embedding_codegen_forward_{unweighted,weighted}
 // (upstream codegen/training/forward/, recalled), i.e. the pooled SpMDM of
 // torch/include/fbgemm/FbgemmEmbedding.h:26-39 applied per table:
 //   out[b, D_off[t] + d] = sum_{l in bag(t,b)} W_t[idx[l], d]   (SUM)
 //   MEAN multiplies the sum by 1/L for L > 0; an empty bag gives 0.
+// fp16 weight rows are widened to fp32 element by element before the sum.
 //
 // Design: G lanes per bag (G = 32 for D <= 128: two bags per wave64).  Lane
 // k owns 4*NCH columns, so a group reads a whole row with one coalesced
@@ -52,15 +53,26 @@ __device__ __forceinline__ void load_vec(const float* p, float (&v)[VEC]) {
   }
 }
 
+// Four consecutive weights of a row as fp32 (16 B of fp32 or 8 B of fp16).
+__device__ __forceinline__ void load_row4(const float* p, float (&v)[4]) { load_vec<4>(p, v); }
+
+__device__ __forceinline__ void load_row4(const __half* p, float (&v)[4]) {
+  const uint2 x = *reinterpret_cast<const uint2*>(p);
+  v[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.x & 0xffffu)));
+  v[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.x >> 16)));
+  v[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.y & 0xffffu)));
+  v[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.y >> 16)));
+}
+
 constexpr int kWavesPerBlock = 4;
 
 // A wave serves 64/G bags at once, G lanes per bag, lane k owning columns
 // (c*G + k)*4 .. +4 (float4 loads: a D=128 row is one 512 B access of 32
 // lanes).  Several bags per wave keep several independent offsets -> indices
 // -> rows chains in flight; each column is still summed in index order.
-template <typename I, int G, int NCH, int U, bool WEIGHTED, bool OUT_F16>
+template <typename I, typename WT, int G, int NCH, int U, bool WEIGHTED, bool OUT_F16>
 __global__ void __launch_bounds__(256)
-    tbe_fwd_group_kernel(const float* __restrict__ W, const int64_t* __restrict__ w_off,
+    tbe_fwd_group_kernel(const WT* __restrict__ W, const int64_t* __restrict__ w_off,
                          const int32_t* __restrict__ D_off, int64_t B,
                          const I* __restrict__ indices, const I* __restrict__ offsets,
                          int32_t pooling, const float* __restrict__ iw, void* __restrict__ out,
@@ -75,7 +87,7 @@ __global__ void __launch_bounds__(256)
   const int64_t b = bag - t * B;
   const int32_t D0 = D_off[t];
   const int32_t D = D_off[t + 1] - D0;
-  const float* __restrict__ Wt = W + w_off[t];
+  const WT* __restrict__ Wt = W + w_off[t];
   const int64_t start = static_cast<int64_t>(offsets[bag]);
   const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
 
@@ -99,10 +111,10 @@ __global__ void __launch_bounds__(256)
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
           const int64_t r = __shfl(my_idx, g * G + j + u, 64);
-          const float* row = Wt + r * D;
+          const WT* row = Wt + r * D;
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            if (active[c]) load_vec<4>(row + (c * G + k) * 4, v[u][c]);
+            if (active[c]) load_row4(row + (c * G + k) * 4, v[u][c]);
         }
       }
 #pragma unroll
@@ -155,10 +167,10 @@ __global__ void __launch_bounds__(256)
 // Same G-lane-per-bag mapping as the forward; the bag's gradient slice stays
 // in registers, each row's dot product is reduced over the group in a fixed
 // xor-tree order.
-template <typename I, int G, int NCH, int U>
+template <typename I, typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256)
     grad_indice_weights_kernel(const float* __restrict__ grad, int64_t total_D,
-                               const float* __restrict__ W, const int64_t* __restrict__ w_off,
+                               const WT* __restrict__ W, const int64_t* __restrict__ w_off,
                                const int32_t* __restrict__ D_off, int64_t B,
                                const I* __restrict__ indices, const I* __restrict__ offsets,
                                int32_t pooling, const int32_t* __restrict__ frg,
@@ -179,7 +191,7 @@ __global__ void __launch_bounds__(256)
   }
   const int32_t D0 = D_off[t];
   const int32_t D = D_off[t + 1] - D0;
-  const float* __restrict__ Wt = W + w_off[t];
+  const WT* __restrict__ Wt = W + w_off[t];
   bool active[NCH];
   float gv[NCH][4];
 #pragma unroll
@@ -203,7 +215,7 @@ __global__ void __launch_bounds__(256)
           const int64_t r = __shfl(my_idx, g * G + j + u, 64);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            if (active[c]) load_vec<4>(Wt + r * D + (c * G + k) * 4, v[u][c]);
+            if (active[c]) load_row4(Wt + r * D + (c * G + k) * 4, v[u][c]);
         }
       }
 #pragma unroll
@@ -224,24 +236,24 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-template <typename I, int G, int NCH, bool WEIGHTED, bool OUT_F16>
-void launch_fwd_group(hipStream_t s, const float* W, const int64_t* w_off, const int32_t* D_off,
+template <typename I, typename WT, int G, int NCH, bool WEIGHTED, bool OUT_F16>
+void launch_fwd_group(hipStream_t s, const WT* W, const int64_t* w_off, const int32_t* D_off,
                       int64_t B, const void* idx, const void* off, int32_t pooling,
                       const float* iw, void* out, int64_t total_D, int64_t nbags) {
   constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
   constexpr int P = 64 / G;
   const int64_t grid = ceil_div(nbags, kWavesPerBlock * P);
-  tbe_fwd_group_kernel<I, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
+  tbe_fwd_group_kernel<I, WT, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
       W, w_off, D_off, B, static_cast<const I*>(idx), static_cast<const I*>(off), pooling, iw, out,
       total_D, nbags);
 }
 
-template <typename I, bool WEIGHTED, bool OUT_F16>
-int dispatch_fwd(hipStream_t s, int32_t max_D, const float* W, const int64_t* w_off,
+template <typename I, typename WT, bool WEIGHTED, bool OUT_F16>
+int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off,
                  const int32_t* D_off, int64_t B, const void* idx, const void* off,
                  int32_t pooling, const float* iw, void* out, int64_t total_D, int64_t nbags) {
 #define MX_FWD_G(G, NCH) \
-  launch_fwd_group<I, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
+  launch_fwd_group<I, WT, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
   if (max_D <= 64)
     MX_FWD_G(16, 1);  // 4 bags per wave
   else if (max_D <= 128)
@@ -261,7 +273,8 @@ int dispatch_fwd(hipStream_t s, int32_t max_D, const float* W, const int64_t* w_
 
 using namespace mx;
 
-extern "C" int mx_tbe_forward(const float* weights, const int64_t* weights_offsets,
+extern "C" int mx_tbe_forward(const void* weights, int32_t weights_ty,
+                              const int64_t* weights_offsets,
                               const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
                               const void* indices, const void* offsets, int32_t index_bytes,
                               int32_t pooling_mode, const float* indice_weights, void* out,
@@ -275,6 +288,8 @@ extern "C" int mx_tbe_forward(const float* weights, const int64_t* weights_offse
              "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
   MX_REQUIRE(out_dtype == MX_SPARSE_FP32 || out_dtype == MX_SPARSE_FP16,
              "output_dtype %d not supported (FP32=0, FP16=1)", out_dtype);
+  MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
+             "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
   const int64_t nbags = static_cast<int64_t>(T) * B;
   if (nbags == 0 || total_D == 0) return MX_OK;
   MX_REQUIRE(weights && weights_offsets && D_offsets && offsets && out, "null pointer argument");
@@ -282,22 +297,36 @@ extern "C" int mx_tbe_forward(const float* weights, const int64_t* weights_offse
   auto* s = as_stream(stream);
   const bool w = indice_weights != nullptr;
   const bool h = out_dtype == MX_SPARSE_FP16;
-#define MX_ARGS s, max_D, weights, weights_offsets, D_offsets, B, indices, offsets, pooling_mode, \
-                indice_weights, out, total_D, nbags
+#define MX_ARGS(WT) s, max_D, static_cast<const WT*>(weights), weights_offsets, D_offsets, B, \
+                indices, offsets, pooling_mode, indice_weights, out, total_D, nbags
+#define MX_FWD_W(I, WT)                                                                          \
+  if (w)                                                                                         \
+    h ? dispatch_fwd<I, WT, true, true>(MX_ARGS(WT)) : dispatch_fwd<I, WT, true, false>(MX_ARGS(WT)); \
+  else                                                                                           \
+    h ? dispatch_fwd<I, WT, false, true>(MX_ARGS(WT)) : dispatch_fwd<I, WT, false, false>(MX_ARGS(WT));
+  const bool w16 = weights_ty == MX_SPARSE_FP16;
   if (index_bytes == 8) {
-    if (w) h ? dispatch_fwd<int64_t, true, true>(MX_ARGS) : dispatch_fwd<int64_t, true, false>(MX_ARGS);
-    else h ? dispatch_fwd<int64_t, false, true>(MX_ARGS) : dispatch_fwd<int64_t, false, false>(MX_ARGS);
+    if (w16) {
+      MX_FWD_W(int64_t, __half)
+    } else {
+      MX_FWD_W(int64_t, float)
+    }
   } else {
-    if (w) h ? dispatch_fwd<int32_t, true, true>(MX_ARGS) : dispatch_fwd<int32_t, true, false>(MX_ARGS);
-    else h ? dispatch_fwd<int32_t, false, true>(MX_ARGS) : dispatch_fwd<int32_t, false, false>(MX_ARGS);
+    if (w16) {
+      MX_FWD_W(int32_t, __half)
+    } else {
+      MX_FWD_W(int32_t, float)
+    }
   }
+#undef MX_FWD_W
 #undef MX_ARGS
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
 
 extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D,
-                                          const float* weights, const int64_t* weights_offsets,
+                                          const void* weights, int32_t weights_ty,
+                                          const int64_t* weights_offsets,
                                           const int32_t* D_offsets, int32_t T, int64_t B,
                                           int32_t max_D, const void* indices, const void* offsets,
                                           int32_t index_bytes, int32_t pooling_mode,
@@ -310,6 +339,8 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
   MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
              "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
+  MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
+             "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
   const int64_t nbags = static_cast<int64_t>(T) * B;
   if (nbags == 0) return MX_OK;
   MX_REQUIRE(grad_output && weights && weights_offsets && D_offsets && offsets &&
@@ -317,10 +348,17 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
              "null pointer argument");
   auto* s = as_stream(stream);
 #define MX_GIW(I, G, NCH, U)                                                                   \
-  grad_indice_weights_kernel<I, G, NCH, U><<<dim3(static_cast<uint32_t>(                      \
+  do {                                                                                         \
+    if (weights_ty == MX_SPARSE_FP16)                                                          \
+      MX_GIW_T(I, __half, G, NCH, U);                                                          \
+    else                                                                                       \
+      MX_GIW_T(I, float, G, NCH, U);                                                           \
+  } while (0)
+#define MX_GIW_T(I, WT, G, NCH, U)                                                             \
+  grad_indice_weights_kernel<I, WT, G, NCH, U><<<dim3(static_cast<uint32_t>(                  \
                                                ceil_div(nbags, kWavesPerBlock * (64 / G)))),   \
                                            256, 0, s>>>(                                      \
-      grad_output, total_D, weights, weights_offsets, D_offsets, B,                            \
+      grad_output, total_D, static_cast<const WT*>(weights), weights_offsets, D_offsets, B,    \
       static_cast<const I*>(indices), static_cast<const I*>(offsets), pooling_mode,            \
       feature_requires_grad, grad_indice_weights, nbags)
 #define MX_GIW_D(I)                 \
@@ -341,6 +379,7 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
   }
 #undef MX_GIW_D
 #undef MX_GIW
+#undef MX_GIW_T
   MX_LAUNCH_CHECK();
   return MX_OK;
 }

@@ -102,7 +102,7 @@ def build_ops(verbose: bool = False) -> Path:
         *inc, f"-I{ROCM / 'include'}", f"-I{INCLUDE}",
         str(CSRC / "ops.cpp"), "-o", str(tmp),
         *[f"-L{d}" for d in libdirs], f"-L{LIB_DIR}",
-        "-lmx_fbgemm_kernels", "-lc10_hip", "-ltorch_cpu", "-lc10", "-ltorch",
+        "-lmx_fbgemm_kernels", "-ltorch_hip", "-lc10_hip", "-ltorch_cpu", "-lc10", "-ltorch",
         "-Wl,-rpath,$ORIGIN", *[f"-Wl,-rpath,{d}" for d in libdirs],
     ]
     _run(cmd, verbose)

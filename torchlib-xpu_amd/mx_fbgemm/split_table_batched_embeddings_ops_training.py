@@ -3,8 +3,10 @@
 
 Mirrors fbgemm_gpu's SplitTableBatchedEmbeddingBagsCodegen (upstream
 fbgemm_gpu/split_table_batched_embeddings_ops_training.py, recalled) for the
-path this build serves: DEVICE placement, fp32 weights, SUM/MEAN pooling and
-the EXACT_ROWWISE_ADAGRAD optimizer fused into the backward.  Weights and the
+path this build serves: DEVICE placement, fp32 or fp16 weights
+(``weights_precision``; fp16 updates round stochastically by default, as
+upstream), SUM/MEAN pooling and the EXACT_ROWWISE_ADAGRAD optimizer fused
+into the backward.  Weights and the
 per-row momentum live in one flat HBM buffer each; tables are laid out back
 to back (weights_offsets, momentum1_offsets in elements).
 """
@@ -64,6 +66,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         device: Optional[torch.device] = None,
         weights_init: Optional[tuple[float, float]] = None,
         bounds_check_mode: BoundsCheckMode = BoundsCheckMode.WARNING,
+        weights_precision: SparseType = SparseType.FP32,
+        stochastic_rounding: bool = True,
     ) -> None:
         super().__init__()
         if optimizer != EmbOptimType.EXACT_ROWWISE_ADAGRAD:
@@ -72,6 +76,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
             raise ValueError(f"pooling_mode {pooling_mode} is not supported")
         if output_dtype != SparseType.FP32:
             raise ValueError("the training lookup produces fp32 output")
+        if weights_precision not in (SparseType.FP32, SparseType.FP16):
+            raise ValueError("weights_precision must be FP32 or FP16")
         if not embedding_specs:
             raise ValueError("at least one table is required")
         for E, D, loc, cd in embedding_specs:
@@ -90,6 +96,9 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.weight_decay = float(weight_decay)
         self.weight_decay_mode = int(weight_decay_mode)
         self.bounds_check_mode = BoundsCheckMode(bounds_check_mode)
+        self.weights_precision = weights_precision
+        # Only fp16 weights have a rounding step; fp32 updates ignore the flag.
+        self.stochastic_rounding = bool(stochastic_rounding)
         rows = [E for E, _, _, _ in embedding_specs]
         dims = [D for _, D, _, _ in embedding_specs]
         self.T = len(embedding_specs)
@@ -111,7 +120,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.register_buffer("momentum1_offsets", torch.tensor(_cumsum(rows)[:-1], **i64))
         lo, hi = weights_init if weights_init is not None else (-0.01, 0.01)
         self.weights_dev = nn.Parameter(
-            torch.empty(sum(w_elems), device=device, dtype=torch.float32).uniform_(lo, hi),
+            torch.empty(sum(w_elems), device=device, dtype=torch.float32).uniform_(lo, hi)
+            .to(weights_precision.as_dtype()),
             requires_grad=False)
         self.register_buffer("momentum1_dev",
                              torch.zeros(sum(rows), device=device, dtype=torch.float32))
@@ -152,7 +162,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
             self.D_offsets, self.total_D, self.max_D, self.hash_size_cumsum,
             self.total_hash_size_bits, indices, offsets, int(self.pooling_mode),
             per_sample_weights, feature_requires_grad,
-            self.lxu_cache_locations, False, 0.0, False, self.momentum1_dev, self.momentum1_uvm,
+            self.lxu_cache_locations, False, 0.0, self.stochastic_rounding, self.momentum1_dev,
+            self.momentum1_uvm,
             self.weights_placements, self.momentum1_offsets, self.eps, self.learning_rate,
             self.weight_decay, self.weight_decay_mode, 0.0, int(SparseType.FP32.as_int()))
 
