@@ -133,6 +133,36 @@ int mx_tbe_forward(const void* weights, int32_t weights_ty, const int64_t* weigh
                    int32_t pooling_mode, const float* indice_weights, void* out,
                    int32_t out_dtype, int64_t total_D, void* stream);
 
+/* ---- variable batch size per feature (VBE) ------------------------------- */
+
+/* Serves fbgemm::generate_vbe_metadata.  Feature (table) t has B[t][r]
+ * samples on rank r (R ranks).  Bags are flattened feature-major and, within
+ * a feature, rank-major: bag(t, b) = B_offsets[t] + b with
+ * b = B_offsets_rank_per_feature[t*(R+1) + r] + b_r.  The pooled output is one
+ * flat buffer, rank-major then feature-major; the (r, t) block starts at
+ * output_offsets_feature_rank[r*T + t].  Writes, per bag,
+ *   row_output_offsets[bag] = output_offsets_feature_rank[r*T + t] + b_r * D
+ *   b_t_map[bag]            = (t << info_B_num_bits) | b
+ * with D = D_offsets[t+1] - D_offsets[t], or fixed_D when fixed_D > 0.
+ *   B_offsets [T+1] int32, B_offsets_rank_per_feature [T][R+1] int32,
+ *   output_offsets_feature_rank [R*T+1] int64, total_B = B_offsets[T]. */
+int mx_generate_vbe_metadata(const int32_t* B_offsets, const int32_t* B_offsets_rank_per_feature,
+                             const int64_t* output_offsets_feature_rank,
+                             const int32_t* D_offsets, int32_t fixed_D, int32_t T, int32_t R,
+                             int32_t info_B_num_bits, int64_t total_B,
+                             int64_t* row_output_offsets, int32_t* b_t_map, void* stream);
+
+/* Serves fbgemm::split_embedding_codegen_forward_{unweighted,weighted}_vbe_cuda:
+ * mx_tbe_forward over total_B flattened bags (offsets [total_B+1]); bag i is
+ * table t, sample b of b_t_map[i] and its pooled row is written at
+ * out + vbe_row_output_offsets[i] (out is the flat VBE output). */
+int mx_tbe_forward_vbe(const void* weights, int32_t weights_ty, const int64_t* weights_offsets,
+                       const int32_t* D_offsets, int32_t T, int64_t total_B, int32_t max_D,
+                       const void* indices, const void* offsets, int32_t index_bytes,
+                       int32_t pooling_mode, const float* indice_weights,
+                       const int64_t* vbe_row_output_offsets, const int32_t* vbe_b_t_map,
+                       int32_t info_B_num_bits, void* out, int32_t out_dtype, void* stream);
+
 /* ---- TBE backward: transpose (sort) and fused exact rowwise Adagrad ----- */
 
 /* Number of info bits used for the bag index b in an info word
@@ -159,7 +189,18 @@ int mx_tbe_transpose_embedding_input(
     int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
     int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace needed by mx_tbe_backward_rowwise_adagrad. */
+/* VBE variant of mx_tbe_transpose_embedding_input (fbgemm's vbe_b_t_map
+ * argument): total_B flattened bags, each bag's info word taken from
+ * vbe_b_t_map; workspace from mx_tbe_transpose_workspace_bytes. */
+int mx_tbe_transpose_embedding_input_vbe(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t total_B, const int32_t* vbe_b_t_map,
+    int32_t total_hash_size_bits, int32_t info_B_num_bits, const void* indices,
+    const void* offsets, int32_t index_bytes, int64_t N, int64_t* linear_indices,
+    int64_t* sorted_linear_indices, int32_t* infos_sorted, int64_t* sorted_linear_indices_run,
+    int32_t* run_lengths, int32_t* num_runs, int32_t* cumulative_run_lengths, void* workspace,
+    size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mx_tbe_backward_rowwise_adagrad(_vbe). */
 size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, int32_t max_D);
 
 /* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_{unweighted,
@@ -189,6 +230,22 @@ int mx_tbe_backward_rowwise_adagrad(
     float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_{unweighted,
+ * weighted}_exact_vbe_cuda: mx_tbe_backward_rowwise_adagrad over total_B
+ * flattened bags (B_offsets [T+1], vbe_row_output_offsets and vbe_b_t_map
+ * [total_B] from mx_generate_vbe_metadata, b < max_B); grad_output is the flat
+ * VBE gradient, the row of bag (t, b) at vbe_row_output_offsets[B_offsets[t] + b]. */
+int mx_tbe_backward_rowwise_adagrad_vbe(
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
+    int32_t T, int64_t max_B, int32_t max_D, const int64_t* hash_size_cumsum,
+    int32_t total_hash_size_bits, const void* indices, const void* offsets, int32_t index_bytes,
+    int64_t N, int32_t pooling_mode, const float* indice_weights, const float* grad_output,
+    int64_t total_B, const int32_t* B_offsets, const int64_t* vbe_row_output_offsets,
+    const int32_t* vbe_b_t_map, int32_t info_B_num_bits, float* momentum1,
+    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
+    int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 /* Serves fbgemm::split_embedding_codegen_grad_indice_weights_cuda: the gradient
  * of a weighted lookup's per-sample weights,
  *   grad_indice_weights[l] = sum_d grad_output[b, D_off[t] + d] * W_t[indices[l], d]
@@ -202,6 +259,17 @@ int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D, const 
                                const void* offsets, int32_t index_bytes, int32_t pooling_mode,
                                const int32_t* feature_requires_grad, float* grad_indice_weights,
                                void* stream);
+
+/* VBE variant of mx_tbe_grad_indice_weights (fbgemm's
+ * split_embedding_codegen_grad_indice_weights_vbe_cuda): grad_output is the
+ * flat VBE gradient, bag i reads its row at vbe_row_output_offsets[i]. */
+int mx_tbe_grad_indice_weights_vbe(
+    const float* grad_output, const void* weights, int32_t weights_ty,
+    const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T, int64_t total_B,
+    int32_t max_D, const void* indices, const void* offsets, int32_t index_bytes,
+    int32_t pooling_mode, const int64_t* vbe_row_output_offsets, const int32_t* vbe_b_t_map,
+    int32_t info_B_num_bits, const int32_t* feature_requires_grad, float* grad_indice_weights,
+    void* stream);
 
 /* ---- index validation ---------------------------------------------------- */
 
@@ -221,6 +289,15 @@ int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B,
                             void* offsets, int32_t index_bytes, int64_t N, int32_t mode,
                             int64_t* warning, void* workspace, size_t workspace_bytes,
                             void* stream);
+
+/* VBE variant (fbgemm's B_offsets argument): total_B bags, bag i of table t
+ * for B_offsets[t] <= i < B_offsets[t+1]; workspace from
+ * mx_bounds_check_workspace_bytes_vbe(total_B). */
+size_t mx_bounds_check_workspace_bytes_vbe(int64_t total_B);
+int mx_bounds_check_indices_vbe(const int64_t* rows_per_table, int32_t T, int64_t total_B,
+                                const int32_t* B_offsets, void* indices, void* offsets,
+                                int32_t index_bytes, int64_t N, int32_t mode, int64_t* warning,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- rowwise quantization codecs ---------------------------------------- */
 

@@ -7,7 +7,8 @@
 //   * repaired offsets o'[i] = max_{j <= i} clamp(o[j], 0, N): in [0, N] and
 //     non-decreasing, so no two bags overlap and no bag runs past the indices;
 //   * every index of bag (t, b), i.e. positions [o'[t*B+b], o'[t*B+b+1]),
-//     outside [0, rows_per_table[t]) is replaced by 0;
+//     outside [0, rows_per_table[t]) is replaced by 0 (variable batch per
+//     feature: bags B_offsets[t] .. B_offsets[t+1]-1 belong to table t);
 //   * each repaired entry (offset or index) adds one to warning[0];
 //   * FATAL repairs nothing and only counts (the host raises on a non-zero
 //     count); NONE does nothing.
@@ -55,7 +56,8 @@ __global__ void __launch_bounds__(256)
 template <typename I>
 __global__ void __launch_bounds__(256)
     check_indices_kernel(const int64_t* __restrict__ rows, I* __restrict__ indices,
-                         const uint32_t* __restrict__ rep, int64_t nbags, int64_t B, int64_t N,
+                         const uint32_t* __restrict__ rep, int64_t nbags, int64_t B,
+                         const int32_t* __restrict__ B_offsets, int32_t T, int64_t N,
                          int32_t mode, unsigned long long* __restrict__ warning) {
   const int64_t l = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   uint32_t bad = 0;
@@ -68,7 +70,20 @@ __global__ void __launch_bounds__(256)
       else
         hi = mid;
     }
-    const int64_t t = lo / B;
+    int64_t t;
+    if (B_offsets) {  // last table whose first bag is <= lo
+      int32_t tl = 0, th = T;
+      while (th - tl > 1) {
+        const int32_t mid = tl + ((th - tl) >> 1);
+        if (B_offsets[mid] <= lo)
+          tl = mid;
+        else
+          th = mid;
+      }
+      t = tl;
+    } else {
+      t = lo / B;
+    }
     const int64_t idx = static_cast<int64_t>(indices[l]);
     if (idx < 0 || idx >= rows[t]) {
       bad = 1;
@@ -97,8 +112,8 @@ BoundsWs carve_bounds(uint8_t* base, int64_t n_off) {
 
 template <typename I>
 int run_bounds(const int64_t* rows, void* indices, void* offsets, int64_t nbags, int64_t B,
-               int64_t N, int32_t mode, unsigned long long* warning, const BoundsWs& w,
-               hipStream_t s) {
+               const int32_t* B_offsets, int32_t T, int64_t N, int32_t mode,
+               unsigned long long* warning, const BoundsWs& w, hipStream_t s) {
   const int64_t n_off = nbags + 1;
   zero_u64_kernel<<<1, 256, 0, s>>>(w.state, w.state_words);
   MX_LAUNCH_CHECK();
@@ -109,7 +124,7 @@ int run_bounds(const int64_t* rows, void* indices, void* offsets, int64_t nbags,
     return rc;
   if (N > 0) {
     check_indices_kernel<I><<<dim3(static_cast<uint32_t>(ceil_div(N, 256))), 256, 0, s>>>(
-        rows, static_cast<I*>(indices), w.rep, nbags, B, N, mode, warning);
+        rows, static_cast<I*>(indices), w.rep, nbags, B, B_offsets, T, N, mode, warning);
     MX_LAUNCH_CHECK();
   }
   fix_offsets_kernel<I><<<dim3(static_cast<uint32_t>(ceil_div(n_off, 256))), 256, 0, s>>>(
@@ -128,16 +143,16 @@ extern "C" size_t mx_bounds_check_workspace_bytes(int32_t T, int64_t B) {
   return carve_bounds(nullptr, static_cast<int64_t>(T) * B + 1).bytes;
 }
 
-extern "C" int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B,
-                                       void* indices, void* offsets, int32_t index_bytes,
-                                       int64_t N, int32_t mode, int64_t* warning,
-                                       void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative size");
+namespace {
+
+int bounds_impl(const int64_t* rows_per_table, int32_t T, int64_t B, int64_t nbags,
+                const int32_t* B_offsets, void* indices, void* offsets, int32_t index_bytes,
+                int64_t N, int32_t mode, int64_t* warning, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0 && nbags >= 0, "negative size");
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
   MX_REQUIRE(mode >= MX_BOUNDS_FATAL && mode <= MX_BOUNDS_NONE, "bounds_check_mode %d invalid",
              mode);
-  const int64_t nbags = static_cast<int64_t>(T) * B;
   if (mode == MX_BOUNDS_NONE || nbags == 0) return MX_OK;
   MX_REQUIRE(N < (int64_t(1) << 32), "N %lld above 2^32 indices", (long long)N);
   MX_REQUIRE(rows_per_table && offsets && warning && (indices || N == 0), "null pointer argument");
@@ -148,7 +163,36 @@ extern "C" int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T,
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   auto* wc = reinterpret_cast<unsigned long long*>(warning);
   auto* s = as_stream(stream);
-  return index_bytes == 8
-             ? run_bounds<int64_t>(rows_per_table, indices, offsets, nbags, B, N, mode, wc, w, s)
-             : run_bounds<int32_t>(rows_per_table, indices, offsets, nbags, B, N, mode, wc, w, s);
+  return index_bytes == 8 ? run_bounds<int64_t>(rows_per_table, indices, offsets, nbags, B,
+                                                B_offsets, T, N, mode, wc, w, s)
+                          : run_bounds<int32_t>(rows_per_table, indices, offsets, nbags, B,
+                                                B_offsets, T, N, mode, wc, w, s);
+}
+
+}  // namespace
+
+extern "C" int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B,
+                                       void* indices, void* offsets, int32_t index_bytes,
+                                       int64_t N, int32_t mode, int64_t* warning,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return bounds_impl(rows_per_table, T, B, static_cast<int64_t>(T) * B, nullptr, indices,
+                     offsets, index_bytes, N, mode, warning, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t mx_bounds_check_workspace_bytes_vbe(int64_t total_B) {
+  if (total_B < 0) return 0;
+  return carve_bounds(nullptr, total_B + 1).bytes;
+}
+
+extern "C" int mx_bounds_check_indices_vbe(const int64_t* rows_per_table, int32_t T,
+                                           int64_t total_B, const int32_t* B_offsets,
+                                           void* indices, void* offsets, int32_t index_bytes,
+                                           int64_t N, int32_t mode, int64_t* warning,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 1 && (total_B == 0 || B_offsets), "VBE needs B_offsets [T+1]");
+  return bounds_impl(rows_per_table, T, 0, total_B, B_offsets, indices, offsets, index_bytes, N,
+                     mode, warning, workspace, workspace_bytes, stream);
 }

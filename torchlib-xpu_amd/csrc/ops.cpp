@@ -306,6 +306,31 @@ void check_device_placement(const Tensor& placements, const Tensor& uvm, const c
   }
 }
 
+// Variable-batch-per-feature (VBE) metadata of one lookup; undefined tensors
+// mean a fixed batch B per table.
+struct VbeMeta {
+  Tensor B_offsets;  // int32 [T+1]: first bag of each table
+  Tensor row_out;    // int64 [total_B]: output (and gradient) row offset of each bag
+  Tensor b_t_map;    // int32 [total_B]: (t << info_B_num_bits) | b of each bag
+  int64_t output_size = 0;
+  int64_t info_B_num_bits = 0;
+  int64_t max_B = 0;
+  bool on() const { return b_t_map.defined(); }
+};
+
+void check_vbe(const VbeMeta& v, int64_t total_B) {
+  TORCH_CHECK(v.row_out.defined() && v.b_t_map.defined(), "VBE needs row offsets and a b_t map");
+  check_gpu(v.row_out, "vbe_row_output_offsets");
+  check_gpu(v.b_t_map, "vbe_b_t_map");
+  TORCH_CHECK(v.row_out.scalar_type() == at::kLong && v.row_out.is_contiguous() &&
+                  v.row_out.numel() == total_B,
+              "vbe_row_output_offsets must be contiguous int64 with one entry per bag");
+  TORCH_CHECK(v.b_t_map.scalar_type() == at::kInt && v.b_t_map.is_contiguous() &&
+                  v.b_t_map.numel() == total_B,
+              "vbe_b_t_map must be contiguous int32 with one entry per bag");
+  TORCH_CHECK(v.info_B_num_bits >= 1 && v.info_B_num_bits <= 32, "info_B_num_bits invalid");
+}
+
 // Element type of TBE training weights: fp32 or fp16 rows.
 int32_t weights_ty_of(const Tensor& w) {
   TORCH_CHECK(w.is_contiguous(), "dev_weights must be contiguous");
@@ -328,7 +353,8 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
                    const Tensor& weights_placements, const Tensor& weights_offsets,
                    const Tensor& D_offsets, int64_t total_D, int64_t max_D, const Tensor& indices,
                    const Tensor& offsets, int64_t pooling_mode,
-                   const std::optional<Tensor>& indice_weights, int64_t output_dtype) {
+                   const std::optional<Tensor>& indice_weights, int64_t output_dtype,
+                   const VbeMeta& vbe = VbeMeta()) {
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
   for (auto* t : {&weights_offsets, &D_offsets, &indices, &offsets}) check_gpu(*t, "TBE argument");
@@ -342,8 +368,8 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
   const int64_t T = D_offsets.numel() - 1;
   TORCH_CHECK(T >= 1, "D_offsets must have T+1 >= 2 entries");
   TORCH_CHECK(weights_offsets.numel() == T, "weights_offsets must have T entries");
-  TORCH_CHECK((offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
-  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(vbe.on() || (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = vbe.on() ? 0 : (offsets.numel() - 1) / T;
   TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
               "output_dtype must be FP32 (0) or FP16 (1)");
   const float* iw = nullptr;
@@ -356,8 +382,21 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
     iw = iwc.data_ptr<float>();
   }
   auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
-  Tensor out = at::empty({B, total_D}, opts);
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  if (vbe.on()) {  // flat output, one row per bag at its row offset
+    const int64_t total_B = offsets.numel() - 1;
+    check_vbe(vbe, total_B);
+    Tensor out = at::zeros({vbe.output_size}, opts);
+    MX_CALL(mx_tbe_forward_vbe(
+        dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
+        D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), total_B,
+        static_cast<int32_t>(max_D), idx.data_ptr(), off.data_ptr(), ib,
+        static_cast<int32_t>(pooling_mode), iw, vbe.row_out.data_ptr<int64_t>(),
+        vbe.b_t_map.data_ptr<int32_t>(), static_cast<int32_t>(vbe.info_B_num_bits),
+        out.data_ptr(), static_cast<int32_t>(output_dtype), stream_of(dev_weights)));
+    return out;
+  }
+  Tensor out = at::empty({B, total_D}, opts);
   MX_CALL(mx_tbe_forward(dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
                          D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B,
                          static_cast<int32_t>(max_D), idx.data_ptr(), off.data_ptr(), ib,
@@ -398,6 +437,102 @@ Tensor forward_weighted(const Tensor& dev_weights, const Tensor& uvm_weights,
                      indice_weights, output_dtype);
 }
 
+// ---- variable batch size per feature (VBE) ----------------------------------
+
+VbeMeta vbe_meta(const Tensor& row_out, const Tensor& b_t_map, int64_t output_size,
+                 int64_t info_B_num_bits, const Tensor& B_offsets = Tensor(),
+                 int64_t max_B = 0) {
+  VbeMeta v;
+  v.row_out = row_out.contiguous();
+  v.b_t_map = b_t_map.contiguous();
+  v.output_size = output_size;
+  v.info_B_num_bits = info_B_num_bits;
+  v.B_offsets = B_offsets;
+  v.max_B = max_B;
+  return v;
+}
+
+// (row_output_offsets int64 [total_B], b_t_map int32 [total_B]).
+std::tuple<Tensor, Tensor> generate_vbe_metadata(
+    const Tensor& B_offsets, const Tensor& B_offsets_rank_per_feature,
+    const Tensor& output_offsets_feature_rank, const Tensor& D_offsets, int64_t D, bool nobag,
+    c10::SymInt max_B_feature_rank, int64_t info_B_num_bits, c10::SymInt total_B_sym) {
+  (void)max_B_feature_rank;
+  for (auto* t : {&B_offsets, &B_offsets_rank_per_feature, &output_offsets_feature_rank,
+                  &D_offsets})
+    check_gpu(*t, "generate_vbe_metadata argument");
+  c10::OptionalDeviceGuard guard(B_offsets.device());
+  TORCH_CHECK(B_offsets.scalar_type() == at::kInt && B_offsets_rank_per_feature.scalar_type() ==
+                  at::kInt && D_offsets.scalar_type() == at::kInt,
+              "B_offsets, B_offsets_rank_per_feature and D_offsets must be int32");
+  TORCH_CHECK(output_offsets_feature_rank.scalar_type() == at::kLong,
+              "output_offsets_feature_rank must be int64");
+  const int64_t T = B_offsets.numel() - 1;
+  TORCH_CHECK(T >= 1 && B_offsets_rank_per_feature.dim() == 2 &&
+                  B_offsets_rank_per_feature.size(0) == T,
+              "B_offsets_rank_per_feature must be [T, R+1]");
+  const int64_t R = B_offsets_rank_per_feature.size(1) - 1;
+  TORCH_CHECK(R >= 1 && output_offsets_feature_rank.numel() == R * T + 1,
+              "output_offsets_feature_rank must have R*T+1 entries");
+  TORCH_CHECK(nobag ? D > 0 : D_offsets.numel() == T + 1, "D_offsets must have T+1 entries");
+  const int64_t total_B = total_B_sym.expect_int();
+  Tensor row_out = at::empty({total_B}, B_offsets.options().dtype(at::kLong));
+  Tensor b_t_map = at::empty({total_B}, B_offsets.options().dtype(at::kInt));
+  const Tensor bo = B_offsets.contiguous(), rpf = B_offsets_rank_per_feature.contiguous(),
+               ofr = output_offsets_feature_rank.contiguous(), dof = D_offsets.contiguous();
+  MX_CALL(mx_generate_vbe_metadata(bo.data_ptr<int32_t>(), rpf.data_ptr<int32_t>(),
+                                   ofr.data_ptr<int64_t>(), dof.data_ptr<int32_t>(),
+                                   nobag ? static_cast<int32_t>(D) : 0, static_cast<int32_t>(T),
+                                   static_cast<int32_t>(R), static_cast<int32_t>(info_B_num_bits),
+                                   total_B, row_out.data_ptr<int64_t>(),
+                                   b_t_map.data_ptr<int32_t>(), stream_of(B_offsets)));
+  return {row_out, b_t_map};
+}
+
+Tensor forward_unweighted_vbe(const Tensor& dev_weights, const Tensor& uvm_weights,
+                              const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+                              const Tensor& weights_offsets, const Tensor& D_offsets,
+                              c10::SymInt total_D, c10::SymInt max_D, const Tensor& indices,
+                              const Tensor& offsets, int64_t pooling_mode,
+                              const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
+                              int64_t output_dtype, const Tensor& vbe_row_output_offsets,
+                              const Tensor& vbe_b_t_map, c10::SymInt vbe_output_size,
+                              int64_t info_B_num_bits, int64_t info_B_mask,
+                              bool is_experimental) {
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  (void)uvm_cache_stats;
+  (void)info_B_mask;
+  (void)is_experimental;
+  return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
+                     total_D.expect_int(), max_D.expect_int(), indices, offsets, pooling_mode,
+                     std::nullopt, output_dtype,
+                     vbe_meta(vbe_row_output_offsets, vbe_b_t_map, vbe_output_size.expect_int(),
+                              info_B_num_bits));
+}
+
+Tensor forward_weighted_vbe(const Tensor& dev_weights, const Tensor& uvm_weights,
+                            const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+                            const Tensor& weights_offsets, const Tensor& D_offsets,
+                            c10::SymInt total_D, c10::SymInt max_D, const Tensor& indices,
+                            const Tensor& offsets, int64_t pooling_mode,
+                            const Tensor& indice_weights, const Tensor& lxu_cache_locations,
+                            const Tensor& uvm_cache_stats, int64_t output_dtype,
+                            const Tensor& vbe_row_output_offsets, const Tensor& vbe_b_t_map,
+                            c10::SymInt vbe_output_size, int64_t info_B_num_bits,
+                            int64_t info_B_mask, bool is_experimental) {
+  (void)lxu_cache_weights;
+  (void)lxu_cache_locations;
+  (void)uvm_cache_stats;
+  (void)info_B_mask;
+  (void)is_experimental;
+  return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
+                     total_D.expect_int(), max_D.expect_int(), indices, offsets, pooling_mode,
+                     indice_weights, output_dtype,
+                     vbe_meta(vbe_row_output_offsets, vbe_b_t_map, vbe_output_size.expect_int(),
+                              info_B_num_bits));
+}
+
 std::tuple<int64_t, int64_t> get_infos_metadata(const Tensor& unused, int64_t B, int64_t T) {
   (void)unused;
   const int32_t nb = mx_tbe_info_B_num_bits(static_cast<int32_t>(T), B);
@@ -413,8 +548,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   (void)info_B_mask;
   (void)total_unique_indices;
   TORCH_CHECK(!nobag, "nobag transpose is not supported");
-  TORCH_CHECK(!(vbe_b_t_map.has_value() && vbe_b_t_map->defined()),
-              "variable batch size (VBE) is not supported");
+  const bool vbe = vbe_b_t_map.has_value() && vbe_b_t_map->defined();
   check_gpu(indices, "indices");
   c10::OptionalDeviceGuard guard(indices.device());
   check_gpu(hash_size_cumsum, "hash_size_cumsum");
@@ -423,8 +557,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
   const int64_t T = hash_size_cumsum.numel() - 1;
-  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
-  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(T >= 1 && (vbe || (offsets.numel() - 1) % T == 0),
+              "offsets must have T*B+1 entries");
+  const int64_t B = vbe ? 0 : (offsets.numel() - 1) / T;
   const int64_t N = indices.numel();
   auto o64 = indices.options().dtype(at::kLong);
   auto o32 = indices.options().dtype(at::kInt);
@@ -435,6 +570,21 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   const size_t ws_bytes = mx_tbe_transpose_workspace_bytes(N, total_hash_size_bits);
   Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  if (vbe) {
+    const int64_t total_B = offsets.numel() - 1;
+    check_gpu(*vbe_b_t_map, "vbe_b_t_map");
+    TORCH_CHECK(vbe_b_t_map->scalar_type() == at::kInt && vbe_b_t_map->numel() == total_B,
+                "vbe_b_t_map must be int32 with one entry per bag");
+    const Tensor btm = vbe_b_t_map->contiguous();
+    MX_CALL(mx_tbe_transpose_embedding_input_vbe(
+        hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(T), total_B,
+        btm.data_ptr<int32_t>(), static_cast<int32_t>(total_hash_size_bits),
+        static_cast<int32_t>(info_B_num_bits), idx.data_ptr(), off.data_ptr(), ib, N,
+        linear.data_ptr<int64_t>(), sorted.data_ptr<int64_t>(), infos.data_ptr<int32_t>(),
+        run.data_ptr<int64_t>(), lengths.data_ptr<int32_t>(), num_runs.data_ptr<int32_t>(),
+        cum.data_ptr<int32_t>(), ws.data_ptr(), ws_bytes, stream_of(indices)));
+    return {linear, sorted, infos, run, lengths, num_runs, cum};
+  }
   MX_CALL(mx_tbe_transpose_embedding_input(
       hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
       static_cast<int32_t>(total_hash_size_bits), static_cast<int32_t>(info_B_num_bits),
@@ -457,7 +607,7 @@ Tensor backward_rowwise_adagrad_impl(
     int64_t max_segment_length_per_warp, bool stochastic_rounding,
     const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
     const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
-    int64_t weight_decay_mode, double max_norm) {
+    int64_t weight_decay_mode, double max_norm, const VbeMeta& vbe = VbeMeta()) {
   (void)lxu_cache_weights;
   (void)weights_placements;
   (void)lxu_cache_locations;
@@ -481,10 +631,15 @@ Tensor backward_rowwise_adagrad_impl(
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
   const int64_t T = D_offsets.numel() - 1;
-  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
-  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(T >= 1 && (vbe.on() || (offsets.numel() - 1) % T == 0),
+              "offsets must have T*B+1 entries");
+  const int64_t B = vbe.on() ? 0 : (offsets.numel() - 1) / T;
   const Tensor g = grad_output.contiguous();
-  TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  if (vbe.on()) {
+    TORCH_CHECK(g.numel() == vbe.output_size, "grad_output must hold the flat VBE output");
+  } else {
+    TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  }
   const int64_t max_D = max_D_sym.expect_int();
   const int64_t N = indices.numel();
   const size_t ws_bytes =
@@ -503,6 +658,27 @@ Tensor backward_rowwise_adagrad_impl(
   // fp16 weights: the update rounds stochastically when asked (fp32: no rounding step).
   const bool sr = wty == MX_SPARSE_FP16 && stochastic_rounding;
   const uint64_t seed = sr ? next_rounding_seed(dev_weights) : 0;
+  if (vbe.on()) {
+    const int64_t total_B = offsets.numel() - 1;
+    check_vbe(vbe, total_B);
+    check_gpu(vbe.B_offsets, "B_offsets");
+    TORCH_CHECK(vbe.B_offsets.scalar_type() == at::kInt && vbe.B_offsets.numel() == T + 1,
+                "B_offsets must be int32 [T+1]");
+    const Tensor bo = vbe.B_offsets.contiguous();
+    MX_CALL(mx_tbe_backward_rowwise_adagrad_vbe(
+        dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
+        D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), vbe.max_B,
+        static_cast<int32_t>(max_D), hash_size_cumsum.data_ptr<int64_t>(),
+        static_cast<int32_t>(total_hash_size_bits), idx.data_ptr(), off.data_ptr(), ib, N,
+        static_cast<int32_t>(pooling_mode), iwc.defined() ? iwc.data_ptr<float>() : nullptr,
+        g.data_ptr<float>(), total_B, bo.data_ptr<int32_t>(), vbe.row_out.data_ptr<int64_t>(),
+        vbe.b_t_map.data_ptr<int32_t>(), static_cast<int32_t>(vbe.info_B_num_bits),
+        momentum1_dev.data_ptr<float>(), momentum1_offsets.data_ptr<int64_t>(),
+        static_cast<float>(learning_rate), static_cast<float>(eps),
+        static_cast<float>(weight_decay), static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0,
+        seed, ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
+    return at::empty({0}, dev_weights.options());
+  }
   MX_CALL(mx_tbe_backward_rowwise_adagrad(
       dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
       D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B, static_cast<int32_t>(max_D),
@@ -557,16 +733,87 @@ Tensor backward_rowwise_adagrad_weighted_exact(
       weight_decay_mode, max_norm);
 }
 
+Tensor backward_rowwise_adagrad_vbe_common(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
+    const Tensor& lxu_cache_locations, int64_t BT_block_size,
+    int64_t max_segment_length_per_warp, bool stochastic_rounding, int64_t info_B_num_bits,
+    const Tensor& B_offsets, const Tensor& vbe_row_output_offsets, const Tensor& vbe_b_t_map,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  // b < 2^info_B_num_bits by the encoding: the widest batch the info words allow.
+  const int64_t max_B = info_B_num_bits >= 32 ? (int64_t(1) << 32) : (int64_t(1) << info_B_num_bits);
+  return backward_rowwise_adagrad_impl(
+      grad_output, dev_weights, uvm_weights, lxu_cache_weights, weights_placements,
+      weights_offsets, D_offsets, std::move(max_D), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, indice_weights, lxu_cache_locations, BT_block_size,
+      max_segment_length_per_warp, stochastic_rounding, momentum1_dev, momentum1_uvm,
+      momentum1_placements, momentum1_offsets, eps, learning_rate, weight_decay,
+      weight_decay_mode, max_norm,
+      vbe_meta(vbe_row_output_offsets, vbe_b_t_map, grad_output.numel(), info_B_num_bits,
+               B_offsets, max_B));
+}
+
+Tensor backward_rowwise_adagrad_exact_vbe(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& lxu_cache_locations,
+    int64_t BT_block_size, int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    int64_t info_B_num_bits, int64_t info_B_mask, const Tensor& B_offsets,
+    const Tensor& vbe_row_output_offsets, const Tensor& vbe_b_t_map,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  (void)info_B_mask;
+  return backward_rowwise_adagrad_vbe_common(
+      grad_output, dev_weights, uvm_weights, lxu_cache_weights, weights_placements,
+      weights_offsets, D_offsets, std::move(max_D), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, Tensor(), lxu_cache_locations, BT_block_size,
+      max_segment_length_per_warp, stochastic_rounding, info_B_num_bits, B_offsets,
+      vbe_row_output_offsets, vbe_b_t_map, momentum1_dev, momentum1_uvm, momentum1_placements,
+      momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm);
+}
+
+Tensor backward_rowwise_adagrad_weighted_exact_vbe(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, const Tensor& D_offsets, c10::SymInt max_D,
+    const Tensor& hash_size_cumsum, int64_t total_hash_size_bits, const Tensor& indices,
+    const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
+    const Tensor& lxu_cache_locations, int64_t BT_block_size,
+    int64_t max_segment_length_per_warp, bool stochastic_rounding, int64_t info_B_num_bits,
+    int64_t info_B_mask, const Tensor& B_offsets, const Tensor& vbe_row_output_offsets,
+    const Tensor& vbe_b_t_map, const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
+    const Tensor& momentum1_placements, const Tensor& momentum1_offsets, double eps,
+    double learning_rate, double weight_decay, int64_t weight_decay_mode, double max_norm) {
+  (void)info_B_mask;
+  TORCH_CHECK(indice_weights.defined(), "the weighted backward needs indice_weights");
+  return backward_rowwise_adagrad_vbe_common(
+      grad_output, dev_weights, uvm_weights, lxu_cache_weights, weights_placements,
+      weights_offsets, D_offsets, std::move(max_D), hash_size_cumsum, total_hash_size_bits,
+      indices, offsets, pooling_mode, indice_weights, lxu_cache_locations, BT_block_size,
+      max_segment_length_per_warp, stochastic_rounding, info_B_num_bits, B_offsets,
+      vbe_row_output_offsets, vbe_b_t_map, momentum1_dev, momentum1_uvm, momentum1_placements,
+      momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm);
+}
+
 // Gradient of the per-sample weights of a weighted SUM/MEAN lookup (fp32 [N]):
 // grad_indice_weights[l] = <grad_output[b, D_t slice], W_t[indices[l]]>, times
 // 1/L under MEAN; 0 for tables whose feature_requires_grad entry is 0.
-Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
-                           const Tensor& uvm_weights, const Tensor& lxu_cache_weights,
-                           const Tensor& weights_placements, const Tensor& weights_offsets,
-                           const Tensor& D_offsets, c10::SymInt max_D_sym, const Tensor& indices,
-                           const Tensor& offsets, const Tensor& lxu_cache_locations,
-                           const std::optional<Tensor>& feature_requires_grad,
-                           int64_t pooling_mode) {
+Tensor grad_indice_weights_impl(const Tensor& grad_output, const Tensor& dev_weights,
+                                const Tensor& uvm_weights, const Tensor& lxu_cache_weights,
+                                const Tensor& weights_placements, const Tensor& weights_offsets,
+                                const Tensor& D_offsets, c10::SymInt max_D_sym,
+                                const Tensor& indices, const Tensor& offsets,
+                                const Tensor& lxu_cache_locations,
+                                const std::optional<Tensor>& feature_requires_grad,
+                                int64_t pooling_mode, const VbeMeta& vbe) {
   (void)lxu_cache_weights;
   (void)weights_placements;
   (void)lxu_cache_locations;
@@ -582,10 +829,15 @@ Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
   const int64_t T = D_offsets.numel() - 1;
-  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
-  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(T >= 1 && (vbe.on() || (offsets.numel() - 1) % T == 0),
+              "offsets must have T*B+1 entries");
+  const int64_t B = vbe.on() ? 0 : (offsets.numel() - 1) / T;
   const Tensor g = grad_output.contiguous();
-  TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  if (vbe.on()) {
+    TORCH_CHECK(g.numel() == vbe.output_size, "grad_output must hold the flat VBE output");
+  } else {
+    TORCH_CHECK(g.dim() == 2 && g.size(0) == B, "grad_output must be [B, total_D]");
+  }
   Tensor frg;
   if (feature_requires_grad.has_value() && feature_requires_grad->defined() &&
       feature_requires_grad->numel() > 0) {
@@ -595,6 +847,19 @@ Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
   }
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
   Tensor out = at::empty({indices.numel()}, dev_weights.options().dtype(at::kFloat));
+  if (vbe.on()) {
+    const int64_t total_B = offsets.numel() - 1;
+    check_vbe(vbe, total_B);
+    MX_CALL(mx_tbe_grad_indice_weights_vbe(
+        g.data_ptr<float>(), dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
+        D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), total_B,
+        static_cast<int32_t>(max_D_sym.expect_int()), idx.data_ptr(), off.data_ptr(), ib,
+        static_cast<int32_t>(pooling_mode), vbe.row_out.data_ptr<int64_t>(),
+        vbe.b_t_map.data_ptr<int32_t>(), static_cast<int32_t>(vbe.info_B_num_bits),
+        frg.defined() ? frg.data_ptr<int32_t>() : nullptr, out.data_ptr<float>(),
+        stream_of(dev_weights)));
+    return out;
+  }
   MX_CALL(mx_tbe_grad_indice_weights(
       g.data_ptr<float>(), g.size(1), dev_weights.data_ptr(), wty,
       weights_offsets.data_ptr<int64_t>(), D_offsets.data_ptr<int32_t>(),
@@ -603,6 +868,37 @@ Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
       frg.defined() ? frg.data_ptr<int32_t>() : nullptr, out.data_ptr<float>(),
       stream_of(dev_weights)));
   return out;
+}
+
+Tensor grad_indice_weights(const Tensor& grad_output, const Tensor& dev_weights,
+                           const Tensor& uvm_weights, const Tensor& lxu_cache_weights,
+                           const Tensor& weights_placements, const Tensor& weights_offsets,
+                           const Tensor& D_offsets, c10::SymInt max_D, const Tensor& indices,
+                           const Tensor& offsets, const Tensor& lxu_cache_locations,
+                           const std::optional<Tensor>& feature_requires_grad,
+                           int64_t pooling_mode) {
+  return grad_indice_weights_impl(grad_output, dev_weights, uvm_weights, lxu_cache_weights,
+                                  weights_placements, weights_offsets, D_offsets,
+                                  std::move(max_D), indices, offsets, lxu_cache_locations,
+                                  feature_requires_grad, pooling_mode, VbeMeta());
+}
+
+Tensor grad_indice_weights_vbe(const Tensor& grad_output, const Tensor& dev_weights,
+                               const Tensor& uvm_weights, const Tensor& lxu_cache_weights,
+                               const Tensor& weights_placements, const Tensor& weights_offsets,
+                               const Tensor& D_offsets, c10::SymInt max_D, const Tensor& indices,
+                               const Tensor& offsets, const Tensor& lxu_cache_locations,
+                               const std::optional<Tensor>& feature_requires_grad,
+                               const Tensor& vbe_row_output_offsets, const Tensor& vbe_b_t_map,
+                               int64_t info_B_num_bits, int64_t info_B_mask,
+                               int64_t pooling_mode) {
+  (void)info_B_mask;
+  return grad_indice_weights_impl(grad_output, dev_weights, uvm_weights, lxu_cache_weights,
+                                  weights_placements, weights_offsets, D_offsets,
+                                  std::move(max_D), indices, offsets, lxu_cache_locations,
+                                  feature_requires_grad, pooling_mode,
+                                  vbe_meta(vbe_row_output_offsets, vbe_b_t_map,
+                                           grad_output.numel(), info_B_num_bits));
 }
 
 class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagrad> {
@@ -619,7 +915,10 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
                         const Tensor& momentum1_placements, const Tensor& momentum1_offsets,
                         double eps, double learning_rate, double weight_decay,
                         int64_t weight_decay_mode, double max_norm, int64_t output_dtype,
-                        bool stochastic_rounding) {
+                        bool stochastic_rounding, const std::optional<Tensor>& vbe_B_offsets,
+                        const std::optional<Tensor>& vbe_row_out,
+                        const std::optional<Tensor>& vbe_b_t_map, int64_t vbe_output_size,
+                        int64_t vbe_info_B_num_bits) {
     (void)placeholder;
     // Stored as IValues: the backward updates dev_weights/momentum1 in place.
     auto& s = ctx->saved_data;
@@ -648,10 +947,26 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     s["weight_decay_mode"] = weight_decay_mode;
     s["max_norm"] = max_norm;
     s["stochastic_rounding"] = stochastic_rounding;
+    const bool vbe = vbe_b_t_map.has_value() && vbe_b_t_map->defined();
+    s["vbe_B_offsets"] = vbe ? *vbe_B_offsets : Tensor();
+    s["vbe_row_out"] = vbe ? *vbe_row_out : Tensor();
+    s["vbe_b_t_map"] = vbe ? *vbe_b_t_map : Tensor();
+    s["vbe_output_size"] = vbe_output_size;
+    s["vbe_info_B_num_bits"] = vbe_info_B_num_bits;
     at::AutoDispatchBelowADInplaceOrView g;
     return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
                        total_D, max_D, indices, offsets, pooling_mode, indice_weights,
-                       output_dtype);
+                       output_dtype, vbe ? saved_vbe(s) : VbeMeta());
+  }
+
+  // The VBE metadata saved by forward (undefined tensors: fixed batch).
+  static VbeMeta saved_vbe(const ska::flat_hash_map<std::string, at::IValue>& s) {
+    const Tensor btm = s.at("vbe_b_t_map").toTensor();
+    if (!btm.defined()) return VbeMeta();
+    const int64_t nb = s.at("vbe_info_B_num_bits").toInt();
+    return vbe_meta(s.at("vbe_row_out").toTensor(), btm, s.at("vbe_output_size").toInt(), nb,
+                    s.at("vbe_B_offsets").toTensor(),
+                    nb >= 32 ? (int64_t(1) << 32) : (int64_t(1) << nb));
   }
 
   // indice_weights is argument 13 of forward() (after ctx) and, when present,
@@ -659,7 +974,7 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
   // per argument.
   static constexpr size_t kIndiceWeightsArg = 13;
   static constexpr size_t kIndiceWeightsEdge = 9;
-  static constexpr size_t kNumInputs = 26;
+  static constexpr size_t kNumInputs = 31;
 
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     auto& s = ctx->saved_data;
@@ -674,12 +989,13 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     // overwrites them (same stream, so ordered).
     if (iw.defined() && ctx->needs_input_grad(kIndiceWeightsEdge)) {
       const Tensor frg = s["feature_requires_grad"].toTensor();
-      out[kIndiceWeightsArg] = grad_indice_weights(
+      out[kIndiceWeightsArg] = grad_indice_weights_impl(
           g, s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
           s["weights_placements"].toTensor(), s["weights_offsets"].toTensor(),
           s["D_offsets"].toTensor(), c10::SymInt(s["max_D"].toInt()), s["indices"].toTensor(),
           s["offsets"].toTensor(), empty,
-          frg.defined() ? std::optional<Tensor>(frg) : std::nullopt, s["pooling_mode"].toInt());
+          frg.defined() ? std::optional<Tensor>(frg) : std::nullopt, s["pooling_mode"].toInt(),
+          saved_vbe(s));
     }
     backward_rowwise_adagrad_impl(
         g, s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
@@ -691,7 +1007,7 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
         s["momentum1_uvm"].toTensor(),
         s["momentum1_placements"].toTensor(), s["momentum1_offsets"].toTensor(),
         s["eps"].toDouble(), s["learning_rate"].toDouble(), s["weight_decay"].toDouble(),
-        s["weight_decay_mode"].toInt(), s["max_norm"].toDouble());
+        s["weight_decay_mode"].toInt(), s["max_norm"].toDouble(), saved_vbe(s));
     return out;
   }
 };
@@ -707,17 +1023,40 @@ Tensor lookup_rowwise_adagrad(
     bool stochastic_rounding, const Tensor& momentum1_dev, const Tensor& momentum1_uvm,
     const Tensor& momentum1_placements, const Tensor& momentum1_offsets, double eps,
     double learning_rate, double weight_decay, int64_t weight_decay_mode, double max_norm,
-    int64_t output_dtype) {
+    int64_t output_dtype, const std::optional<Tensor>& B_offsets,
+    const std::optional<Tensor>& vbe_output_offsets_feature_rank,
+    const std::optional<Tensor>& vbe_B_offsets_rank_per_feature, c10::SymInt max_B,
+    c10::SymInt max_B_feature_rank, c10::SymInt vbe_output_size) {
   (void)lxu_cache_weights;
   (void)lxu_cache_locations;
   TORCH_CHECK(!gradient_clipping || max_gradient <= 0.0, "gradient clipping is not supported");
+  // Variable batch per feature: the per-bag metadata is built once here.
+  std::optional<Tensor> vbe_row_out, vbe_b_t_map;
+  int64_t vbe_size = 0, vbe_nb = 0;
+  if (B_offsets.has_value() && B_offsets->defined()) {
+    TORCH_CHECK(vbe_output_offsets_feature_rank.has_value() &&
+                    vbe_B_offsets_rank_per_feature.has_value(),
+                "VBE needs vbe_output_offsets_feature_rank and vbe_B_offsets_rank_per_feature");
+    const int64_t T = D_offsets.numel() - 1;
+    const int64_t mB = max_B.expect_int();
+    vbe_size = vbe_output_size.expect_int();
+    TORCH_CHECK(mB >= 1 && vbe_size >= 0, "VBE needs max_B >= 1 and vbe_output_size >= 0");
+    vbe_nb = mx_tbe_info_B_num_bits(static_cast<int32_t>(T), mB);
+    TORCH_CHECK(vbe_nb > 0, "T=", T, " and max_B=", mB, " do not fit a 32-bit info word");
+    auto meta = generate_vbe_metadata(*B_offsets, *vbe_B_offsets_rank_per_feature,
+                                      *vbe_output_offsets_feature_rank, D_offsets, -1, false,
+                                      max_B_feature_rank, vbe_nb,
+                                      c10::SymInt(offsets.numel() - 1));
+    vbe_row_out = std::get<0>(meta);
+    vbe_b_t_map = std::get<1>(meta);
+  }
   return LookupRowwiseAdagrad::apply(
       placeholder_autograd_tensor, dev_weights, uvm_weights, weights_placements, weights_offsets,
       D_offsets, total_D.expect_int(), max_D.expect_int(), hash_size_cumsum, total_hash_size_bits,
       indices, offsets, pooling_mode, indice_weights, feature_requires_grad, momentum1_dev,
       momentum1_uvm, momentum1_placements,
       momentum1_offsets, eps, learning_rate, weight_decay, weight_decay_mode, max_norm,
-      output_dtype, stochastic_rounding);
+      output_dtype, stochastic_rounding, B_offsets, vbe_row_out, vbe_b_t_map, vbe_size, vbe_nb);
 }
 
 // ---------------------------------------------------------------------------
@@ -731,6 +1070,7 @@ void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
                           const std::optional<Tensor>& b_t_map, int64_t info_B_num_bits,
                           int64_t info_B_mask, int64_t bounds_check_version) {
   (void)max_B;
+  (void)b_t_map;  // the table of a bag comes from B_offsets
   (void)info_B_num_bits;
   (void)info_B_mask;
   (void)bounds_check_version;
@@ -739,9 +1079,6 @@ void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
   check_gpu(offsets, "offsets");
   check_gpu(rows_per_table, "rows_per_table");
   check_gpu(warning, "warning");
-  TORCH_CHECK(!(B_offsets.has_value() && B_offsets->defined()) &&
-                  !(b_t_map.has_value() && b_t_map->defined()),
-              "variable batch size (VBE) is not supported");
   TORCH_CHECK(bounds_check_mode >= MX_BOUNDS_FATAL && bounds_check_mode <= MX_BOUNDS_NONE,
               "bounds_check_mode must be FATAL(0), WARNING(1), IGNORE(2) or NONE(3)");
   TORCH_CHECK(rows_per_table.scalar_type() == at::kLong, "rows_per_table must be int64");
@@ -753,31 +1090,47 @@ void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
   const int64_t T = rows_per_table.numel();
-  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
-  const int64_t B = (offsets.numel() - 1) / T;
+  // Variable batch per feature: bags B_offsets[t] .. B_offsets[t+1]-1 are table t's.
+  const bool vbe = B_offsets.has_value() && B_offsets->defined();
+  Tensor bo;
+  if (vbe) {
+    check_gpu(*B_offsets, "B_offsets");
+    TORCH_CHECK(B_offsets->scalar_type() == at::kInt && B_offsets->numel() == T + 1,
+                "B_offsets must be int32 [T+1]");
+    bo = B_offsets->contiguous();
+  }
+  TORCH_CHECK(T >= 1 && (vbe || (offsets.numel() - 1) % T == 0),
+              "offsets must have T*B+1 entries");
+  const int64_t B = vbe ? 0 : (offsets.numel() - 1) / T;
+  const int64_t total_B = offsets.numel() - 1;
   if (weights.has_value() && weights->defined())
     TORCH_CHECK(weights->numel() == indices.numel(), "per-sample weights have ",
                 weights->numel(), " entries but there are ", indices.numel(), " indices");
   if (bounds_check_mode == MX_BOUNDS_NONE) return;
   const Tensor rows = rows_per_table.contiguous();
-  const size_t ws_bytes = mx_bounds_check_workspace_bytes(static_cast<int32_t>(T), B);
+  const size_t ws_bytes = vbe ? mx_bounds_check_workspace_bytes_vbe(total_B)
+                              : mx_bounds_check_workspace_bytes(static_cast<int32_t>(T), B);
   Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
-  if (bounds_check_mode == MX_BOUNDS_FATAL) {
-    Tensor count = at::zeros({1}, warning.options());
+  const bool fatal = bounds_check_mode == MX_BOUNDS_FATAL;
+  Tensor count = fatal ? at::zeros({1}, warning.options()) : warning;
+  if (vbe)
+    MX_CALL(mx_bounds_check_indices_vbe(rows.data_ptr<int64_t>(), static_cast<int32_t>(T),
+                                        total_B, bo.data_ptr<int32_t>(), indices.data_ptr(),
+                                        offsets.data_ptr(), ib, indices.numel(),
+                                        static_cast<int32_t>(bounds_check_mode),
+                                        count.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
+                                        stream_of(indices)));
+  else
     MX_CALL(mx_bounds_check_indices(rows.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
                                     indices.data_ptr(), offsets.data_ptr(), ib, indices.numel(),
-                                    MX_BOUNDS_FATAL, count.data_ptr<int64_t>(), ws.data_ptr(),
-                                    ws_bytes, stream_of(indices)));
+                                    static_cast<int32_t>(bounds_check_mode),
+                                    count.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
+                                    stream_of(indices)));
+  if (fatal) {
     const int64_t n = count.item<int64_t>();  // FATAL synchronises to report
     TORCH_CHECK(n == 0, "bounds_check_indices: ", n,
                 " out-of-range indices/offsets (BoundsCheckMode.FATAL)");
-    return;
   }
-  MX_CALL(mx_bounds_check_indices(rows.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
-                                  indices.data_ptr(), offsets.data_ptr(), ib, indices.numel(),
-                                  static_cast<int32_t>(bounds_check_mode),
-                                  warning.data_ptr<int64_t>(), ws.data_ptr(), ws_bytes,
-                                  stream_of(indices)));
 }
 
 // ---------------------------------------------------------------------------
@@ -1004,7 +1357,55 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "bool stochastic_rounding, Tensor momentum1_dev, Tensor momentum1_uvm, "
         "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
         "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
-        "float max_norm=0.0, int output_dtype=0) -> Tensor");
+        "float max_norm=0.0, int output_dtype=0, Tensor? B_offsets=None, "
+        "Tensor? vbe_output_offsets_feature_rank=None, "
+        "Tensor? vbe_B_offsets_rank_per_feature=None, SymInt max_B=-1, "
+        "SymInt max_B_feature_rank=-1, SymInt vbe_output_size=-1) -> Tensor");
+  m.def("generate_vbe_metadata(Tensor B_offsets, Tensor B_offsets_rank_per_feature, "
+        "Tensor output_offsets_feature_rank, Tensor D_offsets, int D, bool nobag, "
+        "SymInt max_B_feature_rank, int info_B_num_bits, SymInt total_B) -> (Tensor, Tensor)");
+  m.def("split_embedding_codegen_forward_unweighted_vbe_cuda(Tensor dev_weights, "
+        "Tensor uvm_weights, Tensor lxu_cache_weights, Tensor weights_placements, "
+        "Tensor weights_offsets, Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, "
+        "Tensor offsets, int pooling_mode, Tensor lxu_cache_locations, Tensor uvm_cache_stats, "
+        "int output_dtype, Tensor vbe_row_output_offsets, Tensor vbe_b_t_map, "
+        "SymInt vbe_output_size, int info_B_num_bits, int info_B_mask, bool is_experimental) "
+        "-> Tensor");
+  m.def("split_embedding_codegen_forward_weighted_vbe_cuda(Tensor dev_weights, "
+        "Tensor uvm_weights, Tensor lxu_cache_weights, Tensor weights_placements, "
+        "Tensor weights_offsets, Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, "
+        "Tensor offsets, int pooling_mode, Tensor indice_weights, Tensor lxu_cache_locations, "
+        "Tensor uvm_cache_stats, int output_dtype, Tensor vbe_row_output_offsets, "
+        "Tensor vbe_b_t_map, SymInt vbe_output_size, int info_B_num_bits, int info_B_mask, "
+        "bool is_experimental) -> Tensor");
+  m.def("split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_vbe_cuda("
+        "Tensor grad_output, Tensor(a!) dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt max_D, Tensor hash_size_cumsum, int total_hash_size_bits, "
+        "Tensor indices, Tensor offsets, int pooling_mode, Tensor lxu_cache_locations, "
+        "int BT_block_size, int max_segment_length_per_warp, bool stochastic_rounding, "
+        "int info_B_num_bits, int info_B_mask, Tensor B_offsets, Tensor vbe_row_output_offsets, "
+        "Tensor vbe_b_t_map, Tensor(b!) momentum1_dev, Tensor momentum1_uvm, "
+        "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
+        "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
+        "float max_norm=0.0) -> Tensor");
+  m.def("split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_vbe_cuda("
+        "Tensor grad_output, Tensor(a!) dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
+        "Tensor D_offsets, SymInt max_D, Tensor hash_size_cumsum, int total_hash_size_bits, "
+        "Tensor indices, Tensor offsets, int pooling_mode, Tensor indice_weights, "
+        "Tensor lxu_cache_locations, int BT_block_size, int max_segment_length_per_warp, "
+        "bool stochastic_rounding, int info_B_num_bits, int info_B_mask, Tensor B_offsets, "
+        "Tensor vbe_row_output_offsets, Tensor vbe_b_t_map, Tensor(b!) momentum1_dev, "
+        "Tensor momentum1_uvm, Tensor momentum1_placements, Tensor momentum1_offsets, "
+        "float eps=0, float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
+        "float max_norm=0.0) -> Tensor");
+  m.def("split_embedding_codegen_grad_indice_weights_vbe_cuda(Tensor grad_output, "
+        "Tensor dev_weights, Tensor uvm_weights, Tensor lxu_cache_weights, "
+        "Tensor weights_placements, Tensor weights_offsets, Tensor D_offsets, SymInt max_D, "
+        "Tensor indices, Tensor offsets, Tensor lxu_cache_locations, "
+        "Tensor? feature_requires_grad, Tensor vbe_row_output_offsets, Tensor vbe_b_t_map, "
+        "int info_B_num_bits, int info_B_mask, int pooling_mode=0) -> Tensor");
   m.def("FloatToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
   m.def("HalfToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
   m.def("FloatOrHalfToFused8BitRowwiseQuantized(Tensor t) -> Tensor");
@@ -1046,6 +1447,17 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
          TORCH_FN(mx_ops::backward_rowwise_adagrad_weighted_exact));
   m.impl("split_embedding_codegen_grad_indice_weights_cuda",
          TORCH_FN(mx_ops::grad_indice_weights));
+  m.impl("generate_vbe_metadata", TORCH_FN(mx_ops::generate_vbe_metadata));
+  m.impl("split_embedding_codegen_forward_unweighted_vbe_cuda",
+         TORCH_FN(mx_ops::forward_unweighted_vbe));
+  m.impl("split_embedding_codegen_forward_weighted_vbe_cuda",
+         TORCH_FN(mx_ops::forward_weighted_vbe));
+  m.impl("split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_vbe_cuda",
+         TORCH_FN(mx_ops::backward_rowwise_adagrad_exact_vbe));
+  m.impl("split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_vbe_cuda",
+         TORCH_FN(mx_ops::backward_rowwise_adagrad_weighted_exact_vbe));
+  m.impl("split_embedding_codegen_grad_indice_weights_vbe_cuda",
+         TORCH_FN(mx_ops::grad_indice_weights_vbe));
   m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
   m.impl("bounds_check_indices", TORCH_FN(mx_ops::bounds_check_indices));
   m.impl("FloatToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_to_8bit));

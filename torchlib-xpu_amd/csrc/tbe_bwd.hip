@@ -68,7 +68,8 @@ template <typename I>
 __global__ void __launch_bounds__(256)
     linearize_kernel(const int64_t* __restrict__ hsc, const I* __restrict__ indices,
                      const I* __restrict__ offsets, int64_t nbags, int64_t B, int32_t nb,
-                     int64_t N, int32_t bits, int32_t passes, int64_t* __restrict__ linear_out,
+                     const int32_t* __restrict__ b_t_map, int64_t N, int32_t bits,
+                     int32_t passes, int64_t* __restrict__ linear_out,
                      uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
                      const float* __restrict__ iw, uint32_t* __restrict__ vals2,
                      uint32_t* __restrict__ ghist) {
@@ -184,13 +185,22 @@ __global__ void __launch_bounds__(256)
     const int64_t l = pbase + it * 64;
     if (l >= lend) continue;
     const int64_t bag = blo + rel[it];
-    const int64_t t = bag / B;
-    const int64_t b = bag - t * B;
+    // Info word (t << nb) | b: computed for a fixed batch, given per bag (VBE).
+    uint32_t info;
+    int64_t t;
+    if (b_t_map) {
+      info = static_cast<uint32_t>(b_t_map[bag]);
+      t = nb >= 32 ? 0 : static_cast<int64_t>(info >> nb);
+    } else {
+      t = bag / B;
+      const int64_t b = bag - t * B;
+      info = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+    }
     const int64_t key = hsc[t] + static_cast<int64_t>(idx[it]);
     if (linear_out) linear_out[l] = key;
     const uint32_t k32 = static_cast<uint32_t>(key);
     keys[l] = k32;
-    vals[l] = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+    vals[l] = info;
     if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
     for (int p = 0; p < passes; ++p)
       atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
@@ -480,13 +490,16 @@ struct TransposeOut {
   float* weights_sorted;  // [N] per-sample weights in sorted order, or null
 };
 
-int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_t nb,
-                  const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
-                  const float* iw, const TransposeOut& o, SortWs& w, hipStream_t s) {
+// nbags = T * B bags of a fixed batch B, or (b_t_map non-null, VBE) the
+// total bag count with each bag's info word given.
+int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
+                  const int32_t* b_t_map, int32_t bits, int32_t nb, const void* indices,
+                  const void* offsets, int32_t index_bytes, int64_t N, const float* iw,
+                  const TransposeOut& o, SortWs& w, hipStream_t s) {
+  (void)T;
   // With per-sample weights the weights travel with the keys as a second payload.
   uint32_t* const v2[2] = {iw ? w.vals2[0] : nullptr, iw ? w.vals2[1] : nullptr};
   uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
-  const int64_t nbags = static_cast<int64_t>(T) * B;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
   const int passes = (bits + kRadixBits - 1) / kRadixBits;
   {  // look-back state of every scan and pass, and the histograms, start at zero
@@ -500,11 +513,11 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t bits, int32_
   if (index_bytes == 8)
     linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
-        nb, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
+        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
   else
     linearize_kernel<int32_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
-        nb, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
+        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
   MX_LAUNCH_CHECK();
 
   const int64_t ntiles = sweep_tiles(N);
@@ -564,6 +577,8 @@ struct BwdArgs {
   const int32_t* cum;
   const int32_t* infos;
   const float* iw_sorted;  // per-sample weights in sorted order, or null
+  const int32_t* B_off;    // VBE: first bag of each table [T+1], or null (fixed batch)
+  const int64_t* row_out;  // VBE: gradient row offset of each bag, or null
   const uint32_t* num_runs;
   const uint32_t* chunk_start;
   uint32_t* chunk_run;  // written by bwd_chunk_kernel, read by bwd_long_run_kernel
@@ -643,15 +658,16 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
   const uint32_t bmask = a.nb >= 32 ? 0xffffffffu : ((1u << a.nb) - 1u);
   for (int64_t base = s0; base < s1; base += G) {
     const int n = static_cast<int>(s1 - base < G ? s1 - base : G);
-    int32_t my_b = 0;
-    float my_s = 1.0f;  // MEAN: 1/L of the occurrence's bag
-    float my_w = 1.0f;  // weighted: the occurrence's per-sample weight
+    int64_t my_row = 0;  // element offset of the occurrence's gradient row slice
+    float my_s = 1.0f;   // MEAN: 1/L of the occurrence's bag
+    float my_w = 1.0f;   // weighted: the occurrence's per-sample weight
     if (k < n) {
       const int32_t info = base == s0 ? info0 : a.infos[base + k];
-      my_b = static_cast<int32_t>(static_cast<uint32_t>(info) & bmask);
+      const int64_t b = static_cast<int64_t>(static_cast<uint32_t>(info) & bmask);
+      const int64_t bag = a.B_off ? a.B_off[t] + b : t * a.B + b;
+      my_row = a.row_out ? a.row_out[bag] : b * a.total_D + D0;
       if (a.pooling == MX_POOL_MEAN) {
         const I* off = static_cast<const I*>(a.offsets);
-        const int64_t bag = t * a.B + my_b;
         const int64_t L = static_cast<int64_t>(off[bag + 1]) - static_cast<int64_t>(off[bag]);
         my_s = L > 0 ? 1.0f / static_cast<float>(L) : 0.0f;
       }
@@ -663,8 +679,7 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
-          const int64_t b = __shfl(my_b, g * G + j + u, 64);
-          const float* row = a.grad + b * a.total_D + D0;
+          const float* row = a.grad + __shfl(my_row, g * G + j + u, 64);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
             if ((c * G + k) * 4 < D) ld4(row + (c * G + k) * 4, v[u][c]);
@@ -1064,27 +1079,42 @@ extern "C" size_t mx_tbe_transpose_workspace_bytes(int64_t N, int32_t total_hash
   return carve_sort(nullptr, N).bytes;
 }
 
-static int check_common(int32_t T, int64_t B, int32_t bits, int32_t nb, int32_t index_bytes,
-                        int64_t N) {
-  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative size");
+namespace {
+
+// Batch layout of a call: a fixed batch B per table (all pointers null,
+// nbags = T * B), or variable batch per feature (VBE): b_t_map [nbags] info
+// word (t << info_B_num_bits) | b of each bag, and for the backward also
+// B_offsets [T+1] (first bag of each table) and row_out [nbags] (gradient row
+// offset of each bag).
+struct Layout {
+  int64_t nbags;
+  const int32_t* B_offsets;
+  const int64_t* row_out;
+  const int32_t* b_t_map;
+};
+
+int check_common(int32_t T, int64_t B, const Layout& lay, int32_t bits, int32_t nb,
+                 int32_t index_bytes, int64_t N) {
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0 && lay.nbags >= 0, "negative size");
   MX_REQUIRE(bits >= 0 && bits <= 32, "total_hash_size_bits %d not in [0, 32]", bits);
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
   MX_REQUIRE(N < 0x7fffffffll, "N %lld too large for int32 run offsets", (long long)N);
   MX_REQUIRE(nb >= 1 && nb <= 32, "info_B_num_bits %d invalid", nb);
   MX_REQUIRE(B <= (int64_t(1) << nb), "B does not fit info_B_num_bits");
-  MX_REQUIRE(N == 0 || (T > 0 && B > 0), "%lld indices but no bags (T=%d, B=%lld)",
-             (long long)N, T, (long long)B);
+  MX_REQUIRE(N == 0 || (T > 0 && lay.nbags > 0), "%lld indices but no bags (T=%d, bags=%lld)",
+             (long long)N, T, (long long)lay.nbags);
   return MX_OK;
 }
 
-extern "C" int mx_tbe_transpose_embedding_input(
-    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
-    int32_t info_B_num_bits, const void* indices, const void* offsets, int32_t index_bytes,
-    int64_t N, int64_t* linear_indices, int64_t* sorted_linear_indices, int32_t* infos_sorted,
-    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
-    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  if (int rc = check_common(T, B, total_hash_size_bits, info_B_num_bits, index_bytes, N)) return rc;
+int transpose_impl(const int64_t* hash_size_cumsum, int32_t T, int64_t B, const Layout& lay,
+                   int32_t total_hash_size_bits, int32_t info_B_num_bits, const void* indices,
+                   const void* offsets, int32_t index_bytes, int64_t N, int64_t* linear_indices,
+                   int64_t* sorted_linear_indices, int32_t* infos_sorted,
+                   int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+                   int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  if (int rc = check_common(T, B, lay, total_hash_size_bits, info_B_num_bits, index_bytes, N))
+    return rc;
   auto* s = as_stream(stream);
   if (N == 0) {  // no runs: num_runs = 0, cumulative_run_lengths = {0}
     if (num_runs || cumulative_run_lengths) {
@@ -1101,28 +1131,20 @@ extern "C" int mx_tbe_transpose_embedding_input(
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   TransposeOut o{linear_indices, sorted_linear_indices, infos_sorted, sorted_linear_indices_run,
                  run_lengths, num_runs, cumulative_run_lengths, nullptr};
-  return run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, info_B_num_bits, indices,
-                       offsets, index_bytes, N, nullptr, o, w, s);
+  return run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map, total_hash_size_bits,
+                       info_B_num_bits, indices, offsets, index_bytes, N, nullptr, o, w, s);
 }
 
-extern "C" size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits,
-                                                  int32_t max_D) {
-  (void)total_hash_size_bits;
-  return carve_bwd(nullptr, N, max_D > 0 ? max_D : 1).bytes;
-}
-
-extern "C" int mx_tbe_backward_rowwise_adagrad(
-    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
-    int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
-    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
-    int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
-    float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
-    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
-    void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  const int32_t nb = mx_tbe_info_B_num_bits(T, B);
-  MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
-  if (int rc = check_common(T, B, total_hash_size_bits, nb, index_bytes, N)) return rc;
+int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offsets,
+                  const int32_t* D_offsets, int32_t T, int64_t B, int32_t nb, const Layout& lay,
+                  int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+                  const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+                  int32_t pooling_mode, const float* indice_weights, const float* grad_output,
+                  int64_t total_D, float* momentum1, const int64_t* momentum1_offsets,
+                  float learning_rate, float eps, float weight_decay, int32_t weight_decay_mode,
+                  int32_t stochastic_rounding, uint64_t seed, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(T, B, lay, total_hash_size_bits, nb, index_bytes, N)) return rc;
   MX_REQUIRE(max_D > 0 && max_D <= 1024 && max_D % 4 == 0,
              "max_D %d must be a multiple of 4 in [4, 1024]", max_D);
   MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
@@ -1141,8 +1163,9 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   auto* s = as_stream(stream);
   TransposeOut o{nullptr, w.sorted, w.infos, w.run, nullptr, nullptr, w.cum,
                  indice_weights ? w.weights_sorted : nullptr};
-  if (int rc = run_transpose(hash_size_cumsum, T, B, total_hash_size_bits, nb, indices, offsets,
-                             index_bytes, N, indice_weights, o, w.sort, s))
+  if (int rc = run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map,
+                             total_hash_size_bits, nb, indices, offsets, index_bytes, N,
+                             indice_weights, o, w.sort, s))
     return rc;
   // Chunk layout of long runs.
   if (int rc = prefix_scan_epi(
@@ -1163,6 +1186,8 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
   a.cum = w.cum;
   a.infos = w.infos;
   a.iw_sorted = indice_weights ? w.weights_sorted : nullptr;
+  a.B_off = lay.b_t_map ? lay.B_offsets : nullptr;
+  a.row_out = lay.b_t_map ? lay.row_out : nullptr;
   a.num_runs = &w.sort.counters[0];
   a.chunk_start = w.chunk_start;
   a.chunk_run = w.chunk_run;
@@ -1185,4 +1210,84 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
                             : dispatch_bwd<int32_t, __half>(a, N, s);
   return index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, N, s)
                           : dispatch_bwd<int32_t, float>(a, N, s);
+}
+
+}  // namespace
+
+extern "C" int mx_tbe_transpose_embedding_input(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
+    int32_t info_B_num_bits, const void* indices, const void* offsets, int32_t index_bytes,
+    int64_t N, int64_t* linear_indices, int64_t* sorted_linear_indices, int32_t* infos_sorted,
+    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const Layout lay{static_cast<int64_t>(T) * B, nullptr, nullptr, nullptr};
+  return transpose_impl(hash_size_cumsum, T, B, lay, total_hash_size_bits, info_B_num_bits,
+                        indices, offsets, index_bytes, N, linear_indices, sorted_linear_indices,
+                        infos_sorted, sorted_linear_indices_run, run_lengths, num_runs,
+                        cumulative_run_lengths, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mx_tbe_transpose_embedding_input_vbe(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t total_B, const int32_t* vbe_b_t_map,
+    int32_t total_hash_size_bits, int32_t info_B_num_bits, const void* indices,
+    const void* offsets, int32_t index_bytes, int64_t N, int64_t* linear_indices,
+    int64_t* sorted_linear_indices, int32_t* infos_sorted, int64_t* sorted_linear_indices_run,
+    int32_t* run_lengths, int32_t* num_runs, int32_t* cumulative_run_lengths, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  clear_error();
+  MX_REQUIRE(total_B == 0 || vbe_b_t_map, "VBE needs the b_t map");
+  // Sorting needs only each bag's info word.
+  const Layout lay{total_B, nullptr, nullptr, vbe_b_t_map};
+  return transpose_impl(hash_size_cumsum, T, 0, lay, total_hash_size_bits, info_B_num_bits,
+                        indices, offsets, index_bytes, N, linear_indices, sorted_linear_indices,
+                        infos_sorted, sorted_linear_indices_run, run_lengths, num_runs,
+                        cumulative_run_lengths, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits,
+                                                  int32_t max_D) {
+  (void)total_hash_size_bits;
+  return carve_bwd(nullptr, N, max_D > 0 ? max_D : 1).bytes;
+}
+
+extern "C" int mx_tbe_backward_rowwise_adagrad(
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
+    int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
+    float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
+    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const int32_t nb = mx_tbe_info_B_num_bits(T, B);
+  MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
+  const Layout lay{static_cast<int64_t>(T) * B, nullptr, nullptr, nullptr};
+  return backward_impl(weights, weights_ty, weights_offsets, D_offsets, T, B, nb, lay, max_D,
+                       hash_size_cumsum, total_hash_size_bits, indices, offsets, index_bytes, N,
+                       pooling_mode, indice_weights, grad_output, total_D, momentum1,
+                       momentum1_offsets, learning_rate, eps, weight_decay, weight_decay_mode,
+                       stochastic_rounding, seed, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mx_tbe_backward_rowwise_adagrad_vbe(
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
+    int32_t T, int64_t max_B, int32_t max_D, const int64_t* hash_size_cumsum,
+    int32_t total_hash_size_bits, const void* indices, const void* offsets, int32_t index_bytes,
+    int64_t N, int32_t pooling_mode, const float* indice_weights, const float* grad_output,
+    int64_t total_B, const int32_t* B_offsets, const int64_t* vbe_row_output_offsets,
+    const int32_t* vbe_b_t_map, int32_t info_B_num_bits, float* momentum1,
+    const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
+    int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  clear_error();
+  MX_REQUIRE(total_B == 0 || (B_offsets && vbe_row_output_offsets && vbe_b_t_map),
+             "VBE needs B_offsets, row output offsets and the b_t map");
+  const Layout lay{total_B, B_offsets, vbe_row_output_offsets, vbe_b_t_map};
+  return backward_impl(weights, weights_ty, weights_offsets, D_offsets, T, max_B,
+                       info_B_num_bits, lay, max_D, hash_size_cumsum, total_hash_size_bits,
+                       indices, offsets, index_bytes, N, pooling_mode, indice_weights,
+                       grad_output, 0, momentum1, momentum1_offsets, learning_rate, eps,
+                       weight_decay, weight_decay_mode, stochastic_rounding, seed, workspace,
+                       workspace_bytes, stream);
 }

@@ -66,6 +66,35 @@ __device__ __forceinline__ void load_row4(const __half* p, float (&v)[4]) {
 
 constexpr int kWavesPerBlock = 4;
 
+}  // namespace
+
+// Where bag i of the flattened (t, b) bag space lives: fixed batch (t = i / B,
+// output row b of stride total_D) or variable batch per feature ("VBE": the
+// bag's (t << nb) | b word and its output element offset, both per bag).
+struct BagMap {
+  int64_t B;
+  int64_t total_D;
+  const int32_t* b_t_map;  // VBE only
+  const int64_t* row_out;  // VBE only
+  int32_t nb;              // VBE only
+  __device__ __forceinline__ void locate(int64_t bag, int64_t& t, int64_t& b) const {
+    if (b_t_map) {
+      const uint32_t info = static_cast<uint32_t>(b_t_map[bag]);
+      t = nb >= 32 ? 0 : static_cast<int64_t>(info >> nb);
+      b = static_cast<int64_t>(nb >= 32 ? info : (info & ((1u << nb) - 1u)));
+    } else {
+      t = bag / B;
+      b = bag - t * B;
+    }
+  }
+  // First element of the bag's output (and gradient) row.
+  __device__ __forceinline__ int64_t out_base(int64_t bag, int64_t b, int32_t D0) const {
+    return row_out ? row_out[bag] : b * total_D + D0;
+  }
+};
+
+namespace {
+
 // A wave serves 64/G bags at once, G lanes per bag, lane k owning columns
 // (c*G + k)*4 .. +4 (float4 loads: a D=128 row is one 512 B access of 32
 // lanes).  Several bags per wave keep several independent offsets -> indices
@@ -73,18 +102,18 @@ constexpr int kWavesPerBlock = 4;
 template <typename I, typename WT, int G, int NCH, int U, bool WEIGHTED, bool OUT_F16>
 __global__ void __launch_bounds__(256)
     tbe_fwd_group_kernel(const WT* __restrict__ W, const int64_t* __restrict__ w_off,
-                         const int32_t* __restrict__ D_off, int64_t B,
+                         const int32_t* __restrict__ D_off, BagMap bm,
                          const I* __restrict__ indices, const I* __restrict__ offsets,
                          int32_t pooling, const float* __restrict__ iw, void* __restrict__ out,
-                         int64_t total_D, int64_t nbags) {
+                         int64_t nbags) {
   constexpr int P = 64 / G;
   const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
   const int64_t bag = (lb * kWavesPerBlock + (threadIdx.x >> 6)) * P + g;
   if (bag >= nbags) return;  // whole group
-  const int64_t t = bag / B;
-  const int64_t b = bag - t * B;
+  int64_t t, b;
+  bm.locate(bag, t, b);
   const int32_t D0 = D_off[t];
   const int32_t D = D_off[t + 1] - D0;
   const WT* __restrict__ Wt = W + w_off[t];
@@ -145,7 +174,7 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[c][e] *= inv;
   }
-  const int64_t obase = b * total_D + D0;
+  const int64_t obase = bm.out_base(bag, b, D0);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (!active[c]) continue;
@@ -169,9 +198,9 @@ __global__ void __launch_bounds__(256)
 // xor-tree order.
 template <typename I, typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256)
-    grad_indice_weights_kernel(const float* __restrict__ grad, int64_t total_D,
+    grad_indice_weights_kernel(const float* __restrict__ grad, BagMap bm,
                                const WT* __restrict__ W, const int64_t* __restrict__ w_off,
-                               const int32_t* __restrict__ D_off, int64_t B,
+                               const int32_t* __restrict__ D_off,
                                const I* __restrict__ indices, const I* __restrict__ offsets,
                                int32_t pooling, const int32_t* __restrict__ frg,
                                float* __restrict__ out, int64_t nbags) {
@@ -181,8 +210,8 @@ __global__ void __launch_bounds__(256)
   const int g = lane / G, k = lane % G;
   const int64_t bag = (lb * kWavesPerBlock + (threadIdx.x >> 6)) * P + g;
   if (bag >= nbags) return;  // whole group
-  const int64_t t = bag / B;
-  const int64_t b = bag - t * B;
+  int64_t t, b;
+  bm.locate(bag, t, b);
   const int64_t start = static_cast<int64_t>(offsets[bag]);
   const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
   if (frg != nullptr && frg[t] == 0) {
@@ -198,7 +227,7 @@ __global__ void __launch_bounds__(256)
   for (int c = 0; c < NCH; ++c) {
     active[c] = (c * G + k) * 4 < D;
     if (active[c])
-      load_vec<4>(grad + b * total_D + D0 + (c * G + k) * 4, gv[c]);
+      load_vec<4>(grad + bm.out_base(bag, b, D0) + (c * G + k) * 4, gv[c]);
     else
       gv[c][0] = gv[c][1] = gv[c][2] = gv[c][3] = 0.0f;
   }
@@ -238,22 +267,22 @@ __global__ void __launch_bounds__(256)
 
 template <typename I, typename WT, int G, int NCH, bool WEIGHTED, bool OUT_F16>
 void launch_fwd_group(hipStream_t s, const WT* W, const int64_t* w_off, const int32_t* D_off,
-                      int64_t B, const void* idx, const void* off, int32_t pooling,
-                      const float* iw, void* out, int64_t total_D, int64_t nbags) {
+                      const BagMap& bm, const void* idx, const void* off, int32_t pooling,
+                      const float* iw, void* out, int64_t nbags) {
   constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
   constexpr int P = 64 / G;
   const int64_t grid = ceil_div(nbags, kWavesPerBlock * P);
   tbe_fwd_group_kernel<I, WT, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
-      W, w_off, D_off, B, static_cast<const I*>(idx), static_cast<const I*>(off), pooling, iw, out,
-      total_D, nbags);
+      W, w_off, D_off, bm, static_cast<const I*>(idx), static_cast<const I*>(off), pooling, iw, out,
+      nbags);
 }
 
 template <typename I, typename WT, bool WEIGHTED, bool OUT_F16>
 int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off,
-                 const int32_t* D_off, int64_t B, const void* idx, const void* off,
-                 int32_t pooling, const float* iw, void* out, int64_t total_D, int64_t nbags) {
+                 const int32_t* D_off, const BagMap& bm, const void* idx, const void* off,
+                 int32_t pooling, const float* iw, void* out, int64_t nbags) {
 #define MX_FWD_G(G, NCH) \
-  launch_fwd_group<I, WT, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, B, idx, off, pooling, iw, out, total_D, nbags)
+  launch_fwd_group<I, WT, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, bm, idx, off, pooling, iw, out, nbags)
   if (max_D <= 64)
     MX_FWD_G(16, 1);  // 4 bags per wave
   else if (max_D <= 128)
@@ -273,14 +302,14 @@ int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off
 
 using namespace mx;
 
-extern "C" int mx_tbe_forward(const void* weights, int32_t weights_ty,
-                              const int64_t* weights_offsets,
-                              const int32_t* D_offsets, int32_t T, int64_t B, int32_t max_D,
-                              const void* indices, const void* offsets, int32_t index_bytes,
-                              int32_t pooling_mode, const float* indice_weights, void* out,
-                              int32_t out_dtype, int64_t total_D, void* stream) {
-  clear_error();
-  MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+namespace {
+
+int tbe_forward_impl(const void* weights, int32_t weights_ty, const int64_t* weights_offsets,
+                     const int32_t* D_offsets, int32_t T, int64_t nbags, int32_t max_D,
+                     const void* indices, const void* offsets, int32_t index_bytes,
+                     int32_t pooling_mode, const float* indice_weights, void* out,
+                     int32_t out_dtype, const BagMap& bm, bool has_output, void* stream) {
+  MX_REQUIRE(T >= 0 && nbags >= 0, "negative T or bag count");
   MX_REQUIRE(max_D >= 0 && max_D <= 1024 && max_D % 4 == 0,
              "max_D %d must be a multiple of 4 in [0, 1024]", max_D);
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
@@ -290,15 +319,14 @@ extern "C" int mx_tbe_forward(const void* weights, int32_t weights_ty,
              "output_dtype %d not supported (FP32=0, FP16=1)", out_dtype);
   MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
              "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
-  const int64_t nbags = static_cast<int64_t>(T) * B;
-  if (nbags == 0 || total_D == 0) return MX_OK;
+  if (nbags == 0 || !has_output) return MX_OK;
   MX_REQUIRE(weights && weights_offsets && D_offsets && offsets && out, "null pointer argument");
   MX_REQUIRE(ceil_div(nbags, kWavesPerBlock) <= 0x7fffffffll, "too many bags");
   auto* s = as_stream(stream);
   const bool w = indice_weights != nullptr;
   const bool h = out_dtype == MX_SPARSE_FP16;
-#define MX_ARGS(WT) s, max_D, static_cast<const WT*>(weights), weights_offsets, D_offsets, B, \
-                indices, offsets, pooling_mode, indice_weights, out, total_D, nbags
+#define MX_ARGS(WT) s, max_D, static_cast<const WT*>(weights), weights_offsets, D_offsets, bm, \
+                indices, offsets, pooling_mode, indice_weights, out, nbags
 #define MX_FWD_W(I, WT)                                                                          \
   if (w)                                                                                         \
     h ? dispatch_fwd<I, WT, true, true>(MX_ARGS(WT)) : dispatch_fwd<I, WT, true, false>(MX_ARGS(WT)); \
@@ -324,16 +352,49 @@ extern "C" int mx_tbe_forward(const void* weights, int32_t weights_ty,
   return MX_OK;
 }
 
-extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D,
-                                          const void* weights, int32_t weights_ty,
-                                          const int64_t* weights_offsets,
-                                          const int32_t* D_offsets, int32_t T, int64_t B,
-                                          int32_t max_D, const void* indices, const void* offsets,
-                                          int32_t index_bytes, int32_t pooling_mode,
-                                          const int32_t* feature_requires_grad,
-                                          float* grad_indice_weights, void* stream) {
+}  // namespace
+
+extern "C" int mx_tbe_forward(const void* weights, int32_t weights_ty,
+                              const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T,
+                              int64_t B, int32_t max_D, const void* indices, const void* offsets,
+                              int32_t index_bytes, int32_t pooling_mode,
+                              const float* indice_weights, void* out, int32_t out_dtype,
+                              int64_t total_D, void* stream) {
   clear_error();
   MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+  const BagMap bm{B, total_D, nullptr, nullptr, 0};
+  return tbe_forward_impl(weights, weights_ty, weights_offsets, D_offsets, T,
+                          static_cast<int64_t>(T) * B, max_D, indices, offsets, index_bytes,
+                          pooling_mode, indice_weights, out, out_dtype, bm, total_D > 0, stream);
+}
+
+extern "C" int mx_tbe_forward_vbe(const void* weights, int32_t weights_ty,
+                                  const int64_t* weights_offsets, const int32_t* D_offsets,
+                                  int32_t T, int64_t total_B, int32_t max_D, const void* indices,
+                                  const void* offsets, int32_t index_bytes, int32_t pooling_mode,
+                                  const float* indice_weights, const int64_t* vbe_row_output_offsets,
+                                  const int32_t* vbe_b_t_map, int32_t info_B_num_bits, void* out,
+                                  int32_t out_dtype, void* stream) {
+  clear_error();
+  MX_REQUIRE(info_B_num_bits >= 1 && info_B_num_bits <= 32, "info_B_num_bits %d invalid",
+             info_B_num_bits);
+  MX_REQUIRE(total_B == 0 || (vbe_row_output_offsets && vbe_b_t_map),
+             "VBE metadata (row output offsets, b_t map) required");
+  const BagMap bm{0, 0, vbe_b_t_map, vbe_row_output_offsets, info_B_num_bits};
+  return tbe_forward_impl(weights, weights_ty, weights_offsets, D_offsets, T, total_B, max_D,
+                          indices, offsets, index_bytes, pooling_mode, indice_weights, out,
+                          out_dtype, bm, true, stream);
+}
+
+namespace {
+
+int grad_indice_weights_impl(const float* grad_output, const BagMap& bm, const void* weights,
+                             int32_t weights_ty, const int64_t* weights_offsets,
+                             const int32_t* D_offsets, int32_t T, int64_t nbags, int32_t max_D,
+                             const void* indices, const void* offsets, int32_t index_bytes,
+                             int32_t pooling_mode, const int32_t* feature_requires_grad,
+                             float* grad_indice_weights, void* stream) {
+  MX_REQUIRE(T >= 0 && nbags >= 0, "negative T or bag count");
   MX_REQUIRE(max_D >= 0 && max_D <= 1024 && max_D % 4 == 0,
              "max_D %d must be a multiple of 4 in [0, 1024]", max_D);
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
@@ -341,7 +402,6 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
              "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
   MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
              "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
-  const int64_t nbags = static_cast<int64_t>(T) * B;
   if (nbags == 0) return MX_OK;
   MX_REQUIRE(grad_output && weights && weights_offsets && D_offsets && offsets &&
                  grad_indice_weights,
@@ -358,7 +418,7 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
   grad_indice_weights_kernel<I, WT, G, NCH, U><<<dim3(static_cast<uint32_t>(                  \
                                                ceil_div(nbags, kWavesPerBlock * (64 / G)))),   \
                                            256, 0, s>>>(                                      \
-      grad_output, total_D, static_cast<const WT*>(weights), weights_offsets, D_offsets, B,    \
+      grad_output, bm, static_cast<const WT*>(weights), weights_offsets, D_offsets,            \
       static_cast<const I*>(indices), static_cast<const I*>(offsets), pooling_mode,            \
       feature_requires_grad, grad_indice_weights, nbags)
 #define MX_GIW_D(I)                 \
@@ -382,4 +442,42 @@ extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t tota
 #undef MX_GIW_T
   MX_LAUNCH_CHECK();
   return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_tbe_grad_indice_weights(const float* grad_output, int64_t total_D,
+                                          const void* weights, int32_t weights_ty,
+                                          const int64_t* weights_offsets,
+                                          const int32_t* D_offsets, int32_t T, int64_t B,
+                                          int32_t max_D, const void* indices, const void* offsets,
+                                          int32_t index_bytes, int32_t pooling_mode,
+                                          const int32_t* feature_requires_grad,
+                                          float* grad_indice_weights, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
+  const BagMap bm{B, total_D, nullptr, nullptr, 0};
+  return grad_indice_weights_impl(grad_output, bm, weights, weights_ty, weights_offsets,
+                                  D_offsets, T, static_cast<int64_t>(T) * B, max_D, indices,
+                                  offsets, index_bytes, pooling_mode, feature_requires_grad,
+                                  grad_indice_weights, stream);
+}
+
+extern "C" int mx_tbe_grad_indice_weights_vbe(
+    const float* grad_output, const void* weights, int32_t weights_ty,
+    const int64_t* weights_offsets, const int32_t* D_offsets, int32_t T, int64_t total_B,
+    int32_t max_D, const void* indices, const void* offsets, int32_t index_bytes,
+    int32_t pooling_mode, const int64_t* vbe_row_output_offsets, const int32_t* vbe_b_t_map,
+    int32_t info_B_num_bits, const int32_t* feature_requires_grad, float* grad_indice_weights,
+    void* stream) {
+  clear_error();
+  MX_REQUIRE(info_B_num_bits >= 1 && info_B_num_bits <= 32, "info_B_num_bits %d invalid",
+             info_B_num_bits);
+  MX_REQUIRE(total_B == 0 || (vbe_row_output_offsets && vbe_b_t_map),
+             "VBE metadata (row output offsets, b_t map) required");
+  const BagMap bm{0, 0, vbe_b_t_map, vbe_row_output_offsets, info_B_num_bits};
+  return grad_indice_weights_impl(grad_output, bm, weights, weights_ty, weights_offsets,
+                                  D_offsets, T, total_B, max_D, indices, offsets, index_bytes,
+                                  pooling_mode, feature_requires_grad, grad_indice_weights,
+                                  stream);
 }

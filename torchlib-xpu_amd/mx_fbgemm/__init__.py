@@ -41,6 +41,12 @@ OPS = (
     "split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
     "split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda",
     "split_embedding_codegen_grad_indice_weights_cuda",
+    "generate_vbe_metadata",
+    "split_embedding_codegen_forward_unweighted_vbe_cuda",
+    "split_embedding_codegen_forward_weighted_vbe_cuda",
+    "split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_vbe_cuda",
+    "split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_vbe_cuda",
+    "split_embedding_codegen_grad_indice_weights_vbe_cuda",
     "split_embedding_codegen_lookup_rowwise_adagrad_function",
     "int_nbit_split_embedding_codegen_lookup_function",
     "bounds_check_indices",

@@ -51,6 +51,12 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     each row is scaled by its weight before pooling, the fused update uses the
     weighted row gradient, and the weights themselves receive a gradient when
     they require one (``feature_requires_grad`` [T] masks tables out).
+
+    ``batch_size_per_feature_per_rank`` ([T][R] ints) selects variable batch
+    size per feature (VBE): table t has sum_r B[t][r] bags, offsets has
+    sum_t sum_r B[t][r] + 1 entries (feature-major, rank-major within a
+    feature), and the output is one flat tensor, rank-major then
+    feature-major, holding B[t][r] rows of D_t per (rank, feature).
     """
 
     def __init__(
@@ -140,22 +146,51 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self._rows = rows
         self._dims = dims
 
+    def _vbe_args(self, batch_size_per_feature_per_rank: list[list[int]], device):
+        """B_offsets, output offsets per (rank, feature), batch offsets per
+        feature and rank, max_B, max_B_feature_rank, output size."""
+        bs = batch_size_per_feature_per_rank
+        if len(bs) != self.T or len({len(r) for r in bs}) != 1:
+            raise ValueError("batch_size_per_feature_per_rank must be [T][R]")
+        R = len(bs[0])
+        per_feature = [sum(r) for r in bs]
+        B_offsets = _cumsum(per_feature)
+        rpf = [_cumsum(r) for r in bs]
+        out_sizes = [bs[t][r] * self._dims[t] for r in range(R) for t in range(self.T)]
+        i32 = dict(device=device, dtype=torch.int32)
+        return dict(
+            B_offsets=torch.tensor(B_offsets, **i32),
+            vbe_output_offsets_feature_rank=torch.tensor(_cumsum(out_sizes), device=device,
+                                                         dtype=torch.int64),
+            vbe_B_offsets_rank_per_feature=torch.tensor(rpf, **i32),
+            max_B=max(per_feature), max_B_feature_rank=max(max(r) for r in bs),
+            vbe_output_size=sum(out_sizes))
+
     def forward(self, indices: torch.Tensor, offsets: torch.Tensor,
                 per_sample_weights: Optional[torch.Tensor] = None,
-                feature_requires_grad: Optional[torch.Tensor] = None) -> torch.Tensor:
+                feature_requires_grad: Optional[torch.Tensor] = None,
+                batch_size_per_feature_per_rank: Optional[list[list[int]]] = None
+                ) -> torch.Tensor:
         if per_sample_weights is not None:
             if per_sample_weights.dtype != torch.float32:
                 raise ValueError("per_sample_weights must be fp32")
             if per_sample_weights.numel() != indices.numel():
                 raise ValueError("per_sample_weights must have one entry per index")
-        if (offsets.numel() - 1) % self.T:
+        vbe = (self._vbe_args(batch_size_per_feature_per_rank, indices.device)
+               if batch_size_per_feature_per_rank is not None else None)
+        if vbe is not None:
+            if offsets.numel() - 1 != int(vbe["B_offsets"][-1]):
+                raise ValueError("offsets must have one entry per bag of every feature, plus one")
+        elif (offsets.numel() - 1) % self.T:
             raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
         if indices.dtype != offsets.dtype:
             offsets = offsets.to(indices.dtype)
         if self.bounds_check_mode != BoundsCheckMode.NONE:
-            torch.ops.fbgemm.bounds_check_indices(self.rows_per_table, indices, offsets,
-                                                  int(self.bounds_check_mode),
-                                                  self.bounds_check_warning, per_sample_weights)
+            torch.ops.fbgemm.bounds_check_indices(
+                self.rows_per_table, indices, offsets, int(self.bounds_check_mode),
+                self.bounds_check_warning, per_sample_weights,
+                vbe["B_offsets"] if vbe is not None else None,
+                vbe["max_B"] if vbe is not None else -1)
         return torch.ops.fbgemm.split_embedding_codegen_lookup_rowwise_adagrad_function(
             self.placeholder_autograd_tensor, self.weights_dev, self.weights_uvm,
             self.lxu_cache_weights, self.weights_placements, self.weights_offsets,
@@ -165,7 +200,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
             self.lxu_cache_locations, False, 0.0, self.stochastic_rounding, self.momentum1_dev,
             self.momentum1_uvm,
             self.weights_placements, self.momentum1_offsets, self.eps, self.learning_rate,
-            self.weight_decay, self.weight_decay_mode, 0.0, int(SparseType.FP32.as_int()))
+            self.weight_decay, self.weight_decay_mode, 0.0, int(SparseType.FP32.as_int()),
+            **(vbe or {}))
 
     @torch.no_grad()
     def split_embedding_weights(self) -> list[torch.Tensor]:
