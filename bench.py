@@ -43,7 +43,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="workload; 2 (default) is the headline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (PMC byte-counter calibration)")
@@ -108,6 +108,54 @@ def cpu_model() -> str:
 
 
 # ---------------------------------------------------------------------------
+
+
+def bench_jagged(args, dev):
+    """Config 1: jagged_to_padded_dense then dense_to_jagged (one round trip
+    per step) on B=512 rows of up to 64 x 128 fp32."""
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    cfg = bench_inputs.config1()
+    v = torch.from_numpy(cfg.values).to(dev)
+    off = torch.from_numpy(cfg.offsets).to(dev)
+    B, D, L, total = cfg.offsets.size - 1, cfg.values.shape[1], cfg.max_L, cfg.values.shape[0]
+    j2pd = torch.ops.fbgemm.jagged_to_padded_dense
+    d2j = torch.ops.fbgemm.dense_to_jagged
+
+    def step():
+        dense = j2pd(v, [off], [L], 0.0)
+        return d2j(dense, [off], total)
+
+    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    # j2pd reads the values and writes the padded dense; d2j reads the dense at
+    # the jagged positions and writes the values; both read the offsets.
+    alg = total * D * 4 + B * L * D * 4 + 2 * total * D * 4 + 2 * (B + 1) * 8
+    res = dict(
+        metric="jagged round trip (jagged_to_padded_dense + dense_to_jagged) bytes/s, 1 MI355X",
+        value=alg * args.steps / wall / 1e9, unit="GB/s", ms_per_step=wall / args.steps * 1e3,
+        dtype="fp32",
+        config={"workload": "config1: jagged round trip, B=512 D=128 max_L=64, len~U{0..64}",
+                "B": B, "D": D, "max_L": L, "total_L": total},
+        kernel="j2pd_kernel + d2j_kernel (one step)", alg_bytes=alg, kernel_ms_mean=mean_ms,
+        kernel_ms_median=med_ms)
+    cpu = None
+    if not args.no_cpu_baseline:
+        vc, oc = v.cpu(), off.cpu()
+
+        def cpu_step():
+            dense = torch.ops.aten._jagged_to_padded_dense_forward(vc, [oc], [L], 0.0)
+            return torch.ops.aten._padded_dense_to_jagged_forward(dense, [oc], total)
+
+        med, runs = cpu_time(cpu_step, args.cpu_seconds)
+        cpu = dict(value=alg / med / 1e9, unit="GB/s", cores=torch.get_num_threads(),
+                   kind="reference",
+                   sample=(f"full config-1 round trip, median of {runs} runs; torch's CPU "
+                           f"aten._jagged_to_padded_dense_forward / _padded_dense_to_jagged_forward "
+                           f"(its port of the fbgemm jagged ops) on {torch.get_num_threads()} "
+                           f"threads; host CPU: {cpu_model()}"))
+    return res, traffic_from_profile("jagged_config1"), cpu
 
 
 def bench_tbe_forward(args, dev):
@@ -367,7 +415,9 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4,
                           "launches": args.steps}))
         return
-    if args.config == 2:
+    if args.config == 1:
+        res, traffic, cpu = bench_jagged(args, dev)
+    elif args.config == 2:
         res, traffic, cpu = bench_tbe_forward(args, dev)
     elif args.config == 3:
         res, traffic, cpu = bench_backward(args, dev)

@@ -9,10 +9,12 @@
 //
 // Design: the ops are pure HBM streams.  One work item moves VEC bytes
 // (16 when the row size and pointers allow it), consecutive work items walk
-// a row, so every wave issues fully coalesced 1 KiB transactions.  The
-// jagged coordinate of a dense row is found by walking the offsets levels
-// (dense -> jagged) or by a binary search per level (jagged -> dense); the
-// offsets are a few KB and stay in L2.
+// a row, so every wave issues fully coalesced 1 KiB transactions.  With one
+// jagged dim (the common case) a bag is a contiguous copy: one block row per
+// bag, no per-item index arithmetic.  With more, the jagged coordinate of a
+// dense row is found by walking the offsets levels (dense -> jagged) or by a
+// binary search per level (jagged -> dense); the offsets are a few KB and
+// stay in L2.
 #include "mx_common.h"
 
 namespace mx {
@@ -200,7 +202,118 @@ __global__ void __launch_bounds__(256) jagged_add_kernel(const uint8_t* __restri
   }
 }
 
+// ---- one jagged dimension: a bag is a contiguous copy ----------------------
+//
+// With a single jagged dim, bag b's values rows are [off[b], off[b+1]) and its
+// dense rows [b*max_L, (b+1)*max_L): both contiguous, so each bag is one
+// straight copy plus padding, with no per-chunk coordinate arithmetic.  Grid
+// (x = bag, y = part of the bag); every thread keeps kJagItems chunks in
+// flight.
+
+constexpr int kJagItems = 4;
+constexpr int64_t kJagSpan = 256 * kJagItems;
+
+template <int VEC, typename I>
+__global__ void __launch_bounds__(256)
+    j2pd1_kernel(const uint8_t* __restrict__ values, uint8_t* __restrict__ out,
+                 const I* __restrict__ off, int64_t max_L, int64_t vpr, Chunk<VEC> pad) {
+  const int64_t b = blockIdx.x;
+  const int64_t begin = static_cast<int64_t>(off[b]);
+  int64_t len = static_cast<int64_t>(off[b + 1]) - begin;
+  len = len < 0 ? 0 : (len > max_L ? max_L : len);
+  const int64_t n_copy = len * vpr, n_all = max_L * vpr;
+  const Chunk<VEC>* __restrict__ src = reinterpret_cast<const Chunk<VEC>*>(values) + begin * vpr;
+  Chunk<VEC>* __restrict__ dst = reinterpret_cast<Chunk<VEC>*>(out) + b * n_all;
+  for (int64_t base = blockIdx.y * kJagSpan; base < n_all; base += gridDim.y * kJagSpan) {
+    Chunk<VEC> c[kJagItems];
+#pragma unroll
+    for (int it = 0; it < kJagItems; ++it) {
+      const int64_t i = base + it * 256 + threadIdx.x;
+      c[it] = i < n_copy ? src[i] : pad;
+    }
+#pragma unroll
+    for (int it = 0; it < kJagItems; ++it) {
+      const int64_t i = base + it * 256 + threadIdx.x;
+      if (i < n_all) dst[i] = c[it];
+    }
+  }
+}
+
+// Values rows [r0, r1) whose first `copy_rows` rows take dense rows from
+// `dense_row0` on and the rest 0; ADD adds x (jagged + dense add), else the
+// dense value is copied (dense -> jagged).
+template <int VEC, bool ADD, int DT>
+__device__ __forceinline__ void emit_rows(const uint8_t* __restrict__ dense,
+                                          const uint8_t* __restrict__ x,
+                                          uint8_t* __restrict__ out, int64_t r0, int64_t r1,
+                                          int64_t copy_rows, int64_t dense_row0, int64_t vpr) {
+  const int64_t n_all = (r1 - r0) * vpr, n_copy = copy_rows * vpr;
+  const Chunk<VEC>* __restrict__ src = reinterpret_cast<const Chunk<VEC>*>(dense) + dense_row0 * vpr;
+  Chunk<VEC>* __restrict__ dst = reinterpret_cast<Chunk<VEC>*>(out) + r0 * vpr;
+  const Chunk<VEC>* __restrict__ xs = reinterpret_cast<const Chunk<VEC>*>(x) + r0 * vpr;
+  for (int64_t base = blockIdx.y * kJagSpan; base < n_all; base += gridDim.y * kJagSpan) {
+    Chunk<VEC> y[kJagItems];
+#pragma unroll
+    for (int it = 0; it < kJagItems; ++it) {
+      const int64_t i = base + it * 256 + threadIdx.x;
+      if (i < n_copy) {
+        y[it] = src[i];
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) y[it].b[e] = 0;  // +0 in every element type
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < kJagItems; ++it) {
+      const int64_t i = base + it * 256 + threadIdx.x;
+      if (i >= n_all) continue;
+      if constexpr (ADD) {
+        const Chunk<VEC> cx = xs[i];
+        Chunk<VEC> co;
+#pragma unroll
+        for (int e = 0; e < VEC; e += AddOp<DT>::kBytes)
+          AddOp<DT>::apply(cx.b + e, y[it].b + e, co.b + e);
+        dst[i] = co;
+      } else {
+        dst[i] = y[it];
+      }
+    }
+  }
+}
+
+// Block x < nbags: bag x.  Block x == nbags: the values rows no bag covers
+// (before off[0], from off[nbags] on), which have no dense position.  Row
+// ranges are clamped to [0, total_L], so malformed offsets never write out
+// of bounds.
+template <int VEC, typename I, bool ADD, int DT>
+__global__ void __launch_bounds__(256)
+    jagged_out1_kernel(const uint8_t* __restrict__ dense, const uint8_t* __restrict__ x,
+                       uint8_t* __restrict__ out, const I* __restrict__ off, int64_t nbags,
+                       int64_t max_L, int64_t total_L, int64_t vpr) {
+  auto clamp = [&](int64_t v, int64_t lo) { return v < lo ? lo : (v > total_L ? total_L : v); };
+  const int64_t b = blockIdx.x;
+  if (b < nbags) {
+    const int64_t r0 = clamp(static_cast<int64_t>(off[b]), 0);
+    const int64_t r1 = clamp(static_cast<int64_t>(off[b + 1]), r0);
+    const int64_t copy = r1 - r0 < max_L ? r1 - r0 : max_L;
+    emit_rows<VEC, ADD, DT>(dense, x, out, r0, r1, copy, b * max_L, vpr);
+  } else {
+    const int64_t head = clamp(static_cast<int64_t>(off[0]), 0);
+    const int64_t tail = clamp(static_cast<int64_t>(off[nbags]), head);
+    emit_rows<VEC, ADD, DT>(dense, x, out, 0, head, 0, 0, vpr);
+    emit_rows<VEC, ADD, DT>(dense, x, out, tail, total_L, 0, 0, vpr);
+  }
+}
+
 // ---- host side ------------------------------------------------------------
+
+// Grid of the single-jagged-dim kernels: one x per bag (plus extra), parts
+// of a bag in y.
+dim3 grid_1d(int64_t bags, int64_t chunks_per_bag) {
+  int64_t parts = ceil_div(chunks_per_bag > 0 ? chunks_per_bag : 1, kJagSpan);
+  if (parts > 64) parts = 64;  // the kernels loop over the rest
+  return dim3(static_cast<uint32_t>(bags), static_cast<uint32_t>(parts));
+}
 
 int pick_vec(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
   for (int vec : {16, 8, 4, 2, 1}) {
@@ -295,13 +408,24 @@ extern "C" int mx_jagged_to_padded_dense(const void* values, int64_t elem_bytes,
   auto* s = as_stream(stream);
   const auto* v = static_cast<const uint8_t*>(values);
   auto* o = static_cast<uint8_t*>(out);
+  const int64_t nbags = offsets_numel[0] - 1;
+  const bool one = num_jagged_dim == 1 && nbags <= 0x7fffffffll;
   MX_VEC_SWITCH(vec, {
     Chunk<V> pad;
     for (int i = 0; i < V; ++i) pad.b[i] = pat[i];
-    if (offset_bytes == 8)
+    if (one) {
+      const dim3 g = grid_1d(nbags, max_lengths[0] * vpr);
+      if (offset_bytes == 8)
+        j2pd1_kernel<V, int64_t><<<g, 256, 0, s>>>(
+            v, o, static_cast<const int64_t*>(offsets[0]), max_lengths[0], vpr, pad);
+      else
+        j2pd1_kernel<V, int32_t><<<g, 256, 0, s>>>(
+            v, o, static_cast<const int32_t*>(offsets[0]), max_lengths[0], vpr, pad);
+    } else if (offset_bytes == 8) {
       j2pd_kernel<V, int64_t><<<grid, 256, 0, s>>>(v, o, m, rows, vpr, pad);
-    else
+    } else {
       j2pd_kernel<V, int32_t><<<grid, 256, 0, s>>>(v, o, m, rows, vpr, pad);
+    }
   });
   MX_LAUNCH_CHECK();
   return MX_OK;
@@ -334,12 +458,24 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
   auto* s = as_stream(stream);
   const auto* d = static_cast<const uint8_t*>(dense);
   auto* o = static_cast<uint8_t*>(out);
+  const int64_t nbags = offsets_numel[0] - 1;
+  const bool one = num_jagged_dim == 1 && nbags < 0x7fffffffll;
+  const dim3 g1 = grid_1d(nbags + 1, max_lengths[0] * vpr);
+  const int64_t L0 = max_lengths[0];
   if (x_values == nullptr) {
     MX_VEC_SWITCH(vec, {
-      if (offset_bytes == 8)
+      if (one) {
+        if (offset_bytes == 8)
+          jagged_out1_kernel<V, int64_t, false, MX_DTYPE_F32><<<g1, 256, 0, s>>>(
+              d, nullptr, o, static_cast<const int64_t*>(offsets[0]), nbags, L0, total_L, vpr);
+        else
+          jagged_out1_kernel<V, int32_t, false, MX_DTYPE_F32><<<g1, 256, 0, s>>>(
+              d, nullptr, o, static_cast<const int32_t*>(offsets[0]), nbags, L0, total_L, vpr);
+      } else if (offset_bytes == 8) {
         d2j_kernel<V, int64_t><<<grid, 256, 0, s>>>(d, o, m, total_L, vpr);
-      else
+      } else {
         d2j_kernel<V, int32_t><<<grid, 256, 0, s>>>(d, o, m, total_L, vpr);
+      }
     });
     MX_LAUNCH_CHECK();
     return MX_OK;
@@ -350,7 +486,13 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
 #define MX_ADD_LAUNCH(DTC)                                                                 \
   MX_VEC_SWITCH(vec, {                                                                     \
     if constexpr (V >= AddOp<DTC>::kBytes) {                                               \
-      if (offset_bytes == 8)                                                               \
+      if (one && offset_bytes == 8)                                                        \
+        jagged_out1_kernel<V, int64_t, true, DTC><<<g1, 256, 0, s>>>(                      \
+            d, x, o, static_cast<const int64_t*>(offsets[0]), nbags, L0, total_L, vpr);    \
+      else if (one)                                                                        \
+        jagged_out1_kernel<V, int32_t, true, DTC><<<g1, 256, 0, s>>>(                      \
+            d, x, o, static_cast<const int32_t*>(offsets[0]), nbags, L0, total_L, vpr);    \
+      else if (offset_bytes == 8)                                                          \
         jagged_add_kernel<V, int64_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
       else                                                                                 \
         jagged_add_kernel<V, int32_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
