@@ -46,6 +46,41 @@ def test_bounds_check_matches_oracle(dev, mode, dtype, T, B, bad_offsets):
     assert int(warn.item()) == 7 + (exp_n if mode != 3 else 0)
 
 
+@pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
+@pytest.mark.parametrize("T,B,maxlen,long_bags",
+                         [(5, 60000, 8, False), (3, 700, 8, True), (2, 3000, 60, False)])
+def test_bounds_check_large_batch_and_long_bags(dev, dtype, T, B, maxlen, long_bags):
+    """Batches past 2^18 bags (multi-block tiles), mean bag lengths that give
+    blocks of 256, 64 and 32 bags, and bags of thousands of indices (a
+    block's positions span many passes); offsets broken at block and tile
+    boundaries, where the carry from earlier bags decides the repair."""
+    print(f"[case] bounds_check large {dtype} T={T} B={B} maxlen={maxlen} long={long_bags}",
+          flush=True)
+    rng = np.random.default_rng(T * B)
+    rows = rng.integers(50, 5000, T)
+    lengths = rng.integers(0, maxlen, T * B)
+    if long_bags:
+        lengths[rng.integers(0, T * B, 4)] = rng.integers(2000, 6000, 4)
+    off = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    N = int(off[-1])
+    idx = rng.integers(-3, int(rows.max()) + 3, N).astype(np.int64)
+    nb = T * B
+    for p in [64, 255, 256, 257, 1024, 4096, nb // 2, nb - 1]:
+        if p < nb:
+            off[p] = off[p] - rng.integers(1, 40) if rng.random() < 0.5 else -1
+    p = nb // 3
+    off[p] = off[min(p + 300, nb)]  # an overshoot: the next ~300 bags (past a block) repair to it
+    off[nb] = N + 5  # the final offset, owned by the last block
+    exp_idx, exp_off, exp_n = orc.bounds_check_indices(rows, idx, off, 1)
+    gi = torch.from_numpy(idx).to(dev, dtype)
+    go = torch.from_numpy(off).to(dev, dtype)
+    warn = torch.zeros(1, dtype=torch.int64, device=dev)
+    torch.ops.fbgemm.bounds_check_indices(torch.from_numpy(rows).to(dev), gi, go, 1, warn)
+    np.testing.assert_array_equal(go.cpu().numpy().astype(np.int64), exp_off)
+    np.testing.assert_array_equal(gi.cpu().numpy().astype(np.int64), exp_idx)
+    assert int(warn.item()) == exp_n
+
+
 def test_fatal_raises_and_repairs_nothing(dev):
     print("[case] bounds_check FATAL", flush=True)
     rng = np.random.default_rng(3)
