@@ -388,7 +388,39 @@ def bench_backward(args, dev):
         kernel="whole backward (transpose + segment reduce + update)", alg_bytes=alg,
         kernel_ms_mean=mean_ms, kernel_ms_median=med_ms,
     )
-    return res, traffic_from_profile("tbe_bwd_config3"), None
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_backward(args, inp, W, grad)
+    return res, traffic_from_profile("tbe_bwd_config3"), cpu
+
+
+def cpu_baseline_backward(args, inp, W, grad):
+    """The C restatement of the backward (stable merge sort of the linearized
+    keys, per-row sum in sorted order, rowwise Adagrad), one thread, in place
+    on host copies of the weights and gradient."""
+    import numpy as np
+
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as orc
+
+    log("CPU baseline: copying weights and gradient to host")
+    T, E, D = inp.T, inp.E[0], inp.D[0]
+    Wh = W.cpu().numpy()
+    gh = grad.cpu().numpy()
+    m1h = np.zeros(T * E, dtype=np.float32)
+    w_off = (np.arange(T) * E * D).astype(np.int64)
+    m_off = (np.arange(T) * E).astype(np.int64)
+    fn = lambda: orc.backward_rowwise_adagrad(  # noqa: E731
+        Wh, w_off, inp.D_offsets, inp.B, inp.hash_size_cumsum, inp.total_hash_size_bits,
+        inp.indices, inp.offsets, 0, gh, m1h, m_off, 0.01, 1e-8, inplace=True)
+    log("CPU baseline: C restatement of the backward, 1 thread")
+    med, runs = cpu_time(fn, args.cpu_seconds)
+    return dict(
+        value=inp.N / med, unit="lookups/s", cores=1, kind="port",
+        sample=(f"full config-3 batch (N={inp.N} lookups), median of {runs} runs; the oracle's C "
+                f"restatement (stable merge sort + segment sum + rowwise Adagrad), one thread, "
+                f"in place; host CPU: {cpu_model()}"),
+    )
 
 
 def main():

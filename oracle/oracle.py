@@ -253,11 +253,18 @@ def transpose_embedding_input(hsc, B, info_B_num_bits, bits, indices, offsets):
 
 def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,
                              momentum1, m1_off, lr, eps, weight_decay=0.0, weight_decay_mode=0,
-                             info_B_num_bits=26, indice_weights=None):
+                             info_B_num_bits=26, indice_weights=None, inplace=False):
     """Updates copies of W and momentum1; returns (W_new, momentum1_new).
-    ``indice_weights`` (fp32 [N]) makes it the weighted backward."""
-    W = np.array(W, dtype=np.float32, copy=True)
-    m1 = np.array(momentum1, dtype=np.float32, copy=True)
+    ``indice_weights`` (fp32 [N]) makes it the weighted backward.  With
+    ``inplace`` W and momentum1 (contiguous fp32) are updated where they lie
+    (the CPU-baseline timing, which must not copy gigabytes per call)."""
+    if inplace:
+        assert W.dtype == np.float32 and W.flags["C_CONTIGUOUS"]
+        assert momentum1.dtype == np.float32 and momentum1.flags["C_CONTIGUOUS"]
+        m1 = momentum1
+    else:
+        W = np.array(W, dtype=np.float32, copy=True)
+        m1 = np.array(momentum1, dtype=np.float32, copy=True)
     w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
     hsc, m1_off = _c(hsc, np.int64), _c(m1_off, np.int64)
     indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
