@@ -405,12 +405,26 @@ struct ChunkCount {
   }
 };
 
+// Chunk marks (a zeroed array over the chunks): chunk q0 + j of long run r,
+// for j = 0, kMarkEvery, 2 kMarkEvery, ..., holds r + 1, with kRunStart set
+// on the run's first chunk.  The owner of any chunk is the nearest mark at
+// or before it, at most kMarkEvery - 1 chunks back: one round of loads.
+constexpr int kMarkEvery = 16;
+constexpr uint32_t kRunStart = 0x80000000u;
+
 // Epilogue of the chunk-count scan: chunk_start[r] = first chunk of run r
-// (runs of at most kLong occurrences own no chunk).
+// (runs of at most kLong occurrences own no chunk) and the chunk marks.
 struct ChunkEpi {
+  const int32_t* cum;
   uint32_t* chunk_start;
+  uint32_t* chunk_mark;
   uint32_t* total_chunks;
-  __device__ void operator()(int64_t r, uint32_t q0) const { chunk_start[r] = q0; }
+  __device__ void operator()(int64_t r, uint32_t q0) const {
+    chunk_start[r] = q0;
+    const uint32_t nq = ChunkCount{cum}(r);
+    for (uint32_t j = 0; j < nq; j += kMarkEvery)
+      chunk_mark[q0 + j] = (static_cast<uint32_t>(r) + 1u) | (j == 0 ? kRunStart : 0u);
+  }
   __device__ void total(uint32_t t) const { *total_chunks = t; }
 };
 
@@ -431,6 +445,7 @@ struct SortWs {
   unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
   uint32_t* ghist;                 // [kMaxPasses][kRadix]
+  uint32_t* chunk_mark;            // [max_chunks(N)] (backward only)
   unsigned long long* sweep;       // kMaxPasses x sweep_pass_words
   int64_t sweep_words;
   uint32_t* counters;  // [0] num_runs, [1] total chunks
@@ -456,11 +471,14 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   w.sweep_words = sweep_pass_words(n);
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
   const size_t hist_bytes = align256(kMaxPasses * kRadix * 4);
-  uint8_t* z = take(scan_bytes + hist_bytes + kMaxPasses * w.sweep_words * 8);
+  const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
+  uint8_t* z = take(scan_bytes + hist_bytes + mark_bytes + kMaxPasses * w.sweep_words * 8);
   w.zeroed = reinterpret_cast<unsigned long long*>(z);
   w.scan_state = w.zeroed;
   w.ghist = z ? reinterpret_cast<uint32_t*>(z + scan_bytes) : nullptr;
-  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + scan_bytes + hist_bytes) : nullptr;
+  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + scan_bytes + hist_bytes) : nullptr;
+  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + scan_bytes + hist_bytes + mark_bytes)
+              : nullptr;
   w.counters = reinterpret_cast<uint32_t*>(take(64));
   w.bytes = off;
   return w;
@@ -469,7 +487,8 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
 // Words to clear for a sort of `passes` passes (the sweep state of unused
 // passes is left alone).
 int64_t zeroed_words(const SortWs& w, int passes) {
-  return kScanSlots * w.scan_slot_words + align256(kMaxPasses * kRadix * 4) / 8 +
+  return (static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.sweep) -
+                               reinterpret_cast<uint8_t*>(w.zeroed))) / 8 +
          passes * w.sweep_words;
 }
 
@@ -581,7 +600,7 @@ struct BwdArgs {
   const int64_t* row_out;  // VBE: gradient row offset of each bag, or null
   const uint32_t* num_runs;
   const uint32_t* chunk_start;
-  uint32_t* chunk_run;  // written by bwd_chunk_kernel, read by bwd_long_run_kernel
+  const uint32_t* chunk_mark;  // chunk marks (kMarkEvery), from the chunk-count scan
   const uint32_t* total_chunks;
   float* partial;
   int64_t B;
@@ -628,6 +647,18 @@ struct MetaView {
   __device__ int64_t w_off(int64_t t) const { return cached ? m.w_off[t] : a.w_off[t]; }
   __device__ int64_t m1_off(int64_t t) const { return cached ? m.m1_off[t] : a.m1_off[t]; }
   __device__ int32_t D_off(int64_t t) const { return cached ? m.D_off[t] : a.D_off[t]; }
+  // Table of a linearized key: the last t with hsc[t] <= key.
+  __device__ int64_t table_of_key(int64_t key) const {
+    int32_t lo = 0, hi = a.T;
+    while (hi - lo > 1) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (hsc(mid) <= key)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    return lo;
+  }
 };
 
 __device__ __forceinline__ void ld4(const float* p, float (&v)[4]) {
@@ -640,6 +671,25 @@ __device__ __forceinline__ void ld4(const float* p, float (&v)[4]) {
 
 __device__ __forceinline__ void st4(float* p, const float (&v)[4]) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Work items [0, total) in sorted-key order, split into one contiguous range
+// per XCD.  Blocks go to the XCDs round-robin (block i runs on XCD i % 8), so
+// the blocks of one XCD walk one range of keys -- one range of tables -- and
+// read only those tables' gradient columns, which then stay in that XCD's L2
+// (each occurrence re-reads its bag's gradient row).  The grid is a multiple
+// of 8.  A wave starts at `first` and steps by `step` while below `end`.
+struct XcdRange {
+  int64_t first, step, end;
+};
+
+template <int P>
+__device__ __forceinline__ XcdRange xcd_range(int64_t total) {
+  constexpr int64_t kXcd = 8;
+  const int64_t x = blockIdx.x % kXcd, j = blockIdx.x / kXcd, per = gridDim.x / kXcd;
+  const int64_t begin = total * x / kXcd;
+  const int64_t wave = threadIdx.x >> 6;
+  return {begin + (j * 4 + wave) * P, per * 4 * P, total * (x + 1) / kXcd};
 }
 
 __device__ __forceinline__ int64_t table_of(const BwdArgs& a, int32_t info) {
@@ -656,13 +706,16 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
                                       int64_t s0, int64_t s1, int g, int k, int32_t info0,
                                       float (&acc)[NCH][4]) {
   const uint32_t bmask = a.nb >= 32 ? 0xffffffffu : ((1u << a.nb) - 1u);
+  int32_t info_cur = info0;
   for (int64_t base = s0; base < s1; base += G) {
     const int n = static_cast<int>(s1 - base < G ? s1 - base : G);
+    // The next batch's infos load now, ahead of this batch's gradient rows.
+    const int32_t info_next = base + G + k < s1 ? a.infos[base + G + k] : 0;
     int64_t my_row = 0;  // element offset of the occurrence's gradient row slice
     float my_s = 1.0f;   // MEAN: 1/L of the occurrence's bag
     float my_w = 1.0f;   // weighted: the occurrence's per-sample weight
     if (k < n) {
-      const int32_t info = base == s0 ? info0 : a.infos[base + k];
+      const int32_t info = info_cur;
       const int64_t b = static_cast<int64_t>(static_cast<uint32_t>(info) & bmask);
       const int64_t bag = a.B_off ? a.B_off[t] + b : t * a.B + b;
       my_row = a.row_out ? a.row_out[bag] : b * a.total_D + D0;
@@ -704,6 +757,7 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
         }
       }
     }
+    info_cur = info_next;
   }
 }
 
@@ -800,7 +854,7 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
 }
 
 // Pass B (long runs): a block owns the long runs whose first chunk lies in
-// its kLongRange-chunk range (found by one parallel read of chunk_run; a long
+// its kLongRange-chunk range (found by one parallel read of the chunk marks; a long
 // run has at least two chunks, so at most two start in a range) and handles
 // them one after another.  Per run, the 256/G groups sum the run's chunk
 // partials round-robin (group j takes chunks j, j + 256/G, ...), the group
@@ -824,10 +878,10 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
     if (threadIdx.x < 64) {  // wave 0 lists the runs starting in the range, in order
       const int64_t q = q0 + threadIdx.x;
       const bool in = threadIdx.x < kLongRange && q < total;
-      const uint32_t r = in ? a.chunk_run[q] : 0u;
-      const bool start = in && (q == 0 || a.chunk_run[q - 1] != r);
+      const uint32_t m = in ? a.chunk_mark[q] : 0u;
+      const bool start = (m & kRunStart) != 0u;
       const uint64_t bal = __ballot(start);
-      if (start) s_runs[__popcll(bal & ((1ull << threadIdx.x) - 1ull))] = r;
+      if (start) s_runs[__popcll(bal & ((1ull << threadIdx.x) - 1ull))] = (m & ~kRunStart) - 1u;
       if (threadIdx.x == 0) s_nruns = __popcll(bal);
     }
     __syncthreads();
@@ -836,12 +890,23 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
       const uint32_t r = s_runs[ri];
       const int64_t s0 = a.cum[r];
       const int64_t s1 = a.cum[r + 1];
-      const int64_t t = table_of(a, a.infos[s0]);
-      const int32_t D0 = mv.D_off(t);
-      const int32_t D = mv.D_off(t + 1) - D0;
-      (void)D0;
+      const int64_t key = a.run[r];
       const int64_t qf = a.chunk_start[r];  // the run's first chunk
       const int64_t q1 = qf + (s1 - s0 + kChunk - 1) / kChunk;
+      const int64_t t = mv.table_of_key(key);
+      const int32_t D = mv.D_off(t + 1) - mv.D_off(t);
+      const int64_t idx = key - mv.hsc(t);
+      const int64_t row0 = mv.w_off(t) + idx * D;
+      WT* wrow = static_cast<WT*>(a.W) + row0;
+      float* hp = a.m1 + mv.m1_off(t) + idx;
+      float w[NCH][4];
+      float h0 = 0.0f;
+      if (grp == 0) {  // the row and its momentum load while the partials are summed
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          if ((c * G + k) * 4 < D) ld_row4(wrow + (c * G + k) * 4, w[c]);
+        h0 = *hp;
+      }
       float gs[NCH][4];
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
@@ -878,15 +943,7 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
             for (int j = 1; j < NG; ++j) x += part[j][(c * G + k) * 4 + e];
             gs[c][e] = x;
           }
-        const int64_t idx = a.run[r] - mv.hsc(t);
-        const int64_t row0 = mv.w_off(t) + idx * D;
-        WT* wrow = static_cast<WT*>(a.W) + row0;
-        float* hp = a.m1 + mv.m1_off(t) + idx;
-        float w[NCH][4];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          if ((c * G + k) * 4 < D) ld_row4(wrow + (c * G + k) * 4, w[c]);
-        adagrad_update<G, NCH>(a, D, k, gs, w, wrow, row0, hp, *hp);
+        adagrad_update<G, NCH>(a, D, k, gs, w, wrow, row0, hp, h0);
       }
       __syncthreads();
     }
@@ -903,32 +960,18 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
   constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
-  const int64_t total = *a.total_chunks;
-  const int64_t nruns = *a.num_runs;
-  for (int64_t qb = wave * P; qb < total; qb += nwaves * P) {
+  const XcdRange xr = xcd_range<P>(*a.total_chunks);
+  for (int64_t qb = xr.first; qb < xr.end; qb += xr.step) {
     const int64_t q = qb + g;
-    if (q >= total) continue;
-    // Owner of chunk q: the last run whose first chunk is <= q (runs without
-    // chunks share the next long run's start, which is larger).  G-ary
-    // search, one probe per lane and round; invariant
-    // chunk_start[lo] <= q < chunk_start[hi] (hi = nruns: past the end).
-    int64_t lo = 0, hi = nruns;
-    while (hi - lo > 1) {
-      const int64_t stride = (hi - lo + G - 1) / G;
-      const int64_t pos = lo + k * stride;
-      const bool le = pos < hi && (k == 0 || static_cast<int64_t>(a.chunk_start[pos]) <= q);
-      const uint64_t bal = __ballot(le);
-      uint64_t mine = bal;
-      if constexpr (G < 64) mine = (bal >> (g * G)) & ((1ull << G) - 1ull);
-      const int c = __popcll(mine);
-      const int64_t nhi = lo + c * stride;
-      lo += (c - 1) * stride;
-      hi = nhi < hi ? nhi : hi;
-    }
-    const int64_t r = lo;
-    if (k == 0) a.chunk_run[q] = static_cast<uint32_t>(r);  // for bwd_long_run_kernel
+    if (q >= xr.end) continue;
+    // Owner: the nearest chunk mark at or before q (lane k < kMarkEvery reads
+    // chunk q - k; the smallest k with a mark wins).
+    static_assert(G >= kMarkEvery, "a group covers the mark spacing");
+    const uint32_t m = k < kMarkEvery && q - k >= 0 ? a.chunk_mark[q - k] : 0u;
+    uint64_t bal = __ballot(m != 0u);
+    if constexpr (G < 64) bal = (bal >> (g * G)) & ((1ull << G) - 1ull);
+    const int nearest = __ffsll(static_cast<long long>(bal)) - 1;  // always a mark within reach
+    const int64_t r = static_cast<int64_t>((__shfl(m, g * G + nearest, 64) & ~kRunStart) - 1u);
     const int64_t s0 = a.cum[r] + (q - a.chunk_start[r]) * kChunk;
     const int64_t e0 = a.cum[r + 1];
     const int64_t s1 = s0 + kChunk < e0 ? s0 + kChunk : e0;
@@ -961,10 +1004,8 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
   constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * P;
-  const int64_t nruns = *a.num_runs;
-  for (int64_t r = wave * P + g; r < nruns; r += stride) {
+  const XcdRange xr = xcd_range<P>(*a.num_runs);
+  for (int64_t r = xr.first + g; r < xr.end; r += xr.step) {
     const int64_t cs0 = a.cum[r];
     const int64_t cs1 = a.cum[r + 1];
     const int64_t ckey = a.run[r];
@@ -999,7 +1040,8 @@ int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   constexpr int P = 64 / G;
   const int64_t want = ceil_div(N, 4 * P);
   const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
-  const dim3 grid(static_cast<uint32_t>(want < 1 ? 1 : (want > cap ? cap : want)));
+  const int64_t nblk = want < 1 ? 1 : (want > cap ? cap : want);
+  const dim3 grid(static_cast<uint32_t>(ceil_div(nblk, 8) * 8));  // whole rounds over the XCDs
   bwd_chunk_kernel<I, G, NCH, UC><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   const int64_t long_cap = static_cast<int64_t>(num_cus()) * 16;
@@ -1028,7 +1070,6 @@ struct BwdWs {
   int64_t* run;
   int32_t* cum;
   uint32_t* chunk_start;
-  uint32_t* chunk_run;
   float* weights_sorted;
   float* partial;
   size_t bytes;
@@ -1050,7 +1091,6 @@ BwdWs carve_bwd(uint8_t* base, int64_t N, int32_t max_D) {
   w.run = reinterpret_cast<int64_t*>(take(n * 8));
   w.cum = reinterpret_cast<int32_t*>(take((n + 1) * 4));
   w.chunk_start = reinterpret_cast<uint32_t*>(take((n + 1) * 4));
-  w.chunk_run = reinterpret_cast<uint32_t*>(take(static_cast<size_t>(max_chunks(n)) * 4));
   w.weights_sorted = reinterpret_cast<float*>(take(n * 4));
   w.partial = reinterpret_cast<float*>(take(static_cast<size_t>(max_chunks(n)) * max_D * 4));
   w.bytes = off;
@@ -1170,7 +1210,8 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   // Chunk layout of long runs.
   if (int rc = prefix_scan_epi(
           ChunkCount{w.cum}, N, reinterpret_cast<const int32_t*>(&w.sort.counters[0]),
-          ChunkEpi{w.chunk_start, &w.sort.counters[1]}, scan_slot(w.sort, 1),
+          ChunkEpi{w.cum, w.chunk_start, w.sort.chunk_mark, &w.sort.counters[1]},
+          scan_slot(w.sort, 1),
           s))
     return rc;
   BwdArgs a;
@@ -1190,7 +1231,7 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   a.row_out = lay.b_t_map ? lay.row_out : nullptr;
   a.num_runs = &w.sort.counters[0];
   a.chunk_start = w.chunk_start;
-  a.chunk_run = w.chunk_run;
+  a.chunk_mark = w.sort.chunk_mark;
   a.T = T;
   a.total_chunks = &w.sort.counters[1];
   a.partial = w.partial;
