@@ -55,3 +55,42 @@ def nbit_forward_gpu(dev, W: torch.Tensor, w_off, tys, dims, indices, offsets, p
         torch.as_tensor(indices).to(dev, index_dtype), torch.as_tensor(offsets).to(dev, index_dtype),
         pooling, None if indice_weights is None else torch.as_tensor(indice_weights).to(dev),
         1 if out_f16 else 0, None, None, row_align)
+
+
+def build_weights_gpu(dev, tys, dims, rows, seed: int, row_align: int = 16):
+    """build_weights' layout and value ranges, generated on the device (the
+    full-size configs hold gigabytes of rows)."""
+    strides = [orc.nbit_row_bytes(ty, D, row_align) for ty, D in zip(tys, dims)]
+    sizes = [E * s for E, s in zip(rows, strides)]
+    w_off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    W = torch.randint(0, 256, (int(sum(sizes)),), generator=g, device=dev, dtype=torch.uint8)
+    for t, (ty, D, E, s) in enumerate(zip(tys, dims, rows, strides)):
+        tab = W[int(w_off[t]): int(w_off[t]) + E * s].view(E, s)
+        if ty in (orc.INT8, orc.INT4, orc.INT2):
+            sc = (torch.rand(E, generator=g, device=dev) * 9e-3 + 1e-3).half()
+            bi = (torch.rand(E, generator=g, device=dev) * 0.2 - 0.1).half()
+            tab[:, 0:2] = sc.view(torch.uint8).view(-1, 2)
+            tab[:, 2:4] = bi.view(torch.uint8).view(-1, 2)
+        elif ty == orc.FP16:
+            v = (torch.rand((E, D), generator=g, device=dev) * 0.02 - 0.01).half()
+            tab[:, : 2 * D] = v.view(torch.uint8).view(E, -1)
+        else:
+            v = torch.rand((E, D), generator=g, device=dev) * 0.02 - 0.01
+            tab[:, : 4 * D] = v.view(torch.uint8).view(E, -1)
+    return W, w_off
+
+
+def sample_bags(indices, offsets, T: int, B: int, bs):
+    """Sub-batch of the bags (t, b) for b in `bs` (every table): (indices,
+    offsets) of a batch of len(bs) bags per table, in the same t-major order."""
+    parts, lens = [], []
+    for t in range(T):
+        for b in bs:
+            s, e = int(offsets[t * B + b]), int(offsets[t * B + b + 1])
+            parts.append(indices[s:e])
+            lens.append(e - s)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    idx = np.concatenate(parts).astype(np.int64) if parts else np.zeros(0, np.int64)
+    return idx, off

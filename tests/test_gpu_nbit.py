@@ -12,7 +12,7 @@ import torch
 
 import oracle as orc
 from mx_fbgemm import bench_inputs
-from nbit_helpers import build_weights, nbit_forward_gpu
+from nbit_helpers import build_weights, build_weights_gpu, nbit_forward_gpu, sample_bags
 from tbe_helpers import random_tbe
 
 pytestmark = pytest.mark.gpu
@@ -65,8 +65,8 @@ def test_mixed_types_weighted_fp32_out(dev):
 
 def test_config4_reduced_batch(dev):
     """Config 4 tables (16 INT8 + 16 INT4, E=1e6, D=128, MEAN, fp16 out) with
-    the batch cut to B=1024 so the oracle stays quick; the full-size run is
-    checked against the same oracle on a sample of bags in the bench tests."""
+    the batch cut to B=1024 so the oracle checks every bag; the full-size
+    batch is checked on a sample of bags below."""
     print("[case] config4 B=1024", flush=True)
     cfg = bench_inputs.config4(B=1024)
     rng = np.random.default_rng(44)
@@ -93,3 +93,30 @@ def test_config5_reduced_batch(dev):
     for t in range(cfg.T):
         d0, d1 = int(cfg.D_offsets[t]), int(cfg.D_offsets[t + 1])
         assert np.all(g[empty[t], d0:d1] == 0.0)
+
+
+@pytest.mark.parametrize("config", [4, 5])
+def test_full_size_sampled_bags(dev, config):
+    """Configs 4 and 5 at full size (the bench's tables, batch and indices):
+    the lookup runs over the whole batch, then 256 sampled bag columns of
+    every table are checked against the oracle; config 5's empty bags are
+    all zero in the full output."""
+    print(f"[case] config{config} full size, sampled bags", flush=True)
+    cfg = bench_inputs.config4() if config == 4 else bench_inputs.config5()
+    pooling = 1 if config == 4 else 0
+    W, w_off = build_weights_gpu(dev, cfg.tys, cfg.D, cfg.E, seed=config)
+    got = nbit_forward_gpu(dev, W, w_off, cfg.tys, cfg.D, cfg.indices, cfg.offsets, pooling,
+                           index_dtype=torch.int32)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(400 + config)
+    bs = np.sort(rng.choice(cfg.B, size=256, replace=False))
+    sidx, soff = sample_bags(cfg.indices, cfg.offsets, cfg.T, cfg.B, bs)
+    buf = W.cpu().numpy()
+    exp = orc.nbit_forward(buf, w_off, cfg.tys, cfg.D_offsets, len(bs), sidx, soff, pooling)
+    _check(got[torch.from_numpy(bs).to(dev)], exp)
+    if config == 5:
+        empty = (np.diff(cfg.offsets) == 0).reshape(cfg.T, cfg.B)
+        g = got.float().cpu().numpy()
+        for t in range(cfg.T):
+            d0, d1 = int(cfg.D_offsets[t]), int(cfg.D_offsets[t + 1])
+            assert np.all(g[empty[t], d0:d1] == 0.0)
