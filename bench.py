@@ -8,13 +8,15 @@ weights are generated on the device).  One step = one
 torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda call over
 the batch, inputs resident in HBM.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config {2,3,4,5}]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config {1,2,3,4,5}]
+                    [--op {lookup,bounds-check}]
 
 Prints one JSON line: lookups/s (whole job), the roofline of the dominant
 kernel (algorithmic bytes per launch / HIP-event-timed launch duration vs
 8 TB/s) and the CPU baseline (FBGEMM's CPU kernel on this host's cores).
---config 3/4/5 print the same line for the backward, the nbit lookup and the
-mixed nbit workload.
+--config 1/3/4/5 print the same line for the jagged round trip, the backward,
+the nbit lookup and the mixed nbit workload; --op bounds-check times
+bounds_check_indices over the config-2 batch.
 """
 
 from __future__ import annotations
@@ -45,6 +47,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="workload; 2 (default) is the headline")
+    ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check"],
+                    help="config 2 only: time bounds_check_indices (WARNING) on the batch "
+                         "instead of the lookup")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -222,6 +227,52 @@ def bench_tbe_forward(args, dev):
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_tbe(args, inp, W)
     return res, traffic, cpu
+
+
+def bench_bounds_check(args, dev):
+    """bounds_check_indices (WARNING) over the config-2 batch: every offset and
+    index is read and checked; the batch is valid, so nothing is rewritten."""
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 2 batch")
+    inp = bench_inputs.config2()
+    rows = torch.tensor(inp.E, dtype=torch.int64, device=dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    warn = torch.zeros(1, dtype=torch.int64, device=dev)
+    op = torch.ops.fbgemm.bounds_check_indices
+
+    def step():
+        op(rows, idx, off, 1, warn)
+
+    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    assert int(warn.item()) == 0, "the config-2 batch is valid"
+    alg = inp.N * 8 + (inp.T * inp.B + 1) * 8
+    res = dict(
+        metric="bounds_check_indices lookups/sec, 1 MI355X", value=inp.N * args.steps / wall,
+        unit="lookups/s", ms_per_step=wall / args.steps * 1e3, dtype="int64",
+        config={"workload": "config2 batch: bounds_check_indices, WARNING mode", "T": inp.T,
+                "B": inp.B, "N": inp.N},
+        kernel="tile_max_kernel + bounds_main_kernel", alg_bytes=alg, kernel_ms_mean=mean_ms,
+        kernel_ms_median=med_ms,
+    )
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        rows_h = np.asarray(inp.E, dtype=np.int64)
+        fn = lambda: orc.bounds_check_indices(rows_h, inp.indices, inp.offsets, 1)  # noqa: E731
+        log("CPU baseline: C restatement of the bounds check, 1 thread")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        cpu = dict(value=inp.N / med, unit="lookups/s", cores=1, kind="port",
+                   sample=(f"full config-2 batch (N={inp.N}), median of {runs} runs; the "
+                           f"oracle's C restatement, one thread, including its copies of "
+                           f"indices and offsets; host CPU: {cpu_model()}"))
+    return res, traffic_from_profile("bounds_check_config2"), cpu
 
 
 def cpu_baseline_tbe(args, inp, W):
@@ -449,6 +500,8 @@ def main():
         return
     if args.config == 1:
         res, traffic, cpu = bench_jagged(args, dev)
+    elif args.config == 2 and args.op == "bounds-check":
+        res, traffic, cpu = bench_bounds_check(args, dev)
     elif args.config == 2:
         res, traffic, cpu = bench_tbe_forward(args, dev)
     elif args.config == 3:
