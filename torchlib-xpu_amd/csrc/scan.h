@@ -81,18 +81,9 @@ constexpr unsigned long long kScanFlagAgg = 1ull << 62;
 constexpr unsigned long long kScanFlagIncl = 2ull << 62;
 constexpr int kScanSpinLimit = 1 << 22;
 
-// Default epilogue: out[i] = scanned value; *total_out = whole aggregate.
-struct StoreOut {
-  uint32_t* out;
-  uint32_t* total_out;
-  __device__ void operator()(int64_t i, uint32_t v) const { out[i] = v; }
-  __device__ void total(uint32_t t) const {
-    if (total_out) *total_out = t;
-  }
-};
-
 // INCL = false: epi(i, op(f(0..i-1))) (identity at 0); true: epi(i, op(f(0..i))).
-// epi.total(aggregate) runs once, in the last tile.
+// epi.total(aggregate) runs once, in the last tile.  An epilogue is a
+// functor with operator()(int64_t i, uint32_t scanned) and total(uint32_t).
 template <class F, class Op, bool INCL, class Epi>
 __global__ void __launch_bounds__(kScanThreads)
     scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
@@ -176,9 +167,9 @@ __global__ void __launch_bounds__(kScanThreads)
   }
 }
 
-// Prefix scan of f over [0, effective length); *total = the whole aggregate.
+// Prefix scan of f over [0, effective length), results handed to `epi`.
 // `st` must have scan_tiles(n) zeroed status words and a zeroed ticket.
-template <class F, class Op = SumOp, bool INCL = false, class Epi = StoreOut>
+template <class F, class Op = SumOp, bool INCL = false, class Epi>
 int prefix_scan_epi(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
                     hipStream_t s) {
   const int64_t nt = scan_tiles(n);
@@ -187,19 +178,6 @@ int prefix_scan_epi(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
       f, n, n_dev, epi, st, nt);
   MX_LAUNCH_CHECK();
   return MX_OK;
-}
-
-template <class F, class Op = SumOp, bool INCL = false>
-int prefix_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
-                ScanState st, hipStream_t s) {
-  return prefix_scan_epi<F, Op, INCL, StoreOut>(f, n, n_dev, StoreOut{out, total}, st, s);
-}
-
-// out[i] = sum_{j<i} f(j); *total = sum of all.
-template <class F>
-int exclusive_scan(F f, int64_t n, const int32_t* n_dev, uint32_t* out, uint32_t* total,
-                   ScanState st, hipStream_t s) {
-  return prefix_scan<F, SumOp, false>(f, n, n_dev, out, total, st, s);
 }
 
 // Fills p[0..n) with zeros (a kernel, not a memset, so callers can capture it).

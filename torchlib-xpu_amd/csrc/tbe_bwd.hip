@@ -1211,8 +1211,7 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   if (int rc = prefix_scan_epi(
           ChunkCount{w.cum}, N, reinterpret_cast<const int32_t*>(&w.sort.counters[0]),
           ChunkEpi{w.cum, w.chunk_start, w.sort.chunk_mark, &w.sort.counters[1]},
-          scan_slot(w.sort, 1),
-          s))
+          scan_slot(w.sort, 1), s))
     return rc;
   BwdArgs a;
   a.W = weights;
