@@ -281,11 +281,15 @@ def test_module_training_step_weighted(dev, pooling):
 
 # ---- fp16 weights: round-to-nearest-even or stochastic rounding -------------
 
-def _f16_bracket(u: np.ndarray, rel: float = 2e-6):
-    """fp16 values bracketing fp32 ``u`` widened by ``rel`` (the GPU's fp32
-    update may differ from the oracle's in its last bits): (lower, upper)."""
-    a = u - np.abs(u) * rel
-    b = u + np.abs(u) * rel
+def _f16_bracket(u: np.ndarray, w_old: np.ndarray, rel: float = 2e-6):
+    """fp16 values bracketing fp32 ``u`` = w_old - m*g, widened by ``rel``
+    times the operands' magnitude |w_old| + |u| (the GPU's fp32 update may
+    differ from the oracle's in the last bits of m*g -- its sum of squares is
+    reduced in another order -- which matters most when u nearly cancels):
+    (lower, upper)."""
+    widen = (np.abs(u) + np.abs(w_old.astype(np.float32))) * rel
+    a = u - widen
+    b = u + widen
     la = a.astype(np.float16)
     la = np.where(la.astype(np.float32) > a, np.nextafter(la, np.float16(-np.inf)), la)
     hb = b.astype(np.float16)
@@ -325,7 +329,7 @@ def _fp16_update(dev, inp, sr, seed=0, lr=0.05, eps=1e-6, pooling=0, weighted=Fa
     got = Wd.cpu().numpy()
     untouched = u == W16.astype(np.float32)
     assert np.array_equal(got[untouched].view(np.uint16), W16[untouched].view(np.uint16))
-    lo, hi = _f16_bracket(u)
+    lo, hi = _f16_bracket(u, W16)
     gf = got.astype(np.float32)
     out = (gf < lo.astype(np.float32)) | (gf > hi.astype(np.float32))
     assert not out.any(), f"{out.sum()} fp16 results outside the bracket of the fp32 update"
@@ -429,5 +433,5 @@ def test_module_training_step_fp16(dev, sr):
         indice_weights=iw)
     np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)
     got = tbe.weights_dev.detach().cpu().numpy().astype(np.float32)
-    lo, hi = _f16_bracket(u)
+    lo, hi = _f16_bracket(u, W0)
     assert np.all((got >= lo.astype(np.float32)) & (got <= hi.astype(np.float32)))

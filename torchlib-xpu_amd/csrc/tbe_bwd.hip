@@ -1046,7 +1046,11 @@ int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   MX_LAUNCH_CHECK();
   const int64_t long_cap = static_cast<int64_t>(num_cus()) * 16;
   const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
-  bwd_long_run_kernel<WT, G, NCH, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
+  // Long runs: twice the lanes per row where the row allows (more groups
+  // summing partials per block; measured 15.1 -> 12.4 us on config 3).
+  constexpr int GL = NCH >= 2 && G < 64 ? 2 * G : G;
+  constexpr int NCHL = GL == 2 * G ? NCH / 2 : NCH;
+  bwd_long_run_kernel<WT, GL, NCHL, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   bwd_update_kernel<I, WT, G, NCH, U><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
