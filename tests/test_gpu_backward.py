@@ -156,6 +156,21 @@ def test_grad_indice_weights(dev, pooling, dims):
                 assert not got[o[0]:o[1]].any()
 
 
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_backward_many_tables(dev, pooling):
+    """700 tables (past the 512 whose metadata the kernels stage in LDS; the
+    info word then needs 10 table bits), mixed D, some rows hit by long runs:
+    transpose bit-exact, update within rtol 1e-5."""
+    print(f"[case] backward 700 tables pool={pooling}", flush=True)
+    rng = np.random.default_rng(7000 + pooling)
+    T, B = 700, 40
+    dims = [int(d) for d in rng.choice([4, 32, 64, 128], T)]
+    rows = [int(r) for r in rng.integers(1, 40, T)]
+    inp = random_tbe(rng, T, B, dims, rows, 6)
+    _check_transpose(dev, inp)
+    _backward_case(dev, inp, pooling, seed=pooling)
+
+
 @pytest.mark.parametrize("wd_mode,wd", [(1, 0.1), (2, 0.05)])
 def test_backward_weight_decay(dev, wd_mode, wd):
     print(f"[case] backward weight decay mode {wd_mode}", flush=True)

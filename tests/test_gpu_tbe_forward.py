@@ -101,6 +101,22 @@ def test_duplicate_heavy_and_repeatable(dev):
                                   inp.offsets, 0))
 
 
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_many_tables(dev, pooling):
+    """700 tables (past the 512 whose metadata the kernels stage in LDS), mixed
+    D and row counts, bit-exact."""
+    print(f"[case] tbe fwd 700 tables pool={pooling}", flush=True)
+    rng = np.random.default_rng(700 + pooling)
+    T, B = 700, 6
+    dims = [int(d) for d in rng.choice([4, 8, 16, 64, 128], T)]
+    rows = [int(r) for r in rng.integers(1, 60, T)]
+    inp = random_tbe(rng, T, B, dims, rows, 5)
+    W = rng.uniform(-1, 1, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    exp = orc.tbe_forward_f32(W, weight_offsets(inp), inp.D_offsets, B, inp.indices, inp.offsets,
+                              pooling)
+    _exact(tbe_forward_gpu(dev, torch.from_numpy(W).to(dev), inp, pooling), exp)
+
+
 def test_config2_full(dev):
     """Config 2 at full size (8 x 1M x 128 fp32, B=4096, Zipf 1.05): every bag
     bit-exact against the oracle."""
