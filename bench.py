@@ -68,24 +68,27 @@ def traffic_from_profile(name: str):
 
 
 def time_launches(fn, steps: int, warmup: int):
-    """Returns (wall seconds for `steps` calls, mean per-launch ms from events)."""
+    """Runs `warmup` untimed steps, then times exactly `steps` steps back to
+    back, synchronised on both sides.  Returns (wall seconds, mean step
+    duration in ms from one pair of HIP events recorded around the steps on
+    the current stream -- the stream the ops launch on).  No event sits
+    between steps: an event record between launches costs ~7 us of GPU time
+    per step here, which is not part of the op."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
+    start.record()
+    for _ in range(steps):
         fn()
-        ends[i].record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return wall, statistics.mean(per), statistics.median(per)
+    return wall, start.elapsed_time(end) / steps
 
 
 def cpu_time(fn, budget_s: float, min_runs: int = 3, warm: int = 1):
@@ -133,7 +136,7 @@ def bench_jagged(args, dev):
         dense = j2pd(v, [off], [L], 0.0)
         return d2j(dense, [off], total)
 
-    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     # j2pd reads the values and writes the padded dense; d2j reads the dense at
     # the jagged positions and writes the values; both read the offsets.
     alg = total * D * 4 + B * L * D * 4 + 2 * total * D * 4 + 2 * (B + 1) * 8
@@ -143,8 +146,7 @@ def bench_jagged(args, dev):
         dtype="fp32",
         config={"workload": "config1: jagged round trip, B=512 D=128 max_L=64, len~U{0..64}",
                 "B": B, "D": D, "max_L": L, "total_L": total},
-        kernel="j2pd_kernel + d2j_kernel (one step)", alg_bytes=alg, kernel_ms_mean=mean_ms,
-        kernel_ms_median=med_ms)
+        kernel="j2pd_kernel + d2j_kernel (one step)", alg_bytes=alg, kernel_ms_mean=mean_ms)
     cpu = None
     if not args.no_cpu_baseline:
         vc, oc = v.cpu(), off.cpu()
@@ -189,7 +191,7 @@ def bench_tbe_forward(args, dev):
                   False)
 
     log(f"timing N={inp.N} lookups, {args.steps} steps")
-    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     N = inp.N
     alg_bytes = N * (D * 4 + 8) + T * B * (8 + D * 4)
 
@@ -215,10 +217,9 @@ def bench_tbe_forward(args, dev):
         config={"workload": "config2: TBE fp32 forward SUM, T=8 E=1e6 D=128 B=4096 "
                             "L~U{1..40} Zipf(1.05) int64 indices",
                 "T": T, "E": E, "D": D, "B": B, "N": N, "indices": "int64"},
-        kernel="tbe_fwd_kernel",
+        kernel="tbe_fwd_group_kernel",
         alg_bytes=alg_bytes,
         kernel_ms_mean=mean_ms,
-        kernel_ms_median=med_ms,
         cold_kernel_ms_median=statistics.median(cold),
     )
     traffic = traffic_from_profile("tbe_fwd_config2")
@@ -248,7 +249,7 @@ def bench_bounds_check(args, dev):
     def step():
         op(rows, idx, off, 1, warn)
 
-    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     assert int(warn.item()) == 0, "the config-2 batch is valid"
     alg = inp.N * 8 + (inp.T * inp.B + 1) * 8
     res = dict(
@@ -257,7 +258,6 @@ def bench_bounds_check(args, dev):
         config={"workload": "config2 batch: bounds_check_indices, WARNING mode", "T": inp.T,
                 "B": inp.B, "N": inp.N},
         kernel="tile_max_kernel + bounds_main_kernel", alg_bytes=alg, kernel_ms_mean=mean_ms,
-        kernel_ms_median=med_ms,
     )
     cpu = None
     if not args.no_cpu_baseline:
@@ -346,7 +346,7 @@ def bench_nbit(args, dev, config: int):
     def step():
         return op(*args_)
 
-    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     N = inp.N
     unpadded = [strides_u for strides_u in
                 [(D + 4) if ty == SparseType.INT8 else (D // 2 + 4) if ty == SparseType.INT4
@@ -364,7 +364,6 @@ def bench_nbit(args, dev, config: int):
             if config == 4 else "mixed nbit SUM fp16 out, 64 tables FP16/INT4 D 32..256 "
             "B=65536 L~Poisson(15) 10% empty Zipf(1.1)")), "T": inp.T, "B": inp.B, "N": N},
         kernel="nbit_fwd_kernel", alg_bytes=alg_bytes, kernel_ms_mean=mean_ms,
-        kernel_ms_median=med_ms,
     )
     cpu = None
     if not args.no_cpu_baseline:
@@ -426,7 +425,7 @@ def bench_backward(args, dev):
         op(grad, W, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits, idx, off, 0,
            e32, 0, 0, False, m1, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
 
-    wall, mean_ms, med_ms = time_launches(step, args.steps, args.warmup)
+    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
                       + inp.indices).size)
     alg = inp.N * 8 + (T * B + 1) * 8 + B * inp.total_D * 4 + U * (2 * D * 4 + 2 * 4)
@@ -437,7 +436,7 @@ def bench_backward(args, dev):
         config={"workload": "config3: TBE backward + exact rowwise Adagrad on config-2 shapes",
                 "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
         kernel="whole backward (transpose + segment reduce + update)", alg_bytes=alg,
-        kernel_ms_mean=mean_ms, kernel_ms_median=med_ms,
+        kernel_ms_mean=mean_ms,
     )
     cpu = None
     if not args.no_cpu_baseline:
@@ -517,8 +516,7 @@ def main():
         roofline=dict(bound="hbm", achieved=achieved, peak=PEAK_HBM_GBS, unit="GB/s",
                       frac=achieved / PEAK_HBM_GBS, traffic=traffic,
                       kernel=res["kernel"], alg_bytes_per_launch=res["alg_bytes"],
-                      launch_ms_mean=res["kernel_ms_mean"],
-                      launch_ms_median=res["kernel_ms_median"]),
+                      launch_ms_mean=res["kernel_ms_mean"]),
         cpu_baseline=cpu,
     )
     if "cold_kernel_ms_median" in res:
