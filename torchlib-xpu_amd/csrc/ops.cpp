@@ -859,6 +859,7 @@ Tensor grad_indice_weights_impl(const Tensor& grad_output, const Tensor& dev_wei
   }
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
   Tensor out = at::empty({indices.numel()}, dev_weights.options().dtype(at::kFloat));
+  if (indices.numel() == 0) return out;  // one entry per index: nothing to compute
   if (vbe.on()) {
     const int64_t total_B = offsets.numel() - 1;
     check_vbe(vbe, total_B);
