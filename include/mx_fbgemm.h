@@ -339,6 +339,8 @@ int64_t mx_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_alignment);
  *                   whose max is 0 is not launched
  *   INT8/INT4/INT2 rows begin with fp16 scale then fp16 bias; INT4 holds
  *   the even element in the low nibble.  value = scale*q + bias (fp32).
+ *   Codes fill whole bytes: every INT4 table's D is even and every INT2
+ *   table's D a multiple of 4 (checked on the maxima; EINVAL otherwise).
  *   output_dtype    MX_SPARSE_FP32 or MX_SPARSE_FP16 (round to nearest even)
  *   out             [B, total_D] */
 int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,

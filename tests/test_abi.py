@@ -108,6 +108,12 @@ def test_bad_arguments_rejected_before_any_launch(lib):
     assert g(None, None, None, None, 1, 1, 0, 0, 2048, 0, 0, None, None, 4, 0, None, 1, 16, None,
              2048, None) == -1  # max D above 1024
     assert b"1024" in lib.mx_last_error()
+    assert g(None, None, None, None, 1, 1, 0, 29, 0, 0, 0, None, None, 4, 0, None, 1, 16, None,
+             29, None) == -1  # odd INT4 D: codes would not fill whole bytes
+    assert b"INT4 D must be even" in lib.mx_last_error()
+    assert g(None, None, None, None, 1, 1, 6, 0, 0, 0, 0, None, None, 4, 0, None, 1, 16, None,
+             6, None) == -1  # INT2 D not a multiple of 4
+    assert b"INT2 D a multiple of 4" in lib.mx_last_error()
     h = lib.mx_tbe_backward_rowwise_adagrad
     h.restype = ctypes.c_int
     h.argtypes = [P, i32, P, P, i32, i64, i32, P, i32, P, P, i32, i64, i32, P, P, i64, P, P,

@@ -419,6 +419,10 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
     if (d > max_D) max_D = d;
   }
   MX_REQUIRE(max_D <= 1024, "max D %d above 1024", max_D);
+  // Codes fill whole bytes of a row (its size is D*bits/8 + 4 rounded down).
+  MX_REQUIRE(max_int4_D % 2 == 0 && max_int2_D % 4 == 0,
+             "INT4 D must be even and INT2 D a multiple of 4 (max_int4_D %d, max_int2_D %d)",
+             max_int4_D, max_int2_D);
   if (static_cast<int64_t>(T) * B == 0 || total_D == 0) return MX_OK;
   MX_REQUIRE(dev_weights && weights_offsets && weights_tys && D_offsets && offsets && out,
              "null pointer argument");
