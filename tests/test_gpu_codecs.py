@@ -35,14 +35,21 @@ def test_fused8bit_round_trip_bits(dev, D):
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
-@pytest.mark.parametrize("D", [8, 16, 36, 128, 256])
+@pytest.mark.parametrize("D", [7, 8, 13, 16, 36, 128, 256])
 def test_fused_nbit_round_trip_bits(dev, bits, D):
+    """D not a multiple of the codes per byte (7, 13): the last byte is
+    partly padding and the dequantized rows come back padded to whole bytes,
+    as FBGEMM's fused N-bit format has it (torch's CPU prepack refuses such D,
+    so there they are checked against the oracle only)."""
     print(f"[case] fused nbit bits={bits} D={D}", flush=True)
     x = _rows(np.random.default_rng(D * bits), 300, D)
     q = torch.ops.fbgemm.FloatToFusedNBitRowwiseQuantizedSBHalf(torch.from_numpy(x).to(dev), bits)
     np.testing.assert_array_equal(q.cpu().numpy(), orc.quantize_fused_nbit(x, bits))
     d = torch.ops.fbgemm.FusedNBitRowwiseQuantizedSBHalfToFloat(q, bits)
-    np.testing.assert_array_equal(d.cpu().numpy(), orc.dequantize_fused_nbit(q.cpu().numpy(), bits, D))
+    d_out = (q.shape[1] - 4) * (8 // bits)
+    assert d.shape[1] == d_out >= D
+    np.testing.assert_array_equal(d.cpu().numpy(),
+                                  orc.dequantize_fused_nbit(q.cpu().numpy(), bits, d_out))
     xh = torch.from_numpy(x).half()
     qh = torch.ops.fbgemm.HalfToFusedNBitRowwiseQuantizedSBHalf(xh.to(dev), bits)
     np.testing.assert_array_equal(qh.cpu().numpy(), orc.quantize_fused_nbit(xh.float().numpy(), bits))
