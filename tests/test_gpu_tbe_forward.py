@@ -137,3 +137,26 @@ def test_config2_full(dev):
     lin = counts.astype(np.float64) @ t0
     np.testing.assert_allclose(got[:, :128].double().sum(0).cpu().numpy(), lin, rtol=1e-4,
                                atol=1e-4)
+
+
+def test_unserved_arguments_raise(dev):
+    """UVM storage and a populated LXU cache are refused, not ignored."""
+    print("[case] tbe fwd unserved arguments", flush=True)
+    rng = np.random.default_rng(3)
+    inp = random_tbe(rng, 2, 4, [8, 8], [5, 5], 3)
+    W = torch.zeros(80, device=dev)
+    w_off = torch.from_numpy(weight_offsets(inp)).to(dev)
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(2, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda
+    with pytest.raises(RuntimeError, match="UVM"):
+        op(W, torch.zeros(4, device=dev), empty, pl, w_off, D_off, 16, 8, idx, off, 0, e32, empty,
+           0, False)
+    with pytest.raises(RuntimeError, match="LXU cache"):
+        op(W, empty, torch.zeros(3, 8, device=dev), pl, w_off, D_off, 16, 8, idx, off, 0, e32,
+           empty, 0, False)
+    op(W, empty, empty, pl, w_off, D_off, 16, 8, idx, off, 0, e32, empty, 0, False)

@@ -306,16 +306,12 @@ std::tuple<Tensor, std::vector<Tensor>> jagged_dense_add_plain(
 // TBE training
 // ---------------------------------------------------------------------------
 
-constexpr int64_t kPlacementDevice = 0;
-
-void check_device_placement(const Tensor& placements, const Tensor& uvm, const char* what) {
-  // DEVICE-only build: UVM / managed caching placements are not served.
-  TORCH_CHECK(uvm.numel() == 0, what, ": UVM storage is not supported (DEVICE placement only)");
-  if (placements.defined() && placements.numel() > 0) {
-    const Tensor pc = placements.to(at::kCPU, /*non_blocking=*/false);
-    TORCH_CHECK((pc == kPlacementDevice).all().item<bool>(), what,
-                ": every table must use EmbeddingLocation.DEVICE");
-  }
+// DEVICE-only build: a populated LXU cache is refused (the per-table
+// placements are validated by the modules; reading them here would need a
+// device-to-host copy on every call).
+void check_no_cache(const Tensor& lxu_cache_weights) {
+  TORCH_CHECK(!lxu_cache_weights.defined() || lxu_cache_weights.numel() == 0,
+              "the LXU cache is not supported (DEVICE placement only)");
 }
 
 // Variable-batch-per-feature (VBE) metadata of one lookup; undefined tensors
@@ -424,7 +420,7 @@ Tensor forward_unweighted(const Tensor& dev_weights, const Tensor& uvm_weights,
                           const Tensor& offsets, int64_t pooling_mode,
                           const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
                           int64_t output_dtype, bool is_experimental) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)lxu_cache_locations;
   (void)uvm_cache_stats;
   (void)is_experimental;
@@ -440,7 +436,7 @@ Tensor forward_weighted(const Tensor& dev_weights, const Tensor& uvm_weights,
                         const Tensor& offsets, int64_t pooling_mode, const Tensor& indice_weights,
                         const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
                         int64_t output_dtype, bool is_experimental) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)lxu_cache_locations;
   (void)uvm_cache_stats;
   (void)is_experimental;
@@ -511,7 +507,7 @@ Tensor forward_unweighted_vbe(const Tensor& dev_weights, const Tensor& uvm_weigh
                               const Tensor& vbe_b_t_map, c10::SymInt vbe_output_size,
                               int64_t info_B_num_bits, int64_t info_B_mask,
                               bool is_experimental) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)lxu_cache_locations;
   (void)uvm_cache_stats;
   (void)info_B_mask;
@@ -533,7 +529,7 @@ Tensor forward_weighted_vbe(const Tensor& dev_weights, const Tensor& uvm_weights
                             const Tensor& vbe_row_output_offsets, const Tensor& vbe_b_t_map,
                             c10::SymInt vbe_output_size, int64_t info_B_num_bits,
                             int64_t info_B_mask, bool is_experimental) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)lxu_cache_locations;
   (void)uvm_cache_stats;
   (void)info_B_mask;
@@ -620,7 +616,7 @@ Tensor backward_rowwise_adagrad_impl(
     const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
     const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
     int64_t weight_decay_mode, double max_norm, const VbeMeta& vbe = VbeMeta()) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)weights_placements;
   (void)lxu_cache_locations;
   (void)BT_block_size;
@@ -826,7 +822,7 @@ Tensor grad_indice_weights_impl(const Tensor& grad_output, const Tensor& dev_wei
                                 const Tensor& lxu_cache_locations,
                                 const std::optional<Tensor>& feature_requires_grad,
                                 int64_t pooling_mode, const VbeMeta& vbe) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)weights_placements;
   (void)lxu_cache_locations;
   check_gpu(dev_weights, "dev_weights");
@@ -1040,7 +1036,7 @@ Tensor lookup_rowwise_adagrad(
     const std::optional<Tensor>& vbe_output_offsets_feature_rank,
     const std::optional<Tensor>& vbe_B_offsets_rank_per_feature, c10::SymInt max_B,
     c10::SymInt max_B_feature_rank, c10::SymInt vbe_output_size) {
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights);
   (void)lxu_cache_locations;
   TORCH_CHECK(!gradient_clipping || max_gradient <= 0.0, "gradient clipping is not supported");
   // Variable batch per feature: the per-bag metadata is built once here.
@@ -1260,7 +1256,7 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
                        std::optional<int64_t> fp8_exponent_bits,
                        std::optional<int64_t> fp8_exponent_bias) {
   (void)weights_placements;
-  (void)lxu_cache_weights;
+  check_no_cache(lxu_cache_weights.value_or(Tensor()));
   (void)lxu_cache_locations;
   (void)fp8_exponent_bits;
   (void)fp8_exponent_bias;
