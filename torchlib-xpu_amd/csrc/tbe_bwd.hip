@@ -43,7 +43,7 @@ constexpr int kMaxPasses = 4;
 constexpr int kSweepItems = 8;                        // keys per lane per pass
 constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;  // 512 keys per wave
 constexpr int64_t kSweepTile = 4 * kSweepWaveKeys;    // 2048 keys per block
-constexpr int kLinItems = 16;
+constexpr int kLinItems = 8;
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
 constexpr int kLong = 32;                             // runs longer than this are chunked
 constexpr int kChunk = 32;                            // occurrences per chunk
