@@ -12,7 +12,7 @@
 // Design:
 //  * Keys fit 32 bits whenever total_hash_size_bits <= 32, so the sort moves
 //    (u32 key, u32 info) pairs: ceil(bits/8) LSD passes of 8-bit digits.
-//  * linearize: a block takes 4096 consecutive positions, finds the bag range
+//  * linearize: a block takes 2048 consecutive positions, finds the bag range
 //    they span with two cooperative 128-ary searches, lets every non-empty
 //    bag mark its first position in LDS and gives each position the latest
 //    mark (a max-scan), so no per-position search.  The same kernel
@@ -29,7 +29,9 @@
 //    owning columns, occurrences added in sorted order.  Runs longer than
 //    kLong are cut into kChunk-occurrence chunks reduced in parallel into a
 //    workspace, then summed in chunk order.  No atomics on data: results are
-//    deterministic.
+//    deterministic.  Runs and chunks are split into one contiguous key range
+//    per XCD, so an XCD re-reads only its tables' gradient columns, from its
+//    own L2.
 #include "mx_common.h"
 #include "scan.h"
 
