@@ -329,9 +329,12 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
   }
   const uint32_t bmask = nb >= 32 ? 0xffffffffu : ((1u << nb) - 1u);
   for (int64_t r = 0; r < nruns; ++r) {
+    /* The row: from the run's first occurrence (features that share a table
+     * share its rows, hash offset and width).  Each occurrence's gradient
+     * slice and bag length: from its own feature tj. */
     const uint32_t info0 = (uint32_t)infos[cum[r]];
     const int64_t t = nb >= 32 ? 0 : (int64_t)(info0 >> nb);
-    const int32_t D0 = D_off[t], D = D_off[t + 1] - D_off[t];
+    const int32_t D = D_off[t + 1] - D_off[t];
     if (D > 1024) {
       rc = -1;
       goto done;
@@ -339,9 +342,14 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
     const int64_t idx = run[r] - hsc[t];
     for (int32_t d = 0; d < D; ++d) g[d] = 0.0f;
     for (int32_t j = cum[r]; j < cum[r + 1]; ++j) {
+      const int64_t tj = nb >= 32 ? 0 : (int64_t)((uint32_t)infos[j] >> nb);
+      if (D_off[tj + 1] - D_off[tj] != D) {
+        rc = -1; /* one key, two widths: not one table */
+        goto done;
+      }
       const int64_t b = (int64_t)((uint32_t)infos[j] & bmask);
-      const float* gr = grad + b * total_D + D0;
-      const int64_t L = offsets[t * B + b + 1] - offsets[t * B + b];
+      const float* gr = grad + b * total_D + D_off[tj];
+      const int64_t L = offsets[tj * B + b + 1] - offsets[tj * B + b];
       const float sc = pooling == ORC_POOL_MEAN ? 1.0f / (float)L : 1.0f; /* L >= 1 here */
       const float wl = iw ? iw[pos[j]] : 1.0f;
       for (int32_t d = 0; d < D; ++d) g[d] = g[d] + (gr[d] * sc) * wl;

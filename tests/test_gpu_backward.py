@@ -171,6 +171,72 @@ def test_backward_many_tables(dev, pooling):
     _backward_case(dev, inp, pooling, seed=pooling)
 
 
+def _shared_tables(rng, ftm, rows, dims, B, max_L, dup=False):
+    """A batch whose features share tables (fbgemm's feature_table_map): per
+    feature weight offsets, hash offsets and momentum offsets point at its
+    table; D_offsets lay the features' columns side by side."""
+    fr, fd = [rows[t] for t in ftm], [dims[t] for t in ftm]
+    inp = random_tbe(rng, len(ftm), B, fd, fr, max_L, dup_heavy=dup)
+    t_off = np.concatenate([[0], np.cumsum([E * D for E, D in zip(rows, dims)])[:-1]])
+    t_hsc = np.concatenate([[0], np.cumsum(rows)[:-1]])
+    w_off = t_off[ftm].astype(np.int64)
+    hsc = np.concatenate([t_hsc[ftm], [sum(rows)]]).astype(np.int64)
+    m1_off = t_hsc[ftm].astype(np.int64)
+    bits = int(np.ceil(np.log2(max(sum(rows), 2))))
+    return inp, w_off, hsc, m1_off, bits
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+@pytest.mark.parametrize("dup", [False, True])
+def test_backward_shared_tables(dev, pooling, weighted, dup):
+    """Features sharing tables (feature_table_map [0, 1, 0, 2, 1]): one run per
+    row of a shared table, each occurrence summing its own feature's gradient
+    columns (MEAN: its own bag length); duplicate-heavy batches reach the
+    chunked long-run path.  Transpose bit-exact, update within rtol 1e-5."""
+    print(f"[case] shared tables pool={pooling} weighted={weighted} dup={dup}", flush=True)
+    rng = np.random.default_rng(50 + pooling + 2 * weighted + 4 * dup)
+    ftm, rows, dims = [0, 1, 0, 2, 1], [300, 200, 50], [64, 32, 128]
+    inp, w_off, hsc, m1_off, bits = _shared_tables(rng, ftm, rows, dims, 120, 30, dup)
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    exp = orc.transpose_embedding_input(hsc, inp.B, nb, bits, inp.indices, inp.offsets)
+    got = torch.ops.fbgemm.transpose_embedding_input(
+        torch.from_numpy(hsc).to(dev), bits, torch.from_numpy(inp.indices).to(dev),
+        torch.from_numpy(inp.offsets).to(dev), False, None, nb)
+    r = int(got[5].item())
+    assert r == exp["num_runs"]
+    np.testing.assert_array_equal(got[1].cpu().numpy(), exp["sorted_linear_indices"])
+    np.testing.assert_array_equal(got[2].cpu().numpy(), exp["infos_sorted"])
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
+    grad = rng.normal(0, 1e-1, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(-1.5, 1.5, inp.N).astype(np.float32) if weighted else None
+    W_exp, m1_exp = orc.backward_rowwise_adagrad(
+        W, w_off, inp.D_offsets, inp.B, hsc, bits, inp.indices, inp.offsets, pooling, grad, m1,
+        m1_off, 0.05, 1e-6, 0.0, 0, nb, indice_weights=iw)
+    Wd, m1d = torch.from_numpy(W).to(dev), torch.from_numpy(m1).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(inp.T, dtype=torch.int32, device=dev)
+    head = (torch.from_numpy(grad).to(dev), Wd, empty, empty, pl, torch.from_numpy(w_off).to(dev),
+            torch.from_numpy(inp.D_offsets).to(dev), max(dims), torch.from_numpy(hsc).to(dev),
+            bits, torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev),
+            pooling)
+    tail = (torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty, pl,
+            torch.from_numpy(m1_off).to(dev), 1e-6, 0.05, 0.0, 0, 0.0)
+    if weighted:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_weighted_exact_cuda(
+            *head, torch.from_numpy(iw).to(dev), *tail)
+    else:
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+            *head, *tail)
+    np.testing.assert_allclose(m1d.cpu().numpy(), m1_exp, rtol=RTOL, atol=0)
+    # Rows here are O(0.5) (a wrong gradient column would show at once), so
+    # the absolute floor is scaled from the 1e-7 used for O(0.01) rows: an
+    # update that nearly cancels the row keeps only the absolute accuracy of
+    # its operands, and the chunked long runs sum in another order.
+    np.testing.assert_allclose(Wd.cpu().numpy(), W_exp, rtol=RTOL, atol=1e-6)
+
+
 @pytest.mark.parametrize("wd_mode,wd", [(1, 0.1), (2, 0.05)])
 def test_backward_weight_decay(dev, wd_mode, wd):
     print(f"[case] backward weight decay mode {wd_mode}", flush=True)

@@ -304,6 +304,57 @@ def test_adagrad_vs_torch_autograd(pooling, wd_mode, wd, weighted):
                                    atol=1e-7)
 
 
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_adagrad_shared_tables_vs_torch_autograd(pooling, weighted):
+    """Features sharing a table (fbgemm's feature_table_map = [0, 1, 0]): the
+    per-feature arrays point features 0 and 2 at table 0's rows, hash offset
+    and momentum, so a row looked up by both is one run whose gradient sums
+    each occurrence's slice from its own feature's columns."""
+    rng = np.random.default_rng(31 + pooling + 2 * weighted)
+    ftm, rows, dims = [0, 1, 0], [30, 20], [16, 8]
+    fr, fd = [rows[t] for t in ftm], [dims[t] for t in ftm]
+    inp = random_tbe(rng, 3, 10, fd, fr, 7, empty_frac=0.1)
+    t_off = np.array([0, rows[0] * dims[0]], np.int64)
+    t_hsc = np.array([0, rows[0]], np.int64)
+    w_off = t_off[ftm]
+    hsc = np.concatenate([t_hsc[ftm], [sum(rows)]]).astype(np.int64)
+    m1_off = t_hsc[ftm]
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E, D in zip(rows, dims))).astype(np.float32)
+    m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
+    grad = rng.normal(0, 1, size=(inp.B, inp.total_D)).astype(np.float32)
+    iw = rng.uniform(-1.5, 1.5, inp.N).astype(np.float32) if weighted else None
+    lr, eps = 0.1, 1e-6
+    W_new, m_new = orc.backward_rowwise_adagrad(
+        W, w_off, inp.D_offsets, inp.B, hsc, 6, inp.indices, inp.offsets, pooling, grad, m1,
+        m1_off, lr, eps, 0.0, 0, orc.info_B_num_bits(3, inp.B), indice_weights=iw)
+    Wt = [torch.tensor(W[t_off[t]: t_off[t] + rows[t] * dims[t]].reshape(rows[t], dims[t]),
+                       requires_grad=True) for t in range(2)]
+    loss = 0
+    for f, t in enumerate(ftm):
+        o = inp.offsets[f * inp.B:(f + 1) * inp.B + 1]
+        psw = None if iw is None else torch.from_numpy(iw[o[0]:o[-1]])
+        out = _torch_bag(Wt[t], torch.from_numpy(inp.indices[o[0]:o[-1]]),
+                         torch.from_numpy(o[:-1] - o[0]), pooling, psw)
+        d0, d1 = inp.D_offsets[f], inp.D_offsets[f + 1]
+        loss = loss + (out * torch.from_numpy(grad[:, d0:d1])).sum()
+    loss.backward()
+    for t in range(2):
+        E, D = rows[t], dims[t]
+        g, w = Wt[t].grad.detach(), Wt[t].detach()
+        seen = np.concatenate([inp.indices[inp.offsets[f * inp.B]: inp.offsets[(f + 1) * inp.B]]
+                               for f in range(3) if ftm[f] == t])
+        touched = torch.from_numpy(np.isin(np.arange(E), seen))
+        h0 = torch.from_numpy(m1[t_hsc[t]: t_hsc[t] + E])
+        h = h0 + (g * g).sum(1) / D
+        m = lr / (h.sqrt() + eps)
+        w_ref = torch.where(touched[:, None], w - m[:, None] * g, w)
+        np.testing.assert_allclose(W_new[t_off[t]: t_off[t] + E * D].reshape(E, D), w_ref.numpy(),
+                                   rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(m_new[t_hsc[t]: t_hsc[t] + E],
+                                   torch.where(touched, h, h0).numpy(), rtol=1e-5, atol=1e-7)
+
+
 def test_adagrad_zero_grad_changes_nothing():
     rng = np.random.default_rng(2)
     inp = random_tbe(rng, 1, 10, [8], [20], 5)

@@ -649,18 +649,6 @@ struct MetaView {
   __device__ int64_t w_off(int64_t t) const { return cached ? m.w_off[t] : a.w_off[t]; }
   __device__ int64_t m1_off(int64_t t) const { return cached ? m.m1_off[t] : a.m1_off[t]; }
   __device__ int32_t D_off(int64_t t) const { return cached ? m.D_off[t] : a.D_off[t]; }
-  // Table of a linearized key: the last t with hsc[t] <= key.
-  __device__ int64_t table_of_key(int64_t key) const {
-    int32_t lo = 0, hi = a.T;
-    while (hi - lo > 1) {
-      const int32_t mid = (lo + hi) >> 1;
-      if (hsc(mid) <= key)
-        lo = mid;
-      else
-        hi = mid;
-    }
-    return lo;
-  }
 };
 
 __device__ __forceinline__ void ld4(const float* p, float (&v)[4]) {
@@ -704,7 +692,7 @@ __device__ __forceinline__ int64_t table_of(const BwdArgs& a, int32_t info) {
 // `info0` is lane k's infos[s0 + k] (valid for k < s1 - s0), already loaded
 // by the caller to find the table.
 template <typename I, int G, int NCH, int U>
-__device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, int32_t D,
+__device__ void group_sum_occurrences(const BwdArgs& a, const MetaView& mv, int32_t D,
                                       int64_t s0, int64_t s1, int g, int k, int32_t info0,
                                       float (&acc)[NCH][4]) {
   const uint32_t bmask = a.nb >= 32 ? 0xffffffffu : ((1u << a.nb) - 1u);
@@ -719,8 +707,11 @@ __device__ void group_sum_occurrences(const BwdArgs& a, int64_t t, int32_t D0, i
     if (k < n) {
       const int32_t info = info_cur;
       const int64_t b = static_cast<int64_t>(static_cast<uint32_t>(info) & bmask);
-      const int64_t bag = a.B_off ? a.B_off[t] + b : t * a.B + b;
-      my_row = a.row_out ? a.row_out[bag] : b * a.total_D + D0;
+      // The occurrence's own feature: features that share a table share its
+      // rows (one run) but each has its own bags and gradient columns.
+      const int64_t tj = table_of(a, info);
+      const int64_t bag = a.B_off ? a.B_off[tj] + b : tj * a.B + b;
+      my_row = a.row_out ? a.row_out[bag] : b * a.total_D + mv.D_off(tj);
       if (a.pooling == MX_POOL_MEAN) {
         const I* off = static_cast<const I*>(a.offsets);
         const int64_t L = static_cast<int64_t>(off[bag + 1]) - static_cast<int64_t>(off[bag]);
@@ -895,7 +886,7 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
       const int64_t key = a.run[r];
       const int64_t qf = a.chunk_start[r];  // the run's first chunk
       const int64_t q1 = qf + (s1 - s0 + kChunk - 1) / kChunk;
-      const int64_t t = mv.table_of_key(key);
+      const int64_t t = table_of(a, a.infos[s0]);  // a feature of the run's table
       const int32_t D = mv.D_off(t + 1) - mv.D_off(t);
       const int64_t idx = key - mv.hsc(t);
       const int64_t row0 = mv.w_off(t) + idx * D;
@@ -986,7 +977,7 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[c][e] = 0.0f;
-    group_sum_occurrences<I, G, NCH, U>(a, t, D0, D, s0, s1, g, k, info0, acc);
+    group_sum_occurrences<I, G, NCH, U>(a, mv, D, s0, s1, g, k, info0, acc);
     float* dst = a.partial + q * a.max_D;
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
@@ -1030,7 +1021,7 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
     for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int e = 0; e < 4; ++e) gs[c][e] = 0.0f;
-    group_sum_occurrences<I, G, NCH, U>(a, t, D0, D, cs0, cs1, g, k, info0, gs);
+    group_sum_occurrences<I, G, NCH, U>(a, mv, D, cs0, cs1, g, k, info0, gs);
     adagrad_update<G, NCH>(a, D, k, gs, w, wrow, row0, hp, h0);
   }
 }
