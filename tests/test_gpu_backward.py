@@ -237,6 +237,44 @@ def test_backward_shared_tables(dev, pooling, weighted, dup):
     np.testing.assert_allclose(Wd.cpu().numpy(), W_exp, rtol=RTOL, atol=1e-6)
 
 
+@pytest.mark.parametrize("weighted", [False, True])
+def test_module_training_step_shared_tables(dev, weighted):
+    """SplitTableBatchedEmbeddingBagsCodegen(specs, feature_table_map=[0, 1, 0]):
+    forward bit-exact against the oracle on the per-feature arrays, and one
+    fused update per row of the shared table (vs the oracle pinned to torch
+    autograd on shared tables)."""
+    print(f"[case] module shared tables weighted={weighted}", flush=True)
+    from mx_fbgemm import ComputeDevice, EmbeddingLocation, PoolingMode
+    from mx_fbgemm.split_table_batched_embeddings_ops_training import (
+        SplitTableBatchedEmbeddingBagsCodegen,
+    )
+
+    ftm, rows, dims = [0, 1, 0], [200, 80], [64, 32]
+    specs = [(E, D, EmbeddingLocation.DEVICE, ComputeDevice.CUDA) for E, D in zip(rows, dims)]
+    tbe = SplitTableBatchedEmbeddingBagsCodegen(specs, ftm, pooling_mode=PoolingMode.SUM,
+                                                learning_rate=0.05, eps=1e-6, device=dev,
+                                                weights_init=(-0.5, 0.5))
+    rng = np.random.default_rng(61 + weighted)
+    inp, w_off, hsc, m1_off, bits = _shared_tables(rng, ftm, rows, dims, 24, 12, dup=True)
+    assert tbe.weights_offsets.tolist() == w_off.tolist()
+    assert tbe.hash_size_cumsum.tolist() == hsc.tolist()
+    W0 = tbe.weights_dev.detach().cpu().numpy().copy()
+    iw = rng.uniform(0.5, 1.5, inp.N).astype(np.float32) if weighted else None
+    out = tbe(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev),
+              per_sample_weights=None if iw is None else torch.from_numpy(iw).to(dev))
+    exp = orc.tbe_forward_f32(W0, w_off, inp.D_offsets, inp.B, inp.indices, inp.offsets, 0,
+                              indice_weights=iw)
+    assert np.array_equal(out.detach().cpu().numpy(), exp)
+    gout = rng.normal(0, 1e-1, size=out.shape).astype(np.float32)
+    out.backward(torch.from_numpy(gout).to(dev))
+    W_exp, m_exp = orc.backward_rowwise_adagrad(
+        W0, w_off, inp.D_offsets, inp.B, hsc, bits, inp.indices, inp.offsets, 0, gout,
+        np.zeros(sum(rows), np.float32), m1_off, 0.05, 1e-6, 0.0, 0,
+        orc.info_B_num_bits(inp.T, inp.B), indice_weights=iw)
+    np.testing.assert_allclose(tbe.weights_dev.detach().cpu().numpy(), W_exp, rtol=RTOL, atol=1e-6)
+    np.testing.assert_allclose(tbe.momentum1_dev.cpu().numpy(), m_exp, rtol=RTOL, atol=0)
+
+
 @pytest.mark.parametrize("wd_mode,wd", [(1, 0.1), (2, 0.05)])
 def test_backward_weight_decay(dev, wd_mode, wd):
     print(f"[case] backward weight decay mode {wd_mode}", flush=True)

@@ -94,3 +94,29 @@ def test_inference_module_assign_and_lookup(dev, ty):
     exp = orc.nbit_forward(buf, m.weights_offsets.cpu().numpy(), [sty.as_int()] * 2,
                            inp.D_offsets, B, inp.indices, inp.offsets, 0, out_f16=False)
     np.testing.assert_allclose(res.cpu().numpy(), exp, rtol=1e-5, atol=1e-5)
+
+
+def test_inference_module_shared_tables(dev):
+    """IntNBitTableBatchedEmbeddingBagsCodegen with feature_table_map [1, 0, 1]:
+    the lookup equals the oracle's on the per-feature arrays."""
+    print("[case] nbit module shared tables", flush=True)
+    from mx_fbgemm import EmbeddingLocation, PoolingMode, SparseType
+    from mx_fbgemm.split_table_batched_embeddings_ops_inference import (
+        IntNBitTableBatchedEmbeddingBagsCodegen,
+    )
+    from tbe_helpers import random_tbe
+
+    ftm = [1, 0, 1]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(
+        [("a", 40, 64, SparseType.INT8, EmbeddingLocation.DEVICE),
+         ("b", 30, 32, SparseType.INT4, EmbeddingLocation.DEVICE)], ftm,
+        pooling_mode=PoolingMode.MEAN, output_dtype=SparseType.FP32, device=dev)
+    m.fill_random_weights(3)
+    rng = np.random.default_rng(13)
+    rows, dims = [40, 30], [64, 32]
+    inp = random_tbe(rng, 3, 20, [dims[t] for t in ftm], [rows[t] for t in ftm], 9)
+    got = m(torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev))
+    exp = orc.nbit_forward(m.weights_dev.cpu().numpy(), m.weights_offsets.cpu().numpy(),
+                           m.weights_tys.cpu().numpy(), inp.D_offsets, inp.B, inp.indices,
+                           inp.offsets, 1, out_f16=False)
+    np.testing.assert_allclose(got.cpu().numpy(), exp, rtol=1e-2, atol=1e-3)

@@ -54,6 +54,25 @@ def test_training_module_arguments():
     assert float(m.weights_dev.abs().max()) <= 0.01
 
 
+def test_training_module_feature_table_map():
+    """Features 0 and 2 share table 0: per-feature offsets point at its rows,
+    hash range and momentum; the output has one column block per feature."""
+    specs = [(100, 64, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (7, 128, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)]
+    m = SplitTableBatchedEmbeddingBagsCodegen(specs, [0, 1, 0], device="cpu")
+    assert m.T == 3
+    assert m.weights_offsets.tolist() == [0, 6400, 0]
+    assert m.D_offsets.tolist() == [0, 64, 192, 256]
+    assert m.hash_size_cumsum.tolist() == [0, 100, 0, 107]
+    assert m.momentum1_offsets.tolist() == [0, 100, 0]
+    assert m.rows_per_table.tolist() == [100, 7, 100]
+    assert m.total_D == 256 and m.max_D == 128 and m.total_hash_size_bits == 7
+    assert m.weights_dev.numel() == 6400 + 896 and m.momentum1_dev.numel() == 107
+    assert [tuple(x.shape) for x in m.split_embedding_weights()] == [(100, 64), (7, 128)]
+    with pytest.raises(ValueError):
+        SplitTableBatchedEmbeddingBagsCodegen(specs, [0, 2], device="cpu")
+
+
 def test_training_module_rejects_unsupported():
     with pytest.raises(ValueError):
         SplitTableBatchedEmbeddingBagsCodegen(
@@ -94,3 +113,16 @@ def test_bench_inputs_shapes():
     assert c4.tys == [2] * 16 + [3] * 16 and np.all(np.diff(c4.offsets) == 20)
     c5 = bench_inputs.config5(T=8, B=200, e_hi=1e5)
     assert c5.D == [32, 64, 128, 256] * 2 and (np.diff(c5.offsets) == 0).mean() > 0.05
+
+
+def test_inference_module_feature_table_map():
+    specs = [("a", 10, 128, SparseType.INT8, EmbeddingLocation.DEVICE),
+             ("b", 20, 64, SparseType.INT4, EmbeddingLocation.DEVICE)]
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(specs, [1, 0, 1], device="cpu")
+    assert m.T == 3 and m.total_D == 256
+    assert m.weights_offsets.tolist() == [1440, 0, 1440]
+    assert m.weights_tys.tolist() == [3, 2, 3]
+    assert m.D_offsets.tolist() == [0, 64, 192, 256]
+    assert m.rows_per_table.tolist() == [20, 10, 20]
+    assert m.weights_dev.numel() == 1440 + 960
+    assert [tuple(x.shape) for x in m.split_embedding_weights()] == [(10, 144), (20, 48)]

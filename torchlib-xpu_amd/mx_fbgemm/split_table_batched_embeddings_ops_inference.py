@@ -64,11 +64,13 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
 
     ``embedding_specs`` holds ``(name, num_embeddings, embedding_dim,
     weight_ty, location)`` per table; only EmbeddingLocation.DEVICE is
-    supported."""
+    supported.  ``feature_table_map`` ([T] table index per feature, default
+    one feature per table) lets several features look up one table."""
 
     def __init__(
         self,
         embedding_specs: list[tuple[str, int, int, SparseType, EmbeddingLocation]],
+        feature_table_map: Optional[list[int]] = None,
         pooling_mode: PoolingMode = PoolingMode.SUM,
         output_dtype: SparseType = SparseType.FP16,
         row_alignment: int = 16,
@@ -95,21 +97,28 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.output_dtype = output_dtype
         self.row_alignment = row_alignment
         self.bounds_check_mode = BoundsCheckMode(bounds_check_mode)
-        self.T = len(embedding_specs)
         dims = [D for _, _, D, _, _ in embedding_specs]
         rows = [E for _, E, _, _, _ in embedding_specs]
         tys = [ty for _, _, _, ty, _ in embedding_specs]
-        self.total_D = sum(dims)
+        ftm = list(range(len(embedding_specs))) if feature_table_map is None else \
+            [int(t) for t in feature_table_map]
+        if not ftm or any(t < 0 or t >= len(embedding_specs) for t in ftm):
+            raise ValueError("feature_table_map must name tables of embedding_specs")
+        self.feature_table_map = ftm
+        self.T = len(ftm)  # features
+        self.total_D = sum(dims[t] for t in ftm)
         self.row_bytes = [padded_row_size_in_bytes(D, ty, row_alignment)
                           for D, ty in zip(dims, tys)]
         sizes = [E * rb for E, rb in zip(rows, self.row_bytes)]
         offs = [0] + list(itertools.accumulate(sizes))
-        self.register_buffer("weights_offsets", torch.tensor(offs[:-1], device=device,
-                                                             dtype=torch.int64))
-        self.register_buffer("weights_tys", torch.tensor([t.as_int() for t in tys],
+        self._table_offsets = offs[:-1]
+        self.register_buffer("weights_offsets", torch.tensor([offs[t] for t in ftm],
+                                                             device=device, dtype=torch.int64))
+        self.register_buffer("weights_tys", torch.tensor([tys[t].as_int() for t in ftm],
                                                          device=device, dtype=torch.uint8))
-        self.register_buffer("D_offsets", torch.tensor([0] + list(itertools.accumulate(dims)),
-                                                       device=device, dtype=torch.int32))
+        self.register_buffer("D_offsets",
+                             torch.tensor([0] + list(itertools.accumulate(dims[t] for t in ftm)),
+                                          device=device, dtype=torch.int32))
         self.register_buffer("weights_placements",
                              torch.full((self.T,), int(EmbeddingLocation.DEVICE), device=device,
                                         dtype=torch.int32))
@@ -126,8 +135,8 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.max_int8_D = max_d(SparseType.INT8)
         self.max_float16_D = max_d(SparseType.FP16)
         self.max_float32_D = max_d(SparseType.FP32)
-        self.register_buffer("rows_per_table", torch.tensor(rows, device=device,
-                                                            dtype=torch.int64))
+        self.register_buffer("rows_per_table", torch.tensor([rows[t] for t in ftm],
+                                                            device=device, dtype=torch.int64))
         self.register_buffer("bounds_check_warning", torch.zeros(1, device=device,
                                                                  dtype=torch.int64))
         self._rows, self._dims, self._tys = rows, dims, tys
@@ -155,8 +164,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
     def split_embedding_weights(self) -> list[torch.Tensor]:
         """Per-table uint8 ``[E_t, row_bytes_t]`` views (qparams included)."""
         out = []
-        for t, (E, rb) in enumerate(zip(self._rows, self.row_bytes)):
-            o = int(self.weights_offsets[t])
+        for o, E, rb in zip(self._table_offsets, self._rows, self.row_bytes):
             out.append(self.weights_dev[o:o + E * rb].view(E, rb))
         return out
 

@@ -41,8 +41,11 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
 
     ``embedding_specs`` holds ``(num_embeddings, embedding_dim, location,
     compute_device)`` per table; only EmbeddingLocation.DEVICE on a GPU is
-    supported.  ``forward(indices, offsets)`` takes t-major offsets of T*B+1
-    entries and returns ``[B, sum(D)]``; ``loss.backward()`` updates the
+    supported.  ``feature_table_map`` ([T] table index per feature, default
+    one feature per table) lets features share a table: they look up the same
+    rows, and the fused update sums every feature's gradient into each row
+    once.  ``forward(indices, offsets)`` takes feature-major offsets of T*B+1
+    entries (T features) and returns ``[B, sum of the features' D]``; ``loss.backward()`` updates the
     weights and momentum in place (the gradient itself is never materialised).
     Indices and offsets are first validated, and repaired in place, by
     ``torch.ops.fbgemm.bounds_check_indices`` (BoundsCheckMode.WARNING by
@@ -62,6 +65,7 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     def __init__(
         self,
         embedding_specs: list[tuple[int, int, EmbeddingLocation, ComputeDevice]],
+        feature_table_map: Optional[list[int]] = None,
         optimizer: EmbOptimType = EmbOptimType.EXACT_ROWWISE_ADAGRAD,
         pooling_mode: PoolingMode = PoolingMode.SUM,
         learning_rate: float = 0.01,
@@ -107,23 +111,36 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.stochastic_rounding = bool(stochastic_rounding)
         rows = [E for E, _, _, _ in embedding_specs]
         dims = [D for _, D, _, _ in embedding_specs]
-        self.T = len(embedding_specs)
-        self.total_D = sum(dims)
-        self.max_D = max(dims)
-        hash_size_cumsum = _cumsum(rows)
-        self.total_hash_size_bits = max(1, int(hash_size_cumsum[-1] - 1).bit_length())
+        # Features (the T of the batch) map onto tables; several features may
+        # share one table, i.e. its rows, hash offset and momentum.
+        ftm = list(range(len(embedding_specs))) if feature_table_map is None else \
+            [int(t) for t in feature_table_map]
+        if not ftm or any(t < 0 or t >= len(embedding_specs) for t in ftm):
+            raise ValueError("feature_table_map must name tables of embedding_specs")
+        self.feature_table_map = ftm
+        self.T = len(ftm)
+        f_rows = [rows[t] for t in ftm]
+        f_dims = [dims[t] for t in ftm]
+        self.total_D = sum(f_dims)
+        self.max_D = max(f_dims)
+        table_hash = _cumsum(rows)
+        self.total_hash_size_bits = max(1, int(table_hash[-1] - 1).bit_length())
         if self.total_hash_size_bits > 32:
             raise ValueError("total hash size above 2^32 rows is not supported")
         w_elems = [E * D for E, D in zip(rows, dims)]
+        table_w_off = _cumsum(w_elems)[:-1]
         i64 = dict(device=device, dtype=torch.int64)
-        self.register_buffer("weights_offsets", torch.tensor(_cumsum(w_elems)[:-1], **i64))
-        self.register_buffer("D_offsets", torch.tensor(_cumsum(dims), device=device,
+        self.register_buffer("weights_offsets",
+                             torch.tensor([table_w_off[t] for t in ftm], **i64))
+        self.register_buffer("D_offsets", torch.tensor(_cumsum(f_dims), device=device,
                                                        dtype=torch.int32))
-        self.register_buffer("hash_size_cumsum", torch.tensor(hash_size_cumsum, **i64))
+        self.register_buffer("hash_size_cumsum",
+                             torch.tensor([table_hash[t] for t in ftm] + [table_hash[-1]], **i64))
         self.register_buffer("weights_placements",
                              torch.full((self.T,), int(EmbeddingLocation.DEVICE), device=device,
                                         dtype=torch.int32))
-        self.register_buffer("momentum1_offsets", torch.tensor(_cumsum(rows)[:-1], **i64))
+        self.register_buffer("momentum1_offsets",
+                             torch.tensor([table_hash[t] for t in ftm], **i64))
         lo, hi = weights_init if weights_init is not None else (-0.01, 0.01)
         self.weights_dev = nn.Parameter(
             torch.empty(sum(w_elems), device=device, dtype=torch.float32).uniform_(lo, hi)
@@ -141,10 +158,13 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         # though the weights are updated by the fused backward, not by autograd.
         self.placeholder_autograd_tensor = nn.Parameter(
             torch.zeros(0, device=device, dtype=torch.float32))
-        self.register_buffer("rows_per_table", torch.tensor(rows, **i64))
+        self.register_buffer("rows_per_table", torch.tensor(f_rows, **i64))
         self.register_buffer("bounds_check_warning", torch.zeros(1, **i64))
         self._rows = rows
         self._dims = dims
+        self._f_dims = f_dims
+        self._table_w_off = table_w_off
+        self._table_m_off = table_hash[:-1]
 
     def _vbe_args(self, batch_size_per_feature_per_rank: list[list[int]], device):
         """B_offsets, output offsets per (rank, feature), batch offsets per
@@ -156,7 +176,7 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         per_feature = [sum(r) for r in bs]
         B_offsets = _cumsum(per_feature)
         rpf = [_cumsum(r) for r in bs]
-        out_sizes = [bs[t][r] * self._dims[t] for r in range(R) for t in range(self.T)]
+        out_sizes = [bs[t][r] * self._f_dims[t] for r in range(R) for t in range(self.T)]
         i32 = dict(device=device, dtype=torch.int32)
         return dict(
             B_offsets=torch.tensor(B_offsets, **i32),
@@ -207,16 +227,11 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     def split_embedding_weights(self) -> list[torch.Tensor]:
         """Per-table ``[E_t, D_t]`` views of the flat weight buffer."""
         out = []
-        for t, (E, D) in enumerate(zip(self._rows, self._dims)):
-            o = int(self.weights_offsets[t])
+        for o, E, D in zip(self._table_w_off, self._rows, self._dims):
             out.append(self.weights_dev.detach()[o:o + E * D].view(E, D))
         return out
 
     @torch.no_grad()
     def split_optimizer_states(self) -> list[list[torch.Tensor]]:
         """Per-table ``[[momentum1 (E_t,)]]`` views."""
-        out = []
-        for t, E in enumerate(self._rows):
-            o = int(self.momentum1_offsets[t])
-            out.append([self.momentum1_dev[o:o + E]])
-        return out
+        return [[self.momentum1_dev[o:o + E]] for o, E in zip(self._table_m_off, self._rows)]
