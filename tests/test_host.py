@@ -73,6 +73,17 @@ def test_training_module_feature_table_map():
         SplitTableBatchedEmbeddingBagsCodegen(specs, [0, 2], device="cpu")
 
 
+def test_training_module_learning_rate_and_init():
+    m = SplitTableBatchedEmbeddingBagsCodegen(
+        [(10, 8, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)], learning_rate=0.1, device="cpu")
+    assert m.get_learning_rate() == 0.1
+    m.set_learning_rate(0.02)
+    assert m.get_learning_rate() == 0.02
+    m.init_embedding_weights_uniform(2.0, 3.0)
+    w = m.split_embedding_weights()[0]
+    assert float(w.min()) >= 2.0 and float(w.max()) <= 3.0
+
+
 def test_training_module_rejects_unsupported():
     with pytest.raises(ValueError):
         SplitTableBatchedEmbeddingBagsCodegen(

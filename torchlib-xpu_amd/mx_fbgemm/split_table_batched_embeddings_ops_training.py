@@ -231,6 +231,20 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
             out.append(self.weights_dev.detach()[o:o + E * D].view(E, D))
         return out
 
+    def set_learning_rate(self, lr: float) -> None:
+        """The rate the next backward's fused update uses."""
+        self.learning_rate = float(lr)
+
+    def get_learning_rate(self) -> float:
+        return self.learning_rate
+
+    @torch.no_grad()
+    def init_embedding_weights_uniform(self, min_val: float, max_val: float) -> None:
+        """Every row of every table drawn from U(min_val, max_val)."""
+        w = torch.empty(self.weights_dev.numel(), device=self.weights_dev.device,
+                        dtype=torch.float32).uniform_(min_val, max_val)
+        self.weights_dev.copy_(w.to(self.weights_dev.dtype))
+
     @torch.no_grad()
     def split_optimizer_states(self) -> list[list[torch.Tensor]]:
         """Per-table ``[[momentum1 (E_t,)]]`` views."""
