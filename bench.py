@@ -208,6 +208,24 @@ def bench_tbe_forward(args, dev):
         cold.append(s.elapsed_time(e))
     del flush
 
+    # Successive batches of one model: 8 batches with the same hot rows and
+    # fresh draws, launched in rotation (each batch's tail rows are new to
+    # the caches, as in training); reported beside the repeated-batch figure.
+    log("generating 7 more config-2 batches of the same tables")
+    batches = [(torch.from_numpy(b.indices).to(dev), torch.from_numpy(b.offsets).to(dev), b.N)
+               for b in bench_inputs.config2_batches(8)]
+    turn = [0]
+
+    def fresh_step():
+        bi, bo, _ = batches[turn[0] % len(batches)]
+        turn[0] += 1
+        return op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, bi, bo, 0, e32, empty, 0,
+                  False)
+
+    fresh_steps = 8 * max(1, args.steps // 8)
+    _, fresh_ms = time_launches(fresh_step, fresh_steps, len(batches))
+    fresh_n = sum(b[2] for b in batches) / len(batches)
+
     res = dict(
         metric="TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
         value=N * args.steps / wall,
@@ -221,6 +239,8 @@ def bench_tbe_forward(args, dev):
         alg_bytes=alg_bytes,
         kernel_ms_mean=mean_ms,
         cold_kernel_ms_median=statistics.median(cold),
+        fresh_batches=dict(batches=len(batches), launch_ms_mean=fresh_ms,
+                           lookups_per_s=fresh_n / (fresh_ms * 1e-3)),
     )
     traffic = traffic_from_profile("tbe_fwd_config2")
 
@@ -521,6 +541,8 @@ def main():
     )
     if "cold_kernel_ms_median" in res:
         line["roofline"]["cold_launch_ms_median"] = res["cold_kernel_ms_median"]
+    if "fresh_batches" in res:
+        line["roofline"]["fresh_batches"] = res["fresh_batches"]
     print(json.dumps(line), flush=True)
 
 

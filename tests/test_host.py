@@ -126,6 +126,19 @@ def test_bench_inputs_shapes():
     assert c5.D == [32, 64, 128, 256] * 2 and (np.diff(c5.offsets) == 0).mean() > 0.05
 
 
+def test_config2_batches_share_hot_rows():
+    """Batch 0 is config2 itself; later batches draw afresh over the same
+    per-table permutations, so each table's hottest row is the same row."""
+    bs = bench_inputs.config2_batches(3, T=3, E=5000, B=300)
+    c2 = bench_inputs.config2(T=3, E=5000, B=300)
+    assert np.array_equal(bs[0].indices, c2.indices) and np.array_equal(bs[0].offsets, c2.offsets)
+    assert not np.array_equal(bs[1].offsets, bs[2].offsets)
+    for t in range(3):
+        tops = {int(np.bincount(b.indices[b.offsets[t * 300]:b.offsets[(t + 1) * 300]],
+                                minlength=5000).argmax()) for b in bs}
+        assert len(tops) == 1
+
+
 def test_inference_module_feature_table_map():
     specs = [("a", 10, 128, SparseType.INT8, EmbeddingLocation.DEVICE),
              ("b", 20, 64, SparseType.INT4, EmbeddingLocation.DEVICE)]

@@ -38,6 +38,20 @@ int num_cus() {
   return cached[dev];
 }
 
+hipStream_t side_stream() {
+  static std::mutex mu;
+  static hipStream_t cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == nullptr) {
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    cached[dev] = st;  // kept until the process ends
+  }
+  return cached[dev];
+}
+
 __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x)

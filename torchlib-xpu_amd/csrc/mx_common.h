@@ -21,6 +21,10 @@ void clear_error();
 
 // Number of compute units of the current device (cached per device).
 int num_cus();
+// A second stream of the current device (non-blocking, default priority),
+// created on first use; null if it cannot be created.  Work forked onto it
+// is joined back to the caller's stream before an entry point returns.
+hipStream_t side_stream();
 
 #define MX_REQUIRE(cond, ...)                                   \
   do {                                                          \

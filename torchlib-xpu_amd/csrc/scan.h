@@ -10,7 +10,7 @@
 namespace mx {
 
 constexpr int kScanThreads = 256;
-constexpr int kScanItems = 8;
+constexpr int kScanItems = 12;  // 3072-element tiles (2048: +2.4 us, 4096: +2.8 us on 668k)
 constexpr int64_t kScanTile = kScanThreads * kScanItems;
 
 inline int64_t scan_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }

@@ -18,8 +18,8 @@
 //    mark (a max-scan), so no per-position search.  The same kernel
 //    accumulates the global digit histograms of every pass (LDS, then one
 //    atomic per bin and block).
-//  * One launch per pass ("onesweep"): a block ranks a 2048-key tile (each
-//    wave 512 keys, 64 at a time, stable ranks from 8 ballots), then thread d
+//  * One launch per pass ("onesweep"): a block ranks a 3072-key tile (each
+//    wave 768 keys, 64 at a time, stable ranks from 8 ballots), then thread d
 //    finds how many keys of digit d earlier tiles hold through a decoupled
 //    look-back over per-(tile, digit) status words, and the tile scatters.
 //    Tiles take tickets in launch order, so every wait ends.
@@ -42,9 +42,12 @@ namespace {
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxPasses = 4;
-constexpr int kSweepItems = 8;                        // keys per lane per pass
-constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;  // 512 keys per wave
-constexpr int64_t kSweepTile = 4 * kSweepWaveKeys;    // 2048 keys per block
+// 3072-key tiles: 218 tiles for config 3's 668k keys, one per CU; 2048-key
+// tiles (two on some CUs) made each pass ~2 us slower, 4096 (half the CUs
+// idle) ~1 us slower.
+constexpr int kSweepItems = 12;                       // keys per lane per pass
+constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;  // 768 keys per wave
+constexpr int64_t kSweepTile = 4 * kSweepWaveKeys;    // 3072 keys per block
 constexpr int kLinItems = 8;
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
 constexpr int kLong = 32;                             // runs longer than this are chunked
@@ -286,8 +289,10 @@ __global__ void __launch_bounds__(256)
       __hip_atomic_store(mine, kSweepAgg | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // Look back kLookBack predecessors per round (independent loads), folding
       // them nearest first until an inclusive word; an unpublished word
-      // (flag 0) ends the round and the next round resumes there.
-      constexpr int kLookBack = 8;
+      // (flag 0) ends the round and the next round resumes there.  Wider
+      // rounds issue more uncached loads than they save in rounds (per pass
+      // at 2048-key tiles: 8 +0.6 us, 16 +2.2, 32 +5.1; 2 is no faster).
+      constexpr int kLookBack = 4;
       int64_t j = tile - 1;  // nearest predecessor not yet folded in
       int spins = 0;
       bool done = false;
@@ -1026,9 +1031,9 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
   }
 }
 
+// Runs longer than kLong: chunk partial sums, then one block per run.
 template <typename I, typename WT, int G, int NCH>
-int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
-  constexpr int U = NCH <= 1 ? 4 : 2;   // runs are short: keep registers low
+int launch_long_runs(const BwdArgs& a, int64_t N, hipStream_t s) {
   constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
   constexpr int P = 64 / G;
   const int64_t want = ceil_div(N, 4 * P);
@@ -1045,19 +1050,62 @@ int launch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
   constexpr int NCHL = GL == 2 * G ? NCH / 2 : NCH;
   bwd_long_run_kernel<WT, GL, NCHL, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+// Runs of at most kLong occurrences: the fused sum + update kernel.
+template <typename I, typename WT, int G, int NCH>
+int launch_short_runs(const BwdArgs& a, int64_t N, hipStream_t s) {
+  constexpr int U = NCH <= 1 ? 4 : 2;   // runs are short: keep registers low
+  constexpr int P = 64 / G;
+  const int64_t want = ceil_div(N, 4 * P);
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
+  const int64_t nblk = want < 1 ? 1 : (want > cap ? cap : want);
+  const dim3 grid(static_cast<uint32_t>(ceil_div(nblk, 8) * 8));  // whole rounds over the XCDs
   bwd_update_kernel<I, WT, G, NCH, U><<<grid, 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
 
+// Chunk layout of the long runs (chunk-count scan), then both run classes.
+// Short and long runs update disjoint rows and momentum words, and the short
+// runs need nothing of the chunk layout, so the long-run path goes to a
+// second stream forked from `s` and joined back into it: the update kernel,
+// bound by its random row read-modify-writes, hides the latency-bound scan
+// and long-run kernels.
+template <typename I, typename WT, int G, int NCH>
+int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
+  hipStream_t side = side_stream();
+  hipEvent_t fork = nullptr, join = nullptr;
+  if (side == nullptr || hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess ||
+      hipEventRecord(fork, s) != hipSuccess || hipStreamWaitEvent(side, fork, 0) != hipSuccess)
+    side = s;  // one stream: the same kernels in order
+  int rc = prefix_scan_epi(
+      ChunkCount{a.cum}, N, reinterpret_cast<const int32_t*>(a.num_runs),
+      ChunkEpi{a.cum, chunk_start, ws.chunk_mark, &ws.counters[1]},
+      scan_slot(ws, 1), side);
+  if (rc == MX_OK) rc = launch_long_runs<I, WT, G, NCH>(a, N, side);
+  const int rc_short = launch_short_runs<I, WT, G, NCH>(a, N, s);
+  if (side != s) {
+    if (hipEventRecord(join, side) != hipSuccess || hipStreamWaitEvent(s, join, 0) != hipSuccess) {
+      hipStreamSynchronize(side);  // nothing may outlive the call unordered
+      if (rc == MX_OK) rc = set_error(MX_EHIP, "joining the long-run stream failed");
+    }
+  }
+  if (fork) hipEventDestroy(fork);
+  if (join) hipEventDestroy(join);
+  return rc != MX_OK ? rc : rc_short;
+}
+
 // Lanes per run (G) and float4 chunks per lane (NCH) from the widest table.
 template <typename I, typename WT>
-int dispatch_bwd(const BwdArgs& a, int64_t N, hipStream_t s) {
-  if (a.max_D <= 64) return launch_bwd<I, WT, 16, 1>(a, N, s);
-  if (a.max_D <= 128) return launch_bwd<I, WT, 16, 2>(a, N, s);
-  if (a.max_D <= 256) return launch_bwd<I, WT, 32, 2>(a, N, s);
-  if (a.max_D <= 512) return launch_bwd<I, WT, 64, 2>(a, N, s);
-  return launch_bwd<I, WT, 64, 4>(a, N, s);
+int dispatch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
+  if (a.max_D <= 64) return launch_bwd<I, WT, 16, 1>(a, ws, chunk_start, N, s);
+  if (a.max_D <= 128) return launch_bwd<I, WT, 16, 2>(a, ws, chunk_start, N, s);
+  if (a.max_D <= 256) return launch_bwd<I, WT, 32, 2>(a, ws, chunk_start, N, s);
+  if (a.max_D <= 512) return launch_bwd<I, WT, 64, 2>(a, ws, chunk_start, N, s);
+  return launch_bwd<I, WT, 64, 4>(a, ws, chunk_start, N, s);
 }
 
 struct BwdWs {
@@ -1204,12 +1252,6 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
                              total_hash_size_bits, nb, indices, offsets, index_bytes, N,
                              indice_weights, o, w.sort, s))
     return rc;
-  // Chunk layout of long runs.
-  if (int rc = prefix_scan_epi(
-          ChunkCount{w.cum}, N, reinterpret_cast<const int32_t*>(&w.sort.counters[0]),
-          ChunkEpi{w.cum, w.chunk_start, w.sort.chunk_mark, &w.sort.counters[1]},
-          scan_slot(w.sort, 1), s))
-    return rc;
   BwdArgs a;
   a.W = weights;
   a.w_off = weights_offsets;
@@ -1243,10 +1285,10 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   a.sr = stochastic_rounding != 0 ? 1 : 0;
   a.seed = seed;
   if (weights_ty == MX_SPARSE_FP16)
-    return index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, N, s)
-                            : dispatch_bwd<int32_t, __half>(a, N, s);
-  return index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, N, s)
-                          : dispatch_bwd<int32_t, float>(a, N, s);
+    return index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, w.sort, w.chunk_start, N, s)
+                            : dispatch_bwd<int32_t, __half>(a, w.sort, w.chunk_start, N, s);
+  return index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, w.sort, w.chunk_start, N, s)
+                          : dispatch_bwd<int32_t, float>(a, w.sort, w.chunk_start, N, s);
 }
 
 }  // namespace

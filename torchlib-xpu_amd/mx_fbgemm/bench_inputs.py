@@ -100,6 +100,30 @@ def config2(T: int = 8, E: int = 1_000_000, D: int = 128, B: int = 4096, max_L: 
     return TbeInput(T=T, E=[E] * T, D=[D] * T, B=B, indices=idx, offsets=off)
 
 
+def config2_batches(k: int, T: int = 8, E: int = 1_000_000, D: int = 128, B: int = 4096,
+                    max_L: int = 40, zipf_a: float = 1.05, seed: int = 0) -> list[TbeInput]:
+    """k config-2 batches of one model: batch 0 is ``config2(seed=seed)``; the
+    others keep its per-table row permutations (the same rows are hot) and
+    draw fresh bag lengths and Zipf ranks, as successive training batches do."""
+    rng = rng_for(2, seed)
+    lengths = rng.integers(1, max_L + 1, size=T * B)
+    off = offsets_from_lengths(lengths)
+    perms = []
+    for t in range(T):  # replays config2's stream to recover its permutations
+        perms.append(rng.permutation(E))
+        bounded_zipf(rng, E, zipf_a, int(off[(t + 1) * B] - off[t * B]))
+    out = [config2(T, E, D, B, max_L, zipf_a, seed)]
+    for j in range(1, k):
+        r = rng_for(2, seed, stream=j)
+        off = offsets_from_lengths(r.integers(1, max_L + 1, size=T * B))
+        idx = np.empty(int(off[-1]), dtype=np.int64)
+        for t in range(T):
+            s, e = int(off[t * B]), int(off[(t + 1) * B])
+            idx[s:e] = perms[t][bounded_zipf(r, E, zipf_a, e - s)]
+        out.append(TbeInput(T=T, E=[E] * T, D=[D] * T, B=B, indices=idx, offsets=off))
+    return out
+
+
 @dataclass
 class NbitInput(TbeInput):
     tys: list[int]  # SparseType ints per table
