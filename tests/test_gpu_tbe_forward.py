@@ -160,3 +160,31 @@ def test_unserved_arguments_raise(dev):
         op(W, empty, torch.zeros(3, 8, device=dev), pl, w_off, D_off, 16, 8, idx, off, 0, e32,
            empty, 0, False)
     op(W, empty, empty, pl, w_off, D_off, 16, 8, idx, off, 0, e32, empty, 0, False)
+
+
+def test_metadata_arguments_checked(dev):
+    """The small arrays the kernels read by pointer must be dense and on the
+    weights' device: a strided view or a host tensor raises instead of being
+    misread; strided indices are copied and served."""
+    print("[case] tbe fwd metadata argument checks", flush=True)
+    rng = np.random.default_rng(4)
+    inp = random_tbe(rng, 2, 4, [8, 8], [5, 5], 3)
+    W = torch.from_numpy(rng.uniform(-1, 1, 80).astype(np.float32)).to(dev)
+    w_off = torch.from_numpy(weight_offsets(inp)).to(dev)
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(2, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda
+    strided = torch.stack([D_off, D_off], 1)[:, 0]
+    assert not strided.is_contiguous()
+    with pytest.raises(RuntimeError, match="D_offsets must be contiguous"):
+        op(W, empty, empty, pl, w_off, strided, 16, 8, idx, off, 0, e32, empty, 0, False)
+    with pytest.raises(RuntimeError, match="weights_offsets must be a GPU"):
+        op(W, empty, empty, pl, w_off.cpu(), D_off, 16, 8, idx, off, 0, e32, empty, 0, False)
+    ref = op(W, empty, empty, pl, w_off, D_off, 16, 8, idx, off, 0, e32, empty, 0, False)
+    idx_strided = torch.stack([idx, idx], 1)[:, 1]
+    got = op(W, empty, empty, pl, w_off, D_off, 16, 8, idx_strided, off, 0, e32, empty, 0, False)
+    assert torch.equal(got, ref)

@@ -49,6 +49,16 @@ void check_same_device(const Tensor& a, const Tensor& b, const char* name) {
   TORCH_CHECK(a.device() == b.device(), name, " is on ", b.device(), " but expected ", a.device());
 }
 
+// An argument the kernels read or write by pointer: on `like`'s device and,
+// for the small metadata arrays (`dense`), contiguous -- a strided view would
+// be read as if it were dense.  Indices, offsets and gradients are made
+// contiguous by the callers instead.
+void check_arg(const Tensor& t, const Tensor& like, const char* name, bool dense) {
+  check_gpu(t, name);
+  check_same_device(like, t, name);
+  TORCH_CHECK(!dense || t.is_contiguous(), name, " must be contiguous");
+}
+
 int32_t index_bytes_of(const Tensor& t, const char* name) {
   TORCH_CHECK(t.scalar_type() == at::kLong || t.scalar_type() == at::kInt, name,
               " must be int32 or int64, got ", t.scalar_type());
@@ -365,7 +375,10 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
                    const VbeMeta& vbe = VbeMeta()) {
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
-  for (auto* t : {&weights_offsets, &D_offsets, &indices, &offsets}) check_gpu(*t, "TBE argument");
+  check_arg(weights_offsets, dev_weights, "weights_offsets", true);
+  check_arg(D_offsets, dev_weights, "D_offsets", true);
+  check_arg(indices, dev_weights, "indices", false);
+  check_arg(offsets, dev_weights, "offsets", false);
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
   (void)weights_placements;  // validated once by the module; avoided here (host sync)
   const int32_t wty = weights_ty_of(dev_weights);
@@ -466,9 +479,10 @@ std::tuple<Tensor, Tensor> generate_vbe_metadata(
     const Tensor& output_offsets_feature_rank, const Tensor& D_offsets, int64_t D, bool nobag,
     c10::SymInt max_B_feature_rank, int64_t info_B_num_bits, c10::SymInt total_B_sym) {
   (void)max_B_feature_rank;
+  check_gpu(B_offsets, "B_offsets");
   for (auto* t : {&B_offsets, &B_offsets_rank_per_feature, &output_offsets_feature_rank,
                   &D_offsets})
-    check_gpu(*t, "generate_vbe_metadata argument");
+    check_arg(*t, B_offsets, "generate_vbe_metadata argument", true);
   c10::OptionalDeviceGuard guard(B_offsets.device());
   TORCH_CHECK(B_offsets.scalar_type() == at::kInt && B_offsets_rank_per_feature.scalar_type() ==
                   at::kInt && D_offsets.scalar_type() == at::kInt,
@@ -559,8 +573,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   const bool vbe = vbe_b_t_map.has_value() && vbe_b_t_map->defined();
   check_gpu(indices, "indices");
   c10::OptionalDeviceGuard guard(indices.device());
-  check_gpu(hash_size_cumsum, "hash_size_cumsum");
-  check_gpu(offsets, "offsets");
+  check_arg(hash_size_cumsum, indices, "hash_size_cumsum", true);
+  check_arg(offsets, indices, "offsets", false);
   TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
@@ -624,9 +638,11 @@ Tensor backward_rowwise_adagrad_impl(
   (void)momentum1_placements;
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
-  for (auto* t : {&grad_output, &weights_offsets, &D_offsets, &hash_size_cumsum, &indices,
-                  &offsets, &momentum1_dev, &momentum1_offsets})
-    check_gpu(*t, "TBE backward argument");
+  for (auto* t : {&grad_output, &indices, &offsets})
+    check_arg(*t, dev_weights, "TBE backward argument", false);
+  for (auto* t : {&weights_offsets, &D_offsets, &hash_size_cumsum, &momentum1_dev,
+                  &momentum1_offsets})
+    check_arg(*t, dev_weights, "TBE backward argument", true);
   TORCH_CHECK(uvm_weights.numel() == 0 && momentum1_uvm.numel() == 0,
               "UVM storage is not supported (DEVICE placement only)");
   TORCH_CHECK(max_norm == 0.0, "max_norm is not supported");
@@ -827,8 +843,10 @@ Tensor grad_indice_weights_impl(const Tensor& grad_output, const Tensor& dev_wei
   (void)lxu_cache_locations;
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
-  for (auto* t : {&grad_output, &weights_offsets, &D_offsets, &indices, &offsets})
-    check_gpu(*t, "grad_indice_weights argument");
+  for (auto* t : {&grad_output, &indices, &offsets})
+    check_arg(*t, dev_weights, "grad_indice_weights argument", false);
+  for (auto* t : {&weights_offsets, &D_offsets})
+    check_arg(*t, dev_weights, "grad_indice_weights argument", true);
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM storage is not supported (DEVICE placement only)");
   const int32_t wty = weights_ty_of(dev_weights);
   TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
@@ -1085,9 +1103,9 @@ void bounds_check_indices(const Tensor& rows_per_table, const Tensor& indices,
   (void)bounds_check_version;
   check_gpu(indices, "indices");
   c10::OptionalDeviceGuard guard(indices.device());
-  check_gpu(offsets, "offsets");
-  check_gpu(rows_per_table, "rows_per_table");
-  check_gpu(warning, "warning");
+  check_arg(offsets, indices, "offsets", false);
+  check_arg(rows_per_table, indices, "rows_per_table", true);
+  check_arg(warning, indices, "warning", true);
   TORCH_CHECK(bounds_check_mode >= MX_BOUNDS_FATAL && bounds_check_mode <= MX_BOUNDS_NONE,
               "bounds_check_mode must be FATAL(0), WARNING(1), IGNORE(2) or NONE(3)");
   TORCH_CHECK(rows_per_table.scalar_type() == at::kLong, "rows_per_table must be int64");
@@ -1262,8 +1280,9 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   (void)fp8_exponent_bias;
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
-  for (auto* t : {&weights_offsets, &weights_tys, &D_offsets, &indices, &offsets})
-    check_gpu(*t, "nbit argument");
+  for (auto* t : {&indices, &offsets}) check_arg(*t, dev_weights, "nbit argument", false);
+  for (auto* t : {&weights_offsets, &weights_tys, &D_offsets})
+    check_arg(*t, dev_weights, "nbit argument", true);
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
   TORCH_CHECK(max_float8_D.value_or(0) == 0, "FP8 tables are not supported");
   TORCH_CHECK(dev_weights.scalar_type() == at::kByte && dev_weights.is_contiguous(),
