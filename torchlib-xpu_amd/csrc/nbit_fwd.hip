@@ -14,10 +14,13 @@
 // [k*CPL, (k+1)*CPL) with CPL = D/G.  A lane reads its CPL codes with one
 // wide load (INT8 D=128: 16 B), the row's qparams with one dword load, and
 // dequantizes in registers as acc += scale*q, keeping sum(bias) apart, so
-// each code costs one convert and one FMA and no cross-lane reduction is
-// needed.  The G indices of a batch are fetched with one coalesced load by
+// each code costs one byte-selecting convert (plus a mask per word of INT4 or
+// INT2 codes) and one FMA, an fp16 element one mixed-precision FMA, and no
+// cross-lane reduction is needed.  The G indices of a batch are fetched with one coalesced load by
 // the group and handed out with ds_bpermute.  Tables of every type share the
 // launch; the type/width switch is wave-uniform.
+#include <type_traits>
+
 #include "mx_common.h"
 
 // Bytes of row data each lane keeps in flight (sets the rows loaded before
@@ -135,6 +138,62 @@ __device__ __forceinline__ float elem(const uint32_t (&w)[BPL >= 4 ? BPL / 4 : 1
   }
 }
 
+// fp32 of byte N of x: v_cvt_f32_ubyteN selects the byte itself, so a code
+// costs one instruction (the compiler emits a bit-field extract and
+// v_cvt_f32_ubyte0 for the shift-and-mask form).
+template <int N>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) {
+  float f;
+  if constexpr (N == 0)
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(x));
+  else if constexpr (N == 1)
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(x));
+  else if constexpr (N == 2)
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(x));
+  else
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(x));
+  return f;
+}
+
+// The 32/bits codes of one little-endian word as fp32, in element order: for
+// INT4 the low and high nibbles of each byte are masked into two words
+// (0x0F0F0F0F), for INT2 the four 2-bit fields into four, and each byte is
+// then converted directly.  Exact: every code is a small integer.
+template <int BITS>
+__device__ __forceinline__ void decode_word(uint32_t w, float (&f)[32 / BITS]) {
+  if constexpr (BITS == 8) {
+    f[0] = ubyte_f32<0>(w);
+    f[1] = ubyte_f32<1>(w);
+    f[2] = ubyte_f32<2>(w);
+    f[3] = ubyte_f32<3>(w);
+  } else {
+    constexpr int K = 8 / BITS;  // codes per byte
+    constexpr uint32_t m = BITS == 4 ? 0x0F0F0F0Fu : 0x03030303u;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const uint32_t p = (w >> (j * BITS)) & m;  // field j of every byte
+      f[0 * K + j] = ubyte_f32<0>(p);
+      f[1 * K + j] = ubyte_f32<1>(p);
+      f[2 * K + j] = ubyte_f32<2>(p);
+      f[3 * K + j] = ubyte_f32<3>(p);
+    }
+  }
+}
+
+// acc + m * (fp16 half H of w), one v_fma_mix_f32 (the half converts inside
+// the FMA, rounded once as fma(float(h), m, acc)).
+template <int H>
+__device__ __forceinline__ float fma_half(uint32_t w, float m, float acc) {
+  float r;
+  if constexpr (H == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(m), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(r)
+        : "v"(w), "v"(m), "v"(acc));
+  return r;
+}
+
 template <typename I>
 __device__ __forceinline__ int64_t idx_at(const void* p, int64_t i) {
   return static_cast<int64_t>(reinterpret_cast<const I*>(p)[i]);
@@ -169,25 +228,31 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   float bsum = 0.0f;
   const bool weighted = a.iw != nullptr;
 
+  // Row numbers travel between lanes as one 32-bit word when the indices are
+  // int32 (one ds_bpermute and one 32x32->64 multiply-add per row); a row is
+  // under 2^32 bytes.
+  using R = std::conditional_t<sizeof(I) == 4, uint32_t, int64_t>;
+  const uint32_t stride32 = static_cast<uint32_t>(stride);
   for (int64_t base = start; base < end; base += G) {
     const int n = static_cast<int>(end - base < G ? end - base : G);
-    const int64_t my_idx = k < n ? idx_at<I>(a.idx, base + k) : 0;
+    const R my_idx = k < n ? static_cast<R>(reinterpret_cast<const I*>(a.idx)[base + k]) : R(0);
     const float my_w = (weighted && k < n) ? a.iw[base + k] : 1.0f;
     for (int j = 0; j < n; j += U) {
       uint32_t codes[U][NW];
       uint32_t qp[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t r = __shfl(my_idx, g * G + ((j + u) < n ? (j + u) : 0), 64);
+        // Lanes past the batch (j + u >= n) hold row 0 and go unused.
+        const R r = __shfl(my_idx, g * G + j + u, 64);
         if (j + u < n) {
-          const uint8_t* row = Wt + r * stride;
+          const uint8_t* row = Wt + static_cast<uint64_t>(r) * stride32;
           load_codes<BPL>(row + lane_off, codes[u]);
           if constexpr (Q) qp[u] = *reinterpret_cast<const uint32_t*>(row);
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float wgt = __shfl(my_w, g * G + ((j + u) < n ? (j + u) : 0), 64);
+        const float wgt = __shfl(my_w, g * G + j + u, 64);
         if (j + u < n) {
           if constexpr (Q) {
             float scale = __half2float(__ushort_as_half(static_cast<uint16_t>(qp[u] & 0xffffu)));
@@ -197,9 +262,24 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
               bias *= wgt;
             }
             bsum += bias;
+            constexpr int EPW = 32 / BITS;  // codes per word
 #pragma unroll
-            for (int e = 0; e < CPL; ++e)
-              acc[e] = __builtin_fmaf(scale, elem<TY, BPL>(codes[u], e), acc[e]);
+            for (int q = 0; q < NW; ++q) {
+              float f[EPW];
+              decode_word<BITS>(codes[u][q], f);
+#pragma unroll
+              for (int j = 0; j < EPW; ++j)
+                if (q * EPW + j < CPL) acc[q * EPW + j] = __builtin_fmaf(scale, f[j], acc[q * EPW + j]);
+            }
+          } else if constexpr (TY == MX_SPARSE_FP16) {
+            // acc += w * h with the fp16 converted inside the FMA (w = 1
+            // unweighted: exactly acc + float(h)).
+            const float m = weighted ? wgt : 1.0f;
+#pragma unroll
+            for (int e = 0; e < CPL; e += 2) {
+              acc[e] = fma_half<0>(codes[u][e / 2], m, acc[e]);
+              if (e + 1 < CPL) acc[e + 1] = fma_half<1>(codes[u][e / 2], m, acc[e + 1]);
+            }
           } else {
             if (weighted) {
 #pragma unroll
@@ -332,7 +412,7 @@ __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
 // paths (fewer registers, higher occupancy); waves whose table has another
 // type return at once.
 template <typename I, int G, int MAXCPL, int TY>
-__global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
+__device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   constexpr int P = 64 / G;  // bags per wave
   // Hardware block order (round-robin over the XCDs): tables of different
   // types interleave on every XCD, so no XCD is left with only the slow ones.
@@ -362,6 +442,20 @@ __global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
   dispatch_cpl<I, G, MAXCPL, TY>(a, D, Wt, stride, start, end, out_col, g, k);
 }
 
+template <typename I, int G, int MAXCPL, int TY>
+__global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
+  nbit_fwd_body<I, G, MAXCPL, TY>(a);
+}
+
+// INT4 tables: the same body held to 96 registers for 5 waves per SIMD
+// (config 5's INT4 launch: 684 against 734 us at 4 waves; the other types
+// either fit already or would spill).
+template <typename I, int G, int MAXCPL, int TY>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
+    nbit_fwd_kernel_w5(NbitArgs a) {
+  nbit_fwd_body<I, G, MAXCPL, TY>(a);
+}
+
 template <int G, int MAXCPL, int TY>
 int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
   constexpr int P = 64 / G;
@@ -369,10 +463,18 @@ int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
   a.nwaves = static_cast<int64_t>(a.T) * (a.Bp / P);
   const int64_t grid = ceil_div(a.nwaves, 4);
   MX_REQUIRE(grid <= 0x7fffffffll, "too many bags");
-  if (index_bytes == 8)
-    nbit_fwd_kernel<int64_t, G, MAXCPL, TY><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
-  else
-    nbit_fwd_kernel<int32_t, G, MAXCPL, TY><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(a);
+  const dim3 gd(static_cast<uint32_t>(grid));
+  if constexpr (TY == MX_SPARSE_INT4) {
+    if (index_bytes == 8)
+      nbit_fwd_kernel_w5<int64_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+    else
+      nbit_fwd_kernel_w5<int32_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+  } else {
+    if (index_bytes == 8)
+      nbit_fwd_kernel<int64_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+    else
+      nbit_fwd_kernel<int32_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+  }
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
