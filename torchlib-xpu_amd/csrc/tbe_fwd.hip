@@ -126,12 +126,18 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[c][e] = 0.0f;
   bool active[NCH];
+  const WT* lane_col[NCH];  // this lane's first column of each chunk, row 0
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) active[c] = (c * G + k) * 4 < D;
+  for (int c = 0; c < NCH; ++c) {
+    active[c] = (c * G + k) * 4 < D;
+    lane_col[c] = Wt + (c * G + k) * 4;
+  }
 
   for (int64_t base = start; base < end; base += G) {
     const int n = static_cast<int>(end - base < G ? end - base : G);
-    const int64_t my_idx = k < n ? static_cast<int64_t>(indices[base + k]) : 0;
+    // The lane that loads an index also turns it into the row's element
+    // offset, once, instead of every lane of the group per row.
+    const int64_t my_off = k < n ? static_cast<int64_t>(indices[base + k]) * D : 0;
     float my_w = 0.0f;
     if constexpr (WEIGHTED) my_w = k < n ? iw[base + k] : 0.0f;
     for (int j = 0; j < n; j += U) {
@@ -139,11 +145,10 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (j + u < n) {
-          const int64_t r = __shfl(my_idx, g * G + j + u, 64);
-          const WT* row = Wt + r * D;
+          const int64_t off = __shfl(my_off, g * G + j + u, 64);
 #pragma unroll
           for (int c = 0; c < NCH; ++c)
-            if (active[c]) load_row4(row + (c * G + k) * 4, v[u][c]);
+            if (active[c]) load_row4(lane_col[c] + off, v[u][c]);
         }
       }
 #pragma unroll
