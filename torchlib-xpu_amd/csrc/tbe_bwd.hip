@@ -1089,12 +1089,12 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
   const int rc_short = launch_short_runs<I, WT, G, NCH>(a, N, s);
   if (side != s) {
     if (hipEventRecord(join, side) != hipSuccess || hipStreamWaitEvent(s, join, 0) != hipSuccess) {
-      hipStreamSynchronize(side);  // nothing may outlive the call unordered
+      (void)hipStreamSynchronize(side);  // nothing may outlive the call unordered
       if (rc == MX_OK) rc = set_error(MX_EHIP, "joining the long-run stream failed");
     }
   }
-  if (fork) hipEventDestroy(fork);
-  if (join) hipEventDestroy(join);
+  if (fork) (void)hipEventDestroy(fork);
+  if (join) (void)hipEventDestroy(join);
   return rc != MX_OK ? rc : rc_short;
 }
 
