@@ -222,6 +222,11 @@ def bench_tbe_forward(args, dev):
         return op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, bi, bo, 0, e32, empty, 0,
                   False)
 
+    # Compulsory bytes: every distinct row once (the Zipf heads repeat).
+    t_of = np.repeat(np.arange(T * B) // B, np.diff(inp.offsets))
+    uniq = int(np.unique(t_of * E + inp.indices).size)
+    compulsory = uniq * D * 4 + N * 8 + (T * B + 1) * 8 + T * B * D * 4
+
     fresh_steps = 8 * max(1, args.steps // 8)
     _, fresh_ms = time_launches(fresh_step, fresh_steps, len(batches))
     fresh_n = sum(b[2] for b in batches) / len(batches)
@@ -241,6 +246,7 @@ def bench_tbe_forward(args, dev):
         cold_kernel_ms_median=statistics.median(cold),
         fresh_batches=dict(batches=len(batches), launch_ms_mean=fresh_ms,
                            lookups_per_s=fresh_n / (fresh_ms * 1e-3)),
+        compulsory_bytes=compulsory, unique_rows=uniq,
     )
     traffic = traffic_from_profile("tbe_fwd_config2")
 
@@ -374,6 +380,12 @@ def bench_nbit(args, dev, config: int):
     lens = np.diff(inp.offsets).reshape(inp.T, inp.B).sum(1)
     alg_bytes = int(sum(int(lens[t]) * (unpadded[t] + 4) for t in range(inp.T))
                     + inp.B * sum(4 + 2 * D for D in inp.D))
+    # Compulsory bytes: every distinct row once, plus indices, offsets and output.
+    uniq = [int(np.count_nonzero(np.bincount(
+        inp.indices[inp.offsets[t * inp.B]: inp.offsets[(t + 1) * inp.B]], minlength=inp.E[t])))
+        for t in range(inp.T)]
+    compulsory = int(sum(u * r for u, r in zip(uniq, unpadded)) + N * 4
+                     + inp.B * sum(4 + 2 * D for D in inp.D))
     res = dict(
         metric="nbit TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
         value=N * args.steps / wall, unit="lookups/s", ms_per_step=wall / args.steps * 1e3,
@@ -384,6 +396,7 @@ def bench_nbit(args, dev, config: int):
             if config == 4 else "mixed nbit SUM fp16 out, 64 tables FP16/INT4 D 32..256 "
             "B=65536 L~Poisson(15) 10% empty Zipf(1.1)")), "T": inp.T, "B": inp.B, "N": N},
         kernel="nbit_fwd_kernel", alg_bytes=alg_bytes, kernel_ms_mean=mean_ms,
+        compulsory_bytes=compulsory, unique_rows=int(sum(uniq)),
     )
     cpu = None
     if not args.no_cpu_baseline:
@@ -543,6 +556,13 @@ def main():
         line["roofline"]["cold_launch_ms_median"] = res["cold_kernel_ms_median"]
     if "fresh_batches" in res:
         line["roofline"]["fresh_batches"] = res["fresh_batches"]
+    if "compulsory_bytes" in res:
+        # The same launch against only the bytes no cache can serve: each
+        # distinct row once, plus indices, offsets and output.
+        comp = res["compulsory_bytes"] / (res["kernel_ms_mean"] * 1e-3) / 1e9
+        line["roofline"].update(compulsory_bytes=res["compulsory_bytes"],
+                                unique_rows=res["unique_rows"], compulsory_GBps=comp,
+                                compulsory_frac=comp / PEAK_HBM_GBS)
     print(json.dumps(line), flush=True)
 
 
