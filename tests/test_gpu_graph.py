@@ -76,3 +76,48 @@ def test_training_step_graph_replays_match_eager(dev):
         assert torch.equal(ms, m_e), f"replay {k}: momentum differs"
         assert torch.equal(Ws, W_e), f"replay {k}: weights differ"
         assert not torch.equal(Ws, W0)
+
+
+def test_backward_on_two_streams_from_two_threads(dev):
+    """Two host threads run training steps on their own streams at once; both
+    fork their long-run path onto the device's one second stream.  Each
+    thread's tables end bit-identical to the same steps run one after the
+    other."""
+    import threading
+
+    print("[case] concurrent backward on two streams", flush=True)
+    rng = np.random.default_rng(9)
+    inp = random_tbe(rng, 3, 256, [32, 64, 128], [500, 2000, 3], 30)
+    nW = sum(E * D for E, D in zip(inp.E, inp.D))
+    W0 = torch.from_numpy(rng.uniform(-0.01, 0.01, nW).astype(np.float32)).to(dev)
+    grads = [torch.from_numpy(rng.normal(0, 1e-2, (inp.B, inp.total_D)).astype(np.float32)).to(dev)
+             for _ in range(3)]
+
+    def run(stream, W, m, g_buf, out):
+        with torch.cuda.stream(stream):
+            step = _step_fn(dev, inp, W, m, g_buf)
+            for g in grads:
+                g_buf.copy_(g)
+                step()
+        stream.synchronize()
+        out.append(True)
+
+    ref_W, ref_m = W0.clone(), torch.zeros(sum(inp.E), device=dev)
+    run(torch.cuda.current_stream(), ref_W, ref_m, torch.empty_like(grads[0]), [])
+    torch.cuda.synchronize()
+
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    state = [(W0.clone(), torch.zeros(sum(inp.E), device=dev), torch.empty_like(grads[0]))
+             for _ in streams]
+    torch.cuda.synchronize()
+    done = []
+    threads = [threading.Thread(target=run, args=(st, *state[i], done))
+               for i, st in enumerate(streams)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert len(done) == 2
+    torch.cuda.synchronize()
+    for W, m, _ in state:
+        assert torch.equal(W, ref_W) and torch.equal(m, ref_m)
