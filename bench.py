@@ -6,17 +6,32 @@ E=1,000,000 x D=128, B=4096 bags per table, pooling factor U{1..40}, int64
 indices Zipf(1.05) with a per-table permutation (seeded synthetic data; the
 weights are generated on the device).  One step = one
 torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda call over
-the batch, inputs resident in HBM.
+one batch, inputs resident in HBM; the timed steps walk a rotation of 8
+batches of the same tables (the same hot rows, fresh draws), as successive
+training batches do.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config {1,2,3,4,5}]
-                    [--op {lookup,bounds-check}]
+                    [--op {lookup,bounds-check}] [--regime {all,steps,warm,cold}]
 
-Prints one JSON line: lookups/s (whole job), the roofline of the dominant
-kernel (algorithmic bytes per launch / HIP-event-timed launch duration vs
-8 TB/s) and the CPU baseline (FBGEMM's CPU kernel on this host's cores).
---config 1/3/4/5 print the same line for the jagged round trip, the backward,
-the nbit lookup and the mixed nbit workload; --op bounds-check times
-bounds_check_indices over the config-2 batch.
+Prints one JSON line.  `value` is lookups/s over the K timed steps.  The
+roofline of the dominant kernel is taken from COLD-cache launches: before
+each of `--cold-launches` launches of batch 0 a 1 GiB buffer is written and read
+(well past the 256 MB Infinity Cache and the L2s), one pair of HIP events
+brackets the launch on the stream it runs on, and `achieved` = the bytes the
+launch must move from HBM / median launch time, so it is an HBM figure: the
+algorithmic bytes (per-unit figure x units), except for Zipf batches (configs
+2 and 5), whose per-lookup count re-reads the hot rows that the L2 serves
+within a launch even from cold; there it is the compulsory bytes (each
+distinct row once + indices, offsets, output).  The per-lookup rate, repeated
+launches of one batch ("warm") and the rotation ("steps") are reported as
+effective rates: caches serve part of them, so they are no HBM bandwidth.  The CPU
+baseline is FBGEMM's CPU kernel (or the C restatement) on this host's cores.
+The default run also carries a `config4` record (nbit INT8/INT4 lookup) with
+its own roofline and CPU baseline.
+
+--regime runs one regime only (for profiling: every launch of the kernel in
+the process then belongs to it): `steps` the rotation, `warm` batch 0
+repeated, `cold` flushed launches of batch 0.
 """
 
 from __future__ import annotations
@@ -28,12 +43,15 @@ import re
 import statistics
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable, Optional
 
 REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO / "torchlib-xpu_amd"))
 
 PEAK_HBM_GBS = 8000.0
+FLUSH_BYTES = 1 << 30
 
 
 def log(msg: str) -> None:
@@ -43,55 +61,115 @@ def log(msg: str) -> None:
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="workload; 2 (default) is the headline")
     ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check"],
                     help="config 2 only: time bounds_check_indices (WARNING) on the batch "
                          "instead of the lookup")
+    ap.add_argument("--regime", default="all", choices=["all", "steps", "warm", "cold"])
+    ap.add_argument("--cold-launches", type=int, default=24,
+                    help="flushed launches whose median gives the roofline")
+    ap.add_argument("--no-config4", action="store_true",
+                    help="config 2 only: leave out the config-4 record")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="bound on the CPU baseline's timed work")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound on each CPU baseline's timed work")
     return ap.parse_args()
 
 
-def traffic_from_profile(name: str):
-    """HBM bytes per launch recorded by the rocprofv3 PMC summary, if present."""
-    p = REPO / "profiles" / f"{name}.md"
-    if not p.exists():
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", p.read_text())
-    return float(m.group(1)) if m else None
+# ---------------------------------------------------------------------------
+# provenance and committed profile figures
 
 
-def time_launches(fn, steps: int, warmup: int):
-    """Runs `warmup` untimed steps, then times exactly `steps` steps back to
-    back, synchronised on both sides.  Returns (wall seconds, mean step
-    duration in ms from one pair of HIP events recorded around the steps on
-    the current stream -- the stream the ops launch on).  No event sits
-    between steps: an event record between launches costs ~7 us of GPU time
-    per step here, which is not part of the op."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def provenance() -> dict:
     import torch
 
-    for _ in range(warmup):
-        fn()
+    return dict(torch_version=torch.__version__, torch_git=torch.version.git_version,
+                hip=torch.version.hip, host_cpu=cpu_model(), host_nproc=os.cpu_count(),
+                host_affinity=len(os.sched_getaffinity(0)))
+
+
+def traffic_from_profile(name: str) -> tuple[Optional[float], Optional[str]]:
+    """HBM bytes per cold launch recorded by the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs of `bench.py --regime cold`)."""
+    p = REPO / "profiles" / f"{name}.md"
+    if not p.exists():
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch_cold:\s*([0-9.eE+]+)", p.read_text())
+    if not m:
+        return None, None
+    return float(m.group(1)), (f"profiles/{name}.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                               f"runs of bench.py --regime cold, calibrated by a 1 GiB copy")
+
+
+# ---------------------------------------------------------------------------
+# timing
+
+
+def time_steps(fns: list[Callable], steps: int, warmup: int):
+    """Calls fns[i % len(fns)] for `warmup` untimed steps, then times exactly
+    `steps` steps back to back, synchronised on both sides.  Returns (wall
+    seconds, mean step in ms from one pair of HIP events around the steps on
+    the current stream, which the ops launch on).  No event sits between
+    steps: an event record between launches adds GPU time that is not the
+    op's."""
+    import torch
+
+    for i in range(warmup):
+        fns[i % len(fns)]()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fns[i % len(fns)]()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall, start.elapsed_time(end) / steps
 
 
+def time_cold(fn: Callable, launches: int, warmup: int, dev) -> list[float]:
+    """Each launch follows a write and then a read of a 1 GiB buffer: neither
+    the L2s nor the 256 MB Infinity Cache then hold any of the launch's inputs,
+    and the lines they do hold are clean (a write-only flush leaves dirty lines
+    whose write-back would land inside the timed launch).  One HIP event pair
+    per launch on the current stream.  Returns the `launches` durations in ms."""
+    import torch
+
+    flush = torch.empty(FLUSH_BYTES // 4, device=dev, dtype=torch.float32)
+    evs = []
+    for i in range(warmup + launches):
+        flush.fill_(float(i))
+        flush.sum()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        if i >= warmup:
+            evs.append((s, e))
+    torch.cuda.synchronize()
+    del flush
+    return [s.elapsed_time(e) for s, e in evs]
+
+
 def cpu_time(fn, budget_s: float, min_runs: int = 3, warm: int = 1):
+    """Median of at least `min_runs` (up to 10) runs within about `budget_s`."""
     for _ in range(warm):
         fn()
     times = []
@@ -105,20 +183,107 @@ def cpu_time(fn, budget_s: float, min_runs: int = 3, warm: int = 1):
     return statistics.median(times), len(times)
 
 
-def cpu_model() -> str:
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
-
-
 # ---------------------------------------------------------------------------
+# workloads
 
 
-def bench_jagged(args, dev):
+@dataclass
+class Workload:
+    metric: str
+    unit: str                       # what `value` counts per second
+    steps: list[Callable]           # one callable per batch of the rotation
+    units: list[float]              # the unit count of each batch (lookups, or bytes)
+    alg_bytes: list[float]          # algorithmic bytes of each batch
+    dtype: str
+    config: dict
+    kernel: str                     # the dominant kernel(s) one step launches
+    profile: str                    # profiles/<profile>.md
+    cpu: Optional[Callable] = None  # -> cpu_baseline dict
+    extra: dict = field(default_factory=dict)
+    # Bytes of batch 0 the roofline divides by the cold launch time, when not
+    # alg_bytes[0]: for Zipf batches, the compulsory bytes (each distinct row
+    # once, plus indices, offsets and output).  The per-lookup count re-reads
+    # the Zipf head, which the L2 serves within a launch even from cold, so it
+    # is no HBM quantity.
+    roof_bytes: Optional[float] = None
+    roof_bytes_kind: str = "algorithmic bytes per launch (per-unit figure x units)"
+
+
+def run_workload(args, wl: Workload, dev) -> dict:
+    """Times the regimes `args.regime` asks for; returns the bench record."""
+    regimes = ["steps", "warm", "cold"] if args.regime == "all" else [args.regime]
+    rec: dict = {}
+    eff: dict = {}
+    n_b = len(wl.steps)
+    if "steps" in regimes:
+        log(f"timing {args.steps} steps over {n_b} batch(es) in rotation")
+        wall, ev_ms = time_steps(wl.steps, args.steps, args.warmup)
+        units = sum(wl.units[i % n_b] for i in range(args.steps))
+        alg = sum(wl.alg_bytes[i % n_b] for i in range(args.steps)) / args.steps
+        rec.update(value=units / wall, ms_per_step=wall / args.steps * 1e3)
+        eff["steps"] = dict(batches=n_b, launch_ms_mean=ev_ms,
+                            effective_GBps=alg / (ev_ms * 1e-3) / 1e9,
+                            note="HIP events around the K timed steps (the batch rotation); "
+                                 "caches serve repeated rows, so not an HBM figure")
+    if "warm" in regimes:
+        log("timing batch 0 repeated (warm caches)")
+        _, warm_ms = time_steps(wl.steps[:1], args.steps, args.warmup)
+        eff["warm"] = dict(launch_ms_mean=warm_ms,
+                           effective_GBps=wl.alg_bytes[0] / (warm_ms * 1e-3) / 1e9,
+                           units_per_s=wl.units[0] / (warm_ms * 1e-3),
+                           note="batch 0 launched back to back: its distinct rows stay in the "
+                                "L2s and the Infinity Cache, so not an HBM figure")
+        if "value" not in rec:
+            rec.update(value=wl.units[0] / (warm_ms * 1e-3), ms_per_step=warm_ms)
+    roof = None
+    if "cold" in regimes:
+        log(f"timing {args.cold_launches} cold-cache launches of batch 0")
+        cold = time_cold(wl.steps[0], args.cold_launches, min(args.warmup, 3), dev)
+        med = statistics.median(cold)
+        nbytes = wl.roof_bytes if wl.roof_bytes is not None else wl.alg_bytes[0]
+        achieved = nbytes / (med * 1e-3) / 1e9
+        traffic, src = traffic_from_profile(wl.profile)
+        roof = dict(bound="hbm", achieved=achieved, peak=PEAK_HBM_GBS, unit="GB/s",
+                    frac=achieved / PEAK_HBM_GBS, traffic=traffic, traffic_source=src,
+                    kernel=wl.kernel, alg_bytes_per_launch=nbytes,
+                    alg_bytes_kind=wl.roof_bytes_kind,
+                    launch_ms=med, launch_ms_min=min(cold), launch_ms_max=max(cold),
+                    regime=(f"cold: median of {len(cold)} launches of batch 0, each after a "
+                            f"1 GiB buffer is written and read; one HIP event pair per "
+                            f"launch"))
+        if wl.roof_bytes is not None:
+            eff["cold_per_lookup_bytes"] = dict(
+                bytes=wl.alg_bytes[0], effective_GBps=wl.alg_bytes[0] / (med * 1e-3) / 1e9,
+                note="every lookup's row counted once per lookup, over the cold launch time: "
+                     "the Zipf head is re-read from the L2 within the launch, so this can pass "
+                     "the HBM peak and is not an HBM figure")
+        if "value" not in rec:
+            rec.update(value=wl.units[0] / (med * 1e-3), ms_per_step=med)
+    rec.update(roofline=roof, effective=eff)
+    rec.update(wl.extra)
+    return rec
+
+
+def make_line(args, wl: Workload, rec: dict, cpu) -> dict:
+    return dict(
+        metric=wl.metric, value=rec["value"], unit=wl.unit, n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=rec["ms_per_step"], higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype=wl.dtype, data="synthetic",
+        config=wl.config, roofline=rec["roofline"], effective=rec["effective"],
+        **{k: v for k, v in rec.items()
+           if k not in ("value", "ms_per_step", "roofline", "effective")},
+        cpu_baseline=cpu,
+    )
+
+
+def cpu_record(value, unit, cores, kind, sample) -> dict:
+    return dict(value=value, unit=unit, cores=cores, kind=kind, sample=sample, **provenance())
+
+
+# -- config 1 ----------------------------------------------------------------
+
+
+def wl_jagged(args, dev) -> Workload:
     """Config 1: jagged_to_padded_dense then dense_to_jagged (one round trip
     per step) on B=512 rows of up to 64 x 128 fp32."""
     import torch
@@ -136,19 +301,11 @@ def bench_jagged(args, dev):
         dense = j2pd(v, [off], [L], 0.0)
         return d2j(dense, [off], total)
 
-    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     # j2pd reads the values and writes the padded dense; d2j reads the dense at
     # the jagged positions and writes the values; both read the offsets.
     alg = total * D * 4 + B * L * D * 4 + 2 * total * D * 4 + 2 * (B + 1) * 8
-    res = dict(
-        metric="jagged round trip (jagged_to_padded_dense + dense_to_jagged) bytes/s, 1 MI355X",
-        value=alg * args.steps / wall / 1e9, unit="GB/s", ms_per_step=wall / args.steps * 1e3,
-        dtype="fp32",
-        config={"workload": "config1: jagged round trip, B=512 D=128 max_L=64, len~U{0..64}",
-                "B": B, "D": D, "max_L": L, "total_L": total},
-        kernel="j2pd_kernel + d2j_kernel (one step)", alg_bytes=alg, kernel_ms_mean=mean_ms)
-    cpu = None
-    if not args.no_cpu_baseline:
+
+    def cpu():
         vc, oc = v.cpu(), off.cpu()
 
         def cpu_step():
@@ -156,107 +313,97 @@ def bench_jagged(args, dev):
             return torch.ops.aten._padded_dense_to_jagged_forward(dense, [oc], total)
 
         med, runs = cpu_time(cpu_step, args.cpu_seconds)
-        cpu = dict(value=alg / med / 1e9, unit="GB/s", cores=torch.get_num_threads(),
-                   kind="reference",
-                   sample=(f"full config-1 round trip, median of {runs} runs; torch's CPU "
-                           f"aten._jagged_to_padded_dense_forward / _padded_dense_to_jagged_forward "
-                           f"(its port of the fbgemm jagged ops) on {torch.get_num_threads()} "
-                           f"threads; host CPU: {cpu_model()}"))
-    return res, traffic_from_profile("jagged_config1"), cpu
+        n = torch.get_num_threads()
+        return cpu_record(alg / med / 1e9, "GB/s", n, "reference",
+                          f"full config-1 round trip, median of {runs} runs; torch's CPU "
+                          f"aten._jagged_to_padded_dense_forward / _padded_dense_to_jagged_forward "
+                          f"(its port of the fbgemm jagged ops) on {n} threads")
+
+    return Workload(
+        metric="jagged round trip (jagged_to_padded_dense + dense_to_jagged) bytes/s, 1 MI355X",
+        unit="GB/s", steps=[step], units=[alg / 1e9], alg_bytes=[alg], dtype="fp32",
+        config={"workload": "config1: jagged round trip, B=512 D=128 max_L=64, len~U{0..64}",
+                "B": B, "D": D, "max_L": L, "total_L": total},
+        kernel="j2pd1_kernel + jagged_out1_kernel (one round trip)", profile="jagged_config1",
+        cpu=cpu)
 
 
-def bench_tbe_forward(args, dev):
+# -- config 2 ----------------------------------------------------------------
+
+
+def wl_tbe_forward(args, dev) -> Workload:
     import numpy as np
     import torch
 
     from mx_fbgemm import bench_inputs
 
-    log("generating config 2 indices")
-    inp = bench_inputs.config2()
+    log("generating 8 config-2 batches (batch 0 is the seed-0 config)")
+    batches = bench_inputs.config2_batches(8)
+    inp = batches[0]
     T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
     w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
     D_off = torch.from_numpy(inp.D_offsets).to(dev)
-    idx = torch.from_numpy(inp.indices).to(dev)
-    off = torch.from_numpy(inp.offsets).to(dev)
     empty = torch.zeros(0, device=dev)
     pl = torch.zeros(T, dtype=torch.int32, device=dev)
     e32 = torch.zeros(0, dtype=torch.int32, device=dev)
     op = torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda
 
-    def step():
-        return op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, idx, off, 0, e32, empty, 0,
-                  False)
+    def make_step(b):
+        idx = torch.from_numpy(b.indices).to(dev)
+        off = torch.from_numpy(b.offsets).to(dev)
+        return lambda: op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, idx, off, 0, e32,
+                          empty, 0, False)
 
-    log(f"timing N={inp.N} lookups, {args.steps} steps")
-    wall, mean_ms = time_launches(step, args.steps, args.warmup)
-    N = inp.N
-    alg_bytes = N * (D * 4 + 8) + T * B * (8 + D * 4)
-
-    # Cold cache: overwrite a 1 GiB buffer before each timed launch.
-    flush = torch.empty(1 << 28, device=dev, dtype=torch.float32)
-    cold = []
-    for _ in range(5):
-        flush.fill_(1.0)
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        step()
-        e.record()
-        torch.cuda.synchronize()
-        cold.append(s.elapsed_time(e))
-    del flush
-
-    # Successive batches of one model: 8 batches with the same hot rows and
-    # fresh draws, launched in rotation (each batch's tail rows are new to
-    # the caches, as in training); reported beside the repeated-batch figure.
-    log("generating 7 more config-2 batches of the same tables")
-    batches = [(torch.from_numpy(b.indices).to(dev), torch.from_numpy(b.offsets).to(dev), b.N)
-               for b in bench_inputs.config2_batches(8)]
-    turn = [0]
-
-    def fresh_step():
-        bi, bo, _ = batches[turn[0] % len(batches)]
-        turn[0] += 1
-        return op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, bi, bo, 0, e32, empty, 0,
-                  False)
-
-    # Compulsory bytes: every distinct row once (the Zipf heads repeat).
+    steps = [make_step(b) for b in batches]
+    # Per lookup: the row and its index; per bag: its offset and output row.
+    alg = [b.N * (D * 4 + 8) + T * B * (8 + D * 4) for b in batches]
+    # Compulsory bytes of batch 0: every distinct row once (the Zipf heads repeat).
     t_of = np.repeat(np.arange(T * B) // B, np.diff(inp.offsets))
     uniq = int(np.unique(t_of * E + inp.indices).size)
-    compulsory = uniq * D * 4 + N * 8 + (T * B + 1) * 8 + T * B * D * 4
+    compulsory = uniq * D * 4 + inp.N * 8 + (T * B + 1) * 8 + T * B * D * 4
 
-    fresh_steps = 8 * max(1, args.steps // 8)
-    _, fresh_ms = time_launches(fresh_step, fresh_steps, len(batches))
-    fresh_n = sum(b[2] for b in batches) / len(batches)
+    def cpu():
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
 
-    res = dict(
+        log("CPU baseline: copying weights to host")
+        Wh = W.cpu().numpy()
+        w_off_h = (np.arange(T) * E * D).astype(np.int64)
+        nthreads = orc.host_threads()
+        fn = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off_h, inp.D_offsets, inp.E, B,  # noqa: E731
+                                                inp.indices, inp.offsets, 0, nthreads=nthreads)
+        log(f"CPU baseline: FBGEMM SpMDM on {nthreads} threads")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        fn1 = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off_h, inp.D_offsets, inp.E, B,  # noqa: E731
+                                                 inp.indices, inp.offsets, 0, nthreads=1)
+        med1, runs1 = cpu_time(fn1, args.cpu_seconds / 3, min_runs=1, warm=0)
+        return cpu_record(
+            inp.N / med, "lookups/s", nthreads, "reference",
+            f"full config-2 batch 0 (N={inp.N} lookups), median of {runs} runs; FBGEMM "
+            f"GenerateEmbeddingSpMDMWithStrides<float,int64,int64,float> from the installed "
+            f"torch (the CPU kernel fbgemm_gpu's CPU TBE forward wraps), {nthreads} threads "
+            f"over (table, 256-bag chunks); 1 thread: {inp.N / med1:.4g} lookups/s ({runs1} runs)")
+
+    return Workload(
         metric="TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
-        value=N * args.steps / wall,
-        unit="lookups/s",
-        ms_per_step=wall / args.steps * 1e3,
+        unit="lookups/s", steps=steps, units=[b.N for b in batches], alg_bytes=alg,
         dtype="fp32",
         config={"workload": "config2: TBE fp32 forward SUM, T=8 E=1e6 D=128 B=4096 "
-                            "L~U{1..40} Zipf(1.05) int64 indices",
-                "T": T, "E": E, "D": D, "B": B, "N": N, "indices": "int64"},
-        kernel="tbe_fwd_group_kernel",
-        alg_bytes=alg_bytes,
-        kernel_ms_mean=mean_ms,
-        cold_kernel_ms_median=statistics.median(cold),
-        fresh_batches=dict(batches=len(batches), launch_ms_mean=fresh_ms,
-                           lookups_per_s=fresh_n / (fresh_ms * 1e-3)),
-        compulsory_bytes=compulsory, unique_rows=uniq,
-    )
-    traffic = traffic_from_profile("tbe_fwd_config2")
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline_tbe(args, inp, W)
-    return res, traffic, cpu
+                            "L~U{1..40} Zipf(1.05) int64 indices; timed steps rotate over 8 "
+                            "batches of the same tables (same hot rows, fresh draws)",
+                "T": T, "E": E, "D": D, "B": B, "N_batch0": inp.N,
+                "N_mean": sum(b.N for b in batches) / len(batches), "indices": "int64"},
+        kernel="tbe_fwd_group_kernel", profile="tbe_fwd_config2", cpu=cpu,
+        roof_bytes=compulsory,
+        roof_bytes_kind=("compulsory bytes of batch 0: its distinct rows once (D*4 each) + "
+                         "indices (8 B) + offsets (8 B per bag) + output (D*4 per bag)"),
+        extra=dict(compulsory=dict(bytes=compulsory, unique_rows=uniq)))
 
 
-def bench_bounds_check(args, dev):
+def wl_bounds_check(args, dev) -> Workload:
     """bounds_check_indices (WARNING) over the config-2 batch: every offset and
     index is read and checked; the batch is valid, so nothing is rewritten."""
     import numpy as np
@@ -275,60 +422,100 @@ def bench_bounds_check(args, dev):
     def step():
         op(rows, idx, off, 1, warn)
 
-    wall, mean_ms = time_launches(step, args.steps, args.warmup)
-    assert int(warn.item()) == 0, "the config-2 batch is valid"
-    alg = inp.N * 8 + (inp.T * inp.B + 1) * 8
-    res = dict(
-        metric="bounds_check_indices lookups/sec, 1 MI355X", value=inp.N * args.steps / wall,
-        unit="lookups/s", ms_per_step=wall / args.steps * 1e3, dtype="int64",
-        config={"workload": "config2 batch: bounds_check_indices, WARNING mode", "T": inp.T,
-                "B": inp.B, "N": inp.N},
-        kernel="tile_max_kernel + bounds_main_kernel", alg_bytes=alg, kernel_ms_mean=mean_ms,
-    )
-    cpu = None
-    if not args.no_cpu_baseline:
+    def cpu():
         sys.path.insert(0, str(REPO / "oracle"))
         import oracle as orc
 
+        assert int(warn.item()) == 0, "the config-2 batch is valid"
         rows_h = np.asarray(inp.E, dtype=np.int64)
         fn = lambda: orc.bounds_check_indices(rows_h, inp.indices, inp.offsets, 1)  # noqa: E731
         log("CPU baseline: C restatement of the bounds check, 1 thread")
         med, runs = cpu_time(fn, args.cpu_seconds)
-        cpu = dict(value=inp.N / med, unit="lookups/s", cores=1, kind="port",
-                   sample=(f"full config-2 batch (N={inp.N}), median of {runs} runs; the "
-                           f"oracle's C restatement, one thread, including its copies of "
-                           f"indices and offsets; host CPU: {cpu_model()}"))
-    return res, traffic_from_profile("bounds_check_config2"), cpu
+        return cpu_record(inp.N / med, "lookups/s", 1, "port",
+                          f"full config-2 batch (N={inp.N}), median of {runs} runs; the "
+                          f"oracle's C restatement, one thread, including its copies of "
+                          f"indices and offsets")
+
+    return Workload(
+        metric="bounds_check_indices lookups/sec, 1 MI355X", unit="lookups/s", steps=[step],
+        units=[inp.N], alg_bytes=[inp.N * 8 + (inp.T * inp.B + 1) * 8], dtype="int64",
+        config={"workload": "config2 batch: bounds_check_indices, WARNING mode", "T": inp.T,
+                "B": inp.B, "N": inp.N},
+        kernel="tile_max_kernel + bounds_main_kernel", profile="bounds_check_config2", cpu=cpu)
 
 
-def cpu_baseline_tbe(args, inp, W):
+# -- config 3 ----------------------------------------------------------------
+
+
+def wl_backward(args, dev) -> Workload:
     import numpy as np
+    import torch
 
-    sys.path.insert(0, str(REPO / "oracle"))
-    import oracle as orc
+    from mx_fbgemm import bench_inputs
 
-    log("CPU baseline: copying weights to host")
-    Wh = W.cpu().numpy()
-    w_off = (np.arange(inp.T) * inp.E[0] * inp.D[0]).astype(np.int64)
-    nthreads = orc.host_threads()
-    fn = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off, inp.D_offsets, inp.E, inp.B, inp.indices,  # noqa: E731
-                                            inp.offsets, 0, nthreads=nthreads)
-    log(f"CPU baseline: FBGEMM SpMDM on {nthreads} threads")
-    med, runs = cpu_time(fn, args.cpu_seconds)
-    fn1 = lambda: orc.fbgemm_tbe_forward_f32(Wh, w_off, inp.D_offsets, inp.E, inp.B, inp.indices,  # noqa: E731
-                                             inp.offsets, 0, nthreads=1)
-    med1, runs1 = cpu_time(fn1, args.cpu_seconds / 3, min_runs=1, warm=0)
-    return dict(
-        value=inp.N / med, unit="lookups/s", cores=nthreads, kind="reference",
-        sample=(f"full config-2 batch (N={inp.N} lookups), median of {runs} runs; FBGEMM "
-                f"GenerateEmbeddingSpMDMWithStrides<float,int64,int64,float> from the installed "
-                f"torch (the CPU kernel fbgemm_gpu's CPU TBE forward wraps), {nthreads} threads "
-                f"over (table, 256-bag chunks); 1 thread: {inp.N / med1:.4g} lookups/s "
-                f"({runs1} runs); host CPU: {cpu_model()}"),
-    )
+    log("generating config 3 (config-2 indices)")
+    inp = bench_inputs.config2()
+    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    m1 = torch.zeros(T * E, device=dev)
+    grad = torch.randn((B, inp.total_D), generator=g, device=dev) * 1e-2
+    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
+    m_off = torch.arange(T, device=dev, dtype=torch.int64) * E
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
+
+    def step():
+        op(grad, W, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits, idx, off, 0,
+           e32, 0, 0, False, m1, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
+
+    U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
+                      + inp.indices).size)
+    alg = inp.N * 8 + (T * B + 1) * 8 + B * inp.total_D * 4 + U * (2 * D * 4 + 2 * 4)
+
+    def cpu():
+        """The C restatement of the backward (stable merge sort of the
+        linearized keys, per-row sum in sorted order, rowwise Adagrad), one
+        thread, in place on host copies of the weights and gradient."""
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        log("CPU baseline: copying weights and gradient to host")
+        Wh = W.cpu().numpy()
+        gh = grad.cpu().numpy()
+        m1h = np.zeros(T * E, dtype=np.float32)
+        w_off_h = (np.arange(T) * E * D).astype(np.int64)
+        m_off_h = (np.arange(T) * E).astype(np.int64)
+        fn = lambda: orc.backward_rowwise_adagrad(  # noqa: E731
+            Wh, w_off_h, inp.D_offsets, B, inp.hash_size_cumsum, inp.total_hash_size_bits,
+            inp.indices, inp.offsets, 0, gh, m1h, m_off_h, 0.01, 1e-8, inplace=True)
+        log("CPU baseline: C restatement of the backward, 1 thread")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        return cpu_record(inp.N / med, "lookups/s", 1, "port",
+                          f"full config-3 batch (N={inp.N} lookups), median of {runs} runs; the "
+                          f"oracle's C restatement (stable merge sort + segment sum + rowwise "
+                          f"Adagrad), one thread, in place")
+
+    return Workload(
+        metric="TBE backward + exact rowwise Adagrad lookups/sec, 1 MI355X", unit="lookups/s",
+        steps=[step], units=[inp.N], alg_bytes=[alg], dtype="fp32",
+        config={"workload": "config3: TBE backward + exact rowwise Adagrad on config-2 shapes",
+                "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
+        kernel="whole backward (transpose + segment reduce + update)",
+        profile="tbe_bwd_config3", cpu=cpu)
 
 
-def bench_nbit(args, dev, config: int):
+# -- configs 4 and 5 ---------------------------------------------------------
+
+
+def wl_nbit(args, dev, config: int) -> Workload:
     import numpy as np
     import torch
 
@@ -360,150 +547,116 @@ def bench_nbit(args, dev, config: int):
     def mx(kind):
         return max([D for D, ty in zip(inp.D, tys) if ty == kind], default=0)
 
+    pooling = 1 if config == 4 else 0
     args_ = (W, torch.zeros(0, dtype=torch.uint8, device=dev),
              torch.zeros(inp.T, dtype=torch.int32, device=dev),
              torch.from_numpy(w_off_np).to(dev),
              torch.tensor(inp.tys, dtype=torch.uint8, device=dev),
              torch.from_numpy(inp.D_offsets).to(dev), inp.total_D, mx(SparseType.INT2),
              mx(SparseType.INT4), mx(SparseType.INT8), mx(SparseType.FP16), mx(SparseType.FP32),
-             idx, off, 1 if config == 4 else 0, None, 1, None, None, 16)
+             idx, off, pooling, None, 1, None, None, 16)
     op = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function
 
     def step():
         return op(*args_)
 
-    wall, mean_ms = time_launches(step, args.steps, args.warmup)
     N = inp.N
-    unpadded = [strides_u for strides_u in
-                [(D + 4) if ty == SparseType.INT8 else (D // 2 + 4) if ty == SparseType.INT4
-                 else 2 * D for D, ty in zip(inp.D, tys)]]
+    unpadded = [(D + 4) if ty == SparseType.INT8 else (D // 2 + 4) if ty == SparseType.INT4
+                else 2 * D for D, ty in zip(inp.D, tys)]
     lens = np.diff(inp.offsets).reshape(inp.T, inp.B).sum(1)
-    alg_bytes = int(sum(int(lens[t]) * (unpadded[t] + 4) for t in range(inp.T))
-                    + inp.B * sum(4 + 2 * D for D in inp.D))
-    # Compulsory bytes: every distinct row once, plus indices, offsets and output.
+    # Per lookup: the unpadded row and its int32 index; per bag: offset + fp16 output row.
+    alg = int(sum(int(lens[t]) * (unpadded[t] + 4) for t in range(inp.T))
+              + inp.B * sum(4 + 2 * D for D in inp.D))
     uniq = [int(np.count_nonzero(np.bincount(
         inp.indices[inp.offsets[t * inp.B]: inp.offsets[(t + 1) * inp.B]], minlength=inp.E[t])))
         for t in range(inp.T)]
     compulsory = int(sum(u * r for u, r in zip(uniq, unpadded)) + N * 4
                      + inp.B * sum(4 + 2 * D for D in inp.D))
-    res = dict(
-        metric="nbit TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
-        value=N * args.steps / wall, unit="lookups/s", ms_per_step=wall / args.steps * 1e3,
-        dtype="int8/int4 codes, fp32 accumulate, fp16 out" if config == 4 else
-        "fp16/int4 codes, fp32 accumulate, fp16 out",
-        config={"workload": (f"config{config}: " + (
-            "nbit MEAN fp16 out, 16 INT8 + 16 INT4 tables E=1e6 D=128 B=16384 L=20"
-            if config == 4 else "mixed nbit SUM fp16 out, 64 tables FP16/INT4 D 32..256 "
-            "B=65536 L~Poisson(15) 10% empty Zipf(1.1)")), "T": inp.T, "B": inp.B, "N": N},
-        kernel="nbit_fwd_kernel", alg_bytes=alg_bytes, kernel_ms_mean=mean_ms,
-        compulsory_bytes=compulsory, unique_rows=int(sum(uniq)),
-    )
-    cpu = None
-    if not args.no_cpu_baseline:
+    # What 128-byte line fills make of the rows: each row's lines once per lookup.
+    line_bytes = 0
+    for t in range(inp.T):
+        s = strides[t]
+        starts = (np.arange(128 // np.gcd(s, 128)) * s) % 128
+        lines = ((starts + unpadded[t] + 127) // 128).mean()
+        line_bytes += int(lens[t]) * lines * 128
+    line_bytes = int(line_bytes + N * 4 + inp.B * sum(4 + 2 * D for D in inp.D))
+
+    def cpu():
         sys.path.insert(0, str(REPO / "oracle"))
         import oracle as orc
 
-        # Bounded sample: the first B_s bags of every table.
+        # Bounded sample: the first Bs bags of every table.
         Bs = min(inp.B, 2048)
-        sel_off = np.concatenate([inp.offsets[t * inp.B: t * inp.B + Bs] for t in range(inp.T)]
-                                 + [[0]])
         idx_parts = [inp.indices[inp.offsets[t * inp.B]: inp.offsets[t * inp.B + Bs]]
                      for t in range(inp.T)]
         sidx = np.concatenate(idx_parts).astype(np.int64)
         lens_s = np.concatenate([np.diff(inp.offsets[t * inp.B: t * inp.B + Bs + 1])
                                  for t in range(inp.T)])
         soff = bench_inputs.offsets_from_lengths(lens_s)
-        del sel_off
         log("CPU baseline: copying nbit weights to host")
         Wh = W.cpu().numpy()
         nthreads = orc.host_threads()
         fn = lambda: orc.fbgemm_nbit_forward(Wh, w_off_np, inp.tys, inp.D_offsets, inp.E, Bs,  # noqa: E731
-                                             sidx, soff, 1 if config == 4 else 0,
-                                             nthreads=nthreads)
+                                             sidx, soff, pooling, nthreads=nthreads)
+        log(f"CPU baseline: FBGEMM nbit kernels on {nthreads} threads")
         med, runs = cpu_time(fn, args.cpu_seconds)
-        cpu = dict(value=sidx.size / med, unit="lookups/s", cores=nthreads, kind="reference",
-                   sample=(f"first {Bs} bags of every table ({sidx.size} lookups), median of "
-                           f"{runs} runs; FBGEMM 8-bit/N-bit/fp16 SpMDM CPU kernels "
-                           f"(scale_bias_last=false) from the installed torch, {nthreads} "
-                           f"threads; host CPU: {cpu_model()}"))
-    return res, traffic_from_profile(f"nbit_fwd_config{config}"), cpu
+        return cpu_record(sidx.size / med, "lookups/s", nthreads, "reference",
+                          f"first {Bs} bags of every table ({sidx.size} lookups), median of "
+                          f"{runs} runs; FBGEMM 8-bit/N-bit/fp16 SpMDM CPU kernels "
+                          f"(scale_bias_last=false) from the installed torch, {nthreads} "
+                          f"threads")
+
+    workload = (f"config{config}: " + (
+        "nbit MEAN fp16 out, 16 INT8 + 16 INT4 tables E=1e6 D=128 B=16384 L=20 uniform int32 "
+        "indices" if config == 4 else "mixed nbit SUM fp16 out, 64 tables FP16/INT4 D 32..256 "
+        "B=65536 L~Poisson(15) 10% empty Zipf(1.1)"))
+    return Workload(
+        metric="nbit TBE fwd lookups/sec + achieved HBM GB/s (% of peak), 1 MI355X",
+        unit="lookups/s", steps=[step], units=[N], alg_bytes=[alg],
+        dtype="int8/int4 codes, fp32 accumulate, fp16 out" if config == 4 else
+        "fp16/int4 codes, fp32 accumulate, fp16 out",
+        config={"workload": workload, "T": inp.T, "B": inp.B, "N": N},
+        kernel="nbit_fwd_kernel (one launch per table type present)",
+        profile=f"nbit_fwd_config{config}", cpu=cpu,
+        # Config 5 draws Zipf indices (the per-lookup count re-reads the hot
+        # rows); config 4's are uniform over 3.6 GB of rows, where a repeated
+        # row is long evicted when it comes again, so every lookup is HBM traffic.
+        roof_bytes=compulsory if config == 5 else None,
+        roof_bytes_kind=("compulsory bytes: distinct rows once (unpadded) + int32 indices + "
+                         "offsets + fp16 output" if config == 5 else
+                         "algorithmic bytes: every lookup's unpadded row + its int32 index, "
+                         "per bag its offset + fp16 output row"),
+        extra=dict(compulsory=dict(bytes=compulsory, unique_rows=int(sum(uniq))),
+                   line_fill=dict(bytes=line_bytes,
+                                  frac_at_peak_alg=alg / line_bytes,
+                                  note="rows fetched as whole 128-B lines, once per lookup: "
+                                       "the algorithmic fraction of peak this traffic allows")))
 
 
-def bench_backward(args, dev):
-    import numpy as np
+# ---------------------------------------------------------------------------
+
+
+def measure(args, config: int, dev) -> dict:
     import torch
 
-    from mx_fbgemm import bench_inputs
-
-    log("generating config 3 (config-2 indices)")
-    inp = bench_inputs.config2()
-    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
-    g = torch.Generator(device=dev)
-    g.manual_seed(0)
-    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
-    m1 = torch.zeros(T * E, device=dev)
-    grad = torch.randn((B, inp.total_D), generator=g, device=dev) * 1e-2
-    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
-    m_off = torch.arange(T, device=dev, dtype=torch.int64) * E
-    D_off = torch.from_numpy(inp.D_offsets).to(dev)
-    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
-    idx = torch.from_numpy(inp.indices).to(dev)
-    off = torch.from_numpy(inp.offsets).to(dev)
-    empty = torch.zeros(0, device=dev)
-    pl = torch.zeros(T, dtype=torch.int32, device=dev)
-    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
-    op = torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
-
-    def step():
-        op(grad, W, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits, idx, off, 0,
-           e32, 0, 0, False, m1, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
-
-    wall, mean_ms = time_launches(step, args.steps, args.warmup)
-    U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
-                      + inp.indices).size)
-    alg = inp.N * 8 + (T * B + 1) * 8 + B * inp.total_D * 4 + U * (2 * D * 4 + 2 * 4)
-    res = dict(
-        metric="TBE backward + exact rowwise Adagrad lookups/sec, 1 MI355X",
-        value=inp.N * args.steps / wall, unit="lookups/s", ms_per_step=wall / args.steps * 1e3,
-        dtype="fp32",
-        config={"workload": "config3: TBE backward + exact rowwise Adagrad on config-2 shapes",
-                "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
-        kernel="whole backward (transpose + segment reduce + update)", alg_bytes=alg,
-        kernel_ms_mean=mean_ms,
-    )
+    if config == 1:
+        wl = wl_jagged(args, dev)
+    elif config == 2 and args.op == "bounds-check":
+        wl = wl_bounds_check(args, dev)
+    elif config == 2:
+        wl = wl_tbe_forward(args, dev)
+    elif config == 3:
+        wl = wl_backward(args, dev)
+    else:
+        wl = wl_nbit(args, dev, config)
+    rec = run_workload(args, wl, dev)
     cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline_backward(args, inp, W, grad)
-    return res, traffic_from_profile("tbe_bwd_config3"), cpu
-
-
-def cpu_baseline_backward(args, inp, W, grad):
-    """The C restatement of the backward (stable merge sort of the linearized
-    keys, per-row sum in sorted order, rowwise Adagrad), one thread, in place
-    on host copies of the weights and gradient."""
-    import numpy as np
-
-    sys.path.insert(0, str(REPO / "oracle"))
-    import oracle as orc
-
-    log("CPU baseline: copying weights and gradient to host")
-    T, E, D = inp.T, inp.E[0], inp.D[0]
-    Wh = W.cpu().numpy()
-    gh = grad.cpu().numpy()
-    m1h = np.zeros(T * E, dtype=np.float32)
-    w_off = (np.arange(T) * E * D).astype(np.int64)
-    m_off = (np.arange(T) * E).astype(np.int64)
-    fn = lambda: orc.backward_rowwise_adagrad(  # noqa: E731
-        Wh, w_off, inp.D_offsets, inp.B, inp.hash_size_cumsum, inp.total_hash_size_bits,
-        inp.indices, inp.offsets, 0, gh, m1h, m_off, 0.01, 1e-8, inplace=True)
-    log("CPU baseline: C restatement of the backward, 1 thread")
-    med, runs = cpu_time(fn, args.cpu_seconds)
-    return dict(
-        value=inp.N / med, unit="lookups/s", cores=1, kind="port",
-        sample=(f"full config-3 batch (N={inp.N} lookups), median of {runs} runs; the oracle's C "
-                f"restatement (stable merge sort + segment sum + rowwise Adagrad), one thread, "
-                f"in place; host CPU: {cpu_model()}"),
-    )
+    if not args.no_cpu_baseline and wl.cpu is not None:
+        cpu = wl.cpu()
+    line = make_line(args, wl, rec, cpu)
+    del wl
+    torch.cuda.empty_cache()
+    return line
 
 
 def main():
@@ -522,7 +675,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     if args.copy_calibration:
-        src = torch.ones(1 << 28, device=dev)
+        src = torch.ones(FLUSH_BYTES // 4, device=dev)
         dst = torch.empty_like(src)
         for _ in range(args.steps):
             dst.copy_(src)
@@ -530,39 +683,13 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4,
                           "launches": args.steps}))
         return
-    if args.config == 1:
-        res, traffic, cpu = bench_jagged(args, dev)
-    elif args.config == 2 and args.op == "bounds-check":
-        res, traffic, cpu = bench_bounds_check(args, dev)
-    elif args.config == 2:
-        res, traffic, cpu = bench_tbe_forward(args, dev)
-    elif args.config == 3:
-        res, traffic, cpu = bench_backward(args, dev)
-    else:
-        res, traffic, cpu = bench_nbit(args, dev, args.config)
-    achieved = res["alg_bytes"] / (res["kernel_ms_mean"] * 1e-3) / 1e9
-    line = dict(
-        metric=res["metric"], value=res["value"], unit=res["unit"], n_gpus=1, steps=args.steps,
-        warmup=args.warmup, ms_per_step=res["ms_per_step"], higher_is_better=True,
-        scaling="weak", vs_baseline=None, dtype=res["dtype"], data="synthetic",
-        config=res["config"],
-        roofline=dict(bound="hbm", achieved=achieved, peak=PEAK_HBM_GBS, unit="GB/s",
-                      frac=achieved / PEAK_HBM_GBS, traffic=traffic,
-                      kernel=res["kernel"], alg_bytes_per_launch=res["alg_bytes"],
-                      launch_ms_mean=res["kernel_ms_mean"]),
-        cpu_baseline=cpu,
-    )
-    if "cold_kernel_ms_median" in res:
-        line["roofline"]["cold_launch_ms_median"] = res["cold_kernel_ms_median"]
-    if "fresh_batches" in res:
-        line["roofline"]["fresh_batches"] = res["fresh_batches"]
-    if "compulsory_bytes" in res:
-        # The same launch against only the bytes no cache can serve: each
-        # distinct row once, plus indices, offsets and output.
-        comp = res["compulsory_bytes"] / (res["kernel_ms_mean"] * 1e-3) / 1e9
-        line["roofline"].update(compulsory_bytes=res["compulsory_bytes"],
-                                unique_rows=res["unique_rows"], compulsory_GBps=comp,
-                                compulsory_frac=comp / PEAK_HBM_GBS)
+    line = measure(args, args.config, dev)
+    if args.config == 2 and args.op == "lookup" and not args.no_config4:
+        # The second headline target: nbit INT8/INT4 lookup at >= 60 % of HBM.
+        c4 = measure(args, 4, dev)
+        line["config4"] = {k: c4[k] for k in ("metric", "value", "unit", "ms_per_step", "dtype",
+                                              "config", "roofline", "effective", "compulsory",
+                                              "line_fill", "cpu_baseline")}
     print(json.dumps(line), flush=True)
 
 

@@ -71,6 +71,23 @@ int mx_version(void);
 /* Thread-local text of the last failing call on this thread ("" if none). */
 const char* mx_last_error(void);
 
+/* ---- look-back failures (no fbgemm counterpart) --------------------------
+ * The radix sort and the prefix scans of the TBE backward and of
+ * transpose_embedding_input wait, tile by tile, for the counts of earlier
+ * tiles (decoupled look-back).  Every such wait is bounded; one that runs
+ * out (never expected: the tile waited on was scheduled earlier and
+ * publishes without waiting) makes the call leave its outputs -- the run
+ * layout, the weight and momentum update -- unwritten, and stores 1 into the
+ * host-visible word registered here for the current device (pinned host
+ * memory owned by the caller, which reads and clears it; NULL unregisters).
+ * Kernels launched before a registration (or captured in a graph before it)
+ * do not see it. */
+int mx_set_status_mailbox(unsigned int* host_word);
+
+/* Test hook: while enabled, every look-back wait of later calls gives up at
+ * once (failure-handling tests; every kernel still exits normally). */
+int mx_test_force_lookback_giveup(int enable);
+
 /* ---- jagged tensor ops ------------------------------------------------- */
 
 /* Serves fbgemm::jagged_to_padded_dense_forward (and the forward of
@@ -180,8 +197,11 @@ size_t mx_tbe_transpose_workspace_bytes(int64_t N, int32_t total_hash_size_bits)
  *                          total_hash_size_bits bits
  *   run / run_lengths      unique keys and their counts, num_runs of them
  *   cumulative_run_lengths [num_runs+1] exclusive cumsum of run_lengths
- * Run arrays are sized N; entries past num_runs are left as they were
- * (num_runs stays on the device).  Integer work: bit-exact. */
+ * Run arrays are sized N (cumulative_run_lengths N+1) and read as the
+ * complete cumsum of the zero-padded run lengths: past num_runs every
+ * run_lengths entry is 0 and every cumulative_run_lengths entry N; run keys
+ * past num_runs are left as they were (num_runs stays on the device).
+ * Integer work: bit-exact. */
 int mx_tbe_transpose_embedding_input(
     const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
     int32_t info_B_num_bits, const void* indices, const void* offsets, int32_t index_bytes,
@@ -199,6 +219,17 @@ int mx_tbe_transpose_embedding_input_vbe(
     int64_t* sorted_linear_indices, int32_t* infos_sorted, int64_t* sorted_linear_indices_run,
     int32_t* run_lengths, int32_t* num_runs, int32_t* cumulative_run_lengths, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Random state of a stochastic-rounding update, in the shape of torch's
+ * Philox state: eager calls pass the seed and offset as values; a call made
+ * under graph capture passes device pointers that the kernel reads when it
+ * runs (offset = *offset_dev + offset), so every replay draws new bits. */
+typedef struct mx_rng_state {
+  uint64_t seed;
+  uint64_t offset;
+  const int64_t* seed_dev;    /* non-NULL: the seed is read from here */
+  const int64_t* offset_dev;  /* non-NULL: the offset is *offset_dev + offset */
+} mx_rng_state;
 
 /* Workspace needed by mx_tbe_backward_rowwise_adagrad(_vbe). */
 size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, int32_t max_D);
@@ -218,20 +249,22 @@ size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, 
  * weights (fp32, or fp16 with weights_ty MX_SPARSE_FP16: w read as fp32, the
  * new value rounded to fp16 -- to nearest even, or stochastically when
  * stochastic_rounding != 0: |w| plus a uniform random amount below fp16's
- * last place, then truncated, the random bits a hash of (seed, element))
+ * last place, then truncated, the random bits a hash of (rng, element); rng
+ * may be NULL when stochastic_rounding is 0)
  * and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are updated
- * in place; no atomics, deterministic for a given seed.  Rows with more than
- * 32 occurrences are updated on a second stream of the device, forked from
- * `stream` by an event and joined back into it before the call returns, so
- * the call is ordered on `stream` like any other (also under graph capture). */
+ * in place; no atomics, deterministic for a given random state.  Rows with
+ * more than 32 occurrences are updated on a second stream kept for `stream`
+ * (one per device and caller stream), forked from `stream` by an event and
+ * joined back into it before the call returns, so the call is ordered on
+ * `stream` like any other (also under graph capture). */
 int mx_tbe_backward_rowwise_adagrad(
     void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
     int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
     int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
     float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
-    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
-    void* workspace, size_t workspace_bytes, void* stream);
+    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding,
+    const mx_rng_state* rng, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Serves fbgemm::split_embedding_backward_codegen_rowwise_adagrad_{unweighted,
  * weighted}_exact_vbe_cuda: mx_tbe_backward_rowwise_adagrad over total_B
@@ -246,8 +279,8 @@ int mx_tbe_backward_rowwise_adagrad_vbe(
     int64_t total_B, const int32_t* B_offsets, const int64_t* vbe_row_output_offsets,
     const int32_t* vbe_b_t_map, int32_t info_B_num_bits, float* momentum1,
     const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
-    int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed, void* workspace,
-    size_t workspace_bytes, void* stream);
+    int32_t weight_decay_mode, int32_t stochastic_rounding, const mx_rng_state* rng,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Serves fbgemm::split_embedding_codegen_grad_indice_weights_cuda: the gradient
  * of a weighted lookup's per-sample weights,

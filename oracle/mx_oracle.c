@@ -274,8 +274,10 @@ static int transpose_impl(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, 
     }
   }
   *num_runs = r + 1;
-  cum[r + 1] = (int32_t)N;
-  for (int64_t k = 0; k <= r; ++k) run_lengths[k] = cum[k + 1] - cum[k];
+  /* Past the runs the arrays are the complete cumsum of the zero-padded
+   * lengths: cum = N, run_lengths = 0 (cum has N+1 entries, run_lengths N). */
+  for (int64_t k = r + 1; k <= N; ++k) cum[k] = (int32_t)N;
+  for (int64_t k = 0; k < N; ++k) run_lengths[k] = k <= r ? cum[k + 1] - cum[k] : 0;
   free(info_raw);
   free(perm);
   free(tmp);

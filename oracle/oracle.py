@@ -248,7 +248,8 @@ def transpose_embedding_input(hsc, B, info_B_num_bits, bits, indices, offsets):
         assert rc == 0
     r = int(num_runs[0])
     return dict(linear_indices=linear[:N], sorted_linear_indices=srt[:N], infos_sorted=infos[:N],
-                run=run[:r], run_lengths=lengths[:r], num_runs=r, cumulative_run_lengths=cum[:r + 1])
+                run=run[:r], run_lengths=lengths[:r], num_runs=r, cumulative_run_lengths=cum[:r + 1],
+                run_lengths_full=lengths[:N], cumulative_run_lengths_full=cum[:N + 1])
 
 
 def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,

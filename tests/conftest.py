@@ -48,3 +48,20 @@ def dev():
     import mx_fbgemm  # noqa: F401  (registers torch.ops.fbgemm.*)
 
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _no_lookback_faults(request):
+    """After every GPU test: no sort or scan look-back wait gave up (the
+    kernels report one through a host-visible word of the device)."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import torch
+
+    if not torch.cuda.is_available():
+        return
+    import mx_fbgemm  # noqa: F401
+
+    assert torch.ops.mx_fbgemm.pending_lookback_faults(0) == 0, \
+        "a look-back wait of the sort or a scan gave up during this test"

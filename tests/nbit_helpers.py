@@ -82,15 +82,32 @@ def build_weights_gpu(dev, tys, dims, rows, seed: int, row_align: int = 16):
     return W, w_off
 
 
-def sample_bags(indices, offsets, T: int, B: int, bs):
-    """Sub-batch of the bags (t, b) for b in `bs` (every table): (indices,
-    offsets) of a batch of len(bs) bags per table, in the same t-major order."""
-    parts, lens = [], []
-    for t in range(T):
-        for b in bs:
-            s, e = int(offsets[t * B + b]), int(offsets[t * B + b + 1])
-            parts.append(indices[s:e])
-            lens.append(e - s)
-    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    idx = np.concatenate(parts).astype(np.int64) if parts else np.zeros(0, np.int64)
-    return idx, off
+def fp16_ulp_distance(a, b) -> np.ndarray:
+    """Distance in fp16 units in the last place between two fp16 arrays: the
+    difference of their bit patterns mapped to a monotonic integer scale
+    (+0 and -0 are the same point)."""
+    def ordinal(x):
+        h = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16).astype(np.int32)
+        mag = h & 0x7FFF
+        return np.where(h & 0x8000, -mag, mag)
+
+    return np.abs(ordinal(a) - ordinal(b))
+
+
+def assert_nbit_close(got, exp, max_ulps: int = 1):
+    """The nbit parity check.  Stated contract: rtol 1e-2 (atol 1e-3 near
+    zero).  What the kernels achieve, and what is asserted on top: fp16
+    outputs within `max_ulps` fp16 place of the oracle (both are fp32 sums of
+    the same terms, grouped differently, rounded once to fp16); fp32 outputs
+    within rtol 1e-5 / atol 1e-5."""
+    g = got.cpu().numpy() if hasattr(got, "cpu") else np.asarray(got)
+    e = np.asarray(exp)
+    np.testing.assert_allclose(g.astype(np.float32), e.astype(np.float32), rtol=1e-2, atol=1e-3)
+    if g.dtype == np.float16:
+        d = fp16_ulp_distance(g, e.astype(np.float16))
+        assert d.max(initial=0) <= max_ulps, (
+            f"{int((d > max_ulps).sum())} outputs differ by more than {max_ulps} fp16 ulp "
+            f"(max {int(d.max())})")
+    else:
+        np.testing.assert_allclose(g.astype(np.float32), e.astype(np.float32), rtol=1e-5,
+                                   atol=1e-5)

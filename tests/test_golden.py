@@ -90,14 +90,13 @@ def test_gpu_tbe_fixture(dev, pooling):
 @pytest.mark.gpu
 @pytest.mark.parametrize("pooling", [0, 1])
 def test_gpu_nbit_fixture(dev, pooling):
-    from nbit_helpers import nbit_forward_gpu
+    from nbit_helpers import assert_nbit_close, nbit_forward_gpu
 
     g = load("nbit")
     dims = list(np.diff(g["D_off"]))
     out = nbit_forward_gpu(dev, torch.from_numpy(g["W"]).to(dev), g["w_off"], list(g["tys"]), dims,
                            g["indices"], g["offsets"], pooling)
-    np.testing.assert_allclose(out.float().cpu().numpy(), g[f"out_p{pooling}"].astype(np.float32),
-                               rtol=1e-2, atol=1e-3)
+    assert_nbit_close(out, g[f"out_p{pooling}"])  # rtol 1e-2 contract and <= 1 fp16 ulp
 
 
 @pytest.mark.gpu

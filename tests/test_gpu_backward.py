@@ -36,6 +36,9 @@ def _check_transpose(dev, inp, index_dtype=torch.int64):
     np.testing.assert_array_equal(run.cpu().numpy()[:r], exp["run"])
     np.testing.assert_array_equal(lengths.cpu().numpy()[:r], exp["run_lengths"])
     np.testing.assert_array_equal(cum.cpu().numpy()[: r + 1], exp["cumulative_run_lengths"])
+    # Whole arrays: past num_runs, run lengths 0 and the cumsum N.
+    np.testing.assert_array_equal(lengths.cpu().numpy(), exp["run_lengths_full"])
+    np.testing.assert_array_equal(cum.cpu().numpy(), exp["cumulative_run_lengths_full"])
 
 
 @pytest.mark.parametrize("T,B,rows,max_L,dup", [
@@ -554,3 +557,47 @@ def test_module_training_step_fp16(dev, sr):
     got = tbe.weights_dev.detach().cpu().numpy().astype(np.float32)
     lo, hi = _f16_bracket(u, W0)
     assert np.all((got >= lo.astype(np.float32)) & (got <= hi.astype(np.float32)))
+
+
+def test_lookback_giveup_is_reported_and_leaves_outputs_alone(dev):
+    """Forced from the host (a test hook makes every look-back wait give up at
+    once; every kernel still exits normally): the transpose and the backward
+    leave their outputs alone, and the next call on the device raises."""
+    print("[case] forced look-back give-up", flush=True)
+    rng = np.random.default_rng(21)
+    inp = random_tbe(rng, 3, 2048, [64] * 3, [5000, 300, 70000], 20)  # ~12 sort tiles
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    _check_transpose(dev, inp)  # registers the device's failure word
+    W0 = rng.uniform(-0.01, 0.01, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
+    W = torch.from_numpy(W0).to(dev)
+    m1 = torch.zeros(sum(inp.E), device=dev)
+    grad = torch.from_numpy(rng.normal(0, 1e-2, (inp.B, inp.total_D)).astype(np.float32)).to(dev)
+    w_off = torch.from_numpy(weight_offsets(inp)).to(dev)
+    m_off = torch.from_numpy(np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(inp.T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+
+    def backward():
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+            grad, W, empty, empty, pl, w_off, torch.from_numpy(inp.D_offsets).to(dev),
+            max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev),
+            inp.total_hash_size_bits, torch.from_numpy(inp.indices).to(dev),
+            torch.from_numpy(inp.offsets).to(dev), 0, e32, 0, 0, False, m1, empty, pl, m_off,
+            1e-8, 0.05, 0.0, 0, 0.0)
+
+    torch.ops.mx_fbgemm.test_force_lookback_giveup(True)
+    try:
+        backward()
+        torch.cuda.synchronize()
+    finally:
+        torch.ops.mx_fbgemm.test_force_lookback_giveup(False)
+    assert np.array_equal(W.cpu().numpy(), W0) and not m1.any(), "a failed call updated rows"
+    with pytest.raises(RuntimeError, match="gave up a look-back wait"):
+        _transpose_gpu(dev, inp, nb)
+    # Reported once; the same calls then run normally.
+    _check_transpose(dev, inp)
+    backward()
+    torch.cuda.synchronize()
+    assert not np.array_equal(W.cpu().numpy(), W0)
+    assert torch.ops.mx_fbgemm.pending_lookback_faults(0) == 0

@@ -121,3 +121,136 @@ def test_backward_on_two_streams_from_two_threads(dev):
     torch.cuda.synchronize()
     for W, m, _ in state:
         assert torch.equal(W, ref_W) and torch.equal(m, ref_m)
+
+
+def test_capture_on_one_thread_while_another_trains_eagerly(dev):
+    """One host thread captures a training step on its stream and replays it
+    while another runs eager steps on its own stream at the same time.  Each
+    caller stream has its own second stream, so the capture takes in none of
+    the other thread's work: both end bit-identical to the same steps run in
+    turn."""
+    import threading
+
+    print("[case] capture + replay on one thread, eager steps on another", flush=True)
+    rng = np.random.default_rng(11)
+    inp = random_tbe(rng, 3, 256, [32, 64, 128], [500, 2000, 3], 30)
+    nW = sum(E * D for E, D in zip(inp.E, inp.D))
+    nM = sum(inp.E)
+    W0 = torch.from_numpy(rng.uniform(-0.01, 0.01, nW).astype(np.float32)).to(dev)
+    grads = [torch.from_numpy(rng.normal(0, 1e-2, (inp.B, inp.total_D)).astype(np.float32)).to(dev)
+             for _ in range(3)]
+
+    ref_W, ref_m, ref_g = W0.clone(), torch.zeros(nM, device=dev), torch.empty_like(grads[0])
+    ref_step = _step_fn(dev, inp, ref_W, ref_m, ref_g)
+    refs = []
+    for g in grads:
+        ref_g.copy_(g)
+        ref_step()
+        refs.append((ref_W.clone(), ref_m.clone()))
+    torch.cuda.synchronize()
+
+    s_cap, s_eager = torch.cuda.Stream(), torch.cuda.Stream()
+    # Warm-up step on each stream with throwaway state: creates each stream's
+    # second stream, and the allocator's blocks, before the capture starts.
+    for st in (s_cap, s_eager):
+        with torch.cuda.stream(st):
+            _step_fn(dev, inp, W0.clone(), torch.zeros(nM, device=dev), grads[0].clone())()
+        st.synchronize()
+
+    start = threading.Barrier(2)
+    errors = []
+    cap_state = (W0.clone(), torch.zeros(nM, device=dev), torch.empty_like(grads[0]))
+    eager_state = (W0.clone(), torch.zeros(nM, device=dev), torch.empty_like(grads[0]))
+    torch.cuda.synchronize()
+
+    def capture_and_replay():
+        try:
+            W, m, gbuf = cap_state
+            with torch.cuda.stream(s_cap):
+                step = _step_fn(dev, inp, W, m, gbuf)
+                graph = torch.cuda.CUDAGraph()
+                start.wait()
+                with torch.cuda.graph(graph, stream=s_cap, capture_error_mode="thread_local"):
+                    step()
+                for k, g in enumerate(grads):
+                    gbuf.copy_(g)
+                    graph.replay()
+                    s_cap.synchronize()
+                    if not (torch.equal(W, refs[k][0]) and torch.equal(m, refs[k][1])):
+                        errors.append(f"replay {k} differs from the sequential step")
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(f"capture thread: {e!r}")
+
+    def eager():
+        try:
+            W, m, gbuf = eager_state
+            with torch.cuda.stream(s_eager):
+                step = _step_fn(dev, inp, W, m, gbuf)
+                start.wait()
+                for k, g in enumerate(grads):
+                    gbuf.copy_(g)
+                    step()
+                    s_eager.synchronize()
+                    if not (torch.equal(W, refs[k][0]) and torch.equal(m, refs[k][1])):
+                        errors.append(f"eager step {k} differs from the sequential step")
+        except Exception as e:  # noqa: BLE001
+            errors.append(f"eager thread: {e!r}")
+
+    threads = [threading.Thread(target=capture_and_replay), threading.Thread(target=eager)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a thread did not finish"
+    torch.cuda.synchronize()
+    assert not errors, errors
+
+
+def test_fp16_stochastic_rounding_graph_replays_draw_fresh_bits(dev):
+    """fp16 weights with stochastic rounding in a captured step: the random
+    state is read when the kernel runs, so each replay rounds with the bits an
+    eager step at the same generator position uses (bit-identical), and
+    successive replays differ from one another."""
+    print("[case] graph-captured fp16 + stochastic rounding step", flush=True)
+    rng = np.random.default_rng(13)
+    inp = random_tbe(rng, 2, 512, [64, 128], [300, 400], 20, empty_frac=0.0)
+    nW = sum(E * D for E, D in zip(inp.E, inp.D))
+    W0 = torch.from_numpy(rng.uniform(-1, 1, nW).astype(np.float16)).to(dev)
+    g0 = torch.from_numpy(rng.normal(0, 1e-1, (inp.B, inp.total_D)).astype(np.float32)).to(dev)
+    w_off = torch.from_numpy(weight_offsets(inp)).to(dev)
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    m1_off = torch.from_numpy(np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(inp.T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+
+    def backward(W, m):
+        torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+            g0, W, empty, empty, pl, w_off, D_off, max(inp.D), hsc, inp.total_hash_size_bits,
+            idx, off, 0, e32, 0, 0, True, m, empty, pl, m1_off, 1e-6, 0.05, 0.0, 0, 0.0)
+
+    torch.manual_seed(7)
+    We, me = W0.clone(), torch.zeros(sum(inp.E), device=dev)
+    eager = []
+    for _ in range(3):
+        backward(We, me)
+        eager.append(We.clone())
+    torch.cuda.synchronize()
+    assert not torch.equal(eager[1], eager[2])
+
+    Wg, mg = W0.clone(), torch.zeros(sum(inp.E), device=dev)
+    backward(W0.clone(), torch.zeros(sum(inp.E), device=dev))  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        backward(Wg, mg)
+    torch.cuda.synchronize()
+    torch.manual_seed(7)  # the replays start where the eager steps started
+    for k in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Wg.view(torch.int16), eager[k].view(torch.int16)), \
+            f"replay {k} rounded with other bits than the eager step"

@@ -1,6 +1,9 @@
 // Status reporting and device queries shared by every entry point.
+#include <atomic>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "mx_common.h"
 #include "scan.h"
@@ -38,19 +41,43 @@ int num_cus() {
   return cached[dev];
 }
 
-hipStream_t side_stream() {
+bool side_path(hipStream_t caller, SidePath* out) {
   static std::mutex mu;
-  static hipStream_t cached[64] = {};
+  static std::map<std::pair<int, hipStream_t>, SidePath> cached;  // kept until the process ends
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, caller);
+  auto it = cached.find(key);
+  if (it == cached.end()) {
+    SidePath p{};
+    if (hipStreamCreateWithFlags(&p.side, hipStreamNonBlocking) != hipSuccess) return false;
+    if (hipEventCreateWithFlags(&p.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&p.join, hipEventDisableTiming) != hipSuccess) {
+      if (p.fork) (void)hipEventDestroy(p.fork);
+      (void)hipStreamDestroy(p.side);
+      return false;
+    }
+    it = cached.emplace(key, p).first;
+  }
+  *out = it->second;
+  return true;
+}
+
+namespace {
+std::mutex g_mailbox_mu;
+unsigned int* g_mailbox[64] = {};
+std::atomic<int> g_force_giveup{0};
+}  // namespace
+
+unsigned int* status_mailbox() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (cached[dev] == nullptr) {
-    hipStream_t st = nullptr;
-    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    cached[dev] = st;  // kept until the process ends
-  }
-  return cached[dev];
+  std::lock_guard<std::mutex> lock(g_mailbox_mu);
+  return g_mailbox[dev];
 }
+
+int lookback_spin_limit(int dflt) { return g_force_giveup.load() ? -1 : dflt; }
 
 __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -63,3 +90,18 @@ __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
 extern "C" int mx_version(void) { return 100; }
 
 extern "C" const char* mx_last_error(void) { return mx::g_last_error.c_str(); }
+
+extern "C" int mx_set_status_mailbox(unsigned int* host_word) {
+  mx::clear_error();
+  int dev = 0;
+  MX_HIP_CHECK(hipGetDevice(&dev));
+  MX_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mx::g_mailbox_mu);
+  mx::g_mailbox[dev] = host_word;
+  return MX_OK;
+}
+
+extern "C" int mx_test_force_lookback_giveup(int enable) {
+  mx::g_force_giveup.store(enable != 0 ? 1 : 0);
+  return MX_OK;
+}

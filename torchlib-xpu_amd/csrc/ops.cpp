@@ -19,7 +19,11 @@
 #include <torch/csrc/autograd/custom_function.h>
 #include <torch/library.h>
 
+#include <hip/hip_runtime_api.h>
+
+#include <array>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "mx_fbgemm.h"
@@ -57,6 +61,82 @@ void check_arg(const Tensor& t, const Tensor& like, const char* name, bool dense
   check_gpu(t, name);
   check_same_device(like, t, name);
   TORCH_CHECK(!dense || t.is_contiguous(), name, " must be contiguous");
+}
+
+// ---------------------------------------------------------------------------
+// Look-back failures of the sort and scans
+// ---------------------------------------------------------------------------
+// The kernels report a look-back wait that exhausted its bound (never
+// expected) by storing 1 in a host-visible word registered for the device;
+// the call's later kernels then leave its outputs (run layout, weights,
+// momentum) alone.  One pinned word per device is registered on the first
+// backward or transpose on that device outside graph capture; every such op
+// reads it first (a host read, no synchronisation) and raises if an earlier
+// call failed.
+
+struct Mailboxes {
+  std::mutex mu;
+  std::array<Tensor, 64> word;  // int32 [1], pinned host memory
+};
+
+Mailboxes& mailboxes() {
+  static Mailboxes m;
+  return m;
+}
+
+int32_t* mailbox_of(int dev) {
+  auto& m = mailboxes();
+  std::lock_guard<std::mutex> lock(m.mu);
+  return m.word[dev].defined() ? m.word[dev].data_ptr<int32_t>() : nullptr;
+}
+
+// Raises if a look-back of an earlier call on `dev` gave up (the word is
+// cleared, so the failure is reported once).
+void raise_if_lookback_failed(int dev) {
+  int32_t* p = mailbox_of(dev);
+  if (p == nullptr || __atomic_load_n(p, __ATOMIC_ACQUIRE) == 0) return;
+  __atomic_store_n(p, 0, __ATOMIC_RELAXED);
+  TORCH_CHECK(false, "an earlier TBE backward or transpose_embedding_input on cuda:", dev,
+              " gave up a look-back wait in its sort or scan, so it left its outputs (sorted "
+              "indices and run layout, or the weight and momentum update) unwritten; that step "
+              "has to be run again");
+}
+
+// Registers the device's mailbox (the caller holds a device guard for it).
+void ensure_mailbox(int dev, void* stream) {
+  TORCH_CHECK(dev >= 0 && dev < 64, "device index ", dev, " out of range");
+  raise_if_lookback_failed(dev);
+  if (mailbox_of(dev) != nullptr) return;
+  // The pinned allocation is left to a call that is not being captured.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) != hipSuccess ||
+      cs != hipStreamCaptureStatusNone)
+    return;
+  Tensor w = at::zeros({1}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+  auto& m = mailboxes();
+  std::lock_guard<std::mutex> lock(m.mu);
+  if (m.word[dev].defined()) return;
+  MX_CALL(mx_set_status_mailbox(reinterpret_cast<unsigned int*>(w.data_ptr<int32_t>())));
+  m.word[dev] = w;
+}
+
+// mx_fbgemm::pending_lookback_faults(device): waits for the device, then
+// returns (and clears) its look-back failure word.
+int64_t pending_lookback_faults(int64_t device) {
+  TORCH_CHECK(device >= 0 && device < 64, "device index ", device, " out of range");
+  c10::DeviceGuard guard(c10::Device(c10::DeviceType::CUDA, static_cast<int8_t>(device)));
+  TORCH_CHECK(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");
+  int32_t* p = mailbox_of(static_cast<int>(device));
+  if (p == nullptr) return 0;
+  const int32_t v = __atomic_load_n(p, __ATOMIC_ACQUIRE);
+  __atomic_store_n(p, 0, __ATOMIC_RELAXED);
+  return v;
+}
+
+// mx_fbgemm::test_force_lookback_giveup(enable): failure-handling tests only --
+// every look-back wait of later calls gives up at once.
+void test_force_lookback_giveup(bool enable) {
+  MX_CALL(mx_test_force_lookback_giveup(enable ? 1 : 0));
 }
 
 int32_t index_bytes_of(const Tensor& t, const char* name) {
@@ -358,13 +438,26 @@ int32_t weights_ty_of(const Tensor& w) {
   return -1;
 }
 
-// Seed of one stochastic-rounding update: drawn from the device's default
-// generator (so torch.manual_seed makes it reproducible) and advanced per call.
-uint64_t next_rounding_seed(const Tensor& on) {
+// Random state of one stochastic-rounding update: the device's default
+// generator (so torch.manual_seed makes it reproducible), advanced per call.
+// philox_cuda_state is torch's capture-safe form: values when eager, device
+// pointers plus this call's offset under graph capture, which the kernel
+// reads when it runs (each replay then draws new bits).
+mx_rng_state next_rounding_state(const Tensor& on) {
   auto gen = at::cuda::detail::getDefaultCUDAGenerator(on.device().index());
   std::lock_guard<std::mutex> lock(gen.mutex());
-  const auto inputs = at::check_generator<at::CUDAGeneratorImpl>(gen)->philox_engine_inputs(4);
-  return inputs.first ^ (inputs.second * 0xD1B54A32D192ED03ull);
+  const at::PhiloxCudaState st =
+      at::check_generator<at::CUDAGeneratorImpl>(gen)->philox_cuda_state(4);
+  mx_rng_state r{};
+  if (st.captured_) {
+    r.seed_dev = st.seed_.ptr;
+    r.offset_dev = st.offset_.ptr;
+    r.offset = st.offset_intragraph_;
+  } else {
+    r.seed = st.seed_.val;
+    r.offset = st.offset_.val;
+  }
+  return r;
 }
 
 Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
@@ -578,6 +671,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  ensure_mailbox(indices.device().index(), stream_of(indices));
   const int64_t T = hash_size_cumsum.numel() - 1;
   TORCH_CHECK(T >= 1 && (vbe || (offsets.numel() - 1) % T == 0),
               "offsets must have T*B+1 entries");
@@ -587,8 +681,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   auto o32 = indices.options().dtype(at::kInt);
   Tensor linear = at::empty({N}, o64), sorted = at::empty({N}, o64);
   Tensor infos = at::empty({N}, o32), run = at::empty({N}, o64);
-  Tensor lengths = at::zeros({N}, o32), num_runs = at::zeros({1}, o32);
-  Tensor cum = at::zeros({N + 1}, o32);
+  // Every entry of lengths and cum is written (past num_runs: 0 and N).
+  Tensor lengths = at::empty({N}, o32), num_runs = at::zeros({1}, o32);
+  Tensor cum = at::empty({N + 1}, o32);
   const size_t ws_bytes = mx_tbe_transpose_workspace_bytes(N, total_hash_size_bits);
   Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
@@ -654,6 +749,7 @@ Tensor backward_rowwise_adagrad_impl(
   TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
   const int32_t ib = index_bytes_of(indices, "indices");
   TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  ensure_mailbox(dev_weights.device().index(), stream_of(dev_weights));
   const int64_t T = D_offsets.numel() - 1;
   TORCH_CHECK(T >= 1 && (vbe.on() || (offsets.numel() - 1) % T == 0),
               "offsets must have T*B+1 entries");
@@ -681,7 +777,7 @@ Tensor backward_rowwise_adagrad_impl(
   }
   // fp16 weights: the update rounds stochastically when asked (fp32: no rounding step).
   const bool sr = wty == MX_SPARSE_FP16 && stochastic_rounding;
-  const uint64_t seed = sr ? next_rounding_seed(dev_weights) : 0;
+  const mx_rng_state rng = sr ? next_rounding_state(dev_weights) : mx_rng_state{};
   if (vbe.on()) {
     const int64_t total_B = offsets.numel() - 1;
     check_vbe(vbe, total_B);
@@ -700,7 +796,7 @@ Tensor backward_rowwise_adagrad_impl(
         momentum1_dev.data_ptr<float>(), momentum1_offsets.data_ptr<int64_t>(),
         static_cast<float>(learning_rate), static_cast<float>(eps),
         static_cast<float>(weight_decay), static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0,
-        seed, ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
+        &rng, ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
     return at::empty({0}, dev_weights.options());
   }
   MX_CALL(mx_tbe_backward_rowwise_adagrad(
@@ -712,7 +808,7 @@ Tensor backward_rowwise_adagrad_impl(
       momentum1_dev.data_ptr<float>(),
       momentum1_offsets.data_ptr<int64_t>(), static_cast<float>(learning_rate),
       static_cast<float>(eps), static_cast<float>(weight_decay),
-      static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0, seed, ws.data_ptr(), ws_bytes,
+      static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0, &rng, ws.data_ptr(), ws_bytes,
       stream_of(dev_weights)));
   return at::empty({0}, dev_weights.options());
 }
@@ -1510,4 +1606,10 @@ TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {
 
 TORCH_LIBRARY_IMPL(fbgemm, CompositeExplicitAutograd, m) {
   m.impl("get_infos_metadata", TORCH_FN(mx_ops::get_infos_metadata));
+}
+
+// Ops of this build that have no fbgemm counterpart.
+TORCH_LIBRARY(mx_fbgemm, m) {
+  m.def("pending_lookback_faults(int device) -> int", &mx_ops::pending_lookback_faults);
+  m.def("test_force_lookback_giveup(bool enable) -> ()", &mx_ops::test_force_lookback_giveup);
 }

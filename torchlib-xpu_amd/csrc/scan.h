@@ -72,9 +72,41 @@ __device__ __forceinline__ int64_t eff_len(int64_t n, const int32_t* n_dev) {
 // took earlier tickets, which are already running and publish their
 // aggregate before they wait themselves, so every wait ends.  The status
 // words and the ticket must be zero before the launch.
+// A look-back that exhausts its spin bound (never expected: a predecessor
+// holds an earlier ticket and publishes without waiting) marks the call as
+// failed: `fail` is a word of the call's zeroed workspace that every later
+// kernel of the call checks before it uses the results, and `mailbox`, when
+// the caller registered one for the device, is a host-visible word through
+// which the failure reaches the host.  Partial prefixes are never larger than
+// the true ones, so the stores made before the check stay in bounds.
+struct Faults {
+  unsigned int* fail;
+  unsigned int* mailbox;  // may be null
+  int spin_limit;         // > 0: spins before giving up; < 0: give up at once (test hook)
+};
+
+__device__ __forceinline__ void report_fault(const Faults& f) {
+  __hip_atomic_store(f.fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (f.mailbox) __hip_atomic_store(f.mailbox, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// True when an earlier kernel of the call gave up (block-uniform).
+__device__ __forceinline__ bool call_failed(const unsigned int* fail) {
+  return fail != nullptr &&
+         __hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+}
+
+// One more spin of a bounded wait; false once the wait must give up.
+__device__ __forceinline__ bool keep_waiting(int& spins, const Faults& f) {
+  if (++spins > f.spin_limit) return false;
+  __builtin_amdgcn_s_sleep(1);
+  return true;
+}
+
 struct ScanState {
   unsigned long long* status;  // one word per tile
-  unsigned int* ticket;        // [0] next tile, [1] set if a look-back gave up
+  unsigned int* ticket;        // [0] next tile
+  Faults faults;
 };
 
 constexpr unsigned long long kScanFlagAgg = 1ull << 62;
@@ -90,7 +122,12 @@ __global__ void __launch_bounds__(kScanThreads)
                         int64_t ntiles) {
   (void)ntiles;
   __shared__ uint32_t s_tile, s_prefix;
-  if (threadIdx.x == 0) s_tile = atomicAdd(st.ticket, 1u);
+  __shared__ bool s_gave_up;
+  if (call_failed(st.faults.fail)) return;  // the input of this scan is not valid
+  if (threadIdx.x == 0) {
+    s_tile = atomicAdd(st.ticket, 1u);
+    s_gave_up = false;
+  }
   __syncthreads();
   const int64_t tile = s_tile;
   const int64_t m = eff_len(n, n_dev);
@@ -124,17 +161,26 @@ __global__ void __launch_bounds__(kScanThreads)
       int64_t j = tile - 1;  // nearest predecessor not yet folded in
       int spins = 0;
       while (true) {
+        if (st.faults.spin_limit < 0) {  // test hook: give up at once
+          if (lane == 0) {
+            report_fault(st.faults);
+            s_gave_up = true;
+          }
+          break;
+        }
         const int64_t idx = j - lane;
         const unsigned long long w =
             idx >= 0 ? __hip_atomic_load(&st.status[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                      : (kScanFlagIncl | Op::identity());  // before tile 0
         const unsigned long long flag = w >> 62;
         if (__ballot(flag == 0) != 0ull) {  // some predecessor has not published yet
-          if (++spins > kScanSpinLimit) {   // never expected; keeps the wait bounded
-            if (lane == 0) st.ticket[1] = 1u;
+          if (!keep_waiting(spins, st.faults)) {  // never expected; keeps the wait bounded
+            if (lane == 0) {
+              report_fault(st.faults);
+              s_gave_up = true;
+            }
             break;
           }
-          __builtin_amdgcn_s_sleep(1);
           continue;
         }
         const unsigned long long incl = __ballot(flag == 2);
@@ -153,10 +199,11 @@ __global__ void __launch_bounds__(kScanThreads)
     }
     if (lane == 0) {
       s_prefix = prefix;
-      if (tile == last) epi.total(Op::apply(prefix, tile_total));
+      if (tile == last && !s_gave_up) epi.total(Op::apply(prefix, tile_total));
     }
   }
   __syncthreads();
+  if (s_gave_up) return;  // block-uniform; later kernels see the failure
   uint32_t run = Op::apply(s_prefix, excl);
 #pragma unroll
   for (int it = 0; it < kScanItems; ++it) {

@@ -222,14 +222,14 @@ __global__ void __launch_bounds__(256)
 constexpr unsigned long long kSweepAgg = 1ull << 62;
 constexpr unsigned long long kSweepIncl = 2ull << 62;
 
-// status: [tiles][kRadix] zeroed words; ticket: zeroed [2] (next tile, give-up
-// flag).  ghist: this pass's global digit counts.
+// status: [tiles][kRadix] zeroed words; ticket: zeroed next-tile counter.
+// ghist: this pass's global digit counts.
 template <bool LAST>
 __global__ void __launch_bounds__(256)
     onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
                     const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
                     const uint32_t* __restrict__ ghist, unsigned long long* status,
-                    unsigned int* ticket, uint32_t* __restrict__ keys_out,
+                    unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
                     int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
                     uint32_t* __restrict__ vals2_out) {
   __shared__ unsigned int s_tile;
@@ -237,6 +237,7 @@ __global__ void __launch_bounds__(256)
   __shared__ uint32_t s_base[kRadix];
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  if (call_failed(faults.fail)) return;  // an earlier pass gave up: nothing valid to sort
   if (threadIdx.x == 0) s_tile = atomicAdd(ticket, 1u);
   for (int i = threadIdx.x; i < 4 * kRadix; i += 256) (&cnt[0][0])[i] = 0u;
   __syncthreads();
@@ -296,6 +297,10 @@ __global__ void __launch_bounds__(256)
       int64_t j = tile - 1;  // nearest predecessor not yet folded in
       int spins = 0;
       bool done = false;
+      if (faults.spin_limit < 0) {  // test hook: give up at once
+        report_fault(faults);
+        done = true;
+      }
       while (!done) {
         unsigned long long x[kLookBack];
 #pragma unroll
@@ -314,12 +319,11 @@ __global__ void __launch_bounds__(256)
           if (flag == 2ull) done = true;
         }
         j -= folded;
-        if (!done && folded < kLookBack) {  // waiting on an unpublished predecessor
-          if (++spins > kScanSpinLimit) {   // never expected; keeps the wait bounded
-            ticket[1] = 1u;
+        if (!done && folded < kLookBack) {     // waiting on an unpublished predecessor
+          if (!keep_waiting(spins, faults)) {  // never expected; keeps the wait bounded
+            report_fault(faults);
             break;
           }
-          __builtin_amdgcn_s_sleep(1);
         }
       }
       __hip_atomic_store(mine, kSweepIncl | (prefix + total), __ATOMIC_RELAXED,
@@ -333,7 +337,7 @@ __global__ void __launch_bounds__(256)
     if (i0 + it * 64 >= n) continue;
     const uint32_t dd = (k[it] >> shift) & mask;
     const uint32_t pos = s_base[dd] + cnt[w][dd] + rank[it];
-    if (pos >= n) continue;  // only after a look-back gave up; keeps stores in bounds
+    if (pos >= n) continue;  // never, unless a look-back gave up; keeps stores in bounds
     if constexpr (LAST)
       keys_out64[pos] = static_cast<int64_t>(k[it]);
     else
@@ -395,13 +399,23 @@ struct RleEpi {
   }
 };
 
+// run_lengths[r] = cum[r+1] - cum[r] for the num_runs runs; past them the
+// arrays read as the complete cumsum of zero-padded lengths: run_lengths 0,
+// cum N.  (Threads r >= m write cum[r+1] > m, threads r < m read cum[<= m]:
+// no overlap.)
 __global__ void __launch_bounds__(256)
-    run_lengths_kernel(const int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
-                       int64_t n, int32_t* __restrict__ lengths) {
+    run_lengths_kernel(int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
+                       int64_t n, int32_t* __restrict__ lengths, const unsigned int* fail) {
+  if (call_failed(fail)) return;  // num_runs was never written
   const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t m = *num_runs;
-  if (r >= m || r >= n) return;
-  lengths[r] = cum[r + 1] - cum[r];
+  if (r >= n) return;
+  if (r < m) {
+    lengths[r] = cum[r + 1] - cum[r];
+  } else {
+    lengths[r] = 0;
+    cum[r + 1] = static_cast<int32_t>(n);
+  }
 }
 
 struct ChunkCount {
@@ -447,8 +461,10 @@ struct SortWs {
   uint32_t* keys[2];
   uint32_t* vals[2];
   uint32_t* vals2[2];  // per-sample weights (weighted backward only)
-  // Zeroed before every call, contiguous: scan slots, digit histograms, sweep state.
+  // Zeroed before every call, contiguous: call status, scan slots, digit
+  // histograms, chunk marks, sweep state.
   unsigned long long* zeroed;
+  unsigned int* fail;              // set when a look-back of the call gave up
   unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
   uint32_t* ghist;                 // [kMaxPasses][kRadix]
@@ -476,12 +492,16 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   }
   w.scan_slot_words = align256(slot_words * 8) / 8;
   w.sweep_words = sweep_pass_words(n);
+  constexpr size_t status_bytes = 256;
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
   const size_t hist_bytes = align256(kMaxPasses * kRadix * 4);
   const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
-  uint8_t* z = take(scan_bytes + hist_bytes + mark_bytes + kMaxPasses * w.sweep_words * 8);
+  uint8_t* z = take(status_bytes + scan_bytes + hist_bytes + mark_bytes +
+                    kMaxPasses * w.sweep_words * 8);
   w.zeroed = reinterpret_cast<unsigned long long*>(z);
-  w.scan_state = w.zeroed;
+  w.fail = reinterpret_cast<unsigned int*>(z);
+  if (z) z += status_bytes;
+  w.scan_state = reinterpret_cast<unsigned long long*>(z);
   w.ghist = z ? reinterpret_cast<uint32_t*>(z + scan_bytes) : nullptr;
   w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + scan_bytes + hist_bytes) : nullptr;
   w.sweep = z ? reinterpret_cast<unsigned long long*>(z + scan_bytes + hist_bytes + mark_bytes)
@@ -499,10 +519,16 @@ int64_t zeroed_words(const SortWs& w, int passes) {
          passes * w.sweep_words;
 }
 
-// Scan-state slot i: status words, then the ticket pair in the last word.
+// Where the call's look-backs report a give-up.
+Faults call_faults(const SortWs& w) {
+  return Faults{w.fail, status_mailbox(), lookback_spin_limit(kScanSpinLimit)};
+}
+
+// Scan-state slot i: status words, then the ticket in the last word.
 ScanState scan_slot(const SortWs& w, int i) {
   unsigned long long* base = w.scan_state + i * w.scan_slot_words;
-  return ScanState{base, reinterpret_cast<unsigned int*>(base + w.scan_slot_words - 1)};
+  return ScanState{base, reinterpret_cast<unsigned int*>(base + w.scan_slot_words - 1),
+                   call_faults(w)};
 }
 
 struct TransposeOut {
@@ -561,14 +587,15 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     unsigned long long* st = w.sweep + p * w.sweep_words;
     unsigned int* ticket = reinterpret_cast<unsigned int*>(st + ntiles * kRadix);
     const uint32_t* gh = w.ghist + p * kRadix;
+    const Faults f = call_faults(w);
     if (p == passes - 1) {
       onesweep_kernel<true><<<gsweep, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, nullptr, o.sorted,
-          reinterpret_cast<uint32_t*>(o.infos), v2_final);
+          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f, nullptr,
+          o.sorted, reinterpret_cast<uint32_t*>(o.infos), v2_final);
     } else {
       onesweep_kernel<false><<<gsweep, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, w.keys[cur ^ 1],
-          nullptr, w.vals[cur ^ 1], v2[cur ^ 1]);
+          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f,
+          w.keys[cur ^ 1], nullptr, w.vals[cur ^ 1], v2[cur ^ 1]);
     }
     MX_LAUNCH_CHECK();
     cur ^= 1;
@@ -580,7 +607,7 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
                                scan_slot(w, 0), s))
     return rc;
   if (o.run_lengths) {
-    run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths);
+    run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths, w.fail);
     MX_LAUNCH_CHECK();
   }
   return MX_OK;
@@ -610,6 +637,7 @@ struct BwdArgs {
   const uint32_t* chunk_mark;  // chunk marks (kMarkEvery), from the chunk-count scan
   const uint32_t* total_chunks;
   float* partial;
+  const unsigned int* fail;  // set when a look-back of the call gave up: nothing is updated
   int64_t B;
   int64_t total_D;
   int32_t T;
@@ -621,8 +649,21 @@ struct BwdArgs {
   float eps;
   float wd;
   int32_t sr;     // fp16 weights: stochastic rounding instead of round-to-nearest-even
-  uint64_t seed;  // random bits of the stochastic rounding: hash(seed, element)
+  // Random state of the stochastic rounding: (seed, offset) as values, or read
+  // when the kernel runs from seed_dev / offset_dev (+ offset) -- the form a
+  // graph-captured call carries, so each replay draws new bits.
+  uint64_t seed;
+  uint64_t offset;
+  const int64_t* seed_dev;
+  const int64_t* offset_dev;
 };
+
+// The call's 64-bit rounding key: seed ^ (offset * odd constant).
+__device__ __forceinline__ uint64_t rounding_key(const BwdArgs& a) {
+  const uint64_t seed = a.seed_dev ? static_cast<uint64_t>(*a.seed_dev) : a.seed;
+  const uint64_t off = a.offset_dev ? static_cast<uint64_t>(*a.offset_dev) + a.offset : a.offset;
+  return seed ^ (off * 0xD1B54A32D192ED03ull);
+}
 
 // Per-table metadata, staged in LDS when T is small enough.
 struct TableMeta {
@@ -793,17 +834,19 @@ __device__ __forceinline__ __half round_half_sr(float x, uint32_t rnd) {
   return __float2half_rz(x + noise);
 }
 
-__device__ __forceinline__ void st_row4(const BwdArgs&, float* p, int64_t, const float (&v)[4]) {
+__device__ __forceinline__ void st_row4(const BwdArgs&, uint64_t, float* p, int64_t,
+                                        const float (&v)[4]) {
   st4(p, v);
 }
 
-// elem: index of p[0] in the weights buffer (keys the random bits).
-__device__ __forceinline__ void st_row4(const BwdArgs& a, __half* p, int64_t elem,
+// elem: index of p[0] in the weights buffer; key: the call's rounding key
+// (together they key the random bits).
+__device__ __forceinline__ void st_row4(const BwdArgs& a, uint64_t key, __half* p, int64_t elem,
                                         const float (&v)[4]) {
   __half h[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    h[e] = a.sr ? round_half_sr(v[e], sr_bits(a.seed, static_cast<uint64_t>(elem + e)))
+    h[e] = a.sr ? round_half_sr(v[e], sr_bits(key, static_cast<uint64_t>(elem + e)))
                 : __float2half_rn(v[e]);
   uint2 x;
   x.x = static_cast<uint32_t>(__half_as_ushort(h[0])) |
@@ -840,13 +883,14 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
     corr = 1.0f - mult * a.wd;
   else if (a.wd_mode == 2)
     corr = 1.0f - a.lr * a.wd;
+  const uint64_t key = a.sr ? rounding_key(a) : 0ull;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if ((c * G + k) * 4 >= D) continue;
     float nw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) nw[e] = __builtin_fmaf(-mult, gs[c][e], __fmul_rn(corr, w[c][e]));
-    st_row4(a, wrow + (c * G + k) * 4, row0 + (c * G + k) * 4, nw);
+    st_row4(a, key, wrow + (c * G + k) * 4, row0 + (c * G + k) * 4, nw);
   }
   if (k == 0) *hp = h;
 }
@@ -862,6 +906,7 @@ constexpr int kLongRange = 4;  // chunks per block range
 
 template <typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
+  if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
   constexpr int NG = 256 / G;
   __shared__ float part[NG][G * NCH * 4];
@@ -952,6 +997,7 @@ __global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
 // Pass A: one group per chunk of a long run -> partial sum in the workspace.
 template <typename I, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
+  if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
   stage_meta(a, meta);
   const MetaView mv{a, meta, a.T <= kMaxCachedTables};
@@ -996,6 +1042,7 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
 // gradient sum.
 template <typename I, typename WT, int G, int NCH, int U>
 __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
+  if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
   stage_meta(a, meta);
   const MetaView mv{a, meta, a.T <= kMaxCachedTables};
@@ -1075,12 +1122,11 @@ int launch_short_runs(const BwdArgs& a, int64_t N, hipStream_t s) {
 // and long-run kernels.
 template <typename I, typename WT, int G, int NCH>
 int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
-  hipStream_t side = side_stream();
-  hipEvent_t fork = nullptr, join = nullptr;
-  if (side == nullptr || hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess ||
-      hipEventRecord(fork, s) != hipSuccess || hipStreamWaitEvent(side, fork, 0) != hipSuccess)
-    side = s;  // one stream: the same kernels in order
+  SidePath sp{};
+  hipStream_t side = s;  // without a second stream: the same kernels in order
+  if (side_path(s, &sp) && hipEventRecord(sp.fork, s) == hipSuccess &&
+      hipStreamWaitEvent(sp.side, sp.fork, 0) == hipSuccess)
+    side = sp.side;
   int rc = prefix_scan_epi(
       ChunkCount{a.cum}, N, reinterpret_cast<const int32_t*>(a.num_runs),
       ChunkEpi{a.cum, chunk_start, ws.chunk_mark, &ws.counters[1]},
@@ -1088,13 +1134,12 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
   if (rc == MX_OK) rc = launch_long_runs<I, WT, G, NCH>(a, N, side);
   const int rc_short = launch_short_runs<I, WT, G, NCH>(a, N, s);
   if (side != s) {
-    if (hipEventRecord(join, side) != hipSuccess || hipStreamWaitEvent(s, join, 0) != hipSuccess) {
+    if (hipEventRecord(sp.join, side) != hipSuccess ||
+        hipStreamWaitEvent(s, sp.join, 0) != hipSuccess) {
       (void)hipStreamSynchronize(side);  // nothing may outlive the call unordered
       if (rc == MX_OK) rc = set_error(MX_EHIP, "joining the long-run stream failed");
     }
   }
-  if (fork) (void)hipEventDestroy(fork);
-  if (join) (void)hipEventDestroy(join);
   return rc != MX_OK ? rc : rc_short;
 }
 
@@ -1227,7 +1272,7 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
                   int32_t pooling_mode, const float* indice_weights, const float* grad_output,
                   int64_t total_D, float* momentum1, const int64_t* momentum1_offsets,
                   float learning_rate, float eps, float weight_decay, int32_t weight_decay_mode,
-                  int32_t stochastic_rounding, uint64_t seed, void* workspace,
+                  int32_t stochastic_rounding, const mx_rng_state* rng, void* workspace,
                   size_t workspace_bytes, void* stream) {
   if (int rc = check_common(T, B, lay, total_hash_size_bits, nb, index_bytes, N)) return rc;
   MX_REQUIRE(max_D > 0 && max_D <= 1024 && max_D % 4 == 0,
@@ -1273,6 +1318,7 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   a.T = T;
   a.total_chunks = &w.sort.counters[1];
   a.partial = w.partial;
+  a.fail = w.sort.fail;
   a.B = B;
   a.total_D = total_D;
   a.max_D = max_D;
@@ -1283,7 +1329,11 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   a.eps = eps;
   a.wd = weight_decay;
   a.sr = stochastic_rounding != 0 ? 1 : 0;
-  a.seed = seed;
+  MX_REQUIRE(!a.sr || rng != nullptr, "stochastic rounding needs a random state");
+  a.seed = a.sr ? rng->seed : 0;
+  a.offset = a.sr ? rng->offset : 0;
+  a.seed_dev = a.sr ? rng->seed_dev : nullptr;
+  a.offset_dev = a.sr ? rng->offset_dev : nullptr;
   if (weights_ty == MX_SPARSE_FP16)
     return index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, w.sort, w.chunk_start, N, s)
                             : dispatch_bwd<int32_t, __half>(a, w.sort, w.chunk_start, N, s);
@@ -1336,8 +1386,8 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
     const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
     int32_t pooling_mode, const float* indice_weights, const float* grad_output, int64_t total_D,
     float* momentum1, const int64_t* momentum1_offsets, float learning_rate, float eps,
-    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed,
-    void* workspace, size_t workspace_bytes, void* stream) {
+    float weight_decay, int32_t weight_decay_mode, int32_t stochastic_rounding,
+    const mx_rng_state* rng, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   const int32_t nb = mx_tbe_info_B_num_bits(T, B);
   MX_REQUIRE(nb > 0, "T=%d, B=%lld do not fit a 32-bit info word", T, (long long)B);
@@ -1346,7 +1396,7 @@ extern "C" int mx_tbe_backward_rowwise_adagrad(
                        hash_size_cumsum, total_hash_size_bits, indices, offsets, index_bytes, N,
                        pooling_mode, indice_weights, grad_output, total_D, momentum1,
                        momentum1_offsets, learning_rate, eps, weight_decay, weight_decay_mode,
-                       stochastic_rounding, seed, workspace, workspace_bytes, stream);
+                       stochastic_rounding, rng, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mx_tbe_backward_rowwise_adagrad_vbe(
@@ -1357,8 +1407,8 @@ extern "C" int mx_tbe_backward_rowwise_adagrad_vbe(
     int64_t total_B, const int32_t* B_offsets, const int64_t* vbe_row_output_offsets,
     const int32_t* vbe_b_t_map, int32_t info_B_num_bits, float* momentum1,
     const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
-    int32_t weight_decay_mode, int32_t stochastic_rounding, uint64_t seed, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    int32_t weight_decay_mode, int32_t stochastic_rounding, const mx_rng_state* rng,
+    void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   MX_REQUIRE(total_B == 0 || (B_offsets && vbe_row_output_offsets && vbe_b_t_map),
              "VBE needs B_offsets, row output offsets and the b_t map");
@@ -1367,6 +1417,6 @@ extern "C" int mx_tbe_backward_rowwise_adagrad_vbe(
                        info_B_num_bits, lay, max_D, hash_size_cumsum, total_hash_size_bits,
                        indices, offsets, index_bytes, N, pooling_mode, indice_weights,
                        grad_output, 0, momentum1, momentum1_offsets, learning_rate, eps,
-                       weight_decay, weight_decay_mode, stochastic_rounding, seed, workspace,
+                       weight_decay, weight_decay_mode, stochastic_rounding, rng, workspace,
                        workspace_bytes, stream);
 }

@@ -43,6 +43,8 @@ HIPCC_FLAGS = [
     # Packed FP32 VALU forms are kept out of every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
+    "-Wextra",
+    "-Werror",
     "-Wno-unused-command-line-argument",
 ]
 
@@ -96,7 +98,8 @@ def build_ops(verbose: bool = False) -> Path:
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     tmp = OPS_LIB.with_suffix(".so.tmp")
     cmd = [
-        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-parameter",
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Werror",
+        "-Wno-unused-parameter",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
         "-DTORCH_EXTENSION_NAME=mx_fbgemm_ops", "-DTORCH_API_INCLUDE_EXTENSION_H",
         *inc, f"-I{ROCM / 'include'}", f"-I{INCLUDE}",
