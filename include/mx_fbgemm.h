@@ -326,6 +326,20 @@ int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T, int64_t B,
                             int64_t* warning, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* No counterpart in the reference or in fbgemm_gpu: mx_bounds_check_indices
+ * for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, semantics and
+ * results, without the workspace: the scratch (at most 1024 per-tile offset
+ * maxima, 4 KiB) is a static device array of the library, one per device,
+ * held until the process ends.  Every batch fits it (tiles widen with the
+ * batch, at most 1024 of them); a scratch need above 4 KiB would return
+ * MX_EWORKSPACE instead of running.  Calls that overlap on one device
+ * (two streams, or two threads, at once) share that array and race; calls
+ * in stream order do not.  Nothing is allocated. */
+int mx_bounds_check_indices_noalloc(const int64_t* rows_per_table, int32_t T, int64_t B,
+                                    void* indices, void* offsets, int32_t index_bytes, int64_t N,
+                                    int32_t mode, int64_t* warning, void* stream);
+
 /* VBE variant (fbgemm's B_offsets argument): total_B bags, bag i of table t
  * for B_offsets[t] <= i < B_offsets[t+1]; workspace from
  * mx_bounds_check_workspace_bytes_vbe(total_B). */

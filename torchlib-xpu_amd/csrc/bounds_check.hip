@@ -23,8 +23,17 @@
 // reads it before or after the repair computes the same o' (the maximum of a
 // prefix is unchanged when some of its entries are replaced by their own
 // prefix maxima), so no block waits on another.
+#include <mutex>
+
 #include "mx_common.h"
 #include "scan.h"
+
+// Scratch of mx_bounds_check_indices_noalloc: the per-tile offset maxima (at
+// most 1024 tiles for any batch), one copy per device, held until the process
+// ends.  Host code never passes this name to a kernel (on the host it is a
+// stand-in, not a device address): it uses the address hipGetSymbolAddress
+// returns for the current device.
+static __device__ __align__(256) uint32_t scratch[1024];
 
 namespace mx {
 namespace {
@@ -249,6 +258,51 @@ extern "C" int mx_bounds_check_indices(const int64_t* rows_per_table, int32_t T,
   clear_error();
   return bounds_impl(rows_per_table, T, B, static_cast<int64_t>(T) * B, nullptr, indices,
                      offsets, index_bytes, N, mode, warning, workspace, workspace_bytes, stream);
+}
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[64] = {};
+
+// Device address of `scratch` on the current device, looked up on the
+// device's first call (with that device current) and kept.
+int scratch_address(void** out) {
+  int dev = 0;
+  MX_HIP_CHECK(hipGetDevice(&dev));
+  MX_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    MX_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MX_REQUIRE(p != nullptr, "no device address for the bounds-check scratch");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_bounds_check_indices_noalloc(const int64_t* rows_per_table, int32_t T,
+                                               int64_t B, void* indices, void* offsets,
+                                               int32_t index_bytes, int64_t N, int32_t mode,
+                                               int64_t* warning, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0, "negative size");
+  const int64_t nbags = static_cast<int64_t>(T) * B;
+  const size_t need = carve_bounds(nullptr, nbags).bytes;
+  if (need > sizeof(scratch))
+    return set_error(MX_EWORKSPACE,
+                     "T*B = %lld bags need %zu bytes of scratch, above the %zu bytes this entry "
+                     "point holds; use mx_bounds_check_indices with a workspace",
+                     (long long)nbags, need, sizeof(scratch));
+  void* ws = nullptr;
+  if (int rc = scratch_address(&ws)) return rc;
+  // Every tile maximum the main kernel reads is written by the tile kernel of
+  // the same call first, so the scratch needs no clearing.
+  return bounds_impl(rows_per_table, T, B, nbags, nullptr, indices, offsets, index_bytes, N,
+                     mode, warning, ws, sizeof(scratch), stream);
 }
 
 extern "C" size_t mx_bounds_check_workspace_bytes_vbe(int64_t total_B) {
