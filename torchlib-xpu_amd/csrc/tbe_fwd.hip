@@ -95,12 +95,101 @@ struct BagMap {
 
 namespace {
 
+// A buffer descriptor of a wave-uniform table base: stride 0 and the whole
+// 32-bit offset range (callers keep every offset below 2^32), gfx9 format word.
+template <typename WT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t table_rsrc(const WT* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<WT*>(base), 0, 0xffffffff, 0x00020000);
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Four consecutive weights at byte `off` of the table as fp32.
+__device__ __forceinline__ void buf_row4(__amdgpu_buffer_rsrc_t r, uint32_t off, const float*,
+                                         float (&v)[4]) {
+  const i32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  v[0] = __int_as_float(x.x);
+  v[1] = __int_as_float(x.y);
+  v[2] = __int_as_float(x.z);
+  v[3] = __int_as_float(x.w);
+}
+
+__device__ __forceinline__ void buf_row4(__amdgpu_buffer_rsrc_t r, uint32_t off, const __half*,
+                                         float (&v)[4]) {
+  const i32x2 x = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  v[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.x & 0xffff)));
+  v[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(static_cast<uint32_t>(x.x) >> 16)));
+  v[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(x.y & 0xffff)));
+  v[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(static_cast<uint32_t>(x.y) >> 16)));
+}
+
+// Adds the n rows of one batch of a bag to the group's accumulators, U rows
+// in flight per lane.  Lane j of the group holds row j's location: its byte
+// offset in the wave's table (BUF: buffer loads off one descriptor, a 32-bit
+// offset per lane) or its element offset (64-bit global addresses).  The loop
+// body has no branch: every one of the U loads is issued (slots past the
+// batch re-read its last row, from cache) and the sums take only the rows of
+// the batch, through a select, so each column still adds exactly its rows in
+// index order.  Straight-line code lets the compiler keep the U loads in
+// flight together instead of waiting on each one.
+template <bool BUF, typename WT, int G, int NCH, int U, bool WEIGHTED>
+__device__ __forceinline__ void pool_batch(uint64_t my_off, float my_w, int n, int g,
+                                           const WT* const (&lane_col)[NCH],
+                                           __amdgpu_buffer_rsrc_t rsrc,
+                                           const uint32_t (&lane_byte)[NCH],
+                                           float (&acc)[NCH][4]) {
+  for (int j = 0; j < n; j += U) {
+    float v[U][NCH][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = j + u < n ? j + u : n - 1;
+      if constexpr (BUF) {
+        const uint32_t off = __shfl(static_cast<uint32_t>(my_off), g * G + r, 64);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) buf_row4(rsrc, off + lane_byte[c], lane_col[c], v[u][c]);
+      } else {
+        const uint64_t off = __shfl(my_off, g * G + r, 64);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) load_row4(lane_col[c] + off, v[u][c]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool take = j + u < n;
+      float wgt = 1.0f;
+      if constexpr (WEIGHTED) wgt = __shfl(my_w, g * G + (take ? j + u : n - 1), 64);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x;
+          if constexpr (WEIGHTED)
+            x = __builtin_fmaf(wgt, v[u][c][e], acc[c][e]);
+          else
+            x = acc[c][e] + v[u][c][e];
+          acc[c][e] = take ? x : acc[c][e];
+        }
+    }
+  }
+}
+
+// Waves per SIMD an instance is compiled for: 8 (a 64-register budget) where
+// that fits without spilling -- one float4 chunk per lane, unweighted, int64
+// indices -- so that 16k waves of a D=128 batch run in 2 rounds instead of
+// 2.3; the compiler's own choice elsewhere.
+template <typename I, int NCH, bool WEIGHTED>
+constexpr int fwd_waves() {
+  return (NCH == 1 && !WEIGHTED && sizeof(I) == 8) ? 8 : 1;
+}
+
 // A wave serves 64/G bags at once, G lanes per bag, lane k owning columns
 // (c*G + k)*4 .. +4 (float4 loads: a D=128 row is one 512 B access of 32
 // lanes).  Several bags per wave keep several independent offsets -> indices
 // -> rows chains in flight; each column is still summed in index order.
 template <typename I, typename WT, int G, int NCH, int U, bool WEIGHTED, bool OUT_F16>
 __global__ void __launch_bounds__(256)
+    __attribute__((amdgpu_waves_per_eu(fwd_waves<I, NCH, WEIGHTED>())))
     tbe_fwd_group_kernel(const WT* __restrict__ W, const int64_t* __restrict__ w_off,
                          const int32_t* __restrict__ D_off, BagMap bm,
                          const I* __restrict__ indices, const I* __restrict__ offsets,
@@ -110,7 +199,8 @@ __global__ void __launch_bounds__(256)
   const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
-  const int64_t bag = (lb * kWavesPerBlock + (threadIdx.x >> 6)) * P + g;
+  const int64_t wbag = (lb * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * P;
+  const int64_t bag = wbag + g;
   if (bag >= nbags) return;  // whole group
   int64_t t, b;
   bm.locate(bag, t, b);
@@ -119,6 +209,11 @@ __global__ void __launch_bounds__(256)
   const WT* __restrict__ Wt = W + w_off[t];
   const int64_t start = static_cast<int64_t>(offsets[bag]);
   const int64_t end = static_cast<int64_t>(offsets[bag + 1]);
+  // When the wave's bags share one table (a fixed batch of even B, or most
+  // waves of any batch), its rows are read through one buffer descriptor.
+  const int64_t tw = readlane_i64(t, __builtin_amdgcn_readfirstlane(lane));
+  const bool one_table = __all(t == tw);  // wave-uniform
+  const __amdgpu_buffer_rsrc_t rsrc = table_rsrc(W + w_off[tw]);
 
   float acc[NCH][4];
 #pragma unroll
@@ -126,50 +221,44 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[c][e] = 0.0f;
   bool active[NCH];
-  const WT* lane_col[NCH];  // this lane's first column of each chunk, row 0
+  const WT* lane_col[NCH];   // this lane's first column of each chunk, row 0
+  uint32_t lane_byte[NCH];   // the same as a byte offset in the table
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     active[c] = (c * G + k) * 4 < D;
-    lane_col[c] = Wt + (c * G + k) * 4;
+    // A chunk past the row's end reads the row's first columns instead (never
+    // stored), so that no load sits behind a branch.
+    const int col = active[c] ? (c * G + k) * 4 : 0;
+    lane_col[c] = Wt + col;
+    lane_byte[c] = static_cast<uint32_t>(col * sizeof(WT));
   }
 
+  // The group's indices come G at a time, one batch ahead of its rows, so a
+  // bag longer than G does not wait for its next batch of indices.
+  I nxt_idx = start + k < end ? indices[start + k] : I(0);
+  float nxt_w = 0.0f;
+  if constexpr (WEIGHTED) nxt_w = start + k < end ? iw[start + k] : 0.0f;
   for (int64_t base = start; base < end; base += G) {
     const int n = static_cast<int>(end - base < G ? end - base : G);
-    // The lane that loads an index also turns it into the row's element
-    // offset, once, instead of every lane of the group per row.
-    const int64_t my_off = k < n ? static_cast<int64_t>(indices[base + k]) * D : 0;
-    float my_w = 0.0f;
-    if constexpr (WEIGHTED) my_w = k < n ? iw[base + k] : 0.0f;
-    for (int j = 0; j < n; j += U) {
-      float v[U][NCH][4];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (j + u < n) {
-          const int64_t off = __shfl(my_off, g * G + j + u, 64);
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-            if (active[c]) load_row4(lane_col[c] + off, v[u][c]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (j + u < n) {
-          float wgt = 1.0f;
-          if constexpr (WEIGHTED) wgt = __shfl(my_w, g * G + j + u, 64);
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-            if (active[c]) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                if constexpr (WEIGHTED)
-                  acc[c][e] = __builtin_fmaf(wgt, v[u][c][e], acc[c][e]);
-                else
-                  acc[c][e] += v[u][c][e];
-              }
-            }
-        }
-      }
+    const I cur_idx = nxt_idx;
+    [[maybe_unused]] const float my_w = nxt_w;
+    if (base + G + k < end) {
+      nxt_idx = indices[base + G + k];
+      if constexpr (WEIGHTED) nxt_w = iw[base + G + k];
     }
+    // The lane that loads an index also turns it into the row's offset,
+    // once, instead of every lane of the group per row: in bytes for buffer
+    // loads when every row of the batch ends below 4 GiB into its table (one
+    // 32-bit word per row between lanes, one 32-bit add per load), else in
+    // elements for 64-bit addresses.
+    const uint64_t my_elem = k < n ? static_cast<uint64_t>(cur_idx) * static_cast<uint64_t>(D) : 0;
+    const uint64_t my_end = (my_elem + static_cast<uint64_t>(D)) * sizeof(WT);
+    if (one_table && __all(my_end <= 0xffffffffull))  // wave-uniform
+      pool_batch<true, WT, G, NCH, U, WEIGHTED>(my_elem * sizeof(WT), my_w, n, g, lane_col, rsrc,
+                                               lane_byte, acc);
+    else  // a wave over two tables, or a table past 4 GiB: half the rows in flight
+      pool_batch<false, WT, G, NCH, (U > 1 ? U / 2 : 1), WEIGHTED>(my_elem, my_w, n, g, lane_col,
+                                                                 rsrc, lane_byte, acc);
   }
   const int64_t L = end - start;
   if (pooling == MX_POOL_MEAN && L > 0) {
@@ -270,11 +359,16 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Rows in flight per lane when a lane owns one float4 column chunk.
+#ifndef MX_FWD_U1
+#define MX_FWD_U1 8
+#endif
+
 template <typename I, typename WT, int G, int NCH, bool WEIGHTED, bool OUT_F16>
 void launch_fwd_group(hipStream_t s, const WT* W, const int64_t* w_off, const int32_t* D_off,
                       const BagMap& bm, const void* idx, const void* off, int32_t pooling,
                       const float* iw, void* out, int64_t nbags) {
-  constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
+  constexpr int U = NCH <= 1 ? MX_FWD_U1 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
   constexpr int P = 64 / G;
   const int64_t grid = ceil_div(nbags, kWavesPerBlock * P);
   tbe_fwd_group_kernel<I, WT, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
@@ -290,8 +384,13 @@ int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off
   launch_fwd_group<I, WT, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, bm, idx, off, pooling, iw, out, nbags)
   if (max_D <= 64)
     MX_FWD_G(16, 1);  // 4 bags per wave
+#ifdef MX_FWD_G16_D128
+  else if (max_D <= 128)
+    MX_FWD_G(16, 2);  // 4 bags per wave, 16 lanes x 2 x 16 B per row
+#else
   else if (max_D <= 128)
     MX_FWD_G(32, 1);  // 2 bags per wave, one D=128 row per 32 lanes x 16 B
+#endif
   else if (max_D <= 256)
     MX_FWD_G(64, 1);
   else if (max_D <= 512)
