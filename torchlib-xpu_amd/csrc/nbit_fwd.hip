@@ -23,6 +23,11 @@
 
 #include "mx_common.h"
 
+// Waves per block: a block ranks its waves x 64/G bags by length.
+#ifndef MX_NBIT_WPB
+#define MX_NBIT_WPB 4
+#endif
+
 // Bytes of row data each lane keeps in flight (sets the rows loaded before
 // any is accumulated).
 #ifndef MX_NBIT_INFLIGHT_BYTES
@@ -42,7 +47,7 @@ struct NbitArgs {
   const float* iw;
   void* out;
   int64_t B;
-  int64_t Bp;  // B rounded up to bags-per-wave
+  int64_t Bp;  // B rounded up to bags-per-block
   int64_t total_D;
   int64_t nwaves;
   int32_t T;
@@ -411,39 +416,65 @@ __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
 // One launch per table type present: the instance holds only that type's
 // paths (fewer registers, higher occupancy); waves whose table has another
 // type return at once.
+constexpr int kWpb = MX_NBIT_WPB;
+constexpr int kBlockThreads = 64 * kWpb;
+
 template <typename I, int G, int MAXCPL, int TY>
 __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
-  constexpr int P = 64 / G;  // bags per wave
+  constexpr int P = 64 / G;           // bags per wave
+  constexpr int BPB = kWpb * P;       // bags per block, all of one table
   // Hardware block order (round-robin over the XCDs): tables of different
   // types interleave on every XCD, so no XCD is left with only the slow ones.
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (wave >= a.nwaves) return;
+  const int64_t slot0 = static_cast<int64_t>(blockIdx.x) * BPB;
+  const int64_t t = slot0 / a.Bp;
+  if (t >= a.T) return;  // block-uniform
+  const int32_t ty = a.tys[t];
+  if (ty != TY) return;  // block-uniform
+  const int64_t b0 = slot0 - t * a.Bp;
+  // A wave lasts as long as its longest bag: the block ranks its BPB bags by
+  // length (longest first, ties by position) and wave w takes ranks
+  // [w*P, w*P + P), so bags of similar length share a wave.  Each bag still
+  // writes its own output row.
+  static_assert(BPB <= kBlockThreads, "one thread per bag ranks the block's bags");
+  __shared__ int64_t s_start[BPB], s_end[BPB];
+  __shared__ int s_bag[BPB];
+  if (threadIdx.x < BPB) {
+    const int64_t b = b0 + threadIdx.x;
+    int64_t start = 0, end = -1;  // slots past the batch rank last
+    if (b < a.B) {
+      start = idx_at<I>(a.off, t * a.B + b);
+      end = idx_at<I>(a.off, t * a.B + b + 1);
+    }
+    s_start[threadIdx.x] = start;
+    s_end[threadIdx.x] = end;
+  }
+  __syncthreads();
+  if (threadIdx.x < BPB) {
+    const int i = threadIdx.x;
+    const int64_t li = s_end[i] - s_start[i];
+    int rank = 0;
+    for (int j = 0; j < BPB; ++j) {
+      const int64_t lj = s_end[j] - s_start[j];
+      rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
+    }
+    s_bag[rank] = i;
+  }
+  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
   const int k = lane % G;
-  const int64_t slot0 = wave * P;
-  const int64_t t = slot0 / a.Bp;
-  if (t >= a.T) return;
-  const int64_t b = slot0 - t * a.Bp + g;
-  const int32_t ty = a.tys[t];
-  if (ty != TY) return;
   const int32_t D0 = a.D_off[t];
   const int32_t D = a.D_off[t + 1] - D0;
   const int64_t stride = row_bytes_of(ty, D, a.row_align);
   const uint8_t* __restrict__ Wt = a.W + a.w_off[t];
-  int64_t start = 0, end = 0;
-  if (b < a.B) {
-    const int64_t bag = t * a.B + b;
-    start = idx_at<I>(a.off, bag);
-    end = idx_at<I>(a.off, bag + 1);
-  }
-  const int64_t out_col = (b < a.B ? b : 0) * a.total_D + D0;
-  if (b >= a.B) return;  // whole group idle; group lanes stay converged
-  dispatch_cpl<I, G, MAXCPL, TY>(a, D, Wt, stride, start, end, out_col, g, k);
+  const int i = s_bag[(threadIdx.x >> 6) * P + g];
+  const int64_t b = b0 + i;
+  if (b >= a.B) return;  // whole group idle (idle slots rank last); its lanes stay converged
+  dispatch_cpl<I, G, MAXCPL, TY>(a, D, Wt, stride, s_start[i], s_end[i], b * a.total_D + D0, g, k);
 }
 
 template <typename I, int G, int MAXCPL, int TY>
-__global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
+__global__ void __launch_bounds__(kBlockThreads) nbit_fwd_kernel(NbitArgs a) {
   nbit_fwd_body<I, G, MAXCPL, TY>(a);
 }
 
@@ -451,29 +482,29 @@ __global__ void __launch_bounds__(256) nbit_fwd_kernel(NbitArgs a) {
 // (config 5's INT4 launch: 684 against 734 us at 4 waves; the other types
 // either fit already or would spill).
 template <typename I, int G, int MAXCPL, int TY>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5)))
+__global__ void __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(5)))
     nbit_fwd_kernel_w5(NbitArgs a) {
   nbit_fwd_body<I, G, MAXCPL, TY>(a);
 }
 
 template <int G, int MAXCPL, int TY>
 int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
-  constexpr int P = 64 / G;
-  a.Bp = ceil_div(a.B, P) * P;
-  a.nwaves = static_cast<int64_t>(a.T) * (a.Bp / P);
-  const int64_t grid = ceil_div(a.nwaves, 4);
+  constexpr int BPB = kWpb * (64 / G);  // bags per block
+  a.Bp = ceil_div(a.B, BPB) * BPB;      // every block within one table
+  a.nwaves = static_cast<int64_t>(a.T) * (a.Bp / BPB) * kWpb;
+  const int64_t grid = ceil_div(a.nwaves, kWpb);
   MX_REQUIRE(grid <= 0x7fffffffll, "too many bags");
   const dim3 gd(static_cast<uint32_t>(grid));
   if constexpr (TY == MX_SPARSE_INT4) {
     if (index_bytes == 8)
-      nbit_fwd_kernel_w5<int64_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+      nbit_fwd_kernel_w5<int64_t, G, MAXCPL, TY><<<gd, kBlockThreads, 0, s>>>(a);
     else
-      nbit_fwd_kernel_w5<int32_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+      nbit_fwd_kernel_w5<int32_t, G, MAXCPL, TY><<<gd, kBlockThreads, 0, s>>>(a);
   } else {
     if (index_bytes == 8)
-      nbit_fwd_kernel<int64_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+      nbit_fwd_kernel<int64_t, G, MAXCPL, TY><<<gd, kBlockThreads, 0, s>>>(a);
     else
-      nbit_fwd_kernel<int32_t, G, MAXCPL, TY><<<gd, 256, 0, s>>>(a);
+      nbit_fwd_kernel<int32_t, G, MAXCPL, TY><<<gd, kBlockThreads, 0, s>>>(a);
   }
   MX_LAUNCH_CHECK();
   return MX_OK;

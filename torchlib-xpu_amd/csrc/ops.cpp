@@ -160,10 +160,29 @@ int32_t mx_dtype_of(at::ScalarType st) {
 }
 
 uint64_t pad_bits_of(double pad, at::ScalarType st) {
-  // Convert on the host with torch's own casting rules, then take the bits.
-  Tensor p = at::scalar_tensor(pad, at::TensorOptions().dtype(st));
+  // The padding value's bits in the element type, converted by torch's own
+  // scalar types (round to nearest even), with no tensor in between.
   uint64_t bits = 0;
-  std::memcpy(&bits, p.data_ptr(), p.element_size());
+  switch (st) {
+    case at::kFloat: {
+      const float f = static_cast<float>(pad);
+      std::memcpy(&bits, &f, sizeof(f));
+      break;
+    }
+    case at::kDouble:
+      std::memcpy(&bits, &pad, sizeof(pad));
+      break;
+    case at::kHalf:
+      bits = c10::Half(static_cast<float>(pad)).x;
+      break;
+    case at::kBFloat16:
+      bits = c10::BFloat16(static_cast<float>(pad)).x;
+      break;
+    default: {
+      Tensor p = at::scalar_tensor(pad, at::TensorOptions().dtype(st));
+      std::memcpy(&bits, p.data_ptr(), p.element_size());
+    }
+  }
   return bits;
 }
 
