@@ -70,7 +70,10 @@ def parse_args():
                          "instead of the lookup")
     ap.add_argument("--regime", default="all", choices=["all", "steps", "warm", "cold"])
     ap.add_argument("--cold-launches", type=int, default=24,
-                    help="flushed launches whose median gives the roofline")
+                    help="flushes whose median launch time gives the roofline")
+    ap.add_argument("--cold-copies", type=int, default=4,
+                    help="launches timed back to back after each flush, each over its own "
+                         "copy of the inputs")
     ap.add_argument("--no-config4", action="store_true",
                     help="config 2 only: leave out the config-4 record")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -144,12 +147,15 @@ def time_steps(fns: list[Callable], steps: int, warmup: int):
     return wall, start.elapsed_time(end) / steps
 
 
-def time_cold(fn: Callable, launches: int, warmup: int, dev) -> list[float]:
-    """Each launch follows a write and then a read of a 1 GiB buffer: neither
-    the L2s nor the 256 MB Infinity Cache then hold any of the launch's inputs,
-    and the lines they do hold are clean (a write-only flush leaves dirty lines
-    whose write-back would land inside the timed launch).  One HIP event pair
-    per launch on the current stream.  Returns the `launches` durations in ms."""
+def time_cold(fns: list[Callable], launches: int, warmup: int, dev) -> list[float]:
+    """Cold launches: a write and then a read of a 1 GiB buffer empty the L2s
+    and the 256 MB Infinity Cache of the inputs and leave only clean lines (a
+    write-only flush leaves dirty lines whose write-back would land inside the
+    timed launches); then the len(fns) launches, each over its own copy of the
+    inputs, so each finds none of its inputs in any cache, run back to back
+    inside one HIP event pair on the current stream (one pair per launch would
+    also time the dispatch gap after the flush).  Returns `launches` per-launch
+    durations in ms, each the mean over one such group."""
     import torch
 
     flush = torch.empty(FLUSH_BYTES // 4, device=dev, dtype=torch.float32)
@@ -159,13 +165,14 @@ def time_cold(fn: Callable, launches: int, warmup: int, dev) -> list[float]:
         flush.sum()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        fn()
+        for fn in fns:
+            fn()
         e.record()
         if i >= warmup:
             evs.append((s, e))
     torch.cuda.synchronize()
     del flush
-    return [s.elapsed_time(e) for s, e in evs]
+    return [s.elapsed_time(e) / len(fns) for s, e in evs]
 
 
 def cpu_time(fn, budget_s: float, min_runs: int = 3, warm: int = 1):
@@ -207,6 +214,9 @@ class Workload:
     # is no HBM quantity.
     roof_bytes: Optional[float] = None
     roof_bytes_kind: str = "algorithmic bytes per launch (per-unit figure x units)"
+    # Launches of batch 0 over disjoint copies of its inputs (the cold regime
+    # times them back to back after each flush); defaults to steps[0] alone.
+    cold_steps: Optional[list[Callable]] = None
 
 
 def run_workload(args, wl: Workload, dev) -> dict:
@@ -237,8 +247,9 @@ def run_workload(args, wl: Workload, dev) -> dict:
             rec.update(value=wl.units[0] / (warm_ms * 1e-3), ms_per_step=warm_ms)
     roof = None
     if "cold" in regimes:
-        log(f"timing {args.cold_launches} cold-cache launches of batch 0")
-        cold = time_cold(wl.steps[0], args.cold_launches, min(args.warmup, 3), dev)
+        cold_fns = wl.cold_steps or wl.steps[:1]
+        log(f"timing {args.cold_launches} x {len(cold_fns)} cold-cache launches of batch 0")
+        cold = time_cold(cold_fns, args.cold_launches, min(args.warmup, 3), dev)
         med = statistics.median(cold)
         nbytes = wl.roof_bytes if wl.roof_bytes is not None else wl.alg_bytes[0]
         achieved = nbytes / (med * 1e-3) / 1e9
@@ -248,9 +259,10 @@ def run_workload(args, wl: Workload, dev) -> dict:
                     kernel=wl.kernel, alg_bytes_per_launch=nbytes,
                     alg_bytes_kind=wl.roof_bytes_kind,
                     launch_ms=med, launch_ms_min=min(cold), launch_ms_max=max(cold),
-                    regime=(f"cold: median of {len(cold)} launches of batch 0, each after a "
-                            f"1 GiB buffer is written and read; one HIP event pair per "
-                            f"launch"))
+                    regime=(f"cold: median over {len(cold)} groups of {len(cold_fns)} launches of "
+                            f"batch 0, each over its own copy of the inputs, back to back after "
+                            f"a 1 GiB buffer is written and read; one HIP event pair per "
+                            f"group"))
         if wl.roof_bytes is not None:
             eff["cold_per_lookup_bytes"] = dict(
                 bytes=wl.alg_bytes[0], effective_GBps=wl.alg_bytes[0] / (med * 1e-3) / 1e9,
@@ -297,10 +309,11 @@ def wl_jagged(args, dev) -> Workload:
     j2pd = torch.ops.fbgemm.jagged_to_padded_dense
     d2j = torch.ops.fbgemm.dense_to_jagged
 
-    def step():
-        dense = j2pd(v, [off], [L], 0.0)
-        return d2j(dense, [off], total)
+    def make_step(vv, oo):
+        return lambda: d2j(j2pd(vv, [oo], [L], 0.0), [oo], total)
 
+    step = make_step(v, off)
+    cold = [make_step(v.clone(), off.clone()) for _ in range(args.cold_copies)]
     # j2pd reads the values and writes the padded dense; d2j reads the dense at
     # the jagged positions and writes the values; both read the offsets.
     alg = total * D * 4 + B * L * D * 4 + 2 * total * D * 4 + 2 * (B + 1) * 8
@@ -325,7 +338,7 @@ def wl_jagged(args, dev) -> Workload:
         config={"workload": "config1: jagged round trip, B=512 D=128 max_L=64, len~U{0..64}",
                 "B": B, "D": D, "max_L": L, "total_L": total},
         kernel="j2pd1_kernel + jagged_out1_kernel (one round trip)", profile="jagged_config1",
-        cpu=cpu)
+        cpu=cpu, cold_steps=cold)
 
 
 # -- config 2 ----------------------------------------------------------------
@@ -351,13 +364,14 @@ def wl_tbe_forward(args, dev) -> Workload:
     e32 = torch.zeros(0, dtype=torch.int32, device=dev)
     op = torch.ops.fbgemm.split_embedding_codegen_forward_unweighted_cuda
 
-    def make_step(b):
+    def make_step(b, Wc):
         idx = torch.from_numpy(b.indices).to(dev)
         off = torch.from_numpy(b.offsets).to(dev)
-        return lambda: op(W, empty, empty, pl, w_off, D_off, inp.total_D, D, idx, off, 0, e32,
+        return lambda: op(Wc, empty, empty, pl, w_off, D_off, inp.total_D, D, idx, off, 0, e32,
                           empty, 0, False)
 
-    steps = [make_step(b) for b in batches]
+    steps = [make_step(b, W) for b in batches]
+    cold = [make_step(inp, W.clone()) for _ in range(args.cold_copies)]
     # Per lookup: the row and its index; per bag: its offset and output row.
     alg = [b.N * (D * 4 + 8) + T * B * (8 + D * 4) for b in batches]
     # Compulsory bytes of batch 0: every distinct row once (the Zipf heads repeat).
@@ -396,7 +410,7 @@ def wl_tbe_forward(args, dev) -> Workload:
                             "batches of the same tables (same hot rows, fresh draws)",
                 "T": T, "E": E, "D": D, "B": B, "N_batch0": inp.N,
                 "N_mean": sum(b.N for b in batches) / len(batches), "indices": "int64"},
-        kernel="tbe_fwd_group_kernel", profile="tbe_fwd_config2", cpu=cpu,
+        kernel="tbe_fwd_group_kernel", profile="tbe_fwd_config2", cpu=cpu, cold_steps=cold,
         roof_bytes=compulsory,
         roof_bytes_kind=("compulsory bytes of batch 0: its distinct rows once (D*4 each) + "
                          "indices (8 B) + offsets (8 B per bag) + output (D*4 per bag)"),
@@ -422,6 +436,11 @@ def wl_bounds_check(args, dev) -> Workload:
     def step():
         op(rows, idx, off, 1, warn)
 
+    def make_cold(ic, oc):
+        return lambda: op(rows, ic, oc, 1, warn)
+
+    cold = [make_cold(idx.clone(), off.clone()) for _ in range(args.cold_copies)]
+
     def cpu():
         sys.path.insert(0, str(REPO / "oracle"))
         import oracle as orc
@@ -441,7 +460,8 @@ def wl_bounds_check(args, dev) -> Workload:
         units=[inp.N], alg_bytes=[inp.N * 8 + (inp.T * inp.B + 1) * 8], dtype="int64",
         config={"workload": "config2 batch: bounds_check_indices, WARNING mode", "T": inp.T,
                 "B": inp.B, "N": inp.N},
-        kernel="tile_max_kernel + bounds_main_kernel", profile="bounds_check_config2", cpu=cpu)
+        kernel="tile_max_kernel + bounds_main_kernel", profile="bounds_check_config2", cpu=cpu,
+        cold_steps=cold)
 
 
 # -- config 3 ----------------------------------------------------------------
@@ -472,9 +492,14 @@ def wl_backward(args, dev) -> Workload:
     e32 = torch.zeros(0, dtype=torch.int32, device=dev)
     op = torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
 
-    def step():
-        op(grad, W, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits, idx, off, 0,
-           e32, 0, 0, False, m1, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
+    def make_step(Wc, mc, gc, ic, oc):
+        return lambda: op(gc, Wc, empty, empty, pl, w_off, D_off, D, hsc, inp.total_hash_size_bits,
+                          ic, oc, 0, e32, 0, 0, False, mc, empty, pl, m_off, 1e-8, 0.01, 0.0, 0,
+                          0.0)
+
+    step = make_step(W, m1, grad, idx, off)
+    cold = [make_step(W.clone(), m1.clone(), grad.clone(), idx.clone(), off.clone())
+            for _ in range(args.cold_copies)]
 
     U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
                       + inp.indices).size)
@@ -509,7 +534,7 @@ def wl_backward(args, dev) -> Workload:
         config={"workload": "config3: TBE backward + exact rowwise Adagrad on config-2 shapes",
                 "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
         kernel="whole backward (transpose + segment reduce + update)",
-        profile="tbe_bwd_config3", cpu=cpu)
+        profile="tbe_bwd_config3", cpu=cpu, cold_steps=cold)
 
 
 # -- configs 4 and 5 ---------------------------------------------------------
@@ -559,6 +584,12 @@ def wl_nbit(args, dev, config: int) -> Workload:
 
     def step():
         return op(*args_)
+
+    def make_cold(Wc, ic, oc):
+        a = (Wc,) + args_[1:12] + (ic, oc) + args_[14:]
+        return lambda: op(*a)
+
+    cold = [make_cold(W.clone(), idx.clone(), off.clone()) for _ in range(args.cold_copies)]
 
     N = inp.N
     unpadded = [(D + 4) if ty == SparseType.INT8 else (D // 2 + 4) if ty == SparseType.INT4
@@ -617,7 +648,7 @@ def wl_nbit(args, dev, config: int) -> Workload:
         "fp16/int4 codes, fp32 accumulate, fp16 out",
         config={"workload": workload, "T": inp.T, "B": inp.B, "N": N},
         kernel="nbit_fwd_kernel (one launch per table type present)",
-        profile=f"nbit_fwd_config{config}", cpu=cpu,
+        profile=f"nbit_fwd_config{config}", cpu=cpu, cold_steps=cold,
         # Config 5 draws Zipf indices (the per-lookup count re-reads the hot
         # rows); config 4's are uniform over 3.6 GB of rows, where a repeated
         # row is long evicted when it comes again, so every lookup is HBM traffic.
