@@ -1,5 +1,6 @@
-"""The package loader: it fails loudly (one RuntimeError naming the likely
-causes) when the native libraries are missing, as the reference's loader does
+"""The package loader: it fails loudly (one RuntimeError naming the library
+that is missing or failed to load) when the native libraries are absent or
+broken, as the reference's loader fails at import
 (packages/torchcodec-xpu/src/torchcodec_xpu/__init__.py:33-54); and the ops it
 registers have no CPU kernels (no silent CPU fallback)."""
 
@@ -24,7 +25,26 @@ def test_missing_library_raises(tmp_path):
             "try:\n    import mx_fbgemm\nexcept RuntimeError as e:\n"
             "    print('RAISED:' + str(e).splitlines()[0])\n" % str(tmp_path))
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
-    assert "RAISED:Could not load mx_fbgemm" in out.stdout, out.stdout + out.stderr
+    assert "RAISED:Could not load mx_fbgemm: its kernel library" in out.stdout, \
+        out.stdout + out.stderr
+    assert "does not exist" in out.stdout
+
+
+def test_unloadable_library_raises(tmp_path):
+    """A kernel library that is present but cannot be loaded (here: not an ELF
+    file) is reported with the loader's own error, not swallowed."""
+    dst = tmp_path / "mx_fbgemm"
+    (dst / "lib").mkdir(parents=True)
+    for f in PKG.glob("*.py"):
+        shutil.copy(f, dst / f.name)
+    (dst / "lib" / "libmx_fbgemm_kernels.so").write_bytes(b"not a shared object")
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "try:\n    import mx_fbgemm\nexcept RuntimeError as e:\n"
+            "    print('RAISED:' + str(e).splitlines()[0])\n" % str(tmp_path))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert "RAISED:Could not load mx_fbgemm: loading its kernel library" in out.stdout, \
+        out.stdout + out.stderr
+    assert "OSError" in out.stdout
 
 
 def test_cpu_tensors_have_no_kernel():

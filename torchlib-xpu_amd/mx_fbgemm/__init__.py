@@ -5,8 +5,8 @@ table-batched-embedding operators, registered under ``torch.ops.fbgemm``.
 define the ``fbgemm`` schemas and register the GPU implementations -- the
 same plugin shape as the reference's loader
 (reference: packages/torchcodec-xpu/src/torchcodec_xpu/__init__.py:25-56):
-load at import, and on failure raise one RuntimeError that lists the likely
-causes and every captured traceback.
+load at import, and on failure raise one RuntimeError that says which
+library failed and why.
 
 There is no CPU fallback: the operators accept HIP tensors only, and the
 import fails loudly when the native libraries are missing.
@@ -89,34 +89,34 @@ def load_mx_fbgemm_library() -> None:
             "implementation (e.g. fbgemm_gpu) is loaded in this process. mx_fbgemm replaces "
             "it and cannot be loaded alongside it."
         )
-    exceptions = []
-    try:
-        # Kernel library first (global so the extension's DT_NEEDED resolves to
-        # this exact file), then the extension that registers the ops.
-        ctypes.CDLL(str(KERNEL_LIBRARY), mode=ctypes.RTLD_GLOBAL)
-        torch.ops.load_library(str(OPS_LIBRARY))
-        _loaded = True
-        return
-    except Exception:
-        exceptions.append(traceback.format_exc())
-
-    traceback_info = (
-        "\n[start of mx_fbgemm loading traceback]\n"
-        + "\n".join(exceptions)
-        + "\n[end of mx_fbgemm loading traceback]."
+    # Step 1: the kernel library, loaded global so that the extension's
+    # DT_NEEDED entry resolves to this exact file.  Step 2: the extension,
+    # whose static initializers register the ops.
+    steps = (
+        ("kernel library", KERNEL_LIBRARY,
+         lambda: ctypes.CDLL(str(KERNEL_LIBRARY), mode=ctypes.RTLD_GLOBAL)),
+        ("torch extension", OPS_LIBRARY, lambda: torch.ops.load_library(str(OPS_LIBRARY))),
     )
-    raise RuntimeError(
-        f"""Could not load mx_fbgemm. Likely causes:
-          1. The native libraries were not built: run
-             `python torchlib-xpu_amd/mx_fbgemm/_build.py` (or __graft_entry__.build()).
-             Expected {KERNEL_LIBRARY} and {OPS_LIBRARY}.
-          2. The PyTorch version ({torch.__version__}, HIP {torch.version.hip}) differs
-             from the one the extension was built against.
-          3. The ROCm runtime (libamdhip64) could not be found.
-        The following exceptions were raised as we tried to load mx_fbgemm:
-        """
-        f"{traceback_info}"
-    )
+    for what, path, load in steps:
+        if not path.is_file():
+            raise RuntimeError(
+                f"Could not load mx_fbgemm: its {what} {path} does not exist. Build it with "
+                "`python torchlib-xpu_amd/mx_fbgemm/_build.py` (or __graft_entry__.build()); "
+                "the operators have no CPU implementation to fall back on."
+            )
+        try:
+            load()
+        except Exception as exc:
+            raise RuntimeError(
+                f"Could not load mx_fbgemm: loading its {what} {path} failed with "
+                f"{type(exc).__name__}: {exc}\n"
+                f"This process runs torch {torch.__version__} with HIP {torch.version.hip}; "
+                "an extension built against another torch, or a ROCm runtime "
+                "(libamdhip64) missing from the loader path, fails this way. Rebuild with "
+                "`python torchlib-xpu_amd/mx_fbgemm/_build.py`.\n"
+                + "".join(traceback.format_exception(type(exc), exc, exc.__traceback__))
+            ) from exc
+    _loaded = True
 
 
 load_mx_fbgemm_library()
