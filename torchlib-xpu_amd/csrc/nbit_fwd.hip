@@ -23,19 +23,12 @@
 
 #include "mx_common.h"
 
-// Waves per block: a block ranks its waves x 64/G bags by length.
-#ifndef MX_NBIT_WPB
-#define MX_NBIT_WPB 4
-#endif
+namespace mx {
+namespace {
 
 // Bytes of row data each lane keeps in flight (sets the rows loaded before
 // any is accumulated).
-#ifndef MX_NBIT_INFLIGHT_BYTES
-#define MX_NBIT_INFLIGHT_BYTES 96
-#endif
-
-namespace mx {
-namespace {
+constexpr int kInflightBytes = 96;
 
 struct NbitArgs {
   const uint8_t* W;
@@ -223,7 +216,7 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   constexpr bool Q = TyInfo<TY>::kQ;
   constexpr int BPL = CPL * BITS / 8;
   constexpr int NW = BPL >= 4 ? BPL / 4 : 1;
-  constexpr int U0 = MX_NBIT_INFLIGHT_BYTES / (BPL + (Q ? 4 : 0));
+  constexpr int U0 = kInflightBytes / (BPL + (Q ? 4 : 0));
   constexpr int U = U0 < 1 ? 1 : (U0 > 8 ? 8 : U0);
   const int64_t lane_off = (Q ? 4 : 0) + static_cast<int64_t>(k) * BPL;
 
@@ -410,14 +403,16 @@ __device__ __forceinline__ void dispatch_cpl(const NbitArgs& a, int32_t D,
   bag_generic<I, G>(a, TY, D, Wt, stride, start, end, out_col, k);
 }
 
+// Waves per block: a block ranks its waves x 64/G bags by length.
+constexpr int kWpb = 4;
+constexpr int kBlockThreads = 64 * kWpb;
+
 // MAXCPL bounds the columns per lane compiled into this instance: the kernel's
 // register budget is set by its widest path, so a launch whose tables are all
 // narrow (max D <= 16*G) runs an instance without the 32-column paths.
 // One launch per table type present: the instance holds only that type's
 // paths (fewer registers, higher occupancy); waves whose table has another
 // type return at once.
-constexpr int kWpb = MX_NBIT_WPB;
-constexpr int kBlockThreads = 64 * kWpb;
 
 template <typename I, int G, int MAXCPL, int TY>
 __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {

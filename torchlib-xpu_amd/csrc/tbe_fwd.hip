@@ -13,6 +13,12 @@
 // sum is bit-identical to a sequential CPU loop.  A bag's indices are fetched
 // G at a time with one coalesced load and handed out with ds_bpermute; U rows
 // are loaded before any is accumulated (D=128: 8 x 512 B in flight per bag).
+// A batch of U loads has no branch between its loads (rows past the bag's end
+// are clamped to its last row and their sums dropped by a select), so the
+// compiler issues all U before the first wait.  When every bag of a wave is
+// in one table and that table fits 4 GiB, rows are read through one buffer
+// descriptor of the table with 32-bit byte offsets (no 64-bit address per
+// row); otherwise through 64-bit pointers.
 // Blocks are remapped so that each XCD works on a contiguous range of bags
 // (t-major), keeping one table's hot rows in one XCD's L2 (measured: 27.8 us
 // vs 31.0 us without the remap on config 2).
@@ -359,16 +365,11 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Rows in flight per lane when a lane owns one float4 column chunk.
-#ifndef MX_FWD_U1
-#define MX_FWD_U1 8
-#endif
-
 template <typename I, typename WT, int G, int NCH, bool WEIGHTED, bool OUT_F16>
 void launch_fwd_group(hipStream_t s, const WT* W, const int64_t* w_off, const int32_t* D_off,
                       const BagMap& bm, const void* idx, const void* off, int32_t pooling,
                       const float* iw, void* out, int64_t nbags) {
-  constexpr int U = NCH <= 1 ? MX_FWD_U1 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
+  constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);  // rows in flight per lane
   constexpr int P = 64 / G;
   const int64_t grid = ceil_div(nbags, kWavesPerBlock * P);
   tbe_fwd_group_kernel<I, WT, G, NCH, U, WEIGHTED, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
@@ -384,13 +385,8 @@ int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off
   launch_fwd_group<I, WT, G, NCH, WEIGHTED, OUT_F16>(s, W, w_off, D_off, bm, idx, off, pooling, iw, out, nbags)
   if (max_D <= 64)
     MX_FWD_G(16, 1);  // 4 bags per wave
-#ifdef MX_FWD_G16_D128
-  else if (max_D <= 128)
-    MX_FWD_G(16, 2);  // 4 bags per wave, 16 lanes x 2 x 16 B per row
-#else
   else if (max_D <= 128)
     MX_FWD_G(32, 1);  // 2 bags per wave, one D=128 row per 32 lanes x 16 B
-#endif
   else if (max_D <= 256)
     MX_FWD_G(64, 1);
   else if (max_D <= 512)
