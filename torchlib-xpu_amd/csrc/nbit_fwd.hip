@@ -208,7 +208,12 @@ __device__ __forceinline__ void store_out(const NbitArgs& a, int64_t col_base, i
   }
 }
 
-// Fast path: CPL columns per lane, CPL*bits a multiple of 8.
+// Fast path: CPL columns per lane, CPL*bits a multiple of 8.  A lane's BPL
+// code bytes are NCHK chunks of CH <= 16 bytes, interleaved across the group:
+// chunk q of lane k is bytes (q*G + k)*CH of the row's codes.  Each load
+// instruction then covers one contiguous G*CH-byte span of every row (one
+// 128-byte line for G*CH = 128) instead of touching every line of a wide row
+// with a few lanes each, which multiplied the texture path's tag lookups.
 template <typename I, int G, int TY, int CPL>
 __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int64_t stride,
                          int64_t start, int64_t end, int64_t out_col, int g, int k) {
@@ -216,9 +221,13 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   constexpr bool Q = TyInfo<TY>::kQ;
   constexpr int BPL = CPL * BITS / 8;
   constexpr int NW = BPL >= 4 ? BPL / 4 : 1;
+  constexpr int CH = BPL < 16 ? BPL : 16;  // bytes per chunk (one load)
+  constexpr int NCHK = BPL / CH;           // chunks per lane
+  constexpr int CPC = CPL / NCHK;          // columns per chunk
+  constexpr int WPC = NW / NCHK;           // code words per chunk
   constexpr int U0 = kInflightBytes / (BPL + (Q ? 4 : 0));
   constexpr int U = U0 < 1 ? 1 : (U0 > 8 ? 8 : U0);
-  const int64_t lane_off = (Q ? 4 : 0) + static_cast<int64_t>(k) * BPL;
+  const int64_t lane_off = (Q ? 4 : 0) + static_cast<int64_t>(k) * CH;
 
   float acc[CPL];
 #pragma unroll
@@ -244,7 +253,10 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
         const R r = __shfl(my_idx, g * G + j + u, 64);
         if (j + u < n) {
           const uint8_t* row = Wt + static_cast<uint64_t>(r) * stride32;
-          load_codes<BPL>(row + lane_off, codes[u]);
+#pragma unroll
+          for (int q = 0; q < NCHK; ++q)
+            load_codes<CH>(row + lane_off + q * G * CH,
+                           *reinterpret_cast<uint32_t(*)[WPC]>(&codes[u][q * WPC]));
           if constexpr (Q) qp[u] = *reinterpret_cast<const uint32_t*>(row);
         }
       }
@@ -301,30 +313,41 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
 #pragma unroll
     for (int e = 0; e < CPL; ++e) res[e] = 0.0f;
   }
-  const int64_t col = out_col + static_cast<int64_t>(k) * CPL;
+  // Element e of the lane is column (q*G + k)*CPC + j of the table, e = q*CPC + j.
+  const int64_t col = out_col + static_cast<int64_t>(k) * CPC;
   if (a.out_f16) {
     __half h[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) h[e] = __float2half_rn(res[e]);
-    __half* o = reinterpret_cast<__half*>(a.out) + col;
-    if constexpr (CPL % 8 == 0) {
 #pragma unroll
-      for (int q = 0; q < CPL / 8; ++q)
-        *reinterpret_cast<uint4*>(o + 8 * q) = *reinterpret_cast<const uint4*>(h + 8 * q);
-    } else {
+    for (int q = 0; q < NCHK; ++q) {
+      __half* o = reinterpret_cast<__half*>(a.out) + col + q * G * CPC;
+      const __half* hq = h + q * CPC;
+      if constexpr (CPC % 8 == 0) {
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) o[e] = h[e];
+        for (int v = 0; v < CPC / 8; ++v)
+          *reinterpret_cast<uint4*>(o + 8 * v) = *reinterpret_cast<const uint4*>(hq + 8 * v);
+      } else if constexpr (CPC == 4) {
+        *reinterpret_cast<uint2*>(o) = *reinterpret_cast<const uint2*>(hq);
+      } else {
+#pragma unroll
+        for (int e = 0; e < CPC; ++e) o[e] = hq[e];
+      }
     }
   } else {
-    float* o = reinterpret_cast<float*>(a.out) + col;
-    if constexpr (CPL % 4 == 0) {
 #pragma unroll
-      for (int q = 0; q < CPL / 4; ++q)
-        *reinterpret_cast<float4*>(o + 4 * q) =
-            make_float4(res[4 * q], res[4 * q + 1], res[4 * q + 2], res[4 * q + 3]);
-    } else {
+    for (int q = 0; q < NCHK; ++q) {
+      float* o = reinterpret_cast<float*>(a.out) + col + q * G * CPC;
+      const float* rq = res + q * CPC;
+      if constexpr (CPC % 4 == 0) {
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) o[e] = res[e];
+        for (int v = 0; v < CPC / 4; ++v)
+          *reinterpret_cast<float4*>(o + 4 * v) =
+              make_float4(rq[4 * v], rq[4 * v + 1], rq[4 * v + 2], rq[4 * v + 3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < CPC; ++e) o[e] = rq[e];
+      }
     }
   }
 }
