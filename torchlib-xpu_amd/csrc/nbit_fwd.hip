@@ -437,18 +437,39 @@ constexpr int kBlockThreads = 64 * kWpb;
 // paths (fewer registers, higher occupancy); waves whose table has another
 // type return at once.
 
+// Block-uniform loads of per-table metadata through the scalar data cache
+// (read-only constant address space: s_load, no vector memory round trip).
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T* p) {
+  using CT = const __attribute__((address_space(4))) T;
+  return *(CT*)(p);  // generic -> constant address space
+}
+
+// Table t's type byte: the scalar unit loads dwords, so the aligned dword
+// holding it is read (its four bytes share one page, so the read stays in
+// mapped memory even for the last byte of the array).
+__device__ __forceinline__ int32_t table_type(const uint8_t* tys, int64_t t) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(tys) + static_cast<uintptr_t>(t);
+  const uint32_t w = load_scalar(reinterpret_cast<const uint32_t*>(addr & ~uintptr_t(3)));
+  return static_cast<int32_t>((w >> (8 * (addr & 3))) & 0xffu);
+}
+
 template <typename I, int G, int MAXCPL, int TY>
 __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   constexpr int P = 64 / G;           // bags per wave
   constexpr int BPB = kWpb * P;       // bags per block, all of one table
   // Hardware block order (round-robin over the XCDs): tables of different
   // types interleave on every XCD, so no XCD is left with only the slow ones.
-  const int64_t slot0 = static_cast<int64_t>(blockIdx.x) * BPB;
-  const int64_t t = slot0 / a.Bp;
-  if (t >= a.T) return;  // block-uniform
-  const int32_t ty = a.tys[t];
+  // Half of a two-type launch's blocks find another type and leave: their
+  // table comes from a 32-bit division and its type from a scalar load, so
+  // they hold their slot for a few hundred cycles.
+  const uint32_t bpt = static_cast<uint32_t>(a.Bp / BPB);  // blocks per table
+  const uint32_t tu = blockIdx.x / bpt;
+  if (tu >= static_cast<uint32_t>(a.T)) return;  // block-uniform
+  const int64_t t = tu;
+  const int32_t ty = table_type(a.tys, t);
   if (ty != TY) return;  // block-uniform
-  const int64_t b0 = slot0 - t * a.Bp;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x - tu * bpt) * BPB;
   // A wave lasts as long as its longest bag: the block ranks its BPB bags by
   // length (longest first, ties by position) and wave w takes ranks
   // [w*P, w*P + P), so bags of similar length share a wave.  Each bag still
@@ -481,10 +502,10 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
   const int k = lane % G;
-  const int32_t D0 = a.D_off[t];
-  const int32_t D = a.D_off[t + 1] - D0;
+  const int32_t D0 = load_scalar(a.D_off + t);
+  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
   const int64_t stride = row_bytes_of(ty, D, a.row_align);
-  const uint8_t* __restrict__ Wt = a.W + a.w_off[t];
+  const uint8_t* __restrict__ Wt = a.W + load_scalar(a.w_off + t);
   const int i = s_bag[(threadIdx.x >> 6) * P + g];
   const int64_t b = b0 + i;
   if (b >= a.B) return;  // whole group idle (idle slots rank last); its lanes stay converged
