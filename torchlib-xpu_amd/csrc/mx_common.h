@@ -71,6 +71,16 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
   return (bid % kXcd) * per + bid / kXcd;
 }
 
+// Block-uniform load through the scalar data cache: the pointer is read as
+// constant address space (s_load), valid for memory no thread of the kernel
+// writes (data an earlier kernel wrote is seen: a dispatch invalidates the
+// scalar cache).
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T* p) {
+  using CT = const __attribute__((address_space(4))) T;
+  return *(CT*)(p);  // generic -> constant address space
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_bcast(T v, int lane) {
   return __shfl(v, lane, kWave);

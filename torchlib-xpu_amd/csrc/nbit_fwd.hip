@@ -437,14 +437,6 @@ constexpr int kBlockThreads = 64 * kWpb;
 // paths (fewer registers, higher occupancy); waves whose table has another
 // type return at once.
 
-// Block-uniform loads of per-table metadata through the scalar data cache
-// (read-only constant address space: s_load, no vector memory round trip).
-template <typename T>
-__device__ __forceinline__ T load_scalar(const T* p) {
-  using CT = const __attribute__((address_space(4))) T;
-  return *(CT*)(p);  // generic -> constant address space
-}
-
 // Table t's type byte: the scalar unit loads dwords, so the aligned dword
 // holding it is read (its four bytes share one page, so the read stays in
 // mapped memory even for the last byte of the array).
