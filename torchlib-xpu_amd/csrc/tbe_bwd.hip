@@ -17,7 +17,7 @@
 //    bag mark its first position in LDS and gives each position the latest
 //    mark (a max-scan), so no per-position search.  The same kernel
 //    accumulates the global digit histograms of every pass (LDS, then one
-//    atomic per bin and block).
+//    atomic per bin and block into its XCD's copy).
 //  * One launch per pass ("onesweep"): a block ranks a 3072-key tile (each
 //    wave 768 keys, 64 at a time, stable ranks from 8 ballots), then thread d
 //    finds how many keys of digit d earlier tiles hold through a decoupled
@@ -42,6 +42,12 @@ namespace {
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxPasses = 4;
+// The digit histograms are kept in one copy per XCD (a linearize block adds
+// into the copy of the XCD it runs on, block i on XCD i % 8), so that the
+// blocks' device-scope atomics spread over 8x more counters; a sort pass sums
+// the copies of its digit.
+constexpr int kHistCopies = 8;
+constexpr int64_t kHistCopyWords = kMaxPasses * kRadix;
 // 3072-key tiles: 218 tiles for config 3's 668k keys, one per CU; 2048-key
 // tiles (two on some CUs) made each pass ~2 us slower, 4096 (half the CUs
 // idle) ~1 us slower.
@@ -211,9 +217,15 @@ __global__ void __launch_bounds__(256)
       atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < passes * kRadix; i += 256) {
+  // Into this XCD's copy, each block starting at another bin so that blocks
+  // finishing together do not queue on the same counters.
+  uint32_t* gcopy = ghist + (blockIdx.x % kHistCopies) * kHistCopyWords;
+  const int nbins = passes * kRadix;
+  const int rot = static_cast<int>((blockIdx.x / kHistCopies) * 97u % static_cast<uint32_t>(nbins));
+  for (int j = threadIdx.x; j < nbins; j += 256) {
+    const int i = j + rot < nbins ? j + rot : j + rot - nbins;
     const uint32_t c = (&h[0][0])[i];
-    if (c) atomicAdd(&ghist[i], c);
+    if (c) atomicAdd(&gcopy[i], c);
   }
 }
 
@@ -223,7 +235,7 @@ constexpr unsigned long long kSweepAgg = 1ull << 62;
 constexpr unsigned long long kSweepIncl = 2ull << 62;
 
 // status: [tiles][kRadix] zeroed words; ticket: zeroed next-tile counter.
-// ghist: this pass's global digit counts.
+// ghist: this pass's digit counts, kHistCopies copies kHistCopyWords apart.
 template <bool LAST>
 __global__ void __launch_bounds__(256)
     onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
@@ -280,7 +292,12 @@ __global__ void __launch_bounds__(256)
   cnt[3][d] = c0 + c1 + c2;
   const bool used = d <= static_cast<int>(mask);  // same for every tile of the pass
   uint32_t gall;
-  const uint32_t goff = block_excl_scan<SumOp>(used ? ghist[d] : 0u, &gall);
+  uint32_t gcount = 0u;
+  if (used) {
+#pragma unroll
+    for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
+  }
+  const uint32_t goff = block_excl_scan<SumOp>(gcount, &gall);
   uint32_t prefix = 0u;
   if (used) {
     unsigned long long* mine = status + tile * kRadix + d;
@@ -467,7 +484,7 @@ struct SortWs {
   unsigned int* fail;              // set when a look-back of the call gave up
   unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
-  uint32_t* ghist;                 // [kMaxPasses][kRadix]
+  uint32_t* ghist;                 // [kHistCopies][kMaxPasses][kRadix]
   uint32_t* chunk_mark;            // [max_chunks(N)] (backward only)
   unsigned long long* sweep;       // kMaxPasses x sweep_pass_words
   int64_t sweep_words;
@@ -494,7 +511,7 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   w.sweep_words = sweep_pass_words(n);
   constexpr size_t status_bytes = 256;
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
-  const size_t hist_bytes = align256(kMaxPasses * kRadix * 4);
+  const size_t hist_bytes = align256(kHistCopies * kHistCopyWords * 4);
   const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
   uint8_t* z = take(status_bytes + scan_bytes + hist_bytes + mark_bytes +
                     kMaxPasses * w.sweep_words * 8);
