@@ -312,28 +312,30 @@ def _update_fp64(inp, pooling, W, m1, m1_off, grad, lr, eps):
     return W64, m64
 
 
-@pytest.mark.parametrize("T,B,dims,rows,max_L", [
-    (3, 259, [20, 216, 232], [2000, 300, 1], 43),
-    (2, 298, [208, 132], [1, 300], 40),
-    (3, 156, [516, 760, 536], [4, 1, 50], 37),
+@pytest.mark.parametrize("T,B,dims,rows,max_L,pooling,dup", [
+    (3, 259, [20, 216, 232], [2000, 300, 1], 43, 1, True),
+    (2, 298, [208, 132], [1, 300], 40, 1, False),
+    (3, 156, [516, 760, 536], [4, 1, 50], 37, 1, True),
+    (4, 252, [648, 772, 248, 556], [4, 300, 1, 1], 42, 1, False),
+    (3, 291, [56, 104, 104], [50, 1, 1], 42, 0, False),
+    (4, 195, [156, 56, 144, 12], [300, 1, 50, 70000], 44, 0, False),
 ])
-def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L):
-    """Tables of 1-4 rows under MEAN pooling: runs of thousands of
-    occurrences.  There the fp32 oracle's sequential sum drifts from the exact
+def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
+    """Tables of 1-4 rows: runs of thousands of occurrences.  There the fp32 oracle's sequential sum drifts from the exact
     value by up to ~3e-7 on the updated weights (past rtol 1e-5 / atol 1e-7 on
     a few elements), while the kernels' chunked sums stay within ~1e-8.  Both
     are checked against a float64 evaluation of the same update; the bound on
     the kernels is 3e-8, ten times tighter than the oracle's own drift."""
-    print(f"[case] extreme runs T={T} B={B} dims={dims} rows={rows}", flush=True)
+    print(f"[case] extreme runs T={T} B={B} dims={dims} rows={rows} pool={pooling}", flush=True)
     rng = np.random.default_rng(B + T)
-    inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=True)
+    inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
     rng = np.random.default_rng(B)
     lr, eps = 0.01, 1e-8
     W = rng.uniform(-0.01, 0.01, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
     m1 = rng.uniform(0, 1e-4, size=sum(inp.E)).astype(np.float32)
     m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
     grad = rng.normal(0, 1e-2, size=(inp.B, inp.total_D)).astype(np.float32)
-    W64, m64 = _update_fp64(inp, 1, W, m1, m1_off, grad, lr, eps)
+    W64, m64 = _update_fp64(inp, pooling, W, m1, m1_off, grad, lr, eps)
     Wd, m1d = torch.from_numpy(W).to(dev), torch.from_numpy(m1).to(dev)
     empty = torch.zeros(0, device=dev)
     pl = torch.zeros(T, dtype=torch.int32, device=dev)
@@ -341,7 +343,7 @@ def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L):
         torch.from_numpy(grad).to(dev), Wd, empty, empty, pl,
         torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
         max(dims), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
-        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), 1,
+        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
         torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty, pl,
         torch.from_numpy(m1_off).to(dev), eps, lr, 0.0, 0, 0.0)
     Wg = Wd.cpu().numpy().astype(np.float64)
