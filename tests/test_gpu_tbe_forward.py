@@ -188,3 +188,58 @@ def test_metadata_arguments_checked(dev):
     idx_strided = torch.stack([idx, idx], 1)[:, 1]
     got = op(W, empty, empty, pl, w_off, D_off, 16, 8, idx_strided, off, 0, e32, empty, 0, False)
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("wdtype,D", [(torch.float32, 128), (torch.float16, 256)])
+def test_table_past_4gib(dev, wdtype, D):
+    """A table of 8.99M rows x 512 bytes (4.6 GB) between two small ones.
+    Rows ending at or below 4 GiB into their table are read through a buffer
+    descriptor with 32-bit byte offsets, the rest through 64-bit addresses;
+    bags lie wholly below the boundary, wholly above it, across it, and on the
+    rows either side of it, in runs of 16 bags (whole waves of one kind) and
+    interleaved (waves that switch path batch by batch).  The expected values
+    come from the oracle on a compact copy of the rows looked up: the same
+    rows summed in the same order, so the comparison is bit-exact."""
+    print(f"[case] tbe fwd table past 4 GiB {wdtype} D={D}", flush=True)
+    row_bytes = D * torch.finfo(wdtype).bits // 8
+    bnd = (1 << 32) // row_bytes  # first row that ends past 4 GiB is bnd - 1
+    E_big = bnd + 600_000
+    rows, dims, B = [1000, E_big, 1000], [64, D, 32], 256
+    rng = np.random.default_rng(4096 + D)
+    lengths = rng.integers(0, 70, size=3 * B)
+    off = bench_inputs.offsets_from_lengths(lengths)
+    idx = np.empty(int(off[-1]), dtype=np.int64)
+    for t in (0, 2):
+        s, e = int(off[t * B]), int(off[(t + 1) * B])
+        idx[s:e] = rng.integers(0, rows[t], size=e - s)
+    for b in range(B):
+        s, e = int(off[B + b]), int(off[B + b + 1])
+        kind = (b // 16) % 4 if b < B // 2 else b % 4
+        lo, hi = [(0, bnd - 1), (bnd, E_big), (0, E_big), (bnd - 3, bnd + 3)][kind]
+        idx[s:e] = rng.integers(lo, hi, size=e - s)
+    inp = bench_inputs.TbeInput(T=3, E=rows, D=dims, B=B, indices=idx, offsets=off)
+    w_off = weight_offsets(inp)
+    n_elem = int(w_off[2]) + rows[2] * dims[2]
+    g = torch.Generator(device=dev)
+    g.manual_seed(D)
+    W = torch.empty(n_elem, dtype=wdtype, device=dev).uniform_(-1, 1, generator=g)
+
+    big = idx[int(off[B]): int(off[2 * B])]
+    used = np.unique(big)
+    assert used[0] < bnd - 1 and used[-1] >= bnd
+    rows_used = W[int(w_off[1]): int(w_off[2])].view(E_big, D)[torch.from_numpy(used).to(dev)]
+    Wc = np.concatenate([W[: int(w_off[1])].cpu().numpy(), rows_used.cpu().numpy().ravel(),
+                         W[int(w_off[2]):].cpu().numpy()])
+    idx_c = idx.copy()
+    idx_c[int(off[B]): int(off[2 * B])] = np.searchsorted(used, big)
+    inp_c = bench_inputs.TbeInput(T=3, E=[rows[0], used.size, rows[2]], D=dims, B=B,
+                                  indices=idx_c, offsets=off)
+    iw = rng.uniform(0, 2, size=inp.N).astype(np.float32)
+    for pooling, weights, index_dtype in [(0, None, torch.int64), (1, iw, torch.int32)]:
+        exp = orc.tbe_forward_f32(Wc, weight_offsets(inp_c), inp.D_offsets, B, idx_c, off,
+                                  pooling, weights)
+        got = tbe_forward_gpu(dev, W, inp, pooling, index_dtype,
+                              indice_weights=None if weights is None else torch.from_numpy(weights))
+        _exact(got, exp)
+    del W, rows_used
+    torch.cuda.empty_cache()
