@@ -88,6 +88,11 @@ int mx_set_status_mailbox(unsigned int* host_word);
  * once (failure-handling tests; every kernel still exits normally). */
 int mx_test_force_lookback_giveup(int enable);
 
+/* Test hook: while enabled, the radix sort of later calls keeps its
+ * look-back counts in 64-bit words, the form used for sorts of 2^30 keys or
+ * more, whatever the key count (lets tests cover that form at small sizes). */
+int mx_test_force_wide_sort_words(int enable);
+
 /* ---- jagged tensor ops ------------------------------------------------- */
 
 /* Serves fbgemm::jagged_to_padded_dense_forward (and the forward of

@@ -55,6 +55,28 @@ def test_transpose_bit_exact(dev, T, B, rows, max_L, dup):
     _check_transpose(dev, inp, torch.int32)
 
 
+@pytest.mark.parametrize("T,B,rows,max_L,dup", [
+    (3, 50, [10, 1000, 70000], 20, False),
+    (2, 300, [5000, 5000], 40, True),
+    (5, 700, [2 ** 20, 3, 100, 9, 2 ** 21], 10, False),
+])
+def test_transpose_wide_sort_words(dev, T, B, rows, max_L, dup):
+    """The sort keeps its look-back counts in 32-bit words below 2^30 keys and
+    in 64-bit words from there on; a test hook selects the 64-bit form here,
+    at sizes the oracle checks bit for bit, and the backward is checked in
+    the same form."""
+    print(f"[case] transpose, 64-bit sort words T={T} B={B} rows={rows}", flush=True)
+    rng = np.random.default_rng(T * 11 + B)
+    inp = random_tbe(rng, T, B, [64] * T, rows, max_L, dup_heavy=dup)
+    torch.ops.mx_fbgemm.test_force_wide_sort_words(True)
+    try:
+        _check_transpose(dev, inp)
+        _check_transpose(dev, inp, torch.int32)
+        _backward_case(dev, inp, 0, seed=T + B)
+    finally:
+        torch.ops.mx_fbgemm.test_force_wide_sort_words(False)
+
+
 def _backward_case(dev, inp, pooling, wd=0.0, wd_mode=0, lr=0.01, eps=1e-8, seed=0,
                    weighted=False, index_dtype=torch.int64):
     rng = np.random.default_rng(seed)

@@ -41,6 +41,8 @@ unsigned int* status_mailbox();
 // Spin bound of the look-back waits: `dflt`, or -1 while the test hook that
 // makes every look-back give up at once is on.
 int lookback_spin_limit(int dflt);
+// Test hook (mx_test_force_wide_sort_words): sort with 64-bit look-back words.
+bool force_wide_sort_words();
 
 #define MX_REQUIRE(cond, ...)                                   \
   do {                                                          \

@@ -139,6 +139,12 @@ void test_force_lookback_giveup(bool enable) {
   MX_CALL(mx_test_force_lookback_giveup(enable ? 1 : 0));
 }
 
+// mx_fbgemm::test_force_wide_sort_words(enable): tests only -- later sorts
+// keep 64-bit look-back words (the form of sorts of 2^30 keys or more).
+void test_force_wide_sort_words(bool enable) {
+  MX_CALL(mx_test_force_wide_sort_words(enable ? 1 : 0));
+}
+
 int32_t index_bytes_of(const Tensor& t, const char* name) {
   TORCH_CHECK(t.scalar_type() == at::kLong || t.scalar_type() == at::kInt, name,
               " must be int32 or int64, got ", t.scalar_type());
@@ -1631,4 +1637,5 @@ TORCH_LIBRARY_IMPL(fbgemm, CompositeExplicitAutograd, m) {
 TORCH_LIBRARY(mx_fbgemm, m) {
   m.def("pending_lookback_faults(int device) -> int", &mx_ops::pending_lookback_faults);
   m.def("test_force_lookback_giveup(bool enable) -> ()", &mx_ops::test_force_lookback_giveup);
+  m.def("test_force_wide_sort_words(bool enable) -> ()", &mx_ops::test_force_wide_sort_words);
 }

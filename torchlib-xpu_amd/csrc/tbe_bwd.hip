@@ -48,12 +48,19 @@ constexpr int kMaxPasses = 4;
 // the copies of its digit.
 constexpr int kHistCopies = 8;
 constexpr int64_t kHistCopyWords = kMaxPasses * kRadix;
-// 3072-key tiles: 218 tiles for config 3's 668k keys, one per CU; 2048-key
-// tiles (two on some CUs) made each pass ~2 us slower, 4096 (half the CUs
-// idle) ~1 us slower.
-constexpr int kSweepItems = 12;                       // keys per lane per pass
-constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;  // 768 keys per wave
-constexpr int64_t kSweepTile = 4 * kSweepWaveKeys;    // 3072 keys per block
+// 3072-key tiles: 218 tiles for config 3's 668k keys, one per CU.  A wave
+// ranks its keys with one ballot per digit bit and one LDS count update per
+// key, a chain of dependent latencies: 16 waves of 3 keys per lane (4 per
+// SIMD) hide what 4 waves of 12 did not (load and rank 5.2 -> 2.2 us per
+// tile, each pass 19.9 -> 17.2 us on config 3).  2048-key tiles lose ~2 us
+// per pass; 4096-key tiles are no faster and 6144-key ones slower (the
+// shorter look-back saves less than the longer ranking costs).
+constexpr int kSweepWaves = 16;                                // waves per sort block
+constexpr int kSweepThreads = 64 * kSweepWaves;
+constexpr int kSweepItems = 3;                                 // keys per lane per pass
+constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;
+constexpr int64_t kSweepTile = kSweepWaves * kSweepWaveKeys;  // keys per block
+static_assert(kSweepThreads >= 256, "the first 256 threads own one digit each");
 constexpr int kLinItems = 8;
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
 constexpr int kLong = 32;                             // runs longer than this are chunked
@@ -231,27 +238,37 @@ __global__ void __launch_bounds__(256)
 
 // ---- radix sort: one launch per pass --------------------------------------
 
-constexpr unsigned long long kSweepAgg = 1ull << 62;
-constexpr unsigned long long kSweepIncl = 2ull << 62;
+// A look-back status word: a flag in the top two bits (0 unpublished, 1 the
+// tile's own count, 2 the inclusive prefix), the count below.  32-bit words
+// (counts below 2^30) halve the uncached look-back traffic against 64-bit
+// ones (config 3: 17.2 -> 16.4 us per pass); larger sorts use 64-bit words.
+template <typename SW>
+struct SweepWord {
+  static constexpr int kFlagShift = 8 * static_cast<int>(sizeof(SW)) - 2;
+  static constexpr SW kAgg = SW(1) << kFlagShift;
+  static constexpr SW kIncl = SW(2) << kFlagShift;
+  static constexpr SW kValue = kAgg - 1;
+};
 
 // status: [tiles][kRadix] zeroed words; ticket: zeroed next-tile counter.
 // ghist: this pass's digit counts, kHistCopies copies kHistCopyWords apart.
-template <bool LAST>
-__global__ void __launch_bounds__(256)
+template <bool LAST, typename SW>
+__global__ void __launch_bounds__(kSweepThreads)
     onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
                     const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
-                    const uint32_t* __restrict__ ghist, unsigned long long* status,
+                    const uint32_t* __restrict__ ghist, SW* status,
                     unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
                     int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
                     uint32_t* __restrict__ vals2_out) {
   __shared__ unsigned int s_tile;
-  __shared__ uint32_t cnt[4][kRadix];  // per-wave digit counts, then per-wave prefixes
+  __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
   __shared__ uint32_t s_base[kRadix];
+  __shared__ uint32_t s_wsum[kRadix / 64];
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   if (call_failed(faults.fail)) return;  // an earlier pass gave up: nothing valid to sort
   if (threadIdx.x == 0) s_tile = atomicAdd(ticket, 1u);
-  for (int i = threadIdx.x; i < 4 * kRadix; i += 256) (&cnt[0][0])[i] = 0u;
+  for (int i = threadIdx.x; i < kSweepWaves * kRadix; i += kSweepThreads) (&cnt[0][0])[i] = 0u;
   __syncthreads();
   const int64_t tile = s_tile;
   const int64_t i0 = tile * kSweepTile + w * kSweepWaveKeys + lane;
@@ -283,71 +300,88 @@ __global__ void __launch_bounds__(256)
     if (valid && (peers & lt) == 0ull) cnt[w][d] = before + static_cast<uint32_t>(__popcll(peers));
   }
   __syncthreads();
-  const int d = threadIdx.x;  // one digit per thread from here on
-  const uint32_t c0 = cnt[0][d], c1 = cnt[1][d], c2 = cnt[2][d], c3 = cnt[3][d];
-  const uint32_t total = c0 + c1 + c2 + c3;
-  cnt[0][d] = 0u;
-  cnt[1][d] = c0;
-  cnt[2][d] = c0 + c1;
-  cnt[3][d] = c0 + c1 + c2;
-  const bool used = d <= static_cast<int>(mask);  // same for every tile of the pass
-  uint32_t gall;
-  uint32_t gcount = 0u;
-  if (used) {
+  // Digit phase: the first kRadix threads (whole waves) own one digit each;
+  // the block's other waves only pass the barriers.
+  const int d = threadIdx.x;
+  const bool digit_wave = w < kRadix / 64;  // wave-uniform
+  const bool used = digit_wave && d <= static_cast<int>(mask);  // same for every tile of the pass
+  uint32_t total = 0u, incl = 0u;
+  if (digit_wave) {
 #pragma unroll
-    for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
+    for (int x = 0; x < kSweepWaves; ++x) {  // per-wave counts -> per-wave prefixes
+      const uint32_t c = cnt[x][d];
+      cnt[x][d] = total;
+      total += c;
+    }
+    uint32_t gcount = 0u;
+    if (used) {
+#pragma unroll
+      for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
+    }
+    incl = wave_incl_scan<SumOp>(gcount);
+    if (lane == 63) s_wsum[w] = incl;
   }
-  const uint32_t goff = block_excl_scan<SumOp>(gcount, &gall);
-  uint32_t prefix = 0u;
-  if (used) {
-    unsigned long long* mine = status + tile * kRadix + d;
-    if (tile == 0) {
-      __hip_atomic_store(mine, kSweepIncl | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      __hip_atomic_store(mine, kSweepAgg | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // Look back kLookBack predecessors per round (independent loads), folding
-      // them nearest first until an inclusive word; an unpublished word
-      // (flag 0) ends the round and the next round resumes there.  Wider
-      // rounds issue more uncached loads than they save in rounds (per pass
-      // at 2048-key tiles: 8 +0.6 us, 16 +2.2, 32 +5.1; 2 is no faster).
-      constexpr int kLookBack = 4;
-      int64_t j = tile - 1;  // nearest predecessor not yet folded in
-      int spins = 0;
-      bool done = false;
-      if (faults.spin_limit < 0) {  // test hook: give up at once
-        report_fault(faults);
-        done = true;
-      }
-      while (!done) {
-        unsigned long long x[kLookBack];
+  __syncthreads();
+  if (digit_wave) {
+    // Exclusive scan of the pass's digit counts: the digit's global base.
+    uint32_t goff = 0u;
 #pragma unroll
-        for (int q = 0; q < kLookBack; ++q)
-          x[q] = j - q >= 0 ? __hip_atomic_load(status + (j - q) * kRadix + d, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT)
-                            : kSweepIncl;  // before tile 0 (never reached: tile 0 is inclusive)
-        int folded = 0;
-#pragma unroll
-        for (int q = 0; q < kLookBack; ++q) {
-          if (done || folded < q) continue;  // stopped earlier in this round
-          const unsigned long long flag = x[q] >> 62;
-          if (flag == 0ull) continue;
-          prefix += static_cast<uint32_t>(x[q]);
-          folded = q + 1;
-          if (flag == 2ull) done = true;
+    for (int i = 0; i < kRadix / 64; ++i)
+      if (i < w) goff += s_wsum[i];
+    const uint32_t prev = __shfl_up(incl, 1, 64);
+    if (lane != 0) goff += prev;
+    uint32_t prefix = 0u;
+    if (used) {
+      using Word = SweepWord<SW>;
+      SW* mine = status + tile * kRadix + d;
+      if (tile == 0) {
+        __hip_atomic_store(mine, Word::kIncl | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        __hip_atomic_store(mine, Word::kAgg | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Look back kLookBack predecessors per round (independent loads), folding
+        // them nearest first until an inclusive word; an unpublished word
+        // (flag 0) ends the round and the next round resumes there.  Wider
+        // rounds issue more uncached loads than they save in rounds (per pass
+        // at 2048-key tiles: 8 +0.6 us, 16 +2.2, 32 +5.1; 2 is no faster).
+        constexpr int kLookBack = 4;
+        int64_t j = tile - 1;  // nearest predecessor not yet folded in
+        int spins = 0;
+        bool done = false;
+        if (faults.spin_limit < 0) {  // test hook: give up at once
+          report_fault(faults);
+          done = true;
         }
-        j -= folded;
-        if (!done && folded < kLookBack) {     // waiting on an unpublished predecessor
-          if (!keep_waiting(spins, faults)) {  // never expected; keeps the wait bounded
-            report_fault(faults);
-            break;
+        while (!done) {
+          SW x[kLookBack];
+#pragma unroll
+          for (int q = 0; q < kLookBack; ++q)
+            x[q] = j - q >= 0 ? __hip_atomic_load(status + (j - q) * kRadix + d, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : Word::kIncl;  // before tile 0 (never reached: tile 0 is inclusive)
+          int folded = 0;
+#pragma unroll
+          for (int q = 0; q < kLookBack; ++q) {
+            if (done || folded < q) continue;  // stopped earlier in this round
+            const SW flag = x[q] >> Word::kFlagShift;
+            if (flag == 0) continue;
+            prefix += static_cast<uint32_t>(x[q] & Word::kValue);
+            folded = q + 1;
+            if (flag == 2) done = true;
+          }
+          j -= folded;
+          if (!done && folded < kLookBack) {     // waiting on an unpublished predecessor
+            if (!keep_waiting(spins, faults)) {  // never expected; keeps the wait bounded
+              report_fault(faults);
+              break;
+            }
           }
         }
+        __hip_atomic_store(mine, Word::kIncl | (prefix + total), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
-      __hip_atomic_store(mine, kSweepIncl | (prefix + total), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
     }
+    s_base[d] = goff + prefix;
   }
-  s_base[d] = goff + prefix;
   __syncthreads();
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
@@ -362,6 +396,17 @@ __global__ void __launch_bounds__(256)
     vals_out[pos] = v[it];
     if (vals2) vals2_out[pos] = v2[it];
   }
+}
+
+// One sort pass over a workspace whose status words are of type SW.
+template <bool LAST, typename SW>
+void sweep(dim3 grid, hipStream_t s, const uint32_t* keys, const uint32_t* vals,
+           const uint32_t* vals2, int64_t n, int shift, int nbits, const uint32_t* ghist,
+           unsigned long long* status, unsigned int* ticket, const Faults& f, uint32_t* keys_out,
+           int64_t* keys_out64, uint32_t* vals_out, uint32_t* vals2_out) {
+  onesweep_kernel<LAST, SW><<<grid, kSweepThreads, 0, s>>>(
+      keys, vals, vals2, n, shift, nbits, ghist, reinterpret_cast<SW*>(status), ticket, f,
+      keys_out, keys_out64, vals_out, vals2_out);
 }
 
 __global__ void copy_keys_kernel(const uint32_t* __restrict__ keys,
@@ -605,15 +650,15 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     unsigned int* ticket = reinterpret_cast<unsigned int*>(st + ntiles * kRadix);
     const uint32_t* gh = w.ghist + p * kRadix;
     const Faults f = call_faults(w);
-    if (p == passes - 1) {
-      onesweep_kernel<true><<<gsweep, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f, nullptr,
-          o.sorted, reinterpret_cast<uint32_t*>(o.infos), v2_final);
-    } else {
-      onesweep_kernel<false><<<gsweep, 256, 0, s>>>(
-          w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f,
-          w.keys[cur ^ 1], nullptr, w.vals[cur ^ 1], v2[cur ^ 1]);
-    }
+    const bool last = p == passes - 1;
+    // Every count fits a 32-bit word's 30 bits.
+    const bool w32 = N < (int64_t(1) << 30) && !force_wide_sort_words();
+    const auto launch = last ? (w32 ? &sweep<true, uint32_t> : &sweep<true, unsigned long long>)
+                             : (w32 ? &sweep<false, uint32_t> : &sweep<false, unsigned long long>);
+    launch(gsweep, s, w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f,
+           last ? nullptr : w.keys[cur ^ 1], last ? o.sorted : nullptr,
+           last ? reinterpret_cast<uint32_t*>(o.infos) : w.vals[cur ^ 1],
+           last ? v2_final : v2[cur ^ 1]);
     MX_LAUNCH_CHECK();
     cur ^= 1;
   }
