@@ -9,8 +9,13 @@
 
 namespace mx {
 
-constexpr int kScanThreads = 256;
-constexpr int kScanItems = 12;  // 3072-element tiles (2048: +2.4 us, 4096: +2.8 us on 668k)
+// 3072-element tiles (2048: +2.4 us, 4096: +2.8 us on 668k) in blocks of 8
+// waves with 6 elements per lane: the run-head scan of config 3 takes 9.0 us
+// against 10.8 with 4 waves of 12 (more waves per SIMD hide the dependent
+// loads); 16 waves of 3 take 8.6 us alone but get fewer CU slots when the
+// chunk-count scan runs beside the update kernel.
+constexpr int kScanThreads = 512;
+constexpr int kScanItems = 6;
 constexpr int64_t kScanTile = kScanThreads * kScanItems;
 
 inline int64_t scan_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
@@ -37,7 +42,7 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Exclusive scan across a 256-thread block; returns the block aggregate in *total.
+// Exclusive scan across a block of kScanThreads threads; returns the block aggregate in *total.
 template <class Op = SumOp>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* total) {
   __shared__ uint32_t wsum[kScanThreads / 64];
@@ -113,9 +118,10 @@ constexpr unsigned long long kScanFlagAgg = 1ull << 62;
 constexpr unsigned long long kScanFlagIncl = 2ull << 62;
 constexpr int kScanSpinLimit = 1 << 22;
 
-// INCL = false: epi(i, op(f(0..i-1))) (identity at 0); true: epi(i, op(f(0..i))).
+// INCL = false: epi(i, op(f(0..i-1)), f(i)) (identity at 0); true: epi(i, op(f(0..i)), f(i)).
 // epi.total(aggregate) runs once, in the last tile.  An epilogue is a
-// functor with operator()(int64_t i, uint32_t scanned) and total(uint32_t).
+// functor with operator()(int64_t i, uint32_t scanned, uint32_t value) and
+// total(uint32_t); `value` is f(i), so the epilogue need not recompute it.
 template <class F, class Op, bool INCL, class Epi>
 __global__ void __launch_bounds__(kScanThreads)
     scan_onepass_kernel(F f, int64_t n, const int32_t* n_dev, Epi epi, ScanState st,
@@ -209,7 +215,7 @@ __global__ void __launch_bounds__(kScanThreads)
   for (int it = 0; it < kScanItems; ++it) {
     const int64_t i = base + it;
     if constexpr (INCL) run = Op::apply(run, v[it]);
-    if (i < m) epi(i, run);
+    if (i < m) epi(i, run, v[it]);
     if constexpr (!INCL) run = Op::apply(run, v[it]);
   }
 }

@@ -90,7 +90,8 @@ __global__ void __launch_bounds__(256)
                      int32_t passes, int64_t* __restrict__ linear_out,
                      uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
                      const float* __restrict__ iw, uint32_t* __restrict__ vals2,
-                     uint32_t* __restrict__ ghist) {
+                     uint32_t* __restrict__ ghist, unsigned long long* __restrict__ zero,
+                     int64_t zero_words) {
   __shared__ uint32_t s_mark[kLinTile];  // bag (relative to blo) starting at each position
   __shared__ int64_t s_range[2][2];      // [half][lo, hi] of the cooperative searches
   __shared__ uint32_t s_cnt[2][2];       // [half][wave of the half]
@@ -100,6 +101,10 @@ __global__ void __launch_bounds__(256)
   const int64_t l0 = static_cast<int64_t>(blockIdx.x) * kLinTile;
   const int64_t lend = l0 + kLinTile < N ? l0 + kLinTile : N;
   const int64_t pbase = l0 + w * kLinWavePos + lane;  // item it: pbase + it * 64
+  // The later kernels' zeroed state, spread over the grid.
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < zero_words;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    zero[i] = 0ull;
   I idx[kLinItems];
 #pragma unroll
   for (int it = 0; it < kLinItems; ++it) {  // in flight during the searches below
@@ -448,8 +453,8 @@ struct RleEpi {
   int32_t* cum;
   uint32_t* num_runs;        // device count used by later kernels
   int32_t* num_runs_out;     // the op's int32 output, may be null
-  __device__ void operator()(int64_t i, uint32_t r) const {
-    if (i == 0 || keys[i] != keys[i - 1]) {
+  __device__ void operator()(int64_t i, uint32_t r, uint32_t head) const {
+    if (head) {
       run_keys[r] = keys[i];
       cum[r] = static_cast<int32_t>(i);
     }
@@ -502,9 +507,8 @@ struct ChunkEpi {
   uint32_t* chunk_start;
   uint32_t* chunk_mark;
   uint32_t* total_chunks;
-  __device__ void operator()(int64_t r, uint32_t q0) const {
+  __device__ void operator()(int64_t r, uint32_t q0, uint32_t nq) const {
     chunk_start[r] = q0;
-    const uint32_t nq = ChunkCount{cum}(r);
     for (uint32_t j = 0; j < nq; j += kMarkEvery)
       chunk_mark[q0 + j] = (static_cast<uint32_t>(r) + 1u) | (j == 0 ? kRunStart : 0u);
   }
@@ -558,26 +562,37 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
   const size_t hist_bytes = align256(kHistCopies * kHistCopyWords * 4);
   const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
-  uint8_t* z = take(status_bytes + scan_bytes + hist_bytes + mark_bytes +
+  // Zeroed state: the failure word and the digit histograms (cleared before
+  // linearize, which adds into the histograms), then the scans' and passes'
+  // look-back state and the chunk marks (cleared by linearize itself).
+  uint8_t* z = take(status_bytes + hist_bytes + scan_bytes + mark_bytes +
                     kMaxPasses * w.sweep_words * 8);
   w.zeroed = reinterpret_cast<unsigned long long*>(z);
   w.fail = reinterpret_cast<unsigned int*>(z);
-  if (z) z += status_bytes;
-  w.scan_state = reinterpret_cast<unsigned long long*>(z);
-  w.ghist = z ? reinterpret_cast<uint32_t*>(z + scan_bytes) : nullptr;
-  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + scan_bytes + hist_bytes) : nullptr;
-  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + scan_bytes + hist_bytes + mark_bytes)
+  w.ghist = z ? reinterpret_cast<uint32_t*>(z + status_bytes) : nullptr;
+  w.scan_state = z ? reinterpret_cast<unsigned long long*>(z + status_bytes + hist_bytes) : nullptr;
+  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + status_bytes + hist_bytes + scan_bytes)
+                   : nullptr;
+  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + status_bytes + hist_bytes + scan_bytes +
+                                                      mark_bytes)
               : nullptr;
   w.counters = reinterpret_cast<uint32_t*>(take(64));
   w.bytes = off;
   return w;
 }
 
-// Words to clear for a sort of `passes` passes (the sweep state of unused
-// passes is left alone).
-int64_t zeroed_words(const SortWs& w, int passes) {
-  return (static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.sweep) -
-                               reinterpret_cast<uint8_t*>(w.zeroed))) / 8 +
+// Words cleared before linearize: the failure word and the histograms.
+int64_t early_zeroed_words(const SortWs& w) {
+  return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.scan_state) -
+                              reinterpret_cast<uint8_t*>(w.zeroed)) / 8;
+}
+
+// Words linearize clears for a sort of `passes` passes: the scan state, the
+// chunk marks and the sweep state of those passes (unused passes' state is
+// left alone).
+int64_t late_zeroed_words(const SortWs& w, int passes) {
+  return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.sweep) -
+                              reinterpret_cast<uint8_t*>(w.scan_state)) / 8 +
          passes * w.sweep_words;
 }
 
@@ -616,22 +631,26 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
   uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
   const int passes = (bits + kRadixBits - 1) / kRadixBits;
-  {  // look-back state of every scan and pass, and the histograms, start at zero
-    const int64_t words = zeroed_words(w, passes);
+  {  // the failure word and the histograms start at zero
+    const int64_t words = early_zeroed_words(w);
     const int64_t blocks = ceil_div(words, 256);
     zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 2048 ? blocks : 2048)), 256, 0, s>>>(
         w.zeroed, words);
     MX_LAUNCH_CHECK();
   }
+  // Linearize also clears the look-back state of the later kernels.
+  const int64_t late_words = late_zeroed_words(w, passes);
   const dim3 glin(static_cast<uint32_t>(ceil_div(N, kLinTile)));
   if (index_bytes == 8)
     linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
-        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
+        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
+        w.scan_state, late_words);
   else
     linearize_kernel<int32_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
-        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist);
+        nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
+        w.scan_state, late_words);
   MX_LAUNCH_CHECK();
 
   const int64_t ntiles = sweep_tiles(N);
