@@ -61,7 +61,9 @@ constexpr int kSweepItems = 3;                                 // keys per lane 
 constexpr int64_t kSweepWaveKeys = 64 * kSweepItems;
 constexpr int64_t kSweepTile = kSweepWaves * kSweepWaveKeys;  // keys per block
 static_assert(kSweepThreads >= 256, "the first 256 threads own one digit each");
-constexpr int kLinItems = 8;
+// 1024-position linearize blocks: 654 blocks on config 3, 2-3 per CU, whose
+// dependent search and marking loads overlap (11.8 -> 10.5 us against 2048).
+constexpr int kLinItems = 4;
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
 constexpr int kLong = 32;                             // runs longer than this are chunked
 constexpr int kChunk = 32;                            // occurrences per chunk
