@@ -257,11 +257,8 @@ size_t mx_tbe_backward_workspace_bytes(int64_t N, int32_t total_hash_size_bits, 
  * last place, then truncated, the random bits a hash of (rng, element); rng
  * may be NULL when stochastic_rounding is 0)
  * and momentum1 (fp32 [E_t] per table at momentum1_offsets[t]) are updated
- * in place; no atomics, deterministic for a given random state.  Rows with
- * more than 32 occurrences are updated on a second stream kept for `stream`
- * (one per device and caller stream), forked from `stream` by an event and
- * joined back into it before the call returns, so the call is ordered on
- * `stream` like any other (also under graph capture). */
+ * in place; no atomics, deterministic for a given random state.  Every
+ * kernel of the call runs on `stream` (also under graph capture). */
 int mx_tbe_backward_rowwise_adagrad(
     void* weights, int32_t weights_ty, const int64_t* weights_offsets, const int32_t* D_offsets,
     int32_t T, int64_t B, int32_t max_D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,

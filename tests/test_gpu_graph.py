@@ -1,7 +1,6 @@
 """TBE training steps captured in a HIP graph (torch.cuda.CUDAGraph): the
-forward lookup and the fused backward + rowwise-Adagrad update, whose
-long-run path forks onto a second stream and joins back into the caller's.
-Each replay must equal the same step run eagerly (both paths are atomic-free,
+forward lookup and the fused backward + rowwise-Adagrad update, every
+kernel of both on the caller's stream.  Each replay must equal the same step run eagerly (both paths are atomic-free,
 so bit-identical), with eager work and synchronisations between replays."""
 
 import numpy as np
@@ -79,10 +78,9 @@ def test_training_step_graph_replays_match_eager(dev):
 
 
 def test_backward_on_two_streams_from_two_threads(dev):
-    """Two host threads run training steps on their own streams at once; both
-    fork their long-run path onto the device's one second stream.  Each
-    thread's tables end bit-identical to the same steps run one after the
-    other."""
+    """Two host threads run training steps on their own streams at once.
+    Each thread's tables end bit-identical to the same steps run one after
+    the other."""
     import threading
 
     print("[case] concurrent backward on two streams", flush=True)
@@ -126,8 +124,8 @@ def test_backward_on_two_streams_from_two_threads(dev):
 def test_capture_on_one_thread_while_another_trains_eagerly(dev):
     """One host thread captures a training step on its stream and replays it
     while another runs eager steps on its own stream at the same time.  Each
-    caller stream has its own second stream, so the capture takes in none of
-    the other thread's work: both end bit-identical to the same steps run in
+    call stays on its caller's stream, so the capture takes in none of the
+    other thread's work: both end bit-identical to the same steps run in
     turn."""
     import threading
 
@@ -150,8 +148,8 @@ def test_capture_on_one_thread_while_another_trains_eagerly(dev):
     torch.cuda.synchronize()
 
     s_cap, s_eager = torch.cuda.Stream(), torch.cuda.Stream()
-    # Warm-up step on each stream with throwaway state: creates each stream's
-    # second stream, and the allocator's blocks, before the capture starts.
+    # Warm-up step on each stream with throwaway state: the allocator's
+    # blocks exist before the capture starts.
     for st in (s_cap, s_eager):
         with torch.cuda.stream(st):
             _step_fn(dev, inp, W0.clone(), torch.zeros(nM, device=dev), grads[0].clone())()

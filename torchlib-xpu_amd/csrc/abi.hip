@@ -1,9 +1,7 @@
 // Status reporting and device queries shared by every entry point.
 #include <atomic>
-#include <map>
 #include <mutex>
 #include <string>
-#include <utility>
 
 #include "mx_common.h"
 #include "scan.h"
@@ -39,29 +37,6 @@ int num_cus() {
     cached[dev] = n;
   }
   return cached[dev];
-}
-
-bool side_path(hipStream_t caller, SidePath* out) {
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, SidePath> cached;  // kept until the process ends
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(dev, caller);
-  auto it = cached.find(key);
-  if (it == cached.end()) {
-    SidePath p{};
-    if (hipStreamCreateWithFlags(&p.side, hipStreamNonBlocking) != hipSuccess) return false;
-    if (hipEventCreateWithFlags(&p.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&p.join, hipEventDisableTiming) != hipSuccess) {
-      if (p.fork) (void)hipEventDestroy(p.fork);
-      (void)hipStreamDestroy(p.side);
-      return false;
-    }
-    it = cached.emplace(key, p).first;
-  }
-  *out = it->second;
-  return true;
 }
 
 namespace {

@@ -21,19 +21,6 @@ void clear_error();
 
 // Number of compute units of the current device (cached per device).
 int num_cus();
-// A second stream of the current device (non-blocking, default priority) and
-// the fork/join event pair of work split off `caller`, one set per (device,
-// caller stream), created on first use and kept until the process ends.
-// Work forked onto `side` is joined back into `caller` before an entry point
-// returns.  Keyed by the caller's stream, so a graph capture on one stream
-// never takes in work that another thread forks from its own stream.
-// Returns false if the stream or events cannot be created.
-struct SidePath {
-  hipStream_t side;
-  hipEvent_t fork;
-  hipEvent_t join;
-};
-bool side_path(hipStream_t caller, SidePath* out);
 
 // Host-visible word registered for the current device (mx_set_status_mailbox),
 // or null: a look-back that gives up stores 1 there.

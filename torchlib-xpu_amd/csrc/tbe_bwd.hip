@@ -803,9 +803,9 @@ struct XcdRange {
 };
 
 template <int P>
-__device__ __forceinline__ XcdRange xcd_range(int64_t total) {
+__device__ __forceinline__ XcdRange xcd_range(int64_t total, int64_t bid, int64_t nblk) {
   constexpr int64_t kXcd = 8;
-  const int64_t x = blockIdx.x % kXcd, j = blockIdx.x / kXcd, per = gridDim.x / kXcd;
+  const int64_t x = bid % kXcd, j = bid / kXcd, per = nblk / kXcd;
   const int64_t begin = total * x / kXcd;
   const int64_t wave = threadIdx.x >> 6;
   return {begin + (j * 4 + wave) * P, per * 4 * P, total * (x + 1) / kXcd};
@@ -986,21 +986,18 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
 // vectors are combined in group order through LDS, and group 0 applies the
 // update.
 constexpr int kLongRange = 4;  // chunks per block range
+constexpr int kLongBlocksPerCu = 2;  // long-run blocks of the runs launch, per CU
 
 template <typename WT, int G, int NCH, int U>
-__global__ void __launch_bounds__(256) bwd_long_run_kernel(BwdArgs a) {
-  if (call_failed(a.fail)) return;  // the run layout is not valid
-  __shared__ TableMeta meta;
+__device__ __forceinline__ void long_run_body(const BwdArgs& a, const MetaView& mv, int64_t bid,
+                                              int64_t nblk) {
   constexpr int NG = 256 / G;
   __shared__ float part[NG][G * NCH * 4];
   __shared__ uint32_t s_runs[kLongRange];
   __shared__ int s_nruns;
-  stage_meta(a, meta);
-  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
   const int grp = threadIdx.x / G, k = threadIdx.x % G;
   const int64_t total = *a.total_chunks;
-  for (int64_t q0 = static_cast<int64_t>(blockIdx.x) * kLongRange; q0 < total;
-       q0 += static_cast<int64_t>(gridDim.x) * kLongRange) {
+  for (int64_t q0 = bid * kLongRange; q0 < total; q0 += nblk * kLongRange) {
     if (threadIdx.x < 64) {  // wave 0 lists the runs starting in the range, in order
       const int64_t q = q0 + threadIdx.x;
       const bool in = threadIdx.x < kLongRange && q < total;
@@ -1087,7 +1084,7 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
   constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
-  const XcdRange xr = xcd_range<P>(*a.total_chunks);
+  const XcdRange xr = xcd_range<P>(*a.total_chunks, blockIdx.x, gridDim.x);
   for (int64_t qb = xr.first; qb < xr.end; qb += xr.step) {
     const int64_t q = qb + g;
     if (q >= xr.end) continue;
@@ -1124,20 +1121,17 @@ __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
 // table of a run comes from the first batch of infos, which is kept for the
 // gradient sum.
 template <typename I, typename WT, int G, int NCH, int U>
-__global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
-  if (call_failed(a.fail)) return;  // the run layout is not valid
-  __shared__ TableMeta meta;
-  stage_meta(a, meta);
-  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
+__device__ __forceinline__ void short_run_body(const BwdArgs& a, const MetaView& mv, int64_t bid,
+                                               int64_t nblk) {
   constexpr int P = 64 / G;
   const int lane = threadIdx.x & 63;
   const int g = lane / G, k = lane % G;
-  const XcdRange xr = xcd_range<P>(*a.num_runs);
+  const XcdRange xr = xcd_range<P>(*a.num_runs, bid, nblk);
   for (int64_t r = xr.first + g; r < xr.end; r += xr.step) {
     const int64_t cs0 = a.cum[r];
     const int64_t cs1 = a.cum[r + 1];
     const int64_t ckey = a.run[r];
-    if (cs1 - cs0 > kLong) continue;  // long runs: bwd_long_run_kernel
+    if (cs1 - cs0 > kLong) continue;  // long runs: long_run_body
     const int32_t info0 = k < cs1 - cs0 ? a.infos[cs0 + k] : 0;
     const int64_t t = table_of(a, __shfl(info0, g * G, 64));
     const int32_t D0 = mv.D_off(t);
@@ -1161,69 +1155,62 @@ __global__ void __launch_bounds__(256) bwd_update_kernel(BwdArgs a) {
   }
 }
 
-// Runs longer than kLong: chunk partial sums, then one block per run.
+// Both run classes in one launch: they update disjoint rows and momentum
+// words and need nothing of each other.  The first `nlong` blocks (a multiple
+// of 8, so that block i of the short-run part still runs on XCD i % 8) combine
+// the long runs' chunk partials; the others sum and update the short runs.
+// The long-run blocks are latency-bound and finish under the short-run
+// blocks' row read-modify-writes (config 3: 164.7 us per backward against
+// 175.5 with the long runs on a second stream, forked and joined around the
+// update).  Rows of up to 2 float4 chunks per lane are held to 80 registers
+// (6 waves per SIMD, the short-run part's own occupancy; a few long-run
+// values spill): 5 waves per SIMD took 167.5 us.
+template <int NCH>
+constexpr int runs_waves() {
+  return NCH <= 2 ? 6 : 1;
+}
+
+template <typename I, typename WT, int G, int NCH, int U, int GL, int NCHL, int UL>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(runs_waves<NCH>())))
+    bwd_runs_kernel(BwdArgs a, int64_t nlong) {
+  if (call_failed(a.fail)) return;  // the run layout is not valid
+  __shared__ TableMeta meta;
+  stage_meta(a, meta);
+  const MetaView mv{a, meta, a.T <= kMaxCachedTables};
+  if (static_cast<int64_t>(blockIdx.x) < nlong)
+    long_run_body<WT, GL, NCHL, UL>(a, mv, blockIdx.x, nlong);
+  else
+    short_run_body<I, WT, G, NCH, U>(a, mv, blockIdx.x - nlong, gridDim.x - nlong);
+}
+
+// After the run encoding: the chunk layout of the long runs (chunk-count
+// scan), their chunk partial sums, then both run classes in one launch.
 template <typename I, typename WT, int G, int NCH>
-int launch_long_runs(const BwdArgs& a, int64_t N, hipStream_t s) {
-  constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
+int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
+  if (int rc = prefix_scan_epi(
+          ChunkCount{a.cum}, N, reinterpret_cast<const int32_t*>(a.num_runs),
+          ChunkEpi{a.cum, chunk_start, ws.chunk_mark, &ws.counters[1]}, scan_slot(ws, 1), s))
+    return rc;
   constexpr int P = 64 / G;
+  const int64_t cus = num_cus();
   const int64_t want = ceil_div(N, 4 * P);
-  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
-  const int64_t nblk = want < 1 ? 1 : (want > cap ? cap : want);
-  const dim3 grid(static_cast<uint32_t>(ceil_div(nblk, 8) * 8));  // whole rounds over the XCDs
-  bwd_chunk_kernel<I, G, NCH, UC><<<grid, 256, 0, s>>>(a);
+  const int64_t nblk = want < 1 ? 1 : (want > cus * 16 ? cus * 16 : want);
+  const int64_t ngrid = ceil_div(nblk, 8) * 8;  // whole rounds over the XCDs
+  constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
+  bwd_chunk_kernel<I, G, NCH, UC><<<dim3(static_cast<uint32_t>(ngrid)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
-  const int64_t long_cap = static_cast<int64_t>(num_cus()) * 16;
-  const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
   // Long runs: twice the lanes per row where the row allows (more groups
   // summing partials per block; measured 15.1 -> 12.4 us on config 3).
   constexpr int GL = NCH >= 2 && G < 64 ? 2 * G : G;
   constexpr int NCHL = GL == 2 * G ? NCH / 2 : NCH;
-  bwd_long_run_kernel<WT, GL, NCHL, 4><<<dim3(static_cast<uint32_t>(long_want < long_cap ? (long_want < 1 ? 1 : long_want) : long_cap)), 256, 0, s>>>(a);
+  constexpr int U = NCH <= 1 ? 4 : 2;  // short runs: keep registers low
+  const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
+  const int64_t long_cap = cus * kLongBlocksPerCu;
+  const int64_t nlong = ceil_div(long_want < long_cap ? long_want : long_cap, 8) * 8;
+  bwd_runs_kernel<I, WT, G, NCH, U, GL, NCHL, 4>
+      <<<dim3(static_cast<uint32_t>(nlong + ngrid)), 256, 0, s>>>(a, nlong);
   MX_LAUNCH_CHECK();
   return MX_OK;
-}
-
-// Runs of at most kLong occurrences: the fused sum + update kernel.
-template <typename I, typename WT, int G, int NCH>
-int launch_short_runs(const BwdArgs& a, int64_t N, hipStream_t s) {
-  constexpr int U = NCH <= 1 ? 4 : 2;   // runs are short: keep registers low
-  constexpr int P = 64 / G;
-  const int64_t want = ceil_div(N, 4 * P);
-  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
-  const int64_t nblk = want < 1 ? 1 : (want > cap ? cap : want);
-  const dim3 grid(static_cast<uint32_t>(ceil_div(nblk, 8) * 8));  // whole rounds over the XCDs
-  bwd_update_kernel<I, WT, G, NCH, U><<<grid, 256, 0, s>>>(a);
-  MX_LAUNCH_CHECK();
-  return MX_OK;
-}
-
-// Chunk layout of the long runs (chunk-count scan), then both run classes.
-// Short and long runs update disjoint rows and momentum words, and the short
-// runs need nothing of the chunk layout, so the long-run path goes to a
-// second stream forked from `s` and joined back into it: the update kernel,
-// bound by its random row read-modify-writes, hides the latency-bound scan
-// and long-run kernels.
-template <typename I, typename WT, int G, int NCH>
-int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
-  SidePath sp{};
-  hipStream_t side = s;  // without a second stream: the same kernels in order
-  if (side_path(s, &sp) && hipEventRecord(sp.fork, s) == hipSuccess &&
-      hipStreamWaitEvent(sp.side, sp.fork, 0) == hipSuccess)
-    side = sp.side;
-  int rc = prefix_scan_epi(
-      ChunkCount{a.cum}, N, reinterpret_cast<const int32_t*>(a.num_runs),
-      ChunkEpi{a.cum, chunk_start, ws.chunk_mark, &ws.counters[1]},
-      scan_slot(ws, 1), side);
-  if (rc == MX_OK) rc = launch_long_runs<I, WT, G, NCH>(a, N, side);
-  const int rc_short = launch_short_runs<I, WT, G, NCH>(a, N, s);
-  if (side != s) {
-    if (hipEventRecord(sp.join, side) != hipSuccess ||
-        hipStreamWaitEvent(s, sp.join, 0) != hipSuccess) {
-      (void)hipStreamSynchronize(side);  // nothing may outlive the call unordered
-      if (rc == MX_OK) rc = set_error(MX_EHIP, "joining the long-run stream failed");
-    }
-  }
-  return rc != MX_OK ? rc : rc_short;
 }
 
 // Lanes per run (G) and float4 chunks per lane (NCH) from the widest table.
