@@ -341,6 +341,7 @@ def _update_fp64(inp, pooling, W, m1, m1_off, grad, lr, eps):
     (4, 252, [648, 772, 248, 556], [4, 300, 1, 1], 42, 1, False),
     (3, 291, [56, 104, 104], [50, 1, 1], 42, 0, False),
     (4, 195, [156, 56, 144, 12], [300, 1, 50, 70000], 44, 0, False),
+    (1, 174, [564], [1], 44, 1, False),  # one row: every occurrence in one run
 ])
 def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
     """Tables of 1-4 rows: runs of thousands of occurrences.  There the fp32 oracle's sequential sum drifts from the exact
