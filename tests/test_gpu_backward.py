@@ -374,11 +374,13 @@ def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
     np.testing.assert_allclose(m1d.cpu().numpy(), m64, rtol=1e-5, atol=0)
 
 
-def test_config3_full(dev):
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_config3_full(dev, pooling):
     """Config 3: config-2 indices (Zipf 1.05, up to ~8k duplicates of one row),
-    8 x 1M x 128 fp32 tables, grad N(0, 1e-2), lr 0.01, eps 1e-8, zero momentum.
-    Transpose bit-exact; updated weights/momentum vs oracle at rtol 1e-5."""
-    print("[case] config3 full size", flush=True)
+    8 x 1M x 128 fp32 tables, grad N(0, 1e-2), lr 0.01, eps 1e-8, zero momentum
+    (SUM, the config, and MEAN).  Transpose bit-exact; updated weights/momentum
+    vs oracle at rtol 1e-5."""
+    print(f"[case] config3 full size pooling={pooling}", flush=True)
     inp = bench_inputs.config2()
     _check_transpose(dev, inp)
     rng = np.random.default_rng(33)
@@ -393,14 +395,14 @@ def test_config3_full(dev):
     m1_off = (np.arange(T) * E).astype(np.int64)
     W_exp, m1_exp = orc.backward_rowwise_adagrad(
         W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
-        inp.total_hash_size_bits, inp.indices, inp.offsets, 0, grad, m1, m1_off, 0.01, 1e-8,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, 0.01, 1e-8,
         0.0, 0, orc.info_B_num_bits(T, inp.B))
     empty = torch.zeros(0, device=dev)
     torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
         torch.from_numpy(grad).to(dev), Wd, empty, empty, torch.zeros(T, dtype=torch.int32, device=dev),
         torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev), D,
         torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
-        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), 0,
+        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
         torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty,
         torch.zeros(T, dtype=torch.int32, device=dev), torch.from_numpy(m1_off).to(dev),
         1e-8, 0.01, 0.0, 0, 0.0)

@@ -139,6 +139,21 @@ def test_config2_full(dev):
                                atol=1e-4)
 
 
+def test_config2_full_mean_int32(dev):
+    """Config 2's batch at full size with MEAN pooling and int32 indices and
+    offsets: every bag bit-exact against the oracle (each column summed in
+    index order, then scaled by 1/L)."""
+    print("[case] config2 full size, MEAN, int32", flush=True)
+    inp = bench_inputs.config2()
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    W = torch.empty(8 * 1_000_000 * 128, device=dev).uniform_(-0.01, 0.01, generator=g)
+    got = tbe_forward_gpu(dev, W, inp, 1, torch.int32)
+    exp = orc.tbe_forward_f32(W.cpu().numpy(), weight_offsets(inp), inp.D_offsets, inp.B,
+                              inp.indices, inp.offsets, 1)
+    _exact(got, exp)
+
+
 def test_unserved_arguments_raise(dev):
     """UVM storage and a populated LXU cache are refused, not ignored."""
     print("[case] tbe fwd unserved arguments", flush=True)
