@@ -154,6 +154,21 @@ def test_config2_full_mean_int32(dev):
     _exact(got, exp)
 
 
+def test_config2_full_fp16_weighted(dev):
+    """Config 2's batch at full size with fp16 weight rows and per-sample
+    weights (SUM): every bag bit-exact against the oracle."""
+    print("[case] config2 full size, fp16 weights, weighted", flush=True)
+    inp = bench_inputs.config2()
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    W = torch.empty(8 * 1_000_000 * 128, dtype=torch.float16, device=dev).uniform_(-1, 1, generator=g)
+    iw = np.random.default_rng(3).uniform(0, 2, size=inp.N).astype(np.float32)
+    got = tbe_forward_gpu(dev, W, inp, 0, indice_weights=torch.from_numpy(iw))
+    exp = orc.tbe_forward_f32(W.cpu().numpy(), weight_offsets(inp), inp.D_offsets, inp.B,
+                              inp.indices, inp.offsets, 0, iw)
+    _exact(got, exp)
+
+
 def test_unserved_arguments_raise(dev):
     """UVM storage and a populated LXU cache are refused, not ignored."""
     print("[case] tbe fwd unserved arguments", flush=True)
