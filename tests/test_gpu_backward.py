@@ -55,6 +55,46 @@ def test_transpose_bit_exact(dev, T, B, rows, max_L, dup):
     _check_transpose(dev, inp, torch.int32)
 
 
+def test_transpose_keys_outside_their_table_sort_globally(dev):
+    """The sort handles each table's positions on its own only when every key
+    lies in its table's range; indices past a table's rows (keys in the next
+    table's range) make it sort all keys together, so the layout stays the
+    global stable order, bit-exact against the oracle."""
+    print("[case] transpose, keys outside their table's range", flush=True)
+    rng = np.random.default_rng(31)
+    inp = random_tbe(rng, 3, 400, [4] * 3, [1000, 1000, 1000], 30)
+    s0, e0 = int(inp.offsets[0]), int(inp.offsets[400])
+    inp.indices[s0:e0] = rng.integers(0, 1100, size=e0 - s0)  # up to 100 rows past table 0
+    _check_transpose(dev, inp)
+    _check_transpose(dev, inp, torch.int32)
+
+
+@pytest.mark.parametrize("T", [63, 64])
+def test_transpose_feature_segments(dev, T):
+    """Up to 63 features sort as per-feature segments, 64 as one batch.  The
+    batch mixes empty features (first, middle, last), a feature of exactly
+    one 3072-key sort tile, one of two tiles plus one key, and many short
+    ones: the layout is the global stable order either way."""
+    print(f"[case] transpose feature segments T={T}", flush=True)
+    rng = np.random.default_rng(6300 + T)
+    B = 64
+    lengths = rng.integers(0, 9, size=(T, B))
+    lengths[[0, 7, T - 1]] = 0
+    lengths[1] = 48                      # 3072 positions
+    lengths[2] = 96
+    lengths[2, 5] += 1                   # 6145 positions
+    rows = [int(r) for r in rng.integers(1, 5000, T)]
+    rows[1], rows[2] = 3, 70000          # long runs; a wide table
+    off = bench_inputs.offsets_from_lengths(lengths.reshape(-1))
+    idx = np.empty(int(off[-1]), dtype=np.int64)
+    for t in range(T):
+        s, e = int(off[t * B]), int(off[(t + 1) * B])
+        idx[s:e] = rng.integers(0, rows[t], size=e - s)
+    inp = bench_inputs.TbeInput(T=T, E=rows, D=[4] * T, B=B, indices=idx, offsets=off)
+    _check_transpose(dev, inp)
+    _check_transpose(dev, inp, torch.int32)
+
+
 @pytest.mark.parametrize("T,B,rows,max_L,dup", [
     (3, 50, [10, 1000, 70000], 20, False),
     (2, 300, [5000, 5000], 40, True),

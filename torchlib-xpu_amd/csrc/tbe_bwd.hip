@@ -12,17 +12,20 @@
 // Design:
 //  * Keys fit 32 bits whenever total_hash_size_bits <= 32, so the sort moves
 //    (u32 key, u32 info) pairs: ceil(bits/8) LSD passes of 8-bit digits.
-//  * linearize: a block takes 2048 consecutive positions, finds the bag range
+//  * linearize: a block takes 1024 consecutive positions, finds the bag range
 //    they span with two cooperative 128-ary searches, lets every non-empty
 //    bag mark its first position in LDS and gives each position the latest
 //    mark (a max-scan), so no per-position search.  The same kernel
-//    accumulates the global digit histograms of every pass (LDS, then one
-//    atomic per bin and block into its XCD's copy).
-//  * One launch per pass ("onesweep"): a block ranks a 3072-key tile (each
-//    wave 768 keys, 64 at a time, stable ranks from 8 ballots), then thread d
-//    finds how many keys of digit d earlier tiles hold through a decoupled
-//    look-back over per-(tile, digit) status words, and the tile scatters.
-//    Tiles take tickets in launch order, so every wait ends.
+//    accumulates the digit counts of every pass (LDS, then one atomic per bin
+//    and block into its XCD's copy): per feature for a fixed batch of at most
+//    kSegMaxT features (a global sort, when some key lies outside its table's
+//    range, sums them), else for the whole batch.
+//  * One launch per pass ("onesweep"): a block of 16 waves ranks a 3072-key
+//    tile (each wave 192 keys, 64 at a time, stable ranks from 8 ballots),
+//    then thread d finds how many keys of digit d earlier tiles of its
+//    segment (its feature's keys, or the whole batch) hold through a
+//    decoupled look-back over per-(tile, digit) status words, and the tile
+//    scatters.  Tiles take tickets in launch order, so every wait ends.
 //  * Run-length encoding is a head-flag scan whose epilogue writes the run
 //    keys and offsets.
 //  * Each run (one distinct (t, i)) is reduced by one G-lane group, lanes
@@ -64,6 +67,10 @@ static_assert(kSweepThreads >= 256, "the first 256 threads own one digit each");
 // 1024-position linearize blocks: 654 blocks on config 3, 2-3 per CU, whose
 // dependent search and marking loads overlap (11.8 -> 10.5 us against 2048).
 constexpr int kLinItems = 4;
+// Segmented sort: at most this many features (one segment each); their digit
+// counts are kept in one copy per XCD, like the batch's.
+constexpr int kSegMaxT = 63;
+constexpr int64_t kSegRow = static_cast<int64_t>(kHistCopies) * kMaxPasses * kRadix;  // per feature
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
 constexpr int kLong = 32;                             // runs longer than this are chunked
 constexpr int kChunk = 32;                            // occurrences per chunk
@@ -77,6 +84,24 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
   const int nb = bits - p * kRadixBits;
   return nb >= kRadixBits ? (kRadix - 1u) : ((1u << nb) - 1u);
 }
+
+// ---- segments -------------------------------------------------------------
+
+// The sort's segments, one per feature of a fixed batch with at most kSegMaxT
+// features.  When every key of feature t lies in [hsc[t], hsc[t+1]) and hsc
+// does not decrease, all keys of feature t precede those of feature t + 1:
+// sorting each feature's positions on its own gives the global order, each
+// segment's tiles (segments start at tile boundaries) look back only over
+// tiles of their own segment, and the chains are T times shorter.  Linearize
+// writes fpos and tprefix, counts each feature's digits, and sets `bad` if a
+// key lies outside its feature's range (then the passes sort globally).
+struct SegSort {
+  int64_t* fpos;         // [T + 1] first position of each feature's positions
+  int32_t* tprefix;      // [T + 1] first tile of each feature's segment
+  uint32_t* fhist;       // [T][kHistCopies][kMaxPasses][kRadix] digit counts (zeroed), a pass's row
+  unsigned int* bad;     // zeroed; nonzero: sort globally
+  int32_t T;             // 0: no segments
+};
 
 // ---- linearize ------------------------------------------------------------
 
@@ -93,8 +118,11 @@ __global__ void __launch_bounds__(256)
                      uint32_t* __restrict__ keys, uint32_t* __restrict__ vals,
                      const float* __restrict__ iw, uint32_t* __restrict__ vals2,
                      uint32_t* __restrict__ ghist, unsigned long long* __restrict__ zero,
-                     int64_t zero_words) {
+                     int64_t zero_words, SegSort seg) {
   __shared__ uint32_t s_mark[kLinTile];  // bag (relative to blo) starting at each position
+  __shared__ uint32_t hf[2][kMaxPasses][kRadix];  // digit counts of the block's first two features
+  __shared__ int s_bad;
+  __shared__ int64_t s_rows[2];
   __shared__ int64_t s_range[2][2];      // [half][lo, hi] of the cooperative searches
   __shared__ uint32_t s_cnt[2][2];       // [half][wave of the half]
   __shared__ uint32_t s_wmax[4];
@@ -150,7 +178,20 @@ __global__ void __launch_bounds__(256)
     }
   }
   const int64_t blo = s_range[0][0], bhi = s_range[1][0];
-  for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
+  // Digit counts: of the whole batch (no segments), or per feature, which
+  // also give the whole batch's when the passes sort globally.
+  if (seg.T > 0)
+    for (int i = threadIdx.x; i < 2 * kMaxPasses * kRadix; i += 256) (&hf[0][0][0])[i] = 0u;
+  else
+    for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
+  const int64_t t_lo = seg.T > 0 ? blo / B : 0;  // the block's first feature
+  if (threadIdx.x == 0) {
+    s_bad = 0;
+    if (seg.T > 0) {  // row counts of the block's first two features
+      s_rows[0] = hsc[t_lo + 1] - hsc[t_lo];
+      s_rows[1] = t_lo + 1 < seg.T ? hsc[t_lo + 2] - hsc[t_lo + 1] : 0;
+    }
+  }
   // Bag of every position without a search when the block spans few bags:
   // each non-empty bag marks its first position, and position l's bag is the
   // largest mark at or before l (an inclusive max-scan; bag ids grow with
@@ -227,10 +268,56 @@ __global__ void __launch_bounds__(256)
     keys[l] = k32;
     vals[l] = info;
     if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
-    for (int p = 0; p < passes; ++p)
-      atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
+    if (seg.T == 0) {
+      for (int p = 0; p < passes; ++p)
+        atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
+    } else {
+      const int64_t i64 = static_cast<int64_t>(idx[it]);
+      const int64_t tf = t - t_lo;
+      const int64_t rows_t = tf == 0 ? s_rows[0] : (tf == 1 ? s_rows[1] : hsc[t + 1] - hsc[t]);
+      if (i64 < 0 || i64 >= rows_t) s_bad = 1;  // outside its feature's range
+      for (int p = 0; p < passes; ++p) {
+        const uint32_t d = (k32 >> (p * kRadixBits)) & digit_mask(bits, p);
+        if (tf == 0 || tf == 1)
+          atomicAdd(&hf[tf][p][d], 1u);
+        else  // a block over three or more features (short features): straight to memory
+          atomicAdd(&seg.fhist[t * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords +
+                               p * kRadix + d], 1u);
+      }
+    }
   }
   __syncthreads();
+  if (seg.T > 0) {
+    if (threadIdx.x == 0 && s_bad) *seg.bad = 1u;
+    const int nbins = passes * kRadix;
+    const int rot = static_cast<int>(blockIdx.x * 97u % static_cast<uint32_t>(nbins));
+    for (int f = 0; f < 2 && t_lo + f < seg.T; ++f)
+      for (int jj = threadIdx.x; jj < nbins; jj += 256) {
+        const int j = jj + rot < nbins ? jj + rot : jj + rot - nbins;
+        const uint32_t c = (&hf[f][0][0])[j];
+        if (c)
+          atomicAdd(&seg.fhist[(t_lo + f) * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords + j],
+                    c);
+      }
+    if (seg.T > 0 && blockIdx.x == 0 && w == 0) {
+      // Lane f <= T: feature f's first position; its segment's tile count; the
+      // features' first tiles by a wave scan.  hsc and the positions must not
+      // decrease for the segments to be in key order.
+      const int T = seg.T;
+      const int64_t fp = lane <= T ? static_cast<int64_t>(offsets[static_cast<int64_t>(lane) * B]) : 0;
+      const int64_t fnext = __shfl(fp, lane + 1 < 64 ? lane + 1 : 63, 64);
+      const uint32_t nt = lane < T ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
+      const uint32_t incl = wave_incl_scan<SumOp>(nt);
+      // The segments must also cover exactly the positions [0, N).
+      bool bad = (lane < T && (fnext < fp || hsc[lane + 1] < hsc[lane])) ||
+                 (lane == 0 && fp != 0) || (lane == T && fp != N);
+      if (lane <= T) seg.fpos[lane] = fp;
+      if (lane < T) seg.tprefix[lane + 1] = static_cast<int32_t>(incl);
+      if (lane == 0) seg.tprefix[0] = 0;
+      if (__any(bad) && lane == 0) *seg.bad = 1u;
+    }
+    return;
+  }
   // Into this XCD's copy, each block starting at another bin so that blocks
   // finishing together do not queue on the same counters.
   uint32_t* gcopy = ghist + (blockIdx.x % kHistCopies) * kHistCopyWords;
@@ -266,7 +353,7 @@ __global__ void __launch_bounds__(kSweepThreads)
                     const uint32_t* __restrict__ ghist, SW* status,
                     unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
                     int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
-                    uint32_t* __restrict__ vals2_out) {
+                    uint32_t* __restrict__ vals2_out, SegSort seg) {
   __shared__ unsigned int s_tile;
   __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
   __shared__ uint32_t s_base[kRadix];
@@ -278,12 +365,32 @@ __global__ void __launch_bounds__(kSweepThreads)
   for (int i = threadIdx.x; i < kSweepWaves * kRadix; i += kSweepThreads) (&cnt[0][0])[i] = 0u;
   __syncthreads();
   const int64_t tile = s_tile;
-  const int64_t i0 = tile * kSweepTile + w * kSweepWaveKeys + lane;
+  // The tile's positions [pbeg, pend) and the first tile of its look-back
+  // chain: its feature's first tile (segments), or tile 0.  Tiles past the
+  // last real tile return (nobody waits on them: their tickets are last).
+  const bool segm = seg.T > 0 && __hip_atomic_load(seg.bad, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) == 0u;
+  int64_t pbeg, pend, tile0 = 0, f = 0;
+  if (segm) {
+    const bool mine = lane < seg.T && seg.tprefix[lane] <= tile && tile < seg.tprefix[lane + 1];
+    const uint64_t m = __ballot(mine);  // one feature at most (wave-uniform)
+    if (m == 0ull) return;              // block-uniform: past every segment
+    f = __ffsll(static_cast<long long>(m)) - 1;
+    tile0 = seg.tprefix[f];
+    const int64_t fe = seg.fpos[f + 1] < n ? seg.fpos[f + 1] : n;  // fpos[T] == n (checked)
+    pbeg = seg.fpos[f] + (tile - tile0) * kSweepTile;
+    pend = pbeg + kSweepTile < fe ? pbeg + kSweepTile : fe;
+  } else {
+    pbeg = tile * kSweepTile;
+    if (pbeg >= n) return;  // block-uniform
+    pend = pbeg + kSweepTile < n ? pbeg + kSweepTile : n;
+  }
+  const int64_t i0 = pbeg + w * kSweepWaveKeys + lane;
   uint32_t k[kSweepItems], v[kSweepItems], v2[kSweepItems], rank[kSweepItems];
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
     const int64_t i = i0 + it * 64;
-    const bool valid = i < n;
+    const bool valid = i < pend;
     k[it] = valid ? keys[i] : 0u;
     v[it] = valid ? vals[i] : 0u;
     v2[it] = (valid && vals2) ? vals2[i] : 0u;
@@ -292,7 +399,7 @@ __global__ void __launch_bounds__(kSweepThreads)
   const uint64_t lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
-    const bool valid = i0 + it * 64 < n;
+    const bool valid = i0 + it * 64 < pend;
     const uint32_t d = (k[it] >> shift) & mask;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < nbits; ++bit) {
@@ -321,7 +428,13 @@ __global__ void __launch_bounds__(kSweepThreads)
       total += c;
     }
     uint32_t gcount = 0u;
-    if (used) {
+    if (used && segm) {
+#pragma unroll
+      for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[f * kSegRow + x * kHistCopyWords + d];
+    } else if (used && seg.T > 0) {  // sorting globally after linearize counted per feature
+      for (int t = 0; t < seg.T; ++t)
+        for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[t * kSegRow + x * kHistCopyWords + d];
+    } else if (used) {
 #pragma unroll
       for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
     }
@@ -337,11 +450,12 @@ __global__ void __launch_bounds__(kSweepThreads)
       if (i < w) goff += s_wsum[i];
     const uint32_t prev = __shfl_up(incl, 1, 64);
     if (lane != 0) goff += prev;
+    if (segm) goff += static_cast<uint32_t>(seg.fpos[f]);  // the segment's first position
     uint32_t prefix = 0u;
     if (used) {
       using Word = SweepWord<SW>;
       SW* mine = status + tile * kRadix + d;
-      if (tile == 0) {
+      if (tile == tile0) {
         __hip_atomic_store(mine, Word::kIncl | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         __hip_atomic_store(mine, Word::kAgg | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -362,9 +476,9 @@ __global__ void __launch_bounds__(kSweepThreads)
           SW x[kLookBack];
 #pragma unroll
           for (int q = 0; q < kLookBack; ++q)
-            x[q] = j - q >= 0 ? __hip_atomic_load(status + (j - q) * kRadix + d, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : Word::kIncl;  // before tile 0 (never reached: tile 0 is inclusive)
+            x[q] = j - q >= tile0 ? __hip_atomic_load(status + (j - q) * kRadix + d,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : Word::kIncl;  // before the chain (never reached: its first tile is inclusive)
           int folded = 0;
 #pragma unroll
           for (int q = 0; q < kLookBack; ++q) {
@@ -392,7 +506,7 @@ __global__ void __launch_bounds__(kSweepThreads)
   __syncthreads();
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
-    if (i0 + it * 64 >= n) continue;
+    if (i0 + it * 64 >= pend) continue;
     const uint32_t dd = (k[it] >> shift) & mask;
     const uint32_t pos = s_base[dd] + cnt[w][dd] + rank[it];
     if (pos >= n) continue;  // never, unless a look-back gave up; keeps stores in bounds
@@ -410,10 +524,10 @@ template <bool LAST, typename SW>
 void sweep(dim3 grid, hipStream_t s, const uint32_t* keys, const uint32_t* vals,
            const uint32_t* vals2, int64_t n, int shift, int nbits, const uint32_t* ghist,
            unsigned long long* status, unsigned int* ticket, const Faults& f, uint32_t* keys_out,
-           int64_t* keys_out64, uint32_t* vals_out, uint32_t* vals2_out) {
+           int64_t* keys_out64, uint32_t* vals_out, uint32_t* vals2_out, const SegSort& seg) {
   onesweep_kernel<LAST, SW><<<grid, kSweepThreads, 0, s>>>(
       keys, vals, vals2, n, shift, nbits, ghist, reinterpret_cast<SW*>(status), ticket, f,
-      keys_out, keys_out64, vals_out, vals2_out);
+      keys_out, keys_out64, vals_out, vals2_out, seg);
 }
 
 __global__ void copy_keys_kernel(const uint32_t* __restrict__ keys,
@@ -522,8 +636,12 @@ struct ChunkEpi {
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 int64_t sweep_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kSweepTile); }
+// Tiles of a pass, with room for segments: each of up to kSegMaxT segments
+// starts at a tile boundary, so they need at most kSegMaxT more tiles.
+int64_t sweep_status_tiles(int64_t n) { return sweep_tiles(n) + kSegMaxT; }
 // Per pass: [tiles][kRadix] status words, then one word holding the ticket pair.
-int64_t sweep_pass_words(int64_t n) { return sweep_tiles(n) * kRadix + 32; }
+int64_t sweep_pass_words(int64_t n) { return sweep_status_tiles(n) * kRadix + 32; }
+constexpr size_t kSegHistBytes = static_cast<size_t>(kSegMaxT) * kSegRow * 4;
 
 struct SortWs {
   uint32_t* keys[2];
@@ -536,6 +654,10 @@ struct SortWs {
   unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
   uint32_t* ghist;                 // [kHistCopies][kMaxPasses][kRadix]
+  uint32_t* fhist;                 // [kSegMaxT][kHistCopies][kMaxPasses][kRadix] per-feature digit counts
+  unsigned int* seg_bad;           // nonzero: the passes sort globally
+  int64_t* fpos;                   // [kSegMaxT + 1] (written by linearize)
+  int32_t* tprefix;                // [kSegMaxT + 1] (written by linearize)
   uint32_t* chunk_mark;            // [max_chunks(N)] (backward only)
   unsigned long long* sweep;       // kMaxPasses x sweep_pass_words
   int64_t sweep_words;
@@ -564,29 +686,34 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
   const size_t hist_bytes = align256(kHistCopies * kHistCopyWords * 4);
   const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
-  // Zeroed state: the failure word and the digit histograms (cleared before
-  // linearize, which adds into the histograms), then the scans' and passes'
-  // look-back state and the chunk marks (cleared by linearize itself).
-  uint8_t* z = take(status_bytes + hist_bytes + scan_bytes + mark_bytes +
-                    kMaxPasses * w.sweep_words * 8);
+  // Zeroed state: the failure and segment words, the digit histograms and
+  // the per-feature digit counts (cleared before linearize, which adds into
+  // the counts), then the scans' and passes' look-back state and the chunk
+  // marks (cleared by linearize itself).
+  const size_t early_bytes = status_bytes + hist_bytes + kSegHistBytes;
+  uint8_t* z = take(early_bytes + scan_bytes + mark_bytes + kMaxPasses * w.sweep_words * 8);
   w.zeroed = reinterpret_cast<unsigned long long*>(z);
   w.fail = reinterpret_cast<unsigned int*>(z);
+  w.seg_bad = z ? reinterpret_cast<unsigned int*>(z + 64) : nullptr;
   w.ghist = z ? reinterpret_cast<uint32_t*>(z + status_bytes) : nullptr;
-  w.scan_state = z ? reinterpret_cast<unsigned long long*>(z + status_bytes + hist_bytes) : nullptr;
-  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + status_bytes + hist_bytes + scan_bytes)
-                   : nullptr;
-  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + status_bytes + hist_bytes + scan_bytes +
-                                                      mark_bytes)
+  w.fhist = z ? reinterpret_cast<uint32_t*>(z + status_bytes + hist_bytes) : nullptr;
+  w.scan_state = z ? reinterpret_cast<unsigned long long*>(z + early_bytes) : nullptr;
+  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + early_bytes + scan_bytes) : nullptr;
+  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + early_bytes + scan_bytes + mark_bytes)
               : nullptr;
+  w.fpos = reinterpret_cast<int64_t*>(take((kSegMaxT + 1) * 8));
+  w.tprefix = reinterpret_cast<int32_t*>(take((kSegMaxT + 1) * 4));
   w.counters = reinterpret_cast<uint32_t*>(take(64));
   w.bytes = off;
   return w;
 }
 
-// Words cleared before linearize: the failure word and the histograms.
-int64_t early_zeroed_words(const SortWs& w) {
-  return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.scan_state) -
-                              reinterpret_cast<uint8_t*>(w.zeroed)) / 8;
+// Words cleared before linearize: the failure and segment words, the
+// histograms, and the digit counts of `seg_features` features.
+int64_t early_zeroed_words(const SortWs& w, int32_t seg_features) {
+  return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.fhist) -
+                              reinterpret_cast<uint8_t*>(w.zeroed)) / 8 +
+         static_cast<int64_t>(seg_features) * kSegRow / 2;
 }
 
 // Words linearize clears for a sort of `passes` passes: the scan state, the
@@ -627,14 +754,17 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
                   const int32_t* b_t_map, int32_t bits, int32_t nb, const void* indices,
                   const void* offsets, int32_t index_bytes, int64_t N, const float* iw,
                   const TransposeOut& o, SortWs& w, hipStream_t s) {
-  (void)T;
   // With per-sample weights the weights travel with the keys as a second payload.
   uint32_t* const v2[2] = {iw ? w.vals2[0] : nullptr, iw ? w.vals2[1] : nullptr};
   uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
   const int passes = (bits + kRadixBits - 1) / kRadixBits;
-  {  // the failure word and the histograms start at zero
-    const int64_t words = early_zeroed_words(w);
+  // Segments (one per feature) for a fixed batch of at most kSegMaxT features.
+  SegSort seg{};
+  if (b_t_map == nullptr && T >= 1 && T <= kSegMaxT && passes > 0)
+    seg = SegSort{w.fpos, w.tprefix, w.fhist, w.seg_bad, T};
+  {  // the failure and segment words, the histograms and digit counts start at zero
+    const int64_t words = early_zeroed_words(w, seg.T);
     const int64_t blocks = ceil_div(words, 256);
     zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 2048 ? blocks : 2048)), 256, 0, s>>>(
         w.zeroed, words);
@@ -647,15 +777,15 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
         nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
-        w.scan_state, late_words);
+        w.scan_state, late_words, seg);
   else
     linearize_kernel<int32_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
         nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
-        w.scan_state, late_words);
+        w.scan_state, late_words, seg);
   MX_LAUNCH_CHECK();
 
-  const int64_t ntiles = sweep_tiles(N);
+  const int64_t ntiles = sweep_tiles(N) + seg.T;  // segments start at tile boundaries
   if (ntiles > 0xffffffffll) return set_error(MX_EINVAL, "too many sort tiles");
   const dim3 gsweep(static_cast<uint32_t>(ntiles));
   int cur = 0;
@@ -668,8 +798,10 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     const int shift = p * kRadixBits;
     const int nbits = bits - shift < kRadixBits ? bits - shift : kRadixBits;
     unsigned long long* st = w.sweep + p * w.sweep_words;
-    unsigned int* ticket = reinterpret_cast<unsigned int*>(st + ntiles * kRadix);
+    unsigned int* ticket = reinterpret_cast<unsigned int*>(st + sweep_status_tiles(N) * kRadix);
     const uint32_t* gh = w.ghist + p * kRadix;
+    SegSort segp = seg;  // this pass's row of the per-feature digit counts
+    if (seg.T > 0) segp.fhist = seg.fhist + p * kRadix;
     const Faults f = call_faults(w);
     const bool last = p == passes - 1;
     // Every count fits a 32-bit word's 30 bits.
@@ -679,7 +811,7 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     launch(gsweep, s, w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f,
            last ? nullptr : w.keys[cur ^ 1], last ? o.sorted : nullptr,
            last ? reinterpret_cast<uint32_t*>(o.infos) : w.vals[cur ^ 1],
-           last ? v2_final : v2[cur ^ 1]);
+           last ? v2_final : v2[cur ^ 1], segp);
     MX_LAUNCH_CHECK();
     cur ^= 1;
   }
