@@ -29,7 +29,9 @@ launches of one batch ("warm") and the rotation ("steps") are reported as
 effective rates: caches serve part of them, so they are no HBM bandwidth.  The CPU
 baseline is FBGEMM's CPU kernel (or the C restatement) on this host's cores.
 The default run also carries a `config4` record (nbit INT8/INT4 lookup) with
-its own roofline and CPU baseline.
+its own roofline and CPU baseline, and `config1`, `config3` and `config5`
+records (jagged round trip, backward + rowwise Adagrad, mixed nbit lookup),
+each measured the same way in the same process.
 
 --regime runs one regime only (for profiling: every launch of the kernel in
 the process then belongs to it): `steps` the rotation, `warm` batch 0
@@ -83,7 +85,8 @@ def parse_args():
                     help="launches timed back to back after each flush, each over its own "
                          "copy of the inputs")
     ap.add_argument("--no-config4", action="store_true",
-                    help="config 2 only: leave out the config-4 record")
+                    help="config 2 only: leave out the config-4, -1, -3 and -5 records "
+                         "(only the --config line)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (PMC byte-counter calibration)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -757,6 +760,12 @@ def main():
         line["config4"] = {k: c4[k] for k in ("metric", "value", "unit", "ms_per_step", "dtype",
                                               "config", "roofline", "effective", "compulsory",
                                               "line_fill", "cpu_baseline")}
+        # The other configurations' records, so that one run observes every target.
+        for c in (1, 3, 5):
+            rc = measure(args, c, dev)
+            line[f"config{c}"] = {k: rc[k] for k in ("metric", "value", "unit", "ms_per_step",
+                                                     "dtype", "config", "roofline", "effective",
+                                                     "cpu_baseline") if k in rc}
     print(json.dumps(line), flush=True)
 
 
