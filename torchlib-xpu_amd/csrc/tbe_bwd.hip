@@ -639,7 +639,8 @@ int64_t sweep_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kSweepTile); }
 // Tiles of a pass, with room for segments: each of up to kSegMaxT segments
 // starts at a tile boundary, so they need at most kSegMaxT more tiles.
 int64_t sweep_status_tiles(int64_t n) { return sweep_tiles(n) + kSegMaxT; }
-// Per pass: [tiles][kRadix] status words, then one word holding the ticket pair.
+// Room per pass, in 8-byte words: the most status words a call can use (8-byte
+// words, every segment tile), then 32 words holding the ticket.
 int64_t sweep_pass_words(int64_t n) { return sweep_status_tiles(n) * kRadix + 32; }
 constexpr size_t kSegHistBytes = static_cast<size_t>(kSegMaxT) * kSegRow * 4;
 
@@ -716,13 +717,20 @@ int64_t early_zeroed_words(const SortWs& w, int32_t seg_features) {
          static_cast<int64_t>(seg_features) * kSegRow / 2;
 }
 
-// Words linearize clears for a sort of `passes` passes: the scan state, the
-// chunk marks and the sweep state of those passes (unused passes' state is
-// left alone).
-int64_t late_zeroed_words(const SortWs& w, int passes) {
+// A call's sweep state per pass, in 8-byte words: `tiles` x kRadix status
+// words of `word_bytes` each, then 32 words holding the ticket (a multiple of
+// 256 bytes; at most the workspace's sweep_words).
+int64_t call_pass_words(int64_t tiles, int word_bytes) {
+  return align256(static_cast<size_t>(tiles) * kRadix * word_bytes) / 8 + 32;
+}
+
+// Words linearize clears for a sort of `passes` passes of `pass_words` each:
+// the scan state, the chunk marks and the sweep state of those passes (the
+// rest of the workspace's sweep state is left alone).
+int64_t late_zeroed_words(const SortWs& w, int passes, int64_t pass_words) {
   return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.sweep) -
                               reinterpret_cast<uint8_t*>(w.scan_state)) / 8 +
-         passes * w.sweep_words;
+         passes * pass_words;
 }
 
 // Where the call's look-backs report a give-up.
@@ -770,8 +778,13 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
         w.zeroed, words);
     MX_LAUNCH_CHECK();
   }
+  const int64_t ntiles = sweep_tiles(N) + seg.T;  // segments start at tile boundaries
+  if (ntiles > 0xffffffffll) return set_error(MX_EINVAL, "too many sort tiles");
+  // Every count fits a 32-bit word's 30 bits.
+  const bool w32 = N < (int64_t(1) << 30) && !force_wide_sort_words();
+  const int64_t pass_words = call_pass_words(ntiles, w32 ? 4 : 8);
   // Linearize also clears the look-back state of the later kernels.
-  const int64_t late_words = late_zeroed_words(w, passes);
+  const int64_t late_words = late_zeroed_words(w, passes, pass_words);
   const dim3 glin(static_cast<uint32_t>(ceil_div(N, kLinTile)));
   if (index_bytes == 8)
     linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
@@ -785,8 +798,6 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
         w.scan_state, late_words, seg);
   MX_LAUNCH_CHECK();
 
-  const int64_t ntiles = sweep_tiles(N) + seg.T;  // segments start at tile boundaries
-  if (ntiles > 0xffffffffll) return set_error(MX_EINVAL, "too many sort tiles");
   const dim3 gsweep(static_cast<uint32_t>(ntiles));
   int cur = 0;
   if (passes == 0) {
@@ -797,15 +808,13 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
   for (int p = 0; p < passes; ++p) {
     const int shift = p * kRadixBits;
     const int nbits = bits - shift < kRadixBits ? bits - shift : kRadixBits;
-    unsigned long long* st = w.sweep + p * w.sweep_words;
-    unsigned int* ticket = reinterpret_cast<unsigned int*>(st + sweep_status_tiles(N) * kRadix);
+    unsigned long long* st = w.sweep + p * pass_words;
+    unsigned int* ticket = reinterpret_cast<unsigned int*>(st + pass_words - 32);
     const uint32_t* gh = w.ghist + p * kRadix;
     SegSort segp = seg;  // this pass's row of the per-feature digit counts
     if (seg.T > 0) segp.fhist = seg.fhist + p * kRadix;
     const Faults f = call_faults(w);
     const bool last = p == passes - 1;
-    // Every count fits a 32-bit word's 30 bits.
-    const bool w32 = N < (int64_t(1) << 30) && !force_wide_sort_words();
     const auto launch = last ? (w32 ? &sweep<true, uint32_t> : &sweep<true, unsigned long long>)
                              : (w32 ? &sweep<false, uint32_t> : &sweep<false, unsigned long long>);
     launch(gsweep, s, w.keys[cur], w.vals[cur], v2[cur], N, shift, nbits, gh, st, ticket, f,
