@@ -254,14 +254,17 @@ def _shared_tables(rng, ftm, rows, dims, B, max_L, dup=False):
 @pytest.mark.parametrize("pooling", [0, 1])
 @pytest.mark.parametrize("weighted", [False, True])
 @pytest.mark.parametrize("dup", [False, True])
-def test_backward_shared_tables(dev, pooling, weighted, dup):
-    """Features sharing tables (feature_table_map [0, 1, 0, 2, 1]): one run per
-    row of a shared table, each occurrence summing its own feature's gradient
-    columns (MEAN: its own bag length); duplicate-heavy batches reach the
-    chunked long-run path.  Transpose bit-exact, update within rtol 1e-5."""
-    print(f"[case] shared tables pool={pooling} weighted={weighted} dup={dup}", flush=True)
-    rng = np.random.default_rng(50 + pooling + 2 * weighted + 4 * dup)
-    ftm, rows, dims = [0, 1, 0, 2, 1], [300, 200, 50], [64, 32, 128]
+@pytest.mark.parametrize("ftm", [[0, 1, 0, 2, 1], [0, 0, 1, 1, 2]])
+def test_backward_shared_tables(dev, pooling, weighted, dup, ftm):
+    """Features sharing tables (fbgemm's feature_table_map; hash_size_cumsum
+    then repeats or decreases, so the sort runs over the whole batch): one run
+    per row of a shared table, each occurrence summing its own feature's
+    gradient columns (MEAN: its own bag length); duplicate-heavy batches reach
+    the chunked long-run path.  Transpose bit-exact, update within rtol 1e-5."""
+    print(f"[case] shared tables ftm={ftm} pool={pooling} weighted={weighted} dup={dup}",
+          flush=True)
+    rng = np.random.default_rng(50 + pooling + 2 * weighted + 4 * dup + 8 * ftm[1])
+    rows, dims = [300, 200, 50], [64, 32, 128]
     inp, w_off, hsc, m1_off, bits = _shared_tables(rng, ftm, rows, dims, 120, 30, dup)
     nb = orc.info_B_num_bits(inp.T, inp.B)
     exp = orc.transpose_embedding_input(hsc, inp.B, nb, bits, inp.indices, inp.offsets)

@@ -35,6 +35,8 @@
 //    deterministic.  Runs and chunks are split into one contiguous key range
 //    per XCD, so an XCD re-reads only its tables' gradient columns, from its
 //    own L2.
+#include <type_traits>
+
 #include "mx_common.h"
 #include "scan.h"
 
@@ -88,18 +90,23 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
 // ---- segments -------------------------------------------------------------
 
 // The sort's segments, one per feature of a fixed batch with at most kSegMaxT
-// features.  When every key of feature t lies in [hsc[t], hsc[t+1]) and hsc
-// does not decrease, all keys of feature t precede those of feature t + 1:
+// features.  When hsc increases strictly and every key of feature t lies in
+// [hsc[t], hsc[t+1]), all keys of feature t precede those of feature t + 1:
 // sorting each feature's positions on its own gives the global order, each
 // segment's tiles (segments start at tile boundaries) look back only over
 // tiles of their own segment, and the chains are T times shorter.  Linearize
-// writes fpos and tprefix, counts each feature's digits, and sets `bad` if a
-// key lies outside its feature's range (then the passes sort globally).
+// checks hsc in every block: when it does not increase strictly (features
+// that share a table), it counts the whole batch's digits and sets `bad` to
+// kSegTables.  Otherwise it writes fpos and tprefix, counts each feature's
+// digits, and sets `bad` to kSegKeys if a key lies outside its feature's
+// range; the passes then sort globally, summing the per-feature counts.
+constexpr unsigned int kSegKeys = 1u;    // a key outside its feature's range
+constexpr unsigned int kSegTables = 2u;  // hsc does not increase strictly
 struct SegSort {
   int64_t* fpos;         // [T + 1] first position of each feature's positions
   int32_t* tprefix;      // [T + 1] first tile of each feature's segment
   uint32_t* fhist;       // [T][kHistCopies][kMaxPasses][kRadix] digit counts (zeroed), a pass's row
-  unsigned int* bad;     // zeroed; nonzero: sort globally
+  unsigned int* bad;     // zeroed; nonzero (kSegKeys or kSegTables): sort globally
   int32_t T;             // 0: no segments
 };
 
@@ -122,7 +129,8 @@ __global__ void __launch_bounds__(256)
   __shared__ uint32_t s_mark[kLinTile];  // bag (relative to blo) starting at each position
   __shared__ uint32_t hf[2][kMaxPasses][kRadix];  // digit counts of the block's first two features
   __shared__ int s_bad;
-  __shared__ int64_t s_rows[2];
+  __shared__ int s_tables_ok;  // hsc increases strictly (per-feature counts)
+  __shared__ int64_t s_hsc[kSegMaxT + 1];  // hsc of a batch of at most kSegMaxT features
   __shared__ int64_t s_range[2][2];      // [half][lo, hi] of the cooperative searches
   __shared__ uint32_t s_cnt[2][2];       // [half][wave of the half]
   __shared__ uint32_t s_wmax[4];
@@ -141,6 +149,9 @@ __global__ void __launch_bounds__(256)
     const int64_t l = pbase + it * 64;
     idx[it] = l < lend ? indices[l] : I(0);
   }
+  // Wave 0 loads hsc (at most kSegMaxT + 1 entries) now and stages it in LDS
+  // after the searches, when it has arrived.
+  const int64_t lane_hsc = seg.T > 0 && w == 0 && lane <= seg.T ? hsc[lane] : 0;
   // Last bag with offsets[bag] <= target (0 when none), for the block's first
   // (half 0) and last (half 1) position: 128-ary searches, one probe per
   // thread and round, so ceil(log128(nbags)) dependent loads instead of
@@ -178,20 +189,20 @@ __global__ void __launch_bounds__(256)
     }
   }
   const int64_t blo = s_range[0][0], bhi = s_range[1][0];
+  if (seg.T > 0 && w == 0) {  // hsc into LDS; does it increase strictly over the T features?
+    const int64_t next = __shfl(lane_hsc, lane + 1 < 64 ? lane + 1 : 63, 64);
+    if (lane <= seg.T) s_hsc[lane] = lane_hsc;
+    const bool all_up = __all(lane >= seg.T || lane_hsc < next);
+    if (lane == 0) s_tables_ok = all_up ? 1 : 0;
+  }
   // Digit counts: of the whole batch (no segments), or per feature, which
   // also give the whole batch's when the passes sort globally.
-  if (seg.T > 0)
-    for (int i = threadIdx.x; i < 2 * kMaxPasses * kRadix; i += 256) (&hf[0][0][0])[i] = 0u;
-  else
-    for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
+  // Both count arrays start at zero (which one is used is known after the
+  // next barrier, which also publishes s_hsc and s_tables_ok).
+  for (int i = threadIdx.x; i < 2 * kMaxPasses * kRadix; i += 256) (&hf[0][0][0])[i] = 0u;
+  for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
   const int64_t t_lo = seg.T > 0 ? blo / B : 0;  // the block's first feature
-  if (threadIdx.x == 0) {
-    s_bad = 0;
-    if (seg.T > 0) {  // row counts of the block's first two features
-      s_rows[0] = hsc[t_lo + 1] - hsc[t_lo];
-      s_rows[1] = t_lo + 1 < seg.T ? hsc[t_lo + 2] - hsc[t_lo + 1] : 0;
-    }
-  }
+  if (threadIdx.x == 0) s_bad = 0;
   // Bag of every position without a search when the block spans few bags:
   // each non-empty bag marks its first position, and position l's bag is the
   // largest mark at or before l (an inclusive max-scan; bag ids grow with
@@ -246,88 +257,99 @@ __global__ void __launch_bounds__(256)
     }
     __syncthreads();  // h cleared
   }
+  // Positions' keys and digit counts, compiled apart for per-feature counts
+  // (PF) and the whole batch's, so that each keeps straight-line code.
+  const bool pf = seg.T > 0 && s_tables_ok != 0;  // block-uniform
+  auto tail = [&](auto pf_c) {
+    constexpr bool PF = decltype(pf_c)::value;
 #pragma unroll
-  for (int it = 0; it < kLinItems; ++it) {
-    const int64_t l = pbase + it * 64;
-    if (l >= lend) continue;
-    const int64_t bag = blo + rel[it];
-    // Info word (t << nb) | b: computed for a fixed batch, given per bag (VBE).
-    uint32_t info;
-    int64_t t;
-    if (b_t_map) {
-      info = static_cast<uint32_t>(b_t_map[bag]);
-      t = nb >= 32 ? 0 : static_cast<int64_t>(info >> nb);
-    } else {
-      t = bag / B;
-      const int64_t b = bag - t * B;
-      info = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
-    }
-    const int64_t key = hsc[t] + static_cast<int64_t>(idx[it]);
-    if (linear_out) linear_out[l] = key;
-    const uint32_t k32 = static_cast<uint32_t>(key);
-    keys[l] = k32;
-    vals[l] = info;
-    if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
-    if (seg.T == 0) {
-      for (int p = 0; p < passes; ++p)
-        atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
-    } else {
-      const int64_t i64 = static_cast<int64_t>(idx[it]);
-      const int64_t tf = t - t_lo;
-      const int64_t rows_t = tf == 0 ? s_rows[0] : (tf == 1 ? s_rows[1] : hsc[t + 1] - hsc[t]);
-      if (i64 < 0 || i64 >= rows_t) s_bad = 1;  // outside its feature's range
-      for (int p = 0; p < passes; ++p) {
-        const uint32_t d = (k32 >> (p * kRadixBits)) & digit_mask(bits, p);
-        if (tf == 0 || tf == 1)
-          atomicAdd(&hf[tf][p][d], 1u);
-        else  // a block over three or more features (short features): straight to memory
-          atomicAdd(&seg.fhist[t * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords +
-                               p * kRadix + d], 1u);
+    for (int it = 0; it < kLinItems; ++it) {
+      const int64_t l = pbase + it * 64;
+      if (l >= lend) continue;
+      const int64_t bag = blo + rel[it];
+      // Info word (t << nb) | b: computed for a fixed batch, given per bag (VBE).
+      uint32_t info;
+      int64_t t;
+      if (b_t_map) {
+        info = static_cast<uint32_t>(b_t_map[bag]);
+        t = nb >= 32 ? 0 : static_cast<int64_t>(info >> nb);
+      } else {
+        t = bag / B;
+        const int64_t b = bag - t * B;
+        info = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
+      }
+      const int64_t key = (seg.T > 0 ? s_hsc[t] : hsc[t]) + static_cast<int64_t>(idx[it]);
+      if (linear_out) linear_out[l] = key;
+      const uint32_t k32 = static_cast<uint32_t>(key);
+      keys[l] = k32;
+      vals[l] = info;
+      if (iw) vals2[l] = __float_as_uint(iw[l]);  // per-sample weight rides along the sort
+      if constexpr (!PF) {
+        for (int p = 0; p < passes; ++p)
+          atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
+      } else {
+        const int64_t i64 = static_cast<int64_t>(idx[it]);
+        const int64_t tf = t - t_lo;
+        const int64_t rows_t = s_hsc[t + 1] - s_hsc[t];
+        if (i64 < 0 || i64 >= rows_t) s_bad = 1;  // outside its feature's range
+        for (int p = 0; p < passes; ++p) {
+          const uint32_t d = (k32 >> (p * kRadixBits)) & digit_mask(bits, p);
+          if (tf == 0 || tf == 1)
+            atomicAdd(&hf[tf][p][d], 1u);
+          else  // a block over three or more features (short features): straight to memory
+            atomicAdd(&seg.fhist[t * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords +
+                                 p * kRadix + d], 1u);
+        }
       }
     }
-  }
-  __syncthreads();
-  if (seg.T > 0) {
-    if (threadIdx.x == 0 && s_bad) *seg.bad = 1u;
-    const int nbins = passes * kRadix;
-    const int rot = static_cast<int>(blockIdx.x * 97u % static_cast<uint32_t>(nbins));
-    for (int f = 0; f < 2 && t_lo + f < seg.T; ++f)
-      for (int jj = threadIdx.x; jj < nbins; jj += 256) {
-        const int j = jj + rot < nbins ? jj + rot : jj + rot - nbins;
-        const uint32_t c = (&hf[f][0][0])[j];
-        if (c)
-          atomicAdd(&seg.fhist[(t_lo + f) * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords + j],
-                    c);
+    __syncthreads();
+    if constexpr (PF) {
+      if (threadIdx.x == 0 && s_bad) *seg.bad = kSegKeys;
+      const int nbins = passes * kRadix;
+      const int rot = static_cast<int>(blockIdx.x * 97u % static_cast<uint32_t>(nbins));
+      for (int f = 0; f < 2 && t_lo + f < seg.T; ++f)
+        for (int jj = threadIdx.x; jj < nbins; jj += 256) {
+          const int j = jj + rot < nbins ? jj + rot : jj + rot - nbins;
+          const uint32_t c = (&hf[f][0][0])[j];
+          if (c)
+            atomicAdd(&seg.fhist[(t_lo + f) * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords + j],
+                      c);
+        }
+      if (blockIdx.x == 0 && w == 0) {
+        // Lane f <= T: feature f's first position; its segment's tile count; the
+        // features' first tiles by a wave scan.  The positions must not decrease
+        // for the segments to be in key order (hsc increases: checked above).
+        const int T = seg.T;
+        const int64_t fp = lane <= T ? static_cast<int64_t>(offsets[static_cast<int64_t>(lane) * B]) : 0;
+        const int64_t fnext = __shfl(fp, lane + 1 < 64 ? lane + 1 : 63, 64);
+        const uint32_t nt = lane < T ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
+        const uint32_t incl = wave_incl_scan<SumOp>(nt);
+        // The segments must also cover exactly the positions [0, N).
+        bool bad = (lane < T && fnext < fp) || (lane == 0 && fp != 0) || (lane == T && fp != N);
+        if (lane <= T) seg.fpos[lane] = fp;
+        if (lane < T) seg.tprefix[lane + 1] = static_cast<int32_t>(incl);
+        if (lane == 0) seg.tprefix[0] = 0;
+        if (__any(bad) && lane == 0) *seg.bad = kSegKeys;
       }
-    if (seg.T > 0 && blockIdx.x == 0 && w == 0) {
-      // Lane f <= T: feature f's first position; its segment's tile count; the
-      // features' first tiles by a wave scan.  hsc and the positions must not
-      // decrease for the segments to be in key order.
-      const int T = seg.T;
-      const int64_t fp = lane <= T ? static_cast<int64_t>(offsets[static_cast<int64_t>(lane) * B]) : 0;
-      const int64_t fnext = __shfl(fp, lane + 1 < 64 ? lane + 1 : 63, 64);
-      const uint32_t nt = lane < T ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
-      const uint32_t incl = wave_incl_scan<SumOp>(nt);
-      // The segments must also cover exactly the positions [0, N).
-      bool bad = (lane < T && (fnext < fp || hsc[lane + 1] < hsc[lane])) ||
-                 (lane == 0 && fp != 0) || (lane == T && fp != N);
-      if (lane <= T) seg.fpos[lane] = fp;
-      if (lane < T) seg.tprefix[lane + 1] = static_cast<int32_t>(incl);
-      if (lane == 0) seg.tprefix[0] = 0;
-      if (__any(bad) && lane == 0) *seg.bad = 1u;
+    } else {
+      // Into this XCD's copy, each block starting at another bin so that blocks
+      // finishing together do not queue on the same counters.
+      uint32_t* gcopy = ghist + (blockIdx.x % kHistCopies) * kHistCopyWords;
+      const int nbins = passes * kRadix;
+      const int rot = static_cast<int>((blockIdx.x / kHistCopies) * 97u % static_cast<uint32_t>(nbins));
+      for (int j = threadIdx.x; j < nbins; j += 256) {
+        const int i = j + rot < nbins ? j + rot : j + rot - nbins;
+        const uint32_t c = (&h[0][0])[i];
+        if (c) atomicAdd(&gcopy[i], c);
+      }
+      // Features that share a table: no segments, the passes read these counts.
+      if (seg.T > 0 && blockIdx.x == 0 && threadIdx.x == 0) *seg.bad = kSegTables;
     }
-    return;
-  }
-  // Into this XCD's copy, each block starting at another bin so that blocks
-  // finishing together do not queue on the same counters.
-  uint32_t* gcopy = ghist + (blockIdx.x % kHistCopies) * kHistCopyWords;
-  const int nbins = passes * kRadix;
-  const int rot = static_cast<int>((blockIdx.x / kHistCopies) * 97u % static_cast<uint32_t>(nbins));
-  for (int j = threadIdx.x; j < nbins; j += 256) {
-    const int i = j + rot < nbins ? j + rot : j + rot - nbins;
-    const uint32_t c = (&h[0][0])[i];
-    if (c) atomicAdd(&gcopy[i], c);
-  }
+  };
+  if (pf)
+    tail(std::true_type{});
+  else
+    tail(std::false_type{});
 }
 
 // ---- radix sort: one launch per pass --------------------------------------
@@ -346,21 +368,24 @@ struct SweepWord {
 
 // status: [tiles][kRadix] zeroed words; ticket: zeroed next-tile counter.
 // ghist: this pass's digit counts, kHistCopies copies kHistCopyWords apart.
-template <bool LAST, typename SW>
-__global__ void __launch_bounds__(kSweepThreads)
-    onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
-                    const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
-                    const uint32_t* __restrict__ ghist, SW* status,
-                    unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
-                    int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
-                    uint32_t* __restrict__ vals2_out, SegSort seg) {
-  __shared__ unsigned int s_tile;
-  __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
-  __shared__ uint32_t s_base[kRadix];
-  __shared__ uint32_t s_wsum[kRadix / 64];
+// One tile of a pass, compiled apart for per-feature segments (kTileSeg), one
+// global sort over the whole batch's digit counts (kTileGlobal) and one over
+// the sum of the per-feature counts (kTileKeys), so that the global path keeps
+// the code of a sort without segments (one body with both paths scheduled it
+// ~2 us per call slower).
+constexpr int kTileSeg = 0, kTileGlobal = 1, kTileKeys = 2;
+template <int MODE, bool LAST, typename SW>
+__device__ __forceinline__ void sweep_tile(
+    const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+    const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
+    const uint32_t* __restrict__ ghist, SW* status, unsigned int* ticket, const Faults& faults,
+    uint32_t* __restrict__ keys_out, int64_t* __restrict__ keys_out64,
+    uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, const SegSort& seg,
+    int64_t lane_fpos, int32_t lane_tp, unsigned int& s_tile,
+    uint32_t (&cnt)[kSweepWaves][kRadix], uint32_t (&s_base)[kRadix],
+    uint32_t (&s_wsum)[kRadix / 64]) {
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (call_failed(faults.fail)) return;  // an earlier pass gave up: nothing valid to sort
   if (threadIdx.x == 0) s_tile = atomicAdd(ticket, 1u);
   for (int i = threadIdx.x; i < kSweepWaves * kRadix; i += kSweepThreads) (&cnt[0][0])[i] = 0u;
   __syncthreads();
@@ -368,17 +393,18 @@ __global__ void __launch_bounds__(kSweepThreads)
   // The tile's positions [pbeg, pend) and the first tile of its look-back
   // chain: its feature's first tile (segments), or tile 0.  Tiles past the
   // last real tile return (nobody waits on them: their tickets are last).
-  const bool segm = seg.T > 0 && __hip_atomic_load(seg.bad, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT) == 0u;
-  int64_t pbeg, pend, tile0 = 0, f = 0;
-  if (segm) {
-    const bool mine = lane < seg.T && seg.tprefix[lane] <= tile && tile < seg.tprefix[lane + 1];
+  int64_t pbeg, pend, tile0 = 0, f = 0, fpos_f = 0;
+  if constexpr (MODE == kTileSeg) {
+    const int32_t tp_next = __shfl(lane_tp, lane + 1 < 64 ? lane + 1 : 63, 64);
+    const bool mine = lane < seg.T && lane_tp <= tile && tile < tp_next;
     const uint64_t m = __ballot(mine);  // one feature at most (wave-uniform)
     if (m == 0ull) return;              // block-uniform: past every segment
     f = __ffsll(static_cast<long long>(m)) - 1;
-    tile0 = seg.tprefix[f];
-    const int64_t fe = seg.fpos[f + 1] < n ? seg.fpos[f + 1] : n;  // fpos[T] == n (checked)
-    pbeg = seg.fpos[f] + (tile - tile0) * kSweepTile;
+    tile0 = __shfl(lane_tp, static_cast<int>(f), 64);
+    fpos_f = __shfl(lane_fpos, static_cast<int>(f), 64);
+    const int64_t fnext = __shfl(lane_fpos, static_cast<int>(f) + 1, 64);
+    const int64_t fe = fnext < n ? fnext : n;  // fpos[T] == n (checked)
+    pbeg = fpos_f + (tile - tile0) * kSweepTile;
     pend = pbeg + kSweepTile < fe ? pbeg + kSweepTile : fe;
   } else {
     pbeg = tile * kSweepTile;
@@ -428,15 +454,22 @@ __global__ void __launch_bounds__(kSweepThreads)
       total += c;
     }
     uint32_t gcount = 0u;
-    if (used && segm) {
+    if constexpr (MODE == kTileSeg) {
+      if (used)
 #pragma unroll
-      for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[f * kSegRow + x * kHistCopyWords + d];
-    } else if (used && seg.T > 0) {  // sorting globally after linearize counted per feature
-      for (int t = 0; t < seg.T; ++t)
-        for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[t * kSegRow + x * kHistCopyWords + d];
-    } else if (used) {
+        for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[f * kSegRow + x * kHistCopyWords + d];
+    } else if constexpr (MODE == kTileKeys) {
+      // A key outside its feature's range (invalid input): linearize counted per
+      // feature, the pass sorts globally over their sum.
+      if (used)
+#pragma unroll 4
+        for (int t = 0; t < seg.T; ++t)
 #pragma unroll
-      for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
+          for (int x = 0; x < kHistCopies; ++x) gcount += seg.fhist[t * kSegRow + x * kHistCopyWords + d];
+    } else {
+      if (used)
+#pragma unroll
+        for (int x = 0; x < kHistCopies; ++x) gcount += ghist[x * kHistCopyWords + d];
     }
     incl = wave_incl_scan<SumOp>(gcount);
     if (lane == 63) s_wsum[w] = incl;
@@ -450,7 +483,7 @@ __global__ void __launch_bounds__(kSweepThreads)
       if (i < w) goff += s_wsum[i];
     const uint32_t prev = __shfl_up(incl, 1, 64);
     if (lane != 0) goff += prev;
-    if (segm) goff += static_cast<uint32_t>(seg.fpos[f]);  // the segment's first position
+    if constexpr (MODE == kTileSeg) goff += static_cast<uint32_t>(fpos_f);  // the segment's first position
     uint32_t prefix = 0u;
     if (used) {
       using Word = SweepWord<SW>;
@@ -517,6 +550,46 @@ __global__ void __launch_bounds__(kSweepThreads)
     vals_out[pos] = v[it];
     if (vals2) vals2_out[pos] = v2[it];
   }
+}
+
+template <bool LAST, typename SW>
+__global__ void __launch_bounds__(kSweepThreads)
+    onesweep_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
+                    const uint32_t* __restrict__ vals2, int64_t n, int shift, int nbits,
+                    const uint32_t* __restrict__ ghist, SW* status,
+                    unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
+                    int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
+                    uint32_t* __restrict__ vals2_out, SegSort seg) {
+  __shared__ unsigned int s_tile;
+  __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
+  __shared__ uint32_t s_base[kRadix];
+  __shared__ uint32_t s_wsum[kRadix / 64];
+  const int lane = threadIdx.x & 63;
+  // The segment state loads while the tile takes its ticket (neither depends
+  // on the other): why the passes sort globally (0: they do not), and lane
+  // f <= T's feature first position and first tile.
+  const unsigned int why = seg.T > 0 ? __hip_atomic_load(seg.bad, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)
+                                     : kSegTables;
+  int64_t lane_fpos = 0;
+  int32_t lane_tp = 0;
+  if (seg.T > 0 && lane <= seg.T) {
+    lane_fpos = seg.fpos[lane];
+    lane_tp = seg.tprefix[lane];
+  }
+  if (call_failed(faults.fail)) return;  // an earlier pass gave up: nothing valid to sort
+  if (why == 0u)  // grid-uniform
+    sweep_tile<kTileSeg, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
+                                   faults, keys_out, keys_out64, vals_out, vals2_out, seg,
+                                   lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
+  else if (why == kSegKeys)
+    sweep_tile<kTileKeys, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
+                                    faults, keys_out, keys_out64, vals_out, vals2_out, seg,
+                                    lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
+  else
+    sweep_tile<kTileGlobal, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
+                                      faults, keys_out, keys_out64, vals_out, vals2_out, seg,
+                                      lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
 }
 
 // One sort pass over a workspace whose status words are of type SW.
