@@ -69,6 +69,30 @@ def test_transpose_keys_outside_their_table_sort_globally(dev):
     _check_transpose(dev, inp, torch.int32)
 
 
+def test_transpose_too_few_key_bits(dev):
+    """With total_hash_size_bits below the keys' width the sort orders keys by
+    their low bits (as a radix sort over those bits does, across features):
+    per-feature segments would not, so the sort runs over the whole batch and
+    matches the oracle's masked stable sort."""
+    print("[case] transpose, 11 key bits for 3,000 rows", flush=True)
+    rng = np.random.default_rng(11)
+    inp = random_tbe(rng, 3, 300, [4] * 3, [1000, 1000, 1000], 20)
+    bits = 11  # 2^11 = 2048 < 3000 rows
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    exp = orc.transpose_embedding_input(inp.hash_size_cumsum, inp.B, nb, bits, inp.indices,
+                                        inp.offsets)
+    for idt in (torch.int64, torch.int32):
+        got = torch.ops.fbgemm.transpose_embedding_input(
+            torch.from_numpy(inp.hash_size_cumsum).to(dev), bits,
+            torch.from_numpy(inp.indices).to(dev, idt), torch.from_numpy(inp.offsets).to(dev, idt),
+            False, None, nb)
+        r = int(got[5].item())
+        assert r == exp["num_runs"]
+        np.testing.assert_array_equal(got[1].cpu().numpy(), exp["sorted_linear_indices"])
+        np.testing.assert_array_equal(got[2].cpu().numpy(), exp["infos_sorted"])
+        np.testing.assert_array_equal(got[6].cpu().numpy()[: r + 1], exp["cumulative_run_lengths"])
+
+
 @pytest.mark.parametrize("T", [63, 64])
 def test_transpose_feature_segments(dev, T):
     """Up to 63 features sort as per-feature segments, 64 as one batch.  The

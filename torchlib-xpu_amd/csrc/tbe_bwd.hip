@@ -90,8 +90,9 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
 // ---- segments -------------------------------------------------------------
 
 // The sort's segments, one per feature of a fixed batch with at most kSegMaxT
-// features.  When hsc increases strictly and every key of feature t lies in
-// [hsc[t], hsc[t+1]), all keys of feature t precede those of feature t + 1:
+// features.  When hsc increases strictly, hsc[T] <= 2^bits and every key of
+// feature t lies in [hsc[t], hsc[t+1]), all keys of feature t precede those of
+// feature t + 1:
 // sorting each feature's positions on its own gives the global order, each
 // segment's tiles (segments start at tile boundaries) look back only over
 // tiles of their own segment, and the chains are T times shorter.  Linearize
@@ -192,7 +193,10 @@ __global__ void __launch_bounds__(256)
   if (seg.T > 0 && w == 0) {  // hsc into LDS; does it increase strictly over the T features?
     const int64_t next = __shfl(lane_hsc, lane + 1 < 64 ? lane + 1 : 63, 64);
     if (lane <= seg.T) s_hsc[lane] = lane_hsc;
-    const bool all_up = __all(lane >= seg.T || lane_hsc < next);
+    // In-range keys must also fit the sorted bits (a sort over fewer bits
+    // orders keys by their low bits, across features).
+    const bool fits = lane != seg.T || bits >= 62 || lane_hsc <= (int64_t(1) << bits);
+    const bool all_up = __all((lane >= seg.T || lane_hsc < next) && fits);
     if (lane == 0) s_tables_ok = all_up ? 1 : 0;
   }
   // Digit counts: of the whole batch (no segments), or per feature, which
