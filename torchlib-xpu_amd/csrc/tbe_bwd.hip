@@ -97,12 +97,12 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
 // segment's tiles (segments start at tile boundaries) look back only over
 // tiles of their own segment, and the chains are T times shorter.  Linearize
 // checks hsc in every block: when it does not increase strictly (features
-// that share a table), it counts the whole batch's digits and sets `bad` to
-// kSegTables.  Otherwise it writes fpos and tprefix, counts each feature's
+// that share a table) or hsc[T] > 2^bits, it counts the whole batch's digits
+// and sets `bad` to kSegTables.  Otherwise it writes fpos and tprefix, counts each feature's
 // digits, and sets `bad` to kSegKeys if a key lies outside its feature's
 // range; the passes then sort globally, summing the per-feature counts.
 constexpr unsigned int kSegKeys = 1u;    // a key outside its feature's range
-constexpr unsigned int kSegTables = 2u;  // hsc does not increase strictly
+constexpr unsigned int kSegTables = 2u;  // hsc does not increase strictly, or exceeds 2^bits
 struct SegSort {
   int64_t* fpos;         // [T + 1] first position of each feature's positions
   int32_t* tprefix;      // [T + 1] first tile of each feature's segment
@@ -199,10 +199,10 @@ __global__ void __launch_bounds__(256)
     const bool all_up = __all((lane >= seg.T || lane_hsc < next) && fits);
     if (lane == 0) s_tables_ok = all_up ? 1 : 0;
   }
-  // Digit counts: of the whole batch (no segments), or per feature, which
-  // also give the whole batch's when the passes sort globally.
-  // Both count arrays start at zero (which one is used is known after the
-  // next barrier, which also publishes s_hsc and s_tables_ok).
+  // Digit counts per feature when segments are possible (their sum gives the
+  // whole batch's if a key turns out to lie outside its feature), else the
+  // whole batch's.  Both count arrays start at zero: which one is used is
+  // known after the next barrier, which also publishes s_hsc and s_tables_ok.
   for (int i = threadIdx.x; i < 2 * kMaxPasses * kRadix; i += 256) (&hf[0][0][0])[i] = 0u;
   for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
   const int64_t t_lo = seg.T > 0 ? blo / B : 0;  // the block's first feature
@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(256)
       }
       rel[it] = static_cast<uint32_t>(lo - blo);
     }
-    __syncthreads();  // h cleared
+    __syncthreads();  // count arrays cleared
   }
   // Positions' keys and digit counts, compiled apart for per-feature counts
   // (PF) and the whole batch's, so that each keeps straight-line code.
@@ -733,7 +733,7 @@ struct SortWs {
   int64_t scan_slot_words;
   uint32_t* ghist;                 // [kHistCopies][kMaxPasses][kRadix]
   uint32_t* fhist;                 // [kSegMaxT][kHistCopies][kMaxPasses][kRadix] per-feature digit counts
-  unsigned int* seg_bad;           // nonzero: the passes sort globally
+  unsigned int* seg_bad;           // nonzero (kSegKeys, kSegTables): the passes sort globally
   int64_t* fpos;                   // [kSegMaxT + 1] (written by linearize)
   int32_t* tprefix;                // [kSegMaxT + 1] (written by linearize)
   uint32_t* chunk_mark;            // [max_chunks(N)] (backward only)
