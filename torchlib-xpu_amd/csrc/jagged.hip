@@ -234,7 +234,17 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int it = 0; it < kJagItems; ++it) {
       const int64_t i = base + it * 256 + threadIdx.x;
-      if (i < n_all) dst[i] = c[it];
+      if (i < n_all) {
+        // The dense output streams past the caches (config 1 cold round trip
+        // 12.4 -> 11.8 us; the same for dense_to_jagged's output gained nothing).
+        if constexpr (VEC == 16) {
+          typedef unsigned int u4nt __attribute__((ext_vector_type(4)));
+          __builtin_nontemporal_store(*reinterpret_cast<const u4nt*>(&c[it]),
+                                      reinterpret_cast<u4nt*>(&dst[i]));
+        } else {
+          dst[i] = c[it];
+        }
+      }
     }
   }
 }
