@@ -74,7 +74,11 @@ constexpr int kLinItems = 4;
 constexpr int kSegMaxT = 63;
 constexpr int64_t kSegRow = static_cast<int64_t>(kHistCopies) * kMaxPasses * kRadix;  // per feature
 constexpr int64_t kLinTile = 256 * kLinItems;         // positions per linearize block
-constexpr int kLong = 32;                             // runs longer than this are chunked
+// Runs longer than kLong are chunked.  A wave's four short runs last as long
+// as the longest (two occurrences per round): 24 instead of 32 moves the
+// 13-16-round runs to the chunk path (config 3: 161.1 -> 158.8 us; 12, 16 and
+// 20 were within 1 us of it, 8 slower).
+constexpr int kLong = 24;
 constexpr int kChunk = 32;                            // occurrences per chunk
 // One-pass scans per backward: run heads, chunk layout.
 constexpr int kScanSlots = 2;
@@ -1197,9 +1201,8 @@ __device__ __forceinline__ void adagrad_update(const BwdArgs& a, int32_t D, int 
 }
 
 // Pass B (long runs): a block owns the long runs whose first chunk lies in
-// its kLongRange-chunk range (found by one parallel read of the chunk marks; a long
-// run has at least two chunks, so at most two start in a range) and handles
-// them one after another.  Per run, the 256/G groups sum the run's chunk
+// its kLongRange-chunk range (found by one parallel read of the chunk marks; at
+// most kLongRange start in a range) and handles them one after another.  Per run, the 256/G groups sum the run's chunk
 // partials round-robin (group j takes chunks j, j + 256/G, ...), the group
 // vectors are combined in group order through LDS, and group 0 applies the
 // update.
