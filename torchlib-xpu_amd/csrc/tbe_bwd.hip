@@ -94,23 +94,25 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
 // ---- segments -------------------------------------------------------------
 
 // The sort's segments, one per feature of a fixed batch with at most kSegMaxT
-// features.  When hsc increases strictly, hsc[T] <= 2^bits and every key of
-// feature t lies in [hsc[t], hsc[t+1]), all keys of feature t precede those of
-// feature t + 1:
-// sorting each feature's positions on its own gives the global order, each
-// segment's tiles (segments start at tile boundaries) look back only over
-// tiles of their own segment, and the chains are T times shorter.  Linearize
-// checks hsc in every block: when it does not increase strictly (features
-// that share a table) or hsc[T] > 2^bits, it counts the whole batch's digits
-// and sets `bad` to kSegTables.  Otherwise it writes fpos and tprefix, counts each feature's
-// digits, and sets `bad` to kSegKeys if a key lies outside its feature's
-// range; the passes then sort globally, summing the per-feature counts.
-constexpr unsigned int kSegKeys = 1u;    // a key outside its feature's range
-constexpr unsigned int kSegTables = 2u;  // hsc does not increase strictly, or exceeds 2^bits
+// features, or per run of consecutive features with equal hsc (features that
+// share one table).  When hsc does not decrease, hsc[T] <= 2^bits and every
+// key of a segment lies in [its hsc, the next segment's hsc), all keys of a
+// segment precede those of the next: sorting each segment's positions on its
+// own gives the global order, each segment's tiles (segments start at tile
+// boundaries) look back only over tiles of their own segment, and the chains
+// are ~S times shorter.  Linearize checks hsc in every block: when it
+// decreases (features sharing tables out of order) or hsc[T] > 2^bits, it
+// counts the whole batch's digits and sets `bad` to kSegTables.  Otherwise it
+// writes fpos and tprefix (per segment; entries S+1 .. T repeat the end),
+// counts each segment's digits, and sets `bad` to kSegKeys if a key lies
+// outside its table's range; the passes then sort globally, summing the
+// per-segment counts.
+constexpr unsigned int kSegKeys = 1u;    // a key outside its table's range
+constexpr unsigned int kSegTables = 2u;  // hsc decreases, or exceeds 2^bits
 struct SegSort {
-  int64_t* fpos;         // [T + 1] first position of each feature's positions
-  int32_t* tprefix;      // [T + 1] first tile of each feature's segment
-  uint32_t* fhist;       // [T][kHistCopies][kMaxPasses][kRadix] digit counts (zeroed), a pass's row
+  int64_t* fpos;         // [T + 1] first position of each segment
+  int32_t* tprefix;      // [T + 1] first tile of each segment
+  uint32_t* fhist;       // [T][kHistCopies][kMaxPasses][kRadix] per-segment digit counts (zeroed), a pass's row
   unsigned int* bad;     // zeroed; nonzero (kSegKeys or kSegTables): sort globally
   int32_t T;             // 0: no segments
 };
@@ -134,8 +136,12 @@ __global__ void __launch_bounds__(256)
   __shared__ uint32_t s_mark[kLinTile];  // bag (relative to blo) starting at each position
   __shared__ uint32_t hf[2][kMaxPasses][kRadix];  // digit counts of the block's first two features
   __shared__ int s_bad;
-  __shared__ int s_tables_ok;  // hsc increases strictly (per-feature counts)
+  __shared__ int s_tables_ok;  // hsc does not decrease and fits the bits (per-segment counts)
+  __shared__ int s_ngroups;    // segments: runs of features with equal hsc (one table)
   __shared__ int64_t s_hsc[kSegMaxT + 1];  // hsc of a batch of at most kSegMaxT features
+  __shared__ int64_t s_gend[kSegMaxT];     // feature t's table end: hsc of the next segment
+  __shared__ int s_gid[kSegMaxT];          // feature t's segment
+  __shared__ int s_gfirst[kSegMaxT + 1];   // segment g's first feature; [S] = T
   __shared__ int64_t s_range[2][2];      // [half][lo, hi] of the cooperative searches
   __shared__ uint32_t s_cnt[2][2];       // [half][wave of the half]
   __shared__ uint32_t s_wmax[4];
@@ -194,14 +200,33 @@ __global__ void __launch_bounds__(256)
     }
   }
   const int64_t blo = s_range[0][0], bhi = s_range[1][0];
-  if (seg.T > 0 && w == 0) {  // hsc into LDS; does it increase strictly over the T features?
+  if (seg.T > 0 && w == 0) {  // hsc into LDS; segments; does hsc not decrease?
     const int64_t next = __shfl(lane_hsc, lane + 1 < 64 ? lane + 1 : 63, 64);
+    const int64_t prev = __shfl(lane_hsc, lane > 0 ? lane - 1 : 0, 64);
     if (lane <= seg.T) s_hsc[lane] = lane_hsc;
     // In-range keys must also fit the sorted bits (a sort over fewer bits
     // orders keys by their low bits, across features).
     const bool fits = lane != seg.T || bits >= 62 || lane_hsc <= (int64_t(1) << bits);
-    const bool all_up = __all((lane >= seg.T || lane_hsc < next) && fits);
-    if (lane == 0) s_tables_ok = all_up ? 1 : 0;
+    const bool all_up = __all((lane >= seg.T || lane_hsc <= next) && fits);
+    // Consecutive features with equal hsc share a table: one segment, whose
+    // keys end at the next segment's hsc (hsc[T] for the last).
+    const bool start = lane < seg.T && (lane == 0 || lane_hsc != prev);
+    const uint64_t sm = __ballot(start);
+    const uint64_t upto = (2ull << lane) - 1ull;  // lanes 0..lane
+    const uint64_t above = sm & ~upto;
+    const int nxt = above ? __ffsll(static_cast<long long>(above)) - 1 : seg.T;
+    const int64_t gend = __shfl(lane_hsc, nxt, 64);
+    const int gid = __popcll(sm & upto) - 1;
+    if (lane < seg.T) {
+      s_gid[lane] = gid;
+      s_gend[lane] = gend;
+    }
+    if (start) s_gfirst[gid] = lane;
+    if (lane == 0) {
+      s_tables_ok = all_up ? 1 : 0;
+      s_ngroups = __popcll(sm);
+      s_gfirst[__popcll(sm)] = seg.T;
+    }
   }
   // Digit counts per feature when segments are possible (their sum gives the
   // whole batch's if a key turns out to lie outside its feature), else the
@@ -297,15 +322,16 @@ __global__ void __launch_bounds__(256)
           atomicAdd(&h[p][(k32 >> (p * kRadixBits)) & digit_mask(bits, p)], 1u);
       } else {
         const int64_t i64 = static_cast<int64_t>(idx[it]);
-        const int64_t tf = t - t_lo;
-        const int64_t rows_t = s_hsc[t + 1] - s_hsc[t];
-        if (i64 < 0 || i64 >= rows_t) s_bad = 1;  // outside its feature's range
+        const int gl = s_gid[t];
+        const int tf = gl - s_gid[t_lo];  // relative to the block's first segment
+        const int64_t rows_t = s_gend[t] - s_hsc[t];
+        if (i64 < 0 || i64 >= rows_t) s_bad = 1;  // outside its table's range
         for (int p = 0; p < passes; ++p) {
           const uint32_t d = (k32 >> (p * kRadixBits)) & digit_mask(bits, p);
           if (tf == 0 || tf == 1)
             atomicAdd(&hf[tf][p][d], 1u);
-          else  // a block over three or more features (short features): straight to memory
-            atomicAdd(&seg.fhist[t * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords +
+          else  // a block over three or more segments (short ones): straight to memory
+            atomicAdd(&seg.fhist[gl * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords +
                                  p * kRadix + d], 1u);
         }
       }
@@ -315,25 +341,28 @@ __global__ void __launch_bounds__(256)
       if (threadIdx.x == 0 && s_bad) *seg.bad = kSegKeys;
       const int nbins = passes * kRadix;
       const int rot = static_cast<int>(blockIdx.x * 97u % static_cast<uint32_t>(nbins));
-      for (int f = 0; f < 2 && t_lo + f < seg.T; ++f)
+      const int g_lo = s_gid[t_lo];
+      for (int f = 0; f < 2 && g_lo + f < s_ngroups; ++f)
         for (int jj = threadIdx.x; jj < nbins; jj += 256) {
           const int j = jj + rot < nbins ? jj + rot : jj + rot - nbins;
           const uint32_t c = (&hf[f][0][0])[j];
           if (c)
-            atomicAdd(&seg.fhist[(t_lo + f) * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords + j],
+            atomicAdd(&seg.fhist[(g_lo + f) * kSegRow + (blockIdx.x % kHistCopies) * kHistCopyWords + j],
                       c);
         }
       if (blockIdx.x == 0 && w == 0) {
-        // Lane f <= T: feature f's first position; its segment's tile count; the
-        // features' first tiles by a wave scan.  The positions must not decrease
-        // for the segments to be in key order (hsc increases: checked above).
-        const int T = seg.T;
-        const int64_t fp = lane <= T ? static_cast<int64_t>(offsets[static_cast<int64_t>(lane) * B]) : 0;
+        // Lane g <= S: segment g's first position (its first feature's); its
+        // tile count; the segments' first tiles by a wave scan.  Entries S+1 .. T
+        // repeat the end, so no tile falls in them.  The positions must not
+        // decrease for the segments to be in key order (hsc does not: checked).
+        const int T = seg.T, S = s_ngroups;
+        const int64_t fp =
+            lane <= S ? static_cast<int64_t>(offsets[static_cast<int64_t>(s_gfirst[lane]) * B]) : N;
         const int64_t fnext = __shfl(fp, lane + 1 < 64 ? lane + 1 : 63, 64);
-        const uint32_t nt = lane < T ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
+        const uint32_t nt = lane < S ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
         const uint32_t incl = wave_incl_scan<SumOp>(nt);
         // The segments must also cover exactly the positions [0, N).
-        bool bad = (lane < T && fnext < fp) || (lane == 0 && fp != 0) || (lane == T && fp != N);
+        bool bad = (lane < S && fnext < fp) || (lane == 0 && fp != 0) || (lane == S && fp != N);
         if (lane <= T) seg.fpos[lane] = fp;
         if (lane < T) seg.tprefix[lane + 1] = static_cast<int32_t>(incl);
         if (lane == 0) seg.tprefix[0] = 0;
