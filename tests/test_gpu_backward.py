@@ -281,8 +281,9 @@ def _shared_tables(rng, ftm, rows, dims, B, max_L, dup=False):
 @pytest.mark.parametrize("ftm", [[0, 1, 0, 2, 1], [0, 0, 1, 1, 2]])
 def test_backward_shared_tables(dev, pooling, weighted, dup, ftm):
     """Features sharing tables (fbgemm's feature_table_map; hash_size_cumsum
-    then repeats or decreases, so the sort runs over the whole batch): one run
-    per row of a shared table, each occurrence summing its own feature's
+    then decreases, and the sort runs over the whole batch, or repeats, and
+    each table's features sort as one segment): one run per row of a shared
+    table, each occurrence summing its own feature's
     gradient columns (MEAN: its own bag length); duplicate-heavy batches reach
     the chunked long-run path.  Transpose bit-exact, update within rtol 1e-5."""
     print(f"[case] shared tables ftm={ftm} pool={pooling} weighted={weighted} dup={dup}",
