@@ -545,9 +545,11 @@ def wl_backward(args, dev) -> Workload:
     alg = inp.N * 8 + (T * B + 1) * 8 + B * inp.total_D * 4 + U * (2 * D * 4 + 2 * 4)
 
     def cpu():
-        """The C restatement of the backward (stable merge sort of the
-        linearized keys, per-row sum in sorted order, rowwise Adagrad), one
-        thread, in place on host copies of the weights and gradient."""
+        """The multithreaded C++ restatement of the backward (key ranges split
+        over the host's threads; per range a sort of (key, position), then
+        each run's sum in position order and its rowwise-Adagrad update), in
+        place on host copies of the weights and gradient; bit-identical to the
+        single-threaded C restatement, which is timed beside it."""
         sys.path.insert(0, str(REPO / "oracle"))
         import oracle as orc
 
@@ -557,15 +559,25 @@ def wl_backward(args, dev) -> Workload:
         m1h = np.zeros(T * E, dtype=np.float32)
         w_off_h = (np.arange(T) * E * D).astype(np.int64)
         m_off_h = (np.arange(T) * E).astype(np.int64)
-        fn = lambda: orc.backward_rowwise_adagrad(  # noqa: E731
+        nthreads = orc.host_threads()
+        fn = lambda: orc.backward_rowwise_adagrad_mt(  # noqa: E731
+            Wh, w_off_h, inp.D_offsets, B, inp.hash_size_cumsum, inp.total_hash_size_bits,
+            inp.indices, inp.offsets, 0, gh, m1h, m_off_h, 0.01, 1e-8, inplace=True,
+            nthreads=nthreads)
+        log(f"CPU baseline: C++ restatement of the backward, {nthreads} threads")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        fn1 = lambda: orc.backward_rowwise_adagrad(  # noqa: E731
             Wh, w_off_h, inp.D_offsets, B, inp.hash_size_cumsum, inp.total_hash_size_bits,
             inp.indices, inp.offsets, 0, gh, m1h, m_off_h, 0.01, 1e-8, inplace=True)
         log("CPU baseline: C restatement of the backward, 1 thread")
-        med, runs = cpu_time(fn, args.cpu_seconds)
-        return cpu_record(inp.N / med, "lookups/s", 1, "port",
+        med1, runs1 = cpu_time(fn1, args.cpu_seconds / 3, min_runs=1, warm=0)
+        return cpu_record(inp.N / med, "lookups/s", nthreads, "port",
                           f"full config-3 batch (N={inp.N} lookups), median of {runs} runs; the "
-                          f"oracle's C restatement (stable merge sort + segment sum + rowwise "
-                          f"Adagrad), one thread, in place")
+                          f"multithreaded C++ restatement (oracle/backward_mt.cpp: key ranges "
+                          f"over {nthreads} threads, sort, per-run sum in position order, "
+                          f"rowwise Adagrad; bit-identical to the C restatement), in place; "
+                          f"1 thread (the C restatement: stable merge sort + segment sum + "
+                          f"update): {inp.N / med1:.4g} lookups/s ({runs1} runs)")
 
     return Workload(
         metric="TBE backward + exact rowwise Adagrad lookups/sec, 1 MI355X", unit="lookups/s",
@@ -729,6 +741,27 @@ def measure(args, config: int, dev) -> dict:
     return line
 
 
+def summary(line: dict) -> dict:
+    """Per configuration, the figures the targets are read from, compactly:
+    value and ms per step (the timed steps), the cold launch time and its
+    fraction of peak HBM, measured traffic over the roofline bytes, and the CPU
+    baseline."""
+    out = {}
+    for c in (1, 2, 3, 4, 5):
+        r = line if c == 2 else line.get(f"config{c}")
+        if not r:
+            continue
+        roof = r.get("roofline") or {}
+        cpu = r.get("cpu_baseline") or {}
+        traffic, nbytes = roof.get("traffic"), roof.get("alg_bytes_per_launch")
+        out[f"config{c}"] = dict(
+            value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"],
+            launch_ms_cold=roof.get("launch_ms"), frac=roof.get("frac"),
+            traffic_over_roof_bytes=(traffic / nbytes) if traffic and nbytes else None,
+            cpu_baseline=cpu.get("value"), cpu_unit=cpu.get("unit"), cpu_cores=cpu.get("cores"))
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -766,6 +799,7 @@ def main():
             line[f"config{c}"] = {k: rc[k] for k in ("metric", "value", "unit", "ms_per_step",
                                                      "dtype", "config", "roofline", "effective",
                                                      "cpu_baseline") if k in rc}
+        line["summary"] = summary(line)  # last: a reader of the line's tail sees every config
     print(json.dumps(line), flush=True)
 
 

@@ -65,7 +65,13 @@ extern "C" {
 /* Maximum number of jagged dimensions the jagged kernels accept. */
 #define MX_MAX_JAGGED_DIM 4
 
-/* Library version (major*10000 + minor*100 + patch). */
+/* Library version (major*10000 + minor*100 + patch).  MX_FBGEMM_VERSION is
+ * the version this header describes; a caller compares it with mx_version()
+ * before binding.  0.2.0: mx_tbe_backward_rowwise_adagrad(_vbe) take their
+ * stochastic-rounding state as `const mx_rng_state*` where 0.1.0 took a
+ * `uint64_t seed` at the same position, and mx_set_status_mailbox takes
+ * MX_STATUS_WORDS words where 0.1.0 took one (not binary compatible). */
+#define MX_FBGEMM_VERSION 200
 int mx_version(void);
 
 /* Thread-local text of the last failing call on this thread ("" if none). */
@@ -77,12 +83,21 @@ const char* mx_last_error(void);
  * tiles (decoupled look-back).  Every such wait is bounded; one that runs
  * out (never expected: the tile waited on was scheduled earlier and
  * publishes without waiting) makes the call leave its outputs -- the run
- * layout, the weight and momentum update -- unwritten, and stores 1 into the
- * host-visible word registered here for the current device (pinned host
- * memory owned by the caller, which reads and clears it; NULL unregisters).
- * Kernels launched before a registration (or captured in a graph before it)
- * do not see it. */
-int mx_set_status_mailbox(unsigned int* host_word);
+ * layout, the weight and momentum update -- unwritten, and stores 1 into
+ * word MX_STATUS_LOOKBACK of the host-visible status words registered here
+ * for the current device.
+ * mx_nbit_forward stores 1 into word MX_STATUS_NBIT_TABLE when a table of the
+ * call cannot be served -- its type byte names no type the call's max_*_D
+ * arguments launch, or it is an INT4 table of odd D or an INT2 table of D not
+ * a multiple of 4 -- after writing that table's output columns as zeros.
+ * host_words points at MX_STATUS_WORDS words of pinned host memory owned by
+ * the caller, which reads and clears them; NULL unregisters.  Kernels
+ * launched before a registration (or captured in a graph before it) do not
+ * see it. */
+#define MX_STATUS_LOOKBACK 0
+#define MX_STATUS_NBIT_TABLE 1
+#define MX_STATUS_WORDS 2
+int mx_set_status_mailbox(unsigned int* host_words);
 
 /* Test hook: while enabled, every look-back wait of later calls gives up at
  * once (failure-handling tests; every kernel still exits normally). */

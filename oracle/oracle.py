@@ -27,6 +27,7 @@ ORACLE_DIR = Path(__file__).resolve().parent
 BUILD_DIR = ORACLE_DIR / "_build"
 ORACLE_LIB = BUILD_DIR / "libmx_oracle.so"
 FBGEMM_LIB = BUILD_DIR / "libfbgemm_cpu.so"
+ORACLE_MT_LIB = BUILD_DIR / "libmx_oracle_mt.so"
 
 POOL_SUM, POOL_MEAN = 0, 1
 FP32, FP16, INT8, INT4, INT2 = 0, 1, 2, 3, 4
@@ -42,6 +43,7 @@ def build(quiet: bool = True) -> None:
 
 _lib = None
 _fb = None
+_mt = None
 
 
 def _load(path: Path):
@@ -82,6 +84,19 @@ def lib():
         _lib.orc_float_to_half.argtypes = [f32]
         _lib.orc_float_to_half.restype = ctypes.c_uint16
     return _lib
+
+
+def lib_mt():
+    """The multithreaded C++ restatement of the backward (backward_mt.cpp)."""
+    global _mt
+    if _mt is None:
+        _mt = _load(ORACLE_MT_LIB)
+        P = ctypes.c_void_p
+        i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+        _mt.orc_backward_rowwise_adagrad_mt.argtypes = [
+            P, P, P, i32, i64, P, i32, P, P, i64, i32, P, P, i64, P, P, f32, f32, f32, i32, i32]
+        _mt.orc_backward_rowwise_adagrad_mt.restype = ctypes.c_int
+    return _mt
 
 
 def fbgemm():
@@ -278,6 +293,35 @@ def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, po
         indices.shape[0], pooling, None if iw is None else _p(iw), _p(grad), grad.shape[1],
         _p(m1), _p(m1_off), lr, eps, weight_decay, weight_decay_mode, info_B_num_bits)
     assert rc == 0, f"orc_backward_rowwise_adagrad failed ({rc})"
+    return W, m1
+
+
+def backward_rowwise_adagrad_mt(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,
+                                momentum1, m1_off, lr, eps, weight_decay=0.0,
+                                weight_decay_mode=0, indice_weights=None, inplace=False,
+                                nthreads=None):
+    """backward_rowwise_adagrad on `nthreads` threads (default: this host's),
+    split over key ranges; bit-identical to it.  Requires every key below
+    2^bits."""
+    if inplace:
+        assert W.dtype == np.float32 and W.flags["C_CONTIGUOUS"]
+        assert momentum1.dtype == np.float32 and momentum1.flags["C_CONTIGUOUS"]
+        m1 = momentum1
+    else:
+        W = np.array(W, dtype=np.float32, copy=True)
+        m1 = np.array(momentum1, dtype=np.float32, copy=True)
+    w_off, D_off = _c(w_off, np.int64), _c(D_off, np.int32)
+    hsc, m1_off = _c(hsc, np.int64), _c(m1_off, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    grad = _c(grad, np.float32)
+    iw = None if indice_weights is None else _c(indice_weights, np.float32)
+    T = D_off.shape[0] - 1
+    rc = lib_mt().orc_backward_rowwise_adagrad_mt(
+        _p(W), _p(w_off), _p(D_off), T, B, _p(hsc), bits, _p(indices), _p(offsets),
+        indices.shape[0], pooling, None if iw is None else _p(iw), _p(grad), grad.shape[1],
+        _p(m1), _p(m1_off), lr, eps, weight_decay, weight_decay_mode,
+        nthreads or host_threads())
+    assert rc == 0, f"orc_backward_rowwise_adagrad_mt failed ({rc})"
     return W, m1
 
 

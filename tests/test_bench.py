@@ -43,3 +43,23 @@ def test_profiles_carry_cold_traffic(bench, name):
 
 def test_missing_profile_gives_no_traffic(bench):
     assert bench.traffic_from_profile("no_such_profile") == (None, None)
+
+
+def test_summary_holds_every_config(bench):
+    """The summary (printed as the line's last key) carries each config's
+    value, step time, cold launch, fraction of peak, traffic ratio and CPU
+    baseline."""
+    def rec(v):
+        return dict(value=v, unit="u", ms_per_step=v / 10,
+                    roofline=dict(launch_ms=v / 20, frac=0.5, traffic=150.0,
+                                  alg_bytes_per_launch=100.0),
+                    cpu_baseline=dict(value=v / 100, unit="u", cores=16))
+    line = rec(2.0)
+    for c in (1, 3, 4, 5):
+        line[f"config{c}"] = rec(float(c))
+    line["summary"] = bench.summary(line)
+    assert list(line)[-1] == "summary"
+    s = line["summary"]
+    assert sorted(s) == [f"config{c}" for c in (1, 2, 3, 4, 5)]
+    assert s["config4"]["ms_per_step"] == 0.4 and s["config4"]["frac"] == 0.5
+    assert s["config3"]["cpu_cores"] == 16 and s["config2"]["traffic_over_roof_bytes"] == 1.5

@@ -9,6 +9,7 @@ import torch
 
 import oracle as orc
 from mx_fbgemm import bench_inputs
+from adagrad_bounds import assert_eps_pin_close, assert_reordered_adagrad_close, eps_pin_case
 from tbe_helpers import random_tbe, weight_offsets
 
 pytestmark = pytest.mark.gpu
@@ -411,12 +412,15 @@ def _update_fp64(inp, pooling, W, m1, m1_off, grad, lr, eps):
     (4, 195, [156, 56, 144, 12], [300, 1, 50, 70000], 44, 0, False),
     (1, 174, [564], [1], 44, 1, False),  # one row: every occurrence in one run
 ])
-def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
-    """Tables of 1-4 rows: runs of thousands of occurrences.  There the fp32 oracle's sequential sum drifts from the exact
-    value by up to ~3e-7 on the updated weights (past rtol 1e-5 / atol 1e-7 on
-    a few elements), while the kernels' chunked sums stay within ~1e-8.  Both
-    are checked against a float64 evaluation of the same update; the bound on
-    the kernels is 3e-8, ten times tighter than the oracle's own drift."""
+def test_extreme_runs_against_oracle_and_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
+    """Tables of 1-4 rows: runs of thousands of occurrences, where the kernels
+    (chunked sums) and the oracle (one sequential sum per run) add each
+    row's gradient terms in very different orders.  Checked against the
+    oracle element by element under the first-order reordering bound of the
+    two summation orders carried through the update (tests/adagrad_bounds.py;
+    a pure rtol fails near cancelled sums by construction), and against a
+    float64 evaluation of the same update: the kernels' fp32 error stays
+    within 3e-8 there, while the oracle's sequential sum drifts up to ~3e-7."""
     print(f"[case] extreme runs T={T} B={B} dims={dims} rows={rows} pool={pooling}", flush=True)
     rng = np.random.default_rng(B + T)
     inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
@@ -437,9 +441,81 @@ def test_extreme_runs_against_fp64(dev, T, B, dims, rows, max_L, pooling, dup):
         torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
         torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty, pl,
         torch.from_numpy(m1_off).to(dev), eps, lr, 0.0, 0, 0.0)
-    Wg = Wd.cpu().numpy().astype(np.float64)
-    assert np.abs(Wg - W64).max() <= 3e-8
-    np.testing.assert_allclose(m1d.cpu().numpy(), m64, rtol=1e-5, atol=0)
+    W_exp, m_exp = orc.backward_rowwise_adagrad(
+        W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
+        0.0, 0, orc.info_B_num_bits(T, inp.B))
+    Wg, mg = Wd.cpu().numpy(), m1d.cpu().numpy()
+    assert_reordered_adagrad_close(Wg, mg, W_exp, m_exp, W, m1, weight_offsets(inp), m1_off, inp,
+                                   grad, pooling, lr, eps)
+    assert np.abs(Wg.astype(np.float64) - W64).max() <= 3e-8
+    np.testing.assert_allclose(mg, m64, rtol=1e-5, atol=0)
+
+
+def _backward_gpu(dev, inp, W, m1, m1_off, grad, pooling, lr, eps):
+    Wd, m1d = torch.from_numpy(W).to(dev), torch.from_numpy(m1).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(inp.T, dtype=torch.int32, device=dev)
+    torch.ops.fbgemm.split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+        torch.from_numpy(grad).to(dev), Wd, empty, empty, pl,
+        torch.from_numpy(weight_offsets(inp)).to(dev), torch.from_numpy(inp.D_offsets).to(dev),
+        max(inp.D), torch.from_numpy(inp.hash_size_cumsum).to(dev), inp.total_hash_size_bits,
+        torch.from_numpy(inp.indices).to(dev), torch.from_numpy(inp.offsets).to(dev), pooling,
+        torch.zeros(0, dtype=torch.int32, device=dev), 0, 0, False, m1d, empty, pl,
+        torch.from_numpy(m1_off).to(dev), eps, lr, 0.0, 0, 0.0)
+    return Wd.cpu().numpy(), m1d.cpu().numpy()
+
+
+def _eps_pin(dev, inp, seed, pooling=0):
+    rng = np.random.default_rng(seed)
+    # MEAN scales each slice by 1/L: a gradient L times larger keeps sqrt(h') at eps.
+    L = np.diff(inp.offsets)
+    sigma = 1e-8 * (float(L[L > 0].mean()) if pooling == 1 else 1.0)
+    W, m1, grad = eps_pin_case(rng, inp, sigma)
+    m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
+    lr, eps = 0.01, 1e-8
+    W_exp, m_exp = orc.backward_rowwise_adagrad(
+        W, weight_offsets(inp), inp.D_offsets, inp.B, inp.hash_size_cumsum,
+        inp.total_hash_size_bits, inp.indices, inp.offsets, pooling, grad, m1, m1_off, lr, eps,
+        0.0, 0, orc.info_B_num_bits(inp.T, inp.B))
+    touched = m_exp > 0
+    ratio = np.sqrt(m_exp[touched]) / eps
+    # The case is one where eps matters: sqrt(h') within a factor 4 of eps
+    # for most touched rows.
+    assert np.median(ratio) > 0.25 and np.median(ratio) < 4, np.median(ratio)
+    Wg, mg = _backward_gpu(dev, inp, W, m1, m1_off, grad, pooling, lr, eps)
+    assert_eps_pin_close(Wg, mg, W_exp, m_exp)
+    # Rows the batch does not touch: bit-identical.
+    keep = np.concatenate([np.repeat(~touched[m1_off[t]:m1_off[t] + E], D)
+                           for t, (E, D) in enumerate(zip(inp.E, inp.D))])
+    assert np.array_equal(Wg[keep], W[keep])
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_eps_pin_small(dev, pooling):
+    """Adagrad's eps where it matters: zero momentum, gradients N(0, 1e-8),
+    so sqrt(h') is about eps and the update's denominator sqrt(h') + eps is
+    about 2 eps.  A kernel with eps inside the root, or without it, is off by
+    orders of magnitude or by 2x; the same check rejects those placements in
+    a CPU copy of the rule (tests/test_adagrad_bounds.py)."""
+    print(f"[case] eps pin small pooling={pooling}", flush=True)
+    rng = np.random.default_rng(71 + pooling)
+    inp = random_tbe(rng, 3, 64, [64, 64, 64], [400, 900, 50], 12)
+    _eps_pin(dev, inp, 72 + pooling, pooling)
+
+
+def test_eps_pin_config3_table(dev):
+    """The eps pin on one full-size config-3 table: table 0 of config 2
+    (E = 1M, D = 128, B = 4096, Zipf(1.05) indices with runs of thousands),
+    gradients N(0, 1e-8), zero momentum, SUM; weights and momentum vs the
+    oracle at rtol 1e-5."""
+    print("[case] eps pin config3 table 0", flush=True)
+    full = bench_inputs.config2()
+    B = full.B
+    inp = bench_inputs.TbeInput(T=1, E=[full.E[0]], D=[full.D[0]], B=B,
+                                indices=full.indices[: int(full.offsets[B])].copy(),
+                                offsets=full.offsets[: B + 1].copy())
+    _eps_pin(dev, inp, 73)
 
 
 @pytest.mark.parametrize("pooling", [0, 1])
@@ -719,8 +795,9 @@ def test_module_training_step_fp16(dev, sr):
 
 def test_lookback_giveup_is_reported_and_leaves_outputs_alone(dev):
     """Forced from the host (a test hook makes every look-back wait give up at
-    once; every kernel still exits normally): the transpose and the backward
-    leave their outputs alone, and the next call on the device raises."""
+    once; every kernel still exits normally): the transpose returns an empty
+    run layout, the backward leaves weights and momentum alone, and the next
+    call on the device raises."""
     print("[case] forced look-back give-up", flush=True)
     rng = np.random.default_rng(21)
     inp = random_tbe(rng, 3, 2048, [64] * 3, [5000, 300, 70000], 20)  # ~12 sort tiles
@@ -743,6 +820,20 @@ def test_lookback_giveup_is_reported_and_leaves_outputs_alone(dev):
             inp.total_hash_size_bits, torch.from_numpy(inp.indices).to(dev),
             torch.from_numpy(inp.offsets).to(dev), 0, e32, 0, 0, False, m1, empty, pl, m_off,
             1e-8, 0.05, 0.0, 0, 0.0)
+
+    # A failed transpose returns an empty layout: no runs, every run length 0,
+    # the whole cumsum 0 (not memory left as allocated).
+    torch.ops.mx_fbgemm.test_force_lookback_giveup(True)
+    try:
+        _, _, _, _, lengths, num_runs, cum = _transpose_gpu(dev, inp, nb)
+        torch.cuda.synchronize()
+    finally:
+        torch.ops.mx_fbgemm.test_force_lookback_giveup(False)
+    assert int(num_runs.item()) == 0
+    assert not lengths.any() and not cum.any(), "a failed transpose left a non-empty layout"
+    with pytest.raises(RuntimeError, match="gave up a look-back wait"):
+        _transpose_gpu(dev, inp, nb)
+    _check_transpose(dev, inp)
 
     torch.ops.mx_fbgemm.test_force_lookback_giveup(True)
     try:

@@ -14,7 +14,8 @@ import torch
 
 import oracle as orc
 from mx_fbgemm import bench_inputs
-from nbit_helpers import assert_nbit_close, build_weights, build_weights_gpu, nbit_forward_gpu
+from nbit_helpers import (assert_nbit_close, build_weights, build_weights_gpu, max_dims,
+                          nbit_forward_gpu)
 from tbe_helpers import random_tbe
 
 pytestmark = pytest.mark.gpu
@@ -121,3 +122,87 @@ def test_full_size_every_bag(dev, config):
         for t in range(cfg.T):
             d0, d1 = int(cfg.D_offsets[t]), int(cfg.D_offsets[t + 1])
             assert np.all(g[empty[t], d0:d1].view(np.uint16) == 0)
+
+
+def _raw_nbit(dev, W, w_off, ty_bytes, dims, indices, offsets, maxima, pooling=0, iw=None):
+    """The op called with maxima chosen by the test (not derived from the tables)."""
+    T = len(ty_bytes)
+    D_off = np.concatenate([[0], np.cumsum(dims)]).astype(np.int32)
+    m2, m4, m8, m16, m32 = maxima
+    return torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
+        W, torch.zeros(0, dtype=torch.uint8, device=dev),
+        torch.zeros(T, dtype=torch.int32, device=dev), torch.as_tensor(w_off, device=dev),
+        torch.as_tensor(np.asarray(ty_bytes, np.uint8), device=dev),
+        torch.as_tensor(D_off, device=dev), int(D_off[-1]), m2, m4, m8, m16, m32,
+        torch.as_tensor(indices, device=dev), torch.as_tensor(offsets, device=dev), pooling,
+        None if iw is None else torch.as_tensor(iw, device=dev), 1, None, None, 16)
+
+
+def test_short_indice_weights_raise(dev):
+    print("[case] nbit indice_weights shorter than indices", flush=True)
+    rng = np.random.default_rng(61)
+    tys, dims = [orc.INT8, orc.INT4], [32, 64]
+    inp = random_tbe(rng, 2, 8, dims, [20, 30], 6, empty_frac=0.0)
+    buf, w_off = build_weights(rng, tys, dims, inp.E)
+    iw = np.ones(inp.N - 1, np.float32)
+    with pytest.raises(RuntimeError, match="one entry per index"):
+        _raw_nbit(dev, torch.from_numpy(buf).to(dev), w_off, tys, dims, inp.indices,
+                  inp.offsets, max_dims(tys, dims), iw=iw)
+
+
+# (bad table's type byte, its D, the type its bytes are built as, maxima override)
+BAD_TABLES = {
+    "bf16_type_byte": (5, 32, orc.FP16, None),           # BF16: no nbit launch serves it
+    "odd_int4_D": (orc.INT4, 7, orc.INT4, None),          # 7 codes leave half a byte
+    "int2_D_not_multiple_of_4": (orc.INT2, 6, orc.INT2, None),
+    "type_with_zero_max_D": (orc.INT2, 16, orc.INT2, 0),  # max_int2_D = 0: not launched
+}
+
+
+@pytest.mark.parametrize("case", sorted(BAD_TABLES))
+def test_unservable_table_is_zeroed_and_reported(dev, case):
+    """A table no launch of the call can serve has its output columns written
+    as zeros (not left as allocated); the other tables match the oracle, and
+    the next nbit call on the device raises, once."""
+    print(f"[case] nbit unservable table: {case}", flush=True)
+    bad_ty, bad_D, build_ty, bad_max = BAD_TABLES[case]
+    rng = np.random.default_rng(62)
+    ty_bytes = [orc.INT8, bad_ty, orc.FP16, orc.INT4]
+    dims = [32, bad_D, 64, 16]
+    build_tys = [orc.INT8, build_ty, orc.FP16, orc.INT4]
+    inp = random_tbe(rng, 4, 37, dims, [50, 40, 30, 20], 9)
+    buf, w_off = build_weights(rng, build_tys, dims, inp.E)
+    good = [0, 2, 3]
+    maxima = list(max_dims([ty_bytes[t] for t in good], [dims[t] for t in good]))
+    if bad_max is not None:
+        maxima[0] = bad_max  # the INT2 slot
+    elif bad_ty == orc.INT2:
+        # INT2 is launched, with a maximum the host check accepts (a multiple
+        # of 4), so the device check is the one that finds the table.  (The
+        # INT4 case keeps the served INT4 table's maximum, 16.)
+        maxima[0] = 8
+    W = torch.from_numpy(buf).to(dev)
+    # The output reuses a freed block full of NaN, so unwritten columns would show.
+    junk = torch.full((inp.B, inp.total_D), float("nan"), dtype=torch.float16, device=dev)
+    del junk
+    got = _raw_nbit(dev, W, w_off, ty_bytes, dims, inp.indices, inp.offsets, maxima)
+    torch.cuda.synchronize()
+    g = got.cpu().numpy()
+    d0 = int(inp.D_offsets[1])
+    assert np.all(g[:, d0:d0 + bad_D].view(np.uint16) == 0), "unservable columns not zeroed"
+    # The served tables: the oracle on the same lookup restricted to them.
+    lens = np.diff(inp.offsets).reshape(inp.T, inp.B)
+    sub_idx = np.concatenate([inp.indices[inp.offsets[t * inp.B]:inp.offsets[(t + 1) * inp.B]]
+                              for t in good])
+    sub_off = bench_inputs.offsets_from_lengths(lens[good].reshape(-1))
+    sub_D_off = np.concatenate([[0], np.cumsum([dims[t] for t in good])]).astype(np.int32)
+    exp = orc.nbit_forward(buf, w_off[good], [ty_bytes[t] for t in good], sub_D_off, inp.B,
+                           sub_idx, sub_off, 0)
+    cols = np.concatenate([np.arange(inp.D_offsets[t], inp.D_offsets[t + 1]) for t in good])
+    assert_nbit_close(g[:, cols], exp)
+    with pytest.raises(RuntimeError, match="cannot serve"):
+        _raw_nbit(dev, W, w_off, ty_bytes, dims, inp.indices, inp.offsets, maxima)
+    # Reported once: a valid call then runs normally.
+    ok = _raw_nbit(dev, W, w_off[good], [ty_bytes[t] for t in good], [dims[t] for t in good],
+                   sub_idx, sub_off, maxima)
+    assert_nbit_close(ok, exp)

@@ -65,17 +65,17 @@ __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
 
 }  // namespace mx
 
-extern "C" int mx_version(void) { return 100; }
+extern "C" int mx_version(void) { return MX_FBGEMM_VERSION; }
 
 extern "C" const char* mx_last_error(void) { return mx::g_last_error.c_str(); }
 
-extern "C" int mx_set_status_mailbox(unsigned int* host_word) {
+extern "C" int mx_set_status_mailbox(unsigned int* host_words) {
   mx::clear_error();
   int dev = 0;
   MX_HIP_CHECK(hipGetDevice(&dev));
   MX_REQUIRE(dev >= 0 && dev < 64, "device %d out of range", dev);
   std::lock_guard<std::mutex> lock(mx::g_mailbox_mu);
-  mx::g_mailbox[dev] = host_word;
+  mx::g_mailbox[dev] = host_words;
   return MX_OK;
 }
 

@@ -22,8 +22,10 @@ void clear_error();
 // Number of compute units of the current device (cached per device).
 int num_cus();
 
-// Host-visible word registered for the current device (mx_set_status_mailbox),
-// or null: a look-back that gives up stores 1 there.
+// Host-visible status words registered for the current device
+// (mx_set_status_mailbox, MX_STATUS_WORDS of them), or null: a look-back that
+// gives up stores 1 into word MX_STATUS_LOOKBACK, an nbit lookup that meets a
+// table it cannot serve into word MX_STATUS_NBIT_TABLE.
 unsigned int* status_mailbox();
 // Spin bound of the look-back waits: `dflt`, or -1 while the test hook that
 // makes every look-back give up at once is on.

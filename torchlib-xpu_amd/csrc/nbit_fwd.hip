@@ -47,7 +47,20 @@ struct NbitArgs {
   int32_t pooling;
   int32_t row_align;
   int32_t out_f16;
+  int32_t served;          // bit ty set: the call launches type ty
+  int32_t check;           // this launch zeroes and reports tables no launch can serve
+  unsigned int* mailbox;   // host-visible status words of the device, may be null
 };
+
+// A table the call can serve: its type has a launch, its D is not negative,
+// and its codes fill whole bytes (INT4: D even, INT2: D a multiple of 4; the
+// row holds D*bits/8 code bytes, rounded down).
+__device__ __forceinline__ bool table_ok(int32_t ty, int32_t D, int32_t served) {
+  if (ty < 0 || ty > MX_SPARSE_INT2 || ((served >> ty) & 1) == 0 || D < 0) return false;
+  if (ty == MX_SPARSE_INT4) return (D & 1) == 0;
+  if (ty == MX_SPARSE_INT2) return (D & 3) == 0;
+  return true;
+}
 
 __device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, int32_t align) {
   int64_t u;
@@ -460,8 +473,34 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   if (tu >= static_cast<uint32_t>(a.T)) return;  // block-uniform
   const int64_t t = tu;
   const int32_t ty = table_type(a.tys, t);
-  if (ty != TY) return;  // block-uniform
+  if (ty != TY && !a.check) return;  // block-uniform
   const int64_t b0 = static_cast<int64_t>(blockIdx.x - tu * bpt) * BPB;
+  const int32_t D0 = load_scalar(a.D_off + t);
+  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
+  if (!table_ok(ty, D, a.served)) {  // block-uniform
+    // No launch of the call serves this table (a type byte outside the
+    // served types, or codes that do not fill whole bytes): one launch, the
+    // call's first, writes its bags' columns as zeros and reports it.
+    if (a.check) {
+      const int64_t c0 = D0 < 0 ? 0 : D0;
+      const int64_t c1 = static_cast<int64_t>(D0) + (D > 0 ? D : 0);
+      const int64_t nc = (c1 < a.total_D ? c1 : a.total_D) - c0;
+      for (int64_t e = threadIdx.x; nc > 0 && e < BPB * nc; e += kBlockThreads) {
+        const int64_t b = b0 + e / nc;
+        if (b >= a.B) break;  // bags ascend with e
+        const int64_t o = b * a.total_D + c0 + e % nc;
+        if (a.out_f16)
+          reinterpret_cast<__half*>(a.out)[o] = __float2half_rn(0.0f);
+        else
+          reinterpret_cast<float*>(a.out)[o] = 0.0f;
+      }
+      if (threadIdx.x == 0 && a.mailbox)
+        __hip_atomic_store(a.mailbox + MX_STATUS_NBIT_TABLE, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    return;
+  }
+  if (ty != TY) return;  // block-uniform
   // A wave lasts as long as its longest bag: the block ranks its BPB bags by
   // length (longest first, ties by position) and wave w takes ranks
   // [w*P, w*P + P), so bags of similar length share a wave.  Each bag still
@@ -494,8 +533,6 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
   const int k = lane % G;
-  const int32_t D0 = load_scalar(a.D_off + t);
-  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
   const int64_t stride = row_bytes_of(ty, D, a.row_align);
   const uint8_t* __restrict__ Wt = a.W + load_scalar(a.w_off + t);
   const int i = s_bag[(threadIdx.x >> 6) * P + g];
@@ -607,12 +644,25 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   a.pooling = pooling_mode;
   a.row_align = row_alignment;
   a.out_f16 = output_dtype == MX_SPARSE_FP16;
+  a.served = (max_int8_D > 0 ? 1 << MX_SPARSE_INT8 : 0) | (max_int4_D > 0 ? 1 << MX_SPARSE_INT4 : 0) |
+             (max_int2_D > 0 ? 1 << MX_SPARSE_INT2 : 0) |
+             (max_float16_D > 0 ? 1 << MX_SPARSE_FP16 : 0) |
+             (max_float32_D > 0 ? 1 << MX_SPARSE_FP32 : 0);
+  a.check = 1;  // the first launch; cleared after it
+  a.mailbox = status_mailbox();
   auto* s = as_stream(stream);
   // Tables of a type whose max_*_D is 0 are not served (the upstream contract:
-  // the maxima describe the tables).
+  // the maxima describe the tables); the first launch zeroes their columns and
+  // reports them, and so it does for INT4/INT2 tables whose D leaves a partial
+  // byte.  With no type to launch, the FP32 instance runs for that alone.
+  if (a.served == 0) return launch_nbit<8, 16, MX_SPARSE_FP32>(a, index_bytes, s);
   if (int rc = launch_type<MX_SPARSE_INT8>(a, max_int8_D, index_bytes, s)) return rc;
+  if (max_int8_D > 0) a.check = 0;
   if (int rc = launch_type<MX_SPARSE_INT4>(a, max_int4_D, index_bytes, s)) return rc;
+  if (max_int4_D > 0) a.check = 0;
   if (int rc = launch_type<MX_SPARSE_INT2>(a, max_int2_D, index_bytes, s)) return rc;
+  if (max_int2_D > 0) a.check = 0;
   if (int rc = launch_type<MX_SPARSE_FP16>(a, max_float16_D, index_bytes, s)) return rc;
+  if (max_float16_D > 0) a.check = 0;
   return launch_type<MX_SPARSE_FP32>(a, max_float32_D, index_bytes, s);
 }

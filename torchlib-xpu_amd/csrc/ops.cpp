@@ -69,14 +69,15 @@ void check_arg(const Tensor& t, const Tensor& like, const char* name, bool dense
 // The kernels report a look-back wait that exhausted its bound (never
 // expected) by storing 1 in a host-visible word registered for the device;
 // the call's later kernels then leave its outputs (run layout, weights,
-// momentum) alone.  One pinned word per device is registered on the first
-// backward or transpose on that device outside graph capture; every such op
-// reads it first (a host read, no synchronisation) and raises if an earlier
-// call failed.
+// momentum) alone.  The nbit lookup reports a table it cannot serve (its
+// columns written as zeros) in a second word.  The pinned words of a device
+// are registered on the first backward, transpose or nbit lookup on that
+// device outside graph capture; every such op reads them first (a host read,
+// no synchronisation) and raises if an earlier call failed.
 
 struct Mailboxes {
   std::mutex mu;
-  std::array<Tensor, 64> word;  // int32 [1], pinned host memory
+  std::array<Tensor, 64> word;  // int32 [MX_STATUS_WORDS], pinned host memory
 };
 
 Mailboxes& mailboxes() {
@@ -90,16 +91,26 @@ int32_t* mailbox_of(int dev) {
   return m.word[dev].defined() ? m.word[dev].data_ptr<int32_t>() : nullptr;
 }
 
-// Raises if a look-back of an earlier call on `dev` gave up (the word is
-// cleared, so the failure is reported once).
+// Raises if a look-back of an earlier call on `dev` gave up, or an earlier
+// nbit lookup met a table it could not serve (the word is cleared, so each
+// failure is reported once).
 void raise_if_lookback_failed(int dev) {
   int32_t* p = mailbox_of(dev);
-  if (p == nullptr || __atomic_load_n(p, __ATOMIC_ACQUIRE) == 0) return;
-  __atomic_store_n(p, 0, __ATOMIC_RELAXED);
-  TORCH_CHECK(false, "an earlier TBE backward or transpose_embedding_input on cuda:", dev,
-              " gave up a look-back wait in its sort or scan, so it left its outputs (sorted "
-              "indices and run layout, or the weight and momentum update) unwritten; that step "
-              "has to be run again");
+  if (p == nullptr) return;
+  if (__atomic_load_n(p + MX_STATUS_LOOKBACK, __ATOMIC_ACQUIRE) != 0) {
+    __atomic_store_n(p + MX_STATUS_LOOKBACK, 0, __ATOMIC_RELAXED);
+    TORCH_CHECK(false, "an earlier TBE backward or transpose_embedding_input on cuda:", dev,
+                " gave up a look-back wait in its sort or scan, so it left its outputs (sorted "
+                "indices and run layout, or the weight and momentum update) unwritten; that "
+                "step has to be run again");
+  }
+  if (__atomic_load_n(p + MX_STATUS_NBIT_TABLE, __ATOMIC_ACQUIRE) != 0) {
+    __atomic_store_n(p + MX_STATUS_NBIT_TABLE, 0, __ATOMIC_RELAXED);
+    TORCH_CHECK(false, "an earlier int_nbit_split_embedding_codegen_lookup_function on cuda:",
+                dev, " met a table it cannot serve (a weights_tys byte naming no type whose "
+                "max_*_D is positive, or an INT4 table of odd D or an INT2 table of D not a "
+                "multiple of 4) and wrote that table's output columns as zeros");
+  }
 }
 
 // Registers the device's mailbox (the caller holds a device guard for it).
@@ -112,7 +123,7 @@ void ensure_mailbox(int dev, void* stream) {
   if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) != hipSuccess ||
       cs != hipStreamCaptureStatusNone)
     return;
-  Tensor w = at::zeros({1}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+  Tensor w = at::zeros({MX_STATUS_WORDS}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
   auto& m = mailboxes();
   std::lock_guard<std::mutex> lock(m.mu);
   if (m.word[dev].defined()) return;
@@ -128,8 +139,8 @@ int64_t pending_lookback_faults(int64_t device) {
   TORCH_CHECK(hipDeviceSynchronize() == hipSuccess, "hipDeviceSynchronize failed");
   int32_t* p = mailbox_of(static_cast<int>(device));
   if (p == nullptr) return 0;
-  const int32_t v = __atomic_load_n(p, __ATOMIC_ACQUIRE);
-  __atomic_store_n(p, 0, __ATOMIC_RELAXED);
+  const int32_t v = __atomic_load_n(p + MX_STATUS_LOOKBACK, __ATOMIC_ACQUIRE);
+  __atomic_store_n(p + MX_STATUS_LOOKBACK, 0, __ATOMIC_RELAXED);
   return v;
 }
 
@@ -706,7 +717,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   auto o32 = indices.options().dtype(at::kInt);
   Tensor linear = at::empty({N}, o64), sorted = at::empty({N}, o64);
   Tensor infos = at::empty({N}, o32), run = at::empty({N}, o64);
-  // Every entry of lengths and cum is written (past num_runs: 0 and N).
+  // Every entry of lengths and cum is written (past num_runs: 0 and N; all 0
+  // when a look-back of the call gave up).
   Tensor lengths = at::empty({N}, o32), num_runs = at::zeros({1}, o32);
   Tensor cum = at::empty({N + 1}, o32);
   const size_t ws_bytes = mx_tbe_transpose_workspace_bytes(N, total_hash_size_bits);
@@ -1424,11 +1436,15 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   const float* iw = nullptr;
   Tensor iwc;
   if (indice_weights.has_value() && indice_weights->defined()) {
-    check_gpu(*indice_weights, "indice_weights");
+    check_arg(*indice_weights, dev_weights, "indice_weights", false);
     TORCH_CHECK(indice_weights->scalar_type() == at::kFloat, "indice_weights must be fp32");
+    TORCH_CHECK(indice_weights->numel() == indices.numel(),
+                "indice_weights must have one entry per index (", indices.numel(), "), got ",
+                indice_weights->numel());
     iwc = indice_weights->contiguous();
     iw = iwc.data_ptr<float>();
   }
+  ensure_mailbox(dev_weights.device().index(), stream_of(dev_weights));
   auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
   Tensor out = at::empty({B, total_D}, opts);
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();

@@ -86,16 +86,20 @@ __device__ __forceinline__ int64_t eff_len(int64_t n, const int32_t* n_dev) {
 // the true ones, so the stores made before the check stay in bounds.
 struct Faults {
   unsigned int* fail;
-  unsigned int* mailbox;  // may be null
+  unsigned int* mailbox;  // the device's MX_STATUS_WORDS host-visible words, may be null
   int spin_limit;         // > 0: spins before giving up; < 0: give up at once (test hook)
 };
 
 __device__ __forceinline__ void report_fault(const Faults& f) {
   __hip_atomic_store(f.fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (f.mailbox) __hip_atomic_store(f.mailbox, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (f.mailbox)
+    __hip_atomic_store(f.mailbox + MX_STATUS_LOOKBACK, 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// True when an earlier kernel of the call gave up (block-uniform).
+// True when a kernel of the call gave up.  Uniform across a block only when
+// the word was set by an earlier launch; a kernel whose own tiles may set it
+// reads it once per block (one thread, broadcast through LDS).
 __device__ __forceinline__ bool call_failed(const unsigned int* fail) {
   return fail != nullptr &&
          __hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
@@ -128,13 +132,18 @@ __global__ void __launch_bounds__(kScanThreads)
                         int64_t ntiles) {
   (void)ntiles;
   __shared__ uint32_t s_tile, s_prefix;
-  __shared__ bool s_gave_up;
-  if (call_failed(st.faults.fail)) return;  // the input of this scan is not valid
+  __shared__ bool s_gave_up, s_failed;
+  // One thread reads the failure word and takes the ticket, so that every
+  // wave of the block sees the same answer: another tile of this launch may
+  // set the word while the block starts.  A block that finds the call failed
+  // takes no ticket; every tile that took one publishes, so no tile waits on it.
   if (threadIdx.x == 0) {
-    s_tile = atomicAdd(st.ticket, 1u);
+    s_failed = call_failed(st.faults.fail);  // the input of this scan is not valid
+    if (!s_failed) s_tile = atomicAdd(st.ticket, 1u);
     s_gave_up = false;
   }
   __syncthreads();
+  if (s_failed) return;  // block-uniform
   const int64_t tile = s_tile;
   const int64_t m = eff_len(n, n_dev);
   // Tiles past the effective length hold only identities: they return at once

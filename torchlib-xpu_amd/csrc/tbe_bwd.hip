@@ -418,14 +418,23 @@ __device__ __forceinline__ void sweep_tile(
     const uint32_t* __restrict__ ghist, SW* status, unsigned int* ticket, const Faults& faults,
     uint32_t* __restrict__ keys_out, int64_t* __restrict__ keys_out64,
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, const SegSort& seg,
-    int64_t lane_fpos, int32_t lane_tp, unsigned int& s_tile,
+    int64_t lane_fpos, int32_t lane_tp, unsigned int& s_tile, unsigned int& s_stop,
     uint32_t (&cnt)[kSweepWaves][kRadix], uint32_t (&s_base)[kRadix],
     uint32_t (&s_wsum)[kRadix / 64]) {
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (threadIdx.x == 0) s_tile = atomicAdd(ticket, 1u);
+  // One thread reads the failure word and takes the ticket, so the whole
+  // block agrees (a tile of this launch may set the word while the block
+  // starts).  A block of a failed call takes no ticket: every tile that took
+  // one publishes, so no tile waits on it.  s_stop is 1 from here on when the
+  // block must not scatter (failed call, or a give-up in the digit phase).
+  if (threadIdx.x == 0) {
+    s_stop = call_failed(faults.fail) ? 1u : 0u;  // an earlier pass gave up: nothing valid to sort
+    if (s_stop == 0u) s_tile = atomicAdd(ticket, 1u);
+  }
   for (int i = threadIdx.x; i < kSweepWaves * kRadix; i += kSweepThreads) (&cnt[0][0])[i] = 0u;
   __syncthreads();
+  if (s_stop != 0u) return;  // block-uniform
   const int64_t tile = s_tile;
   // The tile's positions [pbeg, pend) and the first tile of its look-back
   // chain: its feature's first tile (segments), or tile 0.  Tiles past the
@@ -540,6 +549,7 @@ __device__ __forceinline__ void sweep_tile(
         bool done = false;
         if (faults.spin_limit < 0) {  // test hook: give up at once
           report_fault(faults);
+          s_stop = 1u;
           done = true;
         }
         while (!done) {
@@ -563,6 +573,7 @@ __device__ __forceinline__ void sweep_tile(
           if (!done && folded < kLookBack) {     // waiting on an unpublished predecessor
             if (!keep_waiting(spins, faults)) {  // never expected; keeps the wait bounded
               report_fault(faults);
+              s_stop = 1u;
               break;
             }
           }
@@ -574,12 +585,15 @@ __device__ __forceinline__ void sweep_tile(
     s_base[d] = goff + prefix;
   }
   __syncthreads();
+  // A give-up published a partial prefix (so later tiles end their waits) and
+  // the call is marked failed: the tile writes nothing.
+  if (s_stop != 0u) return;  // block-uniform
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
     if (i0 + it * 64 >= pend) continue;
     const uint32_t dd = (k[it] >> shift) & mask;
     const uint32_t pos = s_base[dd] + cnt[w][dd] + rank[it];
-    if (pos >= n) continue;  // never, unless a look-back gave up; keeps stores in bounds
+    if (pos >= n) continue;  // never; keeps stores in bounds whatever the counts
     if constexpr (LAST)
       keys_out64[pos] = static_cast<int64_t>(k[it]);
     else
@@ -597,7 +611,7 @@ __global__ void __launch_bounds__(kSweepThreads)
                     unsigned int* ticket, Faults faults, uint32_t* __restrict__ keys_out,
                     int64_t* __restrict__ keys_out64, uint32_t* __restrict__ vals_out,
                     uint32_t* __restrict__ vals2_out, SegSort seg) {
-  __shared__ unsigned int s_tile;
+  __shared__ unsigned int s_tile, s_stop;
   __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
   __shared__ uint32_t s_base[kRadix];
   __shared__ uint32_t s_wsum[kRadix / 64];
@@ -614,19 +628,18 @@ __global__ void __launch_bounds__(kSweepThreads)
     lane_fpos = seg.fpos[lane];
     lane_tp = seg.tprefix[lane];
   }
-  if (call_failed(faults.fail)) return;  // an earlier pass gave up: nothing valid to sort
   if (why == 0u)  // grid-uniform
     sweep_tile<kTileSeg, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                    faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                   lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
+                                   lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
   else if (why == kSegKeys)
     sweep_tile<kTileKeys, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                     faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                    lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
+                                    lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
   else
     sweep_tile<kTileGlobal, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                       faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                      lane_fpos, lane_tp, s_tile, cnt, s_base, s_wsum);
+                                      lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
 }
 
 // One sort pass over a workspace whose status words are of type SW.
@@ -695,12 +708,24 @@ struct RleEpi {
 // run_lengths[r] = cum[r+1] - cum[r] for the num_runs runs; past them the
 // arrays read as the complete cumsum of zero-padded lengths: run_lengths 0,
 // cum N.  (Threads r >= m write cum[r+1] > m, threads r < m read cum[<= m]:
-// no overlap.)
+// no overlap.)  When a look-back of the call gave up, the runs were never
+// counted: the outputs become an empty layout (no runs, lengths 0, cum 0).
 __global__ void __launch_bounds__(256)
     run_lengths_kernel(int32_t* __restrict__ cum, const uint32_t* __restrict__ num_runs,
-                       int64_t n, int32_t* __restrict__ lengths, const unsigned int* fail) {
-  if (call_failed(fail)) return;  // num_runs was never written
+                       int64_t n, int32_t* __restrict__ lengths, int32_t* num_runs_out,
+                       const unsigned int* fail) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (call_failed(fail)) {  // set before this launch: the same for every thread
+    if (r == 0) {
+      cum[0] = 0;
+      if (num_runs_out) *num_runs_out = 0;
+    }
+    if (r < n) {
+      lengths[r] = 0;
+      cum[r + 1] = 0;
+    }
+    return;
+  }
   const int64_t m = *num_runs;
   if (r >= n) return;
   if (r < m) {
@@ -941,7 +966,8 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
                                scan_slot(w, 0), s))
     return rc;
   if (o.run_lengths) {
-    run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths, w.fail);
+    run_lengths_kernel<<<g256, 256, 0, s>>>(o.cum, &w.counters[0], N, o.run_lengths,
+                                            o.num_runs, w.fail);
     MX_LAUNCH_CHECK();
   }
   return MX_OK;
