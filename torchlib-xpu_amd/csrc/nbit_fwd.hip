@@ -48,17 +48,24 @@ struct NbitArgs {
   int32_t row_align;
   int32_t out_f16;
   int32_t served;          // bit ty set: the call launches type ty
-  int32_t check;           // this launch zeroes and reports tables no launch can serve
+  uint32_t nchk;           // trailing blocks that check the tables (T in the first launch, else 0)
   unsigned int* mailbox;   // host-visible status words of the device, may be null
 };
 
 // A table the call can serve: its type has a launch, its D is not negative,
 // and its codes fill whole bytes (INT4: D even, INT2: D a multiple of 4; the
 // row holds D*bits/8 code bytes, rounded down).
+template <int TY>
+__device__ __forceinline__ bool whole_bytes(int32_t D) {
+  if constexpr (TY == MX_SPARSE_INT4) return (D & 1) == 0;
+  if constexpr (TY == MX_SPARSE_INT2) return (D & 3) == 0;
+  return true;
+}
+
 __device__ __forceinline__ bool table_ok(int32_t ty, int32_t D, int32_t served) {
   if (ty < 0 || ty > MX_SPARSE_INT2 || ((served >> ty) & 1) == 0 || D < 0) return false;
-  if (ty == MX_SPARSE_INT4) return (D & 1) == 0;
-  if (ty == MX_SPARSE_INT2) return (D & 3) == 0;
+  if (ty == MX_SPARSE_INT4) return whole_bytes<MX_SPARSE_INT4>(D);
+  if (ty == MX_SPARSE_INT2) return whole_bytes<MX_SPARSE_INT2>(D);
   return true;
 }
 
@@ -459,6 +466,30 @@ __device__ __forceinline__ int32_t table_type(const uint8_t* tys, int64_t t) {
   return static_cast<int32_t>((w >> (8 * (addr & 3))) & 0xffu);
 }
 
+// Run by one block per table, appended to the call's first launch: a table
+// no launch of the call serves (a type byte outside the served types, or
+// codes that do not fill whole bytes) gets its columns of every bag written
+// as zeros, and the call reports it through the device's status words.
+__device__ __forceinline__ void check_table(const NbitArgs& a, int64_t t, int32_t ty) {
+  const int32_t D0 = load_scalar(a.D_off + t);
+  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
+  if (table_ok(ty, D, a.served)) return;
+  const int64_t c0 = D0 < 0 ? 0 : D0;
+  const int64_t c1 = static_cast<int64_t>(D0) + (D > 0 ? D : 0);
+  const int64_t nc = (c1 < a.total_D ? c1 : a.total_D) - c0;
+  for (int64_t b = 0; b < a.B; ++b)
+    for (int64_t c = threadIdx.x; c < nc; c += blockDim.x) {
+      const int64_t o = b * a.total_D + c0 + c;
+      if (a.out_f16)
+        reinterpret_cast<__half*>(a.out)[o] = __float2half_rn(0.0f);
+      else
+        reinterpret_cast<float*>(a.out)[o] = 0.0f;
+    }
+  if (threadIdx.x == 0 && a.mailbox)
+    __hip_atomic_store(a.mailbox + MX_STATUS_NBIT_TABLE, 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <typename I, int G, int MAXCPL, int TY>
 __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   constexpr int P = 64 / G;           // bags per wave
@@ -470,37 +501,20 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   // they hold their slot for a few hundred cycles.
   const uint32_t bpt = static_cast<uint32_t>(a.Bp / BPB);  // blocks per table
   const uint32_t tu = blockIdx.x / bpt;
-  if (tu >= static_cast<uint32_t>(a.T)) return;  // block-uniform
-  const int64_t t = tu;
-  const int32_t ty = table_type(a.tys, t);
-  if (ty != TY && !a.check) return;  // block-uniform
-  const int64_t b0 = static_cast<int64_t>(blockIdx.x - tu * bpt) * BPB;
-  const int32_t D0 = load_scalar(a.D_off + t);
-  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
-  if (!table_ok(ty, D, a.served)) {  // block-uniform
-    // No launch of the call serves this table (a type byte outside the
-    // served types, or codes that do not fill whole bytes): one launch, the
-    // call's first, writes its bags' columns as zeros and reports it.
-    if (a.check) {
-      const int64_t c0 = D0 < 0 ? 0 : D0;
-      const int64_t c1 = static_cast<int64_t>(D0) + (D > 0 ? D : 0);
-      const int64_t nc = (c1 < a.total_D ? c1 : a.total_D) - c0;
-      for (int64_t e = threadIdx.x; nc > 0 && e < BPB * nc; e += kBlockThreads) {
-        const int64_t b = b0 + e / nc;
-        if (b >= a.B) break;  // bags ascend with e
-        const int64_t o = b * a.total_D + c0 + e % nc;
-        if (a.out_f16)
-          reinterpret_cast<__half*>(a.out)[o] = __float2half_rn(0.0f);
-        else
-          reinterpret_cast<float*>(a.out)[o] = 0.0f;
-      }
-      if (threadIdx.x == 0 && a.mailbox)
-        __hip_atomic_store(a.mailbox + MX_STATUS_NBIT_TABLE, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_SYSTEM);
-    }
+  if (tu >= static_cast<uint32_t>(a.T)) {  // block-uniform
+    // The call's first launch ends with nchk = T blocks, one per table, that
+    // check the tables.  Config 5 per call, against no check: +2.5 us with
+    // the blocks here, +9.5 us with them first in the grid (every block then
+    // tests its index against nchk) or with the checks made by blocks that
+    // leave at the type test below (half the blocks of a two-type launch).
+    const int64_t tc = static_cast<int64_t>(blockIdx.x) - static_cast<int64_t>(a.T) * bpt;
+    if (tc < a.nchk) check_table(a, tc, table_type(a.tys, tc));
     return;
   }
+  const int64_t t = tu;
+  const int32_t ty = table_type(a.tys, t);
   if (ty != TY) return;  // block-uniform
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x - tu * bpt) * BPB;
   // A wave lasts as long as its longest bag: the block ranks its BPB bags by
   // length (longest first, ties by position) and wave w takes ranks
   // [w*P, w*P + P), so bags of similar length share a wave.  Each bag still
@@ -530,6 +544,10 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
     s_bag[rank] = i;
   }
   __syncthreads();
+  const int32_t D0 = load_scalar(a.D_off + t);
+  const int32_t D = load_scalar(a.D_off + t + 1) - D0;
+  // A table whose codes leave a partial byte is left to the check blocks.
+  if (!whole_bytes<TY>(D)) return;  // block-uniform
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
   const int k = lane % G;
@@ -539,6 +557,11 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   const int64_t b = b0 + i;
   if (b >= a.B) return;  // whole group idle (idle slots rank last); its lanes stay converged
   dispatch_cpl<I, G, MAXCPL, TY>(a, D, Wt, stride, s_start[i], s_end[i], b * a.total_D + D0, g, k);
+}
+
+// The check blocks alone, for a call that launches no type.
+__global__ void __launch_bounds__(kBlockThreads) nbit_check_kernel(NbitArgs a) {
+  check_table(a, blockIdx.x, table_type(a.tys, blockIdx.x));
 }
 
 template <typename I, int G, int MAXCPL, int TY>
@@ -560,7 +583,7 @@ int launch_nbit(NbitArgs a, int32_t index_bytes, hipStream_t s) {
   constexpr int BPB = kWpb * (64 / G);  // bags per block
   a.Bp = ceil_div(a.B, BPB) * BPB;      // every block within one table
   a.nwaves = static_cast<int64_t>(a.T) * (a.Bp / BPB) * kWpb;
-  const int64_t grid = ceil_div(a.nwaves, kWpb);
+  const int64_t grid = ceil_div(a.nwaves, kWpb) + a.nchk;  // + the check blocks
   MX_REQUIRE(grid <= 0x7fffffffll, "too many bags");
   const dim3 gd(static_cast<uint32_t>(grid));
   if constexpr (TY == MX_SPARSE_INT4) {
@@ -648,21 +671,25 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
              (max_int2_D > 0 ? 1 << MX_SPARSE_INT2 : 0) |
              (max_float16_D > 0 ? 1 << MX_SPARSE_FP16 : 0) |
              (max_float32_D > 0 ? 1 << MX_SPARSE_FP32 : 0);
-  a.check = 1;  // the first launch; cleared after it
+  a.nchk = static_cast<uint32_t>(T);  // the first launch checks the tables
   a.mailbox = status_mailbox();
   auto* s = as_stream(stream);
   // Tables of a type whose max_*_D is 0 are not served (the upstream contract:
-  // the maxima describe the tables); the first launch zeroes their columns and
-  // reports them, and so it does for INT4/INT2 tables whose D leaves a partial
-  // byte.  With no type to launch, the FP32 instance runs for that alone.
-  if (a.served == 0) return launch_nbit<8, 16, MX_SPARSE_FP32>(a, index_bytes, s);
+  // the maxima describe the tables); the first launch's check blocks zero their
+  // columns and report them, and so they do for INT4/INT2 tables whose D
+  // leaves a partial byte.  With no type to launch, the check blocks run alone.
+  if (a.served == 0) {
+    nbit_check_kernel<<<dim3(static_cast<uint32_t>(T)), kBlockThreads, 0, s>>>(a);
+    MX_LAUNCH_CHECK();
+    return MX_OK;
+  }
   if (int rc = launch_type<MX_SPARSE_INT8>(a, max_int8_D, index_bytes, s)) return rc;
-  if (max_int8_D > 0) a.check = 0;
+  if (max_int8_D > 0) a.nchk = 0;
   if (int rc = launch_type<MX_SPARSE_INT4>(a, max_int4_D, index_bytes, s)) return rc;
-  if (max_int4_D > 0) a.check = 0;
+  if (max_int4_D > 0) a.nchk = 0;
   if (int rc = launch_type<MX_SPARSE_INT2>(a, max_int2_D, index_bytes, s)) return rc;
-  if (max_int2_D > 0) a.check = 0;
+  if (max_int2_D > 0) a.nchk = 0;
   if (int rc = launch_type<MX_SPARSE_FP16>(a, max_float16_D, index_bytes, s)) return rc;
-  if (max_float16_D > 0) a.check = 0;
+  if (max_float16_D > 0) a.nchk = 0;
   return launch_type<MX_SPARSE_FP32>(a, max_float32_D, index_bytes, s);
 }
