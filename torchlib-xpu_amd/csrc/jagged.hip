@@ -414,12 +414,12 @@ extern "C" int mx_jagged_to_padded_dense(const void* values, int64_t elem_bytes,
   uint8_t pat[16];  // padding pattern replicated over a 16-byte chunk
   for (int i = 0; i < 16; ++i) pat[i] = static_cast<uint8_t>(pad_bits >> (8 * (i % elem_bytes)));
   const int64_t vpr = row_bytes / vec;
-  const int grid = grid_for(rows * vpr);
   auto* s = as_stream(stream);
   const auto* v = static_cast<const uint8_t*>(values);
   auto* o = static_cast<uint8_t*>(out);
   const int64_t nbags = offsets_numel[0] - 1;
   const bool one = num_jagged_dim == 1 && nbags <= 0x7fffffffll;
+  const int grid = one ? 0 : grid_for(rows * vpr);  // the one-dim grid is per bag
   MX_VEC_SWITCH(vec, {
     Chunk<V> pad;
     for (int i = 0; i < V; ++i) pad.b[i] = pat[i];
@@ -464,12 +464,12 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
   const int vec = vec0 < elem_bytes ? static_cast<int>(elem_bytes) : vec0;
   MX_REQUIRE(row_bytes % vec == 0, "misaligned tensors");
   const int64_t vpr = row_bytes / vec;
-  const int grid = grid_for(total_L * vpr);
   auto* s = as_stream(stream);
   const auto* d = static_cast<const uint8_t*>(dense);
   auto* o = static_cast<uint8_t*>(out);
   const int64_t nbags = offsets_numel[0] - 1;
   const bool one = num_jagged_dim == 1 && nbags < 0x7fffffffll;
+  const int grid = one ? 0 : grid_for(total_L * vpr);  // the one-dim grid is per bag
   const dim3 g1 = grid_1d(nbags + 1, max_lengths[0] * vpr);
   const int64_t L0 = max_lengths[0];
   if (x_values == nullptr) {

@@ -203,30 +203,36 @@ uint64_t pad_bits_of(double pad, at::ScalarType st) {
   return bits;
 }
 
+// The offsets of a jagged op as the C-ABI takes them, on the stack (no heap
+// allocation per call); contiguous offsets are used in place, others through
+// a contiguous copy kept here.
 struct OffsetsPack {
-  std::vector<Tensor> keep;
-  std::vector<const void*> ptrs;
-  std::vector<int64_t> numel;
+  std::array<Tensor, MX_MAX_JAGGED_DIM> keep;
+  std::array<const void*, MX_MAX_JAGGED_DIM> ptrs{};
+  std::array<int64_t, MX_MAX_JAGGED_DIM> numel{};
   int32_t bytes = 8;
 };
 
-OffsetsPack pack_offsets(const std::vector<Tensor>& offsets, const Tensor& like) {
+void pack_offsets(const std::vector<Tensor>& offsets, const Tensor& like, OffsetsPack& p) {
   TORCH_CHECK(!offsets.empty(), "offsets must hold at least one tensor");
   TORCH_CHECK(offsets.size() <= MX_MAX_JAGGED_DIM, "at most ", MX_MAX_JAGGED_DIM,
               " jagged dimensions are supported, got ", offsets.size());
-  OffsetsPack p;
   p.bytes = index_bytes_of(offsets[0], "offsets");
-  for (const auto& o : offsets) {
+  for (size_t k = 0; k < offsets.size(); ++k) {
+    const Tensor& o = offsets[k];
     check_gpu(o, "offsets");
     check_same_device(like, o, "offsets");
     TORCH_CHECK(o.dim() == 1, "offsets must be 1-D");
     TORCH_CHECK(index_bytes_of(o, "offsets") == p.bytes, "all offsets must share one dtype");
     TORCH_CHECK(o.numel() >= 1, "offsets must not be empty");
-    p.keep.push_back(o.contiguous());
-    p.ptrs.push_back(p.keep.back().data_ptr());
-    p.numel.push_back(o.numel());
+    if (o.is_contiguous()) {
+      p.ptrs[k] = o.data_ptr();
+    } else {
+      p.keep[k] = o.contiguous();
+      p.ptrs[k] = p.keep[k].data_ptr();
+    }
+    p.numel[k] = o.numel();
   }
-  return p;
 }
 
 Tensor jagged_to_padded_dense_forward(const Tensor& values, const std::vector<Tensor>& offsets,
@@ -237,10 +243,12 @@ Tensor jagged_to_padded_dense_forward(const Tensor& values, const std::vector<Te
   TORCH_CHECK(max_lengths.size() == offsets.size(), "max_lengths has ", max_lengths.size(),
               " entries but there are ", offsets.size(), " offsets");
   TORCH_CHECK(values.dim() >= 1, "values must have at least one dimension");
-  OffsetsPack p = pack_offsets(offsets, values);
-  const Tensor v = values.contiguous();
+  OffsetsPack p;
+  pack_offsets(offsets, values, p);
+  const c10::MaybeOwned<Tensor> vm = values.expect_contiguous();
+  const Tensor& v = *vm;
   const int64_t inner_elems = v.dim() == 1 ? 1 : c10::multiply_integers(v.sizes().slice(1));
-  std::vector<int64_t> shape{p.numel[0] - 1};
+  at::DimVector shape{p.numel[0] - 1};
   for (auto m : max_lengths) shape.push_back(m);
   for (int64_t d = 1; d < v.dim(); ++d) shape.push_back(v.size(d));
   Tensor out = at::empty(shape, v.options());
@@ -260,16 +268,18 @@ Tensor dense_to_jagged_forward(const Tensor& dense, const std::vector<Tensor>& o
   c10::OptionalDeviceGuard guard(dense.device());
   const int64_t nd = static_cast<int64_t>(offsets.size());
   TORCH_CHECK(dense.dim() >= 1 + nd, "dense must have at least ", 1 + nd, " dimensions");
-  OffsetsPack p = pack_offsets(offsets, dense);
+  OffsetsPack p;
+  pack_offsets(offsets, dense, p);
   TORCH_CHECK(dense.size(0) == p.numel[0] - 1, "dense has ", dense.size(0),
               " rows but offsets describe ", p.numel[0] - 1);
-  const Tensor d = dense.contiguous();
-  std::vector<int64_t> max_lengths;
-  for (int64_t k = 0; k < nd; ++k) max_lengths.push_back(d.size(1 + k));
+  const c10::MaybeOwned<Tensor> dm = dense.expect_contiguous();
+  const Tensor& d = *dm;
+  std::array<int64_t, MX_MAX_JAGGED_DIM> max_lengths{};
+  for (int64_t k = 0; k < nd; ++k) max_lengths[k] = d.size(1 + k);
   const int64_t total_L =
-      total_L_sym.has_value() ? total_L_sym->expect_int() : last_offset(p.keep.back());
+      total_L_sym.has_value() ? total_L_sym->expect_int() : last_offset(offsets.back());
   TORCH_CHECK(total_L >= 0, "total_L must be non-negative");
-  std::vector<int64_t> shape{total_L};
+  at::DimVector shape{total_L};
   int64_t inner = 1;
   for (int64_t k = 1 + nd; k < d.dim(); ++k) {
     shape.push_back(d.size(k));
@@ -293,13 +303,16 @@ Tensor jagged_dense_add_forward(const Tensor& x_values, const std::vector<Tensor
   TORCH_CHECK(dt >= 0, "dtype ", x_values.scalar_type(), " is not supported");
   const int64_t nd = static_cast<int64_t>(offsets.size());
   TORCH_CHECK(y.dim() >= 1 + nd, "y must have at least ", 1 + nd, " dimensions");
-  OffsetsPack p = pack_offsets(offsets, x_values);
+  OffsetsPack p;
+  pack_offsets(offsets, x_values, p);
   TORCH_CHECK(y.size(0) == p.numel[0] - 1, "y has ", y.size(0), " rows but offsets describe ",
               p.numel[0] - 1);
-  const Tensor x = x_values.contiguous();
-  const Tensor yc = y.contiguous();
-  std::vector<int64_t> max_lengths;
-  for (int64_t k = 0; k < nd; ++k) max_lengths.push_back(yc.size(1 + k));
+  const c10::MaybeOwned<Tensor> xm = x_values.expect_contiguous();
+  const c10::MaybeOwned<Tensor> ym = y.expect_contiguous();
+  const Tensor& x = *xm;
+  const Tensor& yc = *ym;
+  std::array<int64_t, MX_MAX_JAGGED_DIM> max_lengths{};
+  for (int64_t k = 0; k < nd; ++k) max_lengths[k] = yc.size(1 + k);
   int64_t inner = 1;
   for (int64_t k = 1 + nd; k < yc.dim(); ++k) inner *= yc.size(k);
   const int64_t x_inner = x.dim() == 1 ? 1 : c10::multiply_integers(x.sizes().slice(1));
