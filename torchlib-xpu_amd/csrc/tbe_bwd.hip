@@ -562,7 +562,7 @@ __device__ __forceinline__ void sweep_tile(
           int folded = 0;
 #pragma unroll
           for (int q = 0; q < kLookBack; ++q) {
-            if (done || folded < q) continue;  // stopped earlier in this round
+            if (done || folded < q) continue;  // stopped at an earlier predecessor of these loads
             const SW flag = x[q] >> Word::kFlagShift;
             if (flag == 0) continue;
             prefix += static_cast<uint32_t>(x[q] & Word::kValue);
