@@ -120,6 +120,74 @@ def test_transpose_feature_segments(dev, T):
     _check_transpose(dev, inp, torch.int32)
 
 
+def _bag_input(rng, E, idx, B):
+    """One table of E rows whose B bags hold the indices idx in a random order."""
+    idx = rng.permutation(np.asarray(idx, dtype=np.int64))
+    cuts = np.sort(rng.integers(0, idx.size + 1, size=B - 1))
+    off = np.concatenate([[0], cuts, [idx.size]]).astype(np.int64)
+    return bench_inputs.TbeInput(T=1, E=[E], D=[4], B=B, indices=idx, offsets=off)
+
+
+def test_transpose_concentrated_keys(dev):
+    """16-bit keys, two thirds of them within one 256-key range (one value of
+    the second radix digit): the passes' digit counts are far from uniform,
+    the layout stays bit-exact."""
+    print("[case] transpose, 16384 of 25384 keys in [0, 256)", flush=True)
+    rng = np.random.default_rng(16384)
+    E = 1 << 16
+    idx = np.concatenate([rng.integers(0, 256, size=16384), rng.integers(256, E, size=9000)])
+    inp = _bag_input(rng, E, idx, 1500)
+    _check_transpose(dev, inp)
+    _check_transpose(dev, inp, torch.int32)
+
+
+@pytest.mark.parametrize("E", [1 << 24, (1 << 24) + 1])
+def test_transpose_key_bits_24_and_25(dev, E):
+    """24 key bits sort in three 8-bit passes, 25 in four (the widest
+    histogram slot)."""
+    print(f"[case] transpose, E={E}", flush=True)
+    rng = np.random.default_rng(E % 1000)
+    inp = _bag_input(rng, E, rng.integers(0, E, size=60000), 3000)
+    assert inp.total_hash_size_bits == (24 if E == 1 << 24 else 25)
+    _check_transpose(dev, inp)
+
+
+def _zipf_batch(rng, T, B, E, D, max_L, permute):
+    """Zipf(1.05) indices; without the per-table row permutation each table's
+    first rows are its hot ones (frequency-ordered ids)."""
+    lengths = rng.integers(1, max_L + 1, size=T * B)
+    off = bench_inputs.offsets_from_lengths(lengths)
+    parts = []
+    for t in range(T):
+        z = bench_inputs.bounded_zipf(rng, E, 1.05, int(off[(t + 1) * B] - off[t * B]))
+        parts.append(rng.permutation(E)[z] if permute else z)
+    return bench_inputs.TbeInput(T=T, E=[E] * T, D=[D] * T, B=B, indices=np.concatenate(parts),
+                                 offsets=off)
+
+
+@pytest.mark.parametrize("pooling", [0, 1])
+def test_unpermuted_zipf_batch(dev, pooling):
+    """Frequency-ordered ids: every table's hot rows are its first ones, so
+    most keys share their high digits.  Transpose bit-exact, backward against
+    the oracle."""
+    print(f"[case] unpermuted Zipf batch pooling={pooling}", flush=True)
+    rng = np.random.default_rng(105 + pooling)
+    inp = _zipf_batch(rng, 2, 2048, 200_000, 64, 40, permute=False)
+    _check_transpose(dev, inp)
+    _backward_case(dev, inp, pooling, seed=7)
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_permuted_zipf_backward(dev, weighted):
+    """A permuted Zipf batch of three tables: transpose bit-exact and the
+    backward, weighted or not, against the oracle."""
+    print(f"[case] permuted Zipf batch weighted={weighted}", flush=True)
+    rng = np.random.default_rng(41 + weighted)
+    inp = _zipf_batch(rng, 3, 2048, 200_000, 64, 40, permute=True)
+    _check_transpose(dev, inp)
+    _backward_case(dev, inp, 0, seed=9, weighted=weighted)
+
+
 @pytest.mark.parametrize("T,B,rows,max_L,dup", [
     (3, 50, [10, 1000, 70000], 20, False),
     (2, 300, [5000, 5000], 40, True),
@@ -193,6 +261,18 @@ def test_backward_rowwise_adagrad(dev, pooling, T, B, dims, rows, max_L, dup):
     rng = np.random.default_rng(B + T)
     inp = random_tbe(rng, T, B, dims, rows, max_L, dup_heavy=dup)
     _backward_case(dev, inp, pooling, seed=B)
+
+
+@pytest.mark.parametrize("D", [64, 256, 512, 1024])
+@pytest.mark.parametrize("pooling,weighted", [(0, False), (1, False), (0, True)])
+def test_backward_full_width(dev, D, pooling, weighted):
+    """Every table of width D (the kernels' full-width instances, whose rows
+    have no partial column chunks), with runs long enough for the chunked
+    path: against the oracle."""
+    print(f"[case] full-width backward D={D} pool={pooling} weighted={weighted}", flush=True)
+    rng = np.random.default_rng(D + pooling + 2 * weighted)
+    inp = random_tbe(rng, 3, 96, [D] * 3, [40, 3, 900], 40, dup_heavy=False)
+    _backward_case(dev, inp, pooling, seed=D, weighted=weighted)
 
 
 @pytest.mark.parametrize("pooling", [0, 1])
