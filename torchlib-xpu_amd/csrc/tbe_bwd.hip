@@ -1101,6 +1101,21 @@ __device__ __forceinline__ bool col_in(int c, int k, int32_t D) {
   return FULL || (c * G + k) * 4 < D;
 }
 
+// A plain instance serves the common call -- SUM pooling, no per-sample
+// weights, a fixed batch, no weight decay -- with those options as
+// constants, so every per-element test on them folds away (config 3: update
+// launch 66.7 -> 62.6 us, chunk sums 16.0 -> 14.5 us).
+template <bool PLAIN>
+__device__ __forceinline__ void pin_options(BwdArgs& a) {
+  if constexpr (PLAIN) {
+    a.pooling = MX_POOL_SUM;
+    a.iw_sorted = nullptr;
+    a.B_off = nullptr;
+    a.row_out = nullptr;
+    a.wd_mode = 0;
+  }
+}
+
 // Group-level (G lanes, lane k) sum of the (MEAN-scaled) gradient rows of
 // occurrences [s0, s1) of table t, in order.  Lane k owns columns
 // (c*G + k)*4 .. +4 for c < NCH.  Called with the whole group converged.
@@ -1360,8 +1375,9 @@ __device__ __forceinline__ void long_run_body(const BwdArgs& a, const MetaView& 
 }
 
 // Pass A: one group per chunk of a long run -> partial sum in the workspace.
-template <typename I, int G, int NCH, int U, bool FULL>
+template <typename I, int G, int NCH, int U, bool FULL, bool PLAIN>
 __global__ void __launch_bounds__(256) bwd_chunk_kernel(BwdArgs a) {
+  pin_options<PLAIN>(a);
   if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
   stage_meta(a, meta);
@@ -1453,9 +1469,11 @@ constexpr int runs_waves() {
   return NCH <= 2 ? 6 : 1;
 }
 
-template <typename I, typename WT, int G, int NCH, int U, int GL, int NCHL, int UL, bool FULL>
+template <typename I, typename WT, int G, int NCH, int U, int GL, int NCHL, int UL, bool FULL,
+          bool PLAIN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(runs_waves<NCH>())))
     bwd_runs_kernel(BwdArgs a, int64_t nlong) {
+  pin_options<PLAIN>(a);
   if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
   stage_meta(a, meta);
@@ -1468,7 +1486,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(runs_w
 
 // After the run encoding: the chunk layout of the long runs (chunk-count
 // scan), their chunk partial sums, then both run classes in one launch.
-template <typename I, typename WT, int G, int NCH, bool FULL>
+template <typename I, typename WT, int G, int NCH, bool FULL, bool PLAIN>
 int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
   if (int rc = prefix_scan_epi(
           ChunkCount{a.cum}, N, reinterpret_cast<const int32_t*>(a.num_runs),
@@ -1480,7 +1498,7 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
   const int64_t nblk = want < 1 ? 1 : (want > cus * 16 ? cus * 16 : want);
   const int64_t ngrid = ceil_div(nblk, 8) * 8;  // whole rounds over the XCDs
   constexpr int UC = NCH <= 1 ? 8 : (NCH <= 2 ? 8 : 4);  // chunks are full: more in flight
-  bwd_chunk_kernel<I, G, NCH, UC, FULL><<<dim3(static_cast<uint32_t>(ngrid)), 256, 0, s>>>(a);
+  bwd_chunk_kernel<I, G, NCH, UC, FULL, PLAIN><<<dim3(static_cast<uint32_t>(ngrid)), 256, 0, s>>>(a);
   MX_LAUNCH_CHECK();
   // Long runs: twice the lanes per row where the row allows (more groups
   // summing partials per block; measured 15.1 -> 12.4 us on config 3).
@@ -1490,7 +1508,7 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
   const int64_t long_want = ceil_div(max_chunks(N), kLongRange);
   const int64_t long_cap = cus * kLongBlocksPerCu;
   const int64_t nlong = ceil_div(long_want < long_cap ? long_want : long_cap, 8) * 8;
-  bwd_runs_kernel<I, WT, G, NCH, U, GL, NCHL, 4, FULL>
+  bwd_runs_kernel<I, WT, G, NCH, U, GL, NCHL, 4, FULL, PLAIN>
       <<<dim3(static_cast<uint32_t>(nlong + ngrid)), 256, 0, s>>>(a, nlong);
   MX_LAUNCH_CHECK();
   return MX_OK;
@@ -1498,14 +1516,20 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
 
 // Full-width instance when every table's D equals the row width of the
 // chosen (G, NCH): with a fixed batch, total_D = T * max_D says so (no D
-// exceeds max_D).
+// exceeds max_D, and grad_output's rows are D_offsets[T] wide).  Plain
+// instance for SUM pooling without weights or weight decay.
 template <typename I, typename WT, int G, int NCH>
 int launch_width(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
   constexpr int kWidth = G * NCH * 4;
   const bool full = a.B_off == nullptr && a.max_D == kWidth &&
                     a.total_D == static_cast<int64_t>(a.T) * kWidth;
-  return full ? launch_bwd<I, WT, G, NCH, true>(a, ws, chunk_start, N, s)
-              : launch_bwd<I, WT, G, NCH, false>(a, ws, chunk_start, N, s);
+  const bool plain = a.pooling == MX_POOL_SUM && a.iw_sorted == nullptr && a.B_off == nullptr &&
+                     a.wd_mode == 0;
+  if (full)
+    return plain ? launch_bwd<I, WT, G, NCH, true, true>(a, ws, chunk_start, N, s)
+                 : launch_bwd<I, WT, G, NCH, true, false>(a, ws, chunk_start, N, s);
+  return plain ? launch_bwd<I, WT, G, NCH, false, true>(a, ws, chunk_start, N, s)
+               : launch_bwd<I, WT, G, NCH, false, false>(a, ws, chunk_start, N, s);
 }
 
 // Lanes per run (G) and float4 chunks per lane (NCH) from the widest table.
