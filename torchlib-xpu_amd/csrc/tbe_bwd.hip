@@ -1141,7 +1141,9 @@ __device__ void group_sum_occurrences(const BwdArgs& a, const MetaView& mv, int3
       // rows (one run) but each has its own bags and gradient columns.
       const int64_t tj = table_of(a, info);
       const int64_t bag = a.B_off ? a.B_off[tj] + b : tj * a.B + b;
-      my_row = a.row_out ? a.row_out[bag] : b * a.total_D + mv.D_off(tj);
+      // Full width: every feature's columns start at tj * G*NCH*4 (config 3:
+      // chunk sums 14.5 -> 12.8 us against the table lookup).
+      my_row = a.row_out ? a.row_out[bag] : b * a.total_D + (FULL ? tj * (G * NCH * 4) : mv.D_off(tj));
       if (a.pooling == MX_POOL_MEAN) {
         const I* off = static_cast<const I*>(a.offsets);
         const int64_t L = static_cast<int64_t>(off[bag + 1]) - static_cast<int64_t>(off[bag]);
