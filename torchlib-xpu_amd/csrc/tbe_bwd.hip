@@ -411,6 +411,15 @@ struct SweepWord {
 // the code of a sort without segments (one body with both paths scheduled it
 // ~2 us per call slower).
 constexpr int kTileSeg = 0, kTileGlobal = 1, kTileKeys = 2;
+// A tile in digit order, staged in LDS between its ranking and its stores,
+// with the tile-local scan of its digit counts.
+struct SweepStage {
+  uint32_t k[kSweepTile];
+  uint32_t v[kSweepTile];
+  uint32_t v2[kSweepTile];
+  uint32_t tstart[kRadix];     // a digit's first position in the tile's digit order
+  uint32_t tsum[kRadix / 64];  // per-wave totals of the tile's digit counts
+};
 template <int MODE, bool LAST, typename SW>
 __device__ __forceinline__ void sweep_tile(
     const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals,
@@ -420,7 +429,7 @@ __device__ __forceinline__ void sweep_tile(
     uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, const SegSort& seg,
     int64_t lane_fpos, int32_t lane_tp, unsigned int& s_tile, unsigned int& s_stop,
     uint32_t (&cnt)[kSweepWaves][kRadix], uint32_t (&s_base)[kRadix],
-    uint32_t (&s_wsum)[kRadix / 64]) {
+    uint32_t (&s_wsum)[kRadix / 64], SweepStage& stg) {
   const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   // One thread reads the failure word and takes the ticket, so the whole
@@ -491,7 +500,7 @@ __device__ __forceinline__ void sweep_tile(
   const int d = threadIdx.x;
   const bool digit_wave = w < kRadix / 64;  // wave-uniform
   const bool used = digit_wave && d <= static_cast<int>(mask);  // same for every tile of the pass
-  uint32_t total = 0u, incl = 0u;
+  uint32_t total = 0u, incl = 0u, tincl = 0u;
   if (digit_wave) {
 #pragma unroll
     for (int x = 0; x < kSweepWaves; ++x) {  // per-wave counts -> per-wave prefixes
@@ -499,6 +508,8 @@ __device__ __forceinline__ void sweep_tile(
       cnt[x][d] = total;
       total += c;
     }
+    tincl = wave_incl_scan<SumOp>(total);  // the tile's digit counts: its local digit starts
+    if (lane == 63) stg.tsum[w] = tincl;
     uint32_t gcount = 0u;
     if constexpr (MODE == kTileSeg) {
       if (used)
@@ -530,6 +541,11 @@ __device__ __forceinline__ void sweep_tile(
     const uint32_t prev = __shfl_up(incl, 1, 64);
     if (lane != 0) goff += prev;
     if constexpr (MODE == kTileSeg) goff += static_cast<uint32_t>(fpos_f);  // the segment's first position
+    uint32_t tstart = tincl - total;  // the digit's first position in the tile's digit order
+#pragma unroll
+    for (int i = 0; i < kRadix / 64; ++i)
+      if (i < w) tstart += stg.tsum[i];
+    stg.tstart[d] = tstart;
     uint32_t prefix = 0u;
     if (used) {
       using Word = SweepWord<SW>;
@@ -582,24 +598,41 @@ __device__ __forceinline__ void sweep_tile(
                            __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    s_base[d] = goff + prefix;
+    // Global position of the digit's keys, less their first position in the
+    // tile's digit order (modulo 2^32).
+    s_base[d] = goff + prefix - tstart;
   }
   __syncthreads();
   // A give-up published a partial prefix (so later tiles end their waits) and
   // the call is marked failed: the tile writes nothing.
   if (s_stop != 0u) return;  // block-uniform
+  // The tile in digit order through LDS, then stored by consecutive threads:
+  // the keys of one digit land at consecutive addresses, so a wave's store is
+  // a few runs instead of 64 scattered words.
 #pragma unroll
   for (int it = 0; it < kSweepItems; ++it) {
     if (i0 + it * 64 >= pend) continue;
     const uint32_t dd = (k[it] >> shift) & mask;
-    const uint32_t pos = s_base[dd] + cnt[w][dd] + rank[it];
+    const uint32_t local = stg.tstart[dd] + cnt[w][dd] + rank[it];  // below the tile's size
+    stg.k[local] = k[it];
+    stg.v[local] = v[it];
+    if (vals2) stg.v2[local] = v2[it];
+  }
+  __syncthreads();
+  const int64_t tile_n = pend - pbeg;
+#pragma unroll
+  for (int it = 0; it < kSweepItems; ++it) {
+    const int64_t i = threadIdx.x + it * kSweepThreads;
+    if (i >= tile_n) continue;
+    const uint32_t kk = stg.k[i];
+    const uint32_t pos = s_base[(kk >> shift) & mask] + static_cast<uint32_t>(i);
     if (pos >= n) continue;  // never; keeps stores in bounds whatever the counts
     if constexpr (LAST)
-      keys_out64[pos] = static_cast<int64_t>(k[it]);
+      keys_out64[pos] = static_cast<int64_t>(kk);
     else
-      keys_out[pos] = k[it];
-    vals_out[pos] = v[it];
-    if (vals2) vals2_out[pos] = v2[it];
+      keys_out[pos] = kk;
+    vals_out[pos] = stg.v[i];
+    if (vals2) vals2_out[pos] = stg.v2[i];
   }
 }
 
@@ -615,6 +648,7 @@ __global__ void __launch_bounds__(kSweepThreads)
   __shared__ uint32_t cnt[kSweepWaves][kRadix];  // per-wave digit counts, then per-wave prefixes
   __shared__ uint32_t s_base[kRadix];
   __shared__ uint32_t s_wsum[kRadix / 64];
+  __shared__ SweepStage stg;
   const int lane = threadIdx.x & 63;
   // The segment state loads while the tile takes its ticket (neither depends
   // on the other): why the passes sort globally (0: they do not), and lane
@@ -631,15 +665,15 @@ __global__ void __launch_bounds__(kSweepThreads)
   if (why == 0u)  // grid-uniform
     sweep_tile<kTileSeg, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                    faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                   lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
+                                   lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum, stg);
   else if (why == kSegKeys)
     sweep_tile<kTileKeys, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                     faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                    lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
+                                    lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum, stg);
   else
     sweep_tile<kTileGlobal, LAST, SW>(keys, vals, vals2, n, shift, nbits, ghist, status, ticket,
                                       faults, keys_out, keys_out64, vals_out, vals2_out, seg,
-                                      lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum);
+                                      lane_fpos, lane_tp, s_tile, s_stop, cnt, s_base, s_wsum, stg);
 }
 
 // One sort pass over a workspace whose status words are of type SW.
