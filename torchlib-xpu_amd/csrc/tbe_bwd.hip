@@ -500,7 +500,7 @@ __device__ __forceinline__ void sweep_tile(
   const int d = threadIdx.x;
   const bool digit_wave = w < kRadix / 64;  // wave-uniform
   const bool used = digit_wave && d <= static_cast<int>(mask);  // same for every tile of the pass
-  uint32_t total = 0u, incl = 0u, tincl = 0u;
+  uint32_t total = 0u, incl = 0u, tincl = 0u, gcount = 0u;
   if (digit_wave) {
 #pragma unroll
     for (int x = 0; x < kSweepWaves; ++x) {  // per-wave counts -> per-wave prefixes
@@ -510,7 +510,6 @@ __device__ __forceinline__ void sweep_tile(
     }
     tincl = wave_incl_scan<SumOp>(total);  // the tile's digit counts: its local digit starts
     if (lane == 63) stg.tsum[w] = tincl;
-    uint32_t gcount = 0u;
     if constexpr (MODE == kTileSeg) {
       if (used)
 #pragma unroll
@@ -547,7 +546,10 @@ __device__ __forceinline__ void sweep_tile(
       if (i < w) tstart += stg.tsum[i];
     stg.tstart[d] = tstart;
     uint32_t prefix = 0u;
-    if (used) {
+    // A digit no key of the segment (or batch) holds has no tile to publish
+    // for or wait on (the last pass of a table-wide segment uses ~16 of its
+    // digits).
+    if (used && gcount != 0u) {
       using Word = SweepWord<SW>;
       SW* mine = status + tile * kRadix + d;
       if (tile == tile0) {
