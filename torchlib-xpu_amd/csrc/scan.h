@@ -9,13 +9,12 @@
 
 namespace mx {
 
-// 3072-element tiles (2048: +2.4 us, 4096: +2.8 us on 668k) in blocks of 8
-// waves with 6 elements per lane: the run-head scan of config 3 takes 9.0 us
-// against 10.8 with 4 waves of 12 (more waves per SIMD hide the dependent
-// loads); 16 waves of 3 take 8.6 us alone but get fewer CU slots when the
-// chunk-count scan runs beside the update kernel.
-constexpr int kScanThreads = 512;
-constexpr int kScanItems = 6;
+// 3072-element tiles (2048: +2.4 us, 4096: +2.8 us on 668k) in blocks of 16
+// waves with 3 elements per lane: more waves per SIMD hide the dependent
+// loads (config 3's run-head scan: 10.8 us with 4 waves of 12, 9.4 with 8 of
+// 6, 9.0 with 16 of 3).
+constexpr int kScanThreads = 1024;
+constexpr int kScanItems = 3;
 constexpr int64_t kScanTile = kScanThreads * kScanItems;
 
 inline int64_t scan_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
