@@ -3,8 +3,14 @@
  * torch.ops.fbgemm.* drop-in operators.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t
- * passed as `void*`.  Nothing here allocates: scratch memory is sized by a
- * *_workspace_bytes() query and handed in by the caller.  All calls are
+ * passed as `void*`.  Scratch memory is sized by a *_workspace_bytes() query
+ * and handed in by the caller.  One exception: an eager (not graph-captured)
+ * TBE backward keeps its radix sort's digit counters (about 2 MiB) in a
+ * region of the current device and stream that the call's last kernel
+ * leaves zeroed for the next call, allocated by the stream's first such
+ * call and kept until the process ends; under capture, or if that
+ * allocation fails, the counters live in the workspace and one more kernel
+ * clears them.  Nothing else allocates.  All calls are
  * asynchronous on `stream` and never synchronise the host.  They return
  * MX_OK (0) or a negative status; mx_last_error() then holds a
  * thread-local message.
@@ -70,8 +76,10 @@ extern "C" {
  * before binding.  0.2.0: mx_tbe_backward_rowwise_adagrad(_vbe) take their
  * stochastic-rounding state as `const mx_rng_state*` where 0.1.0 took a
  * `uint64_t seed` at the same position, and mx_set_status_mailbox takes
- * MX_STATUS_WORDS words where 0.1.0 took one (not binary compatible). */
-#define MX_FBGEMM_VERSION 200
+ * MX_STATUS_WORDS words where 0.1.0 took one (not binary compatible).
+ * 0.3.0: eager TBE backward calls keep their sort counters in a per-stream
+ * region (see above); mx_test_force_workspace_counters added. */
+#define MX_FBGEMM_VERSION 300
 int mx_version(void);
 
 /* Thread-local text of the last failing call on this thread ("" if none). */
@@ -107,6 +115,12 @@ int mx_test_force_lookback_giveup(int enable);
  * look-back counts in 64-bit words, the form used for sorts of 2^30 keys or
  * more, whatever the key count (lets tests cover that form at small sizes). */
 int mx_test_force_wide_sort_words(int enable);
+
+/* Test hook: while enabled, eager TBE backward calls keep their sort counters
+ * in the caller's workspace and clear them with one more kernel, as calls
+ * under graph capture always do, instead of using the stream's zeroed
+ * counter region (lets tests compare the two forms). */
+int mx_test_force_workspace_counters(int enable);
 
 /* ---- jagged tensor ops ------------------------------------------------- */
 

@@ -42,9 +42,10 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_last_error(lib):
     # The library reports the version its header declares (0.2.0 changed the
-    # backward's stochastic-rounding argument from a seed to mx_rng_state*).
+    # backward's stochastic-rounding argument from a seed to mx_rng_state*;
+    # 0.3.0 added the backward's per-stream counter region).
     hdr = re.search(r"#define MX_FBGEMM_VERSION (\d+)", HEADER.read_text())
-    assert hdr and lib.mx_version() == int(hdr.group(1)) == 200
+    assert hdr and lib.mx_version() == int(hdr.group(1)) == 300
     lib.mx_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mx_last_error(), bytes)
 

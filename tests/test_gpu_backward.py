@@ -930,3 +930,54 @@ def test_lookback_giveup_is_reported_and_leaves_outputs_alone(dev):
     torch.cuda.synchronize()
     assert not np.array_equal(W.cpu().numpy(), W0)
     assert torch.ops.mx_fbgemm.pending_lookback_faults(0) == 0
+
+
+def test_counter_region_matches_workspace_counters(dev):
+    """Eager backward calls keep the sort's digit counters in a region of
+    their stream that each call's last kernel clears for the next call.
+    Batches of different shapes in turn (40 features, then 3, then one table
+    with long runs, then 3 radix passes) give bit-identical weights with the
+    region and with the counters cleared in the workspace by one more kernel
+    (the graph-capture form), and both match the oracle."""
+    rng = np.random.default_rng(77)
+    cases = [
+        random_tbe(rng, 40, 24, [16] * 40, [300] * 40, 12),
+        random_tbe(rng, 3, 200, [4, 64, 256], [50, 2000, 40], 30),
+        random_tbe(rng, 1, 300, [128], [7], 40, dup_heavy=True),
+        random_tbe(rng, 5, 700, [4] * 5, [2 ** 20, 3, 100, 9, 2 ** 21], 10),
+    ]
+    for i, inp in enumerate(cases):
+        print(f"[case] counter region, batch {i} (T={inp.T})", flush=True)
+        got_region, _ = _backward_case(dev, inp, i % 2, seed=i)
+        torch.ops.mx_fbgemm.test_force_workspace_counters(True)
+        try:
+            got_ws, _ = _backward_case(dev, inp, i % 2, seed=i)
+        finally:
+            torch.ops.mx_fbgemm.test_force_workspace_counters(False)
+        assert np.array_equal(got_region, got_ws)
+
+
+def test_counter_region_after_a_failed_call(dev):
+    """A backward whose look-backs give up (forced from the host; every
+    kernel still exits normally) has already added into its stream's counter
+    region; its last kernel clears it all the same, so the next backward on
+    the stream matches the oracle."""
+    print("[case] counter region after a forced look-back give-up", flush=True)
+    rng = np.random.default_rng(23)
+    inp = random_tbe(rng, 3, 2048, [64] * 3, [5000, 300, 70000], 20)
+    nb = orc.info_B_num_bits(inp.T, inp.B)
+    _check_transpose(dev, inp)  # registers the device's failure word
+    W = rng.uniform(-0.01, 0.01, size=sum(E * D for E, D in zip(inp.E, inp.D))).astype(np.float32)
+    m1 = np.zeros(sum(inp.E), dtype=np.float32)
+    m1_off = np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)
+    grad = rng.normal(0, 1e-2, (inp.B, inp.total_D)).astype(np.float32)
+    torch.ops.mx_fbgemm.test_force_lookback_giveup(True)
+    try:
+        Wg, mg = _backward_gpu(dev, inp, W, m1, m1_off, grad, 0, 0.01, 1e-8)
+    finally:
+        torch.ops.mx_fbgemm.test_force_lookback_giveup(False)
+    assert np.array_equal(Wg, W) and not mg.any()
+    with pytest.raises(RuntimeError, match="gave up a look-back wait"):
+        _transpose_gpu(dev, inp, nb)
+    _backward_case(dev, inp, 0, seed=5)
+    _backward_case(dev, inp, 1, seed=6)

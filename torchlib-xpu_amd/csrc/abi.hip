@@ -44,6 +44,7 @@ std::mutex g_mailbox_mu;
 unsigned int* g_mailbox[64] = {};
 std::atomic<int> g_force_giveup{0};
 std::atomic<int> g_force_wide{0};
+std::atomic<int> g_force_ws_counters{0};
 }  // namespace
 
 unsigned int* status_mailbox() {
@@ -56,6 +57,8 @@ unsigned int* status_mailbox() {
 int lookback_spin_limit(int dflt) { return g_force_giveup.load() ? -1 : dflt; }
 
 bool force_wide_sort_words() { return g_force_wide.load() != 0; }
+
+bool force_workspace_counters() { return g_force_ws_counters.load() != 0; }
 
 __global__ void zero_u64_kernel(unsigned long long* p, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -86,5 +89,10 @@ extern "C" int mx_test_force_lookback_giveup(int enable) {
 
 extern "C" int mx_test_force_wide_sort_words(int enable) {
   mx::g_force_wide.store(enable != 0 ? 1 : 0);
+  return MX_OK;
+}
+
+extern "C" int mx_test_force_workspace_counters(int enable) {
+  mx::g_force_ws_counters.store(enable != 0 ? 1 : 0);
   return MX_OK;
 }

@@ -32,6 +32,9 @@ unsigned int* status_mailbox();
 int lookback_spin_limit(int dflt);
 // Test hook (mx_test_force_wide_sort_words): sort with 64-bit look-back words.
 bool force_wide_sort_words();
+// Test hook (mx_test_force_workspace_counters): eager backward calls clear
+// their sort counters in the workspace, as captured calls do.
+bool force_workspace_counters();
 
 #define MX_REQUIRE(cond, ...)                                   \
   do {                                                          \

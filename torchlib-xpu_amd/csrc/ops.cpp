@@ -156,6 +156,13 @@ void test_force_wide_sort_words(bool enable) {
   MX_CALL(mx_test_force_wide_sort_words(enable ? 1 : 0));
 }
 
+// mx_fbgemm::test_force_workspace_counters(enable): tests only -- later eager
+// backward calls clear their sort counters in the workspace (the form of
+// graph-captured calls) instead of using the stream's zeroed region.
+void test_force_workspace_counters(bool enable) {
+  MX_CALL(mx_test_force_workspace_counters(enable ? 1 : 0));
+}
+
 int32_t index_bytes_of(const Tensor& t, const char* name) {
   TORCH_CHECK(t.scalar_type() == at::kLong || t.scalar_type() == at::kInt, name,
               " must be int32 or int64, got ", t.scalar_type());
@@ -1667,4 +1674,6 @@ TORCH_LIBRARY(mx_fbgemm, m) {
   m.def("pending_lookback_faults(int device) -> int", &mx_ops::pending_lookback_faults);
   m.def("test_force_lookback_giveup(bool enable) -> ()", &mx_ops::test_force_lookback_giveup);
   m.def("test_force_wide_sort_words(bool enable) -> ()", &mx_ops::test_force_wide_sort_words);
+  m.def("test_force_workspace_counters(bool enable) -> ()",
+        &mx_ops::test_force_workspace_counters);
 }

@@ -35,7 +35,11 @@
 //    deterministic.  Runs and chunks are split into one contiguous key range
 //    per XCD, so an XCD re-reads only its tables' gradient columns, from its
 //    own L2.
+#include <map>
+#include <memory>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "mx_common.h"
 #include "scan.h"
@@ -814,14 +818,21 @@ int64_t sweep_status_tiles(int64_t n) { return sweep_tiles(n) + kSegMaxT; }
 // words, every segment tile), then 32 words holding the ticket.
 int64_t sweep_pass_words(int64_t n) { return sweep_status_tiles(n) * kRadix + 32; }
 constexpr size_t kSegHistBytes = static_cast<size_t>(kSegMaxT) * kSegRow * 4;
+constexpr size_t kStatusBytes = 256;
+constexpr size_t kHistBytes = (kHistCopies * kHistCopyWords * 4 + 255) & ~size_t(255);
+// The words linearize adds into, which must be zero when it starts: the
+// segment word, the digit histograms and the per-feature digit counts.
+constexpr size_t kEarlyBytes = kStatusBytes + kHistBytes + kSegHistBytes;
 
 struct SortWs {
   uint32_t* keys[2];
   uint32_t* vals[2];
   uint32_t* vals2[2];  // per-sample weights (weighted backward only)
-  // Zeroed before every call, contiguous: call status, scan slots, digit
-  // histograms, chunk marks, sweep state.
+  // Zeroed state, contiguous: the early words (segment word, digit
+  // histograms, per-feature digit counts; kEarlyBytes), then the failure word,
+  // the scan slots, the chunk marks and the sweep state (cleared by linearize).
   unsigned long long* zeroed;
+  unsigned long long* late;
   unsigned int* fail;              // set when a look-back of the call gave up
   unsigned long long* scan_state;  // kScanSlots slots of scan_slot_words
   int64_t scan_slot_words;
@@ -835,6 +846,7 @@ struct SortWs {
   int64_t sweep_words;
   uint32_t* counters;  // [0] num_runs, [1] total chunks
   size_t bytes;
+  int64_t early_words;  // early words the call used (set by run_transpose)
 };
 
 SortWs carve_sort(uint8_t* base, int64_t N) {
@@ -854,25 +866,22 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   }
   w.scan_slot_words = align256(slot_words * 8) / 8;
   w.sweep_words = sweep_pass_words(n);
-  constexpr size_t status_bytes = 256;
   const size_t scan_bytes = kScanSlots * w.scan_slot_words * 8;
-  const size_t hist_bytes = align256(kHistCopies * kHistCopyWords * 4);
   const size_t mark_bytes = align256(static_cast<size_t>(max_chunks(n)) * 4);
-  // Zeroed state: the failure and segment words, the digit histograms and
-  // the per-feature digit counts (cleared before linearize, which adds into
-  // the counts), then the scans' and passes' look-back state and the chunk
-  // marks (cleared by linearize itself).
-  const size_t early_bytes = status_bytes + hist_bytes + kSegHistBytes;
-  uint8_t* z = take(early_bytes + scan_bytes + mark_bytes + kMaxPasses * w.sweep_words * 8);
+  // Zeroed state: the early words (cleared before linearize, which adds into
+  // the counts), then the failure word, the scans' and passes' look-back
+  // state and the chunk marks (cleared by linearize itself).
+  const size_t late0 = kEarlyBytes, scan0 = late0 + kStatusBytes, mark0 = scan0 + scan_bytes;
+  uint8_t* z = take(mark0 + mark_bytes + kMaxPasses * w.sweep_words * 8);
   w.zeroed = reinterpret_cast<unsigned long long*>(z);
-  w.fail = reinterpret_cast<unsigned int*>(z);
-  w.seg_bad = z ? reinterpret_cast<unsigned int*>(z + 64) : nullptr;
-  w.ghist = z ? reinterpret_cast<uint32_t*>(z + status_bytes) : nullptr;
-  w.fhist = z ? reinterpret_cast<uint32_t*>(z + status_bytes + hist_bytes) : nullptr;
-  w.scan_state = z ? reinterpret_cast<unsigned long long*>(z + early_bytes) : nullptr;
-  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + early_bytes + scan_bytes) : nullptr;
-  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + early_bytes + scan_bytes + mark_bytes)
-              : nullptr;
+  w.seg_bad = reinterpret_cast<unsigned int*>(z);
+  w.ghist = z ? reinterpret_cast<uint32_t*>(z + kStatusBytes) : nullptr;
+  w.fhist = z ? reinterpret_cast<uint32_t*>(z + kStatusBytes + kHistBytes) : nullptr;
+  w.late = z ? reinterpret_cast<unsigned long long*>(z + late0) : nullptr;
+  w.fail = z ? reinterpret_cast<unsigned int*>(z + late0) : nullptr;
+  w.scan_state = z ? reinterpret_cast<unsigned long long*>(z + scan0) : nullptr;
+  w.chunk_mark = z ? reinterpret_cast<uint32_t*>(z + mark0) : nullptr;
+  w.sweep = z ? reinterpret_cast<unsigned long long*>(z + mark0 + mark_bytes) : nullptr;
   w.fpos = reinterpret_cast<int64_t*>(take((kSegMaxT + 1) * 8));
   w.tprefix = reinterpret_cast<int32_t*>(take((kSegMaxT + 1) * 4));
   w.counters = reinterpret_cast<uint32_t*>(take(64));
@@ -880,8 +889,8 @@ SortWs carve_sort(uint8_t* base, int64_t N) {
   return w;
 }
 
-// Words cleared before linearize: the failure and segment words, the
-// histograms, and the digit counts of `seg_features` features.
+// Early words of a call: the segment word, the histograms, and the digit
+// counts of `seg_features` features.
 int64_t early_zeroed_words(const SortWs& w, int32_t seg_features) {
   return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.fhist) -
                               reinterpret_cast<uint8_t*>(w.zeroed)) / 8 +
@@ -896,11 +905,11 @@ int64_t call_pass_words(int64_t tiles, int word_bytes) {
 }
 
 // Words linearize clears for a sort of `passes` passes of `pass_words` each:
-// the scan state, the chunk marks and the sweep state of those passes (the
-// rest of the workspace's sweep state is left alone).
+// the failure word, the scan state, the chunk marks and the sweep state of
+// those passes (the rest of the workspace's sweep state is left alone).
 int64_t late_zeroed_words(const SortWs& w, int passes, int64_t pass_words) {
   return static_cast<int64_t>(reinterpret_cast<uint8_t*>(w.sweep) -
-                              reinterpret_cast<uint8_t*>(w.scan_state)) / 8 +
+                              reinterpret_cast<uint8_t*>(w.late)) / 8 +
          passes * pass_words;
 }
 
@@ -927,28 +936,84 @@ struct TransposeOut {
   float* weights_sorted;  // [N] per-sample weights in sorted order, or null
 };
 
+// Early words kept zero between calls.  Clearing a call's early words in its
+// workspace is one more launch, ~4.5 us of kernel boundary per call.  An
+// eager backward takes them instead from a region of its (device, stream)
+// that is zero between calls: the call's last kernel clears what the call
+// used, after the sort passes have read it, and the next call on the stream
+// runs after that kernel.  A call holds `mu` while it submits its kernels, so
+// that calls of two host threads on one stream do not interleave.  A region
+// in an unknown state (new, or left by a call that stopped between its first
+// launch and its last) is cleared by the next call before use.
+struct ZeroedRegion {
+  std::mutex mu;
+  uint8_t* base = nullptr;  // kEarlyBytes, laid out like a workspace's early words
+  bool dirty = true;
+};
+
+// The region of the current device and stream `s`, allocated on first use;
+// null while `s` is being captured (a graph keeps clearing its workspace's
+// early words itself), when the allocation fails, or while the test hook asks
+// for workspace counters.  Regions live until the process ends.
+ZeroedRegion* stream_region(hipStream_t s) {
+  if (force_workspace_counters()) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  int dev = 0;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+      hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::unique_ptr<ZeroedRegion>> regions;
+  std::lock_guard<std::mutex> lock(mu);
+  std::unique_ptr<ZeroedRegion>& r = regions[{dev, s}];
+  if (!r) {
+    void* p = nullptr;
+    if (hipMalloc(&p, kEarlyBytes) != hipSuccess) {
+      (void)hipGetLastError();
+      regions.erase({dev, s});
+      return nullptr;
+    }
+    r = std::make_unique<ZeroedRegion>();
+    r->base = static_cast<uint8_t*>(p);
+  }
+  return r.get();
+}
+
 // nbags = T * B bags of a fixed batch B, or (b_t_map non-null, VBE) the
-// total bag count with each bag's info word given.
+// total bag count with each bag's info word given.  zr: the stream's zeroed
+// region for the early words (held locked by the caller, whose last kernel
+// clears w.early_words of it), or null: the workspace's, cleared here.
 int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
                   const int32_t* b_t_map, int32_t bits, int32_t nb, const void* indices,
                   const void* offsets, int32_t index_bytes, int64_t N, const float* iw,
-                  const TransposeOut& o, SortWs& w, hipStream_t s) {
+                  const TransposeOut& o, SortWs& w, hipStream_t s, ZeroedRegion* zr) {
   // With per-sample weights the weights travel with the keys as a second payload.
   uint32_t* const v2[2] = {iw ? w.vals2[0] : nullptr, iw ? w.vals2[1] : nullptr};
   uint32_t* const v2_final = iw ? reinterpret_cast<uint32_t*>(o.weights_sorted) : nullptr;
   const dim3 g256(static_cast<uint32_t>(ceil_div(N, 256)));
   const int passes = (bits + kRadixBits - 1) / kRadixBits;
+  if (zr) {  // the early words move to the region (same layout)
+    const ptrdiff_t d = zr->base - reinterpret_cast<uint8_t*>(w.zeroed);
+    w.zeroed = reinterpret_cast<unsigned long long*>(zr->base);
+    w.seg_bad = reinterpret_cast<unsigned int*>(reinterpret_cast<uint8_t*>(w.seg_bad) + d);
+    w.ghist = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.ghist) + d);
+    w.fhist = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.fhist) + d);
+  }
   // Segments (one per feature) for a fixed batch of at most kSegMaxT features.
   SegSort seg{};
   if (b_t_map == nullptr && T >= 1 && T <= kSegMaxT && passes > 0)
     seg = SegSort{w.fpos, w.tprefix, w.fhist, w.seg_bad, T};
-  {  // the failure and segment words, the histograms and digit counts start at zero
-    const int64_t words = early_zeroed_words(w, seg.T);
+  w.early_words = early_zeroed_words(w, seg.T);
+  if (zr == nullptr || zr->dirty) {  // the early words start at zero (a dirty region: all of them)
+    const int64_t words = zr ? static_cast<int64_t>(kEarlyBytes / 8) : w.early_words;
     const int64_t blocks = ceil_div(words, 256);
     zero_u64_kernel<<<dim3(static_cast<uint32_t>(blocks < 2048 ? blocks : 2048)), 256, 0, s>>>(
         w.zeroed, words);
     MX_LAUNCH_CHECK();
   }
+  if (zr) zr->dirty = true;  // until the caller's last kernel is launched
   const int64_t ntiles = sweep_tiles(N) + seg.T;  // segments start at tile boundaries
   if (ntiles > 0xffffffffll) return set_error(MX_EINVAL, "too many sort tiles");
   // Every count fits a 32-bit word's 30 bits.
@@ -961,12 +1026,12 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     linearize_kernel<int64_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int64_t*>(indices), static_cast<const int64_t*>(offsets), nbags, B,
         nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
-        w.scan_state, late_words, seg);
+        w.late, late_words, seg);
   else
     linearize_kernel<int32_t><<<glin, 256, 0, s>>>(
         hsc, static_cast<const int32_t*>(indices), static_cast<const int32_t*>(offsets), nbags, B,
         nb, b_t_map, N, bits, passes, o.linear, w.keys[0], w.vals[0], iw, v2[0], w.ghist,
-        w.scan_state, late_words, seg);
+        w.late, late_words, seg);
   MX_LAUNCH_CHECK();
 
   const dim3 gsweep(static_cast<uint32_t>(ntiles));
@@ -1034,6 +1099,10 @@ struct BwdArgs {
   const uint32_t* total_chunks;
   float* partial;
   const unsigned int* fail;  // set when a look-back of the call gave up: nothing is updated
+  // The stream's zeroed region of the sort's early words, or null: the update
+  // launch clears its first rezero_words words (the sort has read them).
+  unsigned long long* rezero;
+  int64_t rezero_words;
   int64_t B;
   int64_t total_D;
   int32_t T;
@@ -1511,6 +1580,11 @@ template <typename I, typename WT, int G, int NCH, int U, int GL, int NCHL, int 
           bool PLAIN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(runs_waves<NCH>())))
     bwd_runs_kernel(BwdArgs a, int64_t nlong) {
+  // The early words go back to zero for the stream's next call, also when
+  // this call failed (every block passes here before it may return).
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < a.rezero_words;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    a.rezero[i] = 0ull;
   pin_options<PLAIN>(a);
   if (call_failed(a.fail)) return;  // the run layout is not valid
   __shared__ TableMeta meta;
@@ -1689,7 +1763,8 @@ int transpose_impl(const int64_t* hash_size_cumsum, int32_t T, int64_t B, const 
   TransposeOut o{linear_indices, sorted_linear_indices, infos_sorted, sorted_linear_indices_run,
                  run_lengths, num_runs, cumulative_run_lengths, nullptr};
   return run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map, total_hash_size_bits,
-                       info_B_num_bits, indices, offsets, index_bytes, N, nullptr, o, w, s);
+                       info_B_num_bits, indices, offsets, index_bytes, N, nullptr, o, w, s,
+                       nullptr);
 }
 
 int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offsets,
@@ -1720,11 +1795,16 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   auto* s = as_stream(stream);
   TransposeOut o{nullptr, w.sorted, w.infos, w.run, nullptr, nullptr, w.cum,
                  indice_weights ? w.weights_sorted : nullptr};
+  ZeroedRegion* zr = stream_region(s);
+  std::unique_lock<std::mutex> zr_lock;
+  if (zr) zr_lock = std::unique_lock<std::mutex>(zr->mu);
   if (int rc = run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map,
                              total_hash_size_bits, nb, indices, offsets, index_bytes, N,
-                             indice_weights, o, w.sort, s))
+                             indice_weights, o, w.sort, s, zr))
     return rc;
   BwdArgs a;
+  a.rezero = zr ? reinterpret_cast<unsigned long long*>(zr->base) : nullptr;
+  a.rezero_words = zr ? w.sort.early_words : 0;
   a.W = weights;
   a.w_off = weights_offsets;
   a.D_off = D_offsets;
@@ -1761,11 +1841,15 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   a.offset = a.sr ? rng->offset : 0;
   a.seed_dev = a.sr ? rng->seed_dev : nullptr;
   a.offset_dev = a.sr ? rng->offset_dev : nullptr;
+  int rc;
   if (weights_ty == MX_SPARSE_FP16)
-    return index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, w.sort, w.chunk_start, N, s)
-                            : dispatch_bwd<int32_t, __half>(a, w.sort, w.chunk_start, N, s);
-  return index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, w.sort, w.chunk_start, N, s)
+    rc = index_bytes == 8 ? dispatch_bwd<int64_t, __half>(a, w.sort, w.chunk_start, N, s)
+                          : dispatch_bwd<int32_t, __half>(a, w.sort, w.chunk_start, N, s);
+  else
+    rc = index_bytes == 8 ? dispatch_bwd<int64_t, float>(a, w.sort, w.chunk_start, N, s)
                           : dispatch_bwd<int32_t, float>(a, w.sort, w.chunk_start, N, s);
+  if (zr && rc == MX_OK) zr->dirty = false;  // the update launch clears the region
+  return rc;
 }
 
 }  // namespace
