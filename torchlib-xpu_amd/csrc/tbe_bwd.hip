@@ -19,7 +19,10 @@
 //    accumulates the digit counts of every pass (LDS, then one atomic per bin
 //    and block into its XCD's copy): per feature for a fixed batch of at most
 //    kSegMaxT features (a global sort, when some key lies outside its table's
-//    range, sums them), else for the whole batch.
+//    range, sums them), else for the whole batch.  Those counts start at
+//    zero: an eager backward keeps them in a region of its stream that its
+//    update launch clears for the next call; other calls keep them in the
+//    workspace and clear them with one more kernel.
 //  * One launch per pass ("onesweep"): a block of 16 waves ranks a 3072-key
 //    tile (each wave 192 keys, 64 at a time, stable ranks from 8 ballots),
 //    then thread d finds how many keys of digit d earlier tiles of its
