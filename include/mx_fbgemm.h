@@ -8,9 +8,10 @@
  * TBE backward keeps its radix sort's digit counters (about 2 MiB) in a
  * region of the current device and stream that the call's last kernel
  * leaves zeroed for the next call, allocated by the stream's first such
- * call and kept until the process ends; under capture, or if that
- * allocation fails, the counters live in the workspace and one more kernel
- * clears them.  Nothing else allocates.  All calls are
+ * call and kept until the process ends (at most 64 streams per device);
+ * under capture, past those 64 streams, or if that allocation fails, the
+ * counters live in the workspace and one more kernel clears them.  Nothing
+ * else allocates.  All calls are
  * asynchronous on `stream` and never synchronise the host.  They return
  * MX_OK (0) or a negative status; mx_last_error() then holds a
  * thread-local message.

@@ -956,8 +956,12 @@ struct ZeroedRegion {
 
 // The region of the current device and stream `s`, allocated on first use;
 // null while `s` is being captured (a graph keeps clearing its workspace's
-// early words itself), when the allocation fails, or while the test hook asks
-// for workspace counters.  Regions live until the process ends.
+// early words itself), when the allocation fails, once a device holds
+// kMaxStreamRegions regions (a caller that makes a new stream per call pays
+// the clearing launch instead of 2 MB per stream), or while the test hook
+// asks for workspace counters.  Regions live until the process ends.
+constexpr int kMaxStreamRegions = 64;
+
 ZeroedRegion* stream_region(hipStream_t s) {
   if (force_workspace_counters()) return nullptr;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -969,19 +973,20 @@ ZeroedRegion* stream_region(hipStream_t s) {
   }
   static std::mutex mu;
   static std::map<std::pair<int, hipStream_t>, std::unique_ptr<ZeroedRegion>> regions;
+  static std::map<int, int> per_device;
   std::lock_guard<std::mutex> lock(mu);
-  std::unique_ptr<ZeroedRegion>& r = regions[{dev, s}];
-  if (!r) {
-    void* p = nullptr;
-    if (hipMalloc(&p, kEarlyBytes) != hipSuccess) {
-      (void)hipGetLastError();
-      regions.erase({dev, s});
-      return nullptr;
-    }
-    r = std::make_unique<ZeroedRegion>();
-    r->base = static_cast<uint8_t*>(p);
+  auto it = regions.find({dev, s});
+  if (it != regions.end()) return it->second.get();
+  if (per_device[dev] >= kMaxStreamRegions) return nullptr;
+  void* p = nullptr;
+  if (hipMalloc(&p, kEarlyBytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
   }
-  return r.get();
+  auto r = std::make_unique<ZeroedRegion>();
+  r->base = static_cast<uint8_t*>(p);
+  ++per_device[dev];
+  return (regions[{dev, s}] = std::move(r)).get();
 }
 
 // nbags = T * B bags of a fixed batch B, or (b_t_map non-null, VBE) the
