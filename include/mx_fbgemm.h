@@ -97,8 +97,10 @@ const char* mx_last_error(void);
  * for the current device.
  * mx_nbit_forward stores 1 into word MX_STATUS_NBIT_TABLE when a table of the
  * call cannot be served -- its type byte names no type the call's max_*_D
- * arguments launch, or it is an INT4 table of odd D or an INT2 table of D not
- * a multiple of 4 -- after writing that table's output columns as zeros.
+ * arguments launch, it is an INT4 table of odd D or an INT2 table of D not a
+ * multiple of 4, or its rows do not start at 4-byte boundaries (its
+ * weights_offsets entry or its row stride after row_alignment is not a
+ * multiple of 4) -- after writing that table's output columns as zeros.
  * host_words points at MX_STATUS_WORDS words of pinned host memory owned by
  * the caller, which reads and clears them; NULL unregisters.  Kernels
  * launched before a registration (or captured in a graph before it) do not

@@ -150,12 +150,14 @@ def test_short_indice_weights_raise(dev):
                   inp.offsets, max_dims(tys, dims), iw=iw)
 
 
-# (bad table's type byte, its D, the type its bytes are built as, maxima override)
+# (bad table's type byte, its D, the type its bytes are built as, maxima override,
+#  bytes the bad table's rows are moved by in the weights buffer)
 BAD_TABLES = {
-    "bf16_type_byte": (5, 32, orc.FP16, None),           # BF16: no nbit launch serves it
-    "odd_int4_D": (orc.INT4, 7, orc.INT4, None),          # 7 codes leave half a byte
-    "int2_D_not_multiple_of_4": (orc.INT2, 6, orc.INT2, None),
-    "type_with_zero_max_D": (orc.INT2, 16, orc.INT2, 0),  # max_int2_D = 0: not launched
+    "bf16_type_byte": (5, 32, orc.FP16, None, 0),           # BF16: no nbit launch serves it
+    "odd_int4_D": (orc.INT4, 7, orc.INT4, None, 0),          # 7 codes leave half a byte
+    "int2_D_not_multiple_of_4": (orc.INT2, 6, orc.INT2, None, 0),
+    "type_with_zero_max_D": (orc.INT2, 16, orc.INT2, 0, 0),  # max_int2_D = 0: not launched
+    "rows_not_4_byte_aligned": (orc.INT8, 32, orc.INT8, None, 2),  # weights_offsets[t] % 4 == 2
 }
 
 
@@ -165,7 +167,7 @@ def test_unservable_table_is_zeroed_and_reported(dev, case):
     as zeros (not left as allocated); the other tables match the oracle, and
     the next nbit call on the device raises, once."""
     print(f"[case] nbit unservable table: {case}", flush=True)
-    bad_ty, bad_D, build_ty, bad_max = BAD_TABLES[case]
+    bad_ty, bad_D, build_ty, bad_max, shift = BAD_TABLES[case]
     rng = np.random.default_rng(62)
     ty_bytes = [orc.INT8, bad_ty, orc.FP16, orc.INT4]
     dims = [32, bad_D, 64, 16]
@@ -181,11 +183,18 @@ def test_unservable_table_is_zeroed_and_reported(dev, case):
         # of 4), so the device check is the one that finds the table.  (The
         # INT4 case keeps the served INT4 table's maximum, 16.)
         maxima[0] = 8
-    W = torch.from_numpy(buf).to(dev)
+    if shift:  # the bad table's bytes move by `shift`, the next tables' by 4 (aligned again)
+        w_off_k = w_off + np.array([0, shift, 4, 4], np.int64)
+        gap = np.zeros(shift, np.uint8)
+        buf_k = np.concatenate([buf[:w_off[1]], gap, buf[w_off[1]:w_off[2]],
+                                np.zeros(4 - shift, np.uint8), buf[w_off[2]:]])
+    else:
+        w_off_k, buf_k = w_off, buf
+    W = torch.from_numpy(buf_k).to(dev)
     # The output reuses a freed block full of NaN, so unwritten columns would show.
     junk = torch.full((inp.B, inp.total_D), float("nan"), dtype=torch.float16, device=dev)
     del junk
-    got = _raw_nbit(dev, W, w_off, ty_bytes, dims, inp.indices, inp.offsets, maxima)
+    got = _raw_nbit(dev, W, w_off_k, ty_bytes, dims, inp.indices, inp.offsets, maxima)
     torch.cuda.synchronize()
     g = got.cpu().numpy()
     d0 = int(inp.D_offsets[1])
@@ -201,8 +210,8 @@ def test_unservable_table_is_zeroed_and_reported(dev, case):
     cols = np.concatenate([np.arange(inp.D_offsets[t], inp.D_offsets[t + 1]) for t in good])
     assert_nbit_close(g[:, cols], exp)
     with pytest.raises(RuntimeError, match="cannot serve"):
-        _raw_nbit(dev, W, w_off, ty_bytes, dims, inp.indices, inp.offsets, maxima)
+        _raw_nbit(dev, W, w_off_k, ty_bytes, dims, inp.indices, inp.offsets, maxima)
     # Reported once: a valid call then runs normally.
-    ok = _raw_nbit(dev, W, w_off[good], [ty_bytes[t] for t in good], [dims[t] for t in good],
+    ok = _raw_nbit(dev, W, w_off_k[good], [ty_bytes[t] for t in good], [dims[t] for t in good],
                    sub_idx, sub_off, maxima)
     assert_nbit_close(ok, exp)

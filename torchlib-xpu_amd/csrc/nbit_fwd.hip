@@ -62,12 +62,6 @@ __device__ __forceinline__ bool whole_bytes(int32_t D) {
   return true;
 }
 
-__device__ __forceinline__ bool table_ok(int32_t ty, int32_t D, int32_t served) {
-  if (ty < 0 || ty > MX_SPARSE_INT2 || ((served >> ty) & 1) == 0 || D < 0) return false;
-  if (ty == MX_SPARSE_INT4) return whole_bytes<MX_SPARSE_INT4>(D);
-  if (ty == MX_SPARSE_INT2) return whole_bytes<MX_SPARSE_INT2>(D);
-  return true;
-}
 
 __device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, int32_t align) {
   int64_t u;
@@ -81,6 +75,21 @@ __device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, 
   }
   if (align > 1) u = (u + align - 1) / align * align;
   return u;
+}
+
+// Rows start at 4-byte boundaries (the kernels read codes and qparams in
+// 4-byte words): the table's first byte and its row stride are multiples of 4.
+__device__ __host__ __forceinline__ bool rows_aligned(int64_t w_off, int64_t stride) {
+  return ((w_off | stride) & 3) == 0;
+}
+
+__device__ __forceinline__ bool table_ok(int32_t ty, int32_t D, int32_t served, int64_t w_off,
+                                         int32_t align) {
+  if (ty < 0 || ty > MX_SPARSE_INT2 || ((served >> ty) & 1) == 0 || D < 0) return false;
+  if (!rows_aligned(w_off, row_bytes_of(ty, D, align))) return false;
+  if (ty == MX_SPARSE_INT4) return whole_bytes<MX_SPARSE_INT4>(D);
+  if (ty == MX_SPARSE_INT2) return whole_bytes<MX_SPARSE_INT2>(D);
+  return true;
 }
 
 template <int TY>
@@ -485,7 +494,7 @@ __device__ __forceinline__ int32_t table_type(const uint8_t* tys, int64_t t) {
 __device__ __forceinline__ void check_table(const NbitArgs& a, int64_t t, int32_t ty) {
   const int32_t D0 = load_scalar(a.D_off + t);
   const int32_t D = load_scalar(a.D_off + t + 1) - D0;
-  if (table_ok(ty, D, a.served)) return;
+  if (table_ok(ty, D, a.served, load_scalar(a.w_off + t), a.row_align)) return;
   const int64_t c0 = D0 < 0 ? 0 : D0;
   const int64_t c1 = static_cast<int64_t>(D0) + (D > 0 ? D : 0);
   const int64_t nc = (c1 < a.total_D ? c1 : a.total_D) - c0;
@@ -558,13 +567,15 @@ __device__ __forceinline__ void nbit_fwd_body(const NbitArgs& a) {
   __syncthreads();
   const int32_t D0 = load_scalar(a.D_off + t);
   const int32_t D = load_scalar(a.D_off + t + 1) - D0;
-  // A table whose codes leave a partial byte is left to the check blocks.
-  if (!whole_bytes<TY>(D)) return;  // block-uniform
+  const int64_t stride = row_bytes_of(ty, D, a.row_align);
+  const int64_t wo = load_scalar(a.w_off + t);
+  // A table whose codes leave a partial byte, or whose rows do not start at
+  // 4-byte boundaries, is left to the check blocks.
+  if (!whole_bytes<TY>(D) || !rows_aligned(wo, stride)) return;  // block-uniform
   const int lane = threadIdx.x & 63;
   const int g = lane / G;
   const int k = lane % G;
-  const int64_t stride = row_bytes_of(ty, D, a.row_align);
-  const uint8_t* __restrict__ Wt = a.W + load_scalar(a.w_off + t);
+  const uint8_t* __restrict__ Wt = a.W + wo;
   const int i = s_bag[(threadIdx.x >> 6) * P + g];
   const int64_t b = b0 + i;
   if (b >= a.B) return;  // whole group idle (idle slots rank last); its lanes stay converged

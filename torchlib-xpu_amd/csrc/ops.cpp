@@ -108,8 +108,10 @@ void raise_if_lookback_failed(int dev) {
     __atomic_store_n(p + MX_STATUS_NBIT_TABLE, 0, __ATOMIC_RELAXED);
     TORCH_CHECK(false, "an earlier int_nbit_split_embedding_codegen_lookup_function on cuda:",
                 dev, " met a table it cannot serve (a weights_tys byte naming no type whose "
-                "max_*_D is positive, or an INT4 table of odd D or an INT2 table of D not a "
-                "multiple of 4) and wrote that table's output columns as zeros");
+                "max_*_D is positive, an INT4 table of odd D, an INT2 table of D not a "
+                "multiple of 4, or rows not starting at 4-byte boundaries: weights_offsets[t] "
+                "or the row stride after row_alignment not a multiple of 4) and wrote that "
+                "table's output columns as zeros");
   }
 }
 
