@@ -108,6 +108,14 @@ def test_inference_module_arguments():
     assert (m.max_int8_D, m.max_int4_D, m.max_float16_D, m.max_int2_D, m.max_float32_D) == \
         (128, 64, 32, 0, 0)
     assert m.weights_dev.numel() == 1440 + 960 + 320
+    # INT2 rows of D = 8 are 6 bytes: row_alignment 1 or 2 would leave them off
+    # 4-byte boundaries, which the kernels cannot read.
+    int2 = [("d", 10, 8, SparseType.INT2, EmbeddingLocation.DEVICE)]
+    m4 = IntNBitTableBatchedEmbeddingBagsCodegen(int2, row_alignment=4, device="cpu")
+    assert m4.row_bytes == [8]
+    for bad in (0, 1, 2):
+        with pytest.raises(ValueError):
+            IntNBitTableBatchedEmbeddingBagsCodegen(int2, row_alignment=bad, device="cpu")
 
 
 def test_quantize_rows_needs_gpu():

@@ -90,6 +90,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
                 raise ValueError(f"weight type {ty} is not supported")
             if D <= 0 or D > 1024 or D % 8:
                 raise ValueError(f"embedding_dim {D} must be a positive multiple of 8, <= 1024")
+            if row_alignment < 1 or padded_row_size_in_bytes(D, ty, row_alignment) % 4:
+                # The kernels read codes and qparams in 4-byte words.
+                raise ValueError(f"row_alignment {row_alignment} leaves {ty} rows of D={D} "
+                                 f"off 4-byte boundaries")
         device = torch.device(device) if device is not None else torch.device(
             "cuda", torch.cuda.current_device())
         self.embedding_specs = embedding_specs
