@@ -10,6 +10,7 @@
 // kernel call write a table's D-slice of the [B, total_D] output and read
 // padded rows; scale_bias_last = false selects the TBE row layout (fp16
 // scale and bias at the front of each quantized row, :88-92,144-149).
+#include <fbgemm/FbgemmConvert.h>
 #include <fbgemm/FbgemmEmbedding.h>
 
 #include <algorithm>
@@ -28,6 +29,7 @@ int64_t row_bytes(int ty, int D, int align) {
     case 2: u = D + 4ll; break;
     case 3: u = D / 2 + 4ll; break;
     case 4: u = D / 4 + 4ll; break;
+    case 6: u = D; break;
     default: return -1;
   }
   if (align > 1) u = (u + align - 1) / align * align;
@@ -115,11 +117,25 @@ extern "C" int fb_tbe_forward_f16w(const uint16_t* W, const int64_t* w_off, cons
   });
 }
 
+// FBGEMM's hfp8 conversions (FbgemmConvert.h:181-200), one value at a time.
+extern "C" float fb_hfp8_to_float(uint8_t v, int ebits, int ebias) {
+  float f;
+  fbgemm::Float8ToFloat_ref(v, &f, ebits, ebias);
+  return f;
+}
+
+extern "C" uint8_t fb_float_to_hfp8(float x, int ebits, int ebias) {
+  uint8_t v;
+  fbgemm::FloatToFloat8_ref(x, &v, ebits, ebias);
+  return v;
+}
+
 extern "C" int fb_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                                const int32_t* D_off, int T, int64_t B, const int64_t* indices,
                                const int64_t* offsets, int pooling, const float* iw,
                                int row_align, int out_f16, void* out, int64_t total_D,
-                               const int64_t* rows_per_table, int nthreads) {
+                               const int64_t* rows_per_table, int nthreads, int fp8_ebits,
+                               int fp8_ebias) {
   if (!out_f16) return -3;  // the harness serves fp16 output (the nbit configs)
   using K8 = fbgemm::EmbeddingSpMDMKernelSignature<uint8_t, int64_t, int64_t, uint16_t>::Type;
   using K16 = fbgemm::EmbeddingSpMDMKernelSignature<uint16_t, int64_t, int64_t, uint16_t>::Type;
@@ -150,6 +166,10 @@ extern "C" int fb_nbit_forward(const uint8_t* W, const int64_t* w_off, const uin
         k8[t] = fbgemm::GenerateEmbeddingSpMDMNBitWithStrides<int64_t, int64_t, uint16_t>(
             tys[t] == 3 ? 4 : 2, D, w, mean, 16, false, true, total_D, stride,
             /*scale_bias_last=*/false);
+        break;
+      case 6:  // weighted when the call passes weights
+        k8[t] = fbgemm::GenerateEmbeddingSpMDMFP8WithStrides<int64_t, int64_t, uint16_t>(
+            D, mean, false, true, total_D, stride, fp8_ebits, fp8_ebias);
         break;
       default:
         return -1;

@@ -110,6 +110,42 @@ void orc_tbe_forward_f32(const float* W, const int64_t* w_off, const int32_t* D_
   }
 }
 
+/* ---- hfp8 ---------------------------------------------------------------------
+ * FBGEMM's 8-bit float of the nbit TBE (SparseType FP8; fbgemm::Float8ToFloat_ref
+ * and FloatToFloat8_ref, torch/include/fbgemm/FbgemmConvert.h:181-200): a sign
+ * bit, `ebits` exponent bits and m = 7 - ebits mantissa bits, exponent bias
+ * `ebias`, subnormals where the exponent field is 0, no infinity or NaN codes:
+ *   E > 0: (-1)^s * 2^(E - ebias) * (1 + M / 2^m)
+ *   E = 0: (-1)^s * 2^(1 - ebias) * M / 2^m
+ * Every code is exact in fp32.  Encoding clamps |x| to max_pos, then rounds
+ * to the nearest code, ties to even (the grid of x's binade, or the
+ * subnormal grid below 2^(1 - ebias)); NaN inputs are not defined. */
+float orc_hfp8_to_float(uint8_t v, int32_t ebits, int32_t ebias) {
+  const int m = 7 - ebits;
+  const int E = (v & 0x7f) >> m, M = v & ((1 << m) - 1);
+  const float a = E > 0 ? ldexpf(1.0f + ldexpf((float)M, -m), E - ebias)
+                        : ldexpf((float)M, 1 - ebias - m);
+  return (v & 0x80) ? -a : a;
+}
+
+uint8_t orc_float_to_hfp8(float x, int32_t ebits, int32_t ebias, float max_pos) {
+  const int m = 7 - ebits;
+  const uint8_t s = signbit(x) ? 0x80 : 0;
+  float a = fabsf(x);
+  if (a > max_pos) a = max_pos;
+  if (a < ldexpf(1.0f, 1 - ebias)) /* subnormal grid, quantum 2^(1 - ebias - m) */
+    return (uint8_t)(s | (uint8_t)rintf(ldexpf(a, ebias + m - 1)));
+  int e;
+  (void)frexpf(a, &e); /* a in [2^(e-1), 2^e) */
+  const float k = rintf(ldexpf(a, m - (e - 1))); /* in [2^m, 2^(m+1)] */
+  int E = e - 1 + ebias, M = (int)k - (1 << m);
+  if (M == (1 << m)) { /* rounded up into the next binade */
+    E += 1;
+    M = 0;
+  }
+  return (uint8_t)(s | (uint8_t)((E << m) | M));
+}
+
 /* ---- nbit forward -------------------------------------------------------------
  * Row (t, i) starts at byte w_off[t] + i * stride_t, stride_t =
  * round_up(unpadded, row_align).  Quantized rows carry an fp16 scale and
@@ -125,14 +161,17 @@ int64_t orc_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_align) {
     case ORC_INT8: u = D + 4ll; break;
     case ORC_INT4: u = D / 2 + 4ll; break;
     case ORC_INT2: u = D / 4 + 4ll; break;
+    case ORC_FP8: u = D; break;
     default: return -1;
   }
   if (row_align > 1) u = (u + row_align - 1) / row_align * row_align;
   return u;
 }
 
-static float nbit_code(const uint8_t* codes, int32_t ty, int32_t d) {
+static float nbit_code(const uint8_t* codes, int32_t ty, int32_t d, int32_t ebits,
+                       int32_t ebias) {
   switch (ty) {
+    case ORC_FP8: return orc_hfp8_to_float(codes[d], ebits, ebias);
     case ORC_FP32: {
       float f;
       memcpy(&f, codes + 4 * d, 4);
@@ -152,7 +191,8 @@ static float nbit_code(const uint8_t* codes, int32_t ty, int32_t d) {
 int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                      const int32_t* D_off, int32_t T, int64_t B, const int64_t* indices,
                      const int64_t* offsets, int32_t pooling, const float* iw, int32_t row_align,
-                     int32_t out_f16, void* out, int64_t total_D) {
+                     int32_t out_f16, void* out, int64_t total_D, int32_t fp8_ebits,
+                     int32_t fp8_ebias) {
   float* acc = NULL;
   for (int32_t t = 0; t < T; ++t) {
     const int32_t ty = tys[t];
@@ -184,10 +224,10 @@ int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
             scale = scale * wgt;
             bias = bias * wgt;
           }
-          for (int32_t d = 0; d < D; ++d) acc[d] = fmaf(scale, nbit_code(row + 4, ty, d), acc[d] + bias);
+          for (int32_t d = 0; d < D; ++d) acc[d] = fmaf(scale, nbit_code(row + 4, ty, d, 0, 0), acc[d] + bias);
         } else {
           for (int32_t d = 0; d < D; ++d) {
-            const float v = nbit_code(row, ty, d);
+            const float v = nbit_code(row, ty, d, fp8_ebits, fp8_ebias);
             acc[d] = iw ? fmaf(wgt, v, acc[d]) : acc[d] + v;
           }
         }

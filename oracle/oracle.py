@@ -30,7 +30,7 @@ FBGEMM_LIB = BUILD_DIR / "libfbgemm_cpu.so"
 ORACLE_MT_LIB = BUILD_DIR / "libmx_oracle_mt.so"
 
 POOL_SUM, POOL_MEAN = 0, 1
-FP32, FP16, INT8, INT4, INT2 = 0, 1, 2, 3, 4
+FP32, FP16, INT8, INT4, INT2, FP8 = 0, 1, 2, 3, 4, 6
 
 
 def build(quiet: bool = True) -> None:
@@ -60,7 +60,8 @@ def lib():
         i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
         _lib.orc_tbe_forward_f32.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64]
         _lib.orc_tbe_forward_f32.restype = None
-        _lib.orc_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64]
+        _lib.orc_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64,
+                                          i32, i32]
         _lib.orc_nbit_forward.restype = ctypes.c_int
         _lib.orc_nbit_row_bytes.argtypes = [i32, i32, i32]
         _lib.orc_nbit_row_bytes.restype = i64
@@ -83,6 +84,10 @@ def lib():
         _lib.orc_half_to_float.restype = f32
         _lib.orc_float_to_half.argtypes = [f32]
         _lib.orc_float_to_half.restype = ctypes.c_uint16
+        _lib.orc_hfp8_to_float.argtypes = [ctypes.c_uint8, i32, i32]
+        _lib.orc_hfp8_to_float.restype = f32
+        _lib.orc_float_to_hfp8.argtypes = [f32, i32, i32, f32]
+        _lib.orc_float_to_hfp8.restype = ctypes.c_uint8
     return _lib
 
 
@@ -112,8 +117,12 @@ def fbgemm():
         _fb.fb_tbe_forward_f16w.argtypes = [P, P, P, i32, i64, P, P, i32, P, P, i64, P, i32]
         _fb.fb_tbe_forward_f16w.restype = ctypes.c_int
         _fb.fb_nbit_forward.argtypes = [P, P, P, P, i32, i64, P, P, i32, P, i32, i32, P, i64, P,
-                                        i32]
+                                        i32, i32, i32]
         _fb.fb_nbit_forward.restype = ctypes.c_int
+        _fb.fb_hfp8_to_float.argtypes = [ctypes.c_uint8, i32, i32]
+        _fb.fb_hfp8_to_float.restype = ctypes.c_float
+        _fb.fb_float_to_hfp8.argtypes = [ctypes.c_float, i32, i32]
+        _fb.fb_float_to_hfp8.restype = ctypes.c_uint8
     return _fb
 
 
@@ -223,12 +232,49 @@ def tbe_forward_f32(W, w_off, D_off, B, indices, offsets, pooling=POOL_SUM, indi
     return out
 
 
+def hfp8_to_float(codes, ebits: int, ebias: int) -> np.ndarray:
+    """Decodes hfp8 codes (uint8) to fp32 (the C restatement)."""
+    f = lib().orc_hfp8_to_float
+    c = np.asarray(codes, dtype=np.uint8)
+    return np.array([f(int(v), ebits, ebias) for v in c.ravel()], np.float32).reshape(c.shape)
+
+
+def float_to_hfp8(x, ebits: int, ebias: int, max_pos: float) -> np.ndarray:
+    """Encodes fp32 values as hfp8 codes (the C restatement)."""
+    f = lib().orc_float_to_hfp8
+    a = np.asarray(x, dtype=np.float32)
+    return np.array([f(float(v), ebits, ebias, max_pos) for v in a.ravel()],
+                    np.uint8).reshape(a.shape)
+
+
+def hfp8_max_pos(ebits: int, ebias: int) -> float:
+    """The largest magnitude FBGEMM's hfp8 encoder produces: the top exponent
+    field is left unused by encoding (decoding still defines it)."""
+    m = 7 - ebits
+    return float(np.ldexp(2.0 - 2.0 ** -m, (1 << ebits) - 2 - ebias))
+
+
+def fbgemm_hfp8_to_float(codes, ebits: int, ebias: int) -> np.ndarray:
+    """fbgemm::Float8ToFloat_ref on each code."""
+    f = fbgemm().fb_hfp8_to_float
+    c = np.asarray(codes, dtype=np.uint8)
+    return np.array([f(int(v), ebits, ebias) for v in c.ravel()], np.float32).reshape(c.shape)
+
+
+def fbgemm_float_to_hfp8(x, ebits: int, ebias: int) -> np.ndarray:
+    """fbgemm::FloatToFloat8_ref on each value."""
+    f = fbgemm().fb_float_to_hfp8
+    a = np.asarray(x, dtype=np.float32)
+    return np.array([f(float(v), ebits, ebias) for v in a.ravel()], np.uint8).reshape(a.shape)
+
+
 def nbit_row_bytes(ty: int, D: int, row_align: int) -> int:
     return int(lib().orc_nbit_row_bytes(ty, D, row_align))
 
 
 def nbit_forward(W, w_off, tys, D_off, B, indices, offsets, pooling=POOL_SUM,
-                 indice_weights=None, row_align=16, out_f16=True):
+                 indice_weights=None, row_align=16, out_f16=True, fp8_exponent_bits=4,
+                 fp8_exponent_bias=7):
     W = _c(W, np.uint8)
     w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
     indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
@@ -238,7 +284,7 @@ def nbit_forward(W, w_off, tys, D_off, B, indices, offsets, pooling=POOL_SUM,
     out = np.zeros((B, total_D), dtype=np.float16 if out_f16 else np.float32)
     rc = lib().orc_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
                                 _p(offsets), pooling, _p(iw), row_align, int(out_f16), _p(out),
-                                total_D)
+                                total_D, fp8_exponent_bits, fp8_exponent_bias)
     assert rc == 0, f"orc_nbit_forward failed ({rc})"
     return out
 
@@ -438,7 +484,8 @@ def _fbgemm_tbe_forward_f16w(W, w_off, D_off, rows_per_table, B, indices, offset
 
 
 def fbgemm_nbit_forward(W, w_off, tys, D_off, rows_per_table, B, indices, offsets,
-                        pooling=POOL_SUM, indice_weights=None, row_align=16, nthreads=1):
+                        pooling=POOL_SUM, indice_weights=None, row_align=16, nthreads=1,
+                        fp8_exponent_bits=4, fp8_exponent_bias=7):
     W = _c(W, np.uint8)
     w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
     rows = _c(rows_per_table, np.int64)
@@ -449,7 +496,7 @@ def fbgemm_nbit_forward(W, w_off, tys, D_off, rows_per_table, B, indices, offset
     out = np.zeros((B, total_D), dtype=np.float16)
     rc = fbgemm().fb_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
                                   _p(offsets), pooling, _p(iw), row_align, 1, _p(out), total_D,
-                                  _p(rows), nthreads)
+                                  _p(rows), nthreads, fp8_exponent_bits, fp8_exponent_bias)
     assert rc == 0, f"FBGEMM nbit kernel reported failure ({rc})"
     return out
 

@@ -224,6 +224,8 @@ static void run_nbit(const Batch* b, const int32_t* tys) {
           const uint16_t h = orc_float_to_half(rnd_unit() - 0.5f);
           memcpy(row + 2 * d, &h, 2);
         }
+      } else if (tys[t] == ORC_FP8) {
+        /* every byte is a finite hfp8 code */
       } else {
         const uint16_t s = orc_float_to_half(1e-3f + rnd_unit() * 9e-3f);
         const uint16_t bi = orc_float_to_half(rnd_unit() * 0.2f - 0.1f);
@@ -239,9 +241,9 @@ static void run_nbit(const Batch* b, const int32_t* tys) {
   for (int pooling = 0; pooling < 2; ++pooling)
     for (int f16 = 0; f16 < 2; ++f16) {
       CHECK(orc_nbit_forward(W, w_off, tys8, b->D_off, b->T, b->B, b->indices, b->offsets,
-                             pooling, NULL, 16, f16, out, total_D) == 0);
+                             pooling, NULL, 16, f16, out, total_D, 4, 7) == 0);
       CHECK(orc_nbit_forward(W, w_off, tys8, b->D_off, b->T, b->B, b->indices, b->offsets,
-                             pooling, iw, 16, f16, out, total_D) == 0);
+                             pooling, iw, 16, f16, out, total_D, 5, 15) == 0);
     }
   free(W);
   free(w_off);
@@ -285,13 +287,22 @@ int main(void) {
   const int32_t dims3[3] = {4, 32, 128};
   const int32_t dims5[5] = {8, 16, 24, 64, 256};
   const int32_t tys5[5] = {ORC_FP32, ORC_FP16, ORC_INT8, ORC_INT4, ORC_INT2};
+  const int32_t tys5b[5] = {ORC_FP8, ORC_FP16, ORC_INT8, ORC_INT4, ORC_FP8};
   for (int rep = 0; rep < 24; ++rep) {
     Batch a = make_batch(3, 17 + 13 * rep, 9 + rep, 20, dims3);
     run_tbe(&a);
     free_batch(&a);
     Batch c = make_batch(5, 13 + 5 * rep, 7, 25, dims5);
-    run_nbit(&c, tys5);
+    run_nbit(&c, rep % 2 ? tys5b : tys5);
     free_batch(&c);
+  }
+  /* hfp8: every code decodes to a value that encodes back to the code */
+  for (int cfg = 0; cfg < 2; ++cfg) {
+    const int ebits = cfg ? 5 : 4, ebias = cfg ? 15 : 7, m = 7 - ebits;
+    const float max_pos = ldexpf(2.0f - ldexpf(1.0f, -m), (1 << ebits) - 1 - ebias);
+    for (int v = 0; v < 256; ++v)
+      CHECK(orc_float_to_hfp8(orc_hfp8_to_float((uint8_t)v, ebits, ebias), ebits, ebias,
+                              max_pos) == (uint8_t)v);
   }
   /* edge cases: all bags empty (N = 0), one bag, no bags */
   Batch e = make_batch(3, 5, 9, 100, dims3);

@@ -8,11 +8,13 @@ import torch
 import oracle as orc
 
 
-def build_weights(rng: np.random.Generator, tys, dims, rows, row_align: int = 16):
+def build_weights(rng: np.random.Generator, tys, dims, rows, row_align: int = 16,
+                  fp8_exponent_bits: int = 4, fp8_exponent_bias: int = 7):
     """uint8 buffer with every table's padded rows, plus weights_offsets.
 
     Quantized rows: fp16 scale in [1e-3, 1e-2), fp16 bias in [-0.1, 0.1),
-    uniform codes; FP16/FP32 rows: values in [-0.01, 0.01)."""
+    uniform codes; FP16/FP32 rows: values in [-0.01, 0.01); FP8 rows: values
+    in [-0.5, 0.5) rounded to the nearest hfp8 code."""
     strides = [orc.nbit_row_bytes(ty, D, row_align) for ty, D in zip(tys, dims)]
     sizes = [E * s for E, s in zip(rows, strides)]
     w_off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
@@ -28,6 +30,10 @@ def build_weights(rng: np.random.Generator, tys, dims, rows, row_align: int = 16
         elif ty == orc.FP16:
             v = rng.uniform(-0.01, 0.01, size=(E, D)).astype(np.float16)
             tab[:, : 2 * D] = v.view(np.uint8).reshape(E, 2 * D)
+        elif ty == orc.FP8:
+            v = rng.uniform(-0.5, 0.5, size=(E, D)).astype(np.float32)
+            tab[:, :D] = orc.float_to_hfp8(v, fp8_exponent_bits, fp8_exponent_bias,
+                                           orc.hfp8_max_pos(fp8_exponent_bits, fp8_exponent_bias))
         else:
             v = rng.uniform(-0.01, 0.01, size=(E, D)).astype(np.float32)
             tab[:, : 4 * D] = v.view(np.uint8).reshape(E, 4 * D)

@@ -6,8 +6,9 @@ chosen so that a dropped term, a wrong index or a transposed operand fails.
   (torch's port of the fbgemm jagged ops), bit-exact;
 * TBE forward: FBGEMM's exported CPU SpMDM kernel (the CPU kernel fbgemm_gpu's
   CPU TBE op wraps), bit-exact; F.embedding_bag within fp32 rounding;
-* nbit: FBGEMM's exported 8-bit / N-bit / fp16 CPU kernels with the TBE row
-  layout (scale_bias_last=false), fp16 output;
+* nbit: FBGEMM's exported 8-bit / N-bit / fp16 / FP8 CPU kernels with the TBE
+  row layout (scale_bias_last=false), fp16 output; the hfp8 decode and encode
+  against FBGEMM's Float8ToFloat_ref / FloatToFloat8_ref;
 * transpose: numpy stable argsort + unique (brute force), bit-exact;
 * rowwise Adagrad: torch autograd of embedding_bag for the row gradient and
   the update rule evaluated with torch fp32 ops.
@@ -178,6 +179,61 @@ def test_nbit_vs_fbgemm_cpu(ty, pooling):
     exp = orc.fbgemm_nbit_forward(buf, w_off, [ty, ty], inp.D_offsets, rows, inp.B, inp.indices,
                                   inp.offsets, pooling, nthreads=2)
     # Same terms, same order, same fp32 fma steps: bit-exact fp16 output.
+    np.testing.assert_array_equal(got.view(np.uint16), exp.view(np.uint16))
+
+
+HFP8_CONFIGS = [(4, 7), (5, 15), (3, 3), (4, 8), (2, 1), (5, 20)]  # (exponent bits, bias)
+
+
+@pytest.mark.parametrize("ebits,ebias", HFP8_CONFIGS)
+def test_hfp8_decode_vs_fbgemm(ebits, ebias):
+    """Every one of the 256 codes decodes to FBGEMM's Float8ToFloat_ref value, bit for bit."""
+    codes = np.arange(256, dtype=np.uint8)
+    got = orc.hfp8_to_float(codes, ebits, ebias)
+    exp = orc.fbgemm_hfp8_to_float(codes, ebits, ebias)
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("ebits,ebias", HFP8_CONFIGS)
+def test_hfp8_encode_vs_fbgemm(ebits, ebias):
+    """The encoder gives FBGEMM's FloatToFloat8_ref code on every code's value,
+    on the midpoints between neighbouring codes (ties to even) and one fp32
+    ulp either side of them, on normal and log-uniform samples from 1e-12 to
+    past the largest code, on subnormal-range values, signed zeros and values
+    past the clamp."""
+    rng = np.random.default_rng(ebits * 100 + ebias)
+    mx = orc.hfp8_max_pos(ebits, ebias)
+    vals = orc.hfp8_to_float(np.arange(256, dtype=np.uint8), ebits, ebias)
+    pos = np.unique(np.abs(vals))
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    around = np.concatenate([np.nextafter(mids, np.float32(np.inf)),
+                             np.nextafter(mids, np.float32(0))])
+    normal = (rng.standard_normal(5000) * mx / 3).astype(np.float32)
+    logs = np.exp(rng.uniform(np.log(1e-12), np.log(mx * 4), 5000))
+    logs = (logs * rng.choice([-1, 1], logs.size)).astype(np.float32)
+    edge = np.array([0.0, -0.0, mx, -mx, mx * 1.01, 1e30, -1e30, 1e-40, -1e-40], np.float32)
+    x = np.concatenate([vals, mids, -mids, around, -around, normal, logs, edge])
+    np.testing.assert_array_equal(orc.float_to_hfp8(x, ebits, ebias, mx),
+                                  orc.fbgemm_float_to_hfp8(x, ebits, ebias))
+
+
+@pytest.mark.parametrize("ebits,ebias", [(4, 7), (5, 15)])
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nbit_fp8_vs_fbgemm_cpu(ebits, ebias, pooling, weighted):
+    """FP8 tables: FBGEMM's GenerateEmbeddingSpMDMFP8WithStrides, bit-exact fp16 output."""
+    rng = np.random.default_rng(ebits + 10 * pooling + 100 * weighted)
+    dims, rows = [32, 64], [40, 70]
+    inp = random_tbe(rng, 2, 15, dims, rows, 20)
+    buf, w_off = build_weights(rng, [orc.FP8] * 2, dims, rows, fp8_exponent_bits=ebits,
+                               fp8_exponent_bias=ebias)
+    iw = rng.uniform(-1, 1, inp.N).astype(np.float32) if weighted else None
+    got = orc.nbit_forward(buf, w_off, [orc.FP8] * 2, inp.D_offsets, inp.B, inp.indices,
+                           inp.offsets, pooling, indice_weights=iw, fp8_exponent_bits=ebits,
+                           fp8_exponent_bias=ebias)
+    exp = orc.fbgemm_nbit_forward(buf, w_off, [orc.FP8] * 2, inp.D_offsets, rows, inp.B,
+                                  inp.indices, inp.offsets, pooling, indice_weights=iw,
+                                  nthreads=2, fp8_exponent_bits=ebits, fp8_exponent_bias=ebias)
     np.testing.assert_array_equal(got.view(np.uint16), exp.view(np.uint16))
 
 
