@@ -57,6 +57,7 @@ extern "C" {
 #define MX_SPARSE_INT4 3
 #define MX_SPARSE_INT2 4
 #define MX_SPARSE_BF16 5
+#define MX_SPARSE_FP8 6
 
 /* fbgemm_gpu PoolingMode values. */
 #define MX_POOL_SUM 0
@@ -79,8 +80,11 @@ extern "C" {
  * `uint64_t seed` at the same position, and mx_set_status_mailbox takes
  * MX_STATUS_WORDS words where 0.1.0 took one (not binary compatible).
  * 0.3.0: eager TBE backward calls keep their sort counters in a per-stream
- * region (see above); mx_test_force_workspace_counters added. */
-#define MX_FBGEMM_VERSION 300
+ * region (see above); mx_test_force_workspace_counters added.  0.4.0:
+ * mx_nbit_forward takes max_float8_D, fp8_exponent_bits and
+ * fp8_exponent_bias after row_alignment (FP8 tables; not binary compatible);
+ * mx_float_to_hfp8 and mx_hfp8_to_float added. */
+#define MX_FBGEMM_VERSION 400
 int mx_version(void);
 
 /* Thread-local text of the last failing call on this thread ("" if none). */
@@ -407,6 +411,17 @@ int mx_dequantize_fused_nbit_rowwise(const uint8_t* in, int64_t rows, int64_t D,
                                      int32_t bit_rate, void* out, int32_t out_dtype,
                                      void* stream);
 
+/* Serve fbgemm::FloatToHFP8Quantized and fbgemm::HFP8QuantizedToFloat: fp32
+ * <-> hfp8 codes, one byte per element (sign, ebits exponent bits, 7 - ebits
+ * mantissa bits, bias exponent_bias, subnormals at exponent field 0; FBGEMM's
+ * FloatToFloat8_ref / Float8ToFloat_ref).  Encoding clamps |x| to max_pos
+ * (and to the largest code), then rounds to the nearest code, ties to even;
+ * NaN encodes as the clamp.  1 <= ebits <= 7, 0 <= exponent_bias <= 120. */
+int mx_float_to_hfp8(const float* in, int64_t n, int32_t ebits, int32_t exponent_bias,
+                     float max_pos, uint8_t* out, void* stream);
+int mx_hfp8_to_float(const uint8_t* in, int64_t n, int32_t ebits, int32_t exponent_bias,
+                     float* out, void* stream);
+
 /* ---- TBE nbit inference forward ---------------------------------------- */
 
 /* Padded size in bytes of one row of a table of type `ty` and dim D:
@@ -425,6 +440,10 @@ int64_t mx_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_alignment);
  *   the even element in the low nibble.  value = scale*q + bias (fp32).
  *   Codes fill whole bytes: every INT4 table's D is even and every INT2
  *   table's D a multiple of 4 (checked on the maxima; EINVAL otherwise).
+ *   FP8 rows are D hfp8 codes (sign, fp8_exponent_bits exponent bits,
+ *   7 - fp8_exponent_bits mantissa bits, bias fp8_exponent_bias, subnormals
+ *   at exponent field 0; fbgemm's Float8ToFloat_ref); max_float8_D > 0 needs
+ *   1 <= fp8_exponent_bits <= 7 and 0 <= fp8_exponent_bias <= 120.
  *   output_dtype    MX_SPARSE_FP32 or MX_SPARSE_FP16 (round to nearest even)
  *   out             [B, total_D] */
 int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
@@ -433,6 +452,7 @@ int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
                     int32_t max_float16_D, int32_t max_float32_D, const void* indices,
                     const void* offsets, int32_t index_bytes, int32_t pooling_mode,
                     const float* indice_weights, int32_t output_dtype, int32_t row_alignment,
+                    int32_t max_float8_D, int32_t fp8_exponent_bits, int32_t fp8_exponent_bias,
                     void* out, int64_t total_D, void* stream);
 
 #ifdef __cplusplus

@@ -49,7 +49,8 @@ def max_dims(tys, dims):
 
 def nbit_forward_gpu(dev, W: torch.Tensor, w_off, tys, dims, indices, offsets, pooling: int,
                      out_f16: bool = True, indice_weights=None, row_align: int = 16,
-                     index_dtype=torch.int64):
+                     index_dtype=torch.int64, fp8_exponent_bits: int = 4,
+                     fp8_exponent_bias: int = 7):
     T = len(tys)
     D_off = np.concatenate([[0], np.cumsum(dims)]).astype(np.int32)
     m2, m4, m8, m16, m32 = max_dims(tys, dims)
@@ -60,7 +61,9 @@ def nbit_forward_gpu(dev, W: torch.Tensor, w_off, tys, dims, indices, offsets, p
         torch.as_tensor(D_off, device=dev), int(D_off[-1]), m2, m4, m8, m16, m32,
         torch.as_tensor(indices).to(dev, index_dtype), torch.as_tensor(offsets).to(dev, index_dtype),
         pooling, None if indice_weights is None else torch.as_tensor(indice_weights).to(dev),
-        1 if out_f16 else 0, None, None, row_align)
+        1 if out_f16 else 0, None, None, row_align,
+        max([D for t, D in zip(tys, dims) if t == orc.FP8], default=0), fp8_exponent_bits,
+        fp8_exponent_bias)
 
 
 def build_weights_gpu(dev, tys, dims, rows, seed: int, row_align: int = 16):
@@ -124,3 +127,21 @@ def assert_nbit_close(got, exp, max_ulps: int = 1, min_exact: float = 0.9):
     else:
         np.testing.assert_allclose(g.astype(np.float32), e.astype(np.float32), rtol=1e-5,
                                    atol=1e-5)
+
+
+def hfp8_probe_values(rng: np.random.Generator, ebits: int, ebias: int) -> np.ndarray:
+    """fp32 values that exercise an hfp8 encoder: every code's value, the
+    midpoints between neighbouring codes (ties) and one fp32 ulp either side
+    of them, normal and log-uniform samples from 1e-12 to past the largest
+    code, signed zeros, fp32 subnormals and values past the clamp."""
+    mx = orc.hfp8_max_pos(ebits, ebias)
+    vals = orc.hfp8_to_float(np.arange(256, dtype=np.uint8), ebits, ebias)
+    pos = np.unique(np.abs(vals))
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    around = np.concatenate([np.nextafter(mids, np.float32(np.inf)),
+                             np.nextafter(mids, np.float32(0))])
+    normal = (rng.standard_normal(5000) * mx / 3).astype(np.float32)
+    logs = np.exp(rng.uniform(np.log(1e-12), np.log(min(mx * 4, 1e38)), 5000))
+    logs = (logs * rng.choice([-1, 1], logs.size)).astype(np.float32)
+    edge = np.array([0.0, -0.0, mx, -mx, mx * 1.01, 1e30, -1e30, 1e-40, -1e-40], np.float32)
+    return np.concatenate([vals, mids, -mids, around, -around, normal, logs, edge])

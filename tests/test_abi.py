@@ -43,9 +43,10 @@ def test_every_declared_symbol_is_exported(lib):
 def test_version_and_last_error(lib):
     # The library reports the version its header declares (0.2.0 changed the
     # backward's stochastic-rounding argument from a seed to mx_rng_state*;
-    # 0.3.0 added the backward's per-stream counter region).
+    # 0.3.0 added the backward's per-stream counter region; 0.4.0 the FP8
+    # arguments of mx_nbit_forward and the hfp8 codecs).
     hdr = re.search(r"#define MX_FBGEMM_VERSION (\d+)", HEADER.read_text())
-    assert hdr and lib.mx_version() == int(hdr.group(1)) == 300
+    assert hdr and lib.mx_version() == int(hdr.group(1)) == 400
     lib.mx_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mx_last_error(), bytes)
 
@@ -108,16 +109,28 @@ def test_bad_arguments_rejected_before_any_launch(lib):
     assert f(None, 1, None, None, 0, 0, 128, None, None, 8, 0, None, None, 0, 128, None) == 0
     g = lib.mx_nbit_forward
     g.argtypes = [P, P, P, P, i32, i64] + [i32] * 5 + \
-        [P, P, i32, i32, P, i32, i32, P, i64, P]
-    assert g(None, None, None, None, 1, 1, 0, 0, 2048, 0, 0, None, None, 4, 0, None, 1, 16, None,
-             2048, None) == -1  # max D above 1024
+        [P, P, i32, i32, P, i32, i32, i32, i32, i32, P, i64, P]
+    assert g(None, None, None, None, 1, 1, 0, 0, 2048, 0, 0, None, None, 4, 0, None, 1, 16,
+             0, -1, -1, None, 2048, None) == -1  # max D above 1024
     assert b"1024" in lib.mx_last_error()
-    assert g(None, None, None, None, 1, 1, 0, 29, 0, 0, 0, None, None, 4, 0, None, 1, 16, None,
-             29, None) == -1  # odd INT4 D: codes would not fill whole bytes
+    assert g(None, None, None, None, 1, 1, 0, 29, 0, 0, 0, None, None, 4, 0, None, 1, 16,
+             0, -1, -1, None, 29, None) == -1  # odd INT4 D: codes would not fill whole bytes
     assert b"INT4 D must be even" in lib.mx_last_error()
-    assert g(None, None, None, None, 1, 1, 6, 0, 0, 0, 0, None, None, 4, 0, None, 1, 16, None,
-             6, None) == -1  # INT2 D not a multiple of 4
+    assert g(None, None, None, None, 1, 1, 6, 0, 0, 0, 0, None, None, 4, 0, None, 1, 16,
+             0, -1, -1, None, 6, None) == -1  # INT2 D not a multiple of 4
     assert b"INT2 D a multiple of 4" in lib.mx_last_error()
+    for ebits, bias in ((0, 7), (8, 7), (4, -1), (4, 121)):  # FP8 formats outside the served range
+        assert g(None, None, None, None, 1, 1, 0, 0, 0, 0, 0, None, None, 4, 0, None, 1, 16,
+                 64, ebits, bias, None, 64, None) == -1
+        assert b"fp8_exponent_bits" in lib.mx_last_error()
+    e = lib.mx_float_to_hfp8
+    e.argtypes = [P, i64, i32, i32, f32, P, P]
+    assert e(None, 8, 4, 7, 0.0, None, None) == -1 and b"max_pos" in lib.mx_last_error()
+    assert e(None, 8, 9, 7, 240.0, None, None) == -1 and b"ebits" in lib.mx_last_error()
+    assert e(None, 0, 4, 7, 240.0, None, None) == 0  # nothing to convert
+    d = lib.mx_hfp8_to_float
+    d.argtypes = [P, i64, i32, i32, P, P]
+    assert d(None, 8, 4, 130, None, None) == -1 and b"exponent_bias" in lib.mx_last_error()
     h = lib.mx_tbe_backward_rowwise_adagrad
     h.restype = ctypes.c_int
     h.argtypes = [P, i32, P, P, i32, i64, i32, P, i32, P, P, i32, i64, i32, P, P, i64, P, P,

@@ -55,7 +55,28 @@ def test_fused_nbit_round_trip_bits(dev, bits, D):
     np.testing.assert_array_equal(qh.cpu().numpy(), orc.quantize_fused_nbit(xh.float().numpy(), bits))
 
 
-@pytest.mark.parametrize("ty", ["INT8", "INT4", "INT2", "FP16"])
+@pytest.mark.parametrize("ebits,ebias", [(4, 7), (5, 15), (3, 3), (2, 1), (7, 0), (1, 0)])
+def test_hfp8_codecs(dev, ebits, ebias):
+    """fbgemm::HFP8QuantizedToFloat on all 256 codes and FloatToHFP8Quantized on
+    the encoder probe values (ties, ulps around them, subnormal range, zeros,
+    values past the clamp), bit-exact to the oracle (itself bit-exact to
+    FBGEMM's Float8ToFloat_ref / FloatToFloat8_ref)."""
+    from nbit_helpers import hfp8_probe_values
+
+    print(f"[case] hfp8 codecs ebits={ebits} bias={ebias}", flush=True)
+    codes = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    dec = torch.ops.fbgemm.HFP8QuantizedToFloat(torch.from_numpy(codes).to(dev), ebits, ebias)
+    assert dec.dtype == torch.float32 and dec.shape == (16, 16)
+    np.testing.assert_array_equal(dec.cpu().numpy().view(np.uint32),
+                                  orc.hfp8_to_float(codes, ebits, ebias).view(np.uint32))
+    x = hfp8_probe_values(np.random.default_rng(ebits * 31 + ebias), ebits, ebias)
+    mx = orc.hfp8_max_pos(ebits, ebias)
+    enc = torch.ops.fbgemm.FloatToHFP8Quantized(torch.from_numpy(x).to(dev), ebits, ebias, mx)
+    assert enc.dtype == torch.uint8
+    np.testing.assert_array_equal(enc.cpu().numpy(), orc.float_to_hfp8(x, ebits, ebias, mx))
+
+
+@pytest.mark.parametrize("ty", ["INT8", "INT4", "INT2", "FP16", "FP8"])
 def test_inference_module_assign_and_lookup(dev, ty):
     """quantize_rows' TBE layout decodes (through the nbit lookup) to the
     codec's own dequantization, and the module matches the oracle."""
@@ -82,6 +103,8 @@ def test_inference_module_assign_and_lookup(dev, ty):
         d = w.shape[1]
         if sty == SparseType.FP16:
             exp = w.half().float().numpy()
+        elif sty == SparseType.FP8:  # the module's default format, e4m3 with bias 7
+            exp = orc.hfp8_to_float(orc.float_to_hfp8(w.numpy(), 4, 7, orc.hfp8_max_pos(4, 7)), 4, 7)
         else:
             q = orc.quantize_fused_nbit(w.numpy(), sty.bit_rate())
             exp = orc.dequantize_fused_nbit(q, sty.bit_rate(), d)

@@ -45,12 +45,39 @@ def test_single_type(dev, ty, D):
         _check(got, exp)
 
 
+@pytest.mark.parametrize("ebits,ebias", [(4, 7), (5, 15), (3, 3)])
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 96, 128, 256, 520])
+def test_fp8_tables(dev, ebits, ebias, D):
+    """FP8 (hfp8) tables: every code decodes exactly and the rows add in index
+    order, as in the oracle (bit-exact to FBGEMM's FP8 CPU kernel), so SUM and
+    MEAN, weighted or not, fp16 or fp32 out, match bit for bit; D = 24 and
+    520 take the general path."""
+    print(f"[case] nbit fp8 ebits={ebits} bias={ebias} D={D}", flush=True)
+    rng = np.random.default_rng(ebits * 1000 + D)
+    inp = random_tbe(rng, 2, 19, [D, D], [37, 5], 25)
+    tys = [orc.FP8, orc.FP8]
+    buf, w_off = build_weights(rng, tys, inp.D, inp.E, fp8_exponent_bits=ebits,
+                               fp8_exponent_bias=ebias)
+    iw = rng.uniform(-1, 1, size=inp.N).astype(np.float32)
+    for pooling, weights, out_f16 in ((0, None, True), (1, None, True), (0, iw, False),
+                                      (1, iw, True)):
+        exp = orc.nbit_forward(buf, w_off, tys, inp.D_offsets, inp.B, inp.indices, inp.offsets,
+                               pooling, indice_weights=weights, out_f16=out_f16,
+                               fp8_exponent_bits=ebits, fp8_exponent_bias=ebias)
+        got = nbit_forward_gpu(dev, torch.from_numpy(buf).to(dev), w_off, tys, inp.D,
+                               inp.indices, inp.offsets, pooling, out_f16=out_f16,
+                               indice_weights=weights, fp8_exponent_bits=ebits,
+                               fp8_exponent_bias=ebias).cpu().numpy()
+        view = np.uint16 if out_f16 else np.uint32
+        np.testing.assert_array_equal(got.view(view), exp.view(view))
+
+
 def test_mixed_types_weighted_fp32_out(dev):
     print("[case] nbit mixed types, weighted, fp32 out, int32 indices", flush=True)
     rng = np.random.default_rng(5)
-    tys = [orc.INT8, orc.INT4, orc.FP16, orc.INT2, orc.FP32, orc.INT4]
-    dims = [128, 64, 32, 256, 16, 512]
-    rows = [100, 200, 50, 10, 30, 40]
+    tys = [orc.INT8, orc.INT4, orc.FP16, orc.INT2, orc.FP32, orc.INT4, orc.FP8]
+    dims = [128, 64, 32, 256, 16, 512, 64]
+    rows = [100, 200, 50, 10, 30, 40, 60]
     inp = random_tbe(rng, len(tys), 33, dims, rows, 30)
     buf, w_off = build_weights(rng, tys, dims, rows)
     iw = rng.uniform(0, 1, size=inp.N).astype(np.float32)

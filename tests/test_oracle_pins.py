@@ -20,7 +20,7 @@ import torch
 
 import oracle as orc
 from mx_fbgemm import bench_inputs
-from nbit_helpers import build_weights
+from nbit_helpers import build_weights, hfp8_probe_values
 from tbe_helpers import random_tbe, weight_offsets
 
 
@@ -202,18 +202,8 @@ def test_hfp8_encode_vs_fbgemm(ebits, ebias):
     past the largest code, on subnormal-range values, signed zeros and values
     past the clamp."""
     rng = np.random.default_rng(ebits * 100 + ebias)
-    mx = orc.hfp8_max_pos(ebits, ebias)
-    vals = orc.hfp8_to_float(np.arange(256, dtype=np.uint8), ebits, ebias)
-    pos = np.unique(np.abs(vals))
-    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
-    around = np.concatenate([np.nextafter(mids, np.float32(np.inf)),
-                             np.nextafter(mids, np.float32(0))])
-    normal = (rng.standard_normal(5000) * mx / 3).astype(np.float32)
-    logs = np.exp(rng.uniform(np.log(1e-12), np.log(mx * 4), 5000))
-    logs = (logs * rng.choice([-1, 1], logs.size)).astype(np.float32)
-    edge = np.array([0.0, -0.0, mx, -mx, mx * 1.01, 1e30, -1e30, 1e-40, -1e-40], np.float32)
-    x = np.concatenate([vals, mids, -mids, around, -around, normal, logs, edge])
-    np.testing.assert_array_equal(orc.float_to_hfp8(x, ebits, ebias, mx),
+    x = hfp8_probe_values(rng, ebits, ebias)
+    np.testing.assert_array_equal(orc.float_to_hfp8(x, ebits, ebias, orc.hfp8_max_pos(ebits, ebias)),
                                   orc.fbgemm_float_to_hfp8(x, ebits, ebias))
 
 

@@ -173,10 +173,64 @@ __global__ void __launch_bounds__(256)
 
 dim3 rows_grid(int64_t rows) { return dim3(static_cast<uint32_t>(ceil_div(rows, 4))); }
 
+// hfp8 codecs: elementwise, grid-stride.
+__global__ void __launch_bounds__(256)
+    float_to_hfp8_kernel(const float* __restrict__ in, int64_t n, Hfp8 f, float clamp,
+                         uint8_t* __restrict__ out) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    out[i] = static_cast<uint8_t>(f.encode(in[i], clamp));
+}
+
+__global__ void __launch_bounds__(256)
+    hfp8_to_float_kernel(const uint8_t* __restrict__ in, int64_t n, Hfp8 f,
+                         float* __restrict__ out) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    out[i] = f.decode(in[i]);
+}
+
+dim3 elementwise_grid(int64_t n) {
+  const int64_t b = ceil_div(n, 256);
+  return dim3(static_cast<uint32_t>(b < 8192 ? b : 8192));
+}
+
 }  // namespace
 }  // namespace mx
 
 using namespace mx;
+
+extern "C" int mx_float_to_hfp8(const float* in, int64_t n, int32_t ebits, int32_t exponent_bias,
+                                float max_pos, uint8_t* out, void* stream) {
+  clear_error();
+  MX_REQUIRE(n >= 0, "negative size");
+  MX_REQUIRE(hfp8_format_ok(ebits, exponent_bias),
+             "hfp8 needs 1 <= ebits <= 7 and 0 <= exponent_bias <= 120 (got %d, %d)", ebits,
+             exponent_bias);
+  MX_REQUIRE(max_pos > 0.0f, "max_pos must be positive");
+  if (n == 0) return MX_OK;
+  MX_REQUIRE(in && out, "null pointer argument");
+  const Hfp8 f = Hfp8::make(ebits, exponent_bias);
+  float_to_hfp8_kernel<<<elementwise_grid(n), 256, 0, as_stream(stream)>>>(
+      in, n, f, max_pos < f.max_code ? max_pos : f.max_code, out);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+extern "C" int mx_hfp8_to_float(const uint8_t* in, int64_t n, int32_t ebits,
+                                int32_t exponent_bias, float* out, void* stream) {
+  clear_error();
+  MX_REQUIRE(n >= 0, "negative size");
+  MX_REQUIRE(hfp8_format_ok(ebits, exponent_bias),
+             "hfp8 needs 1 <= ebits <= 7 and 0 <= exponent_bias <= 120 (got %d, %d)", ebits,
+             exponent_bias);
+  if (n == 0) return MX_OK;
+  MX_REQUIRE(in && out, "null pointer argument");
+  hfp8_to_float_kernel<<<elementwise_grid(n), 256, 0, as_stream(stream)>>>(
+      in, n, Hfp8::make(ebits, exponent_bias), out);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
 
 extern "C" int mx_quantize_fused8bit_rowwise(const void* in, int32_t in_dtype, int64_t rows,
                                              int64_t D, uint8_t* out, void* stream) {

@@ -6,6 +6,7 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 
@@ -103,5 +104,67 @@ template <typename I>
 __device__ __forceinline__ int64_t ld_index(const void* p, int64_t i) {
   return static_cast<int64_t>(reinterpret_cast<const I*>(p)[i]);
 }
+
+// hfp8: the 8-bit float of fbgemm's FP8 TBE tables and HFP8 codecs (FBGEMM's
+// Float8ToFloat_ref / FloatToFloat8_ref, torch/include/fbgemm/
+// FbgemmConvert.h:181-200): a sign bit, `ebits` exponent bits and
+// m = 7 - ebits mantissa bits, exponent bias `bias`; a code of exponent field
+// E > 0 is 2^(E - bias) (1 + M / 2^m), of E = 0 the subnormal M 2^(1 - bias - m).
+// With 1 <= ebits <= 7 and 0 <= bias <= 120 every code is a normal fp32
+// number or zero, so decoding is exact and denormal-free.
+inline bool hfp8_format_ok(int ebits, int bias) {
+  return ebits >= 1 && ebits <= 7 && bias >= 0 && bias <= 120;
+}
+
+struct Hfp8 {
+  int32_t m;        // mantissa bits
+  int32_t bias;
+  int32_t exp_off;  // 127 - bias: added to a code's exponent field gives fp32's
+  float sub_scale;  // 2^(1 - bias - m), the subnormal quantum
+  float sub_inv;    // 2^(bias + m - 1)
+  float min_normal; // 2^(1 - bias)
+  float max_code;   // the largest magnitude (every exponent field a number)
+
+  static Hfp8 make(int ebits, int bias) {
+    Hfp8 f;
+    f.m = 7 - ebits;
+    f.bias = bias;
+    f.exp_off = 127 - bias;
+    f.sub_scale = ldexpf(1.0f, 1 - bias - f.m);
+    f.sub_inv = ldexpf(1.0f, bias + f.m - 1);
+    f.min_normal = ldexpf(1.0f, 1 - bias);
+    f.max_code = ldexpf(2.0f - ldexpf(1.0f, -f.m), (1 << ebits) - 1 - bias);
+    return f;
+  }
+
+  // Code c (0..255) as fp32: a nonzero exponent field is built directly as
+  // fp32 bits (the magnitude bits under fp32's exponent field, rebased), a
+  // zero one as M times the quantum; the sign bit last (0x80 is -0).
+  __device__ __forceinline__ float decode(uint32_t c) const {
+    const uint32_t mag = c & 0x7fu;
+    const float normal =
+        __uint_as_float((mag << (23 - m)) + (static_cast<uint32_t>(exp_off) << 23));
+    const float v = (mag >> m) != 0u ? normal : static_cast<float>(mag) * sub_scale;
+    return __uint_as_float(__float_as_uint(v) | ((c & 0x80u) << 24));
+  }
+
+  // The code nearest to x (ties to even) after |x| is clamped to `clamp`
+  // (at most max_code): below min_normal on the subnormal grid, else on the
+  // grid of x's binade, a round-up into the next binade carrying into the
+  // exponent field.  NaN encodes as the clamp.
+  __device__ __forceinline__ uint32_t encode(float x, float clamp) const {
+    const uint32_t s = (__float_as_uint(x) >> 24) & 0x80u;
+    const float a = fminf(fabsf(x), clamp);
+    if (a < min_normal) return s | static_cast<uint32_t>(rintf(a * sub_inv));
+    const int be = static_cast<int>((__float_as_uint(a) >> 23) & 0xffu) - 127;
+    const uint32_t k = static_cast<uint32_t>(rintf(ldexpf(a, m - be)));  // 2^m .. 2^(m+1)
+    uint32_t e = static_cast<uint32_t>(be + bias), mant = k - (1u << m);
+    if (mant == (1u << m)) {
+      e += 1u;
+      mant = 0u;
+    }
+    return s | (e << m) | mant;
+  }
+};
 
 }  // namespace mx

@@ -48,6 +48,7 @@ struct NbitArgs {
   int32_t row_align;
   int32_t out_f16;
   int32_t served;          // bit ty set: the call launches type ty
+  Hfp8 fp8;                // FP8 tables' format (when served)
   uint32_t nchk;           // trailing blocks that check the tables (T in the first launch, else 0)
   unsigned int* mailbox;   // host-visible status words of the device, may be null
 };
@@ -71,6 +72,7 @@ __device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, 
     case MX_SPARSE_INT8: u = D + 4ll; break;
     case MX_SPARSE_INT4: u = D / 2 + 4ll; break;
     case MX_SPARSE_INT2: u = D / 4 + 4ll; break;
+    case MX_SPARSE_FP8: u = D; break;
     default: return -1;
   }
   if (align > 1) u = (u + align - 1) / align * align;
@@ -85,7 +87,8 @@ __device__ __host__ __forceinline__ bool rows_aligned(int64_t w_off, int64_t str
 
 __device__ __forceinline__ bool table_ok(int32_t ty, int32_t D, int32_t served, int64_t w_off,
                                          int32_t align) {
-  if (ty < 0 || ty > MX_SPARSE_INT2 || ((served >> ty) & 1) == 0 || D < 0) return false;
+  if (ty < 0 || ty > MX_SPARSE_FP8 || ty == MX_SPARSE_BF16 || ((served >> ty) & 1) == 0 || D < 0)
+    return false;
   if (!rows_aligned(w_off, row_bytes_of(ty, D, align))) return false;
   if (ty == MX_SPARSE_INT4) return whole_bytes<MX_SPARSE_INT4>(D);
   if (ty == MX_SPARSE_INT2) return whole_bytes<MX_SPARSE_INT2>(D);
@@ -119,6 +122,12 @@ struct TyInfo<MX_SPARSE_INT2> {
   static constexpr int kBits = 2;
   static constexpr bool kQ = true;
 };
+template <>
+struct TyInfo<MX_SPARSE_FP8> {
+  static constexpr int kBits = 8;
+  static constexpr bool kQ = false;
+};
+
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
@@ -322,6 +331,12 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
               for (int j = 0; j < EPW; ++j)
                 if (q * EPW + j < CPL) acc[q * EPW + j] = __builtin_fmaf(scale, f[j], acc[q * EPW + j]);
             }
+          } else if constexpr (TY == MX_SPARSE_FP8) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+              const float v = a.fp8.decode((codes[u][e >> 2] >> ((e & 3) * 8)) & 0xffu);
+              acc[e] = weighted ? __builtin_fmaf(wgt, v, acc[e]) : acc[e] + v;
+            }
           } else if constexpr (TY == MX_SPARSE_FP16) {
             // acc += w * h with the fp16 converted inside the FMA (w = 1
             // unweighted: exactly acc + float(h)).
@@ -398,9 +413,9 @@ template <typename I, int G>
 __device__ void bag_generic(const NbitArgs& a, int32_t ty, int32_t D,
                             const uint8_t* __restrict__ Wt, int64_t stride, int64_t start,
                             int64_t end, int64_t out_col, int k) {
-  const int bits = ty == MX_SPARSE_FP32 ? 32 : ty == MX_SPARSE_FP16 ? 16 : ty == MX_SPARSE_INT8 ? 8
-                 : ty == MX_SPARSE_INT4 ? 4 : 2;
-  const bool q = bits <= 8;
+  const int bits = ty == MX_SPARSE_FP32 ? 32 : ty == MX_SPARSE_FP16 ? 16
+                 : (ty == MX_SPARSE_INT8 || ty == MX_SPARSE_FP8) ? 8 : ty == MX_SPARSE_INT4 ? 4 : 2;
+  const bool q = ty == MX_SPARSE_INT8 || ty == MX_SPARSE_INT4 || ty == MX_SPARSE_INT2;
   const int64_t L = end - start;
   const float inv = (a.pooling == MX_POOL_MEAN && L > 0) ? 1.0f / static_cast<float>(L) : 1.0f;
   for (int cb = k * 8; cb < D; cb += G * 8) {
@@ -424,6 +439,8 @@ __device__ void bag_generic(const NbitArgs& a, int32_t ty, int32_t D,
         float v;
         if (bits == 32) {
           v = reinterpret_cast<const float*>(row)[c];
+        } else if (ty == MX_SPARSE_FP8) {
+          v = a.fp8.decode(row[c]);
         } else if (bits == 16) {
           v = __half2float(__ushort_as_half(reinterpret_cast<const uint16_t*>(row)[c]));
         } else {
@@ -650,8 +667,10 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
                                int32_t max_int8_D, int32_t max_float16_D, int32_t max_float32_D,
                                const void* indices, const void* offsets, int32_t index_bytes,
                                int32_t pooling_mode, const float* indice_weights,
-                               int32_t output_dtype, int32_t row_alignment, void* out,
-                               int64_t total_D, void* stream) {
+                               int32_t output_dtype, int32_t row_alignment,
+                               int32_t max_float8_D, int32_t fp8_exponent_bits,
+                               int32_t fp8_exponent_bias, void* out, int64_t total_D,
+                               void* stream) {
   clear_error();
   MX_REQUIRE(T >= 0 && B >= 0, "negative T or B");
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
@@ -661,7 +680,8 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
              "output_dtype %d not supported (FP32=0, FP16=1)", output_dtype);
   MX_REQUIRE(row_alignment >= 1, "row_alignment must be positive");
   int32_t max_D = 0;
-  for (int32_t d : {max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D}) {
+  for (int32_t d :
+       {max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D, max_float8_D}) {
     MX_REQUIRE(d >= 0, "negative max_D");
     if (d > max_D) max_D = d;
   }
@@ -670,6 +690,9 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   MX_REQUIRE(max_int4_D % 2 == 0 && max_int2_D % 4 == 0,
              "INT4 D must be even and INT2 D a multiple of 4 (max_int4_D %d, max_int2_D %d)",
              max_int4_D, max_int2_D);
+  MX_REQUIRE(max_float8_D == 0 || hfp8_format_ok(fp8_exponent_bits, fp8_exponent_bias),
+             "FP8 tables need 1 <= fp8_exponent_bits <= 7 and 0 <= fp8_exponent_bias <= 120 "
+             "(got %d, %d)", fp8_exponent_bits, fp8_exponent_bias);
   if (static_cast<int64_t>(T) * B == 0 || total_D == 0) return MX_OK;
   MX_REQUIRE(dev_weights && weights_offsets && weights_tys && D_offsets && offsets && out,
              "null pointer argument");
@@ -693,7 +716,9 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   a.served = (max_int8_D > 0 ? 1 << MX_SPARSE_INT8 : 0) | (max_int4_D > 0 ? 1 << MX_SPARSE_INT4 : 0) |
              (max_int2_D > 0 ? 1 << MX_SPARSE_INT2 : 0) |
              (max_float16_D > 0 ? 1 << MX_SPARSE_FP16 : 0) |
-             (max_float32_D > 0 ? 1 << MX_SPARSE_FP32 : 0);
+             (max_float32_D > 0 ? 1 << MX_SPARSE_FP32 : 0) |
+             (max_float8_D > 0 ? 1 << MX_SPARSE_FP8 : 0);
+  a.fp8 = max_float8_D > 0 ? Hfp8::make(fp8_exponent_bits, fp8_exponent_bias) : Hfp8::make(4, 7);
   a.nchk = static_cast<uint32_t>(T);  // the first launch checks the tables
   a.mailbox = status_mailbox();
   auto* s = as_stream(stream);
@@ -714,5 +739,7 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   if (max_int2_D > 0) a.nchk = 0;
   if (int rc = launch_type<MX_SPARSE_FP16>(a, max_float16_D, index_bytes, s)) return rc;
   if (max_float16_D > 0) a.nchk = 0;
+  if (int rc = launch_type<MX_SPARSE_FP8>(a, max_float8_D, index_bytes, s)) return rc;
+  if (max_float8_D > 0) a.nchk = 0;
   return launch_type<MX_SPARSE_FP32>(a, max_float32_D, index_bytes, s);
 }

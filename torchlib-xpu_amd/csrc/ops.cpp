@@ -1385,6 +1385,31 @@ Tensor dequantize_nbit(const Tensor& input, int64_t bit_rate, at::ScalarType st)
   return out;
 }
 
+Tensor float_to_hfp8(const Tensor& input, int64_t ebits, int64_t exponent_bias,
+                     double max_pos) {
+  check_gpu(input, "input");
+  TORCH_CHECK(input.scalar_type() == at::kFloat, "input must be float32");
+  c10::OptionalDeviceGuard guard(input.device());
+  const Tensor x = input.contiguous();
+  Tensor out = at::empty(x.sizes(), x.options().dtype(at::kByte));
+  MX_CALL(mx_float_to_hfp8(x.data_ptr<float>(), x.numel(), static_cast<int32_t>(ebits),
+                           static_cast<int32_t>(exponent_bias), static_cast<float>(max_pos),
+                           out.data_ptr<uint8_t>(), stream_of(x)));
+  return out;
+}
+
+Tensor hfp8_to_float(const Tensor& input, int64_t ebits, int64_t exponent_bias) {
+  check_gpu(input, "input");
+  TORCH_CHECK(input.scalar_type() == at::kByte, "input must be uint8");
+  c10::OptionalDeviceGuard guard(input.device());
+  const Tensor q = input.contiguous();
+  Tensor out = at::empty(q.sizes(), q.options().dtype(at::kFloat));
+  MX_CALL(mx_hfp8_to_float(q.data_ptr<uint8_t>(), q.numel(), static_cast<int32_t>(ebits),
+                           static_cast<int32_t>(exponent_bias), out.data_ptr<float>(),
+                           stream_of(q)));
+  return out;
+}
+
 Tensor float_to_8bit(const Tensor& t) {
   TORCH_CHECK(t.scalar_type() == at::kFloat, "input must be float32");
   return quantize_8bit(t);
@@ -1431,15 +1456,12 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   (void)weights_placements;
   check_no_cache(lxu_cache_weights.value_or(Tensor()));
   (void)lxu_cache_locations;
-  (void)fp8_exponent_bits;
-  (void)fp8_exponent_bias;
   check_gpu(dev_weights, "dev_weights");
   c10::OptionalDeviceGuard guard(dev_weights.device());
   for (auto* t : {&indices, &offsets}) check_arg(*t, dev_weights, "nbit argument", false);
   for (auto* t : {&weights_offsets, &weights_tys, &D_offsets})
     check_arg(*t, dev_weights, "nbit argument", true);
   TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
-  TORCH_CHECK(max_float8_D.value_or(0) == 0, "FP8 tables are not supported");
   TORCH_CHECK(dev_weights.scalar_type() == at::kByte && dev_weights.is_contiguous(),
               "dev_weights must be contiguous uint8");
   TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
@@ -1477,7 +1499,10 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
       static_cast<int32_t>(max_int8_D), static_cast<int32_t>(max_float16_D),
       static_cast<int32_t>(max_float32_D), idx.data_ptr(), off.data_ptr(), ib,
       static_cast<int32_t>(pooling_mode), iw, static_cast<int32_t>(output_dtype),
-      static_cast<int32_t>(row_alignment.value_or(16)), out.data_ptr(), total_D,
+      static_cast<int32_t>(row_alignment.value_or(16)),
+      static_cast<int32_t>(max_float8_D.value_or(0)),
+      static_cast<int32_t>(fp8_exponent_bits.value_or(-1)),
+      static_cast<int32_t>(fp8_exponent_bias.value_or(-1)), out.data_ptr(), total_D,
       stream_of(dev_weights)));
   return out;
 }
@@ -1603,6 +1628,8 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
   m.def("FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf(Tensor input, int bit_rate) -> Tensor");
   m.def("FusedNBitRowwiseQuantizedSBHalfToFloat(Tensor input, int bit_rate) -> Tensor");
   m.def("FusedNBitRowwiseQuantizedSBHalfToHalf(Tensor input, int bit_rate) -> Tensor");
+  m.def("FloatToHFP8Quantized(Tensor input, int ebits, int exponent_bias, float max_pos) -> Tensor");
+  m.def("HFP8QuantizedToFloat(Tensor input, int ebits, int exponent_bias) -> Tensor");
   m.def("bounds_check_indices(Tensor rows_per_table, Tensor(a!) indices, Tensor(b!) offsets, "
         "int bounds_check_mode, Tensor(c!) warning, Tensor? weights=None, "
         "Tensor? B_offsets=None, SymInt max_B=-1, Tensor? b_t_map=None, int info_B_num_bits=-1, "
@@ -1657,6 +1684,8 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf", TORCH_FN(mx_ops::float_or_half_to_nbit));
   m.impl("FusedNBitRowwiseQuantizedSBHalfToFloat", TORCH_FN(mx_ops::nbit_to_float));
   m.impl("FusedNBitRowwiseQuantizedSBHalfToHalf", TORCH_FN(mx_ops::nbit_to_half));
+  m.impl("FloatToHFP8Quantized", TORCH_FN(mx_ops::float_to_hfp8));
+  m.impl("HFP8QuantizedToFloat", TORCH_FN(mx_ops::hfp8_to_float));
 }
 
 TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {

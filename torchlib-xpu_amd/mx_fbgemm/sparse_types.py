@@ -21,9 +21,11 @@ class SparseType(enum.Enum):
     INT4 = "int4"
     INT2 = "int2"
     BF16 = "bf16"
+    FP8 = "fp8"
 
     def as_int(self) -> int:
-        return {"fp32": 0, "fp16": 1, "int8": 2, "int4": 3, "int2": 4, "bf16": 5}[self.value]
+        return {"fp32": 0, "fp16": 1, "int8": 2, "int4": 3, "int2": 4, "bf16": 5,
+                "fp8": 6}[self.value]
 
     @staticmethod
     def from_int(ty: int) -> "SparseType":
@@ -33,7 +35,8 @@ class SparseType(enum.Enum):
         raise ValueError(f"unknown SparseType value {ty}")
 
     def bit_rate(self) -> int:
-        return {"fp32": 32, "fp16": 16, "int8": 8, "int4": 4, "int2": 2, "bf16": 16}[self.value]
+        return {"fp32": 32, "fp16": 16, "int8": 8, "int4": 4, "int2": 2, "bf16": 16,
+                "fp8": 8}[self.value]
 
     def as_dtype(self) -> torch.dtype:
         return {
@@ -43,6 +46,7 @@ class SparseType(enum.Enum):
             "int8": torch.uint8,
             "int4": torch.quint4x2,
             "int2": torch.quint2x4,
+            "fp8": torch.uint8,
         }[self.value]
 
     def is_rowwise_quantized(self) -> bool:
@@ -88,6 +92,8 @@ def unpadded_row_size_in_bytes(dim: int, weight_ty: SparseType) -> int:
         return dim * 4
     if weight_ty in (SparseType.FP16, SparseType.BF16):
         return dim * 2
+    if weight_ty == SparseType.FP8:
+        return dim
     if weight_ty == SparseType.INT8:
         return dim + QPARAM_BYTES
     if weight_ty == SparseType.INT4:

@@ -5,8 +5,9 @@ Mirrors fbgemm_gpu's IntNBitTableBatchedEmbeddingBagsCodegen (upstream
 fbgemm_gpu/split_table_batched_embeddings_ops_inference.py, recalled) for
 DEVICE placement: all tables live in one uint8 HBM buffer, each row padded
 to ``row_alignment`` bytes; INT8/INT4/INT2 rows start with an fp16 scale and
-an fp16 bias.  Also carries the rowwise quantizer that produces that layout
-from fp32 rows.
+an fp16 bias; FP8 rows are D hfp8 codes (``fp8_exponent_bits`` exponent bits,
+bias ``fp8_exponent_bias``).  Also carries the rowwise quantizer that produces
+that layout from fp32 rows.
 """
 
 from __future__ import annotations
@@ -30,16 +31,25 @@ from .sparse_types import (
 load_mx_fbgemm_library()
 
 
-def quantize_rows(weights: torch.Tensor, weight_ty: SparseType,
-                  row_alignment: int = 16) -> torch.Tensor:
+def hfp8_max_pos(exponent_bits: int, exponent_bias: int) -> float:
+    """The largest magnitude FBGEMM's hfp8 encoder produces (it leaves the top
+    exponent field unused): 2^(2^ebits - 2 - bias) * (2 - 2^-(7 - ebits))."""
+    m = 7 - exponent_bits
+    return (2.0 - 2.0 ** -m) * 2.0 ** ((1 << exponent_bits) - 2 - exponent_bias)
+
+
+def quantize_rows(weights: torch.Tensor, weight_ty: SparseType, row_alignment: int = 16,
+                  fp8_exponent_bits: int = 4, fp8_exponent_bias: int = 7) -> torch.Tensor:
     """fp32/fp16 ``[E, D]`` (on the GPU) -> uint8 ``[E, padded_row_bytes]`` in
     the TBE row layout.
 
     INT8/INT4/INT2 rows are quantized by
     ``torch.ops.fbgemm.FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf`` (bit rate
     8/4/2: fp16 scale and bias) and the two fp16 qparams are moved from the
-    row end to the row front, as the TBE layout wants; FP16/FP32 rows are
-    stored as-is.  Padding bytes are zero."""
+    row end to the row front, as the TBE layout wants; FP8 rows are encoded by
+    ``torch.ops.fbgemm.FloatToHFP8Quantized`` (nearest code, clamped to
+    ``hfp8_max_pos``); FP16/FP32 rows are stored as-is.  Padding bytes are
+    zero."""
     if not weights.is_cuda:
         raise ValueError("quantize_rows runs on the GPU; move the weights to the device first")
     E, D = weights.shape
@@ -50,6 +60,11 @@ def quantize_rows(weights: torch.Tensor, weight_ty: SparseType,
         return out
     if weight_ty == SparseType.FP16:
         out[:, : 2 * D] = weights.half().contiguous().view(torch.uint8).view(E, 2 * D)
+        return out
+    if weight_ty == SparseType.FP8:
+        out[:, :D] = torch.ops.fbgemm.FloatToHFP8Quantized(
+            weights.float().contiguous(), fp8_exponent_bits, fp8_exponent_bias,
+            hfp8_max_pos(fp8_exponent_bits, fp8_exponent_bias))
         return out
     q = torch.ops.fbgemm.FloatOrHalfToFusedNBitRowwiseQuantizedSBHalf(
         weights.contiguous(), weight_ty.bit_rate())
@@ -76,6 +91,8 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         row_alignment: int = 16,
         device: Optional[torch.device] = None,
         bounds_check_mode: BoundsCheckMode = BoundsCheckMode.WARNING,
+        fp8_exponent_bits: Optional[int] = None,
+        fp8_exponent_bias: Optional[int] = None,
     ) -> None:
         super().__init__()
         if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
@@ -86,7 +103,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
             if loc != EmbeddingLocation.DEVICE:
                 raise ValueError("only EmbeddingLocation.DEVICE is supported")
             if ty not in (SparseType.FP32, SparseType.FP16, SparseType.INT8, SparseType.INT4,
-                          SparseType.INT2):
+                          SparseType.INT2, SparseType.FP8):
                 raise ValueError(f"weight type {ty} is not supported")
             if D <= 0 or D > 1024 or D % 8:
                 raise ValueError(f"embedding_dim {D} must be a positive multiple of 8, <= 1024")
@@ -139,6 +156,16 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.max_int8_D = max_d(SparseType.INT8)
         self.max_float16_D = max_d(SparseType.FP16)
         self.max_float32_D = max_d(SparseType.FP32)
+        self.max_float8_D = max_d(SparseType.FP8)
+        # hfp8 format of the FP8 tables (e4m3 with bias 7 unless given); -1 without them.
+        self.fp8_exponent_bits = -1
+        self.fp8_exponent_bias = -1
+        if self.max_float8_D > 0:
+            self.fp8_exponent_bits = 4 if fp8_exponent_bits is None else int(fp8_exponent_bits)
+            self.fp8_exponent_bias = 7 if fp8_exponent_bias is None else int(fp8_exponent_bias)
+            if not (1 <= self.fp8_exponent_bits <= 7 and 0 <= self.fp8_exponent_bias <= 120):
+                raise ValueError("FP8 tables need 1 <= fp8_exponent_bits <= 7 and "
+                                 "0 <= fp8_exponent_bias <= 120")
         self.register_buffer("rows_per_table", torch.tensor([rows[t] for t in ftm],
                                                             device=device, dtype=torch.int64))
         self.register_buffer("bounds_check_warning", torch.zeros(1, device=device,
@@ -162,7 +189,7 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
             self.weights_tys, self.D_offsets, self.total_D, self.max_int2_D, self.max_int4_D,
             self.max_int8_D, self.max_float16_D, self.max_float32_D, indices, offsets,
             int(self.pooling_mode), per_sample_weights, self.output_dtype.as_int(), None, None,
-            self.row_alignment)
+            self.row_alignment, self.max_float8_D, self.fp8_exponent_bits, self.fp8_exponent_bias)
 
     @torch.no_grad()
     def split_embedding_weights(self) -> list[torch.Tensor]:
@@ -176,11 +203,13 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
     def assign_embedding_weights(self, weights: list[torch.Tensor]) -> None:
         """Quantize fp32 ``[E_t, D_t]`` tables into the device buffer."""
         for t, (w, dst) in enumerate(zip(weights, self.split_embedding_weights())):
-            dst.copy_(quantize_rows(w.to(dst.device), self._tys[t], self.row_alignment))
+            dst.copy_(quantize_rows(w.to(dst.device), self._tys[t], self.row_alignment,
+                                    self.fp8_exponent_bits, self.fp8_exponent_bias))
 
     @torch.no_grad()
     def fill_random_weights(self, seed: int = 0) -> None:
-        """Random codes, fp16 scale in [1e-3, 1e-2), bias in [-0.1, 0.1)."""
+        """Random codes (FP8 rows: random hfp8 codes), fp16 scale in
+        [1e-3, 1e-2), bias in [-0.1, 0.1)."""
         g = torch.Generator(device=self.weights_dev.device)
         g.manual_seed(seed)
         for t, dst in enumerate(self.split_embedding_weights()):
