@@ -444,7 +444,9 @@ int64_t mx_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_alignment);
  *   7 - fp8_exponent_bits mantissa bits, bias fp8_exponent_bias, subnormals
  *   at exponent field 0; fbgemm's Float8ToFloat_ref); max_float8_D > 0 needs
  *   1 <= fp8_exponent_bits <= 7 and 0 <= fp8_exponent_bias <= 120.
- *   output_dtype    MX_SPARSE_FP32 or MX_SPARSE_FP16 (round to nearest even)
+ *   output_dtype    MX_SPARSE_FP32, MX_SPARSE_FP16 (round to nearest even) or
+ *                   MX_SPARSE_BF16 (to nearest, ties away from zero, as
+ *                   FBGEMM's CPU kernels write bf16)
  *   out             [B, total_D] */
 int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
                     const uint8_t* weights_tys, const int32_t* D_offsets, int32_t T, int64_t B,

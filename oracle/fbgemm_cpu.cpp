@@ -133,10 +133,11 @@ extern "C" uint8_t fb_float_to_hfp8(float x, int ebits, int ebias) {
 extern "C" int fb_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                                const int32_t* D_off, int T, int64_t B, const int64_t* indices,
                                const int64_t* offsets, int pooling, const float* iw,
-                               int row_align, int out_f16, void* out, int64_t total_D,
+                               int row_align, int out_kind, void* out, int64_t total_D,
                                const int64_t* rows_per_table, int nthreads, int fp8_ebits,
                                int fp8_ebias) {
-  if (!out_f16) return -3;  // the harness serves fp16 output (the nbit configs)
+  if (out_kind != 1 && out_kind != 2) return -3;  // the harness serves fp16 and bf16 output
+  const bool bf16 = out_kind == 2;
   using K8 = fbgemm::EmbeddingSpMDMKernelSignature<uint8_t, int64_t, int64_t, uint16_t>::Type;
   using K16 = fbgemm::EmbeddingSpMDMKernelSignature<uint16_t, int64_t, int64_t, uint16_t>::Type;
   using K32 = fbgemm::EmbeddingSpMDMKernelSignature<float, int64_t, int64_t, uint16_t>::Type;
@@ -151,25 +152,25 @@ extern "C" int fb_nbit_forward(const uint8_t* W, const int64_t* w_off, const uin
     switch (tys[t]) {
       case 0:
         k32[t] = fbgemm::GenerateEmbeddingSpMDMWithStrides<float, int64_t, int64_t, uint16_t>(
-            D, w, mean, 16, false, true, total_D, stride / 4);
+            D, w, mean, 16, false, true, total_D, stride / 4, true, false, bf16);
         break;
       case 1:
         k16[t] = fbgemm::GenerateEmbeddingSpMDMWithStrides<uint16_t, int64_t, int64_t, uint16_t>(
-            D, w, mean, 16, false, true, total_D, stride / 2);
+            D, w, mean, 16, false, true, total_D, stride / 2, true, false, bf16);
         break;
       case 2:
         k8[t] = fbgemm::GenerateEmbeddingSpMDMWithStrides<uint8_t, int64_t, int64_t, uint16_t>(
-            D, w, mean, 16, false, true, total_D, stride, /*scale_bias_last=*/false);
+            D, w, mean, 16, false, true, total_D, stride, /*scale_bias_last=*/false, false, bf16);
         break;
       case 3:
       case 4:
         k8[t] = fbgemm::GenerateEmbeddingSpMDMNBitWithStrides<int64_t, int64_t, uint16_t>(
             tys[t] == 3 ? 4 : 2, D, w, mean, 16, false, true, total_D, stride,
-            /*scale_bias_last=*/false);
+            /*scale_bias_last=*/false, bf16);
         break;
       case 6:  // weighted when the call passes weights
         k8[t] = fbgemm::GenerateEmbeddingSpMDMFP8WithStrides<int64_t, int64_t, uint16_t>(
-            D, mean, false, true, total_D, stride, fp8_ebits, fp8_ebias);
+            D, mean, false, true, total_D, stride, fp8_ebits, fp8_ebias, bf16);
         break;
       default:
         return -1;

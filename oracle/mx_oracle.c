@@ -51,6 +51,18 @@ float orc_half_to_float(uint16_t h) {
   return f;
 }
 
+/* bfloat16 of f as FBGEMM's CPU embedding kernels write bf16 output: the
+ * top half of f's bits after adding 0x8000, i.e. to nearest with ties away
+ * from zero (matched bit for bit against their is_bf16_out output, where
+ * every tie went away from zero and every other value to nearest); NaN stays
+ * a quiet NaN. */
+uint16_t orc_float_to_bf16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  return (uint16_t)((x + 0x8000u) >> 16);
+}
+
 uint16_t orc_float_to_half(float f) {
   uint32_t x;
   memcpy(&x, &f, 4);
@@ -191,7 +203,7 @@ static float nbit_code(const uint8_t* codes, int32_t ty, int32_t d, int32_t ebit
 int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                      const int32_t* D_off, int32_t T, int64_t B, const int64_t* indices,
                      const int64_t* offsets, int32_t pooling, const float* iw, int32_t row_align,
-                     int32_t out_f16, void* out, int64_t total_D, int32_t fp8_ebits,
+                     int32_t out_kind, void* out, int64_t total_D, int32_t fp8_ebits,
                      int32_t fp8_ebias) {
   float* acc = NULL;
   for (int32_t t = 0; t < T; ++t) {
@@ -236,9 +248,10 @@ int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
         const float inv = 1.0f / (float)(e - s);
         for (int32_t d = 0; d < D; ++d) acc[d] = acc[d] * inv;
       }
-      if (out_f16) {
+      if (out_kind == 1 || out_kind == 2) { /* fp16, bf16 */
         uint16_t* o = (uint16_t*)out + b * total_D + D0;
-        for (int32_t d = 0; d < D; ++d) o[d] = orc_float_to_half(acc[d]);
+        for (int32_t d = 0; d < D; ++d)
+          o[d] = out_kind == 1 ? orc_float_to_half(acc[d]) : orc_float_to_bf16(acc[d]);
       } else {
         float* o = (float*)out + b * total_D + D0;
         for (int32_t d = 0; d < D; ++d) o[d] = acc[d];

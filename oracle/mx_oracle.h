@@ -16,6 +16,7 @@
 
 float orc_half_to_float(uint16_t h);
 uint16_t orc_float_to_half(float f);
+uint16_t orc_float_to_bf16(float f);
 float orc_hfp8_to_float(uint8_t v, int32_t ebits, int32_t ebias);
 uint8_t orc_float_to_hfp8(float x, int32_t ebits, int32_t ebias, float max_pos);
 
@@ -28,7 +29,7 @@ int64_t orc_nbit_row_bytes(int32_t ty, int32_t D, int32_t row_align);
 int orc_nbit_forward(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
                      const int32_t* D_off, int32_t T, int64_t B, const int64_t* indices,
                      const int64_t* offsets, int32_t pooling, const float* iw, int32_t row_align,
-                     int32_t out_f16, void* out, int64_t total_D, int32_t fp8_ebits,
+                     int32_t out_kind, void* out, int64_t total_D, int32_t fp8_ebits,
                      int32_t fp8_ebias);
 
 int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t bits,

@@ -274,16 +274,19 @@ def nbit_row_bytes(ty: int, D: int, row_align: int) -> int:
 
 def nbit_forward(W, w_off, tys, D_off, B, indices, offsets, pooling=POOL_SUM,
                  indice_weights=None, row_align=16, out_f16=True, fp8_exponent_bits=4,
-                 fp8_exponent_bias=7):
+                 fp8_exponent_bias=7, out_bf16=False):
+    """Pooled nbit lookup; output fp16 (out_f16), bf16 (out_bf16, returned as
+    the uint16 bits) or fp32."""
     W = _c(W, np.uint8)
     w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
     indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
     iw = _c(indice_weights, np.float32)
     T = D_off.shape[0] - 1
     total_D = int(D_off[-1])
-    out = np.zeros((B, total_D), dtype=np.float16 if out_f16 else np.float32)
+    kind = 2 if out_bf16 else (1 if out_f16 else 0)
+    out = np.zeros((B, total_D), dtype=(np.float32, np.float16, np.uint16)[kind])
     rc = lib().orc_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
-                                _p(offsets), pooling, _p(iw), row_align, int(out_f16), _p(out),
+                                _p(offsets), pooling, _p(iw), row_align, kind, _p(out),
                                 total_D, fp8_exponent_bits, fp8_exponent_bias)
     assert rc == 0, f"orc_nbit_forward failed ({rc})"
     return out
@@ -485,7 +488,7 @@ def _fbgemm_tbe_forward_f16w(W, w_off, D_off, rows_per_table, B, indices, offset
 
 def fbgemm_nbit_forward(W, w_off, tys, D_off, rows_per_table, B, indices, offsets,
                         pooling=POOL_SUM, indice_weights=None, row_align=16, nthreads=1,
-                        fp8_exponent_bits=4, fp8_exponent_bias=7):
+                        fp8_exponent_bits=4, fp8_exponent_bias=7, out_bf16=False):
     W = _c(W, np.uint8)
     w_off, tys, D_off = _c(w_off, np.int64), _c(tys, np.uint8), _c(D_off, np.int32)
     rows = _c(rows_per_table, np.int64)
@@ -493,9 +496,10 @@ def fbgemm_nbit_forward(W, w_off, tys, D_off, rows_per_table, B, indices, offset
     iw = _c(indice_weights, np.float32)
     T = D_off.shape[0] - 1
     total_D = int(D_off[-1])
-    out = np.zeros((B, total_D), dtype=np.float16)
+    out = np.zeros((B, total_D), dtype=np.uint16 if out_bf16 else np.float16)
     rc = fbgemm().fb_nbit_forward(_p(W), _p(w_off), _p(tys), _p(D_off), T, B, _p(indices),
-                                  _p(offsets), pooling, _p(iw), row_align, 1, _p(out), total_D,
+                                  _p(offsets), pooling, _p(iw), row_align, 2 if out_bf16 else 1,
+                                  _p(out), total_D,
                                   _p(rows), nthreads, fp8_exponent_bits, fp8_exponent_bias)
     assert rc == 0, f"FBGEMM nbit kernel reported failure ({rc})"
     return out

@@ -239,7 +239,7 @@ static void run_nbit(const Batch* b, const int32_t* tys) {
   for (int64_t i = 0; i < b->N; ++i) iw[i] = rnd_unit();
   void* out = xmalloc(sizeof(float) * b->B * total_D);
   for (int pooling = 0; pooling < 2; ++pooling)
-    for (int f16 = 0; f16 < 2; ++f16) {
+    for (int f16 = 0; f16 < 3; ++f16) { /* fp32, fp16, bf16 output */
       CHECK(orc_nbit_forward(W, w_off, tys8, b->D_off, b->T, b->B, b->indices, b->offsets,
                              pooling, NULL, 16, f16, out, total_D, 4, 7) == 0);
       CHECK(orc_nbit_forward(W, w_off, tys8, b->D_off, b->T, b->B, b->indices, b->offsets,

@@ -50,7 +50,7 @@ def max_dims(tys, dims):
 def nbit_forward_gpu(dev, W: torch.Tensor, w_off, tys, dims, indices, offsets, pooling: int,
                      out_f16: bool = True, indice_weights=None, row_align: int = 16,
                      index_dtype=torch.int64, fp8_exponent_bits: int = 4,
-                     fp8_exponent_bias: int = 7):
+                     fp8_exponent_bias: int = 7, out_bf16: bool = False):
     T = len(tys)
     D_off = np.concatenate([[0], np.cumsum(dims)]).astype(np.int32)
     m2, m4, m8, m16, m32 = max_dims(tys, dims)
@@ -61,7 +61,7 @@ def nbit_forward_gpu(dev, W: torch.Tensor, w_off, tys, dims, indices, offsets, p
         torch.as_tensor(D_off, device=dev), int(D_off[-1]), m2, m4, m8, m16, m32,
         torch.as_tensor(indices).to(dev, index_dtype), torch.as_tensor(offsets).to(dev, index_dtype),
         pooling, None if indice_weights is None else torch.as_tensor(indice_weights).to(dev),
-        1 if out_f16 else 0, None, None, row_align,
+        5 if out_bf16 else (1 if out_f16 else 0), None, None, row_align,
         max([D for t, D in zip(tys, dims) if t == orc.FP8], default=0), fp8_exponent_bits,
         fp8_exponent_bias)
 
@@ -101,6 +101,17 @@ def fp16_ulp_distance(a, b) -> np.ndarray:
         return np.where(h & 0x8000, -mag, mag)
 
     return np.abs(ordinal(a) - ordinal(b))
+
+
+def bf16_ulp_distance(a_bits, b_bits) -> np.ndarray:
+    """Distance in bf16 units in the last place between two arrays of bf16 bit
+    patterns (uint16), on the same monotonic scale as fp16_ulp_distance."""
+    def ordinal(x):
+        h = np.ascontiguousarray(x, dtype=np.uint16).astype(np.int32)
+        mag = h & 0x7FFF
+        return np.where(h & 0x8000, -mag, mag)
+
+    return np.abs(ordinal(a_bits) - ordinal(b_bits))
 
 
 def assert_nbit_close(got, exp, max_ulps: int = 1, min_exact: float = 0.9):

@@ -14,7 +14,7 @@ import torch
 
 import oracle as orc
 from mx_fbgemm import bench_inputs
-from nbit_helpers import (assert_nbit_close, build_weights, build_weights_gpu, max_dims,
+from nbit_helpers import (assert_nbit_close, bf16_ulp_distance, build_weights, build_weights_gpu, max_dims,
                           nbit_forward_gpu)
 from tbe_helpers import random_tbe
 
@@ -70,6 +70,35 @@ def test_fp8_tables(dev, ebits, ebias, D):
                                fp8_exponent_bias=ebias).cpu().numpy()
         view = np.uint16 if out_f16 else np.uint32
         np.testing.assert_array_equal(got.view(view), exp.view(view))
+
+
+@pytest.mark.parametrize("ty", TYPES + [orc.FP8])
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_bf16_output(dev, ty, pooling, weighted):
+    """bf16 output, rounded to nearest with ties away from zero as FBGEMM's CPU
+    kernels do (the oracle matches them bit for bit).  Weights in steps of 1/4
+    put many sums exactly between two bf16 values.  FP32/FP16/FP8 rows add in
+    the oracle's order: bit-exact; quantized rows group scale*q and bias
+    differently: within one bf16 place, at least 90 % exact."""
+    print(f"[case] nbit bf16 out ty={ty} pool={pooling} weighted={weighted}", flush=True)
+    rng = np.random.default_rng(ty * 7 + 3 * weighted + pooling)
+    dims, rows = [32, 64, 24], [40, 70, 30]
+    inp = random_tbe(rng, 3, 40, dims, rows, 20)
+    tys = [ty] * 3
+    buf, w_off = build_weights(rng, tys, dims, rows)
+    iw = (rng.integers(-4, 5, inp.N) / 4).astype(np.float32) if weighted else None
+    exp = orc.nbit_forward(buf, w_off, tys, inp.D_offsets, inp.B, inp.indices, inp.offsets,
+                           pooling, indice_weights=iw, out_bf16=True)
+    got = nbit_forward_gpu(dev, torch.from_numpy(buf).to(dev), w_off, tys, dims, inp.indices,
+                           inp.offsets, pooling, indice_weights=iw, out_bf16=True)
+    assert got.dtype == torch.bfloat16
+    g = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    if ty in (orc.INT8, orc.INT4, orc.INT2):
+        d = bf16_ulp_distance(g, exp)
+        assert d.max() <= 1 and (d == 0).mean() >= 0.9, (d.max(), (d == 0).mean())
+    else:
+        np.testing.assert_array_equal(g, exp)
 
 
 def test_mixed_types_weighted_fp32_out(dev):

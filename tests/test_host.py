@@ -20,7 +20,9 @@ from mx_fbgemm.split_table_batched_embeddings_ops_training import (
 
 def test_enums_match_fbgemm_values():
     assert [s.as_int() for s in (SparseType.FP32, SparseType.FP16, SparseType.INT8, SparseType.INT4,
-                                 SparseType.INT2, SparseType.BF16)] == [0, 1, 2, 3, 4, 5]
+                                 SparseType.INT2, SparseType.BF16, SparseType.FP8)] == \
+        [0, 1, 2, 3, 4, 5, 6]
+    assert SparseType.from_int(6) == SparseType.FP8
     assert (PoolingMode.SUM, PoolingMode.MEAN, PoolingMode.NONE) == (0, 1, 2)
     assert EmbeddingLocation.DEVICE == 0 and EmbeddingLocation.HOST == 3
     assert SparseType.from_int(3) == SparseType.INT4

@@ -227,6 +227,26 @@ def test_nbit_fp8_vs_fbgemm_cpu(ebits, ebias, pooling, weighted):
     np.testing.assert_array_equal(got.view(np.uint16), exp.view(np.uint16))
 
 
+@pytest.mark.parametrize("ty", [orc.INT8, orc.INT4, orc.INT2, orc.FP16, orc.FP32, orc.FP8])
+@pytest.mark.parametrize("pooling", [0, 1])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nbit_bf16_out_vs_fbgemm_cpu(ty, pooling, weighted):
+    """bf16 output (FBGEMM's is_bf16_out), bit-exact.  Weights in steps of 1/4
+    keep many sums exactly halfway between two bf16 values, where FBGEMM
+    rounds away from zero: the oracle must follow it on every tie."""
+    rng = np.random.default_rng(ty * 7 + 3 * weighted + pooling)
+    dims, rows = [32, 64], [40, 70]
+    inp = random_tbe(rng, 2, 40, dims, rows, 20)
+    buf, w_off = build_weights(rng, [ty] * 2, dims, rows)
+    iw = (rng.integers(-4, 5, inp.N) / 4).astype(np.float32) if weighted else None
+    got = orc.nbit_forward(buf, w_off, [ty] * 2, inp.D_offsets, inp.B, inp.indices,
+                           inp.offsets, pooling, indice_weights=iw, out_bf16=True)
+    exp = orc.fbgemm_nbit_forward(buf, w_off, [ty] * 2, inp.D_offsets, rows, inp.B,
+                                  inp.indices, inp.offsets, pooling, indice_weights=iw,
+                                  nthreads=2, out_bf16=True)
+    np.testing.assert_array_equal(got, exp)
+
+
 def test_nbit_int8_vs_quantized_embedding_bag_byte():
     # torch's byte rowwise op keeps fp32 scale/bias at the row end; move ours there.
     rng = np.random.default_rng(12)

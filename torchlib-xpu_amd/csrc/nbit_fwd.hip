@@ -1,5 +1,6 @@
 // Quantized ("nbit") TBE inference forward for gfx950: FP32, FP16, INT8,
-// INT4 and INT2 tables in one launch.
+// INT4, INT2 and FP8 (hfp8) tables, one launch per type present; fp32, fp16
+// or bf16 output.
 //
 // Semantics: fbgemm_gpu int_nbit_split_embedding_codegen_lookup_function
 // (upstream codegen/inference/, recalled).  Row layout is the TBE layout of
@@ -46,7 +47,7 @@ struct NbitArgs {
   int32_t T;
   int32_t pooling;
   int32_t row_align;
-  int32_t out_f16;
+  int32_t out_kind;        // output element: 0 fp32, 1 fp16, 2 bf16
   int32_t served;          // bit ty set: the call launches type ty
   Hfp8 fp8;                // FP8 tables' format (when served)
   uint32_t nchk;           // trailing blocks that check the tables (T in the first launch, else 0)
@@ -62,7 +63,6 @@ __device__ __forceinline__ bool whole_bytes(int32_t D) {
   if constexpr (TY == MX_SPARSE_INT2) return (D & 3) == 0;
   return true;
 }
-
 
 __device__ __host__ __forceinline__ int64_t row_bytes_of(int32_t ty, int32_t D, int32_t align) {
   int64_t u;
@@ -127,7 +127,6 @@ struct TyInfo<MX_SPARSE_FP8> {
   static constexpr int kBits = 8;
   static constexpr bool kQ = false;
 };
-
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
@@ -235,11 +234,21 @@ __device__ __forceinline__ int64_t idx_at(const void* p, int64_t i) {
   return static_cast<int64_t>(reinterpret_cast<const I*>(p)[i]);
 }
 
+// A 16-bit output element: fp16 rounded to nearest even, or bf16 as FBGEMM's
+// CPU kernels write it (the top half of the fp32 bits after adding 0x8000:
+// to nearest, ties away from zero; NaN stays a quiet NaN).
+__device__ __forceinline__ uint16_t out16(float v, int32_t kind) {
+  if (kind == 1) return __half_as_ushort(__float2half_rn(v));
+  const uint32_t x = __float_as_uint(v);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
+  return static_cast<uint16_t>((x + 0x8000u) >> 16);
+}
+
 __device__ __forceinline__ void store_out(const NbitArgs& a, int64_t col_base, int ncols,
                                           const float* v) {
-  if (a.out_f16) {
-    __half* o = reinterpret_cast<__half*>(a.out) + col_base;
-    for (int e = 0; e < ncols; ++e) o[e] = __float2half_rn(v[e]);
+  if (a.out_kind != 0) {
+    uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + col_base;
+    for (int e = 0; e < ncols; ++e) o[e] = out16(v[e], a.out_kind);
   } else {
     float* o = reinterpret_cast<float*>(a.out) + col_base;
     for (int e = 0; e < ncols; ++e) o[e] = v[e];
@@ -371,14 +380,14 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   }
   // Element e of the lane is column (q*G + k)*CPC + j of the table, e = q*CPC + j.
   const int64_t col = out_col + static_cast<int64_t>(k) * CPC;
-  if (a.out_f16) {
-    __half h[CPL];
+  if (a.out_kind != 0) {
+    uint16_t h[CPL];
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) h[e] = __float2half_rn(res[e]);
+    for (int e = 0; e < CPL; ++e) h[e] = out16(res[e], a.out_kind);
 #pragma unroll
     for (int q = 0; q < NCHK; ++q) {
-      __half* o = reinterpret_cast<__half*>(a.out) + col + q * G * CPC;
-      const __half* hq = h + q * CPC;
+      uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + col + q * G * CPC;
+      const uint16_t* hq = h + q * CPC;
       if constexpr (CPC % 8 == 0) {
 #pragma unroll
         for (int v = 0; v < CPC / 8; ++v)
@@ -518,8 +527,8 @@ __device__ __forceinline__ void check_table(const NbitArgs& a, int64_t t, int32_
   for (int64_t b = 0; b < a.B; ++b)
     for (int64_t c = threadIdx.x; c < nc; c += blockDim.x) {
       const int64_t o = b * a.total_D + c0 + c;
-      if (a.out_f16)
-        reinterpret_cast<__half*>(a.out)[o] = __float2half_rn(0.0f);
+      if (a.out_kind != 0)
+        reinterpret_cast<uint16_t*>(a.out)[o] = 0u;  // +0 in fp16 and bf16
       else
         reinterpret_cast<float*>(a.out)[o] = 0.0f;
     }
@@ -676,8 +685,9 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
   MX_REQUIRE(pooling_mode == MX_POOL_SUM || pooling_mode == MX_POOL_MEAN,
              "pooling_mode %d not supported (SUM=0, MEAN=1)", pooling_mode);
-  MX_REQUIRE(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
-             "output_dtype %d not supported (FP32=0, FP16=1)", output_dtype);
+  MX_REQUIRE(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16 ||
+                 output_dtype == MX_SPARSE_BF16,
+             "output_dtype %d not supported (FP32=0, FP16=1, BF16=5)", output_dtype);
   MX_REQUIRE(row_alignment >= 1, "row_alignment must be positive");
   int32_t max_D = 0;
   for (int32_t d :
@@ -712,7 +722,7 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   a.T = T;
   a.pooling = pooling_mode;
   a.row_align = row_alignment;
-  a.out_f16 = output_dtype == MX_SPARSE_FP16;
+  a.out_kind = output_dtype == MX_SPARSE_FP16 ? 1 : (output_dtype == MX_SPARSE_BF16 ? 2 : 0);
   a.served = (max_int8_D > 0 ? 1 << MX_SPARSE_INT8 : 0) | (max_int4_D > 0 ? 1 << MX_SPARSE_INT4 : 0) |
              (max_int2_D > 0 ? 1 << MX_SPARSE_INT2 : 0) |
              (max_float16_D > 0 ? 1 << MX_SPARSE_FP16 : 0) |

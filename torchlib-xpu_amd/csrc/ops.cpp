@@ -1475,8 +1475,9 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   TORCH_CHECK((offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
   const int64_t B = (offsets.numel() - 1) / T;
   const int64_t total_D = total_D_sym.expect_int();
-  TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
-              "output_dtype must be FP32 (0) or FP16 (1)");
+  TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16 ||
+                  output_dtype == MX_SPARSE_BF16,
+              "output_dtype must be FP32 (0), FP16 (1) or BF16 (5)");
   const float* iw = nullptr;
   Tensor iwc;
   if (indice_weights.has_value() && indice_weights->defined()) {
@@ -1489,7 +1490,9 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
     iw = iwc.data_ptr<float>();
   }
   ensure_mailbox(dev_weights.device().index(), stream_of(dev_weights));
-  auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
+  auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16   ? at::kHalf
+                                          : output_dtype == MX_SPARSE_BF16 ? at::kBFloat16
+                                                                           : at::kFloat);
   Tensor out = at::empty({B, total_D}, opts);
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
   MX_CALL(mx_nbit_forward(

@@ -97,8 +97,8 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         super().__init__()
         if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
             raise ValueError(f"pooling_mode {pooling_mode} is not supported")
-        if output_dtype not in (SparseType.FP16, SparseType.FP32):
-            raise ValueError("output_dtype must be FP16 or FP32")
+        if output_dtype not in (SparseType.FP16, SparseType.FP32, SparseType.BF16):
+            raise ValueError("output_dtype must be FP16, FP32 or BF16")
         for _, E, D, ty, loc in embedding_specs:
             if loc != EmbeddingLocation.DEVICE:
                 raise ValueError("only EmbeddingLocation.DEVICE is supported")
