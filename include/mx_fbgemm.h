@@ -83,8 +83,12 @@ extern "C" {
  * region (see above); mx_test_force_workspace_counters added.  0.4.0:
  * mx_nbit_forward takes max_float8_D, fp8_exponent_bits and
  * fp8_exponent_bias after row_alignment (FP8 tables; not binary compatible);
- * mx_float_to_hfp8 and mx_hfp8_to_float added. */
-#define MX_FBGEMM_VERSION 400
+ * mx_float_to_hfp8 and mx_hfp8_to_float added; output_dtype MX_SPARSE_BF16
+ * accepted.  0.5.0: the PoolingMode NONE (sequence) entry points added:
+ * mx_tbe_forward_nobag, mx_tbe_backward_rowwise_adagrad_nobag,
+ * mx_tbe_transpose_embedding_input_nobag, mx_nbit_forward_nobag and their
+ * workspace queries (all earlier ones unchanged). */
+#define MX_FBGEMM_VERSION 500
 int mx_version(void);
 
 /* Thread-local text of the last failing call on this thread ("" if none). */
@@ -221,6 +225,18 @@ int mx_tbe_forward_vbe(const void* weights, int32_t weights_ty, const int64_t* w
                        const int64_t* vbe_row_output_offsets, const int32_t* vbe_b_t_map,
                        int32_t info_B_num_bits, void* out, int32_t out_dtype, void* stream);
 
+/* Serves fbgemm::split_embedding_nobag_codegen_forward_unweighted_cuda (the
+ * PoolingMode NONE forward of the lookup function): every table has width D
+ * (a multiple of 4, at most 1024) and position l of bag (t, b) writes its own
+ * row, out[l, :] = W_t[indices[l], :] (fp16 weights widened to fp32, then
+ * the output type: fp32, or fp16 rounded to nearest even).
+ *   out     [N, D]; positions outside every bag (before offsets[0], from
+ *           offsets[T*B] on) are written as zeros. */
+int mx_tbe_forward_nobag(const void* weights, int32_t weights_ty, const int64_t* weights_offsets,
+                         int32_t T, int64_t B, int32_t D, const void* indices,
+                         const void* offsets, int32_t index_bytes, int64_t N, void* out,
+                         int32_t out_dtype, void* stream);
+
 /* ---- TBE backward: transpose (sort) and fused exact rowwise Adagrad ----- */
 
 /* Number of info bits used for the bag index b in an info word
@@ -260,6 +276,20 @@ int mx_tbe_transpose_embedding_input_vbe(
     int64_t* sorted_linear_indices, int32_t* infos_sorted, int64_t* sorted_linear_indices_run,
     int32_t* run_lengths, int32_t* num_runs, int32_t* cumulative_run_lengths, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mx_tbe_transpose_embedding_input_nobag. */
+size_t mx_tbe_transpose_nobag_workspace_bytes(int64_t N, int32_t T, int32_t total_hash_size_bits);
+
+/* Serves fbgemm::transpose_embedding_input with nobag = true (sequence
+ * lookups): as mx_tbe_transpose_embedding_input, except that each position
+ * is its own occurrence and its info is int64, l * T + t (l the position, t
+ * its table).  Needs offsets[0] = 0 and offsets[T*B] = N, as upstream. */
+int mx_tbe_transpose_embedding_input_nobag(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    int64_t* linear_indices, int64_t* sorted_linear_indices, int64_t* infos_sorted,
+    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Random state of a stochastic-rounding update, in the shape of torch's
  * Philox state: eager calls pass the seed and offset as values; a call made
@@ -319,6 +349,25 @@ int mx_tbe_backward_rowwise_adagrad_vbe(
     const int64_t* momentum1_offsets, float learning_rate, float eps, float weight_decay,
     int32_t weight_decay_mode, int32_t stochastic_rounding, const mx_rng_state* rng,
     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by mx_tbe_backward_rowwise_adagrad_nobag. */
+size_t mx_tbe_backward_nobag_workspace_bytes(int64_t N, int32_t T, int32_t total_hash_size_bits,
+                                             int32_t D);
+
+/* Serves fbgemm::split_embedding_nobag_backward_codegen_rowwise_adagrad_
+ * unweighted_exact_cuda (the PoolingMode NONE backward): every table has
+ * width D and grad_output is [N, D], row l the gradient of position l.  For
+ * each distinct (t, i): g = the sum of its positions' gradient rows in sorted
+ * (position) order, then the update of mx_tbe_backward_rowwise_adagrad.
+ * Needs offsets[0] = 0 and offsets[T*B] = N, as upstream. */
+int mx_tbe_backward_rowwise_adagrad_nobag(
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, int32_t T, int64_t B,
+    int32_t D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    const float* grad_output, float* momentum1, const int64_t* momentum1_offsets,
+    float learning_rate, float eps, float weight_decay, int32_t weight_decay_mode,
+    int32_t stochastic_rounding, const mx_rng_state* rng, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* Serves fbgemm::split_embedding_codegen_grad_indice_weights_cuda: the gradient
  * of a weighted lookup's per-sample weights,
@@ -456,6 +505,24 @@ int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weights_offsets,
                     const float* indice_weights, int32_t output_dtype, int32_t row_alignment,
                     int32_t max_float8_D, int32_t fp8_exponent_bits, int32_t fp8_exponent_bias,
                     void* out, int64_t total_D, void* stream);
+
+/* Serves fbgemm::int_nbit_split_embedding_codegen_lookup_function with
+ * pooling_mode MX_POOL_NONE (fbgemm's int_nbit_split_embedding_nobag_codegen_
+ * forward_unweighted_cuda): D is the largest max_*_D and position l of bag
+ * (t, b) writes its own dequantized row, out[l, :], out [N, D].  An
+ * INT8/INT4/INT2 element is fmaf(scale, q, bias); FP32, FP16 and FP8 elements
+ * are the stored values; then the output type of mx_nbit_forward.  A table
+ * whose D is not D, or that mx_nbit_forward could not serve, has its
+ * positions written as zeros and is reported in MX_STATUS_NBIT_TABLE;
+ * positions outside every bag are written as zeros. */
+int mx_nbit_forward_nobag(const uint8_t* dev_weights, const int64_t* weights_offsets,
+                          const uint8_t* weights_tys, const int32_t* D_offsets, int32_t T,
+                          int64_t B, int32_t max_int2_D, int32_t max_int4_D, int32_t max_int8_D,
+                          int32_t max_float16_D, int32_t max_float32_D, const void* indices,
+                          const void* offsets, int32_t index_bytes, int64_t N,
+                          int32_t output_dtype, int32_t row_alignment, int32_t max_float8_D,
+                          int32_t fp8_exponent_bits, int32_t fp8_exponent_bias, void* out,
+                          void* stream);
 
 #ifdef __cplusplus
 }

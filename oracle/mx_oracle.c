@@ -355,6 +355,22 @@ int orc_transpose(const int64_t* hsc, int32_t T, int64_t B, int32_t nb, int32_t 
  *   c    = 1 (mode 0), 1 - m*wd (mode 1), 1 - lr*wd (mode 2)
  *   w_d  = fmaf(-m, g_d, c * w_d)
  * (recalled rowwise_adagrad rule of fbgemm_gpu's optimizer templates). */
+static void adagrad_row(float* w, float* h, const float* g, int32_t D, float lr, float eps,
+                        float wd, int32_t wd_mode) {
+  float ss = 0.0f;
+  for (int32_t d = 0; d < D; ++d) {
+    const float s = wd_mode == 1 ? fmaf(wd, w[d], g[d]) : g[d];
+    ss = ss + s * s;
+  }
+  const float hn = *h + ss / (float)D;
+  const float m = lr / (sqrtf(hn) + eps);
+  float c = 1.0f;
+  if (wd_mode == 1) c = 1.0f - m * wd;
+  if (wd_mode == 2) c = 1.0f - lr * wd;
+  for (int32_t d = 0; d < D; ++d) w[d] = fmaf(-m, g[d], c * w[d]);
+  *h = hn;
+}
+
 int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* D_off,
                                  int32_t T, int64_t B, const int64_t* hsc, int32_t bits,
                                  const int64_t* indices, const int64_t* offsets, int64_t N,
@@ -409,20 +425,7 @@ int orc_backward_rowwise_adagrad(float* W, const int64_t* w_off, const int32_t* 
       const float wl = iw ? iw[pos[j]] : 1.0f;
       for (int32_t d = 0; d < D; ++d) g[d] = g[d] + (gr[d] * sc) * wl;
     }
-    float* w = W + w_off[t] + idx * D;
-    float ss = 0.0f;
-    for (int32_t d = 0; d < D; ++d) {
-      const float s = wd_mode == 1 ? fmaf(wd, w[d], g[d]) : g[d];
-      ss = ss + s * s;
-    }
-    float* h = m1 + m1_off[t] + idx;
-    const float hn = *h + ss / (float)D;
-    const float m = lr / (sqrtf(hn) + eps);
-    float c = 1.0f;
-    if (wd_mode == 1) c = 1.0f - m * wd;
-    if (wd_mode == 2) c = 1.0f - lr * wd;
-    for (int32_t d = 0; d < D; ++d) w[d] = fmaf(-m, g[d], c * w[d]);
-    *h = hn;
+    adagrad_row(W + w_off[t] + idx * D, m1 + m1_off[t] + idx, g, D, lr, eps, wd, wd_mode);
   }
 done:
   free(linear);
@@ -591,4 +594,96 @@ void orc_dequantize_nbit(const uint8_t* in, int64_t rows, int64_t D, int32_t bit
       out[r * D + j] = fmaf((float)c, scale, bias);
     }
   }
+}
+
+/* ---- sequence lookups (PoolingMode NONE) -------------------------------------
+ * Every table of width D; position l of bag (t, b) is its own occurrence
+ * (recalled fbgemm_gpu nobag kernels). */
+
+/* out[l, :] = the dequantized row of position l: fmaf(scale, q, bias) for
+ * INT8/INT4/INT2, the stored value for FP32/FP16/FP8; then the output type
+ * (out_kind 0 fp32, 1 fp16, 2 bf16).  Positions outside every bag stay as
+ * the caller left them. */
+int orc_nbit_forward_nobag(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
+                           int32_t D, int32_t T, int64_t B, const int64_t* indices,
+                           const int64_t* offsets, int32_t row_align, int32_t out_kind,
+                           void* out, int32_t fp8_ebits, int32_t fp8_ebias) {
+  for (int32_t t = 0; t < T; ++t) {
+    const int32_t ty = tys[t];
+    const int64_t stride = orc_nbit_row_bytes(ty, D, row_align);
+    if (stride < 0) return -1;
+    const int quant = ty == ORC_INT8 || ty == ORC_INT4 || ty == ORC_INT2;
+    for (int64_t l = offsets[t * B]; l < offsets[(t + 1) * B]; ++l) {
+      const uint8_t* row = W + w_off[t] + indices[l] * stride;
+      float scale = 0.0f, bias = 0.0f;
+      if (quant) {
+        uint16_t hs, hb;
+        memcpy(&hs, row, 2);
+        memcpy(&hb, row + 2, 2);
+        scale = orc_half_to_float(hs);
+        bias = orc_half_to_float(hb);
+      }
+      for (int32_t d = 0; d < D; ++d) {
+        const float v = quant ? fmaf(scale, nbit_code(row + 4, ty, d, 0, 0), bias)
+                              : nbit_code(row, ty, d, fp8_ebits, fp8_ebias);
+        if (out_kind == 1 || out_kind == 2)
+          ((uint16_t*)out)[l * D + d] = out_kind == 1 ? orc_float_to_half(v) : orc_float_to_bf16(v);
+        else
+          ((float*)out)[l * D + d] = v;
+      }
+    }
+  }
+  return 0;
+}
+
+/* The nobag backward: keys hsc[t] + indices[l] stably sorted (ties in
+ * position order); each run sums grad[l, :] of its positions in that order,
+ * then the rowwise Adagrad step of orc_backward_rowwise_adagrad. */
+int orc_backward_rowwise_adagrad_nobag(float* W, const int64_t* w_off, int32_t D, int32_t T,
+                                       int64_t B, const int64_t* hsc, int32_t bits,
+                                       const int64_t* indices, const int64_t* offsets, int64_t N,
+                                       const float* grad, float* m1, const int64_t* m1_off,
+                                       float lr, float eps, float wd, int32_t wd_mode,
+                                       int32_t nb) {
+  const int64_t n = N > 0 ? N : 1;
+  int64_t* linear = (int64_t*)malloc(sizeof(int64_t) * n);
+  int64_t* sorted = (int64_t*)malloc(sizeof(int64_t) * n);
+  int32_t* infos = (int32_t*)malloc(sizeof(int32_t) * n);
+  int64_t* run = (int64_t*)malloc(sizeof(int64_t) * n);
+  int32_t* lens = (int32_t*)malloc(sizeof(int32_t) * n);
+  int32_t* cum = (int32_t*)malloc(sizeof(int32_t) * (n + 1));
+  int64_t* pos = (int64_t*)malloc(sizeof(int64_t) * n);
+  float* g = (float*)malloc(sizeof(float) * (D > 0 ? D : 1));
+  int rc = 0;
+  if (!linear || !sorted || !infos || !run || !lens || !cum || !pos || !g) {
+    rc = -2;
+    goto done;
+  }
+  int64_t nruns = 0;
+  if (N > 0) {
+    rc = transpose_impl(hsc, T, B, nb, bits, indices, offsets, N, linear, sorted, infos, run,
+                        lens, &nruns, cum, pos);
+    if (rc) goto done;
+  }
+  for (int64_t r = 0; r < nruns; ++r) {
+    const uint32_t info0 = (uint32_t)infos[cum[r]];
+    const int64_t t = nb >= 32 ? 0 : (int64_t)(info0 >> nb);
+    const int64_t idx = run[r] - hsc[t];
+    for (int32_t d = 0; d < D; ++d) g[d] = 0.0f;
+    for (int32_t j = cum[r]; j < cum[r + 1]; ++j) {
+      const float* gr = grad + pos[j] * D;
+      for (int32_t d = 0; d < D; ++d) g[d] = g[d] + gr[d];
+    }
+    adagrad_row(W + w_off[t] + idx * D, m1 + m1_off[t] + idx, g, D, lr, eps, wd, wd_mode);
+  }
+done:
+  free(linear);
+  free(sorted);
+  free(infos);
+  free(run);
+  free(lens);
+  free(cum);
+  free(pos);
+  free(g);
+  return rc;
 }

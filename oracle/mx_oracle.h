@@ -49,6 +49,16 @@ void orc_grad_indice_weights(const float* grad, int64_t total_D, const float* W,
                              const int32_t* frg, float* giw);
 int64_t orc_bounds_check(const int64_t* rows, int32_t T, int64_t B, int64_t* indices,
                          int64_t* offsets, int64_t N, int32_t mode);
+int orc_nbit_forward_nobag(const uint8_t* W, const int64_t* w_off, const uint8_t* tys,
+                           int32_t D, int32_t T, int64_t B, const int64_t* indices,
+                           const int64_t* offsets, int32_t row_align, int32_t out_kind,
+                           void* out, int32_t fp8_ebits, int32_t fp8_ebias);
+int orc_backward_rowwise_adagrad_nobag(float* W, const int64_t* w_off, int32_t D, int32_t T,
+                                       int64_t B, const int64_t* hsc, int32_t bits,
+                                       const int64_t* indices, const int64_t* offsets, int64_t N,
+                                       const float* grad, float* m1, const int64_t* m1_off,
+                                       float lr, float eps, float wd, int32_t wd_mode,
+                                       int32_t nb);
 void orc_quantize_8bit(const float* x, int64_t rows, int64_t D, uint8_t* out);
 void orc_dequantize_8bit(const uint8_t* in, int64_t rows, int64_t D, float* out);
 void orc_quantize_nbit(const float* x, int64_t rows, int64_t D, int32_t bits, uint8_t* out);

@@ -29,7 +29,7 @@ ORACLE_LIB = BUILD_DIR / "libmx_oracle.so"
 FBGEMM_LIB = BUILD_DIR / "libfbgemm_cpu.so"
 ORACLE_MT_LIB = BUILD_DIR / "libmx_oracle_mt.so"
 
-POOL_SUM, POOL_MEAN = 0, 1
+POOL_SUM, POOL_MEAN, POOL_NONE = 0, 1, 2
 FP32, FP16, INT8, INT4, INT2, FP8 = 0, 1, 2, 3, 4, 6
 
 
@@ -70,6 +70,12 @@ def lib():
         _lib.orc_backward_rowwise_adagrad.argtypes = [
             P, P, P, i32, i64, P, i32, P, P, i64, i32, P, P, i64, P, P, f32, f32, f32, i32, i32]
         _lib.orc_backward_rowwise_adagrad.restype = ctypes.c_int
+        _lib.orc_nbit_forward_nobag.argtypes = [P, P, P, i32, i32, i64, P, P, i32, i32, P, i32,
+                                                i32]
+        _lib.orc_nbit_forward_nobag.restype = ctypes.c_int
+        _lib.orc_backward_rowwise_adagrad_nobag.argtypes = [
+            P, P, i32, i32, i64, P, i32, P, P, i64, P, P, P, f32, f32, f32, i32, i32]
+        _lib.orc_backward_rowwise_adagrad_nobag.restype = ctypes.c_int
         _lib.orc_grad_indice_weights.argtypes = [P, i64, P, P, P, i32, i64, P, P, i32, P, P]
         _lib.orc_grad_indice_weights.restype = None
         _lib.orc_bounds_check.argtypes = [P, i32, i64, P, P, i64, i32]
@@ -232,6 +238,49 @@ def tbe_forward_f32(W, w_off, D_off, B, indices, offsets, pooling=POOL_SUM, indi
     return out
 
 
+def position_tables(offsets, T: int, B: int, N: int) -> np.ndarray:
+    """Table of each of the N positions of a t-major batch (-1 outside every bag)."""
+    offsets = np.asarray(offsets, np.int64)
+    t_of = np.full(N, -1, np.int64)
+    for t in range(T):
+        t_of[max(offsets[t * B], 0): max(offsets[(t + 1) * B], 0)] = t
+    return t_of
+
+
+def tbe_forward_nobag(W, w_off, D: int, B: int, indices, offsets, N: int | None = None):
+    """PoolingMode NONE training forward: out[l] = W_t[indices[l]] (fp16 rows
+    widened to fp32); rows of positions outside every bag are 0."""
+    W = np.asarray(W)
+    w_off = np.asarray(w_off, np.int64)
+    indices = np.asarray(indices, np.int64)
+    T = w_off.shape[0]
+    N = indices.shape[0] if N is None else N
+    t_of = position_tables(offsets, T, B, N)
+    out = np.zeros((N, D), np.float32)
+    inb = np.nonzero(t_of >= 0)[0]
+    if inb.size:
+        start = w_off[t_of[inb]] + indices[inb] * D
+        out[inb] = W[start[:, None] + np.arange(D)[None, :]].astype(np.float32)
+    return out
+
+
+def nbit_forward_nobag(W, w_off, tys, D: int, B: int, indices, offsets, row_align=16,
+                       out_kind: int = 1, fp8_exponent_bits=4, fp8_exponent_bias=7):
+    """PoolingMode NONE nbit lookup, out [N, D] (out_kind 0 fp32, 1 fp16, 2 bf16
+    bits as uint16); rows of positions outside every bag are 0."""
+    W = _c(W, np.uint8)
+    w_off, tys = _c(w_off, np.int64), _c(tys, np.uint8)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    T = w_off.shape[0]
+    N = indices.shape[0]
+    out = np.zeros((N, D), dtype=(np.float32, np.float16, np.uint16)[out_kind])
+    rc = lib().orc_nbit_forward_nobag(_p(W), _p(w_off), _p(tys), D, T, B, _p(indices),
+                                      _p(offsets), row_align, out_kind, _p(out),
+                                      fp8_exponent_bits, fp8_exponent_bias)
+    assert rc == 0, f"orc_nbit_forward_nobag failed ({rc})"
+    return out
+
+
 def hfp8_to_float(codes, ebits: int, ebias: int) -> np.ndarray:
     """Decodes hfp8 codes (uint8) to fp32 (the C restatement)."""
     f = lib().orc_hfp8_to_float
@@ -343,6 +392,54 @@ def backward_rowwise_adagrad(W, w_off, D_off, B, hsc, bits, indices, offsets, po
         _p(m1), _p(m1_off), lr, eps, weight_decay, weight_decay_mode, info_B_num_bits)
     assert rc == 0, f"orc_backward_rowwise_adagrad failed ({rc})"
     return W, m1
+
+
+def backward_rowwise_adagrad_nobag(W, w_off, D: int, B: int, hsc, bits, indices, offsets, grad,
+                                   momentum1, m1_off, lr, eps, weight_decay=0.0,
+                                   weight_decay_mode=0):
+    """PoolingMode NONE backward (grad [N, D], row l the gradient of position
+    l) on copies of W and momentum1; returns (W_new, momentum1_new)."""
+    W = np.array(W, dtype=np.float32, copy=True)
+    m1 = np.array(momentum1, dtype=np.float32, copy=True)
+    w_off, hsc, m1_off = _c(w_off, np.int64), _c(hsc, np.int64), _c(m1_off, np.int64)
+    indices, offsets = _c(indices, np.int64), _c(offsets, np.int64)
+    grad = _c(grad, np.float32)
+    T = w_off.shape[0]
+    N = indices.shape[0]
+    assert grad.shape == (N, D)
+    rc = lib().orc_backward_rowwise_adagrad_nobag(
+        _p(W), _p(w_off), D, T, B, _p(hsc), bits, _p(indices), _p(offsets), N, _p(grad),
+        _p(m1), _p(m1_off), lr, eps, weight_decay, weight_decay_mode, info_B_num_bits(T, B))
+    assert rc == 0, f"orc_backward_rowwise_adagrad_nobag failed ({rc})"
+    return W, m1
+
+
+def transpose_embedding_input_nobag(hsc, B, bits, indices, offsets):
+    """transpose_embedding_input(nobag=True): keys hsc[t] + indices[l] stably
+    sorted on their low ``bits`` bits, infos l * T + t (int64), runs as in the
+    pooled transpose.  numpy (a stable argsort), no C."""
+    hsc = np.asarray(hsc, np.int64)
+    indices = np.asarray(indices, np.int64)
+    T = hsc.shape[0] - 1
+    N = indices.shape[0]
+    t_of = position_tables(offsets, T, B, N)
+    linear = hsc[t_of] + indices
+    mask = (1 << bits) - 1 if bits < 63 else -1
+    order = np.argsort(linear & mask, kind="stable")
+    srt = linear[order]
+    infos = order.astype(np.int64) * T + t_of[order]
+    if N:
+        heads = np.concatenate([[True], srt[1:] != srt[:-1]])
+        starts = np.nonzero(heads)[0]
+        run = srt[starts]
+        lengths = np.diff(np.concatenate([starts, [N]])).astype(np.int32)
+    else:
+        run = np.zeros(0, np.int64)
+        lengths = np.zeros(0, np.int32)
+    r = run.shape[0]
+    cum = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    return dict(linear_indices=linear, sorted_linear_indices=srt, infos_sorted=infos, run=run,
+                run_lengths=lengths, num_runs=r, cumulative_run_lengths=cum)
 
 
 def backward_rowwise_adagrad_mt(W, w_off, D_off, B, hsc, bits, indices, offsets, pooling, grad,

@@ -46,7 +46,7 @@ def test_version_and_last_error(lib):
     # 0.3.0 added the backward's per-stream counter region; 0.4.0 the FP8
     # arguments of mx_nbit_forward and the hfp8 codecs).
     hdr = re.search(r"#define MX_FBGEMM_VERSION (\d+)", HEADER.read_text())
-    assert hdr and lib.mx_version() == int(hdr.group(1)) == 400
+    assert hdr and lib.mx_version() == int(hdr.group(1)) == 500
     lib.mx_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mx_last_error(), bytes)
 

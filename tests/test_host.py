@@ -93,10 +93,32 @@ def test_training_module_rejects_unsupported():
     with pytest.raises(ValueError):
         SplitTableBatchedEmbeddingBagsCodegen(
             [(10, 8, EmbeddingLocation.MANAGED, ComputeDevice.CUDA)], device="cpu")
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError, match="one embedding_dim"):  # NONE: one width for all
         SplitTableBatchedEmbeddingBagsCodegen(
-            [(10, 8, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)], pooling_mode=PoolingMode.NONE,
-            device="cpu")
+            [(10, 8, EmbeddingLocation.DEVICE, ComputeDevice.CUDA),
+             (10, 16, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)],
+            pooling_mode=PoolingMode.NONE, device="cpu")
+    m = SplitTableBatchedEmbeddingBagsCodegen(
+        [(10, 8, EmbeddingLocation.DEVICE, ComputeDevice.CUDA)] * 2, pooling_mode=PoolingMode.NONE,
+        device="cpu")
+    with pytest.raises(ValueError, match="PoolingMode.NONE takes no"):
+        m(torch.zeros(2, dtype=torch.int64), torch.tensor([0, 1, 2]),
+          per_sample_weights=torch.ones(2))
+
+
+def test_inference_module_nobag_arguments():
+    with pytest.raises(ValueError, match="one embedding_dim"):
+        IntNBitTableBatchedEmbeddingBagsCodegen(
+            [("a", 10, 16, SparseType.INT8, EmbeddingLocation.DEVICE),
+             ("b", 10, 32, SparseType.INT8, EmbeddingLocation.DEVICE)],
+            pooling_mode=PoolingMode.NONE, device="cpu")
+    m = IntNBitTableBatchedEmbeddingBagsCodegen(
+        [("a", 10, 16, SparseType.INT8, EmbeddingLocation.DEVICE),
+         ("b", 10, 16, SparseType.FP16, EmbeddingLocation.DEVICE)],
+        pooling_mode=PoolingMode.NONE, device="cpu")
+    with pytest.raises(ValueError, match="PoolingMode.NONE takes no"):
+        m(torch.zeros(2, dtype=torch.int64), torch.tensor([0, 1, 2]),
+          per_sample_weights=torch.ones(2))
 
 
 def test_inference_module_arguments():

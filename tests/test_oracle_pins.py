@@ -544,3 +544,139 @@ def test_codecs_vs_torch_quantized_prepack(D):
         np.testing.assert_array_equal(q, pack(xt).numpy())
         np.testing.assert_array_equal(orc.dequantize_fused_nbit(q, bits, D),
                                       unpack(torch.from_numpy(q)).numpy())
+
+
+# ---- sequence lookups (PoolingMode NONE) --------------------------------------
+
+def _nobag_case(seed, T=3, B=14, D=16, rows=(40, 9, 70), max_L=7):
+    rng = np.random.default_rng(seed)
+    inp = random_tbe(rng, T, B, [D] * T, list(rows), max_L, empty_frac=0.2)
+    return rng, inp
+
+
+@pytest.mark.parametrize("wdtype", [np.float32, np.float16])
+def test_tbe_forward_nobag_vs_embedding(wdtype):
+    """out[l] = F.embedding(indices of table t, W_t)[l], bit for bit (fp16 rows widened)."""
+    rng, inp = _nobag_case(5)
+    D = 16
+    W = rng.uniform(-1, 1, size=sum(E * D for E in (40, 9, 70))).astype(wdtype)
+    w_off = weight_offsets(inp)
+    got = orc.tbe_forward_nobag(W, w_off, D, inp.B, inp.indices, inp.offsets)
+    for t, E in enumerate((40, 9, 70)):
+        o0, o1 = inp.offsets[t * inp.B], inp.offsets[(t + 1) * inp.B]
+        Wt = torch.from_numpy(W[w_off[t]: w_off[t] + E * D].reshape(E, D))
+        ref = torch.nn.functional.embedding(torch.from_numpy(inp.indices[o0:o1]), Wt).float()
+        np.testing.assert_array_equal(got[o0:o1], ref.numpy())
+
+
+def _bf16_bits_to_f32(u16):
+    return (np.asarray(u16, np.uint32) << 16).view(np.float32)
+
+
+def _nbit_rows_f32(buf, w_off, ty, D, idx):
+    """Closed form of dequantized rows in fp32: fma(scale, q, bias) is the
+    float64 value of scale*q + bias rounded once to fp32 (both exact in
+    float64 for fp16 qparams and codes below 256); other types as stored."""
+    stride = orc.nbit_row_bytes(ty, D, 16)
+    rows = np.stack([buf[w_off + i * stride: w_off + (i + 1) * stride] for i in idx])
+    if ty in (orc.INT8, orc.INT4, orc.INT2):
+        bits = {orc.INT8: 8, orc.INT4: 4, orc.INT2: 2}[ty]
+        sc = rows[:, 0:2].copy().view(np.float16).astype(np.float64)
+        bi = rows[:, 2:4].copy().view(np.float16).astype(np.float64)
+        codes = rows[:, 4:]
+        per = 8 // bits
+        q = np.stack([(codes[:, d // per] >> ((d % per) * bits)) & ((1 << bits) - 1)
+                      for d in range(D)], axis=1).astype(np.float64)
+        return (sc * q + bi).astype(np.float32)
+    if ty == orc.FP16:
+        return rows[:, :2 * D].copy().view(np.float16).astype(np.float32)
+    if ty == orc.FP8:
+        return orc.hfp8_to_float(rows[:, :D], 4, 7)
+    return rows[:, :4 * D].copy().view(np.float32)
+
+
+@pytest.mark.parametrize("ty", [orc.INT8, orc.INT4, orc.INT2, orc.FP16, orc.FP32, orc.FP8])
+@pytest.mark.parametrize("out_kind", [0, 1, 2])
+def test_nbit_nobag_vs_fbgemm_cpu(ty, out_kind):
+    """fp16 / bf16 out: each position's row equals FBGEMM's CPU kernel on a bag
+    holding that row alone (a table's positions as bags of length one), as
+    values (FBGEMM's first row adds to +0.0, so a stored -0.0 is +0.0 there
+    and -0.0 here).  fp32 out: the closed form, bit for bit."""
+    rng, inp = _nobag_case(ty * 3 + out_kind, D=32)
+    D, rows = 32, [40, 9, 70]
+    tys = [ty] * 3
+    buf, w_off = build_weights(rng, tys, [D] * 3, rows)
+    got = orc.nbit_forward_nobag(buf, w_off, tys, D, inp.B, inp.indices, inp.offsets,
+                                 out_kind=out_kind)
+    for t in range(3):
+        o0, o1 = int(inp.offsets[t * inp.B]), int(inp.offsets[(t + 1) * inp.B])
+        n = o1 - o0
+        if n == 0:
+            continue
+        g = got[o0:o1]
+        if out_kind == 0:
+            exp = _nbit_rows_f32(buf, int(w_off[t]), ty, D, inp.indices[o0:o1])
+            np.testing.assert_array_equal(g.view(np.uint32), exp.view(np.uint32))
+            continue
+        exp = orc.fbgemm_nbit_forward(buf, np.array([w_off[t]]), [ty], np.array([0, D], np.int32),
+                                      [rows[t]], n, inp.indices[o0:o1],
+                                      np.arange(n + 1, dtype=np.int64), 0, nthreads=1,
+                                      out_bf16=out_kind == 2)
+        if out_kind == 2:
+            np.testing.assert_array_equal(_bf16_bits_to_f32(g), _bf16_bits_to_f32(exp))
+        else:
+            np.testing.assert_array_equal(g.astype(np.float32), exp.astype(np.float32))
+
+
+@pytest.mark.parametrize("wd_mode,wd", [(0, 0.0), (1, 0.1), (2, 0.05)])
+def test_adagrad_nobag_vs_torch_autograd(wd_mode, wd):
+    """The nobag row gradient is torch autograd of F.embedding (the sum of the
+    positions' gradient rows per row), then the rule in torch fp32."""
+    rng, inp = _nobag_case(77, D=8, rows=(30, 6, 25))
+    D, rows = 8, (30, 6, 25)
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E in rows)).astype(np.float32)
+    m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
+    m1_off = np.array([0, rows[0], rows[0] + rows[1]], np.int64)
+    grad = rng.normal(0, 1, size=(inp.N, D)).astype(np.float32)
+    lr, eps = 0.1, 1e-6
+    w_off = weight_offsets(inp)
+    W_new, m_new = orc.backward_rowwise_adagrad_nobag(
+        W, w_off, D, inp.B, inp.hash_size_cumsum, inp.total_hash_size_bits, inp.indices,
+        inp.offsets, grad, m1, m1_off, lr, eps, wd, wd_mode)
+    for t, E in enumerate(rows):
+        o0, o1 = inp.offsets[t * inp.B], inp.offsets[(t + 1) * inp.B]
+        Wt = torch.tensor(W[w_off[t]: w_off[t] + E * D].reshape(E, D), requires_grad=True)
+        out = torch.nn.functional.embedding(torch.from_numpy(inp.indices[o0:o1]), Wt)
+        (out * torch.from_numpy(grad[o0:o1])).sum().backward()
+        g, w = Wt.grad.detach(), Wt.detach()
+        touched = torch.from_numpy(np.isin(np.arange(E), inp.indices[o0:o1]))
+        s = g + wd * w if wd_mode == 1 else g
+        h0 = torch.from_numpy(m1[m1_off[t]: m1_off[t] + E])
+        h = h0 + (s * s).sum(1) / D
+        m = lr / (h.sqrt() + eps)
+        c = 1 - m * wd if wd_mode == 1 else torch.full_like(m, 1 - lr * wd if wd_mode == 2 else 1)
+        w_ref = torch.where(touched[:, None], c[:, None] * w - m[:, None] * g, w)
+        np.testing.assert_allclose(W_new[w_off[t]: w_off[t] + E * D].reshape(E, D), w_ref.numpy(),
+                                   rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(m_new[m1_off[t]: m1_off[t] + E],
+                                   torch.where(touched, h, h0).numpy(), rtol=1e-5, atol=1e-7)
+
+
+def test_transpose_nobag_vs_pooled_transpose():
+    """The numpy nobag transpose against the C pooled one on the same batch:
+    identical keys and runs, and each nobag info l*T + t names the table and,
+    through offsets, the bag of the pooled info at the same sorted place."""
+    _, inp = _nobag_case(9, rows=(40, 9, 70), max_L=9)
+    T = 3
+    nb = orc.info_B_num_bits(T, inp.B)
+    a = orc.transpose_embedding_input_nobag(inp.hash_size_cumsum, inp.B, inp.total_hash_size_bits,
+                                            inp.indices, inp.offsets)
+    b = orc.transpose_embedding_input(inp.hash_size_cumsum, inp.B, nb, inp.total_hash_size_bits,
+                                      inp.indices, inp.offsets)
+    for k in ("sorted_linear_indices", "run", "run_lengths", "cumulative_run_lengths"):
+        np.testing.assert_array_equal(a[k], b[k])
+    l, t = a["infos_sorted"] // T, a["infos_sorted"] % T
+    bag = np.searchsorted(inp.offsets, l, side="right") - 1
+    np.testing.assert_array_equal(t, b["infos_sorted"] >> nb)
+    np.testing.assert_array_equal(bag - t * inp.B, b["infos_sorted"] & ((1 << nb) - 1))
+    np.testing.assert_array_equal(a["linear_indices"], b["linear_indices"])

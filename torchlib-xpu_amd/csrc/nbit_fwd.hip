@@ -660,6 +660,193 @@ int launch_type(const NbitArgs& a, int32_t max_D, int32_t index_bytes, hipStream
   return launch_nbit<32, 32, TY>(a, index_bytes, s);
 }
 
+// ---- sequence lookups (PoolingMode NONE) -----------------------------------
+//
+// Semantics: fbgemm_gpu int_nbit_split_embedding_nobag_codegen_forward_
+// unweighted_cuda (recalled): every table has the same D (the largest max_*_D)
+// and position l writes its own dequantized row, out[l, :].  An INT8/INT4/INT2
+// element is fma(scale, q, bias) in fp32 (one rounding, as FBGEMM's CPU kernels
+// dequantize the first row of a bag); FP32, FP16 and FP8 elements are the row's
+// values themselves.  Then the output rounding of the pooled lookup.
+//
+// Design: a gather over positions, one launch per type present: G = 16 lanes
+// per position, lane k the 8-element blocks k, k + 16, ... of the row; a group
+// takes 16 consecutive positions (one coalesced index load), each lane finds
+// its position's table by a binary search over the tables' first positions in
+// LDS, and positions of another type's tables are left to that type's launch.
+// U rows are loaded before the first is stored.  Tables the call cannot serve
+// (unlaunched type, partial code bytes, misaligned rows, D other than the
+// call's) and positions outside every bag are written as zeros by the check
+// launch, which reports such tables through the status words.
+constexpr int kNobagMaxT = 1024;
+constexpr int kNobagG = 16;
+constexpr int kNobagU = 4;
+
+// Table of position l: the last t with offsets[t*B] <= l.
+template <typename I>
+__device__ __forceinline__ int32_t nobag_table(const int64_t* s_pos, bool lds, const NbitArgs& a,
+                                               int64_t l) {
+  int32_t lo = 0, hi = a.T;
+  while (hi - lo > 1) {
+    const int32_t mid = lo + ((hi - lo) >> 1);
+    const int64_t pm = lds ? s_pos[mid] : idx_at<I>(a.off, mid * a.B);
+    if (pm <= l)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+template <typename I>
+__device__ __forceinline__ void stage_positions(const NbitArgs& a, int64_t* s_pos, bool lds) {
+  if (lds)
+    for (int t = threadIdx.x; t <= a.T; t += blockDim.x) s_pos[t] = idx_at<I>(a.off, t * a.B);
+  __syncthreads();
+}
+
+// Bytes [o, o + n) of a row (n <= 32, o at the element block's start) into
+// little-endian words: whole words when the block's bytes are whole words at
+// 4-byte alignment (rows start 4-aligned), else byte by byte.
+template <int NB>
+__device__ __forceinline__ void load_block(const uint8_t* p, int n, uint32_t (&w)[8]) {
+  if (n == NB && (NB % 4 == 0)) {
+#pragma unroll
+    for (int q = 0; q < NB / 4; ++q) w[q] = reinterpret_cast<const uint32_t*>(p)[q];
+  } else if (n == NB && NB == 2) {
+    w[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) w[q] = 0u;
+    for (int i = 0; i < n; ++i) w[i >> 2] |= static_cast<uint32_t>(p[i]) << ((i & 3) * 8);
+  }
+}
+
+// Element e of a block of TY codes (the raw code for integer types).
+template <int TY>
+__device__ __forceinline__ float block_elem(const NbitArgs& a, const uint32_t (&w)[8], int e) {
+  constexpr int bits = TyInfo<TY>::kBits;
+  const int bit = e * bits;
+  const uint32_t word = w[bit >> 5];
+  const int sh = bit & 31;
+  if constexpr (TY == MX_SPARSE_FP32) return __uint_as_float(word);
+  if constexpr (TY == MX_SPARSE_FP16)
+    return __half2float(__ushort_as_half(static_cast<uint16_t>(word >> sh)));
+  if constexpr (TY == MX_SPARSE_FP8) return a.fp8.decode((word >> sh) & 0xffu);
+  return static_cast<float>((word >> sh) & ((1u << bits) - 1u));
+}
+
+template <typename I, int TY>
+__global__ void __launch_bounds__(256) nbit_nobag_kernel(NbitArgs a, int32_t D, int64_t N) {
+  constexpr int G = kNobagG, U = kNobagU, NG = 256 / G;
+  constexpr int BITS = TyInfo<TY>::kBits;
+  constexpr bool Q = TyInfo<TY>::kQ;
+  constexpr int NB = 8 * BITS / 8;  // bytes of a full 8-element block
+  __shared__ int64_t s_pos[kNobagMaxT + 1];
+  const bool lds = a.T <= kNobagMaxT;
+  stage_positions<I>(a, s_pos, lds);
+  const int64_t p0 = lds ? s_pos[0] : idx_at<I>(a.off, 0);
+  const int64_t p1 = lds ? s_pos[a.T] : idx_at<I>(a.off, static_cast<int64_t>(a.T) * a.B);
+  const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
+  const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * NG * G;
+  for (int64_t base = (lb * NG + threadIdx.x / G) * G; base < N; base += step) {
+    const int64_t l = base + k;
+    int64_t my_row = -1;  // byte offset of l's row in the weights; -1: not this launch's
+    if (l < N && l >= p0 && l < p1) {
+      const int32_t t = nobag_table<I>(s_pos, lds, a, l);
+      const int32_t Dt = a.D_off[t + 1] - a.D_off[t];
+      const int64_t wo = a.w_off[t];
+      if (static_cast<int32_t>(a.tys[t]) == TY && Dt == D &&
+          table_ok(TY, Dt, a.served, wo, a.row_align))
+        my_row = wo + idx_at<I>(a.idx, l) * row_bytes_of(TY, Dt, a.row_align);
+    }
+    const int n = static_cast<int>(N - base < G ? N - base : G);
+    for (int j = 0; j < n; j += U) {
+      int64_t roff[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) roff[u] = __shfl(my_row, g * G + (j + u < n ? j + u : n - 1), 64);
+      for (int cb = k * 8; cb < D; cb += G * 8) {
+        const int nc = D - cb < 8 ? D - cb : 8;
+        const int nbytes = nc * BITS / 8;
+        uint32_t w[U][8];
+        uint32_t qp[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          qp[u] = 0u;
+          if (j + u < n && roff[u] >= 0) {
+            const uint8_t* row = a.W + roff[u];
+            load_block<NB>(row + (Q ? 4 : 0) + cb * BITS / 8, nbytes, w[u]);
+            if constexpr (Q) qp[u] = *reinterpret_cast<const uint32_t*>(row);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (j + u >= n || roff[u] < 0) continue;
+          float v[8];
+          const float scale = __half2float(__ushort_as_half(static_cast<uint16_t>(qp[u] & 0xffffu)));
+          const float bias = __half2float(__ushort_as_half(static_cast<uint16_t>(qp[u] >> 16)));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = block_elem<TY>(a, w[u], e);
+            v[e] = Q ? __builtin_fmaf(scale, x, bias) : x;
+          }
+          store_out(a, (base + j + u) * D + cb, nc, v);
+        }
+      }
+    }
+  }
+}
+
+// One block per table zeroes the positions of a table the call cannot serve
+// and reports it; block T zeroes the positions outside every bag.
+template <typename I>
+__global__ void __launch_bounds__(256) nbit_nobag_check_kernel(NbitArgs a, int32_t D, int64_t N) {
+  const int64_t t = blockIdx.x;
+  int64_t lo, hi, lo2 = 0, hi2 = 0;
+  if (t < a.T) {
+    const int32_t Dt = a.D_off[t + 1] - a.D_off[t];
+    if (Dt == D && table_ok(a.tys[t], Dt, a.served, a.w_off[t], a.row_align)) return;
+    lo = idx_at<I>(a.off, t * a.B);
+    hi = idx_at<I>(a.off, (t + 1) * a.B);
+    if (threadIdx.x == 0 && a.mailbox)
+      __hip_atomic_store(a.mailbox + MX_STATUS_NBIT_TABLE, 1u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+  } else {
+    lo = 0;
+    hi = idx_at<I>(a.off, 0);
+    lo2 = idx_at<I>(a.off, static_cast<int64_t>(a.T) * a.B);
+    hi2 = N;
+  }
+  for (int r = 0; r < 2; ++r) {
+    int64_t s0 = r == 0 ? lo : lo2, s1 = r == 0 ? hi : hi2;
+    s0 = s0 < 0 ? 0 : s0;
+    s1 = s1 > N ? N : s1;
+    for (int64_t i = s0 * D + threadIdx.x; i < s1 * D; i += blockDim.x) {
+      if (a.out_kind != 0)
+        reinterpret_cast<uint16_t*>(a.out)[i] = 0u;
+      else
+        reinterpret_cast<float*>(a.out)[i] = 0.0f;
+    }
+  }
+}
+
+template <int TY>
+int launch_nobag_type(const NbitArgs& a, int32_t max_D, int32_t D, int64_t N,
+                      int32_t index_bytes, hipStream_t s) {
+  if (max_D <= 0) return MX_OK;
+  const int64_t want = ceil_div(N, 256);  // 256 positions per block and round
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
+  const dim3 gd(static_cast<uint32_t>(want < cap ? want : cap));
+  if (index_bytes == 8)
+    nbit_nobag_kernel<int64_t, TY><<<gd, 256, 0, s>>>(a, D, N);
+  else
+    nbit_nobag_kernel<int32_t, TY><<<gd, 256, 0, s>>>(a, D, N);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
 }  // namespace
 }  // namespace mx
 
@@ -752,4 +939,77 @@ extern "C" int mx_nbit_forward(const uint8_t* dev_weights, const int64_t* weight
   if (int rc = launch_type<MX_SPARSE_FP8>(a, max_float8_D, index_bytes, s)) return rc;
   if (max_float8_D > 0) a.nchk = 0;
   return launch_type<MX_SPARSE_FP32>(a, max_float32_D, index_bytes, s);
+}
+
+extern "C" int mx_nbit_forward_nobag(const uint8_t* dev_weights, const int64_t* weights_offsets,
+                                     const uint8_t* weights_tys, const int32_t* D_offsets,
+                                     int32_t T, int64_t B, int32_t max_int2_D, int32_t max_int4_D,
+                                     int32_t max_int8_D, int32_t max_float16_D,
+                                     int32_t max_float32_D, const void* indices,
+                                     const void* offsets, int32_t index_bytes, int64_t N,
+                                     int32_t output_dtype, int32_t row_alignment,
+                                     int32_t max_float8_D, int32_t fp8_exponent_bits,
+                                     int32_t fp8_exponent_bias, void* out, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative T, B or N");
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16 ||
+                 output_dtype == MX_SPARSE_BF16,
+             "output_dtype %d not supported (FP32=0, FP16=1, BF16=5)", output_dtype);
+  MX_REQUIRE(row_alignment >= 1, "row_alignment must be positive");
+  int32_t D = 0;
+  for (int32_t d :
+       {max_int2_D, max_int4_D, max_int8_D, max_float16_D, max_float32_D, max_float8_D}) {
+    MX_REQUIRE(d >= 0, "negative max_D");
+    if (d > D) D = d;
+  }
+  MX_REQUIRE(D <= 1024, "max D %d above 1024", D);
+  MX_REQUIRE(max_int4_D % 2 == 0 && max_int2_D % 4 == 0,
+             "INT4 D must be even and INT2 D a multiple of 4 (max_int4_D %d, max_int2_D %d)",
+             max_int4_D, max_int2_D);
+  MX_REQUIRE(max_float8_D == 0 || hfp8_format_ok(fp8_exponent_bits, fp8_exponent_bias),
+             "FP8 tables need 1 <= fp8_exponent_bits <= 7 and 0 <= fp8_exponent_bias <= 120 "
+             "(got %d, %d)", fp8_exponent_bits, fp8_exponent_bias);
+  if (N == 0 || D == 0) return MX_OK;
+  MX_REQUIRE(T > 0 && B > 0, "%lld indices but no bags (T=%d, B=%lld)", (long long)N, T,
+             (long long)B);
+  MX_REQUIRE(dev_weights && weights_offsets && weights_tys && D_offsets && indices && offsets &&
+                 out,
+             "null pointer argument");
+  NbitArgs a{};
+  a.W = dev_weights;
+  a.w_off = weights_offsets;
+  a.tys = weights_tys;
+  a.D_off = D_offsets;
+  a.idx = indices;
+  a.off = offsets;
+  a.iw = nullptr;
+  a.out = out;
+  a.B = B;
+  a.total_D = D;
+  a.T = T;
+  a.pooling = MX_POOL_NONE;
+  a.row_align = row_alignment;
+  a.out_kind = output_dtype == MX_SPARSE_FP16 ? 1 : (output_dtype == MX_SPARSE_BF16 ? 2 : 0);
+  a.served = (max_int8_D > 0 ? 1 << MX_SPARSE_INT8 : 0) | (max_int4_D > 0 ? 1 << MX_SPARSE_INT4 : 0) |
+             (max_int2_D > 0 ? 1 << MX_SPARSE_INT2 : 0) |
+             (max_float16_D > 0 ? 1 << MX_SPARSE_FP16 : 0) |
+             (max_float32_D > 0 ? 1 << MX_SPARSE_FP32 : 0) |
+             (max_float8_D > 0 ? 1 << MX_SPARSE_FP8 : 0);
+  a.fp8 = max_float8_D > 0 ? Hfp8::make(fp8_exponent_bits, fp8_exponent_bias) : Hfp8::make(4, 7);
+  a.nchk = 0;
+  a.mailbox = status_mailbox();
+  auto* s = as_stream(stream);
+  const dim3 cg(static_cast<uint32_t>(T) + 1);
+  if (index_bytes == 8)
+    nbit_nobag_check_kernel<int64_t><<<cg, 256, 0, s>>>(a, D, N);
+  else
+    nbit_nobag_check_kernel<int32_t><<<cg, 256, 0, s>>>(a, D, N);
+  MX_LAUNCH_CHECK();
+  if (int rc = launch_nobag_type<MX_SPARSE_INT8>(a, max_int8_D, D, N, index_bytes, s)) return rc;
+  if (int rc = launch_nobag_type<MX_SPARSE_INT4>(a, max_int4_D, D, N, index_bytes, s)) return rc;
+  if (int rc = launch_nobag_type<MX_SPARSE_INT2>(a, max_int2_D, D, N, index_bytes, s)) return rc;
+  if (int rc = launch_nobag_type<MX_SPARSE_FP16>(a, max_float16_D, D, N, index_bytes, s)) return rc;
+  if (int rc = launch_nobag_type<MX_SPARSE_FP8>(a, max_float8_D, D, N, index_bytes, s)) return rc;
+  return launch_nobag_type<MX_SPARSE_FP32>(a, max_float32_D, D, N, index_bytes, s);
 }

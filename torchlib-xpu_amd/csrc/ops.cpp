@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <array>
 #include <cstring>
 #include <mutex>
@@ -110,8 +111,9 @@ void raise_if_lookback_failed(int dev) {
                 dev, " met a table it cannot serve (a weights_tys byte naming no type whose "
                 "max_*_D is positive, an INT4 table of odd D, an INT2 table of D not a "
                 "multiple of 4, or rows not starting at 4-byte boundaries: weights_offsets[t] "
-                "or the row stride after row_alignment not a multiple of 4) and wrote that "
-                "table's output columns as zeros");
+                "or the row stride after row_alignment not a multiple of 4; with PoolingMode "
+                "NONE also a table whose D is not the largest max_*_D) and wrote that "
+                "table's output (columns, or rows of its positions) as zeros");
   }
 }
 
@@ -577,6 +579,51 @@ Tensor tbe_forward(const Tensor& dev_weights, const Tensor& uvm_weights,
   return out;
 }
 
+// PoolingMode NONE: out [N, D], row l the row of position l.
+Tensor tbe_forward_nobag(const Tensor& dev_weights, const Tensor& uvm_weights,
+                         const Tensor& weights_offsets, int64_t D, const Tensor& indices,
+                         const Tensor& offsets, int64_t output_dtype) {
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  check_arg(weights_offsets, dev_weights, "weights_offsets", true);
+  check_arg(indices, dev_weights, "indices", false);
+  check_arg(offsets, dev_weights, "offsets", false);
+  TORCH_CHECK(uvm_weights.numel() == 0, "UVM weights are not supported (DEVICE placement only)");
+  const int32_t wty = weights_ty_of(dev_weights);
+  TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  const int64_t T = weights_offsets.numel();
+  TORCH_CHECK(T >= 1 && (offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  TORCH_CHECK(output_dtype == MX_SPARSE_FP32 || output_dtype == MX_SPARSE_FP16,
+              "output_dtype must be FP32 (0) or FP16 (1)");
+  const int64_t N = indices.numel();
+  auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16 ? at::kHalf : at::kFloat);
+  Tensor out = at::empty({N, D}, opts);
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  MX_CALL(mx_tbe_forward_nobag(dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(),
+                               static_cast<int32_t>(T), B, static_cast<int32_t>(D),
+                               idx.data_ptr(), off.data_ptr(), ib, N, out.data_ptr(),
+                               static_cast<int32_t>(output_dtype), stream_of(dev_weights)));
+  return out;
+}
+
+Tensor forward_nobag_unweighted(const Tensor& dev_weights, const Tensor& uvm_weights,
+                                const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+                                const Tensor& weights_offsets, c10::SymInt D,
+                                const Tensor& indices, const Tensor& offsets,
+                                const Tensor& lxu_cache_locations, const Tensor& uvm_cache_stats,
+                                int64_t output_dtype, bool is_experimental) {
+  check_no_cache(lxu_cache_weights);
+  (void)weights_placements;
+  (void)lxu_cache_locations;
+  (void)uvm_cache_stats;
+  (void)is_experimental;
+  return tbe_forward_nobag(dev_weights, uvm_weights, weights_offsets, D.expect_int(), indices,
+                           offsets, output_dtype);
+}
+
 Tensor forward_unweighted(const Tensor& dev_weights, const Tensor& uvm_weights,
                           const Tensor& lxu_cache_weights, const Tensor& weights_placements,
                           const Tensor& weights_offsets, const Tensor& D_offsets,
@@ -720,8 +767,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
     int64_t info_B_num_bits, int64_t info_B_mask, int64_t total_unique_indices) {
   (void)info_B_mask;
   (void)total_unique_indices;
-  TORCH_CHECK(!nobag, "nobag transpose is not supported");
   const bool vbe = vbe_b_t_map.has_value() && vbe_b_t_map->defined();
+  TORCH_CHECK(!(nobag && vbe), "nobag transpose takes no vbe_b_t_map");
   check_gpu(indices, "indices");
   c10::OptionalDeviceGuard guard(indices.device());
   check_arg(hash_size_cumsum, indices, "hash_size_cumsum", true);
@@ -737,6 +784,23 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   const int64_t N = indices.numel();
   auto o64 = indices.options().dtype(at::kLong);
   auto o32 = indices.options().dtype(at::kInt);
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  if (nobag) {  // sequence lookups: int64 infos l * T + t
+    Tensor linear = at::empty({N}, o64), sorted = at::empty({N}, o64);
+    Tensor infos = at::empty({N}, o64), run = at::empty({N}, o64);
+    Tensor lengths = at::empty({N}, o32), num_runs = at::zeros({1}, o32);
+    Tensor cum = at::empty({N + 1}, o32);
+    const size_t nb_bytes = mx_tbe_transpose_nobag_workspace_bytes(
+        N, static_cast<int32_t>(T), static_cast<int32_t>(total_hash_size_bits));
+    Tensor nws = at::empty({static_cast<int64_t>(nb_bytes)}, indices.options().dtype(at::kByte));
+    MX_CALL(mx_tbe_transpose_embedding_input_nobag(
+        hash_size_cumsum.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
+        static_cast<int32_t>(total_hash_size_bits), idx.data_ptr(), off.data_ptr(), ib, N,
+        linear.data_ptr<int64_t>(), sorted.data_ptr<int64_t>(), infos.data_ptr<int64_t>(),
+        run.data_ptr<int64_t>(), lengths.data_ptr<int32_t>(), num_runs.data_ptr<int32_t>(),
+        cum.data_ptr<int32_t>(), nws.data_ptr(), nb_bytes, stream_of(indices)));
+    return {linear, sorted, infos, run, lengths, num_runs, cum};
+  }
   Tensor linear = at::empty({N}, o64), sorted = at::empty({N}, o64);
   Tensor infos = at::empty({N}, o32), run = at::empty({N}, o64);
   // Every entry of lengths and cum is written (past num_runs: 0 and N; all 0
@@ -745,7 +809,6 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> transpose_emb
   Tensor cum = at::empty({N + 1}, o32);
   const size_t ws_bytes = mx_tbe_transpose_workspace_bytes(N, total_hash_size_bits);
   Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, indices.options().dtype(at::kByte));
-  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
   if (vbe) {
     const int64_t total_B = offsets.numel() - 1;
     check_gpu(*vbe_b_t_map, "vbe_b_t_map");
@@ -869,6 +932,70 @@ Tensor backward_rowwise_adagrad_impl(
       static_cast<float>(eps), static_cast<float>(weight_decay),
       static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0, &rng, ws.data_ptr(), ws_bytes,
       stream_of(dev_weights)));
+  return at::empty({0}, dev_weights.options());
+}
+
+// PoolingMode NONE: grad_output [N, D], row l the gradient of position l.
+Tensor backward_rowwise_adagrad_nobag(
+    const Tensor& grad_output, const Tensor& dev_weights, const Tensor& uvm_weights,
+    const Tensor& lxu_cache_weights, const Tensor& weights_placements,
+    const Tensor& weights_offsets, c10::SymInt D_sym, const Tensor& hash_size_cumsum,
+    int64_t total_hash_size_bits, const Tensor& indices, const Tensor& offsets,
+    const Tensor& lxu_cache_locations, int64_t BT_block_size,
+    int64_t max_segment_length_per_warp, bool stochastic_rounding,
+    const Tensor& momentum1_dev, const Tensor& momentum1_uvm, const Tensor& momentum1_placements,
+    const Tensor& momentum1_offsets, double eps, double learning_rate, double weight_decay,
+    int64_t weight_decay_mode, double max_norm) {
+  check_no_cache(lxu_cache_weights);
+  (void)weights_placements;
+  (void)lxu_cache_locations;
+  (void)BT_block_size;
+  (void)max_segment_length_per_warp;
+  (void)momentum1_placements;
+  check_gpu(dev_weights, "dev_weights");
+  c10::OptionalDeviceGuard guard(dev_weights.device());
+  for (auto* t : {&grad_output, &indices, &offsets})
+    check_arg(*t, dev_weights, "TBE backward argument", false);
+  for (auto* t : {&weights_offsets, &hash_size_cumsum, &momentum1_dev, &momentum1_offsets})
+    check_arg(*t, dev_weights, "TBE backward argument", true);
+  TORCH_CHECK(uvm_weights.numel() == 0 && momentum1_uvm.numel() == 0,
+              "UVM storage is not supported (DEVICE placement only)");
+  TORCH_CHECK(max_norm == 0.0, "max_norm is not supported");
+  const int32_t wty = weights_ty_of(dev_weights);
+  TORCH_CHECK(momentum1_dev.scalar_type() == at::kFloat && momentum1_dev.is_contiguous(),
+              "momentum1_dev must be contiguous fp32");
+  TORCH_CHECK(grad_output.scalar_type() == at::kFloat, "grad_output must be fp32");
+  TORCH_CHECK(weights_offsets.scalar_type() == at::kLong, "weights_offsets must be int64");
+  TORCH_CHECK(momentum1_offsets.scalar_type() == at::kLong, "momentum1_offsets must be int64");
+  TORCH_CHECK(hash_size_cumsum.scalar_type() == at::kLong, "hash_size_cumsum must be int64");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  TORCH_CHECK(index_bytes_of(offsets, "offsets") == ib, "indices and offsets must share a dtype");
+  ensure_mailbox(dev_weights.device().index(), stream_of(dev_weights));
+  const int64_t T = weights_offsets.numel();
+  TORCH_CHECK(T >= 1 && hash_size_cumsum.numel() == T + 1 && momentum1_offsets.numel() == T,
+              "hash_size_cumsum must have T+1 and momentum1_offsets T entries");
+  TORCH_CHECK((offsets.numel() - 1) % T == 0, "offsets must have T*B+1 entries");
+  const int64_t B = (offsets.numel() - 1) / T;
+  const int64_t D = D_sym.expect_int();
+  const int64_t N = indices.numel();
+  const Tensor g = grad_output.contiguous();
+  TORCH_CHECK(g.dim() == 2 && g.size(0) == N && g.size(1) == D, "grad_output must be [N, D] = [",
+              N, ", ", D, "]");
+  const size_t ws_bytes = mx_tbe_backward_nobag_workspace_bytes(
+      N, static_cast<int32_t>(T), static_cast<int32_t>(total_hash_size_bits),
+      static_cast<int32_t>(D));
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, dev_weights.options().dtype(at::kByte));
+  const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  const bool sr = wty == MX_SPARSE_FP16 && stochastic_rounding;
+  const mx_rng_state rng = sr ? next_rounding_state(dev_weights) : mx_rng_state{};
+  MX_CALL(mx_tbe_backward_rowwise_adagrad_nobag(
+      dev_weights.data_ptr(), wty, weights_offsets.data_ptr<int64_t>(), static_cast<int32_t>(T), B,
+      static_cast<int32_t>(D), hash_size_cumsum.data_ptr<int64_t>(),
+      static_cast<int32_t>(total_hash_size_bits), idx.data_ptr(), off.data_ptr(), ib, N,
+      g.data_ptr<float>(), momentum1_dev.data_ptr<float>(), momentum1_offsets.data_ptr<int64_t>(),
+      static_cast<float>(learning_rate), static_cast<float>(eps),
+      static_cast<float>(weight_decay), static_cast<int32_t>(weight_decay_mode), sr ? 1 : 0,
+      &rng, ws.data_ptr(), ws_bytes, stream_of(dev_weights)));
   return at::empty({0}, dev_weights.options());
 }
 
@@ -1136,6 +1263,18 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     s["vbe_output_size"] = vbe_output_size;
     s["vbe_info_B_num_bits"] = vbe_info_B_num_bits;
     at::AutoDispatchBelowADInplaceOrView g;
+    if (pooling_mode == MX_POOL_NONE) {  // sequence lookups: [N, max_D]
+      const int64_t T = D_offsets.numel() - 1;
+      TORCH_CHECK(!vbe, "PoolingMode NONE takes no VBE metadata");
+      TORCH_CHECK(!indice_weights.has_value() || !indice_weights->defined(),
+                  "PoolingMode NONE takes no indice_weights");
+      // Every D_t <= max_D, so total_D = T * max_D makes all of them max_D.
+      TORCH_CHECK(T >= 1 && total_D == T * max_D,
+                  "PoolingMode NONE needs every table of one width (total_D ", total_D,
+                  " != T * max_D = ", T * max_D, ")");
+      return tbe_forward_nobag(dev_weights, uvm_weights, weights_offsets, max_D, indices, offsets,
+                               output_dtype);
+    }
     return tbe_forward(dev_weights, uvm_weights, weights_placements, weights_offsets, D_offsets,
                        total_D, max_D, indices, offsets, pooling_mode, indice_weights,
                        output_dtype, vbe ? saved_vbe(s) : VbeMeta());
@@ -1167,6 +1306,18 @@ class LookupRowwiseAdagrad : public torch::autograd::Function<LookupRowwiseAdagr
     const Tensor g = grad.contiguous();
     const Tensor iw = s["indice_weights"].toTensor();
     variable_list out(kNumInputs);
+    if (s["pooling_mode"].toInt() == MX_POOL_NONE) {
+      backward_rowwise_adagrad_nobag(
+          g, s["dev_weights"].toTensor(), s["uvm_weights"].toTensor(), empty,
+          s["weights_placements"].toTensor(), s["weights_offsets"].toTensor(),
+          c10::SymInt(s["max_D"].toInt()), s["hash_size_cumsum"].toTensor(),
+          s["total_hash_size_bits"].toInt(), s["indices"].toTensor(), s["offsets"].toTensor(),
+          empty, 0, 0, s["stochastic_rounding"].toBool(), s["momentum1_dev"].toTensor(),
+          s["momentum1_uvm"].toTensor(), s["momentum1_placements"].toTensor(),
+          s["momentum1_offsets"].toTensor(), s["eps"].toDouble(), s["learning_rate"].toDouble(),
+          s["weight_decay"].toDouble(), s["weight_decay_mode"].toInt(), s["max_norm"].toDouble());
+      return out;
+    }
     // The weight gradient reads the rows before the fused update below
     // overwrites them (same stream, so ordered).
     if (iw.defined() && ctx->needs_input_grad(kIndiceWeightsEdge)) {
@@ -1493,8 +1644,26 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   auto opts = dev_weights.options().dtype(output_dtype == MX_SPARSE_FP16   ? at::kHalf
                                           : output_dtype == MX_SPARSE_BF16 ? at::kBFloat16
                                                                            : at::kFloat);
-  Tensor out = at::empty({B, total_D}, opts);
   const Tensor idx = indices.contiguous(), off = offsets.contiguous();
+  if (pooling_mode == MX_POOL_NONE) {  // sequence lookups: [N, D], D the largest max_*_D
+    TORCH_CHECK(iw == nullptr, "PoolingMode NONE takes no indice_weights");
+    const int64_t D = std::max({max_int2_D, max_int4_D, max_int8_D, max_float16_D,
+                                max_float32_D, max_float8_D.value_or(0)});
+    Tensor out = at::empty({indices.numel(), D}, opts);
+    MX_CALL(mx_nbit_forward_nobag(
+        dev_weights.data_ptr<uint8_t>(), weights_offsets.data_ptr<int64_t>(),
+        weights_tys.data_ptr<uint8_t>(), D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T),
+        B, static_cast<int32_t>(max_int2_D), static_cast<int32_t>(max_int4_D),
+        static_cast<int32_t>(max_int8_D), static_cast<int32_t>(max_float16_D),
+        static_cast<int32_t>(max_float32_D), idx.data_ptr(), off.data_ptr(), ib, indices.numel(),
+        static_cast<int32_t>(output_dtype), static_cast<int32_t>(row_alignment.value_or(16)),
+        static_cast<int32_t>(max_float8_D.value_or(0)),
+        static_cast<int32_t>(fp8_exponent_bits.value_or(-1)),
+        static_cast<int32_t>(fp8_exponent_bias.value_or(-1)), out.data_ptr(),
+        stream_of(dev_weights)));
+    return out;
+  }
+  Tensor out = at::empty({B, total_D}, opts);
   MX_CALL(mx_nbit_forward(
       dev_weights.data_ptr<uint8_t>(), weights_offsets.data_ptr<int64_t>(),
       weights_tys.data_ptr<uint8_t>(), D_offsets.data_ptr<int32_t>(), static_cast<int32_t>(T), B,
@@ -1534,6 +1703,20 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, Tensor offsets, "
         "int pooling_mode, Tensor indice_weights, Tensor lxu_cache_locations, "
         "Tensor uvm_cache_stats, int output_dtype, bool is_experimental) -> Tensor");
+  m.def("split_embedding_nobag_codegen_forward_unweighted_cuda(Tensor dev_weights, "
+        "Tensor uvm_weights, Tensor lxu_cache_weights, Tensor weights_placements, "
+        "Tensor weights_offsets, SymInt D, Tensor indices, Tensor offsets, "
+        "Tensor lxu_cache_locations, Tensor uvm_cache_stats, int output_dtype, "
+        "bool is_experimental) -> Tensor");
+  m.def("split_embedding_nobag_backward_codegen_rowwise_adagrad_unweighted_exact_cuda("
+        "Tensor grad_output, Tensor(a!) dev_weights, Tensor uvm_weights, "
+        "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, SymInt D, "
+        "Tensor hash_size_cumsum, int total_hash_size_bits, Tensor indices, Tensor offsets, "
+        "Tensor lxu_cache_locations, int BT_block_size, int max_segment_length_per_warp, "
+        "bool stochastic_rounding, Tensor(b!) momentum1_dev, Tensor momentum1_uvm, "
+        "Tensor momentum1_placements, Tensor momentum1_offsets, float eps=0, "
+        "float learning_rate=0, float weight_decay=0.0, int weight_decay_mode=0, "
+        "float max_norm=0.0) -> Tensor");
   m.def("get_infos_metadata(Tensor unused, int B, int T) -> (int, int)");
   m.def("transpose_embedding_input(Tensor hash_size_cumsum, int total_hash_size_bits, "
         "Tensor indices, Tensor offsets, bool nobag=False, Tensor? vbe_b_t_map=None, "
@@ -1656,6 +1839,10 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("split_embedding_codegen_forward_unweighted_cuda", TORCH_FN(mx_ops::forward_unweighted));
   m.impl("split_embedding_codegen_forward_weighted_cuda", TORCH_FN(mx_ops::forward_weighted));
   m.impl("transpose_embedding_input", TORCH_FN(mx_ops::transpose_embedding_input));
+  m.impl("split_embedding_nobag_codegen_forward_unweighted_cuda",
+         TORCH_FN(mx_ops::forward_nobag_unweighted));
+  m.impl("split_embedding_nobag_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
+         TORCH_FN(mx_ops::backward_rowwise_adagrad_nobag));
   m.impl("split_embedding_backward_codegen_rowwise_adagrad_unweighted_exact_cuda",
          TORCH_FN(mx_ops::backward_rowwise_adagrad_exact));
   m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",

@@ -1939,3 +1939,226 @@ extern "C" int mx_tbe_backward_rowwise_adagrad_vbe(
                        weight_decay, weight_decay_mode, stochastic_rounding, rng, workspace,
                        workspace_bytes, stream);
 }
+
+// ---- sequence lookups (PoolingMode NONE) -----------------------------------
+//
+// Semantics: fbgemm_gpu split_embedding_nobag_backward_codegen_rowwise_adagrad_
+// unweighted_exact_cuda and transpose_embedding_input(nobag=True) (recalled):
+// every position l of bag (t, b) is its own occurrence with its own gradient
+// row grad_output[l, :] (all tables of width D); each distinct (t, i) sums the
+// rows of its occurrences in sorted (position) order and takes the rowwise
+// Adagrad step of the pooled backward.  The nobag transpose's info of a
+// position is l * T + t (int64).
+//
+// Design: the batch is recast as a variable batch in which every position is
+// a bag of length one: bag l has offsets l and l + 1, belongs to table t with
+// b = l - offsets[t*B] (the b_t word (t << nb) | b), and its gradient row
+// starts at l * D.  The sort, run encoding and update then run unchanged.
+// Needs offsets[0] = 0 and offsets[T*B] = N, as upstream.
+namespace mx {
+namespace {
+
+constexpr int kNobagMaxT = 1024;  // tables whose first positions fit LDS
+
+template <typename I>
+__global__ void __launch_bounds__(256)
+    nobag_layout_kernel(const I* __restrict__ offsets, int32_t T, int64_t B, int64_t N,
+                        int32_t D, int32_t nb, I* __restrict__ bag_offsets,
+                        int32_t* __restrict__ b_t_map, int64_t* __restrict__ row_out,
+                        int32_t* __restrict__ B_offsets, int32_t* __restrict__ D_offsets) {
+  __shared__ int64_t s_pos[kNobagMaxT + 1];
+  const bool lds = T <= kNobagMaxT;
+  if (lds)
+    for (int t = threadIdx.x; t <= T; t += 256) s_pos[t] = static_cast<int64_t>(offsets[t * B]);
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int t = threadIdx.x; t <= T; t += 256) {
+      if (B_offsets) B_offsets[t] = static_cast<int32_t>(offsets[t * B]);
+      if (D_offsets) D_offsets[t] = t * D;
+    }
+    if (threadIdx.x == 0) bag_offsets[N] = static_cast<I>(N);
+  }
+  for (int64_t l = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; l < N;
+       l += static_cast<int64_t>(gridDim.x) * 256) {
+    int32_t lo = 0, hi = T;  // pos[lo] <= l < pos[hi] (lo = 0 or T - 1 outside every bag)
+    while (hi - lo > 1) {
+      const int32_t mid = lo + ((hi - lo) >> 1);
+      const int64_t pm = lds ? s_pos[mid] : static_cast<int64_t>(offsets[mid * B]);
+      if (pm <= l)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    const int64_t p = lds ? s_pos[lo] : static_cast<int64_t>(offsets[lo * B]);
+    const int64_t b = l - p > 0 ? l - p : 0;
+    bag_offsets[l] = static_cast<I>(l);
+    b_t_map[l] = static_cast<int32_t>((nb >= 32 ? 0u : (static_cast<uint32_t>(lo) << nb)) |
+                                      static_cast<uint32_t>(b));
+    if (row_out) row_out[l] = l * D;
+  }
+}
+
+// Sorted (t << nb) | b words of the recast batch -> the nobag infos l * T + t.
+template <typename I>
+__global__ void __launch_bounds__(256)
+    nobag_infos_kernel(const int32_t* __restrict__ infos, const I* __restrict__ offsets,
+                       int32_t T, int64_t B, int64_t N, int32_t nb, int64_t* __restrict__ out) {
+  const uint32_t bmask = nb >= 32 ? 0xffffffffu : ((1u << nb) - 1u);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const uint32_t w = static_cast<uint32_t>(infos[i]);
+    const int64_t t = nb >= 32 ? 0 : static_cast<int64_t>(w >> nb);
+    const int64_t l = static_cast<int64_t>(offsets[t * B]) + static_cast<int64_t>(w & bmask);
+    out[i] = l * T + t;
+  }
+}
+
+// The recast batch's arrays, after the backward's (or transpose's) workspace.
+struct NobagWs {
+  void* bag_offsets;  // [N + 1] of the index type
+  int32_t* b_t_map;   // [N]
+  int64_t* row_out;   // [N]
+  int32_t* B_offsets; // [T + 1]
+  int32_t* D_offsets; // [T + 1]
+  int32_t* infos;     // [N] (transpose: the sorted b_t words)
+  size_t bytes;
+};
+
+NobagWs carve_nobag(uint8_t* base, size_t off, int64_t N, int32_t T, int32_t index_bytes) {
+  NobagWs w{};
+  auto take = [&](size_t bytes) {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  const int64_t n = N > 0 ? N : 1;
+  w.bag_offsets = take(static_cast<size_t>(n + 1) * static_cast<size_t>(index_bytes));
+  w.b_t_map = reinterpret_cast<int32_t*>(take(n * 4));
+  w.row_out = reinterpret_cast<int64_t*>(take(n * 8));
+  w.B_offsets = reinterpret_cast<int32_t*>(take(static_cast<size_t>(T + 1) * 4));
+  w.D_offsets = reinterpret_cast<int32_t*>(take(static_cast<size_t>(T + 1) * 4));
+  w.infos = reinterpret_cast<int32_t*>(take(n * 4));
+  w.bytes = off;
+  return w;
+}
+
+int launch_nobag_layout(const void* offsets, int32_t index_bytes, int32_t T, int64_t B,
+                        int64_t N, int32_t D, int32_t nb, const NobagWs& w, bool backward,
+                        hipStream_t s) {
+  const int64_t want = ceil_div(N, 256);
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
+  const dim3 gd(static_cast<uint32_t>(want < 1 ? 1 : (want < cap ? want : cap)));
+  if (index_bytes == 8)
+    nobag_layout_kernel<int64_t><<<gd, 256, 0, s>>>(
+        static_cast<const int64_t*>(offsets), T, B, N, D, nb,
+        static_cast<int64_t*>(w.bag_offsets), w.b_t_map, backward ? w.row_out : nullptr,
+        backward ? w.B_offsets : nullptr, backward ? w.D_offsets : nullptr);
+  else
+    nobag_layout_kernel<int32_t><<<gd, 256, 0, s>>>(
+        static_cast<const int32_t*>(offsets), T, B, N, D, nb,
+        static_cast<int32_t*>(w.bag_offsets), w.b_t_map, backward ? w.row_out : nullptr,
+        backward ? w.B_offsets : nullptr, backward ? w.D_offsets : nullptr);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+int check_nobag(int32_t T, int64_t B, int32_t D, int32_t index_bytes, int64_t N) {
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative T, B or N");
+  MX_REQUIRE(D > 0 && D <= 1024 && D % 4 == 0, "D %d must be a multiple of 4 in [4, 1024]", D);
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(N < 0x7fffffffll, "N %lld too large for int32 positions", (long long)N);
+  MX_REQUIRE(N == 0 || (T > 0 && B > 0), "%lld indices but no bags (T=%d, B=%lld)",
+             (long long)N, T, (long long)B);
+  return MX_OK;
+}
+
+}  // namespace
+}  // namespace mx
+
+extern "C" size_t mx_tbe_backward_nobag_workspace_bytes(int64_t N, int32_t T,
+                                                        int32_t total_hash_size_bits, int32_t D) {
+  (void)total_hash_size_bits;
+  const size_t base = carve_bwd(nullptr, N, D > 0 ? D : 1).bytes;
+  return carve_nobag(nullptr, base, N, T > 0 ? T : 0, 8).bytes;
+}
+
+extern "C" int mx_tbe_backward_rowwise_adagrad_nobag(
+    void* weights, int32_t weights_ty, const int64_t* weights_offsets, int32_t T, int64_t B,
+    int32_t D, const int64_t* hash_size_cumsum, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    const float* grad_output, float* momentum1, const int64_t* momentum1_offsets,
+    float learning_rate, float eps, float weight_decay, int32_t weight_decay_mode,
+    int32_t stochastic_rounding, const mx_rng_state* rng, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_nobag(T, B, D, index_bytes, N)) return rc;
+  if (N == 0) return MX_OK;
+  MX_REQUIRE(offsets && workspace, "null pointer argument");
+  const int32_t nb = mx_tbe_info_B_num_bits(T, N);
+  MX_REQUIRE(nb > 0, "T=%d and N=%lld do not fit a 32-bit info word", T, (long long)N);
+  const size_t base = carve_bwd(nullptr, N, D).bytes;
+  const NobagWs nw = carve_nobag(static_cast<uint8_t*>(workspace), base, N, T, index_bytes);
+  if (workspace_bytes < nw.bytes)
+    return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", nw.bytes);
+  auto* s = as_stream(stream);
+  if (int rc = launch_nobag_layout(offsets, index_bytes, T, B, N, D, nb, nw, true, s)) return rc;
+  const Layout lay{N, nw.B_offsets, nw.row_out, nw.b_t_map};
+  return backward_impl(weights, weights_ty, weights_offsets, nw.D_offsets, T, N, nb, lay, D,
+                       hash_size_cumsum, total_hash_size_bits, indices, nw.bag_offsets,
+                       index_bytes, N, MX_POOL_SUM, nullptr, grad_output, 0, momentum1,
+                       momentum1_offsets, learning_rate, eps, weight_decay, weight_decay_mode,
+                       stochastic_rounding, rng, workspace, base, stream);
+}
+
+extern "C" size_t mx_tbe_transpose_nobag_workspace_bytes(int64_t N, int32_t T,
+                                                         int32_t total_hash_size_bits) {
+  (void)total_hash_size_bits;
+  return carve_nobag(nullptr, carve_sort(nullptr, N).bytes, N, T > 0 ? T : 0, 8).bytes;
+}
+
+extern "C" int mx_tbe_transpose_embedding_input_nobag(
+    const int64_t* hash_size_cumsum, int32_t T, int64_t B, int32_t total_hash_size_bits,
+    const void* indices, const void* offsets, int32_t index_bytes, int64_t N,
+    int64_t* linear_indices, int64_t* sorted_linear_indices, int64_t* infos_sorted,
+    int64_t* sorted_linear_indices_run, int32_t* run_lengths, int32_t* num_runs,
+    int32_t* cumulative_run_lengths, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative T, B or N");
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(N < 0x7fffffffll, "N %lld too large for int32 positions", (long long)N);
+  const Layout empty{0, nullptr, nullptr, nullptr};
+  if (N == 0)
+    return transpose_impl(hash_size_cumsum, T, 0, empty, total_hash_size_bits, 26, indices,
+                          offsets, index_bytes, 0, linear_indices, sorted_linear_indices,
+                          nullptr, sorted_linear_indices_run, run_lengths, num_runs,
+                          cumulative_run_lengths, workspace, workspace_bytes, stream);
+  MX_REQUIRE(T > 0 && B > 0, "%lld indices but no bags (T=%d, B=%lld)", (long long)N, T,
+             (long long)B);
+  MX_REQUIRE(offsets && infos_sorted && workspace, "null pointer argument");
+  const int32_t nb = mx_tbe_info_B_num_bits(T, N);
+  MX_REQUIRE(nb > 0, "T=%d and N=%lld do not fit a 32-bit info word", T, (long long)N);
+  const size_t base = carve_sort(nullptr, N).bytes;
+  const NobagWs nw = carve_nobag(static_cast<uint8_t*>(workspace), base, N, T, index_bytes);
+  if (workspace_bytes < nw.bytes)
+    return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", nw.bytes);
+  auto* s = as_stream(stream);
+  if (int rc = launch_nobag_layout(offsets, index_bytes, T, B, N, 4, nb, nw, false, s)) return rc;
+  const Layout lay{N, nullptr, nullptr, nw.b_t_map};
+  if (int rc = transpose_impl(hash_size_cumsum, T, 0, lay, total_hash_size_bits, nb, indices,
+                              nw.bag_offsets, index_bytes, N, linear_indices,
+                              sorted_linear_indices, nw.infos, sorted_linear_indices_run,
+                              run_lengths, num_runs, cumulative_run_lengths, workspace, base,
+                              stream))
+    return rc;
+  const int64_t want = ceil_div(N, 256);
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
+  const dim3 gd(static_cast<uint32_t>(want < cap ? want : cap));
+  if (index_bytes == 8)
+    nobag_infos_kernel<int64_t><<<gd, 256, 0, s>>>(nw.infos, static_cast<const int64_t*>(offsets),
+                                                   T, B, N, nb, infos_sorted);
+  else
+    nobag_infos_kernel<int32_t><<<gd, 256, 0, s>>>(nw.infos, static_cast<const int32_t*>(offsets),
+                                                   T, B, N, nb, infos_sorted);
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}

@@ -441,6 +441,130 @@ int dispatch_fwd(hipStream_t s, int32_t max_D, const WT* W, const int64_t* w_off
   return MX_OK;
 }
 
+// ---- sequence lookups (PoolingMode NONE) -----------------------------------
+//
+// Semantics: fbgemm_gpu split_embedding_nobag_codegen_forward_unweighted_cuda
+// (recalled): every table has the same D and position l of bag (t, b) writes
+// its own row, out[l, :] = W_t[indices[l], :] (fp16 rows widened to fp32).
+// Positions outside every bag (before offsets[0] or from offsets[T*B] on) are
+// written as zeros.
+//
+// Design: a gather over positions, not bags, so no wave waits on a long bag.
+// G lanes per position, lane k one float4 chunk per row; a group takes G
+// consecutive positions at a time (one coalesced index load), each lane finds
+// its own position's table by a binary search over the tables' first
+// positions offsets[t*B] staged in LDS, and the group then copies U rows at a
+// time (all U loads before the first store).  Blocks are remapped so that each
+// XCD copies a contiguous range of positions (t-major, so mostly its own
+// tables' hot rows).
+constexpr int kNobagMaxT = 1024;  // tables whose first positions fit LDS; more: searched in memory
+
+template <typename I>
+__device__ __forceinline__ int32_t nobag_table(const int64_t* s_pos, bool lds, const I* offsets,
+                                               int64_t B, int32_t T, int64_t l) {
+  int32_t lo = 0, hi = T;  // pos[lo] <= l < pos[hi]
+  while (hi - lo > 1) {
+    const int32_t mid = lo + ((hi - lo) >> 1);
+    const int64_t pm = lds ? s_pos[mid] : static_cast<int64_t>(offsets[mid * B]);
+    if (pm <= l)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+template <typename I, typename WT, int G, int NCH, int U, bool OUT_F16>
+__global__ void __launch_bounds__(256)
+    tbe_fwd_nobag_kernel(const WT* __restrict__ W, const int64_t* __restrict__ w_off,
+                         const I* __restrict__ indices, const I* __restrict__ offsets, int32_t T,
+                         int64_t B, int32_t D, int64_t N, void* __restrict__ out) {
+  __shared__ int64_t s_pos[kNobagMaxT + 1];
+  const bool lds = T <= kNobagMaxT;
+  if (lds)
+    for (int t = threadIdx.x; t <= T; t += 256) s_pos[t] = static_cast<int64_t>(offsets[t * B]);
+  __syncthreads();
+  const int64_t p0 = lds ? s_pos[0] : static_cast<int64_t>(offsets[0]);
+  const int64_t p1 = lds ? s_pos[T] : static_cast<int64_t>(offsets[static_cast<int64_t>(T) * B]);
+  constexpr int NG = 256 / G;  // groups per block
+  const int lane = threadIdx.x & 63;
+  const int g = lane / G, k = lane % G;
+  const int64_t lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * NG * G;
+  for (int64_t base = (lb * NG + threadIdx.x / G) * G; base < N; base += step) {
+    const int64_t l = base + k;
+    int64_t my_row = -1;  // element offset of position l's row; -1: zeros
+    if (l < N && l >= p0 && l < p1) {
+      const int32_t t = nobag_table(s_pos, lds, offsets, B, T, l);
+      my_row = w_off[t] + static_cast<int64_t>(indices[l]) * D;
+    }
+    const int n = static_cast<int>(N - base < G ? N - base : G);
+    for (int j = 0; j < n; j += U) {
+      float v[U][NCH][4];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = j + u < n ? j + u : n - 1;
+        const int64_t off = __shfl(my_row, g * G + r, 64);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int col = (c * G + k) * 4;
+          if (col < D && off >= 0)
+            load_row4(W + off + col, v[u][c]);
+          else
+            v[u][c][0] = v[u][c][1] = v[u][c][2] = v[u][c][3] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j + u >= n) continue;
+        const int64_t o = (base + j + u) * D;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int col = (c * G + k) * 4;
+          if (col >= D) continue;
+          if constexpr (OUT_F16) {
+            __half2 h[2] = {__floats2half2_rn(v[u][c][0], v[u][c][1]),
+                            __floats2half2_rn(v[u][c][2], v[u][c][3])};
+            *reinterpret_cast<uint2*>(static_cast<__half*>(out) + o + col) =
+                *reinterpret_cast<const uint2*>(h);
+          } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + o + col) =
+                make_float4(v[u][c][0], v[u][c][1], v[u][c][2], v[u][c][3]);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename I, typename WT, int G, int NCH, bool OUT_F16>
+void launch_nobag(hipStream_t s, const WT* W, const int64_t* w_off, const void* idx,
+                  const void* off, int32_t T, int64_t B, int32_t D, int64_t N, void* out) {
+  constexpr int U = NCH <= 1 ? 8 : (NCH <= 2 ? 4 : 2);
+  const int64_t want = ceil_div(N, 256);  // 256 positions per block and round
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
+  const int64_t grid = want < cap ? want : cap;
+  tbe_fwd_nobag_kernel<I, WT, G, NCH, U, OUT_F16><<<dim3(static_cast<uint32_t>(grid)), 256, 0, s>>>(
+      W, w_off, static_cast<const I*>(idx), static_cast<const I*>(off), T, B, D, N, out);
+}
+
+template <typename I, typename WT, bool OUT_F16>
+void dispatch_nobag(hipStream_t s, const WT* W, const int64_t* w_off, const void* idx,
+                    const void* off, int32_t T, int64_t B, int32_t D, int64_t N, void* out) {
+#define MX_NOBAG_G(G, NCH) launch_nobag<I, WT, G, NCH, OUT_F16>(s, W, w_off, idx, off, T, B, D, N, out)
+  if (D <= 64)
+    MX_NOBAG_G(16, 1);
+  else if (D <= 128)
+    MX_NOBAG_G(32, 1);
+  else if (D <= 256)
+    MX_NOBAG_G(64, 1);
+  else if (D <= 512)
+    MX_NOBAG_G(64, 2);
+  else
+    MX_NOBAG_G(64, 4);
+#undef MX_NOBAG_G
+}
+
 }  // namespace
 }  // namespace mx
 
@@ -528,6 +652,47 @@ extern "C" int mx_tbe_forward_vbe(const void* weights, int32_t weights_ty,
   return tbe_forward_impl(weights, weights_ty, weights_offsets, D_offsets, T, total_B, max_D,
                           indices, offsets, index_bytes, pooling_mode, indice_weights, out,
                           out_dtype, bm, true, stream);
+}
+
+extern "C" int mx_tbe_forward_nobag(const void* weights, int32_t weights_ty,
+                                    const int64_t* weights_offsets, int32_t T, int64_t B,
+                                    int32_t D, const void* indices, const void* offsets,
+                                    int32_t index_bytes, int64_t N, void* out, int32_t out_dtype,
+                                    void* stream) {
+  clear_error();
+  MX_REQUIRE(T >= 0 && B >= 0 && N >= 0, "negative T, B or N");
+  MX_REQUIRE(D > 0 && D <= 1024 && D % 4 == 0, "D %d must be a multiple of 4 in [4, 1024]", D);
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
+  MX_REQUIRE(out_dtype == MX_SPARSE_FP32 || out_dtype == MX_SPARSE_FP16,
+             "output_dtype %d not supported (FP32=0, FP16=1)", out_dtype);
+  MX_REQUIRE(weights_ty == MX_SPARSE_FP32 || weights_ty == MX_SPARSE_FP16,
+             "weights type %d not supported (FP32=0, FP16=1)", weights_ty);
+  if (N == 0) return MX_OK;
+  MX_REQUIRE(T > 0 && B > 0, "%lld indices but no bags (T=%d, B=%lld)", (long long)N, T,
+             (long long)B);
+  MX_REQUIRE(weights && weights_offsets && indices && offsets && out, "null pointer argument");
+  auto* s = as_stream(stream);
+  const bool h = out_dtype == MX_SPARSE_FP16;
+#define MX_NB(I, WT)                                                                          \
+  (h ? dispatch_nobag<I, WT, true>(s, static_cast<const WT*>(weights), weights_offsets,       \
+                                   indices, offsets, T, B, D, N, out)                          \
+     : dispatch_nobag<I, WT, false>(s, static_cast<const WT*>(weights), weights_offsets,      \
+                                    indices, offsets, T, B, D, N, out))
+  const bool w16 = weights_ty == MX_SPARSE_FP16;
+  if (index_bytes == 8) {
+    if (w16)
+      MX_NB(int64_t, __half);
+    else
+      MX_NB(int64_t, float);
+  } else {
+    if (w16)
+      MX_NB(int32_t, __half);
+    else
+      MX_NB(int32_t, float);
+  }
+#undef MX_NB
+  MX_LAUNCH_CHECK();
+  return MX_OK;
 }
 
 namespace {

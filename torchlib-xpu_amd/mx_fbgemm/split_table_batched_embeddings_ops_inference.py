@@ -80,7 +80,9 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
     ``embedding_specs`` holds ``(name, num_embeddings, embedding_dim,
     weight_ty, location)`` per table; only EmbeddingLocation.DEVICE is
     supported.  ``feature_table_map`` ([T] table index per feature, default
-    one feature per table) lets several features look up one table."""
+    one feature per table) lets several features look up one table.
+    PoolingMode.NONE (sequence lookups) needs every table of one width D and
+    returns ``[N, D]``, row l the dequantized row of index l."""
 
     def __init__(
         self,
@@ -95,8 +97,10 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
         fp8_exponent_bias: Optional[int] = None,
     ) -> None:
         super().__init__()
-        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
+        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN, PoolingMode.NONE):
             raise ValueError(f"pooling_mode {pooling_mode} is not supported")
+        if pooling_mode == PoolingMode.NONE and len({D for _, _, D, _, _ in embedding_specs}) > 1:
+            raise ValueError("PoolingMode.NONE needs every table of one embedding_dim")
         if output_dtype not in (SparseType.FP16, SparseType.FP32, SparseType.BF16):
             raise ValueError("output_dtype must be FP16, FP32 or BF16")
         for _, E, D, ty, loc in embedding_specs:
@@ -178,6 +182,8 @@ class IntNBitTableBatchedEmbeddingBagsCodegen(nn.Module):
                 per_sample_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
         if (offsets.numel() - 1) % self.T:
             raise ValueError(f"offsets must have T*B+1 entries (T={self.T})")
+        if self.pooling_mode == PoolingMode.NONE and per_sample_weights is not None:
+            raise ValueError("PoolingMode.NONE takes no per_sample_weights")
         if indices.dtype != offsets.dtype:
             offsets = offsets.to(indices.dtype)
         if self.bounds_check_mode != BoundsCheckMode.NONE:

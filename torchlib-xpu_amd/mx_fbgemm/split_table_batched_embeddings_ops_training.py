@@ -60,6 +60,10 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
     sum_t sum_r B[t][r] + 1 entries (feature-major, rank-major within a
     feature), and the output is one flat tensor, rank-major then
     feature-major, holding B[t][r] rows of D_t per (rank, feature).
+
+    PoolingMode.NONE (sequence lookups) needs every feature of one width D:
+    ``forward`` returns ``[N, D]``, row l the row of index l, and the fused
+    update sums each row's gradient rows (no per-sample weights, no VBE).
     """
 
     def __init__(
@@ -82,7 +86,7 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         super().__init__()
         if optimizer != EmbOptimType.EXACT_ROWWISE_ADAGRAD:
             raise ValueError(f"optimizer {optimizer} is not supported")
-        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN):
+        if pooling_mode not in (PoolingMode.SUM, PoolingMode.MEAN, PoolingMode.NONE):
             raise ValueError(f"pooling_mode {pooling_mode} is not supported")
         if output_dtype != SparseType.FP32:
             raise ValueError("the training lookup produces fp32 output")
@@ -121,6 +125,8 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
         self.T = len(ftm)
         f_rows = [rows[t] for t in ftm]
         f_dims = [dims[t] for t in ftm]
+        if pooling_mode == PoolingMode.NONE and len(set(f_dims)) > 1:
+            raise ValueError("PoolingMode.NONE needs every feature of one embedding_dim")
         self.total_D = sum(f_dims)
         self.max_D = max(f_dims)
         table_hash = _cumsum(rows)
@@ -196,6 +202,9 @@ class SplitTableBatchedEmbeddingBagsCodegen(nn.Module):
                 raise ValueError("per_sample_weights must be fp32")
             if per_sample_weights.numel() != indices.numel():
                 raise ValueError("per_sample_weights must have one entry per index")
+        if self.pooling_mode == PoolingMode.NONE and (
+                per_sample_weights is not None or batch_size_per_feature_per_rank is not None):
+            raise ValueError("PoolingMode.NONE takes no per_sample_weights and no VBE batch")
         vbe = (self._vbe_args(batch_size_per_feature_per_rank, indices.device)
                if batch_size_per_feature_per_rank is not None else None)
         if vbe is not None:
