@@ -382,8 +382,13 @@ __device__ void bag_fast(const NbitArgs& a, const uint8_t* __restrict__ Wt, int6
   const int64_t col = out_col + static_cast<int64_t>(k) * CPC;
   if (a.out_kind != 0) {
     uint16_t h[CPL];
+    if (a.out_kind == 1) {  // the conversion loops apart, so each stays straight-line
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) h[e] = out16(res[e], a.out_kind);
+      for (int e = 0; e < CPL; ++e) h[e] = __half_as_ushort(__float2half_rn(res[e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) h[e] = out16(res[e], 2);
+    }
 #pragma unroll
     for (int q = 0; q < NCHK; ++q) {
       uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + col + q * G * CPC;
