@@ -87,7 +87,8 @@ extern "C" {
  * accepted.  0.5.0: the PoolingMode NONE (sequence) entry points added:
  * mx_tbe_forward_nobag, mx_tbe_backward_rowwise_adagrad_nobag,
  * mx_tbe_transpose_embedding_input_nobag, mx_nbit_forward_nobag and their
- * workspace queries (all earlier ones unchanged). */
+ * workspace queries, and mx_cumsum, mx_permute_2d_lengths, mx_permute_2d_data
+ * with mx_cumsum_workspace_bytes (all earlier ones unchanged). */
 #define MX_FBGEMM_VERSION 500
 int mx_version(void);
 
@@ -470,6 +471,37 @@ int mx_float_to_hfp8(const float* in, int64_t n, int32_t ebits, int32_t exponent
                      float max_pos, uint8_t* out, void* stream);
 int mx_hfp8_to_float(const uint8_t* in, int64_t n, int32_t ebits, int32_t exponent_bias,
                      float* out, void* stream);
+
+/* ---- sparse-feature helpers ------------------------------------------------ */
+
+/* Workspace needed by mx_cumsum over n elements of elem_bytes (4 or 8). */
+size_t mx_cumsum_workspace_bytes(int64_t n, int32_t elem_bytes);
+
+/* Serves fbgemm::asynchronous_exclusive_cumsum (kind 0), asynchronous_
+ * inclusive_cumsum (1) and asynchronous_complete_cumsum (2: n + 1 outputs,
+ * out[0] = 0; with rows > 1, x is [rows, n] and each row gets its own n + 1).
+ * int32 or int64 (elem_bytes 4 or 8) in and out, two's complement
+ * wrap-around; exact.  rows > 1 needs kind 2 and no workspace. */
+int mx_cumsum(const void* in, int32_t elem_bytes, int64_t rows, int64_t n, int32_t kind,
+              void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* fbgemm::permute_2D_sparse_data, step 1: permuted_lengths [T_out, B] with
+ * row f = lengths row permute[f] (int32 permute; a feature outside [0, T)
+ * gets zero lengths).  lengths int32 or int64 (length_bytes). */
+int mx_permute_2d_lengths(const int32_t* permute, int64_t T_out, const void* lengths,
+                          int32_t length_bytes, int32_t T, int64_t B, void* permuted_lengths,
+                          void* stream);
+
+/* fbgemm::permute_2D_sparse_data, step 2: bag (f, b) of the output, at
+ * output_offsets[f*B + b] (the complete cumsum of the permuted lengths), is a
+ * copy of the input bag (permute[f], b) at input_offsets[permute[f]*B + b]
+ * (the complete cumsum of the lengths); weights (fp32, may be NULL) travel
+ * with their indices.  out_len = output_offsets[T_out*B]. */
+int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t T, int64_t B,
+                       const void* input_offsets, const void* output_offsets,
+                       int32_t offset_bytes, const void* indices, int32_t index_bytes,
+                       const float* weights, int64_t out_len, void* permuted_indices,
+                       float* permuted_weights, void* stream);
 
 /* ---- TBE nbit inference forward ---------------------------------------- */
 

@@ -281,6 +281,47 @@ def nbit_forward_nobag(W, w_off, tys, D: int, B: int, indices, offsets, row_alig
     return out
 
 
+def cumsum(x, kind: int) -> np.ndarray:
+    """asynchronous_{exclusive,inclusive,complete}_cumsum (kind 0/1/2) in the
+    input's integer type, wrapping as its adds do; a 2-D input (complete only)
+    per row."""
+    x = np.asarray(x)
+    assert x.dtype in (np.int32, np.int64)
+    inc = np.cumsum(x, axis=-1, dtype=x.dtype)
+    zero = np.zeros(x.shape[:-1] + (1,), x.dtype)
+    if kind == 1:
+        return inc
+    if kind == 0:
+        return np.concatenate([zero, inc[..., :-1]], axis=-1)[..., :x.shape[-1]]
+    return np.concatenate([zero, inc], axis=-1)
+
+
+def permute_2d_sparse_data(permute, lengths, indices, weights=None):
+    """permute_2D_sparse_data: output feature f is input feature permute[f]
+    (lengths [T, B]); returns (permuted_lengths, permuted_indices,
+    permuted_weights or None)."""
+    permute = np.asarray(permute, np.int64)
+    lengths = np.asarray(lengths)
+    T, B = lengths.shape
+    off = np.concatenate([[0], np.cumsum(lengths.reshape(-1), dtype=np.int64)])
+    plen = np.zeros((permute.shape[0], B), lengths.dtype)
+    segs_i, segs_w = [], []
+    for f, src in enumerate(permute):
+        if not 0 <= src < T:
+            continue
+        plen[f] = lengths[src]
+        for b in range(B):
+            s, e = off[src * B + b], off[src * B + b + 1]
+            segs_i.append(indices[s:e])
+            if weights is not None:
+                segs_w.append(weights[s:e])
+    cat_i = np.concatenate(segs_i) if segs_i else np.zeros(0, np.asarray(indices).dtype)
+    cat_w = None
+    if weights is not None:
+        cat_w = np.concatenate(segs_w) if segs_w else np.zeros(0, np.float32)
+    return plen, cat_i, cat_w
+
+
 def hfp8_to_float(codes, ebits: int, ebias: int) -> np.ndarray:
     """Decodes hfp8 codes (uint8) to fp32 (the C restatement)."""
     f = lib().orc_hfp8_to_float

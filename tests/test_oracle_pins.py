@@ -680,3 +680,52 @@ def test_transpose_nobag_vs_pooled_transpose():
     np.testing.assert_array_equal(t, b["infos_sorted"] >> nb)
     np.testing.assert_array_equal(bag - t * inp.B, b["infos_sorted"] & ((1 << nb) - 1))
     np.testing.assert_array_equal(a["linear_indices"], b["linear_indices"])
+
+
+# ---- sparse-feature helpers ----------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_cumsum_vs_python_loop(dtype, kind):
+    """A running sum in Python integers, reduced to the type's two's complement,
+    on values that wrap the int32 range."""
+    rng = np.random.default_rng(kind)
+    big = np.iinfo(dtype).max // 3
+    for x in (np.zeros(0, dtype), np.array([5], dtype), rng.integers(-100, 100, 37).astype(dtype),
+              np.array([big, big, big, big, -7, big], dtype)):
+        bits = np.dtype(dtype).itemsize * 8
+        acc, inc = 0, []
+        for v in x.tolist():
+            acc = (acc + v + (1 << (bits - 1))) % (1 << bits) - (1 << (bits - 1))
+            inc.append(acc)
+        exp = {1: inc, 0: [0] + inc[:-1] if inc else [], 2: [0] + inc}[kind]
+        np.testing.assert_array_equal(orc.cumsum(x, kind), np.array(exp, dtype))
+    m = rng.integers(0, 9, (4, 6)).astype(dtype)
+    if kind == 2:  # 2-D: per row
+        np.testing.assert_array_equal(orc.cumsum(m, 2), np.stack([orc.cumsum(r, 2) for r in m]))
+
+
+def test_permute_2d_sparse_data_vs_bag_lists():
+    """Against lists of bags: output bag (f, b) is input bag (permute[f], b);
+    repeats and a feature outside the range (zero lengths) included."""
+    rng = np.random.default_rng(3)
+    T, B = 4, 5
+    lengths = rng.integers(0, 4, (T, B)).astype(np.int64)
+    n = int(lengths.sum())
+    idx = rng.integers(0, 1000, n).astype(np.int64)
+    w = rng.standard_normal(n).astype(np.float32)
+    bags, p = [], 0
+    for t in range(T):
+        row = []
+        for b in range(B):
+            row.append((idx[p:p + lengths[t, b]], w[p:p + lengths[t, b]]))
+            p += lengths[t, b]
+        bags.append(row)
+    permute = [2, 0, 2, 3, 9]
+    pl, pi, pw = orc.permute_2d_sparse_data(permute, lengths, idx, w)
+    exp_i = [bags[s][b][0] for s in permute if s < T for b in range(B)]
+    exp_w = [bags[s][b][1] for s in permute if s < T for b in range(B)]
+    np.testing.assert_array_equal(pi, np.concatenate(exp_i))
+    np.testing.assert_array_equal(pw, np.concatenate(exp_w))
+    np.testing.assert_array_equal(pl[:4], lengths[[2, 0, 2, 3]])
+    assert np.all(pl[4] == 0)

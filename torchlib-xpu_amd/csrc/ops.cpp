@@ -1679,9 +1679,86 @@ Tensor int_nbit_lookup(const Tensor& dev_weights, const Tensor& uvm_weights,
   return out;
 }
 
+// ---------------------------------------------------------------------------
+// Sparse-feature helpers: cumsums and permute_2D_sparse_data
+// ---------------------------------------------------------------------------
+
+// kind 0 exclusive, 1 inclusive, 2 complete.
+Tensor cumsum_impl(const Tensor& t_in, int32_t kind) {
+  check_gpu(t_in, "t_in");
+  c10::OptionalDeviceGuard guard(t_in.device());
+  TORCH_CHECK(t_in.scalar_type() == at::kInt || t_in.scalar_type() == at::kLong,
+              "cumsum input must be int32 or int64, got ", t_in.scalar_type());
+  TORCH_CHECK(t_in.dim() == 1 || (kind == 2 && t_in.dim() == 2),
+              kind == 2 ? "complete cumsum input must be 1-D or 2-D" : "cumsum input must be 1-D");
+  const Tensor x = t_in.contiguous();
+  const int32_t eb = static_cast<int32_t>(x.element_size());
+  const int64_t rows = x.dim() == 2 ? x.size(0) : 1;
+  const int64_t n = x.dim() == 2 ? x.size(1) : x.numel();
+  Tensor out = x.dim() == 2 ? at::empty({rows, n + 1}, x.options())
+                            : at::empty({kind == 2 ? n + 1 : n}, x.options());
+  if (rows == 0) return out;
+  const size_t ws_bytes = rows == 1 ? mx_cumsum_workspace_bytes(n, eb) : 0;
+  Tensor ws = at::empty({static_cast<int64_t>(ws_bytes)}, x.options().dtype(at::kByte));
+  MX_CALL(mx_cumsum(x.data_ptr(), eb, rows, n, kind, out.data_ptr(), ws.data_ptr(), ws_bytes,
+                    stream_of(x)));
+  return out;
+}
+
+Tensor exclusive_cumsum(const Tensor& t_in) { return cumsum_impl(t_in, 0); }
+Tensor inclusive_cumsum(const Tensor& t_in) { return cumsum_impl(t_in, 1); }
+Tensor complete_cumsum(const Tensor& t_in) { return cumsum_impl(t_in, 2); }
+
+std::tuple<Tensor, Tensor, std::optional<Tensor>> permute_2D_sparse_data(
+    const Tensor& permute, const Tensor& lengths, const Tensor& indices,
+    const std::optional<Tensor>& weights, std::optional<c10::SymInt> permuted_lengths_sum) {
+  check_gpu(lengths, "lengths");
+  c10::OptionalDeviceGuard guard(lengths.device());
+  check_arg(permute, lengths, "permute", true);
+  check_arg(indices, lengths, "indices", false);
+  TORCH_CHECK(permute.scalar_type() == at::kInt && permute.dim() == 1, "permute must be 1-D int32");
+  TORCH_CHECK(lengths.dim() == 2, "lengths must be [T, B]");
+  TORCH_CHECK(lengths.scalar_type() == at::kInt || lengths.scalar_type() == at::kLong,
+              "lengths must be int32 or int64");
+  const int32_t ib = index_bytes_of(indices, "indices");
+  const int64_t T = lengths.size(0), B = lengths.size(1), Tp = permute.numel();
+  TORCH_CHECK(T <= 0x7fffffffll, "too many features");
+  const Tensor perm = permute.contiguous(), len = lengths.contiguous(), idx = indices.contiguous();
+  const int32_t lb = static_cast<int32_t>(len.element_size());
+  Tensor plen = at::empty({Tp, B}, len.options());
+  MX_CALL(mx_permute_2d_lengths(perm.data_ptr<int32_t>(), Tp, len.data_ptr(), lb,
+                                static_cast<int32_t>(T), B, plen.data_ptr(), stream_of(len)));
+  const Tensor in_off = cumsum_impl(len.view({-1}), 2);
+  const Tensor out_off = cumsum_impl(plen.view({-1}), 2);
+  const int64_t out_len = permuted_lengths_sum.has_value()
+                              ? permuted_lengths_sum->expect_int()
+                              : out_off[Tp * B].item<int64_t>();  // one host sync, as upstream
+  Tensor pidx = at::empty({out_len}, idx.options());
+  std::optional<Tensor> pw;
+  Tensor wc;
+  if (weights.has_value() && weights->defined()) {
+    check_arg(*weights, lengths, "weights", false);
+    TORCH_CHECK(weights->scalar_type() == at::kFloat && weights->numel() == indices.numel(),
+                "weights must be fp32 with one entry per index");
+    wc = weights->contiguous();
+    pw = at::empty({out_len}, wc.options());
+  }
+  MX_CALL(mx_permute_2d_data(perm.data_ptr<int32_t>(), Tp, static_cast<int32_t>(T), B,
+                             in_off.data_ptr(), out_off.data_ptr(), lb, idx.data_ptr(), ib,
+                             wc.defined() ? wc.data_ptr<float>() : nullptr, out_len,
+                             pidx.data_ptr(), pw.has_value() ? pw->data_ptr<float>() : nullptr,
+                             stream_of(len)));
+  return {plen, pidx, pw};
+}
+
 }  // namespace mx_ops
 
 TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
+  m.def("asynchronous_exclusive_cumsum(Tensor t_in) -> Tensor");
+  m.def("asynchronous_inclusive_cumsum(Tensor t_in) -> Tensor");
+  m.def("asynchronous_complete_cumsum(Tensor t_in) -> Tensor");
+  m.def("permute_2D_sparse_data(Tensor permute, Tensor lengths, Tensor values, "
+        "Tensor? weights=None, SymInt? permuted_lengths_sum=None) -> (Tensor, Tensor, Tensor?)");
   m.def("jagged_to_padded_dense_forward(Tensor values, Tensor[] offsets, SymInt[] max_lengths, "
         "float padding_value=0) -> Tensor");
   m.def("jagged_to_padded_dense(Tensor values, Tensor[] offsets, SymInt[] max_lengths, "
@@ -1864,6 +1941,10 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
          TORCH_FN(mx_ops::grad_indice_weights_vbe));
   m.impl("int_nbit_split_embedding_codegen_lookup_function", TORCH_FN(mx_ops::int_nbit_lookup));
   m.impl("bounds_check_indices", TORCH_FN(mx_ops::bounds_check_indices));
+  m.impl("asynchronous_exclusive_cumsum", TORCH_FN(mx_ops::exclusive_cumsum));
+  m.impl("asynchronous_inclusive_cumsum", TORCH_FN(mx_ops::inclusive_cumsum));
+  m.impl("asynchronous_complete_cumsum", TORCH_FN(mx_ops::complete_cumsum));
+  m.impl("permute_2D_sparse_data", TORCH_FN(mx_ops::permute_2D_sparse_data));
   m.impl("FloatToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_to_8bit));
   m.impl("HalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::half_to_8bit));
   m.impl("FloatOrHalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_or_half_to_8bit));

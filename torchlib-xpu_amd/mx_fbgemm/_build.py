@@ -31,7 +31,7 @@ KERNEL_LIB = LIB_DIR / "libmx_fbgemm_kernels.so"
 OPS_LIB = LIB_DIR / "mx_fbgemm_ops.so"
 
 HIP_SOURCES = ["abi.hip", "jagged.hip", "tbe_fwd.hip", "tbe_bwd.hip", "nbit_fwd.hip",
-               "bounds_check.hip", "codec.hip", "vbe.hip"]
+               "bounds_check.hip", "codec.hip", "vbe.hip", "sparse_ops.hip"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
