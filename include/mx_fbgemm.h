@@ -87,8 +87,9 @@ extern "C" {
  * accepted.  0.5.0: the PoolingMode NONE (sequence) entry points added:
  * mx_tbe_forward_nobag, mx_tbe_backward_rowwise_adagrad_nobag,
  * mx_tbe_transpose_embedding_input_nobag, mx_nbit_forward_nobag and their
- * workspace queries, and mx_cumsum, mx_permute_2d_lengths, mx_permute_2d_data
- * with mx_cumsum_workspace_bytes (all earlier ones unchanged). */
+ * workspace queries, mx_cumsum, mx_permute_2d_lengths, mx_permute_2d_data
+ * with mx_cumsum_workspace_bytes, and mx_jagged_dense_elementwise_mul (all
+ * earlier ones unchanged). */
 #define MX_FBGEMM_VERSION 500
 int mx_version(void);
 
@@ -170,6 +171,15 @@ int mx_dense_to_jagged(const void* dense, int64_t elem_bytes, int64_t inner,
  *   (f16/bf16 computed in fp32 and rounded to nearest even); where the
  *   coordinate lies outside y, out[i] = x[i] + 0. */
 int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense, int32_t dtype,
+                                    int64_t inner, int32_t num_jagged_dim,
+                                    const void* const* offsets, int32_t offset_bytes,
+                                    const int64_t* offsets_numel, const int64_t* max_lengths,
+                                    int64_t total_L, void* out, void* stream);
+
+/* Serves fbgemm::jagged_dense_elementwise_mul: out[i] = x[i] * y[coordinate(i)]
+ * in the element type's arithmetic (f16/bf16 computed in fp32 and rounded to
+ * nearest even); where the coordinate lies outside y, out[i] = x[i] * 0. */
+int mx_jagged_dense_elementwise_mul(const void* x_values, const void* y_dense, int32_t dtype,
                                     int64_t inner, int32_t num_jagged_dim,
                                     const void* const* offsets, int32_t offset_bytes,
                                     const int64_t* offsets_numel, const int64_t* max_lengths,

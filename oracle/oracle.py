@@ -220,6 +220,21 @@ def jagged_dense_elementwise_add(x: np.ndarray, offsets, y: np.ndarray, dtype: s
     del nd
 
 
+def jagged_dense_elementwise_mul(x: np.ndarray, offsets, y: np.ndarray, dtype: str):
+    """out[i] = x[i] * y[coord(i)] (x[i] * 0 outside y); f16/bf16 in fp32 (the
+    product of two such values is exact there), rounded once, RNE."""
+    yz = dense_to_jagged(y, offsets, total_L=x.shape[0])
+    if dtype == "f32":
+        return (x.astype(np.float32) * yz.astype(np.float32)).astype(np.float32)
+    if dtype == "f64":
+        return x.astype(np.float64) * yz.astype(np.float64)
+    if dtype == "f16":
+        return (x.astype(np.float32) * yz.astype(np.float32)).astype(np.float16)
+    if dtype == "bf16":
+        return _f32_to_bf16(_bf16_to_f32(x) * _bf16_to_f32(yz))
+    raise ValueError(dtype)
+
+
 # ---------------------------------------------------------------------------
 # TBE (C restatement)
 # ---------------------------------------------------------------------------

@@ -161,3 +161,94 @@ def test_jagged_to_padded_dense_backward_op(dev):
     got = torch.ops.fbgemm.jagged_to_padded_dense_backward(
         torch.from_numpy(g).to(dev), [torch.from_numpy(off).to(dev)], 11)
     _bits_equal(got, orc.dense_to_jagged(g, [off], total_L=11))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64", "f16", "bf16"])
+@pytest.mark.parametrize("lengths,max_L,D", CASES)
+def test_jagged_dense_mul(dev, dtype, lengths, max_L, D):
+    """x * y at the jagged coordinates (x * 0 past max_L), bit for bit."""
+    print(f"[case] mul {dtype} lengths={lengths} max_L={max_L} D={D}", flush=True)
+    rng = np.random.default_rng(13)
+    off = _offsets(lengths)
+    tdt = {"f32": torch.float32, "f64": torch.float64, "f16": torch.float16,
+           "bf16": torch.bfloat16}[dtype]
+    xt = torch.from_numpy(rng.standard_normal((int(off[-1]), D))).to(tdt)
+    yt = torch.from_numpy(rng.standard_normal((len(lengths), max_L, D))).to(tdt)
+    if dtype == "bf16":
+        xn, yn = xt.view(torch.int16).numpy().view(np.uint16), yt.view(torch.int16).numpy().view(np.uint16)
+    else:
+        xn, yn = xt.numpy(), yt.numpy()
+    exp = orc.jagged_dense_elementwise_mul(xn, [off], yn, dtype)
+    got = torch.ops.fbgemm.jagged_dense_elementwise_mul(xt.to(dev), [torch.from_numpy(off).to(dev)],
+                                                        yt.to(dev))
+    _bits_equal(got, exp)
+
+
+def test_jagged_dense_mul_two_dims_and_autograd(dev):
+    """Two jagged dims; d/dx = grad * y at the coordinates, d/dy = the padded
+    dense of grad * x, both against the oracle's gather / scatter, bit for bit."""
+    print("[case] mul two jagged dims + autograd", flush=True)
+    rng = np.random.default_rng(14)
+    off0 = _offsets([2, 0, 3])
+    off1 = _offsets([1, 4, 0, 2, 3])
+    offs = [torch.from_numpy(off0).to(dev), torch.from_numpy(off1).to(dev)]
+    x = rng.standard_normal((10, 3)).astype(np.float32)
+    y = rng.standard_normal((3, 2, 3, 3)).astype(np.float32)
+    xt = torch.from_numpy(x).to(dev).requires_grad_()
+    yt = torch.from_numpy(y).to(dev).requires_grad_()
+    out = torch.ops.fbgemm.jagged_dense_elementwise_mul(xt, offs, yt)
+    _bits_equal(out, orc.jagged_dense_elementwise_mul(x, [off0, off1], y, "f32"))
+    g = rng.standard_normal((10, 3)).astype(np.float32)
+    (out * torch.from_numpy(g).to(dev)).sum().backward()
+    _bits_equal(xt.grad, orc.jagged_dense_elementwise_mul(g, [off0, off1], y, "f32"))
+    _bits_equal(yt.grad, orc.jagged_to_padded_dense((g * x).astype(np.float32), [off0, off1],
+                                                    [2, 3], 0.0))
+
+
+@pytest.mark.parametrize("lengths,max_L,D", CASES)
+def test_jagged_2d_to_dense(dev, lengths, max_L, D):
+    print(f"[case] jagged_2d_to_dense lengths={lengths} max_L={max_L} D={D}", flush=True)
+    rng = np.random.default_rng(15)
+    off = _offsets(lengths)
+    v = rng.standard_normal((int(off[-1]), D)).astype(np.float32)
+    vt = torch.from_numpy(v).to(dev).requires_grad_()
+    got = torch.ops.fbgemm.jagged_2d_to_dense(vt, torch.from_numpy(off).to(dev), max_L)
+    _bits_equal(got, orc.jagged_to_padded_dense(v, [off], [max_L], 0.0))
+    g = rng.standard_normal(tuple(got.shape)).astype(np.float32)
+    (got * torch.from_numpy(g).to(dev)).sum().backward()
+    _bits_equal(vt.grad, orc.dense_to_jagged(g, [off], total_L=int(off[-1])))
+
+
+@pytest.mark.parametrize("dtype,pad", [(np.int64, -1), (np.int64, (1 << 62) + 3),
+                                       (np.int32, 7), (np.float32, -2)])
+def test_jagged_1d_to_dense(dev, dtype, pad):
+    """Integer padding keeps every bit of an int64 (2^62 + 3 is not a double)."""
+    print(f"[case] jagged_1d_to_dense {np.dtype(dtype).name} pad={pad}", flush=True)
+    rng = np.random.default_rng(16)
+    lengths = [3, 0, 6, 1, 2]
+    off = _offsets(lengths)
+    v = rng.integers(-1000, 1000, int(off[-1])).astype(dtype)
+    got = torch.ops.fbgemm.jagged_1d_to_dense(torch.from_numpy(v).to(dev),
+                                              torch.from_numpy(off).to(dev), 4, pad)
+    exp = np.full((len(lengths), 4), pad, dtype)
+    for b, n in enumerate(lengths):
+        k = min(n, 4)
+        exp[b, :k] = v[off[b]:off[b] + k]
+    _bits_equal(got, exp)
+
+
+def test_jagged_dense_add_autograd_two_dims(dev):
+    """The add's backward with two jagged dims: grad_x = grad, grad_y = the
+    padded dense of grad (the offsets list is one argument of the node)."""
+    print("[case] add autograd two jagged dims", flush=True)
+    rng = np.random.default_rng(17)
+    off0 = _offsets([2, 0, 3])
+    off1 = _offsets([1, 4, 0, 2, 3])
+    offs = [torch.from_numpy(off0).to(dev), torch.from_numpy(off1).to(dev)]
+    xt = torch.from_numpy(rng.standard_normal((10, 3)).astype(np.float32)).to(dev).requires_grad_()
+    yt = torch.from_numpy(rng.standard_normal((3, 2, 3, 3)).astype(np.float32)).to(dev).requires_grad_()
+    out, _ = torch.ops.fbgemm.jagged_dense_elementwise_add_jagged_output(xt, offs, yt)
+    g = rng.standard_normal((10, 3)).astype(np.float32)
+    (out * torch.from_numpy(g).to(dev)).sum().backward()
+    _bits_equal(xt.grad, g)
+    _bits_equal(yt.grad, orc.jagged_to_padded_dense(g, [off0, off1], [2, 3], 0.0))

@@ -729,3 +729,28 @@ def test_permute_2d_sparse_data_vs_bag_lists():
     np.testing.assert_array_equal(pw, np.concatenate(exp_w))
     np.testing.assert_array_equal(pl[:4], lengths[[2, 0, 2, 3]])
     assert np.all(pl[4] == 0)
+
+
+def test_jagged_mul_vs_torch_composition():
+    """x * y at the jagged coordinates: torch's own padded-dense-to-jagged
+    gather of y, times x, in each dtype (f16/bf16 through fp32, as torch's
+    half and bfloat16 mul compute); rows past max_L give x * 0 (signed zero)."""
+    rng = np.random.default_rng(4)
+    off = np.array([0, 3, 3, 9, 10], np.int64)  # bag 2 has 6 rows, max_L 4: two past it
+    for dt, tdt in (("f32", torch.float32), ("f64", torch.float64), ("f16", torch.float16),
+                    ("bf16", torch.bfloat16)):
+        x = torch.from_numpy(rng.standard_normal((10, 3))).to(tdt)
+        y = torch.from_numpy(rng.standard_normal((4, 4, 3))).to(tdt)
+        yg = torch.zeros_like(x)
+        for b in range(4):
+            n = min(off[b + 1] - off[b], 4)
+            yg[off[b]:off[b] + n] = y[b, :n]
+        exp = x * yg
+        as_np = (lambda t: t.view(torch.int16).numpy().view(np.uint16)) if dt == "bf16" else \
+            (lambda t: t.numpy())
+        got = orc.jagged_dense_elementwise_mul(as_np(x), [off], as_np(y), dt)
+        if dt == "bf16":
+            np.testing.assert_array_equal(got, as_np(exp))
+        else:
+            np.testing.assert_array_equal(np.signbit(got), np.signbit(exp.numpy()))
+            np.testing.assert_array_equal(got, exp.numpy())

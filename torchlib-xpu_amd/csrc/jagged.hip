@@ -1,8 +1,9 @@
 // Jagged <-> padded-dense kernels for gfx950.
 //
 // Semantics follow fbgemm_gpu's jagged_to_padded_dense_forward,
-// dense_to_jagged_forward and jagged_dense_elementwise_add_jagged_output
-// (upstream src/jagged_tensor_ops/, recalled), restated from torch's own
+// dense_to_jagged_forward, jagged_dense_elementwise_add_jagged_output and
+// jagged_dense_elementwise_mul (upstream src/jagged_tensor_ops/, recalled;
+// outside the dense the add gives x + 0 and the mul x * 0), restated from torch's own
 // port of the same ops: torch/_inductor/jagged_lowerings.py:161-177 (masked
 // load, else padding value) and :231-249 (jagged rows past max length become
 // 0).
@@ -139,50 +140,53 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-template <int DT>
-struct AddOp;
+// x (op) y per element in the element type's arithmetic: f32/f64 natively,
+// f16/bf16 computed in fp32 (sums and products of two such values are then
+// rounded once to the element type, to nearest even).
+template <int DT, bool MUL>
+struct BinOp;
 
-template <>
-struct AddOp<MX_DTYPE_F32> {
+template <bool MUL>
+struct BinOp<MX_DTYPE_F32, MUL> {
   static constexpr int kBytes = 4;
   __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
-    const float r = *reinterpret_cast<const float*>(x) + *reinterpret_cast<const float*>(y);
-    *reinterpret_cast<float*>(o) = r;
+    const float a = *reinterpret_cast<const float*>(x), b = *reinterpret_cast<const float*>(y);
+    *reinterpret_cast<float*>(o) = MUL ? a * b : a + b;
   }
 };
-template <>
-struct AddOp<MX_DTYPE_F64> {
+template <bool MUL>
+struct BinOp<MX_DTYPE_F64, MUL> {
   static constexpr int kBytes = 8;
   __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
-    const double r = *reinterpret_cast<const double*>(x) + *reinterpret_cast<const double*>(y);
-    *reinterpret_cast<double*>(o) = r;
+    const double a = *reinterpret_cast<const double*>(x), b = *reinterpret_cast<const double*>(y);
+    *reinterpret_cast<double*>(o) = MUL ? a * b : a + b;
   }
 };
-template <>
-struct AddOp<MX_DTYPE_F16> {
+template <bool MUL>
+struct BinOp<MX_DTYPE_F16, MUL> {
   static constexpr int kBytes = 2;
   __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
-    const float r = __half2float(*reinterpret_cast<const __half*>(x)) +
-                    __half2float(*reinterpret_cast<const __half*>(y));
-    *reinterpret_cast<__half*>(o) = __float2half_rn(r);
+    const float a = __half2float(*reinterpret_cast<const __half*>(x));
+    const float b = __half2float(*reinterpret_cast<const __half*>(y));
+    *reinterpret_cast<__half*>(o) = __float2half_rn(MUL ? a * b : a + b);
   }
 };
-template <>
-struct AddOp<MX_DTYPE_BF16> {
+template <bool MUL>
+struct BinOp<MX_DTYPE_BF16, MUL> {
   static constexpr int kBytes = 2;
   __device__ static void apply(const uint8_t* x, const uint8_t* y, uint8_t* o) {
-    const float r = bf16_to_f32(*reinterpret_cast<const uint16_t*>(x)) +
-                    bf16_to_f32(*reinterpret_cast<const uint16_t*>(y));
-    *reinterpret_cast<uint16_t*>(o) = f32_to_bf16(r);
+    const float a = bf16_to_f32(*reinterpret_cast<const uint16_t*>(x));
+    const float b = bf16_to_f32(*reinterpret_cast<const uint16_t*>(y));
+    *reinterpret_cast<uint16_t*>(o) = f32_to_bf16(MUL ? a * b : a + b);
   }
 };
 
-template <int VEC, typename I, int DT>
+template <int VEC, typename I, int DT, bool MUL>
 __global__ void __launch_bounds__(256) jagged_add_kernel(const uint8_t* __restrict__ x,
                                                          const uint8_t* __restrict__ y,
                                                          uint8_t* __restrict__ out, JaggedMeta m,
                                                          int64_t total_L, int64_t vpr) {
-  using Op = AddOp<DT>;
+  using Op = BinOp<DT, MUL>;
   const int64_t total = total_L * vpr;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < total;
@@ -250,9 +254,9 @@ __global__ void __launch_bounds__(256)
 }
 
 // Values rows [r0, r1) whose first `copy_rows` rows take dense rows from
-// `dense_row0` on and the rest 0; ADD adds x (jagged + dense add), else the
-// dense value is copied (dense -> jagged).
-template <int VEC, bool ADD, int DT>
+// `dense_row0` on and the rest 0; ADD combines x with them (x + y, or x * y
+// with MUL), else the dense value is copied (dense -> jagged).
+template <int VEC, bool ADD, int DT, bool MUL>
 __device__ __forceinline__ void emit_rows(const uint8_t* __restrict__ dense,
                                           const uint8_t* __restrict__ x,
                                           uint8_t* __restrict__ out, int64_t r0, int64_t r1,
@@ -281,8 +285,8 @@ __device__ __forceinline__ void emit_rows(const uint8_t* __restrict__ dense,
         const Chunk<VEC> cx = xs[i];
         Chunk<VEC> co;
 #pragma unroll
-        for (int e = 0; e < VEC; e += AddOp<DT>::kBytes)
-          AddOp<DT>::apply(cx.b + e, y[it].b + e, co.b + e);
+        for (int e = 0; e < VEC; e += BinOp<DT, MUL>::kBytes)
+          BinOp<DT, MUL>::apply(cx.b + e, y[it].b + e, co.b + e);
         dst[i] = co;
       } else {
         dst[i] = y[it];
@@ -295,7 +299,7 @@ __device__ __forceinline__ void emit_rows(const uint8_t* __restrict__ dense,
 // (before off[0], from off[nbags] on), which have no dense position.  Row
 // ranges are clamped to [0, total_L], so malformed offsets never write out
 // of bounds.
-template <int VEC, typename I, bool ADD, int DT>
+template <int VEC, typename I, bool ADD, int DT, bool MUL>
 __global__ void __launch_bounds__(256)
     jagged_out1_kernel(const uint8_t* __restrict__ dense, const uint8_t* __restrict__ x,
                        uint8_t* __restrict__ out, const I* __restrict__ off, int64_t nbags,
@@ -306,12 +310,12 @@ __global__ void __launch_bounds__(256)
     const int64_t r0 = clamp(static_cast<int64_t>(off[b]), 0);
     const int64_t r1 = clamp(static_cast<int64_t>(off[b + 1]), r0);
     const int64_t copy = r1 - r0 < max_L ? r1 - r0 : max_L;
-    emit_rows<VEC, ADD, DT>(dense, x, out, r0, r1, copy, b * max_L, vpr);
+    emit_rows<VEC, ADD, DT, MUL>(dense, x, out, r0, r1, copy, b * max_L, vpr);
   } else {
     const int64_t head = clamp(static_cast<int64_t>(off[0]), 0);
     const int64_t tail = clamp(static_cast<int64_t>(off[nbags]), head);
-    emit_rows<VEC, ADD, DT>(dense, x, out, 0, head, 0, 0, vpr);
-    emit_rows<VEC, ADD, DT>(dense, x, out, tail, total_L, 0, 0, vpr);
+    emit_rows<VEC, ADD, DT, MUL>(dense, x, out, 0, head, 0, 0, vpr);
+    emit_rows<VEC, ADD, DT, MUL>(dense, x, out, tail, total_L, 0, 0, vpr);
   }
 }
 
@@ -442,12 +446,12 @@ extern "C" int mx_jagged_to_padded_dense(const void* values, int64_t elem_bytes,
 }
 
 // Shared host path of dense_to_jagged (x_values == NULL) and of the
-// jagged + dense add (x_values != NULL).
+// jagged (op) dense elementwise ops (x_values != NULL; mul: x * y, else x + y).
 static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner,
                             int32_t num_jagged_dim, const void* const* offsets,
                             int32_t offset_bytes, const int64_t* offsets_numel,
                             const int64_t* max_lengths, int64_t total_L, const void* x_values,
-                            int32_t add_dtype, void* out, void* stream) {
+                            int32_t add_dtype, bool mul, void* out, void* stream) {
   JaggedMeta m;
   if (int rc = build_meta(m, num_jagged_dim, offsets, offset_bytes, offsets_numel, max_lengths))
     return rc;
@@ -476,10 +480,10 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
     MX_VEC_SWITCH(vec, {
       if (one) {
         if (offset_bytes == 8)
-          jagged_out1_kernel<V, int64_t, false, MX_DTYPE_F32><<<g1, 256, 0, s>>>(
+          jagged_out1_kernel<V, int64_t, false, MX_DTYPE_F32, false><<<g1, 256, 0, s>>>(
               d, nullptr, o, static_cast<const int64_t*>(offsets[0]), nbags, L0, total_L, vpr);
         else
-          jagged_out1_kernel<V, int32_t, false, MX_DTYPE_F32><<<g1, 256, 0, s>>>(
+          jagged_out1_kernel<V, int32_t, false, MX_DTYPE_F32, false><<<g1, 256, 0, s>>>(
               d, nullptr, o, static_cast<const int32_t*>(offsets[0]), nbags, L0, total_L, vpr);
       } else if (offset_bytes == 8) {
         d2j_kernel<V, int64_t><<<grid, 256, 0, s>>>(d, o, m, total_L, vpr);
@@ -493,21 +497,27 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
   MX_REQUIRE(dtype_bytes(add_dtype) == elem_bytes, "dtype %d does not match element size %lld",
              add_dtype, (long long)elem_bytes);
   const auto* x = static_cast<const uint8_t*>(x_values);
-#define MX_ADD_LAUNCH(DTC)                                                                 \
-  MX_VEC_SWITCH(vec, {                                                                     \
-    if constexpr (V >= AddOp<DTC>::kBytes) {                                               \
-      if (one && offset_bytes == 8)                                                        \
-        jagged_out1_kernel<V, int64_t, true, DTC><<<g1, 256, 0, s>>>(                      \
-            d, x, o, static_cast<const int64_t*>(offsets[0]), nbags, L0, total_L, vpr);    \
-      else if (one)                                                                        \
-        jagged_out1_kernel<V, int32_t, true, DTC><<<g1, 256, 0, s>>>(                      \
-            d, x, o, static_cast<const int32_t*>(offsets[0]), nbags, L0, total_L, vpr);    \
-      else if (offset_bytes == 8)                                                          \
-        jagged_add_kernel<V, int64_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
-      else                                                                                 \
-        jagged_add_kernel<V, int32_t, DTC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
-    }                                                                                      \
+#define MX_OP_LAUNCH(DTC, MULC)                                                                 \
+  MX_VEC_SWITCH(vec, {                                                                          \
+    if constexpr (V >= BinOp<DTC, MULC>::kBytes) {                                              \
+      if (one && offset_bytes == 8)                                                             \
+        jagged_out1_kernel<V, int64_t, true, DTC, MULC><<<g1, 256, 0, s>>>(                     \
+            d, x, o, static_cast<const int64_t*>(offsets[0]), nbags, L0, total_L, vpr);         \
+      else if (one)                                                                             \
+        jagged_out1_kernel<V, int32_t, true, DTC, MULC><<<g1, 256, 0, s>>>(                     \
+            d, x, o, static_cast<const int32_t*>(offsets[0]), nbags, L0, total_L, vpr);         \
+      else if (offset_bytes == 8)                                                               \
+        jagged_add_kernel<V, int64_t, DTC, MULC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
+      else                                                                                      \
+        jagged_add_kernel<V, int32_t, DTC, MULC><<<grid, 256, 0, s>>>(x, d, o, m, total_L, vpr); \
+    }                                                                                           \
   })
+#define MX_ADD_LAUNCH(DTC)    \
+  if (mul) {                  \
+    MX_OP_LAUNCH(DTC, true);  \
+  } else {                    \
+    MX_OP_LAUNCH(DTC, false); \
+  }
   switch (add_dtype) {
     case MX_DTYPE_F32: MX_ADD_LAUNCH(MX_DTYPE_F32); break;
     case MX_DTYPE_F64: MX_ADD_LAUNCH(MX_DTYPE_F64); break;
@@ -516,6 +526,7 @@ static int jagged_output_op(const void* dense, int64_t elem_bytes, int64_t inner
     default: return set_error(MX_EUNSUPPORTED, "dtype %d not supported", add_dtype);
   }
 #undef MX_ADD_LAUNCH
+#undef MX_OP_LAUNCH
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
@@ -527,7 +538,7 @@ extern "C" int mx_dense_to_jagged(const void* dense, int64_t elem_bytes, int64_t
                                   void* stream) {
   clear_error();
   return jagged_output_op(dense, elem_bytes, inner, num_jagged_dim, offsets, offset_bytes,
-                          offsets_numel, max_lengths, total_L, nullptr, 0, out, stream);
+                          offsets_numel, max_lengths, total_L, nullptr, 0, false, out, stream);
 }
 
 extern "C" int mx_jagged_dense_elementwise_add(const void* x_values, const void* y_dense,
@@ -542,5 +553,20 @@ extern "C" int mx_jagged_dense_elementwise_add(const void* x_values, const void*
   MX_REQUIRE(x_values != nullptr || total_L == 0, "null x_values");
   if (total_L == 0 || inner == 0) return MX_OK;
   return jagged_output_op(y_dense, eb, inner, num_jagged_dim, offsets, offset_bytes,
-                          offsets_numel, max_lengths, total_L, x_values, dtype, out, stream);
+                          offsets_numel, max_lengths, total_L, x_values, dtype, false, out, stream);
+}
+
+extern "C" int mx_jagged_dense_elementwise_mul(const void* x_values, const void* y_dense,
+                                               int32_t dtype, int64_t inner,
+                                               int32_t num_jagged_dim, const void* const* offsets,
+                                               int32_t offset_bytes, const int64_t* offsets_numel,
+                                               const int64_t* max_lengths, int64_t total_L,
+                                               void* out, void* stream) {
+  clear_error();
+  const int64_t eb = dtype_bytes(dtype);
+  if (eb < 0) return set_error(MX_EUNSUPPORTED, "dtype %d not supported", dtype);
+  MX_REQUIRE(x_values != nullptr || total_L == 0, "null x_values");
+  if (total_L == 0 || inner == 0) return MX_OK;
+  return jagged_output_op(y_dense, eb, inner, num_jagged_dim, offsets, offset_bytes,
+                          offsets_numel, max_lengths, total_L, x_values, dtype, true, out, stream);
 }

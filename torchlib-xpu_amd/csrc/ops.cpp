@@ -336,6 +336,39 @@ Tensor jagged_dense_add_forward(const Tensor& x_values, const std::vector<Tensor
   return out;
 }
 
+Tensor jagged_dense_mul_forward(const Tensor& x_values, const std::vector<Tensor>& offsets,
+                                const Tensor& y) {
+  check_gpu(x_values, "x_values");
+  check_gpu(y, "y");
+  check_same_device(x_values, y, "y");
+  c10::OptionalDeviceGuard guard(x_values.device());
+  TORCH_CHECK(x_values.scalar_type() == y.scalar_type(), "x_values and y must share a dtype");
+  const int32_t dt = mx_dtype_of(x_values.scalar_type());
+  TORCH_CHECK(dt >= 0, "dtype ", x_values.scalar_type(), " is not supported");
+  const int64_t nd = static_cast<int64_t>(offsets.size());
+  TORCH_CHECK(y.dim() >= 1 + nd, "y must have at least ", 1 + nd, " dimensions");
+  OffsetsPack p;
+  pack_offsets(offsets, x_values, p);
+  TORCH_CHECK(y.size(0) == p.numel[0] - 1, "y has ", y.size(0), " rows but offsets describe ",
+              p.numel[0] - 1);
+  const c10::MaybeOwned<Tensor> xm = x_values.expect_contiguous();
+  const c10::MaybeOwned<Tensor> ym = y.expect_contiguous();
+  const Tensor& x = *xm;
+  const Tensor& yc = *ym;
+  std::array<int64_t, MX_MAX_JAGGED_DIM> max_lengths{};
+  for (int64_t k = 0; k < nd; ++k) max_lengths[k] = yc.size(1 + k);
+  int64_t inner = 1;
+  for (int64_t k = 1 + nd; k < yc.dim(); ++k) inner *= yc.size(k);
+  const int64_t x_inner = x.dim() == 1 ? 1 : c10::multiply_integers(x.sizes().slice(1));
+  TORCH_CHECK(x_inner == inner, "x_values inner size ", x_inner, " != y inner size ", inner);
+  Tensor out = at::empty_like(x);
+  MX_CALL(mx_jagged_dense_elementwise_mul(x.data_ptr(), yc.data_ptr(), dt, inner,
+                                          static_cast<int32_t>(nd), p.ptrs.data(), p.bytes,
+                                          p.numel.data(), max_lengths.data(), x.size(0),
+                                          out.data_ptr(), stream_of(x)));
+  return out;
+}
+
 Tensor jagged_to_padded_dense_backward(const Tensor& grad_output,
                                        const std::vector<Tensor>& offsets,
                                        c10::SymInt total_L) {
@@ -361,7 +394,8 @@ class JaggedToPaddedDense : public torch::autograd::Function<JaggedToPaddedDense
   static variable_list backward(AutogradContext* ctx, variable_list grads) {
     const auto offsets = ctx->get_saved_variables();
     const int64_t total_L = ctx->saved_data["total_L"].toInt();
-    variable_list out(1 + offsets.size() + 2);  // values, offsets..., max_lengths, padding
+    // One slot per forward argument (the offsets list is one).
+    variable_list out(4);  // values, offsets, max_lengths, padding_value
     out[0] = dense_to_jagged_forward(grads[0], offsets, c10::SymInt(total_L));
     return out;
   }
@@ -382,7 +416,7 @@ class DenseToJagged : public torch::autograd::Function<DenseToJagged> {
     const auto offsets = ctx->get_saved_variables();
     const auto ml = ctx->saved_data["max_lengths"].toIntVector();
     std::vector<c10::SymInt> sml(ml.begin(), ml.end());
-    variable_list out(1 + offsets.size() + 1);  // dense, offsets..., total_L
+    variable_list out(3);  // dense, offsets, total_L
     out[0] = jagged_to_padded_dense_forward(grads[0], offsets, sml, 0.0);
     return out;
   }
@@ -403,9 +437,40 @@ class JaggedDenseAdd : public torch::autograd::Function<JaggedDenseAdd> {
     const auto offsets = ctx->get_saved_variables();
     const auto ml = ctx->saved_data["max_lengths"].toIntVector();
     std::vector<c10::SymInt> sml(ml.begin(), ml.end());
-    variable_list out(1 + offsets.size() + 1);  // x, offsets..., y
+    variable_list out(3);  // x, offsets (one argument), y
     out[0] = grads[0];
-    out.back() = jagged_to_padded_dense_forward(grads[0], offsets, sml, 0.0);
+    out[2] = jagged_to_padded_dense_forward(grads[0], offsets, sml, 0.0);
+    return out;
+  }
+};
+
+// d(x * y): grad_x = grad * y at the coordinates (the mul again), grad_y =
+// the padded dense of grad * x (zero where no jagged element lies).
+class JaggedDenseMul : public torch::autograd::Function<JaggedDenseMul> {
+ public:
+  static Tensor forward(AutogradContext* ctx, const Tensor& x, const std::vector<Tensor>& offsets,
+                        const Tensor& y) {
+    std::vector<Tensor> keep(offsets);
+    keep.push_back(x);
+    keep.push_back(y);
+    ctx->save_for_backward(keep);
+    ctx->saved_data["num_offsets"] = static_cast<int64_t>(offsets.size());
+    at::AutoDispatchBelowADInplaceOrView g;
+    return jagged_dense_mul_forward(x, offsets, y);
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    auto saved = ctx->get_saved_variables();
+    const int64_t nd = ctx->saved_data["num_offsets"].toInt();
+    const Tensor y = saved.back();
+    saved.pop_back();
+    const Tensor x = saved.back();
+    saved.pop_back();
+    std::vector<c10::SymInt> sml;
+    for (int64_t k = 0; k < nd; ++k) sml.emplace_back(y.size(1 + k));
+    const Tensor g = grads[0].contiguous();
+    variable_list out(3);  // x, offsets (one argument), y
+    out[0] = jagged_dense_mul_forward(g, saved, y);
+    out[2] = jagged_to_padded_dense_forward(g * x, saved, sml, 0.0);
     return out;
   }
 };
@@ -435,6 +500,47 @@ std::tuple<Tensor, std::vector<Tensor>> jagged_dense_add_autograd(
     const Tensor& x, const std::vector<Tensor>& offsets, const Tensor& y) {
   if (!wants_grad(x, y)) return {jagged_dense_add_forward(x, offsets, y), offsets};
   return {JaggedDenseAdd::apply(x, offsets, y), offsets};
+}
+
+Tensor jagged_dense_mul_autograd(const Tensor& x, const std::vector<Tensor>& offsets,
+                                 const Tensor& y) {
+  if (!wants_grad(x, y)) return jagged_dense_mul_forward(x, offsets, y);
+  return JaggedDenseMul::apply(x, offsets, y);
+}
+
+// The older one-dim spellings: values [total_L, D] (2d) or [total_L] (1d).
+Tensor jagged_2d_to_dense_autograd(const Tensor& values, const Tensor& offsets,
+                                   c10::SymInt max_sequence_length) {
+  TORCH_CHECK(values.dim() == 2, "jagged_2d_to_dense takes values [total_L, D]");
+  const std::vector<c10::SymInt> ml{max_sequence_length};
+  return jagged_to_padded_dense_autograd(values, {offsets}, ml, 0.0);
+}
+
+Tensor jagged_2d_to_dense_plain(const Tensor& values, const Tensor& offsets,
+                                c10::SymInt max_sequence_length) {
+  TORCH_CHECK(values.dim() == 2, "jagged_2d_to_dense takes values [total_L, D]");
+  const std::vector<c10::SymInt> ml{max_sequence_length};
+  return jagged_to_padded_dense_forward(values, {offsets}, ml, 0.0);
+}
+
+Tensor jagged_1d_to_dense(const Tensor& values, const Tensor& offsets,
+                          c10::SymInt max_sequence_length, int64_t padding_value) {
+  TORCH_CHECK(values.dim() == 1, "jagged_1d_to_dense takes values [total_L]");
+  check_gpu(values, "values");
+  c10::OptionalDeviceGuard guard(values.device());
+  const int64_t max_L = max_sequence_length.expect_int();
+  OffsetsPack p;
+  pack_offsets({offsets}, values, p);
+  const c10::MaybeOwned<Tensor> vm = values.expect_contiguous();
+  const Tensor& v = *vm;
+  Tensor out = at::empty({p.numel[0] - 1, max_L}, v.options());
+  // An integer padding keeps every bit of its type (no trip through a double).
+  const uint64_t pad = at::isIntegralType(v.scalar_type(), false)
+                           ? static_cast<uint64_t>(padding_value)
+                           : pad_bits_of(static_cast<double>(padding_value), v.scalar_type());
+  MX_CALL(mx_jagged_to_padded_dense(v.data_ptr(), v.element_size(), 1, 1, p.ptrs.data(), p.bytes,
+                                    p.numel.data(), &max_L, pad, out.data_ptr(), stream_of(v)));
+  return out;
 }
 
 Tensor jagged_to_padded_dense_plain(const Tensor& values, const std::vector<Tensor>& offsets,
@@ -1770,6 +1876,10 @@ TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
         "-> (Tensor, Tensor[])");
   m.def("jagged_dense_elementwise_add_jagged_output(Tensor x_values, Tensor[] x_offsets, "
         "Tensor y) -> (Tensor, Tensor[])");
+  m.def("jagged_dense_elementwise_mul(Tensor x_values, Tensor[] x_offsets, Tensor y) -> Tensor");
+  m.def("jagged_2d_to_dense(Tensor values, Tensor offsets, SymInt max_sequence_length) -> Tensor");
+  m.def("jagged_1d_to_dense(Tensor values, Tensor offsets, SymInt max_sequence_length, "
+        "int padding_value) -> Tensor");
   m.def("split_embedding_codegen_forward_unweighted_cuda(Tensor dev_weights, Tensor uvm_weights, "
         "Tensor lxu_cache_weights, Tensor weights_placements, Tensor weights_offsets, "
         "Tensor D_offsets, SymInt total_D, SymInt max_D, Tensor indices, Tensor offsets, "
@@ -1913,6 +2023,9 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("dense_to_jagged_forward", TORCH_FN(mx_ops::dense_to_jagged_forward));
   m.impl("dense_to_jagged", TORCH_FN(mx_ops::dense_to_jagged_plain));
   m.impl("jagged_dense_elementwise_add_jagged_output", TORCH_FN(mx_ops::jagged_dense_add_plain));
+  m.impl("jagged_dense_elementwise_mul", TORCH_FN(mx_ops::jagged_dense_mul_forward));
+  m.impl("jagged_2d_to_dense", TORCH_FN(mx_ops::jagged_2d_to_dense_plain));
+  m.impl("jagged_1d_to_dense", TORCH_FN(mx_ops::jagged_1d_to_dense));
   m.impl("split_embedding_codegen_forward_unweighted_cuda", TORCH_FN(mx_ops::forward_unweighted));
   m.impl("split_embedding_codegen_forward_weighted_cuda", TORCH_FN(mx_ops::forward_weighted));
   m.impl("transpose_embedding_input", TORCH_FN(mx_ops::transpose_embedding_input));
@@ -1963,6 +2076,8 @@ TORCH_LIBRARY_IMPL(fbgemm, Autograd, m) {
   m.impl("jagged_to_padded_dense", TORCH_FN(mx_ops::jagged_to_padded_dense_autograd));
   m.impl("dense_to_jagged", TORCH_FN(mx_ops::dense_to_jagged_autograd));
   m.impl("jagged_dense_elementwise_add_jagged_output", TORCH_FN(mx_ops::jagged_dense_add_autograd));
+  m.impl("jagged_dense_elementwise_mul", TORCH_FN(mx_ops::jagged_dense_mul_autograd));
+  m.impl("jagged_2d_to_dense", TORCH_FN(mx_ops::jagged_2d_to_dense_autograd));
   m.impl("split_embedding_codegen_lookup_rowwise_adagrad_function",
          TORCH_FN(mx_ops::lookup_rowwise_adagrad));
 }
