@@ -88,8 +88,8 @@ extern "C" {
  * mx_tbe_forward_nobag, mx_tbe_backward_rowwise_adagrad_nobag,
  * mx_tbe_transpose_embedding_input_nobag, mx_nbit_forward_nobag and their
  * workspace queries, mx_cumsum, mx_permute_2d_lengths, mx_permute_2d_data
- * with mx_cumsum_workspace_bytes, and mx_jagged_dense_elementwise_mul (all
- * earlier ones unchanged). */
+ * with mx_cumsum_workspace_bytes, mx_offsets_range, mx_expand_into_jagged_permute
+ * and mx_jagged_dense_elementwise_mul (all earlier ones unchanged). */
 #define MX_FBGEMM_VERSION 500
 int mx_version(void);
 
@@ -512,6 +512,21 @@ int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t T, int64_t
                        int32_t offset_bytes, const void* indices, int32_t index_bytes,
                        const float* weights, int64_t out_len, void* permuted_indices,
                        float* permuted_weights, void* stream);
+
+/* Serves fbgemm::offsets_range: out[j] = j - offsets[i] for j in segment i =
+ * [offsets[i], offsets[i + 1]) (the last segment ends at range_size); out
+ * [range_size], int32 or int64 like offsets. */
+int mx_offsets_range(const void* offsets, int32_t index_bytes, int64_t nseg, int64_t range_size,
+                     void* out, void* stream);
+
+/* Serves fbgemm::expand_into_jagged_permute: for output feature t,
+ * out[output_offsets[t] + j] = input_offsets[permute[t]] + j, j below its
+ * length (output_offsets[t+1] - output_offsets[t]; output_size for the last
+ * when output_offsets has T entries). */
+int mx_expand_into_jagged_permute(const int32_t* permute, int64_t T, const void* input_offsets,
+                                  int64_t input_numel, const void* output_offsets,
+                                  int64_t output_numel, int32_t index_bytes, int64_t output_size,
+                                  void* out, void* stream);
 
 /* ---- TBE nbit inference forward ---------------------------------------- */
 

@@ -337,6 +337,33 @@ def permute_2d_sparse_data(permute, lengths, indices, weights=None):
     return plen, cat_i, cat_w
 
 
+def offsets_range(offsets, range_size: int) -> np.ndarray:
+    """out[j] = j - offsets[i] over segment i = [offsets[i], offsets[i+1]) (the
+    last ends at range_size)."""
+    offsets = np.asarray(offsets)
+    out = np.zeros(range_size, offsets.dtype)
+    ends = np.concatenate([offsets[1:], [range_size]]).astype(np.int64)
+    for s, e in zip(offsets.astype(np.int64), ends):
+        s, e = max(int(s), 0), min(int(e), range_size)
+        out[s:e] = np.arange(e - s, dtype=offsets.dtype)
+    return out
+
+
+def expand_into_jagged_permute(permute, input_offsets, output_offsets, output_size: int):
+    """out[output_offsets[t] + j] = input_offsets[permute[t]] + j over output
+    feature t's length."""
+    output_offsets = np.asarray(output_offsets)
+    input_offsets = np.asarray(input_offsets)
+    T = len(permute)
+    ends = output_offsets[1:T + 1] if output_offsets.shape[0] == T + 1 else \
+        np.concatenate([output_offsets[1:T], [output_size]])
+    out = np.zeros(output_size, input_offsets.dtype)
+    for t in range(T):
+        d0, d1 = int(output_offsets[t]), min(int(ends[t]), output_size)
+        out[d0:d1] = input_offsets[permute[t]] + np.arange(d1 - d0, dtype=input_offsets.dtype)
+    return out
+
+
 def hfp8_to_float(codes, ebits: int, ebias: int) -> np.ndarray:
     """Decodes hfp8 codes (uint8) to fp32 (the C restatement)."""
     f = lib().orc_hfp8_to_float

@@ -1,8 +1,9 @@
 """GPU parity of the sparse-feature helpers against the oracle, bit-exact:
 asynchronous_{exclusive,inclusive,complete}_cumsum (int32/int64, 1-D and
-2-D, sizes around the 8192-element tile, wrap-around) and
-permute_2D_sparse_data (repeats, dropped and out-of-range features,
-weights, with and without permuted_lengths_sum)."""
+2-D, sizes around the 8192-element tile, wrap-around),
+permute_2D_sparse_data / permute_1D_sparse_data (repeats, dropped and
+out-of-range features, weights, with and without permuted_lengths_sum),
+offsets_range and expand_into_jagged_permute."""
 
 import numpy as np
 import pytest
@@ -93,3 +94,54 @@ def test_permute_2d_sparse_data_subset(dev):
     np.testing.assert_array_equal(pl.cpu().numpy(), exp_l)
     np.testing.assert_array_equal(pi.cpu().numpy(), exp_i)
     assert pw is None
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_permute_1d_sparse_data(dev, weighted):
+    print(f"[case] permute_1D w={weighted}", flush=True)
+    rng = np.random.default_rng(21)
+    T = 40
+    lengths = rng.integers(0, 50, T)
+    idx = rng.integers(0, 10**6, int(lengths.sum()))
+    w = rng.standard_normal(idx.size).astype(np.float32) if weighted else None
+    permute = rng.permutation(T).astype(np.int32)[:30]
+    exp_l, exp_i, exp_w = orc.permute_2d_sparse_data(permute, lengths[:, None], idx, w)
+    pl, pi, pw = torch.ops.fbgemm.permute_1D_sparse_data(
+        torch.from_numpy(permute).to(dev), torch.from_numpy(lengths).to(dev),
+        torch.from_numpy(idx).to(dev), None if w is None else torch.from_numpy(w).to(dev))
+    np.testing.assert_array_equal(pl.cpu().numpy(), exp_l.reshape(-1))
+    np.testing.assert_array_equal(pi.cpu().numpy(), exp_i)
+    if weighted:
+        np.testing.assert_array_equal(pw.cpu().numpy(), exp_w)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_offsets_range(dev, dtype):
+    print(f"[case] offsets_range {np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(22)
+    lengths = rng.integers(0, 100, 5000)
+    lengths[::7] = 0
+    off = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(dtype)
+    n = int(lengths.sum())
+    got = torch.ops.fbgemm.offsets_range(torch.from_numpy(off).to(dev), n)
+    np.testing.assert_array_equal(got.cpu().numpy(), orc.offsets_range(off, n))
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+@pytest.mark.parametrize("with_end", [False, True])
+def test_expand_into_jagged_permute(dev, dtype, with_end):
+    print(f"[case] expand_into_jagged_permute {np.dtype(dtype).name} end={with_end}", flush=True)
+    rng = np.random.default_rng(23)
+    T = 300
+    in_len = rng.integers(0, 40, T)
+    in_off = np.concatenate([[0], np.cumsum(in_len)[:-1]]).astype(dtype)
+    permute = rng.permutation(T).astype(np.int32)
+    out_len = in_len[permute]
+    out_off = np.concatenate([[0], np.cumsum(out_len)]).astype(dtype)
+    size = int(out_len.sum())
+    oo = out_off if with_end else out_off[:-1]
+    got = torch.ops.fbgemm.expand_into_jagged_permute(
+        torch.from_numpy(permute).to(dev), torch.from_numpy(in_off).to(dev),
+        torch.from_numpy(oo).to(dev), size)
+    np.testing.assert_array_equal(got.cpu().numpy(),
+                                  orc.expand_into_jagged_permute(permute, in_off, oo, size))

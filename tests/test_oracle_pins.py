@@ -754,3 +754,25 @@ def test_jagged_mul_vs_torch_composition():
         else:
             np.testing.assert_array_equal(np.signbit(got), np.signbit(exp.numpy()))
             np.testing.assert_array_equal(got, exp.numpy())
+
+
+def test_offsets_range_and_expand_permute_vs_python():
+    """Element by element in Python: offsets_range's positions within their
+    segments, and expand_into_jagged_permute's source positions."""
+    off = np.array([0, 3, 3, 7], np.int64)
+    exp = []
+    bounds = [0, 3, 3, 7, 10]
+    for i in range(4):
+        exp += list(range(bounds[i + 1] - bounds[i]))
+    np.testing.assert_array_equal(orc.offsets_range(off, 10), np.array(exp, np.int64))
+    in_len = [2, 5, 0, 3]
+    in_off = np.array([0, 2, 7, 7], np.int64)
+    permute = [3, 1, 0, 1]
+    out_len = [in_len[p] for p in permute]
+    out_off = np.array([0, 3, 8, 10, 15], np.int64)
+    exp = [in_off[p] + j for p in permute for j in range(in_len[p])]
+    np.testing.assert_array_equal(orc.expand_into_jagged_permute(permute, in_off, out_off, 15),
+                                  np.array(exp, np.int64))
+    np.testing.assert_array_equal(orc.expand_into_jagged_permute(permute, in_off, out_off[:4], 15),
+                                  np.array(exp, np.int64))
+    assert sum(out_len) == 15

@@ -1857,9 +1857,56 @@ std::tuple<Tensor, Tensor, std::optional<Tensor>> permute_2D_sparse_data(
   return {plen, pidx, pw};
 }
 
+std::tuple<Tensor, Tensor, std::optional<Tensor>> permute_1D_sparse_data(
+    const Tensor& permute, const Tensor& lengths, const Tensor& indices,
+    const std::optional<Tensor>& weights, std::optional<c10::SymInt> permuted_lengths_sum) {
+  TORCH_CHECK(lengths.dim() == 1, "lengths must be 1-D [T]");
+  auto r = permute_2D_sparse_data(permute, lengths.view({-1, 1}), indices, weights,
+                                  permuted_lengths_sum);
+  return {std::get<0>(r).view({-1}), std::get<1>(r), std::get<2>(r)};
+}
+
+Tensor offsets_range(const Tensor& offsets, c10::SymInt range_size_sym) {
+  check_gpu(offsets, "offsets");
+  c10::OptionalDeviceGuard guard(offsets.device());
+  TORCH_CHECK(offsets.dim() == 1, "offsets must be 1-D");
+  const int32_t ib = index_bytes_of(offsets, "offsets");
+  const int64_t range_size = range_size_sym.expect_int();
+  const Tensor off = offsets.contiguous();
+  Tensor out = at::empty({range_size}, off.options());
+  MX_CALL(mx_offsets_range(off.data_ptr(), ib, off.numel(), range_size, out.data_ptr(),
+                           stream_of(off)));
+  return out;
+}
+
+Tensor expand_into_jagged_permute(const Tensor& permute, const Tensor& input_offsets,
+                                  const Tensor& output_offsets, c10::SymInt output_size_sym) {
+  check_gpu(permute, "permute");
+  c10::OptionalDeviceGuard guard(permute.device());
+  check_arg(input_offsets, permute, "input_offsets", true);
+  check_arg(output_offsets, permute, "output_offsets", true);
+  TORCH_CHECK(permute.scalar_type() == at::kInt, "permute must be int32");
+  const int32_t ib = index_bytes_of(input_offsets, "input_offsets");
+  TORCH_CHECK(index_bytes_of(output_offsets, "output_offsets") == ib,
+              "input_offsets and output_offsets must share a dtype");
+  const int64_t output_size = output_size_sym.expect_int();
+  const Tensor p = permute.contiguous(), io = input_offsets.contiguous(),
+               oo = output_offsets.contiguous();
+  Tensor out = at::empty({output_size}, io.options());
+  MX_CALL(mx_expand_into_jagged_permute(p.data_ptr<int32_t>(), p.numel(), io.data_ptr(),
+                                        io.numel(), oo.data_ptr(), oo.numel(), ib, output_size,
+                                        out.data_ptr(), stream_of(p)));
+  return out;
+}
+
 }  // namespace mx_ops
 
 TORCH_LIBRARY_FRAGMENT(fbgemm, m) {
+  m.def("permute_1D_sparse_data(Tensor permute, Tensor lengths, Tensor values, "
+        "Tensor? weights=None, SymInt? permuted_lengths_sum=None) -> (Tensor, Tensor, Tensor?)");
+  m.def("offsets_range(Tensor offsets, SymInt range_size) -> Tensor");
+  m.def("expand_into_jagged_permute(Tensor permute, Tensor input_offset, Tensor output_offset, "
+        "SymInt output_size) -> Tensor");
   m.def("asynchronous_exclusive_cumsum(Tensor t_in) -> Tensor");
   m.def("asynchronous_inclusive_cumsum(Tensor t_in) -> Tensor");
   m.def("asynchronous_complete_cumsum(Tensor t_in) -> Tensor");
@@ -2058,6 +2105,9 @@ TORCH_LIBRARY_IMPL(fbgemm, CUDA, m) {
   m.impl("asynchronous_inclusive_cumsum", TORCH_FN(mx_ops::inclusive_cumsum));
   m.impl("asynchronous_complete_cumsum", TORCH_FN(mx_ops::complete_cumsum));
   m.impl("permute_2D_sparse_data", TORCH_FN(mx_ops::permute_2D_sparse_data));
+  m.impl("permute_1D_sparse_data", TORCH_FN(mx_ops::permute_1D_sparse_data));
+  m.impl("offsets_range", TORCH_FN(mx_ops::offsets_range));
+  m.impl("expand_into_jagged_permute", TORCH_FN(mx_ops::expand_into_jagged_permute));
   m.impl("FloatToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_to_8bit));
   m.impl("HalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::half_to_8bit));
   m.impl("FloatOrHalfToFused8BitRowwiseQuantized", TORCH_FN(mx_ops::float_or_half_to_8bit));

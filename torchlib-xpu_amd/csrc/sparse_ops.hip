@@ -12,7 +12,13 @@
 //    feature f is input feature permute[f]: permuted_lengths[f, :] =
 //    lengths[permute[f], :], and the indices (and weights) of each bag (f, b)
 //    are the input's bag (permute[f], b), in order.  permute may repeat or
-//    drop features.
+//    drop features.  permute_1D_sparse_data is the same with one bag per
+//    feature (lengths [T]).
+//  * offsets_range(offsets [N], range_size): out[j] = j - offsets[i] for j in
+//    segment i = [offsets[i], offsets[i + 1]) (the last ends at range_size).
+//  * expand_into_jagged_permute(permute [T], input_offsets, output_offsets,
+//    output_size): out[output_offsets[t] + j] = input_offsets[permute[t]] + j
+//    for j below output feature t's length.
 //
 // Design: integer work, HBM-bound.  The scans are reduce-then-scan with no
 // waits between blocks: a block sums its 8192-element tile, one block scans
@@ -216,6 +222,46 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// A 16-lane group per segment writes j - start over its range.
+template <typename I>
+__global__ void __launch_bounds__(256)
+    offsets_range_kernel(const I* __restrict__ offsets, int64_t nseg, int64_t range_size,
+                         I* __restrict__ out) {
+  constexpr int G = 16;
+  const int k = threadIdx.x % G;
+  const int64_t ngrp = static_cast<int64_t>(gridDim.x) * (256 / G);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G; i < nseg;
+       i += ngrp) {
+    int64_t s0 = static_cast<int64_t>(offsets[i]);
+    int64_t s1 = i + 1 < nseg ? static_cast<int64_t>(offsets[i + 1]) : range_size;
+    s0 = s0 < 0 ? 0 : s0;
+    s1 = s1 > range_size ? range_size : s1;
+    for (int64_t j = s0 + k; j < s1; j += G) out[j] = static_cast<I>(j - s0);
+  }
+}
+
+// A 16-lane group per output feature t.
+template <typename I>
+__global__ void __launch_bounds__(256)
+    expand_permute_kernel(const int32_t* __restrict__ permute, const I* __restrict__ in_off,
+                          int64_t in_n, const I* __restrict__ out_off, int64_t T, bool out_has_end,
+                          int64_t output_size, I* __restrict__ out) {
+  constexpr int G = 16;
+  const int k = threadIdx.x % G;
+  const int64_t ngrp = static_cast<int64_t>(gridDim.x) * (256 / G);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G; t < T;
+       t += ngrp) {
+    const int32_t src = permute[t];
+    if (src < 0 || src >= in_n) continue;
+    int64_t d0 = static_cast<int64_t>(out_off[t]);
+    int64_t d1 = out_has_end || t + 1 < T ? static_cast<int64_t>(out_off[t + 1]) : output_size;
+    d0 = d0 < 0 ? 0 : d0;
+    d1 = d1 > output_size ? output_size : d1;
+    const int64_t s0 = static_cast<int64_t>(in_off[src]);
+    for (int64_t j = d0 + k; j < d1; j += G) out[j] = static_cast<I>(s0 + (j - d0));
+  }
+}
+
 int grid_for(int64_t work, int64_t per_block) {
   const int64_t want = ceil_div(work > 0 ? work : 1, per_block);
   const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
@@ -327,6 +373,55 @@ extern "C" int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t
       MX_PERM(int32_t, int32_t);
   }
 #undef MX_PERM
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+extern "C" int mx_offsets_range(const void* offsets, int32_t index_bytes, int64_t nseg,
+                                int64_t range_size, void* out, void* stream) {
+  clear_error();
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "offsets must be int32 or int64");
+  MX_REQUIRE(nseg >= 0 && range_size >= 0, "negative size");
+  if (nseg == 0 || range_size == 0) return MX_OK;
+  MX_REQUIRE(offsets && out, "null pointer argument");
+  auto* s = as_stream(stream);
+  const dim3 gd(static_cast<uint32_t>(grid_for(nseg, 256 / 16)));
+  if (index_bytes == 8)
+    offsets_range_kernel<int64_t><<<gd, 256, 0, s>>>(static_cast<const int64_t*>(offsets), nseg,
+                                                     range_size, static_cast<int64_t*>(out));
+  else
+    offsets_range_kernel<int32_t><<<gd, 256, 0, s>>>(static_cast<const int32_t*>(offsets), nseg,
+                                                     range_size, static_cast<int32_t*>(out));
+  MX_LAUNCH_CHECK();
+  return MX_OK;
+}
+
+extern "C" int mx_expand_into_jagged_permute(const int32_t* permute, int64_t T,
+                                             const void* input_offsets, int64_t input_numel,
+                                             const void* output_offsets, int64_t output_numel,
+                                             int32_t index_bytes, int64_t output_size, void* out,
+                                             void* stream) {
+  clear_error();
+  MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "offsets must be int32 or int64");
+  MX_REQUIRE(T >= 0 && output_size >= 0, "negative size");
+  MX_REQUIRE(output_numel == T || output_numel == T + 1,
+             "output_offsets must have T or T+1 entries (T=%lld, got %lld)", (long long)T,
+             (long long)output_numel);
+  if (T == 0 || output_size == 0) return MX_OK;
+  MX_REQUIRE(permute && input_offsets && output_offsets && out, "null pointer argument");
+  auto* s = as_stream(stream);
+  const dim3 gd(static_cast<uint32_t>(grid_for(T, 256 / 16)));
+  const bool has_end = output_numel == T + 1;
+  if (index_bytes == 8)
+    expand_permute_kernel<int64_t><<<gd, 256, 0, s>>>(
+        permute, static_cast<const int64_t*>(input_offsets), input_numel,
+        static_cast<const int64_t*>(output_offsets), T, has_end, output_size,
+        static_cast<int64_t*>(out));
+  else
+    expand_permute_kernel<int32_t><<<gd, 256, 0, s>>>(
+        permute, static_cast<const int32_t*>(input_offsets), input_numel,
+        static_cast<const int32_t*>(output_offsets), T, has_end, output_size,
+        static_cast<int32_t*>(out));
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
