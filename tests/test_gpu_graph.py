@@ -1,6 +1,7 @@
 """TBE training steps captured in a HIP graph (torch.cuda.CUDAGraph): the
-forward lookup and the fused backward + rowwise-Adagrad update, every
-kernel of both on the caller's stream.  Each replay must equal the same step run eagerly (both paths are atomic-free,
+forward lookup and the fused backward + rowwise-Adagrad update (pooled, and
+PoolingMode NONE with an nbit sequence lookup), every kernel on the caller's
+stream.  Each replay must equal the same step run eagerly (both paths are atomic-free,
 so bit-identical), with eager work and synchronisations between replays."""
 
 import numpy as np
@@ -252,3 +253,71 @@ def test_fp16_stochastic_rounding_graph_replays_draw_fresh_bits(dev):
         torch.cuda.synchronize()
         assert torch.equal(Wg.view(torch.int16), eager[k].view(torch.int16)), \
             f"replay {k} rounded with other bits than the eager step"
+
+
+def test_nobag_training_step_graph_replays_match_eager(dev):
+    """PoolingMode NONE: the nobag forward, the nobag backward (its batch recast
+    as one-position bags on the device) and an nbit nobag lookup, captured
+    together; every replay equals the eager step bit for bit."""
+    print("[case] graph-captured nobag forward + backward + nbit nobag, 4 replays", flush=True)
+    rng = np.random.default_rng(6)
+    D = 64
+    inp = random_tbe(rng, 3, 128, [D] * 3, [400, 3, 900], 20)
+    nW = sum(E * D for E in inp.E)
+    W0 = torch.from_numpy(rng.uniform(-0.5, 0.5, nW).astype(np.float32)).to(dev)
+    grads = [torch.from_numpy(rng.normal(0, 1e-2, (inp.N, D)).astype(np.float32)).to(dev)
+             for _ in range(4)]
+    w_off = torch.from_numpy(weight_offsets(inp)).to(dev)
+    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    m1_off = torch.from_numpy(np.concatenate([[0], np.cumsum(inp.E)[:-1]]).astype(np.int64)).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(inp.T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    # An nbit FP16 copy of the same tables (row_alignment 16: 128-B rows).
+    q = torch.zeros(nW * 2, dtype=torch.uint8, device=dev)
+    tys = torch.full((inp.T,), 1, dtype=torch.uint8, device=dev)
+    D_off = torch.from_numpy(inp.D_offsets).to(dev)
+
+    def make(W, m1, g):
+        def step():
+            q.copy_(W.half().view(torch.uint8))
+            out = torch.ops.fbgemm.split_embedding_nobag_codegen_forward_unweighted_cuda(
+                W, empty, empty, pl, w_off, D, idx, off, e32, empty, 0, False)
+            nb = torch.ops.fbgemm.int_nbit_split_embedding_codegen_lookup_function(
+                q, torch.zeros(0, dtype=torch.uint8, device=dev), pl, w_off * 2, tys, D_off,
+                inp.total_D, 0, 0, 0, D, 0, idx, off, 2, None, 1, None, None, 16, 0, -1, -1)
+            torch.ops.fbgemm.split_embedding_nobag_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+                g, W, empty, empty, pl, w_off, D, hsc, inp.total_hash_size_bits, idx, off, e32, 0,
+                0, False, m1, empty, pl, m1_off, 1e-8, 0.05, 0.0, 0, 0.0)
+            return out, nb
+        return step
+
+    We, me, ge = W0.clone(), torch.zeros(sum(inp.E), device=dev), torch.empty_like(grads[0])
+    eager = make(We, me, ge)
+    ref = []
+    for g in grads:
+        ge.copy_(g)
+        out, nb = eager()
+        ref.append((out.clone(), nb.clone(), We.clone(), me.clone()))
+    torch.cuda.synchronize()
+    Ws, ms, gs = W0.clone(), torch.zeros(sum(inp.E), device=dev), torch.empty_like(grads[0])
+    step = make(Ws, ms, gs)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s, nb_s = step()
+    torch.cuda.synchronize()
+    assert torch.equal(Ws, W0) and not ms.any()
+    for k, g in enumerate(grads):
+        gs.copy_(g)
+        graph.replay()
+        torch.cuda.synchronize()
+        noise = torch.randn(1 << 20, device=dev).sum()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        out_e, nb_e, W_e, m_e = ref[k]
+        assert torch.equal(out_s, out_e), f"replay {k}: nobag output differs"
+        assert torch.equal(nb_s, nb_e), f"replay {k}: nbit nobag output differs"
+        assert torch.equal(ms, m_e), f"replay {k}: momentum differs"
+        assert torch.equal(Ws, W_e), f"replay {k}: weights differ"
