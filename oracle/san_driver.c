@@ -83,6 +83,14 @@ static void free_batch(Batch* b) {
   free(b->indices);
 }
 
+/* Every table of one width: the batch can be a sequence (nobag) lookup. */
+static int32_t uniform_D(const Batch* b) {
+  const int32_t D = b->T > 0 ? b->D_off[1] - b->D_off[0] : 0;
+  for (int32_t t = 1; t < b->T; ++t)
+    if (b->D_off[t + 1] - b->D_off[t] != D) return -1;
+  return D;
+}
+
 static int bits_for(int64_t n) {
   int b = 1;
   while ((int64_t)1 << b < n) ++b;
@@ -157,6 +165,17 @@ static void run_tbe(const Batch* b) {
                                          m1_off, 0.01f, 1e-8f, 0.0f, mode, nb) == 0);
     }
   for (int64_t i = 0; i < nw; ++i) CHECK(isfinite(W[i]));
+  const int32_t Du = uniform_D(b);
+  if (Du > 0) { /* the nobag backward: one gradient row per position */
+    float* gn = (float*)xmalloc(sizeof(float) * n * Du);
+    for (int64_t i = 0; i < b->N * Du; ++i) gn[i] = rnd_unit() * 0.02f - 0.01f;
+    for (int mode = 0; mode < 3; ++mode)
+      CHECK(orc_backward_rowwise_adagrad_nobag(W, w_off, Du, b->T, b->B, hsc, bits, b->indices,
+                                               b->offsets, b->N, gn, m1, m1_off, 0.01f, 1e-8f,
+                                               0.01f, mode, nb) == 0);
+    for (int64_t i = 0; i < nw; ++i) CHECK(isfinite(W[i]));
+    free(gn);
+  }
 
   /* bounds check on a broken copy: repaired offsets are monotone in [0, N] */
   int64_t* idx2 = (int64_t*)xmalloc(sizeof(int64_t) * n);
@@ -245,6 +264,14 @@ static void run_nbit(const Batch* b, const int32_t* tys) {
       CHECK(orc_nbit_forward(W, w_off, tys8, b->D_off, b->T, b->B, b->indices, b->offsets,
                              pooling, iw, 16, f16, out, total_D, 5, 15) == 0);
     }
+  const int32_t Du = uniform_D(b);
+  if (Du > 0) { /* the nobag lookup: one output row per position */
+    void* on = xmalloc(sizeof(float) * (b->N > 0 ? b->N : 1) * Du);
+    for (int kind = 0; kind < 3; ++kind)
+      CHECK(orc_nbit_forward_nobag(W, w_off, tys8, Du, b->T, b->B, b->indices, b->offsets, 16,
+                                   kind, on, 4, 7) == 0);
+    free(on);
+  }
   free(W);
   free(w_off);
   free(tys8);
@@ -288,6 +315,8 @@ int main(void) {
   const int32_t dims5[5] = {8, 16, 24, 64, 256};
   const int32_t tys5[5] = {ORC_FP32, ORC_FP16, ORC_INT8, ORC_INT4, ORC_INT2};
   const int32_t tys5b[5] = {ORC_FP8, ORC_FP16, ORC_INT8, ORC_INT4, ORC_FP8};
+  const int32_t dims3u[3] = {32, 32, 32};
+  const int32_t dims5u[5] = {16, 16, 16, 16, 16};
   for (int rep = 0; rep < 24; ++rep) {
     Batch a = make_batch(3, 17 + 13 * rep, 9 + rep, 20, dims3);
     run_tbe(&a);
@@ -295,6 +324,12 @@ int main(void) {
     Batch c = make_batch(5, 13 + 5 * rep, 7, 25, dims5);
     run_nbit(&c, rep % 2 ? tys5b : tys5);
     free_batch(&c);
+    Batch u = make_batch(3, 11 + 7 * rep, 12, 20, dims3u); /* sequence lookups */
+    run_tbe(&u);
+    free_batch(&u);
+    Batch v = make_batch(5, 9 + 3 * rep, 6, 25, dims5u);
+    run_nbit(&v, rep % 2 ? tys5b : tys5);
+    free_batch(&v);
   }
   /* hfp8: every code decodes to a value that encodes back to the code */
   for (int cfg = 0; cfg < 2; ++cfg) {
