@@ -1635,14 +1635,14 @@ int launch_bwd(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, h
 }
 
 // Full-width instance when every table's D equals the row width of the
-// chosen (G, NCH): with a fixed batch, total_D = T * max_D says so (no D
-// exceeds max_D, and grad_output's rows are D_offsets[T] wide).  Plain
-// instance for SUM pooling without weights or weight decay.
+// chosen (G, NCH): total_D = T * max_D says so (no D exceeds max_D, and the
+// D_offsets sum to total_D: a fixed batch's grad_output width, the recast
+// sequence batch's T * D; a variable batch passes 0).  Plain instance for SUM
+// pooling without weights or weight decay.
 template <typename I, typename WT, int G, int NCH>
 int launch_width(const BwdArgs& a, SortWs& ws, uint32_t* chunk_start, int64_t N, hipStream_t s) {
   constexpr int kWidth = G * NCH * 4;
-  const bool full = a.B_off == nullptr && a.max_D == kWidth &&
-                    a.total_D == static_cast<int64_t>(a.T) * kWidth;
+  const bool full = a.max_D == kWidth && a.total_D == static_cast<int64_t>(a.T) * kWidth;
   const bool plain = a.pooling == MX_POOL_SUM && a.iw_sorted == nullptr && a.B_off == nullptr &&
                      a.wd_mode == 0;
   if (full)
@@ -2103,9 +2103,11 @@ extern "C" int mx_tbe_backward_rowwise_adagrad_nobag(
   auto* s = as_stream(stream);
   if (int rc = launch_nobag_layout(offsets, index_bytes, T, B, N, D, nb, nw, true, s)) return rc;
   const Layout lay{N, nw.B_offsets, nw.row_out, nw.b_t_map};
+  // total_D = T * D: every table is D wide (the full-width instances apply).
   return backward_impl(weights, weights_ty, weights_offsets, nw.D_offsets, T, N, nb, lay, D,
                        hash_size_cumsum, total_hash_size_bits, indices, nw.bag_offsets,
-                       index_bytes, N, MX_POOL_SUM, nullptr, grad_output, 0, momentum1,
+                       index_bytes, N, MX_POOL_SUM, nullptr, grad_output,
+                       static_cast<int64_t>(T) * D, momentum1,
                        momentum1_offsets, learning_rate, eps, weight_decay, weight_decay_mode,
                        stochastic_rounding, rng, workspace, base, stream);
 }
