@@ -71,9 +71,10 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="workload; 2 (default) is the headline")
-    ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check"],
-                    help="config 2 only: time bounds_check_indices (WARNING) on the batch "
-                         "instead of the lookup")
+    ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check", "nobag"],
+                    help="bounds-check (config 2): time bounds_check_indices (WARNING) on the "
+                         "batch instead of the lookup; nobag (config 2 / 3): the PoolingMode NONE "
+                         "forward / backward on the same batch (not the headline)")
     ap.add_argument("--regime", default="all", choices=["all", "steps", "warm", "cold"])
     ap.add_argument("--cold-launches", type=int, default=25,
                     help="flushes (groups of --cold-copies launches) whose median launch "
@@ -503,6 +504,63 @@ def wl_bounds_check(args, dev) -> Workload:
         cold_steps=cold)
 
 
+def wl_nobag_forward(args, dev) -> Workload:
+    """PoolingMode NONE forward on the config-2 batch: every position's row
+    copied to its own output row ([N, 128] fp32)."""
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 2 batch")
+    inp = bench_inputs.config2()
+    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_nobag_codegen_forward_unweighted_cuda
+
+    def make_step(Wc, ic, oc):
+        return lambda: op(Wc, empty, empty, pl, w_off, D, ic, oc, e32, empty, 0, False)
+
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    step = make_step(W, idx, off)
+    cold = [make_step(W.clone(), idx.clone(), off.clone()) for _ in range(args.cold_copies)]
+    alg = inp.N * (D * 4 + 8 + D * 4)
+    t_of = np.repeat(np.arange(T * B) // B, np.diff(inp.offsets))
+    uniq = int(np.unique(t_of * E + inp.indices).size)
+    compulsory = uniq * D * 4 + inp.N * 8 + (T * B + 1) * 8 + inp.N * D * 4
+
+    def cpu():
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        Wh = W.cpu().numpy()
+        w_off_h = (np.arange(T) * E * D).astype(np.int64)
+        fn = lambda: orc.tbe_forward_nobag(Wh, w_off_h, D, B, inp.indices, inp.offsets)  # noqa: E731
+        log("CPU baseline: numpy gather of the nobag oracle, 1 process")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        return cpu_record(inp.N / med, "lookups/s", 1, "port",
+                          f"full config-2 batch (N={inp.N}), median of {runs} runs; the "
+                          f"oracle's numpy gather (one process)")
+
+    return Workload(
+        metric="TBE nobag fwd lookups/sec, 1 MI355X", unit="lookups/s", steps=[step],
+        units=[inp.N], alg_bytes=[alg], dtype="fp32",
+        config={"workload": "config2 batch, PoolingMode NONE forward: out [N, 128] fp32",
+                "T": T, "E": E, "D": D, "B": B, "N": inp.N},
+        kernel="tbe_fwd_nobag_kernel", profile="tbe_fwd_nobag_config2", cpu=cpu,
+        cold_steps=cold, roof_bytes=compulsory,
+        roof_bytes_kind=("compulsory bytes: distinct rows once (D*4) + indices + offsets + "
+                         "one output row (D*4) per position"),
+        extra=dict(compulsory=dict(bytes=compulsory, unique_rows=uniq)))
+
+
 # -- config 3 ----------------------------------------------------------------
 
 
@@ -586,6 +644,70 @@ def wl_backward(args, dev) -> Workload:
                 "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
         kernel="whole backward (transpose + segment reduce + update)",
         profile="tbe_bwd_config3", cpu=cpu, cold_steps=cold)
+
+
+def wl_nobag_backward(args, dev) -> Workload:
+    """PoolingMode NONE backward + exact rowwise Adagrad on the config-3
+    batch: one gradient row per position ([N, 128] fp32)."""
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 3 batch")
+    inp = bench_inputs.config2()
+    T, E, D, B = inp.T, inp.E[0], inp.D[0], inp.B
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    W = torch.empty(T * E * D, device=dev).uniform_(-0.01, 0.01, generator=g)
+    m1 = torch.zeros(T * E, device=dev)
+    grad = torch.randn((inp.N, D), generator=g, device=dev) * 1e-2
+    w_off = torch.arange(T, device=dev, dtype=torch.int64) * (E * D)
+    m_off = torch.arange(T, device=dev, dtype=torch.int64) * E
+    hsc = torch.from_numpy(inp.hash_size_cumsum).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    e32 = torch.zeros(0, dtype=torch.int32, device=dev)
+    op = torch.ops.fbgemm.split_embedding_nobag_backward_codegen_rowwise_adagrad_unweighted_exact_cuda
+
+    def make_step(Wc, mc, gc, ic, oc):
+        return lambda: op(gc, Wc, empty, empty, pl, w_off, D, hsc, inp.total_hash_size_bits, ic,
+                          oc, e32, 0, 0, False, mc, empty, pl, m_off, 1e-8, 0.01, 0.0, 0, 0.0)
+
+    idx = torch.from_numpy(inp.indices).to(dev)
+    off = torch.from_numpy(inp.offsets).to(dev)
+    step = make_step(W, m1, grad, idx, off)
+    cold = [make_step(W.clone(), m1.clone(), grad.clone(), idx.clone(), off.clone())
+            for _ in range(args.cold_copies)]
+    U = int(np.unique(inp.hash_size_cumsum[np.repeat(np.arange(T), np.diff(inp.offsets[::B]))]
+                      + inp.indices).size)
+    alg = inp.N * 8 + (T * B + 1) * 8 + inp.N * D * 4 + U * (2 * D * 4 + 2 * 4)
+
+    def cpu():
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        Wh = W.cpu().numpy()
+        gh = grad.cpu().numpy()
+        w_off_h = (np.arange(T) * E * D).astype(np.int64)
+        m_off_h = (np.arange(T) * E).astype(np.int64)
+        m1h = np.zeros(T * E, dtype=np.float32)
+        fn = lambda: orc.backward_rowwise_adagrad_nobag(  # noqa: E731
+            Wh, w_off_h, D, B, inp.hash_size_cumsum, inp.total_hash_size_bits, inp.indices,
+            inp.offsets, gh, m1h, m_off_h, 0.01, 1e-8)
+        log("CPU baseline: C restatement of the nobag backward, 1 thread")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        return cpu_record(inp.N / med, "lookups/s", 1, "port",
+                          f"full config-3 batch (N={inp.N}), median of {runs} runs; the "
+                          f"oracle's C restatement, one thread, on copies of the weights")
+
+    return Workload(
+        metric="TBE nobag backward + exact rowwise Adagrad lookups/sec, 1 MI355X",
+        unit="lookups/s", steps=[step], units=[inp.N], alg_bytes=[alg], dtype="fp32",
+        config={"workload": "config3 batch, PoolingMode NONE backward: grad_output [N, 128]",
+                "T": T, "E": E, "D": D, "B": B, "N": inp.N, "unique_rows": U},
+        kernel="whole nobag backward (layout + transpose + segment reduce + update)",
+        profile="tbe_bwd_nobag_config3", cpu=cpu, cold_steps=cold)
 
 
 # -- configs 4 and 5 ---------------------------------------------------------
@@ -725,6 +847,10 @@ def measure(args, config: int, dev) -> dict:
         wl = wl_jagged(args, dev)
     elif config == 2 and args.op == "bounds-check":
         wl = wl_bounds_check(args, dev)
+    elif config == 2 and args.op == "nobag":
+        wl = wl_nobag_forward(args, dev)
+    elif config == 3 and args.op == "nobag":
+        wl = wl_nobag_backward(args, dev)
     elif config == 2:
         wl = wl_tbe_forward(args, dev)
     elif config == 3:
