@@ -506,12 +506,14 @@ int mx_permute_2d_lengths(const int32_t* permute, int64_t T_out, const void* len
  * output_offsets[f*B + b] (the complete cumsum of the permuted lengths), is a
  * copy of the input bag (permute[f], b) at input_offsets[permute[f]*B + b]
  * (the complete cumsum of the lengths); weights (fp32, may be NULL) travel
- * with their indices.  out_len = output_offsets[T_out*B]. */
+ * with their indices.  in_len = the number of indices (and weights), out_len
+ * = output_offsets[T_out*B]; lengths that disagree with either stop the copy
+ * of their bag at the array's end. */
 int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t T, int64_t B,
                        const void* input_offsets, const void* output_offsets,
                        int32_t offset_bytes, const void* indices, int32_t index_bytes,
-                       const float* weights, int64_t out_len, void* permuted_indices,
-                       float* permuted_weights, void* stream);
+                       int64_t in_len, const float* weights, int64_t out_len,
+                       void* permuted_indices, float* permuted_weights, void* stream);
 
 /* Serves fbgemm::offsets_range: out[j] = j - offsets[i] for j in segment i =
  * [offsets[i], offsets[i + 1]) (the last segment ends at range_size); out

@@ -1851,7 +1851,7 @@ std::tuple<Tensor, Tensor, std::optional<Tensor>> permute_2D_sparse_data(
   }
   MX_CALL(mx_permute_2d_data(perm.data_ptr<int32_t>(), Tp, static_cast<int32_t>(T), B,
                              in_off.data_ptr(), out_off.data_ptr(), lb, idx.data_ptr(), ib,
-                             wc.defined() ? wc.data_ptr<float>() : nullptr, out_len,
+                             idx.numel(), wc.defined() ? wc.data_ptr<float>() : nullptr, out_len,
                              pidx.data_ptr(), pw.has_value() ? pw->data_ptr<float>() : nullptr,
                              stream_of(len)));
   return {plen, pidx, pw};

@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(256)
     permute_data_kernel(const int32_t* __restrict__ permute, const L* __restrict__ in_off,
                         const L* __restrict__ out_off, int32_t T, int64_t B, int64_t Tp,
                         const I* __restrict__ indices, const W* __restrict__ weights,
-                        I* __restrict__ out_indices, W* __restrict__ out_weights,
+                        int64_t in_len, I* __restrict__ out_indices, W* __restrict__ out_weights,
                         int64_t out_len) {
   constexpr int G = 16;
   const int k = threadIdx.x % G;
@@ -215,7 +215,9 @@ __global__ void __launch_bounds__(256)
     const int64_t d0 = static_cast<int64_t>(out_off[bag]);
     const int64_t len = static_cast<int64_t>(out_off[bag + 1]) - d0;
     for (int64_t j = k; j < len; j += G) {
-      if (d0 + j >= out_len) break;
+      // Lengths that disagree with the index count or the given output size
+      // stop the copy instead of reading or writing past either array.
+      if (d0 + j >= out_len || s0 + j >= in_len) break;
       out_indices[d0 + j] = indices[s0 + j];
       if (weights) out_weights[d0 + j] = weights[s0 + j];
     }
@@ -344,12 +346,13 @@ extern "C" int mx_permute_2d_lengths(const int32_t* permute, int64_t T_out, cons
 extern "C" int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t T, int64_t B,
                                   const void* input_offsets, const void* output_offsets,
                                   int32_t offset_bytes, const void* indices, int32_t index_bytes,
-                                  const float* weights, int64_t out_len, void* permuted_indices,
-                                  float* permuted_weights, void* stream) {
+                                  int64_t in_len, const float* weights, int64_t out_len,
+                                  void* permuted_indices, float* permuted_weights,
+                                  void* stream) {
   clear_error();
   MX_REQUIRE(offset_bytes == 4 || offset_bytes == 8, "offsets must be int32 or int64");
   MX_REQUIRE(index_bytes == 4 || index_bytes == 8, "indices must be int32 or int64");
-  MX_REQUIRE(T >= 0 && B >= 0 && T_out >= 0 && out_len >= 0, "negative size");
+  MX_REQUIRE(T >= 0 && B >= 0 && T_out >= 0 && out_len >= 0 && in_len >= 0, "negative size");
   MX_REQUIRE(!weights == !permuted_weights, "weights and permuted_weights go together");
   if (T_out * B == 0 || out_len == 0) return MX_OK;
   MX_REQUIRE(permute && input_offsets && output_offsets && indices && permuted_indices,
@@ -359,8 +362,8 @@ extern "C" int mx_permute_2d_data(const int32_t* permute, int64_t T_out, int32_t
 #define MX_PERM(L, I)                                                                       \
   permute_data_kernel<L, I, float><<<gd, 256, 0, s>>>(                                      \
       permute, static_cast<const L*>(input_offsets), static_cast<const L*>(output_offsets), \
-      T, B, T_out, static_cast<const I*>(indices), weights, static_cast<I*>(permuted_indices), \
-      permuted_weights, out_len)
+      T, B, T_out, static_cast<const I*>(indices), weights, in_len,                          \
+      static_cast<I*>(permuted_indices), permuted_weights, out_len)
   if (offset_bytes == 8) {
     if (index_bytes == 8)
       MX_PERM(int64_t, int64_t);
