@@ -7,7 +7,9 @@ features of up to 200,000 rows; bit-exact over the whole run layout) and one
 backward case (unweighted with any run lengths, under the reordering bound of
 adagrad_bounds.py; or weighted, L2 or decoupled weight decay on rows of at
 least 200, at rtol 1e-5).  A quarter of the cases draw their indices from
-three rows per table, so long runs and repeated rows are common."""
+three rows per table, so long runs and repeated rows are common.  A second
+sweep draws sequence lookups (PoolingMode NONE: forward, nbit, backward),
+cumsums and feature permutes."""
 
 import numpy as np
 import pytest
@@ -97,3 +99,82 @@ def test_random_sweep(dev, seed):
         _forward(dev, rng, i)
         _transpose(dev, rng, i)
         _backward(dev, rng, i, seed)
+
+
+SEQ_ROUNDS = 10
+
+
+def _sequence_and_sparse(dev, rng, i):
+    """One round: a sequence-lookup forward, an nbit sequence lookup, a
+    sequence-lookup backward, a cumsum and a feature permute, each against the
+    oracle (bit-exact; the backward at rtol 1e-5, 1e-4 on momentum when long
+    runs reorder the sums)."""
+    from nbit_helpers import build_weights
+    from test_gpu_nobag import _backward_nobag, _forward_nobag, _nbit_nobag
+
+    T = int(rng.integers(1, 6))
+    B = int(rng.integers(1, 200))
+    D = int(rng.choice([4, 8, 16, 36, 64, 128, 256, 512]))
+    rows = [int(rng.integers(1, 3000)) for _ in range(T)]
+    dup = bool(rng.integers(0, 3) == 0)
+    itype = torch.int32 if rng.integers(0, 2) else torch.int64
+    f16 = bool(rng.integers(0, 2))
+    print(f"[case] sweep seq {i}: T={T} B={B} D={D} rows={rows} dup={dup} {itype} f16={f16}",
+          flush=True)
+    inp = random_tbe(rng, T, B, [D] * T, rows, int(rng.integers(0, 40)), dup_heavy=dup)
+    W = rng.uniform(-0.5, 0.5, size=sum(E * D for E in rows)).astype(np.float32)
+    Wd = torch.from_numpy(W).to(dev).to(torch.float16 if f16 else torch.float32)
+    got = _forward_nobag(dev, Wd, inp, D, 0, itype)
+    exp = orc.tbe_forward_nobag(Wd.cpu().numpy(), weight_offsets(inp), D, B, inp.indices,
+                                inp.offsets)
+    np.testing.assert_array_equal(got.cpu().numpy(), exp)
+
+    Dq = int(rng.choice([8, 16, 32, 64, 128, 256]))
+    tys = [int(rng.choice([orc.INT8, orc.INT4, orc.INT2, orc.FP16, orc.FP32, orc.FP8]))
+           for _ in range(T)]
+    inq = random_tbe(rng, T, B, [Dq] * T, rows, int(rng.integers(0, 30)))
+    buf, w_off = build_weights(rng, tys, [Dq] * T, rows)
+    out_dtype = int(rng.choice([0, 1, 5]))
+    kind = {0: 0, 1: 1, 5: 2}[out_dtype]
+    g = _nbit_nobag(dev, buf, w_off, tys, Dq, inq, out_dtype, itype).cpu()
+    e = orc.nbit_forward_nobag(buf, w_off, tys, Dq, B, inq.indices, inq.offsets, out_kind=kind)
+    g = g.view(torch.int16).numpy().view(np.uint16) if kind else g.numpy().view(np.uint32)
+    np.testing.assert_array_equal(g, e.view(np.uint32) if kind == 0 else e.view(np.uint16))
+
+    m1 = rng.uniform(0, 0.01, size=sum(rows)).astype(np.float32)
+    m1_off = np.concatenate([[0], np.cumsum(rows)[:-1]]).astype(np.int64)
+    grad = rng.normal(0, 0.01, size=(inp.N, D)).astype(np.float32)
+    Wb, mb = torch.from_numpy(W).to(dev), torch.from_numpy(m1).to(dev)
+    _backward_nobag(dev, Wb, mb, m1_off, inp, D, grad, 0.05, 1e-8, 0.0, 0, itype)
+    W_exp, m_exp = orc.backward_rowwise_adagrad_nobag(
+        W, weight_offsets(inp), D, B, inp.hash_size_cumsum, inp.total_hash_size_bits,
+        inp.indices, inp.offsets, grad, m1, m1_off, 0.05, 1e-8)
+    np.testing.assert_allclose(mb.cpu().numpy(), m_exp, rtol=1e-4 if dup else 1e-5, atol=0)
+    np.testing.assert_allclose(Wb.cpu().numpy(), W_exp, rtol=1e-5, atol=1e-6 if dup else 1e-7)
+
+    n = int(rng.choice([0, 1, 100, 8191, 8193, 50_000, 400_000]))
+    ck = int(rng.integers(0, 3))
+    cdt = np.int32 if rng.integers(0, 2) else np.int64
+    x = rng.integers(-5, 60, n).astype(cdt)
+    op = ("asynchronous_exclusive_cumsum", "asynchronous_inclusive_cumsum",
+          "asynchronous_complete_cumsum")[ck]
+    np.testing.assert_array_equal(getattr(torch.ops.fbgemm, op)(torch.from_numpy(x).to(dev)).cpu().numpy(),
+                                  orc.cumsum(x, ck))
+
+    Tp = int(rng.integers(1, 10))
+    lengths = rng.integers(0, 20, (T, B))
+    idx = rng.integers(0, 10**6, int(lengths.sum()))
+    permute = rng.integers(0, T, Tp).astype(np.int32)
+    el, ei, _ = orc.permute_2d_sparse_data(permute, lengths, idx)
+    pl, pi, _ = torch.ops.fbgemm.permute_2D_sparse_data(
+        torch.from_numpy(permute).to(dev), torch.from_numpy(lengths).to(dev),
+        torch.from_numpy(idx).to(dev, itype))
+    np.testing.assert_array_equal(pl.cpu().numpy(), el)
+    np.testing.assert_array_equal(pi.cpu().numpy(), ei)
+
+
+@pytest.mark.parametrize("seed", [11, 22])
+def test_random_sweep_sequence_and_sparse(dev, seed):
+    rng = np.random.default_rng(seed)
+    for i in range(SEQ_ROUNDS):
+        _sequence_and_sparse(dev, rng, i)
