@@ -122,6 +122,7 @@ struct SegSort {
   uint32_t* fhist;       // [T][kHistCopies][kMaxPasses][kRadix] per-segment digit counts (zeroed), a pass's row
   unsigned int* bad;     // zeroed; nonzero (kSegKeys or kSegTables): sort globally
   int32_t T;             // 0: no segments
+  const int32_t* B_off;  // [T + 1] first bag of each feature (variable batch); null: t * B
 };
 
 // ---- linearize ------------------------------------------------------------
@@ -146,6 +147,7 @@ __global__ void __launch_bounds__(256)
   __shared__ int s_tables_ok;  // hsc does not decrease and fits the bits (per-segment counts)
   __shared__ int s_ngroups;    // segments: runs of features with equal hsc (one table)
   __shared__ int64_t s_hsc[kSegMaxT + 1];  // hsc of a batch of at most kSegMaxT features
+  __shared__ int32_t s_boff[kSegMaxT + 1]; // first bag of each feature (variable batch)
   __shared__ int64_t s_gend[kSegMaxT];     // feature t's table end: hsc of the next segment
   __shared__ int s_gid[kSegMaxT];          // feature t's segment
   __shared__ int s_gfirst[kSegMaxT + 1];   // segment g's first feature; [S] = T
@@ -170,6 +172,7 @@ __global__ void __launch_bounds__(256)
   // Wave 0 loads hsc (at most kSegMaxT + 1 entries) now and stages it in LDS
   // after the searches, when it has arrived.
   const int64_t lane_hsc = seg.T > 0 && w == 0 && lane <= seg.T ? hsc[lane] : 0;
+  const int32_t lane_boff = seg.B_off && w == 0 && lane <= seg.T ? seg.B_off[lane] : 0;
   // Last bag with offsets[bag] <= target (0 when none), for the block's first
   // (half 0) and last (half 1) position: 128-ary searches, one probe per
   // thread and round, so ceil(log128(nbags)) dependent loads instead of
@@ -210,7 +213,10 @@ __global__ void __launch_bounds__(256)
   if (seg.T > 0 && w == 0) {  // hsc into LDS; segments; does hsc not decrease?
     const int64_t next = __shfl(lane_hsc, lane + 1 < 64 ? lane + 1 : 63, 64);
     const int64_t prev = __shfl(lane_hsc, lane > 0 ? lane - 1 : 0, 64);
-    if (lane <= seg.T) s_hsc[lane] = lane_hsc;
+    if (lane <= seg.T) {
+      s_hsc[lane] = lane_hsc;
+      s_boff[lane] = lane_boff;
+    }
     // In-range keys must also fit the sorted bits (a sort over fewer bits
     // orders keys by their low bits, across features).
     const bool fits = lane != seg.T || bits >= 62 || lane_hsc <= (int64_t(1) << bits);
@@ -241,7 +247,14 @@ __global__ void __launch_bounds__(256)
   // known after the next barrier, which also publishes s_hsc and s_tables_ok.
   for (int i = threadIdx.x; i < 2 * kMaxPasses * kRadix; i += 256) (&hf[0][0][0])[i] = 0u;
   for (int i = threadIdx.x; i < kMaxPasses * kRadix; i += 256) (&h[0][0])[i] = 0u;
-  const int64_t t_lo = seg.T > 0 ? blo / B : 0;  // the block's first feature
+  // The block's first feature: its first bag's (checked below for a variable
+  // batch, whose bags need not match a feature's B_off range).
+  int64_t t_lo = 0;
+  if (seg.T > 0) {
+    t_lo = seg.B_off ? (nb >= 32 ? 0 : static_cast<int64_t>(static_cast<uint32_t>(b_t_map[blo]) >> nb))
+                     : blo / B;
+    if (t_lo >= seg.T) t_lo = seg.T - 1;
+  }
   if (threadIdx.x == 0) s_bad = 0;
   // Bag of every position without a search when the block spans few bags:
   // each non-empty bag marks its first position, and position l's bag is the
@@ -318,6 +331,12 @@ __global__ void __launch_bounds__(256)
         const int64_t b = bag - t * B;
         info = (nb >= 32 ? 0u : (static_cast<uint32_t>(t) << nb)) | static_cast<uint32_t>(b);
       }
+      // A variable batch's segments take their positions from B_off, so each
+      // bag must lie in its own feature's range of bags; else the sort is global.
+      if (seg.B_off && (t >= seg.T || bag < s_boff[t] || bag >= s_boff[t + 1])) {
+        s_bad = 1;
+        if (t >= seg.T) t = seg.T - 1;  // in-bounds LDS reads
+      }
       const int64_t key = (seg.T > 0 ? s_hsc[t] : hsc[t]) + static_cast<int64_t>(idx[it]);
       if (linear_out) linear_out[l] = key;
       const uint32_t k32 = static_cast<uint32_t>(key);
@@ -363,8 +382,10 @@ __global__ void __launch_bounds__(256)
         // repeat the end, so no tile falls in them.  The positions must not
         // decrease for the segments to be in key order (hsc does not: checked).
         const int T = seg.T, S = s_ngroups;
-        const int64_t fp =
-            lane <= S ? static_cast<int64_t>(offsets[static_cast<int64_t>(s_gfirst[lane]) * B]) : N;
+        int64_t fbag = seg.B_off ? static_cast<int64_t>(s_boff[s_gfirst[lane < S ? lane : S]])
+                                 : static_cast<int64_t>(s_gfirst[lane < S ? lane : S]) * B;
+        fbag = fbag < 0 ? 0 : (fbag > nbags ? nbags : fbag);  // a bad B_off fails the checks below
+        const int64_t fp = lane <= S ? static_cast<int64_t>(offsets[fbag]) : N;
         const int64_t fnext = __shfl(fp, lane + 1 < 64 ? lane + 1 : 63, 64);
         const uint32_t nt = lane < S ? static_cast<uint32_t>(ceil_div(fnext - fp, kSweepTile)) : 0u;
         const uint32_t incl = wave_incl_scan<SumOp>(nt);
@@ -994,7 +1015,7 @@ ZeroedRegion* stream_region(hipStream_t s) {
 // region for the early words (held locked by the caller, whose last kernel
 // clears w.early_words of it), or null: the workspace's, cleared here.
 int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
-                  const int32_t* b_t_map, int32_t bits, int32_t nb, const void* indices,
+                  const int32_t* b_t_map, const int32_t* B_off, int32_t bits, int32_t nb, const void* indices,
                   const void* offsets, int32_t index_bytes, int64_t N, const float* iw,
                   const TransposeOut& o, SortWs& w, hipStream_t s, ZeroedRegion* zr) {
   // With per-sample weights the weights travel with the keys as a second payload.
@@ -1009,10 +1030,11 @@ int run_transpose(const int64_t* hsc, int32_t T, int64_t B, int64_t nbags,
     w.ghist = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.ghist) + d);
     w.fhist = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(w.fhist) + d);
   }
-  // Segments (one per feature) for a fixed batch of at most kSegMaxT features.
+  // Segments (one per feature) for a batch of at most kSegMaxT features: a
+  // fixed batch, or a variable one whose features' first bags are given.
   SegSort seg{};
-  if (b_t_map == nullptr && T >= 1 && T <= kSegMaxT && passes > 0)
-    seg = SegSort{w.fpos, w.tprefix, w.fhist, w.seg_bad, T};
+  if ((b_t_map == nullptr || B_off != nullptr) && T >= 1 && T <= kSegMaxT && passes > 0)
+    seg = SegSort{w.fpos, w.tprefix, w.fhist, w.seg_bad, T, b_t_map ? B_off : nullptr};
   w.early_words = early_zeroed_words(w, seg.T);
   if (zr == nullptr || zr->dirty) {  // the early words start at zero (a dirty region: all of them)
     const int64_t words = zr ? static_cast<int64_t>(kEarlyBytes / 8) : w.early_words;
@@ -1770,7 +1792,8 @@ int transpose_impl(const int64_t* hash_size_cumsum, int32_t T, int64_t B, const 
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", w.bytes);
   TransposeOut o{linear_indices, sorted_linear_indices, infos_sorted, sorted_linear_indices_run,
                  run_lengths, num_runs, cumulative_run_lengths, nullptr};
-  return run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map, total_hash_size_bits,
+  return run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map, lay.B_offsets,
+                       total_hash_size_bits,
                        info_B_num_bits, indices, offsets, index_bytes, N, nullptr, o, w, s,
                        nullptr);
 }
@@ -1806,7 +1829,7 @@ int backward_impl(void* weights, int32_t weights_ty, const int64_t* weights_offs
   ZeroedRegion* zr = stream_region(s);
   std::unique_lock<std::mutex> zr_lock;
   if (zr) zr_lock = std::unique_lock<std::mutex>(zr->mu);
-  if (int rc = run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map,
+  if (int rc = run_transpose(hash_size_cumsum, T, B, lay.nbags, lay.b_t_map, lay.B_offsets,
                              total_hash_size_bits, nb, indices, offsets, index_bytes, N,
                              indice_weights, o, w.sort, s, zr))
     return rc;
@@ -2052,12 +2075,12 @@ int launch_nobag_layout(const void* offsets, int32_t index_bytes, int32_t T, int
     nobag_layout_kernel<int64_t><<<gd, 256, 0, s>>>(
         static_cast<const int64_t*>(offsets), T, B, N, D, nb,
         static_cast<int64_t*>(w.bag_offsets), w.b_t_map, backward ? w.row_out : nullptr,
-        backward ? w.B_offsets : nullptr, backward ? w.D_offsets : nullptr);
+        w.B_offsets, backward ? w.D_offsets : nullptr);
   else
     nobag_layout_kernel<int32_t><<<gd, 256, 0, s>>>(
         static_cast<const int32_t*>(offsets), T, B, N, D, nb,
         static_cast<int32_t*>(w.bag_offsets), w.b_t_map, backward ? w.row_out : nullptr,
-        backward ? w.B_offsets : nullptr, backward ? w.D_offsets : nullptr);
+        w.B_offsets, backward ? w.D_offsets : nullptr);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
@@ -2145,7 +2168,7 @@ extern "C" int mx_tbe_transpose_embedding_input_nobag(
     return set_error(MX_EWORKSPACE, "workspace of %zu bytes needed", nw.bytes);
   auto* s = as_stream(stream);
   if (int rc = launch_nobag_layout(offsets, index_bytes, T, B, N, 4, nb, nw, false, s)) return rc;
-  const Layout lay{N, nullptr, nullptr, nw.b_t_map};
+  const Layout lay{N, nw.B_offsets, nullptr, nw.b_t_map};  // B_offsets: per-feature sort segments
   if (int rc = transpose_impl(hash_size_cumsum, T, 0, lay, total_hash_size_bits, nb, indices,
                               nw.bag_offsets, index_bytes, N, linear_indices,
                               sorted_linear_indices, nw.infos, sorted_linear_indices_run,
