@@ -100,8 +100,9 @@ __device__ __forceinline__ uint32_t digit_mask(int bits, int p) {
 
 // ---- segments -------------------------------------------------------------
 
-// The sort's segments, one per feature of a fixed batch with at most kSegMaxT
-// features, or per run of consecutive features with equal hsc (features that
+// The sort's segments, one per feature of a batch with at most kSegMaxT
+// features (a fixed batch, or a variable one whose B_off gives each feature's
+// first bag), or per run of consecutive features with equal hsc (features that
 // share one table).  When hsc does not decrease, hsc[T] <= 2^bits and every
 // key of a segment lies in [its hsc, the next segment's hsc), all keys of a
 // segment precede those of the next: sorting each segment's positions on its
