@@ -277,3 +277,66 @@ def test_inference_module_nobag(dev, out):
     g = got.cpu()
     g = g.view(torch.int16).numpy().view(np.uint16) if kind else g.numpy().view(np.uint32)
     np.testing.assert_array_equal(g, exp.view(np.uint32) if kind == 0 else exp.view(np.uint16))
+
+
+@pytest.mark.parametrize("layout", ["empty_first", "empty_middle", "empty_last", "shared_table"])
+def test_nobag_sort_segments(dev, layout):
+    """The recast batch sorts in per-feature segments: whole features without
+    positions (first, middle, last) and two features sharing one table (equal
+    hash_size_cumsum entries: one segment), each feature over several
+    3072-key sort tiles; backward and transpose against the oracle."""
+    print(f"[case] nobag sort segments {layout}", flush=True)
+    seed = {"empty_first": 1, "empty_middle": 2, "empty_last": 3, "shared_table": 4}[layout]
+    rng = np.random.default_rng(700 + seed)
+    T, B, D = 4, 1500, 64
+    rows = [300, 400, 400, 60]
+    lengths = rng.integers(0, 11, size=(T, B))
+    lengths[rng.random((T, B)) < 0.2] = 0
+    if layout != "shared_table":
+        lengths[{"empty_first": 0, "empty_middle": 2, "empty_last": 3}[layout]] = 0
+    offsets = bench_inputs.offsets_from_lengths(lengths.reshape(-1))
+    indices = np.concatenate([rng.integers(0, rows[t], int(lengths[t].sum())) for t in range(T)])
+    if layout == "shared_table":  # features 1 and 2 look up the same 400-row table
+        hsc = np.array([0, 300, 300, 700, 760], np.int64)
+        w_off = np.array([0, 300 * D, 300 * D, 700 * D], np.int64)
+        m1_off = np.array([0, 300, 300, 700], np.int64)
+        n_rows = 760
+    else:
+        hsc = bench_inputs.offsets_from_lengths(np.asarray(rows, np.int64))
+        w_off = hsc[:-1] * D
+        m1_off = hsc[:-1].copy()
+        n_rows = int(hsc[-1])
+    bits = max(1, int(hsc[-1] - 1).bit_length())
+    N = indices.size
+    W = rng.uniform(-0.5, 0.5, size=n_rows * D).astype(np.float32)
+    m1 = rng.uniform(0, 0.01, size=n_rows).astype(np.float32)
+    grad = rng.normal(0, 0.01, size=(N, D)).astype(np.float32)
+    lr, eps = 0.05, 1e-8
+    Wd, m1d = torch.from_numpy(W).to(dev), torch.from_numpy(m1).to(dev)
+    empty = torch.zeros(0, device=dev)
+    pl = torch.zeros(T, dtype=torch.int32, device=dev)
+    hsc_d = torch.from_numpy(hsc).to(dev)
+    idx_d, off_d = torch.from_numpy(indices).to(dev), torch.from_numpy(offsets).to(dev)
+    torch.ops.fbgemm.split_embedding_nobag_backward_codegen_rowwise_adagrad_unweighted_exact_cuda(
+        torch.from_numpy(grad).to(dev), Wd, empty, empty, pl, torch.from_numpy(w_off).to(dev),
+        D, hsc_d, bits, idx_d, off_d, torch.zeros(0, dtype=torch.int32, device=dev), 0, 0,
+        False, m1d, empty, pl, torch.from_numpy(m1_off).to(dev), eps, lr, 0.0, 0, 0.0)
+    W_exp, m_exp = orc.backward_rowwise_adagrad_nobag(
+        W, w_off, D, B, hsc, bits, indices, offsets, grad, m1, m1_off, lr, eps)
+    Wg, mg = Wd.cpu().numpy(), m1d.cpu().numpy()
+    # Runs past 24 occurrences sum in 32-row chunks: another association of the terms.
+    np.testing.assert_allclose(mg, m_exp, rtol=1e-4, atol=0)
+    np.testing.assert_allclose(Wg, W_exp, rtol=RTOL, atol=1e-6)
+    untouched = W_exp == W
+    assert np.array_equal(Wg[untouched], W[untouched])
+    out = torch.ops.fbgemm.transpose_embedding_input(hsc_d, bits, idx_d, off_d, True)
+    linear, srt, infos, run, lens, num_runs, cum = [o.cpu().numpy() for o in out]
+    exp = orc.transpose_embedding_input_nobag(hsc, B, bits, indices, offsets)
+    r = int(num_runs[0])
+    assert r == exp["num_runs"]
+    np.testing.assert_array_equal(linear, exp["linear_indices"])
+    np.testing.assert_array_equal(srt, exp["sorted_linear_indices"])
+    np.testing.assert_array_equal(infos, exp["infos_sorted"])
+    np.testing.assert_array_equal(run[:r], exp["run"])
+    np.testing.assert_array_equal(lens[:r], exp["run_lengths"])
+    np.testing.assert_array_equal(cum[:r + 1], exp["cumulative_run_lengths"])
