@@ -22,6 +22,8 @@ CASES = [
     ([[3, 0, 2], [1, 4, 1]], [8, 4], [10, 20], 5),
     ([[40], [7], [0], [129]], [128, 64, 32, 256], [500, 70, 9, 3000], 12),   # one rank, an empty table
     ([[5, 9, 1, 30], [0, 0, 2, 2], [17, 3, 3, 3]], [36, 128, 4], [60, 2000, 11], 30),
+    # several 3072-key sort tiles per feature segment, an empty feature between
+    ([[900, 300], [0, 0], [1200, 40]], [64, 32, 128], [5000, 40, 300], 12),
 ]
 
 
