@@ -214,6 +214,7 @@ __global__ void __launch_bounds__(256)
     const int64_t s0 = static_cast<int64_t>(in_off[static_cast<int64_t>(src) * B + b]);
     const int64_t d0 = static_cast<int64_t>(out_off[bag]);
     const int64_t len = static_cast<int64_t>(out_off[bag + 1]) - d0;
+    if (s0 < 0 || d0 < 0) continue;  // negative lengths upstream: nothing in bounds to copy
     for (int64_t j = k; j < len; j += G) {
       // Lengths that disagree with the index count or the given output size
       // stop the copy instead of reading or writing past either array.
