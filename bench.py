@@ -71,7 +71,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
                     help="workload; 2 (default) is the headline")
-    ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check", "nobag"],
+    ap.add_argument("--op", default="lookup", choices=["lookup", "bounds-check", "nobag", "permute"],
                     help="bounds-check (config 2): time bounds_check_indices (WARNING) on the "
                          "batch instead of the lookup; nobag (config 2 / 3): the PoolingMode NONE "
                          "forward / backward on the same batch (not the headline)")
@@ -561,6 +561,55 @@ def wl_nobag_forward(args, dev) -> Workload:
         extra=dict(compulsory=dict(bytes=compulsory, unique_rows=uniq)))
 
 
+def wl_permute(args, dev) -> Workload:
+    """permute_2D_sparse_data on the config-2 batch (lengths [8, 4096] int64,
+    668k int64 indices, no weights): the features in reverse order, with
+    permuted_lengths_sum given (no host sync), as a caller reorders a batch's
+    features into its tables' order before the lookup."""
+    import numpy as np
+    import torch
+
+    from mx_fbgemm import bench_inputs
+
+    log("generating config 2 batch")
+    inp = bench_inputs.config2()
+    T, B, N = inp.T, inp.B, inp.N
+    lengths_h = np.diff(inp.offsets).reshape(T, B)
+    perm_h = np.arange(T - 1, -1, -1, dtype=np.int32)
+    op = torch.ops.fbgemm.permute_2D_sparse_data
+
+    def make_step(pc, lc, ic):
+        return lambda: op(pc, lc, ic, None, N)
+
+    perm = torch.from_numpy(perm_h).to(dev)
+    lengths = torch.from_numpy(lengths_h).to(dev)
+    idx = torch.from_numpy(inp.indices).to(dev)
+    step = make_step(perm, lengths, idx)
+    cold = [make_step(perm.clone(), lengths.clone(), idx.clone()) for _ in range(args.cold_copies)]
+    # indices read and written once, lengths read and written once
+    compulsory = 2 * N * 8 + 2 * T * B * 8
+
+    def cpu():
+        sys.path.insert(0, str(REPO / "oracle"))
+        import oracle as orc
+
+        fn = lambda: orc.permute_2d_sparse_data(perm_h, lengths_h, inp.indices)  # noqa: E731
+        log("CPU baseline: numpy feature permute of the oracle, 1 process")
+        med, runs = cpu_time(fn, args.cpu_seconds)
+        return cpu_record(N / med, "indices/s", 1, "port",
+                          f"full config-2 batch (N={N}), median of {runs} runs; the oracle's "
+                          f"numpy permute (one process)")
+
+    return Workload(
+        metric="permute_2D_sparse_data indices/sec, 1 MI355X", unit="indices/s", steps=[step],
+        units=[N], alg_bytes=[compulsory], dtype="int64",
+        config={"workload": "config2 batch, permute_2D_sparse_data (features reversed, "
+                            "int64 lengths and indices, no weights)", "T": T, "B": B, "N": N},
+        kernel="whole op (permuted lengths, two complete cumsums, the copy)",
+        profile="permute_2d_config2", cpu=cpu, cold_steps=cold, roof_bytes=compulsory,
+        roof_bytes_kind="compulsory bytes: indices and lengths each read and written once")
+
+
 # -- config 3 ----------------------------------------------------------------
 
 
@@ -849,6 +898,8 @@ def measure(args, config: int, dev) -> dict:
         wl = wl_bounds_check(args, dev)
     elif config == 2 and args.op == "nobag":
         wl = wl_nobag_forward(args, dev)
+    elif config == 2 and args.op == "permute":
+        wl = wl_permute(args, dev)
     elif config == 3 and args.op == "nobag":
         wl = wl_nobag_backward(args, dev)
     elif config == 2:

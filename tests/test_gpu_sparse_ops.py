@@ -145,3 +145,22 @@ def test_expand_into_jagged_permute(dev, dtype, with_end):
         torch.from_numpy(oo).to(dev), size)
     np.testing.assert_array_equal(got.cpu().numpy(),
                                   orc.expand_into_jagged_permute(permute, in_off, oo, size))
+
+
+@pytest.mark.parametrize("T,B,Tp", [(8, 8192, 8), (8, 8192, 9), (3, 30000, 3), (1, 70000, 2)])
+@pytest.mark.parametrize("ldtype", [torch.int32, torch.int64])
+def test_permute_2d_sparse_data_sizes(dev, T, B, Tp, ldtype):
+    """Batches of 65,536 bags and more (cumsums over several 8192-element
+    tiles), more output features than input ones, and one feature copied twice."""
+    print(f"[case] permute_2D sizes T={T} B={B} Tp={Tp} l={ldtype}", flush=True)
+    rng = np.random.default_rng(T * B + Tp)
+    lengths = rng.integers(0, 6, (T, B))
+    idx = rng.integers(0, 10**6, int(lengths.sum()))
+    permute = rng.integers(0, T, Tp).astype(np.int32)
+    exp_l, exp_i, _ = orc.permute_2d_sparse_data(permute, lengths, idx)
+    pl, pi, pw = torch.ops.fbgemm.permute_2D_sparse_data(
+        torch.from_numpy(permute).to(dev), torch.from_numpy(lengths).to(dev, ldtype),
+        torch.from_numpy(idx).to(dev))
+    np.testing.assert_array_equal(pl.cpu().numpy(), exp_l)
+    np.testing.assert_array_equal(pi.cpu().numpy(), exp_i)
+    assert pw is None
