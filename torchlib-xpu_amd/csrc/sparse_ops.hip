@@ -76,14 +76,18 @@ __device__ __forceinline__ T block_excl(T v, T* total) {
   return wsub(wadd(before, incl), v);
 }
 
+// A tile's sum: wrap-around integer sums do not depend on the order, so each
+// thread adds a strided slice and every load instruction is coalesced.
 template <typename T>
 __global__ void __launch_bounds__(kCsThreads)
     cumsum_tile_kernel(const T* __restrict__ x, int64_t n, T* __restrict__ partial) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kCsTile + threadIdx.x * kCsItems;
+  const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kCsTile;
   T s = 0;
 #pragma unroll
-  for (int it = 0; it < kCsItems; ++it)
-    if (base + it < n) s = wadd(s, x[base + it]);
+  for (int it = 0; it < kCsItems; ++it) {
+    const int64_t i = tile0 + it * kCsThreads + threadIdx.x;
+    if (i < n) s = wadd(s, x[i]);
+  }
   T total;
   (void)block_excl<T>(s, &total);
   if (threadIdx.x == 0) partial[blockIdx.x] = total;
@@ -105,29 +109,47 @@ __global__ void __launch_bounds__(kCsThreads) cumsum_spine_kernel(T* __restrict_
 }
 
 // KIND 0 exclusive, 1 inclusive, 2 complete (out[0] = 0, out[i + 1] = inclusive[i]).
+// The tile passes through LDS both ways, so that the global loads and stores
+// are coalesced while each thread scans kCsItems consecutive elements; a row
+// of kCsItems elements takes kCsPad slots (fewer bank conflicts).
+constexpr int kCsPad = kCsItems + 1;
+__device__ __forceinline__ int cs_slot(int j) { return (j / kCsItems) * kCsPad + j % kCsItems; }
+
 template <typename T, int KIND>
 __global__ void __launch_bounds__(kCsThreads)
     cumsum_scan_kernel(const T* __restrict__ x, int64_t n, const T* __restrict__ prefix,
                        T* __restrict__ out) {
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kCsTile + threadIdx.x * kCsItems;
+  __shared__ T s_buf[kCsThreads * kCsPad];
+  const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kCsTile;
+#pragma unroll
+  for (int it = 0; it < kCsItems; ++it) {
+    const int j = it * kCsThreads + threadIdx.x;
+    s_buf[cs_slot(j)] = tile0 + j < n ? x[tile0 + j] : T(0);
+  }
+  __syncthreads();
   T v[kCsItems];
   T s = 0;
 #pragma unroll
   for (int it = 0; it < kCsItems; ++it) {
-    v[it] = base + it < n ? x[base + it] : T(0);
+    v[it] = s_buf[threadIdx.x * kCsPad + it];
     s = wadd(s, v[it]);
   }
   T total;
+  // block_excl's barriers also order every thread's reads above before the
+  // writes below.
   T run = wadd(block_excl<T>(s, &total), prefix ? prefix[blockIdx.x] : T(0));
+#pragma unroll
+  for (int it = 0; it < kCsItems; ++it) {
+    const T before = run;
+    run = wadd(run, v[it]);
+    s_buf[threadIdx.x * kCsPad + it] = KIND == 0 ? before : run;
+  }
+  __syncthreads();
   if (KIND == 2 && blockIdx.x == 0 && threadIdx.x == 0) out[0] = 0;
 #pragma unroll
   for (int it = 0; it < kCsItems; ++it) {
-    const int64_t i = base + it;
-    if (i >= n) break;
-    if constexpr (KIND == 0) out[i] = run;
-    run = wadd(run, v[it]);
-    if constexpr (KIND == 1) out[i] = run;
-    if constexpr (KIND == 2) out[i + 1] = run;
+    const int j = it * kCsThreads + threadIdx.x;
+    if (tile0 + j < n) out[tile0 + j + (KIND == 2 ? 1 : 0)] = s_buf[cs_slot(j)];
   }
 }
 
