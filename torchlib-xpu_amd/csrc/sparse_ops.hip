@@ -115,12 +115,20 @@ __global__ void __launch_bounds__(kCsThreads) cumsum_spine_kernel(T* __restrict_
 constexpr int kCsPad = kCsItems + 1;
 __device__ __forceinline__ int cs_slot(int j) { return (j / kCsItems) * kCsPad + j % kCsItems; }
 
+// prefix: null (one tile), the tiles' exclusive prefixes, or with `raw` the
+// tiles' sums (at most kCsThreads tiles), which each block adds up to its own.
 template <typename T, int KIND>
 __global__ void __launch_bounds__(kCsThreads)
     cumsum_scan_kernel(const T* __restrict__ x, int64_t n, const T* __restrict__ prefix,
-                       T* __restrict__ out) {
+                       bool raw, T* __restrict__ out) {
   __shared__ T s_buf[kCsThreads * kCsPad];
   const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * kCsTile;
+  T pre = 0;
+  if (raw) {  // block-uniform
+    (void)block_excl<T>(threadIdx.x < blockIdx.x ? prefix[threadIdx.x] : T(0), &pre);
+  } else if (prefix) {
+    pre = prefix[blockIdx.x];
+  }
 #pragma unroll
   for (int it = 0; it < kCsItems; ++it) {
     const int j = it * kCsThreads + threadIdx.x;
@@ -137,7 +145,7 @@ __global__ void __launch_bounds__(kCsThreads)
   T total;
   // block_excl's barriers also order every thread's reads above before the
   // writes below.
-  T run = wadd(block_excl<T>(s, &total), prefix ? prefix[blockIdx.x] : T(0));
+  T run = wadd(block_excl<T>(s, &total), pre);
 #pragma unroll
   for (int it = 0; it < kCsItems; ++it) {
     const T before = run;
@@ -188,17 +196,20 @@ int cumsum_t(const T* x, int64_t n, int32_t kind, T* out, T* partial, hipStream_
   MX_REQUIRE(nt <= 0x7fffffffll, "cumsum of %lld elements too long", (long long)n);
   const dim3 gd(static_cast<uint32_t>(nt));
   const T* prefix = nullptr;
+  // Up to kCsThreads tiles each scan block adds the tile sums before its own
+  // (one launch fewer than the spine kernel, which scans them beyond that).
+  const bool raw = nt > 1 && nt <= kCsThreads;
   if (nt > 1) {
     cumsum_tile_kernel<T><<<gd, kCsThreads, 0, s>>>(x, n, partial);
-    cumsum_spine_kernel<T><<<1, kCsThreads, 0, s>>>(partial, nt);
+    if (!raw) cumsum_spine_kernel<T><<<1, kCsThreads, 0, s>>>(partial, nt);
     prefix = partial;
   }
   if (kind == 0)
-    cumsum_scan_kernel<T, 0><<<gd, kCsThreads, 0, s>>>(x, n, prefix, out);
+    cumsum_scan_kernel<T, 0><<<gd, kCsThreads, 0, s>>>(x, n, prefix, raw, out);
   else if (kind == 1)
-    cumsum_scan_kernel<T, 1><<<gd, kCsThreads, 0, s>>>(x, n, prefix, out);
+    cumsum_scan_kernel<T, 1><<<gd, kCsThreads, 0, s>>>(x, n, prefix, raw, out);
   else
-    cumsum_scan_kernel<T, 2><<<gd, kCsThreads, 0, s>>>(x, n, prefix, out);
+    cumsum_scan_kernel<T, 2><<<gd, kCsThreads, 0, s>>>(x, n, prefix, raw, out);
   MX_LAUNCH_CHECK();
   return MX_OK;
 }
