@@ -21,9 +21,10 @@
 //    for j below output feature t's length.
 //
 // Design: integer work, HBM-bound.  The scans are reduce-then-scan with no
-// waits between blocks: a block sums its 8192-element tile, one block scans
-// the tile sums, and every block then scans its tile from its prefix (a batch
-// of one tile takes only the last launch).  A 2-D complete cumsum gives each
+// waits between blocks: a block sums its 8192-element tile, then every block
+// scans its tile from its prefix, the sum of the tiles before it (added up by
+// the block itself up to 1024 tiles, beyond that scanned first by one block;
+// a batch of one tile takes only the last launch).  A 2-D complete cumsum gives each
 // row to one block.  The permute copies each output bag with one 16-lane
 // group (consecutive elements, coalesced), from the two complete cumsums.
 #include <type_traits>
